@@ -1,0 +1,80 @@
+// Internal interface between the runtime (runtime.cpp) and the kernel
+// families (*.hip).  Each kernel class has one launcher that validates its
+// operands against the arena and, unless `dry`, enqueues its kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstdio>
+
+#include "../../include/dgen_hip.h"
+
+namespace dgen {
+
+struct Launch {
+  hipStream_t stream = nullptr;
+  float* arena = nullptr;       // device arena base
+  uint64_t arena_floats = 0;    // arena size in floats
+  uint32_t frames = 0;          // frame_count of this run
+  int device = 0;
+  int cu_count = 256;
+  bool dry = false;             // validate only
+};
+
+// Thread-local last-error text; returns `code` for tail calls.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// Cell-range check: [off, off+n) inside the arena and off >= 0.
+int check_cell(const Launch& L, int64_t off, uint64_t n, const char* what);
+inline float* cell(const Launch& L, int64_t off) { return L.arena + off; }
+
+#define DGEN_CHECK_CELL(L, off, n, what)                      \
+  do {                                                        \
+    int _rc = ::dgen::check_cell((L), (off), (uint64_t)(n), (what)); \
+    if (_rc) return _rc;                                      \
+  } while (0)
+
+#define DGEN_REQUIRE(cond, ...)                                  \
+  do {                                                           \
+    if (!(cond)) return ::dgen::fail(DGEN_HIP_E_INVALID, __VA_ARGS__); \
+  } while (0)
+
+#define DGEN_HIP_TRY(expr)                                                              \
+  do {                                                                                  \
+    hipError_t _e = (expr);                                                             \
+    if (_e != hipSuccess)                                                               \
+      return ::dgen::fail(DGEN_HIP_E_DEVICE, "%s failed: %s", #expr, hipGetErrorString(_e)); \
+  } while (0)
+
+// Launch-error check after a kernel launch.
+#define DGEN_LAUNCH_CHECK(name)                                                         \
+  do {                                                                                  \
+    hipError_t _e = hipGetLastError();                                                  \
+    if (_e != hipSuccess)                                                               \
+      return ::dgen::fail(DGEN_HIP_E_DEVICE, "launch of %s failed: %s", name, hipGetErrorString(_e)); \
+  } while (0)
+
+using Launcher = int (*)(const Launch&, const dgen_hip_op&);
+
+int launch_accum_table(const Launch&, const dgen_hip_op&);
+int launch_dense_small(const Launch&, const dgen_hip_op&);
+int launch_dense_small_wgrad(const Launch&, const dgen_hip_op&);
+int launch_gemm(const Launch&, const dgen_hip_op&);
+int launch_colsum(const Launch&, const dgen_hip_op&);
+int launch_heads_fwd(const Launch&, const dgen_hip_op&);
+int launch_heads_bwd(const Launch&, const dgen_hip_op&);
+int launch_phasor_carry(const Launch&, const dgen_hip_op&);
+int launch_synth_fwd(const Launch&, const dgen_hip_op&);
+int launch_synth_bwd(const Launch&, const dgen_hip_op&);
+int launch_synth_bwd_reduce(const Launch&, const dgen_hip_op&);
+int launch_spectral_loss(const Launch&, const dgen_hip_op&);
+int launch_spectral_gather(const Launch&, const dgen_hip_op&);
+int launch_adam(const Launch&, const dgen_hip_op&);
+int launch_osc_bank(const Launch&, const dgen_hip_op&);
+int launch_noise_table(const Launch&, const dgen_hip_op&);
+int launch_row_schedule(const Launch&, const dgen_hip_op&);
+int launch_fft_tables(const Launch&, const dgen_hip_op&);
+
+}  // namespace dgen

@@ -1,0 +1,254 @@
+// fp32 GEMM on the gfx950 matrix cores (v_mfma_f32_32x32x2_f32) for the
+// control network: forward layers with fused bias+tanh, backward data GEMMs
+// with the fused tanh derivative, and weight-gradient GEMMs reduced over the
+// 32k-row batch with a deterministic split-K.
+//
+// The reference lowers these matmuls to 8x8 simdgroup fp32 tiles
+// (Sources/DGen/Emit+GEMM.swift:10-80, GEMMPass.swift:60-109); here each
+// 256-thread workgroup owns a 128x128 output tile, each wave a 64x64 quadrant
+// of four 32x32 MFMA accumulators (64 fp32 registers per lane).
+//
+// LDS holds both operand tiles k-major ([BK][BM] and [BK][BN]) so every
+// layout (A as [M][K] or [K][M], B as [K][N] or [N][K]) feeds the MFMA with
+// conflict-free single-float reads; tiles are double buffered with one
+// barrier per k-step.
+#include "internal.h"
+
+namespace dgen {
+
+constexpr int BM = 128, BN = 128, BK = 16, LDSROW = BM + 4;
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+enum { EPI_NONE = 0, EPI_BIAS = 1, EPI_BIAS_TANH = 2, EPI_TANH_GRAD = 3 };
+
+template <bool VEC>
+__device__ __forceinline__ float4 load4(const float* __restrict__ p, int valid) {
+  if (VEC && valid >= 4) return *reinterpret_cast<const float4*>(p);
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (valid > 0) v.x = p[0];
+  if (valid > 1) v.y = p[1];
+  if (valid > 2) v.z = p[2];
+  if (valid > 3) v.w = p[3];
+  return v;
+}
+
+__device__ __forceinline__ float apply_epi(int epi, float acc, int row, int col, const float* __restrict__ bias,
+                                           const float* __restrict__ aux, int ldaux) {
+  switch (epi) {
+    case EPI_BIAS: return acc + bias[col];
+    case EPI_BIAS_TANH: return tanhf(acc + bias[col]);
+    case EPI_TANH_GRAD: {
+      float h = aux[(size_t)row * ldaux + col];
+      return acc * (1.f - h * h);
+    }
+    default: return acc;
+  }
+}
+
+// A_KMAJ: A stored [K][M] (else [M][K]); B_NK: B stored [N][K] (else [K][N]).
+template <bool A_KMAJ, bool B_NK, bool VEC>
+__global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const float* __restrict__ B,
+                                              float* __restrict__ C, int M, int N, int K, int lda, int ldb, int ldc,
+                                              int epi, const float* __restrict__ bias, const float* __restrict__ aux,
+                                              int ldaux, int kchunk, float* __restrict__ ws) {
+  __shared__ float As[2][BK][LDSROW];
+  __shared__ float Bs[2][BK][LDSROW];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int h = lane >> 5, r = lane & 31;
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int kbeg = blockIdx.z * kchunk;
+  const int kend = min(K, kbeg + kchunk);
+
+  floatx16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  float4 ra[2], rb[2];
+
+  auto load_tile = [&](int k0) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int q = tid + p * 256;
+      if (!A_KMAJ) {  // [M][K]: float4 along k
+        const int i = q >> 2, kq = (q & 3) * 4;
+        const int row = m0 + i, k = k0 + kq;
+        int valid = (row < M) ? min(4, kend - k) : 0;
+        ra[p] = load4<VEC>(A + (size_t)row * lda + k, valid);
+      } else {  // [K][M]: float4 along m
+        const int kk = q >> 5, iq = (q & 31) * 4;
+        const int k = k0 + kk, col = m0 + iq;
+        int valid = (k < kend) ? min(4, M - col) : 0;
+        ra[p] = load4<VEC>(A + (size_t)k * lda + col, valid);
+      }
+      if (!B_NK) {  // [K][N]: float4 along n
+        const int kk = q >> 5, jq = (q & 31) * 4;
+        const int k = k0 + kk, col = n0 + jq;
+        int valid = (k < kend) ? min(4, N - col) : 0;
+        rb[p] = load4<VEC>(B + (size_t)k * ldb + col, valid);
+      } else {  // [N][K]: float4 along k
+        const int j = q >> 2, kq = (q & 3) * 4;
+        const int col = n0 + j, k = k0 + kq;
+        int valid = (col < N) ? min(4, kend - k) : 0;
+        rb[p] = load4<VEC>(B + (size_t)col * ldb + k, valid);
+      }
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int q = tid + p * 256;
+      if (!A_KMAJ) {
+        const int i = q >> 2, kq = (q & 3) * 4;
+        As[buf][kq + 0][i] = ra[p].x;
+        As[buf][kq + 1][i] = ra[p].y;
+        As[buf][kq + 2][i] = ra[p].z;
+        As[buf][kq + 3][i] = ra[p].w;
+      } else {
+        const int kk = q >> 5, iq = (q & 31) * 4;
+        *reinterpret_cast<float4*>(&As[buf][kk][iq]) = ra[p];
+      }
+      if (!B_NK) {
+        const int kk = q >> 5, jq = (q & 31) * 4;
+        *reinterpret_cast<float4*>(&Bs[buf][kk][jq]) = rb[p];
+      } else {
+        const int j = q >> 2, kq = (q & 3) * 4;
+        Bs[buf][kq + 0][j] = rb[p].x;
+        Bs[buf][kq + 1][j] = rb[p].y;
+        Bs[buf][kq + 2][j] = rb[p].z;
+        Bs[buf][kq + 3][j] = rb[p].w;
+      }
+    }
+  };
+
+  int buf = 0;
+  if (kbeg < kend) {
+    load_tile(kbeg);
+    store_tile(0);
+  }
+  __syncthreads();
+  for (int k0 = kbeg; k0 < kend; k0 += BK) {
+    const bool more = k0 + BK < kend;
+    if (more) load_tile(k0 + BK);
+#pragma unroll
+    for (int s = 0; s < BK / 2; ++s) {
+      const int k = 2 * s + h;
+      float a0 = As[buf][k][wm + r];
+      float a1 = As[buf][k][wm + 32 + r];
+      float b0 = Bs[buf][k][wn + r];
+      float b1 = Bs[buf][k][wn + 32 + r];
+      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
+      acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
+      acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
+      acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+    }
+    if (more) store_tile(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+  }
+
+  // Accumulator layout of a 32x32 MFMA block: register v of lane l holds
+  // row 8*(v/4) + 4*(l/32) + v%4, column l%32.
+#pragma unroll
+  for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+    for (int tj = 0; tj < 2; ++tj)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int row = m0 + wm + ti * 32 + (v >> 2) * 8 + h * 4 + (v & 3);
+        const int col = n0 + wn + tj * 32 + r;
+        if (row < M && col < N) {
+          if (ws)
+            ws[((size_t)blockIdx.z * M + row) * N + col] = acc[ti][tj][v];
+          else
+            C[(size_t)row * ldc + col] = apply_epi(epi, acc[ti][tj][v], row, col, bias, aux, ldaux);
+        }
+      }
+}
+
+__global__ void k_splitk_reduce(const float* __restrict__ ws, float* __restrict__ C, int M, int N, int ldc, int splits,
+                                int epi, const float* __restrict__ bias, const float* __restrict__ aux, int ldaux) {
+  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (size_t)M * N) return;
+  const int row = (int)(idx / N), col = (int)(idx % N);
+  float s = 0.f;
+  for (int z = 0; z < splits; ++z) s += ws[(size_t)z * M * N + idx];
+  C[(size_t)row * ldc + col] = apply_epi(epi, s, row, col, bias, aux, ldaux);
+}
+
+template <bool AK, bool BT>
+static void launch_variant(bool vec, dim3 g, hipStream_t s, const float* A, const float* B, float* C, int M, int N,
+                           int K, int lda, int ldb, int ldc, int epi, const float* bias, const float* aux, int ldaux,
+                           int kchunk, float* ws) {
+  if (vec)
+    hipLaunchKernelGGL((k_gemm<AK, BT, true>), g, dim3(256), 0, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias, aux,
+                       ldaux, kchunk, ws);
+  else
+    hipLaunchKernelGGL((k_gemm<AK, BT, false>), g, dim3(256), 0, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias, aux,
+                       ldaux, kchunk, ws);
+}
+
+int launch_gemm(const Launch& L, const dgen_hip_op& op) {
+  const int64_t A = op.arg[0], Bc = op.arg[1], Cc = op.arg[2], M = op.arg[3], N = op.arg[4], K = op.arg[5];
+  const int64_t lda = op.arg[6], ldb = op.arg[7], ldc = op.arg[8], alay = op.arg[9], blay = op.arg[10];
+  const int64_t epi = op.arg[11], bias = op.arg[12], aux = op.arg[13], ldaux = op.arg[14];
+  const int64_t split = op.arg[15], ws = op.arg[16];
+  DGEN_REQUIRE(M > 0 && N > 0 && K > 0 && M < (1ll << 31) && N < (1ll << 31) && K < (1ll << 31),
+               "gemm: M %lld N %lld K %lld", (long long)M, (long long)N, (long long)K);
+  DGEN_REQUIRE(alay == 0 || alay == 1, "gemm: a_layout %lld", (long long)alay);
+  DGEN_REQUIRE(blay == 0 || blay == 1, "gemm: b_layout %lld", (long long)blay);
+  DGEN_REQUIRE(epi >= 0 && epi <= 3, "gemm: epilogue %lld", (long long)epi);
+  DGEN_REQUIRE(split >= 1 && split <= 1024, "gemm: split_k %lld", (long long)split);
+  DGEN_REQUIRE(ldc >= N, "gemm: ldc %lld < N %lld", (long long)ldc, (long long)N);
+  DGEN_REQUIRE(alay == 0 ? lda >= K : lda >= M, "gemm: lda %lld too small", (long long)lda);
+  DGEN_REQUIRE(blay == 0 ? ldb >= N : ldb >= K, "gemm: ldb %lld too small", (long long)ldb);
+  DGEN_CHECK_CELL(L, A, alay == 0 ? (M - 1) * lda + K : (K - 1) * lda + M, "gemm.A");
+  DGEN_CHECK_CELL(L, Bc, blay == 0 ? (K - 1) * ldb + N : (N - 1) * ldb + K, "gemm.B");
+  DGEN_CHECK_CELL(L, Cc, (M - 1) * ldc + N, "gemm.C");
+  if (epi == EPI_BIAS || epi == EPI_BIAS_TANH) DGEN_CHECK_CELL(L, bias, N, "gemm.bias");
+  if (epi == EPI_TANH_GRAD) {
+    DGEN_REQUIRE(ldaux >= N, "gemm: ld aux %lld", (long long)ldaux);
+    DGEN_CHECK_CELL(L, aux, (M - 1) * ldaux + N, "gemm.aux");
+  }
+  // k-chunk per split, a multiple of BK
+  int64_t kchunk = (K + split - 1) / split;
+  kchunk = (kchunk + BK - 1) / BK * BK;
+  const int64_t splits = (K + kchunk - 1) / kchunk;
+  if (split > 1) DGEN_CHECK_CELL(L, ws, splits * M * N, "gemm.workspace");
+  DGEN_REQUIRE((M + BM - 1) / BM <= 65535 && splits <= 65535, "gemm: grid too large");
+  if (L.dry) return 0;
+  const bool vec = (lda % 4 == 0) && (ldb % 4 == 0) && (A % 4 == 0) && (Bc % 4 == 0);
+  dim3 g((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM), (unsigned)splits);
+  const float* pa = cell(L, A);
+  const float* pb = cell(L, Bc);
+  float* pc = cell(L, Cc);
+  const float* pbias = (epi == EPI_BIAS || epi == EPI_BIAS_TANH) ? cell(L, bias) : nullptr;
+  const float* paux = epi == EPI_TANH_GRAD ? cell(L, aux) : nullptr;
+  float* pws = split > 1 ? cell(L, ws) : nullptr;
+  const int e = split > 1 ? EPI_NONE : (int)epi;
+  if (alay == 0 && blay == 0)
+    launch_variant<false, false>(vec, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk, pws);
+  else if (alay == 0 && blay == 1)
+    launch_variant<false, true>(vec, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk, pws);
+  else if (alay == 1 && blay == 0)
+    launch_variant<true, false>(vec, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk, pws);
+  else
+    launch_variant<true, true>(vec, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk, pws);
+  DGEN_LAUNCH_CHECK("k_gemm");
+  if (split > 1) {
+    const size_t total = (size_t)M * N;
+    hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, L.stream, pws, pc, (int)M,
+                       (int)N, (int)ldc, (int)splits, (int)epi, pbias, paux, (int)ldaux);
+    DGEN_LAUNCH_CHECK("k_splitk_reduce");
+  }
+  return 0;
+}
+
+}  // namespace dgen

@@ -1,0 +1,264 @@
+// Control-network pieces around the GEMMs: the small-fan-in first layer and
+// its weight gradient, the decoder head activations and their backward, the
+// bias-gradient column sums and the Adam update.
+//
+// Reference: HarmonicDecoderModel (Examples/HarmonicE2E/Model.swift:96-157),
+// Adam.step (Sources/DGenLazy/Optimizers.swift:164-204), AD rules for tanh,
+// max, abs, exp, log (Sources/DGen/Gradients.swift:398-490).
+//
+// Reductions are deterministic: fixed-order per-thread loops and fixed-shape
+// two-stage sums, no atomics.
+#include "internal.h"
+
+namespace dgen {
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+// ---------------------------------------------------------------- layer 1
+// H[m][j] = tanh(sum_i X[m][i] W[i][j] + b[j]) for a fan-in of a few inputs.
+__global__ void k_dense_small(const float* __restrict__ X, const float* __restrict__ W, const float* __restrict__ b,
+                              float* __restrict__ H, int rows, int fan, int width) {
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  const int m = blockIdx.y;
+  if (j >= width || m >= rows) return;
+  float s = 0.f;
+  for (int i = 0; i < fan; ++i) s += X[(size_t)m * fan + i] * W[(size_t)i * width + j];
+  H[(size_t)m * width + j] = tanhf(s + b[j]);
+}
+
+int launch_dense_small(const Launch& L, const dgen_hip_op& op) {
+  const int64_t X = op.arg[0], W = op.arg[1], b = op.arg[2], H = op.arg[3];
+  const int64_t rows = op.arg[4], fan = op.arg[5], width = op.arg[6];
+  DGEN_REQUIRE(rows > 0 && rows <= 65535 * 64 && fan > 0 && fan <= 64 && width > 0 && width <= 65536,
+               "dense_small: rows %lld fan %lld width %lld", (long long)rows, (long long)fan, (long long)width);
+  DGEN_CHECK_CELL(L, X, rows * fan, "dense_small.X");
+  DGEN_CHECK_CELL(L, W, fan * width, "dense_small.W");
+  DGEN_CHECK_CELL(L, b, width, "dense_small.b");
+  DGEN_CHECK_CELL(L, H, rows * width, "dense_small.H");
+  if (L.dry) return 0;
+  DGEN_REQUIRE(rows <= 65535, "dense_small: rows %lld exceed grid y", (long long)rows);
+  hipLaunchKernelGGL(k_dense_small, dim3((unsigned)((width + 255) / 256), (unsigned)rows), dim3(256), 0, L.stream,
+                     cell(L, X), cell(L, W), cell(L, b), cell(L, H), (int)rows, (int)fan, (int)width);
+  DGEN_LAUNCH_CHECK("k_dense_small");
+  return 0;
+}
+
+// Two-stage column reduction: partial[c][n] = sum over row chunk c of
+// scale_row(m) * A[m][n]; out[n] = sum_c partial[c][n] in chunk order.
+constexpr int kColChunks = 256;
+
+__global__ void k_colsum_partial(const float* __restrict__ A, int lda, const float* __restrict__ X, int ldx,
+                                 int xcol, float* __restrict__ part, int rows, int cols, int chunk) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  const int c = blockIdx.y;
+  if (n >= cols) return;
+  const int m0 = c * chunk, m1 = min(rows, m0 + chunk);
+  float s = 0.f;
+  if (X) {
+    for (int m = m0; m < m1; ++m) s += X[(size_t)m * ldx + xcol] * A[(size_t)m * lda + n];
+  } else {
+    for (int m = m0; m < m1; ++m) s += A[(size_t)m * lda + n];
+  }
+  part[(size_t)c * cols + n] = s;
+}
+
+__global__ void k_colsum_final(const float* __restrict__ part, float* __restrict__ out, int chunks, int cols) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= cols) return;
+  float s = 0.f;
+  for (int c = 0; c < chunks; ++c) s += part[(size_t)c * cols + n];
+  out[n] = s;
+}
+
+static int colsum_chunks(int64_t rows) { return (int)std::min<int64_t>(kColChunks, std::max<int64_t>(1, rows / 16)); }
+
+int launch_colsum(const Launch& L, const dgen_hip_op& op) {
+  const int64_t A = op.arg[0], out = op.arg[1], rows = op.arg[2], cols = op.arg[3], lda = op.arg[4], ws = op.arg[5];
+  DGEN_REQUIRE(rows > 0 && cols > 0 && lda >= cols && cols <= 65536, "colsum: rows %lld cols %lld lda %lld",
+               (long long)rows, (long long)cols, (long long)lda);
+  const int chunks = colsum_chunks(rows);
+  DGEN_CHECK_CELL(L, A, (rows - 1) * lda + cols, "colsum.A");
+  DGEN_CHECK_CELL(L, out, cols, "colsum.out");
+  DGEN_CHECK_CELL(L, ws, (int64_t)chunks * cols, "colsum.workspace");
+  if (L.dry) return 0;
+  const int chunk = (int)((rows + chunks - 1) / chunks);
+  hipLaunchKernelGGL(k_colsum_partial, dim3((unsigned)((cols + 63) / 64), chunks), dim3(64), 0, L.stream, cell(L, A),
+                     (int)lda, nullptr, 0, 0, cell(L, ws), (int)rows, (int)cols, chunk);
+  DGEN_LAUNCH_CHECK("k_colsum_partial");
+  hipLaunchKernelGGL(k_colsum_final, dim3((unsigned)((cols + 255) / 256)), dim3(256), 0, L.stream, cell(L, ws),
+                     cell(L, out), chunks, (int)cols);
+  DGEN_LAUNCH_CHECK("k_colsum_final");
+  return 0;
+}
+
+// dW[i][j] = sum_m X[m][i] dZ[m][j] for a small fan-in (first layer).
+int launch_dense_small_wgrad(const Launch& L, const dgen_hip_op& op) {
+  const int64_t X = op.arg[0], dZ = op.arg[1], dW = op.arg[2], rows = op.arg[3], fan = op.arg[4],
+                width = op.arg[5], ws = op.arg[6];
+  DGEN_REQUIRE(rows > 0 && fan > 0 && fan <= 64 && width > 0 && width <= 65536,
+               "dense_small_wgrad: rows %lld fan %lld width %lld", (long long)rows, (long long)fan,
+               (long long)width);
+  const int chunks = colsum_chunks(rows);
+  DGEN_CHECK_CELL(L, X, rows * fan, "dense_small_wgrad.X");
+  DGEN_CHECK_CELL(L, dZ, rows * width, "dense_small_wgrad.dZ");
+  DGEN_CHECK_CELL(L, dW, fan * width, "dense_small_wgrad.dW");
+  DGEN_CHECK_CELL(L, ws, (int64_t)chunks * width, "dense_small_wgrad.workspace");
+  if (L.dry) return 0;
+  const int chunk = (int)((rows + chunks - 1) / chunks);
+  for (int i = 0; i < fan; ++i) {
+    hipLaunchKernelGGL(k_colsum_partial, dim3((unsigned)((width + 63) / 64), chunks), dim3(64), 0, L.stream,
+                       cell(L, dZ), (int)width, cell(L, X), (int)fan, i, cell(L, ws), (int)rows, (int)width, chunk);
+    DGEN_LAUNCH_CHECK("k_colsum_partial");
+    hipLaunchKernelGGL(k_colsum_final, dim3((unsigned)((width + 255) / 256)), dim3(256), 0, L.stream, cell(L, ws),
+                       cell(L, dW) + (size_t)i * width, chunks, (int)width);
+    DGEN_LAUNCH_CHECK("k_colsum_final");
+  }
+  return 0;
+}
+
+// ---------------------------------------------------------------- heads
+// softplus(x) = max(x,0) + log(1 + exp(-|x|))  (Model.swift:153-157)
+__device__ __forceinline__ float softplus(float x) { return fmaxf(x, 0.f) + logf(1.f + expf(-fabsf(x))); }
+// d softplus through the reference AD rules: [x>=0] - sign(x) e^{-|x|}/(1+e^{-|x|})
+__device__ __forceinline__ float softplus_grad(float x) {
+  float e = expf(-fabsf(x));
+  float sg = x > 0.f ? 1.f : (x < 0.f ? -1.f : 0.f);
+  return (x >= 0.f ? 1.f : 0.f) - sg * (e / (1.f + e));
+}
+
+// One wave per row; Z and ctrl rows have stride ldz / ldc.
+__global__ void k_heads_fwd(const float* __restrict__ Z, int ldz, float* __restrict__ C, int ldc, int rows, int K,
+                            int NF) {
+  const int m = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  if (m >= rows) return;
+  const float* z = Z + (size_t)m * ldz;
+  float* c = C + (size_t)m * ldc;
+  float den = 0.f;
+  for (int k = lane; k < K; k += kWave) den += softplus(z[k]);
+  den = wave_sum(den) + 1e-6f;
+  for (int k = lane; k < K; k += kWave) c[k] = softplus(z[k]) / den;
+  if (lane == 0) {
+    c[K] = softplus(z[K]);
+    c[K + 1] = softplus(z[K + 1]);
+  }
+  float nrm = 0.f;
+  for (int i = lane; i < NF; i += kWave) nrm += fabsf(tanhf(z[K + 2 + i]));
+  nrm = wave_sum(nrm) + 1e-4f;
+  for (int i = lane; i < NF; i += kWave) c[K + 2 + i] = tanhf(z[K + 2 + i]) / nrm;
+}
+
+__global__ void k_heads_bwd(const float* __restrict__ Z, int ldz, const float* __restrict__ dC, int ldc,
+                            float* __restrict__ dZ, int lddz, int rows, int K, int NF) {
+  const int m = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  if (m >= rows) return;
+  const float* z = Z + (size_t)m * ldz;
+  const float* dc = dC + (size_t)m * ldc;
+  float* dz = dZ + (size_t)m * lddz;
+  float den = 0.f;
+  for (int k = lane; k < K; k += kWave) den += softplus(z[k]);
+  den = wave_sum(den) + 1e-6f;
+  float dot = 0.f;
+  for (int k = lane; k < K; k += kWave) dot += dc[k] * (softplus(z[k]) / den);
+  dot = wave_sum(dot);
+  for (int k = lane; k < K; k += kWave) dz[k] = (dc[k] - dot) / den * softplus_grad(z[k]);
+  if (lane == 0) {
+    dz[K] = dc[K] * softplus_grad(z[K]);
+    dz[K + 1] = dc[K + 1] * softplus_grad(z[K + 1]);
+  }
+  float nrm = 0.f, dot2 = 0.f;
+  for (int i = lane; i < NF; i += kWave) nrm += fabsf(tanhf(z[K + 2 + i]));
+  nrm = wave_sum(nrm) + 1e-4f;
+  for (int i = lane; i < NF; i += kWave) dot2 += dc[K + 2 + i] * (tanhf(z[K + 2 + i]) / nrm);
+  dot2 = wave_sum(dot2);
+  for (int i = lane; i < NF; i += kWave) {
+    float s = tanhf(z[K + 2 + i]);
+    float sg = s > 0.f ? 1.f : (s < 0.f ? -1.f : 0.f);
+    dz[K + 2 + i] = (dc[K + 2 + i] - sg * dot2) / nrm * (1.f - s * s);
+  }
+  // padding columns of the stored dZ row stay exactly zero
+  for (int c = K + 2 + NF + lane; c < lddz; c += kWave) dz[c] = 0.f;
+}
+
+int launch_heads_fwd(const Launch& L, const dgen_hip_op& op) {
+  const int64_t Z = op.arg[0], C = op.arg[1], rows = op.arg[2], K = op.arg[3], NF = op.arg[4];
+  const int64_t ld = op.arg[5];
+  DGEN_REQUIRE(rows > 0 && K > 0 && NF > 0 && ld >= K + 2 + NF, "heads_fwd: rows %lld K %lld NF %lld ld %lld",
+               (long long)rows, (long long)K, (long long)NF, (long long)ld);
+  DGEN_CHECK_CELL(L, Z, rows * ld, "heads_fwd.Z");
+  DGEN_CHECK_CELL(L, C, rows * ld, "heads_fwd.ctrl");
+  if (L.dry) return 0;
+  hipLaunchKernelGGL(k_heads_fwd, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, L.stream, cell(L, Z), (int)ld,
+                     cell(L, C), (int)ld, (int)rows, (int)K, (int)NF);
+  DGEN_LAUNCH_CHECK("k_heads_fwd");
+  return 0;
+}
+
+int launch_heads_bwd(const Launch& L, const dgen_hip_op& op) {
+  const int64_t Z = op.arg[0], dC = op.arg[1], dZ = op.arg[2], rows = op.arg[3], K = op.arg[4], NF = op.arg[5];
+  const int64_t ld = op.arg[6];
+  DGEN_REQUIRE(rows > 0 && K > 0 && NF > 0 && ld >= K + 2 + NF, "heads_bwd: rows %lld K %lld NF %lld ld %lld",
+               (long long)rows, (long long)K, (long long)NF, (long long)ld);
+  DGEN_CHECK_CELL(L, Z, rows * ld, "heads_bwd.Z");
+  DGEN_CHECK_CELL(L, dC, rows * ld, "heads_bwd.dctrl");
+  DGEN_CHECK_CELL(L, dZ, rows * ld, "heads_bwd.dZ");
+  if (L.dry) return 0;
+  hipLaunchKernelGGL(k_heads_bwd, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, L.stream, cell(L, Z), (int)ld,
+                     cell(L, dC), (int)ld, cell(L, dZ), (int)ld, (int)rows, (int)K, (int)NF);
+  DGEN_LAUNCH_CHECK("k_heads_bwd");
+  return 0;
+}
+
+// ---------------------------------------------------------------- Adam
+// Adam.step (Optimizers.swift:164-204): t += 1; bias corrections in fp32;
+// m = b1 m + (1-b1) g; v = b2 v + (1-b2) g g; p -= lr mhat / (sqrt(vhat)+eps).
+// The step counter lives in a device cell; it is read by every thread and
+// incremented afterwards by a separate one-thread launch (stream order).
+#pragma clang fp contract(off)
+__global__ void k_adam(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ m,
+                       float* __restrict__ v, size_t n, const float* __restrict__ tcell, float lr, float b1, float b2,
+                       float eps) {
+  const float t = tcell[0] + 1.0f;
+  const float bc1 = 1.0f - powf(b1, t);
+  const float bc2 = 1.0f - powf(b2, t);
+  for (size_t j = (size_t)blockIdx.x * blockDim.x + threadIdx.x; j < n; j += (size_t)gridDim.x * blockDim.x) {
+    float gj = g[j];
+    float mj = b1 * m[j] + (1.0f - b1) * gj;
+    float vj = b2 * v[j] + (1.0f - b2) * gj * gj;
+    float mh = mj / bc1, vh = vj / bc2;
+    p[j] = p[j] - lr * mh / (sqrtf(vh) + eps);
+    m[j] = mj;
+    v[j] = vj;
+  }
+}
+#pragma clang fp contract(on)
+
+__global__ void k_increment(float* c) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) c[0] = c[0] + 1.0f;
+}
+
+int launch_adam(const Launch& L, const dgen_hip_op& op) {
+  const int64_t P = op.arg[0], G = op.arg[1], M = op.arg[2], V = op.arg[3], n = op.arg[4], tc = op.arg[5];
+  DGEN_REQUIRE(n > 0, "adam: n %lld", (long long)n);
+  DGEN_CHECK_CELL(L, P, n, "adam.params");
+  DGEN_CHECK_CELL(L, G, n, "adam.grads");
+  DGEN_CHECK_CELL(L, M, n, "adam.m");
+  DGEN_CHECK_CELL(L, V, n, "adam.v");
+  DGEN_CHECK_CELL(L, tc, 1, "adam.step");
+  if (L.dry) return 0;
+  unsigned blocks = (unsigned)std::min<int64_t>((n + 255) / 256, (int64_t)L.cu_count * 8);
+  hipLaunchKernelGGL(k_adam, dim3(blocks), dim3(256), 0, L.stream, cell(L, P), cell(L, G), cell(L, M), cell(L, V),
+                     (size_t)n, cell(L, tc), op.farg[0], op.farg[1], op.farg[2], op.farg[3]);
+  DGEN_LAUNCH_CHECK("k_adam");
+  hipLaunchKernelGGL(k_increment, dim3(1), dim3(64), 0, L.stream, cell(L, tc));
+  DGEN_LAUNCH_CHECK("k_increment");
+  return 0;
+}
+
+}  // namespace dgen

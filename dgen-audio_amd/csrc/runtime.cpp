@@ -1,0 +1,397 @@
+// libdgen_hip runtime: context, arena + pinned host mirror, schedule,
+// streams, timing.  The C ABI is declared in include/dgen_hip.h.
+//
+// Design notes
+// - One device arena per context (hipMalloc once at configure), addressed
+//   by float offsets: the reference's flat `memory` of cells
+//   (Sources/DGen/Compilation/MemoryAllocation.swift:4-24).  The reference
+//   relies on host-coherent storage (MetalRuntime.swift:232); on discrete HBM
+//   the host mirror is pinned and moved only by explicit upload/download.
+// - Stream 0 carries the schedule; ops flagged SIDE run on a second stream
+//   (default priority) that first waits for the run's start event, and a JOIN
+//   op makes stream 0 wait for the side stream before it launches.
+// - run() is synchronous like MetalCompiledKernel.run (commit+wait,
+//   MetalRuntime.swift:334-337).
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "internal.h"
+
+namespace dgen {
+
+static thread_local char g_err[1024] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_cell(const Launch& L, int64_t off, uint64_t n, const char* what) {
+  if (off < 0 || (uint64_t)off > L.arena_floats || n > L.arena_floats - (uint64_t)off)
+    return fail(DGEN_HIP_E_RANGE, "%s: cell range [%lld, +%llu) outside arena of %llu floats", what,
+                (long long)off, (unsigned long long)n, (unsigned long long)L.arena_floats);
+  return 0;
+}
+
+static Launcher launcher_for(uint32_t k) {
+  switch (k) {
+    case DGEN_HIP_K_ACCUM_TABLE: return launch_accum_table;
+    case DGEN_HIP_K_DENSE_SMALL: return launch_dense_small;
+    case DGEN_HIP_K_GEMM: return launch_gemm;
+    case DGEN_HIP_K_HEADS_FWD: return launch_heads_fwd;
+    case DGEN_HIP_K_PHASOR_CARRY: return launch_phasor_carry;
+    case DGEN_HIP_K_SYNTH_FWD: return launch_synth_fwd;
+    case DGEN_HIP_K_SPECTRAL_LOSS: return launch_spectral_loss;
+    case DGEN_HIP_K_SPECTRAL_GATHER: return launch_spectral_gather;
+    case DGEN_HIP_K_SYNTH_BWD: return launch_synth_bwd;
+    case DGEN_HIP_K_SYNTH_BWD_REDUCE: return launch_synth_bwd_reduce;
+    case DGEN_HIP_K_HEADS_BWD: return launch_heads_bwd;
+    case DGEN_HIP_K_COLSUM: return launch_colsum;
+    case DGEN_HIP_K_DENSE_SMALL_WGRAD: return launch_dense_small_wgrad;
+    case DGEN_HIP_K_ADAM: return launch_adam;
+    case DGEN_HIP_K_OSC_BANK: return launch_osc_bank;
+    case DGEN_HIP_K_NOISE_TABLE: return launch_noise_table;
+    case DGEN_HIP_K_ROW_SCHEDULE: return launch_row_schedule;
+    case DGEN_HIP_K_FFT_TABLES: return launch_fft_tables;
+    default: return nullptr;
+  }
+}
+
+}  // namespace dgen
+
+using namespace dgen;
+
+struct dgen_hip_ctx {
+  int device = 0;
+  int cu_count = 256;
+  hipStream_t s0 = nullptr, s1 = nullptr;
+  hipEvent_t ev_start = nullptr, ev_side = nullptr;
+  float* d_arena = nullptr;
+  float* h_arena = nullptr;
+  uint64_t floats = 0;
+  uint32_t max_frames = 0;
+  std::vector<dgen_hip_op> ops;
+  bool configured = false;
+};
+
+static int set_device(dgen_hip_ctx* c) {
+  DGEN_HIP_TRY(hipSetDevice(c->device));
+  return 0;
+}
+
+static Launch make_launch(dgen_hip_ctx* c, hipStream_t s, uint32_t frames, bool dry) {
+  Launch L;
+  L.stream = s;
+  L.arena = c->d_arena;
+  L.arena_floats = c->floats;
+  L.frames = frames;
+  L.device = c->device;
+  L.cu_count = c->cu_count;
+  L.dry = dry;
+  return L;
+}
+
+static void release_arena(dgen_hip_ctx* c) {
+  if (c->d_arena) (void)hipFree(c->d_arena);
+  if (c->h_arena) (void)hipHostFree(c->h_arena);
+  c->d_arena = nullptr;
+  c->h_arena = nullptr;
+  c->floats = 0;
+  c->configured = false;
+}
+
+// Enqueue ops [0, n) that match `static_pass`; optional per-op event timing.
+static int enqueue(dgen_hip_ctx* c, uint32_t frames, bool static_pass, std::vector<hipEvent_t>* evs) {
+  DGEN_HIP_TRY(hipEventRecord(c->ev_start, c->s0));
+  DGEN_HIP_TRY(hipStreamWaitEvent(c->s1, c->ev_start, 0));
+  bool side_used = false;
+  for (size_t i = 0; i < c->ops.size(); ++i) {
+    const dgen_hip_op& op = c->ops[i];
+    bool is_static = (op.flags & DGEN_HIP_OP_STATIC) != 0;
+    if (is_static != static_pass) continue;
+    if (op.flags & DGEN_HIP_OP_JOIN) {
+      DGEN_HIP_TRY(hipEventRecord(c->ev_side, c->s1));
+      DGEN_HIP_TRY(hipStreamWaitEvent(c->s0, c->ev_side, 0));
+    }
+    hipStream_t s = (op.flags & DGEN_HIP_OP_SIDE) ? c->s1 : c->s0;
+    side_used |= (s == c->s1);
+    Launch L = make_launch(c, s, frames, false);
+    if (evs) DGEN_HIP_TRY(hipEventRecord((*evs)[2 * i], s));
+    int rc = launcher_for(op.kernel)(L, op);
+    if (rc) return rc;
+    if (evs) DGEN_HIP_TRY(hipEventRecord((*evs)[2 * i + 1], s));
+  }
+  // Never leave side-stream work unjoined past the end of a run.
+  if (side_used) {
+    DGEN_HIP_TRY(hipEventRecord(c->ev_side, c->s1));
+    DGEN_HIP_TRY(hipStreamWaitEvent(c->s0, c->ev_side, 0));
+  }
+  return 0;
+}
+
+static int run_static(dgen_hip_ctx* c);
+
+extern "C" {
+
+int dgen_hip_abi_version(void) { return DGEN_HIP_ABI_VERSION; }
+
+int dgen_hip_device_count(int* out) {
+  if (!out) return fail(DGEN_HIP_E_INVALID, "device_count: null out");
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) {
+    *out = 0;
+    return fail(DGEN_HIP_E_DEVICE, "hipGetDeviceCount: %s", hipGetErrorString(e));
+  }
+  *out = n;
+  return 0;
+}
+
+const char* dgen_hip_last_error(void) { return g_err; }
+
+int dgen_hip_create(int device, dgen_hip_ctx** out) {
+  if (!out) return fail(DGEN_HIP_E_INVALID, "create: null out");
+  *out = nullptr;
+  int n = 0;
+  DGEN_HIP_TRY(hipGetDeviceCount(&n));
+  if (device < 0 || device >= n) return fail(DGEN_HIP_E_INVALID, "create: device %d of %d", device, n);
+  dgen_hip_ctx* c = new (std::nothrow) dgen_hip_ctx();
+  if (!c) return fail(DGEN_HIP_E_NOMEM, "create: out of host memory");
+  c->device = device;
+  int rc = set_device(c);
+  if (!rc) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) == hipSuccess) c->cu_count = prop.multiProcessorCount;
+    if (hipStreamCreateWithFlags(&c->s0, hipStreamNonBlocking) != hipSuccess ||
+        hipStreamCreateWithFlags(&c->s1, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&c->ev_start, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&c->ev_side, hipEventDisableTiming) != hipSuccess)
+      rc = fail(DGEN_HIP_E_DEVICE, "create: stream/event creation failed");
+  }
+  if (rc) {
+    dgen_hip_destroy(c);
+    return rc;
+  }
+  *out = c;
+  return 0;
+}
+
+int dgen_hip_destroy(dgen_hip_ctx* c) {
+  if (!c) return 0;
+  (void)hipSetDevice(c->device);
+  if (c->s0) (void)hipStreamSynchronize(c->s0);
+  if (c->s1) (void)hipStreamSynchronize(c->s1);
+  release_arena(c);
+  if (c->ev_start) (void)hipEventDestroy(c->ev_start);
+  if (c->ev_side) (void)hipEventDestroy(c->ev_side);
+  if (c->s0) (void)hipStreamDestroy(c->s0);
+  if (c->s1) (void)hipStreamDestroy(c->s1);
+  delete c;
+  return 0;
+}
+
+int dgen_hip_configure(dgen_hip_ctx* c, const dgen_hip_op* ops, uint32_t n_ops, uint64_t memory_floats,
+                       uint32_t max_frames) {
+  if (!c) return fail(DGEN_HIP_E_INVALID, "configure: null context");
+  if (n_ops && !ops) return fail(DGEN_HIP_E_INVALID, "configure: null ops");
+  if (memory_floats == 0) return fail(DGEN_HIP_E_INVALID, "configure: empty arena");
+  int rc = set_device(c);
+  if (rc) return rc;
+  DGEN_HIP_TRY(hipStreamSynchronize(c->s0));
+  DGEN_HIP_TRY(hipStreamSynchronize(c->s1));
+  release_arena(c);
+  // Validate the schedule before allocating (dry launches need sizes only).
+  c->floats = memory_floats;
+  for (uint32_t i = 0; i < n_ops; ++i) {
+    Launcher f = launcher_for(ops[i].kernel);
+    if (!f) return fail(DGEN_HIP_E_INVALID, "configure: op %u has unknown kernel class %u", i, ops[i].kernel);
+    Launch L = make_launch(c, c->s0, max_frames, true);
+    rc = f(L, ops[i]);
+    if (rc) {
+      std::string msg = g_err;
+      c->floats = 0;
+      return fail(rc, "configure: op %u (kernel %u): %s", i, ops[i].kernel, msg.c_str());
+    }
+  }
+  c->floats = 0;
+  size_t bytes = (size_t)memory_floats * sizeof(float);
+  if (hipMalloc(&c->d_arena, bytes) != hipSuccess) {
+    c->d_arena = nullptr;
+    return fail(DGEN_HIP_E_NOMEM, "configure: hipMalloc of %zu bytes failed", bytes);
+  }
+  if (hipHostMalloc(&c->h_arena, bytes, hipHostMallocDefault) != hipSuccess) {
+    c->h_arena = nullptr;
+    release_arena(c);
+    return fail(DGEN_HIP_E_NOMEM, "configure: pinned host allocation of %zu bytes failed", bytes);
+  }
+  c->floats = memory_floats;
+  memset(c->h_arena, 0, bytes);
+  DGEN_HIP_TRY(hipMemsetAsync(c->d_arena, 0, bytes, c->s0));
+  c->ops.assign(ops, ops + n_ops);
+  c->max_frames = max_frames;
+  c->configured = true;
+  return run_static(c);
+}
+
+float* dgen_hip_host_memory(dgen_hip_ctx* c) { return c ? c->h_arena : nullptr; }
+
+static int range_ok(dgen_hip_ctx* c, uint64_t off, uint64_t n, const char* what) {
+  if (!c || !c->configured) return fail(DGEN_HIP_E_STATE, "%s: context not configured", what);
+  if (off > c->floats || n > c->floats - off)
+    return fail(DGEN_HIP_E_RANGE, "%s: [%llu, +%llu) outside arena of %llu floats", what,
+                (unsigned long long)off, (unsigned long long)n, (unsigned long long)c->floats);
+  return 0;
+}
+
+int dgen_hip_upload(dgen_hip_ctx* c, uint64_t off, uint64_t n) {
+  int rc = range_ok(c, off, n, "upload");
+  if (rc) return rc;
+  if ((rc = set_device(c))) return rc;
+  if (!n) return 0;
+  DGEN_HIP_TRY(hipMemcpyAsync(c->d_arena + off, c->h_arena + off, n * sizeof(float), hipMemcpyHostToDevice, c->s0));
+  DGEN_HIP_TRY(hipStreamSynchronize(c->s0));
+  return 0;
+}
+
+int dgen_hip_download(dgen_hip_ctx* c, uint64_t off, uint64_t n) {
+  int rc = range_ok(c, off, n, "download");
+  if (rc) return rc;
+  if ((rc = set_device(c))) return rc;
+  if (!n) return 0;
+  DGEN_HIP_TRY(hipMemcpyAsync(c->h_arena + off, c->d_arena + off, n * sizeof(float), hipMemcpyDeviceToHost, c->s0));
+  DGEN_HIP_TRY(hipStreamSynchronize(c->s0));
+  return 0;
+}
+
+int dgen_hip_zero(dgen_hip_ctx* c, uint64_t off, uint64_t n) {
+  if (c && c->configured && n == 0 && off == 0) n = c->floats;
+  int rc = range_ok(c, off, n, "zero");
+  if (rc) return rc;
+  if ((rc = set_device(c))) return rc;
+  if (!n) return 0;
+  DGEN_HIP_TRY(hipMemsetAsync(c->d_arena + off, 0, n * sizeof(float), c->s0));
+  DGEN_HIP_TRY(hipStreamSynchronize(c->s0));
+  return run_static(c);
+}
+
+static int run_checks(dgen_hip_ctx* c, uint32_t frame_count) {
+  if (!c || !c->configured) return fail(DGEN_HIP_E_STATE, "run: context not configured");
+  if (frame_count > c->max_frames)
+    return fail(DGEN_HIP_E_RANGE, "run: frame_count %u > max_frames %u", frame_count, c->max_frames);
+  return set_device(c);
+}
+
+// Static ops (temporality .static) depend only on their constant arguments;
+// they run at configure and again after any zero() that may have cleared
+// their outputs.
+static int run_static(dgen_hip_ctx* c) {
+  bool any = false;
+  for (auto& op : c->ops) any |= (op.flags & DGEN_HIP_OP_STATIC) != 0;
+  if (!any) return 0;
+  int rc = enqueue(c, c->max_frames, true, nullptr);
+  if (rc) return rc;
+  DGEN_HIP_TRY(hipStreamSynchronize(c->s0));
+  DGEN_HIP_TRY(hipStreamSynchronize(c->s1));
+  return 0;
+}
+
+int dgen_hip_run_async(dgen_hip_ctx* c, uint32_t frame_count) {
+  int rc = run_checks(c, frame_count);
+  if (rc) return rc;
+  return enqueue(c, frame_count, false, nullptr);
+}
+
+int dgen_hip_sync(dgen_hip_ctx* c) {
+  if (!c) return fail(DGEN_HIP_E_INVALID, "sync: null context");
+  int rc = set_device(c);
+  if (rc) return rc;
+  DGEN_HIP_TRY(hipStreamSynchronize(c->s0));
+  DGEN_HIP_TRY(hipStreamSynchronize(c->s1));
+  return 0;
+}
+
+int dgen_hip_run(dgen_hip_ctx* c, uint32_t frame_count) {
+  int rc = dgen_hip_run_async(c, frame_count);
+  if (rc) {
+    if (c) (void)dgen_hip_sync(c);
+    return rc;
+  }
+  return dgen_hip_sync(c);
+}
+
+int dgen_hip_profile(dgen_hip_ctx* c, uint32_t frame_count, dgen_hip_kernel_time* out, size_t cap, size_t* n_out) {
+  int rc = run_checks(c, frame_count);
+  if (rc) return rc;
+  std::vector<hipEvent_t> evs(2 * c->ops.size(), nullptr);
+  for (auto& e : evs) DGEN_HIP_TRY(hipEventCreate(&e));
+  rc = enqueue(c, frame_count, false, &evs);
+  int rc2 = dgen_hip_sync(c);
+  size_t n = 0;
+  if (!rc && !rc2) {
+    for (size_t i = 0; i < c->ops.size(); ++i) {
+      if (c->ops[i].flags & DGEN_HIP_OP_STATIC) continue;
+      float ms = 0.f;
+      if (hipEventElapsedTime(&ms, evs[2 * i], evs[2 * i + 1]) != hipSuccess) ms = -1.f;
+      if (out && n < cap) out[n] = dgen_hip_kernel_time{(uint32_t)i, c->ops[i].kernel, ms};
+      ++n;
+    }
+  }
+  for (auto& e : evs) (void)hipEventDestroy(e);
+  if (n_out) *n_out = n;
+  return rc ? rc : rc2;
+}
+
+int dgen_hip_time_runs(dgen_hip_ctx* c, uint32_t frame_count, int warmup, int iters, double* ms_out) {
+  if (!ms_out || iters <= 0 || warmup < 0) return fail(DGEN_HIP_E_INVALID, "time_runs: bad arguments");
+  int rc = run_checks(c, frame_count);
+  if (rc) return rc;
+  for (int i = 0; i < warmup; ++i)
+    if ((rc = enqueue(c, frame_count, false, nullptr))) return rc;
+  if ((rc = dgen_hip_sync(c))) return rc;
+  hipEvent_t a, b;
+  DGEN_HIP_TRY(hipEventCreate(&a));
+  DGEN_HIP_TRY(hipEventCreate(&b));
+  DGEN_HIP_TRY(hipEventRecord(a, c->s0));
+  for (int i = 0; i < iters && !rc; ++i) rc = enqueue(c, frame_count, false, nullptr);
+  DGEN_HIP_TRY(hipEventRecord(b, c->s0));
+  int rc2 = dgen_hip_sync(c);
+  float ms = 0.f;
+  if (!rc && !rc2) DGEN_HIP_TRY(hipEventElapsedTime(&ms, a, b));
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  *ms_out = ms;
+  return rc ? rc : rc2;
+}
+
+int dgen_hip_time_op(dgen_hip_ctx* c, uint32_t frame_count, uint32_t op_index, int iters, double* ms_out) {
+  if (!ms_out || iters <= 0) return fail(DGEN_HIP_E_INVALID, "time_op: bad arguments");
+  int rc = run_checks(c, frame_count);
+  if (rc) return rc;
+  if (op_index >= c->ops.size() || (c->ops[op_index].flags & DGEN_HIP_OP_STATIC))
+    return fail(DGEN_HIP_E_INVALID, "time_op: op %u is not a per-run op", op_index);
+  std::vector<hipEvent_t> evs(2 * c->ops.size(), nullptr);
+  for (auto& e : evs) DGEN_HIP_TRY(hipEventCreate(&e));
+  double total = 0.0;
+  for (int it = 0; it < iters && !rc; ++it) {
+    rc = enqueue(c, frame_count, false, &evs);
+    int rc2 = dgen_hip_sync(c);
+    if (!rc) rc = rc2;
+    float ms = 0.f;
+    if (!rc && hipEventElapsedTime(&ms, evs[2 * op_index], evs[2 * op_index + 1]) != hipSuccess)
+      rc = fail(DGEN_HIP_E_DEVICE, "time_op: hipEventElapsedTime failed");
+    total += ms;
+  }
+  for (auto& e : evs) (void)hipEventDestroy(e);
+  *ms_out = total / iters;
+  return rc;
+}
+
+}  // extern "C"

@@ -1,0 +1,241 @@
+"""Schedules for the BASELINE workloads, as the HIP renderer lowers them.
+
+Each builder returns a :class:`Program` whose ops follow the block order the
+reference compiler produces for the same DGenLazy graph (forward blocks, then
+the gradient blocks of ``loss.backward``, then the optimiser), with the
+blocks pattern-matched to hand-written kernel classes.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import runtime as R
+from .program import Program
+from .workloads import HarmonicConfig, OscBankConfig
+
+SEG = 64          # frames per synth segment (checkpoint spacing)
+SLOTS = 4         # control rows a segment may touch
+ROW_ENTRIES = 8   # (segment, slot) entries per control row
+LDC = 128         # padded control-row stride (K + 2 + NF <= 128)
+SPLITK_ROWS = 1024  # rows per split of the weight-gradient GEMMs
+
+
+def _f32(x) -> float:
+    return float(np.float32(x))
+
+
+# ------------------------------------------------------------------ config 1
+def oscbank_program(cfg: OscBankConfig) -> Program:
+    """Signal.phasor(Tensor) bank -> sin -> *amps -> sum -> history one-pole."""
+    p = Program(max_frames=cfg.frames)
+    freqs = p.alloc("freqs", cfg.n_osc)
+    amps = p.alloc("amps", cfg.n_osc)
+    out = p.alloc("out", cfg.frames)
+    chunks = (cfg.frames + 255) // 256
+    ws = p.alloc("workspace", cfg.frames + 2 * chunks)
+    p.add(R.K_OSC_BANK, [freqs, amps, out, cfg.n_osc, cfg.frames, ws], [cfg.sr, cfg.pole], label="osc_bank",
+          dispatch=f"perFrame({cfg.frames}) + chunked scan")
+    p.output_cell = "out"
+    return p
+
+
+# ------------------------------------------------------------------ config 3
+def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = True) -> Program:
+    """Batched harmonic + noise synth with MLP decoder and MSS loss.
+
+    ``train=False`` builds the forward render only (controls -> audio), used
+    to render targets.  With ``train=True`` the schedule is forward, loss,
+    backward to every parameter and (``optimizer``) one Adam step."""
+    B, T, F, K, NF, NC, M = cfg.B, cfg.T, cfg.F, cfg.K, cfg.NF, cfg.NC, cfg.M
+    Hd, din, Lyr = cfg.hidden, cfg.din, cfg.layers
+    if NC > LDC:
+        raise ValueError(f"K + 2 + NF = {NC} exceeds {LDC}")
+    if K > 64:
+        raise ValueError("K > 64 harmonics is not supported by the synth kernels")
+    nseg = (T + SEG - 1) // SEG
+    p = Program(max_frames=T)
+    p.meta.update(cfg=cfg, nseg=nseg, train=train)
+
+    # ---- data, parameters, optimiser state
+    X = p.alloc("X", M * din)
+    f0 = p.alloc("f0", F * B)
+    uv = p.alloc("uv", F * B)
+    npar = cfg.param_count()
+    P = p.alloc("params", npar)
+    woff, off = [], 0
+    fan = din
+    for _ in range(Lyr):
+        woff.append((P + off, P + off + fan * Hd))
+        off += fan * Hd + Hd
+        fan = Hd
+    Wh, bh = P + off, P + off + Hd * NC
+    p.meta["param_offsets"] = [(w - P, b - P) for w, b in woff] + [(Wh - P, bh - P)]
+
+    # ---- static tables
+    play = p.alloc("playhead", T)
+    lerp = p.alloc("lerp", T * 8)
+    segrows = p.alloc("seg_rows", nseg * SLOTS)
+    rowlist = p.alloc("row_list", F * ROW_ENTRIES)
+    flag = p.alloc("row_flag", 1)
+    noise = p.alloc("noise", T)
+    fmaxi = np.float32(max(0, F - 1))
+    step = fmaxi / np.float32(max(1, T - 1))
+    hi = np.float32(max(np.float32(0.0), fmaxi - np.float32(1e-4)))
+    p.add(R.K_ACCUM_TABLE, [play, T], [step, 0.0, fmaxi if F > 1 else 1.0, 0.0, hi], flags=R.OP_STATIC,
+          label="playhead", dispatch="static singleThreaded")
+    p.add(R.K_NOISE_TABLE, [noise, T], flags=R.OP_STATIC, label="noise", dispatch="static singleThreaded")
+    p.add(R.K_ROW_SCHEDULE, [play, lerp, segrows, rowlist, flag, F, T, SEG], flags=R.OP_STATIC,
+          label="row_schedule", dispatch="static singleThreaded")
+
+    # ---- activations
+    Hs = [p.alloc(f"H{l + 1}", M * Hd) for l in range(Lyr)]
+    Z = p.alloc("Z", M * LDC)
+    ctrl = p.alloc("ctrl", M * LDC)
+    ck = p.alloc("checkpoints", nseg * B * K)
+    y = p.alloc("y", B * T)
+
+    # ---- forward
+    p.add(R.K_PHASOR_CARRY, [lerp, f0, ck, B, K, F, T, SEG], [cfg.sr], flags=R.OP_SIDE, label="phasor_carry",
+          dispatch=f"fixedWithFrameLoop({B * K})")
+    W1, b1 = woff[0]
+    p.add(R.K_DENSE_SMALL, [X, W1, b1, Hs[0], M, din, Hd], label="mlp_in", dispatch="gemmSmall")
+    for l in range(1, Lyr):
+        W, b = woff[l]
+        p.add(R.K_GEMM, [Hs[l - 1], W, Hs[l], M, Hd, Hd, Hd, Hd, Hd, 0, 0, R.EPI_BIAS_TANH, b, -1, 0, 1, 0],
+              label=f"mlp_l{l + 1}", dispatch="gemm")
+    p.add(R.K_GEMM, [Hs[-1], Wh, Z, M, NC, Hd, Hd, NC, LDC, 0, 0, R.EPI_BIAS, bh, -1, 0, 1, 0], label="mlp_heads",
+          dispatch="gemm")
+    p.add(R.K_HEADS_FWD, [Z, ctrl, M, K, NF, LDC], label="heads", dispatch=f"perFrameScaled({M})")
+    synth_args = [ctrl, f0, uv, lerp, ck, y, B, K, NF, F, T, SEG, -1, noise, LDC]
+    hs, ns = cfg.hscale, cfg.nscale
+    p.add(R.K_SYNTH_FWD, synth_args, [cfg.sr, hs, ns], flags=R.OP_JOIN, label="synth_fwd",
+          dispatch=f"perFrameScaled({B})")
+    p.output_cell = "y"
+    if not train:
+        return p
+
+    # ---- loss + backward
+    target = p.alloc("target", B * T)
+    lossf = p.alloc("loss_frames", T)
+    dy = p.alloc("dy", B * T)
+    sizes = list(cfg.fft_sizes)
+    if len(sizes) > 8:
+        raise ValueError("at most 8 FFT sizes")
+    ns_ = np.float32(len(sizes))
+    wl = np.float32(cfg.w_lin) / ns_
+    wg = np.float32(cfg.w_log) / ns_
+    maxf = np.float32(T)
+    gl = wl / maxf / np.float32(B)
+    gg = wg / maxf / np.float32(B)
+    wgrad_cells, wloss_cells = [], []
+    for N in sizes:
+        hop = max(1, N // cfg.hop_div)
+        nwin = (T + hop - 1) // hop
+        tab = p.alloc(f"fft_tables_{N}", 3 * N - 2)
+        p.add(R.K_FFT_TABLES, [tab, N], flags=R.OP_STATIC, label=f"fft_tables_{N}", dispatch="static")
+        wlc = p.alloc(f"win_loss_{N}", nwin * B * 2)
+        wgc = p.alloc(f"win_grad_{N}", nwin * B * N)
+        p.add(R.K_SPECTRAL_LOSS, [y, target, wlc, wgc, B, T, N, hop, tab], [gl, gg], label=f"spectral_{N}",
+              dispatch=f"perFrameScaledThreadgroup1({B}) hop {hop}")
+        wgrad_cells.append(wgc)
+        wloss_cells.append(wlc)
+    garg = [dy, lossf, B, T, len(sizes)] + (sizes + [0] * 8)[:8] + (wgrad_cells + [0] * 8)[:8] \
+        + (wloss_cells + [0] * 8)[:8] + [cfg.hop_div]
+    p.add(R.K_SPECTRAL_GATHER, garg, [wl, wg, maxf], label="spectral_gather", dispatch=f"perFrameScaled({B})")
+
+    part = p.alloc("synth_partials", B * nseg * SLOTS * LDC)
+    dctrl = p.alloc("dctrl", M * LDC)
+    bargs = list(synth_args)
+    bargs[5] = dy
+    bargs[12] = part
+    p.add(R.K_SYNTH_BWD, bargs, [cfg.sr, hs, ns], label="synth_bwd", dispatch=f"selfManagedThreads({B})")
+    p.add(R.K_SYNTH_BWD_REDUCE, [part, rowlist, dctrl, B, NC, F, T, SEG, LDC], label="synth_bwd_reduce",
+          dispatch=f"perFrameScaled({M})")
+    dZ = p.alloc("dZ", M * LDC)
+    p.add(R.K_HEADS_BWD, [Z, dctrl, dZ, M, K, NF, LDC], label="heads_bwd", dispatch=f"perFrameScaled({M})")
+
+    G = p.alloc("grads", npar)
+    split = max(1, (M + SPLITK_ROWS - 1) // SPLITK_ROWS)
+    ws_gemm = p.alloc("splitk_ws", split * Hd * max(Hd, NC))
+    chunks = min(256, max(1, M // 16))
+    ws_col = p.alloc("colsum_ws", chunks * max(Hd, NC))
+    gW = [(G + (w - P), G + (b - P)) for (w, b) in woff]
+    gWh, gbh = G + (Wh - P), G + (bh - P)
+    # heads: dWh = H_L^T dZ ; dbh = colsum(dZ) ; dH_L = (dZ Wh^T) * (1 - H_L^2)
+    p.add(R.K_GEMM, [Hs[-1], dZ, gWh, Hd, NC, M, Hd, LDC, NC, 1, 0, R.EPI_NONE, -1, -1, 0, split, ws_gemm],
+          label="dW_heads", dispatch="gemmChunkPartials")
+    p.add(R.K_COLSUM, [dZ, gbh, M, NC, LDC, ws_col], label="db_heads", dispatch="chunkPartialsReduceToCell")
+    dH = [p.alloc(f"dZ{l + 1}", M * Hd) for l in range(Lyr)]
+    p.add(R.K_GEMM, [dZ, Wh, dH[-1], M, Hd, NC, LDC, NC, Hd, 0, 1, R.EPI_TANH_GRAD, -1, Hs[-1], Hd, 1, 0],
+          label=f"dX_heads", dispatch="gemm")
+    for l in range(Lyr - 1, 0, -1):
+        W, _b = woff[l]
+        gw, gb = gW[l]
+        p.add(R.K_GEMM, [Hs[l - 1], dH[l], gw, Hd, Hd, M, Hd, Hd, Hd, 1, 0, R.EPI_NONE, -1, -1, 0, split, ws_gemm],
+              label=f"dW_l{l + 1}", dispatch="gemmChunkPartials")
+        p.add(R.K_COLSUM, [dH[l], gb, M, Hd, Hd, ws_col], label=f"db_l{l + 1}", dispatch="chunkPartialsReduceToCell")
+        p.add(R.K_GEMM, [dH[l], W, dH[l - 1], M, Hd, Hd, Hd, Hd, Hd, 0, 1, R.EPI_TANH_GRAD, -1, Hs[l - 1], Hd, 1, 0],
+              label=f"dX_l{l + 1}", dispatch="gemm")
+    gw1, gb1 = gW[0]
+    p.add(R.K_DENSE_SMALL_WGRAD, [X, dH[0], gw1, M, din, Hd, ws_col], label="dW_l1",
+          dispatch="chunkPartialsReduceToCell")
+    p.add(R.K_COLSUM, [dH[0], gb1, M, Hd, Hd, ws_col], label="db_l1", dispatch="chunkPartialsReduceToCell")
+    if optimizer:
+        m = p.alloc("adam_m", npar)
+        v = p.alloc("adam_v", npar)
+        tcell = p.alloc("adam_t", 1)
+        p.add(R.K_ADAM, [P, G, m, v, npar, tcell], [cfg.lr, 0.9, 0.999, 1e-8], label="adam",
+              dispatch=f"staticThreads({npar})")
+    p.output_cell = "y"
+    return p
+
+
+def check_row_schedule(rt: R.HIPLazyRuntime) -> None:
+    """The static row schedule reports overflow in a flag cell; fail loudly."""
+    flag = float(rt.read("row_flag")[0])
+    if flag != 0.0:
+        raise R.HIPError(f"row schedule overflow (flag {flag}): a synth segment touches more than {SLOTS} "
+                         f"control rows or a row more than {ROW_ENTRIES} segments")
+
+
+class HarmonicSession:
+    """Owns a training runtime (and a render runtime for the target) for one
+    HarmonicConfig.  Inputs are staged once; every ``step()`` is one
+    forward+backward(+Adam) pass with all data resident in HBM."""
+
+    def __init__(self, cfg: HarmonicConfig, device: int = 0, optimizer: bool = True, target=None):
+        self.cfg = cfg
+        f0, uv, X = cfg.data()
+        self.f0, self.uv, self.X = f0, uv, X
+        self.params0 = cfg.weights()
+        if target is None:
+            target = self.render(cfg.weights(seed=cfg.target_seed), device)
+        self.target = np.ascontiguousarray(target, np.float32).reshape(cfg.B, cfg.T)
+        self.program = harmonic_program(cfg, train=True, optimizer=optimizer)
+        self.rt = R.HIPLazyRuntime(self.program, device)
+        check_row_schedule(self.rt)
+        self.rt.write("X", X)
+        self.rt.write("f0", f0)
+        self.rt.write("uv", uv)
+        self.rt.write("params", self.params0)
+        self.rt.write("target", self.target)
+
+    def render(self, params, device: int = 0) -> np.ndarray:
+        prog = harmonic_program(self.cfg, train=False)
+        with R.HIPLazyRuntime(prog, device) as rt:
+            check_row_schedule(rt)
+            rt.write("X", self.X)
+            rt.write("f0", self.f0)
+            rt.write("uv", self.uv)
+            rt.write("params", params)
+            rt.runNoCopy()
+            return rt.read("y").reshape(self.cfg.B, self.cfg.T)
+
+    def step(self) -> None:
+        self.rt.runNoCopy()
+
+    def loss(self) -> float:
+        return float(self.rt.read("loss_frames").astype(np.float64).sum())
+
+    def close(self):
+        self.rt.close()

@@ -1,0 +1,239 @@
+"""ctypes binding of libdgen_hip.so and the host-side runtime object.
+
+``HIPLazyRuntime`` mirrors the reference's ``LazyRuntime`` protocol
+(Sources/DGenLazy/Realize.swift:12-19): ``cellAllocations``,
+``zeroAllBuffers()``, ``runNoCopy(frameCount)``, ``memoryPointer()``,
+``outputsPointer()`` and ``profileKernels(frameCount)``.  It drives the C ABI
+declared in include/dgen_hip.h; there is no CPU fallback: every call goes to
+the HIP library, and a missing library or device raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+from .program import Program
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libdgen_hip.so")
+
+NARG, NFARG = 32, 8
+
+# kernel classes (enum dgen_hip_kernel)
+K_ACCUM_TABLE = 1
+K_DENSE_SMALL = 2
+K_GEMM = 3
+K_HEADS_FWD = 4
+K_PHASOR_CARRY = 5
+K_SYNTH_FWD = 6
+K_SPECTRAL_LOSS = 7
+K_SPECTRAL_GATHER = 8
+K_SYNTH_BWD = 9
+K_SYNTH_BWD_REDUCE = 10
+K_HEADS_BWD = 11
+K_COLSUM = 12
+K_DENSE_SMALL_WGRAD = 13
+K_ADAM = 14
+K_OSC_BANK = 15
+K_NOISE_TABLE = 16
+K_ROW_SCHEDULE = 17
+K_FFT_TABLES = 18
+
+KERNEL_NAMES = {v: k[2:].lower() for k, v in globals().items() if k.startswith("K_")}
+
+EPI_NONE, EPI_BIAS, EPI_BIAS_TANH, EPI_TANH_GRAD = 0, 1, 2, 3
+OP_STATIC, OP_SIDE, OP_JOIN = 1, 2, 4
+
+EXPORTED_SYMBOLS = (
+    "dgen_hip_abi_version", "dgen_hip_device_count", "dgen_hip_create", "dgen_hip_destroy",
+    "dgen_hip_last_error", "dgen_hip_configure", "dgen_hip_host_memory", "dgen_hip_upload",
+    "dgen_hip_download", "dgen_hip_zero", "dgen_hip_run", "dgen_hip_run_async", "dgen_hip_sync",
+    "dgen_hip_profile", "dgen_hip_time_runs", "dgen_hip_time_op",
+)
+
+
+class HIPError(RuntimeError):
+    """A libdgen_hip call returned a negative status."""
+
+
+class COp(ctypes.Structure):
+    _fields_ = [("kernel", ctypes.c_uint32), ("flags", ctypes.c_uint32),
+                ("arg", ctypes.c_int64 * NARG), ("farg", ctypes.c_float * NFARG)]
+
+
+class CKernelTime(ctypes.Structure):
+    _fields_ = [("index", ctypes.c_uint32), ("kernel", ctypes.c_uint32), ("gpu_ms", ctypes.c_float)]
+
+
+_LIB: ctypes.CDLL | None = None
+
+
+def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load libdgen_hip.so (built in-tree by __graft_entry__.build())."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not os.path.exists(path):
+        raise HIPError(f"{path} is missing: build the HIP extension first (python -c "
+                       f"'import __graft_entry__ as g; g.build()')")
+    L = ctypes.CDLL(path)
+    vp, u32, u64, i32 = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int
+    sig = {
+        "dgen_hip_abi_version": ([], i32),
+        "dgen_hip_device_count": ([ctypes.POINTER(i32)], i32),
+        "dgen_hip_create": ([i32, ctypes.POINTER(vp)], i32),
+        "dgen_hip_destroy": ([vp], i32),
+        "dgen_hip_last_error": ([], ctypes.c_char_p),
+        "dgen_hip_configure": ([vp, ctypes.POINTER(COp), u32, u64, u32], i32),
+        "dgen_hip_host_memory": ([vp], ctypes.POINTER(ctypes.c_float)),
+        "dgen_hip_upload": ([vp, u64, u64], i32),
+        "dgen_hip_download": ([vp, u64, u64], i32),
+        "dgen_hip_zero": ([vp, u64, u64], i32),
+        "dgen_hip_run": ([vp, u32], i32),
+        "dgen_hip_run_async": ([vp, u32], i32),
+        "dgen_hip_sync": ([vp], i32),
+        "dgen_hip_profile": ([vp, u32, ctypes.POINTER(CKernelTime), ctypes.c_size_t,
+                              ctypes.POINTER(ctypes.c_size_t)], i32),
+        "dgen_hip_time_runs": ([vp, u32, i32, i32, ctypes.POINTER(ctypes.c_double)], i32),
+        "dgen_hip_time_op": ([vp, u32, u32, i32, ctypes.POINTER(ctypes.c_double)], i32),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = res
+    _LIB = L
+    return L
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load_library().dgen_hip_last_error().decode(errors="replace")
+        raise HIPError(f"{what} failed ({rc}): {msg}")
+
+
+def device_count() -> int:
+    L = load_library()
+    n = ctypes.c_int(0)
+    rc = L.dgen_hip_device_count(ctypes.byref(n))
+    return n.value if rc == 0 else 0
+
+
+@dataclass
+class KernelTiming:
+    index: int
+    name: str
+    dispatch_info: str
+    gpu_ms: float
+
+
+class HIPLazyRuntime:
+    """Runtime for one compiled program on one device (LazyRuntime mirror)."""
+
+    def __init__(self, program: Program, device: int = 0):
+        self.L = load_library()
+        self.program = program
+        self.cellAllocations = program.cells
+        ctx = ctypes.c_void_p()
+        _check(self.L.dgen_hip_create(device, ctypes.byref(ctx)), "dgen_hip_create")
+        self._ctx = ctx
+        ops = (COp * max(1, len(program.ops)))()
+        for i, op in enumerate(program.ops):
+            ops[i].kernel = op.kernel
+            ops[i].flags = op.flags
+            for j, a in enumerate(op.arg):
+                ops[i].arg[j] = int(a)
+            for j, a in enumerate(op.farg):
+                ops[i].farg[j] = float(a)
+        self._ops = ops
+        # Static ops run inside configure and may read data cells, so data
+        # staged before configure would be lost; the program's static ops only
+        # read constants, and inputs are written afterwards via write().
+        _check(self.L.dgen_hip_configure(ctx, ops, len(program.ops), program.size, program.max_frames),
+               "dgen_hip_configure")
+        ptr = self.L.dgen_hip_host_memory(ctx)
+        self._host = np.ctypeslib.as_array(ptr, shape=(program.size,))
+
+    # -- LazyRuntime protocol -------------------------------------------
+    def zeroAllBuffers(self) -> None:
+        _check(self.L.dgen_hip_zero(self._ctx, 0, 0), "dgen_hip_zero")
+        self._host[:] = 0.0
+
+    def runNoCopy(self, frameCount: int | None = None) -> None:
+        _check(self.L.dgen_hip_run(self._ctx, frameCount or self.program.max_frames), "dgen_hip_run")
+
+    def memoryPointer(self) -> np.ndarray:
+        return self._host
+
+    def outputsPointer(self) -> np.ndarray:
+        c = self.program.cells[self.program.output_cell]
+        self.download(self.program.output_cell)
+        return self._host[c.off:c.off + c.n]
+
+    def profileKernels(self, frameCount: int | None = None) -> list[KernelTiming]:
+        cap = len(self.program.ops)
+        buf = (CKernelTime * max(1, cap))()
+        n = ctypes.c_size_t(0)
+        _check(self.L.dgen_hip_profile(self._ctx, frameCount or self.program.max_frames, buf, cap,
+                                       ctypes.byref(n)), "dgen_hip_profile")
+        out = []
+        for i in range(min(n.value, cap)):
+            op = self.program.ops[buf[i].index]
+            out.append(KernelTiming(buf[i].index, op.label or KERNEL_NAMES.get(buf[i].kernel, "?"),
+                                    op.dispatch, buf[i].gpu_ms))
+        return out
+
+    # -- cell helpers ---------------------------------------------------
+    def write(self, name: str, data) -> None:
+        c = self.program.cells[name]
+        a = np.ascontiguousarray(data, dtype=np.float32).reshape(-1)
+        if a.size != c.n:
+            raise ValueError(f"cell {name}: {a.size} values for {c.n} floats")
+        self._host[c.off:c.off + c.n] = a
+        _check(self.L.dgen_hip_upload(self._ctx, c.off, c.n), f"upload {name}")
+
+    def download(self, name: str) -> None:
+        c = self.program.cells[name]
+        _check(self.L.dgen_hip_download(self._ctx, c.off, c.n), f"download {name}")
+
+    def read(self, name: str) -> np.ndarray:
+        c = self.program.cells[name]
+        self.download(name)
+        return self._host[c.off:c.off + c.n].copy()
+
+    def run_async(self, frameCount: int | None = None) -> None:
+        _check(self.L.dgen_hip_run_async(self._ctx, frameCount or self.program.max_frames), "dgen_hip_run_async")
+
+    def sync(self) -> None:
+        _check(self.L.dgen_hip_sync(self._ctx), "dgen_hip_sync")
+
+    def time_runs(self, warmup: int, iters: int, frameCount: int | None = None) -> float:
+        ms = ctypes.c_double(0.0)
+        _check(self.L.dgen_hip_time_runs(self._ctx, frameCount or self.program.max_frames, warmup, iters,
+                                         ctypes.byref(ms)), "dgen_hip_time_runs")
+        return ms.value
+
+    def time_op(self, index: int, iters: int, frameCount: int | None = None) -> float:
+        ms = ctypes.c_double(0.0)
+        _check(self.L.dgen_hip_time_op(self._ctx, frameCount or self.program.max_frames, index, iters,
+                                       ctypes.byref(ms)), "dgen_hip_time_op")
+        return ms.value
+
+    def close(self) -> None:
+        if getattr(self, "_ctx", None):
+            self.L.dgen_hip_destroy(self._ctx)
+            self._ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()

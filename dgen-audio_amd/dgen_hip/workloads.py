@@ -1,0 +1,174 @@
+"""Synthetic, seeded inputs for the five BASELINE workloads.
+
+All randomness comes from SplitMix64, the generator the reference's
+HarmonicE2E example uses (Examples/HarmonicE2E/Config.swift:245-259), so every
+array here is reproducible bit-for-bit on any host.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+
+_M64 = (1 << 64) - 1
+
+
+class SplitMix64:
+    """SplitMix64 stream; seed 0 is replaced by the golden-ratio increment
+    (Examples/HarmonicE2E/Config.swift:248-258)."""
+
+    def __init__(self, seed: int):
+        self.state = 0x9E3779B97F4A7C15 if seed == 0 else seed & _M64
+
+    def next(self) -> int:
+        self.state = (self.state + 0x9E3779B97F4A7C15) & _M64
+        z = self.state
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & _M64
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & _M64
+        return z ^ (z >> 31)
+
+    def next_array(self, n: int) -> np.ndarray:
+        """n raw uint64 draws, vectorised (identical to n calls of next())."""
+        inc = np.uint64(0x9E3779B97F4A7C15)
+        with np.errstate(over="ignore"):
+            st = np.uint64(self.state) + inc * np.arange(1, n + 1, dtype=np.uint64)
+            z = st
+            z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+            z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+            z = z ^ (z >> np.uint64(31))
+        self.state = int(st[-1]) if n else self.state
+        return z
+
+    def uniform(self, n: int) -> np.ndarray:
+        """U[0,1) doubles from the top 53 bits."""
+        return (self.next_array(n) >> np.uint64(11)).astype(np.float64) * (1.0 / (1 << 53))
+
+    def normal(self, n: int) -> np.ndarray:
+        """Box-Muller N(0,1) doubles."""
+        m = (n + 1) // 2
+        u1 = np.maximum(self.uniform(m), 1e-300)
+        u2 = self.uniform(m)
+        r = np.sqrt(-2.0 * np.log(u1))
+        return np.concatenate([r * np.cos(2 * math.pi * u2), r * np.sin(2 * math.pi * u2)])[:n]
+
+
+def reference_random_array(rng: SplitMix64, count: int, scale: float) -> np.ndarray:
+    """HarmonicDecoderModel.randomArray (Examples/HarmonicE2E/Model.swift:141-151):
+    r = Float(next() & 0xFFFF) / Float(UInt16.max); w = (r*2 - 1) * scale."""
+    raw = (rng.next_array(count) & np.uint64(0xFFFF)).astype(np.float32)
+    r = raw / np.float32(65535.0)
+    return ((r * np.float32(2.0) - np.float32(1.0)) * np.float32(scale)).astype(np.float32)
+
+
+# ---------------------------------------------------------------- config 1
+@dataclass
+class OscBankConfig:
+    n_osc: int = 16
+    f_base: float = 220.0
+    sr: float = 44100.0
+    pole: float = 0.9
+    frames: int = 65536
+    seed: int = 1
+
+    def inputs(self):
+        freqs = (np.arange(1, self.n_osc + 1, dtype=np.float32) * np.float32(self.f_base)).astype(np.float32)
+        a = SplitMix64(self.seed).uniform(self.n_osc).astype(np.float32)
+        amps = (a / a.sum(dtype=np.float32)).astype(np.float32)
+        return freqs, amps
+
+
+# ---------------------------------------------------------------- config 3
+@dataclass
+class HarmonicConfig:
+    """Batched DDSP harmonic + FIR-noise synth with MLP decoder and MSS loss."""
+    B: int = 32
+    T: int = 64000
+    sr: float = 16000.0
+    K: int = 60
+    NF: int = 65
+    control_hop: int = 64
+    din: int = 2
+    hidden: int = 512
+    layers: int = 3
+    fft_sizes: tuple = (2048, 1024, 512, 256, 128, 64)
+    hop_div: int = 4
+    w_lin: float = 1.0
+    w_log: float = 0.5
+    min_f0: float = 50.0
+    max_f0: float = 1000.0
+    hscale: float = 1.0
+    nscale: float = 1.0
+    data_seed: int = 3
+    weight_seed: int = 5
+    target_seed: int = 4
+    lr: float = 1e-3
+
+    @property
+    def F(self) -> int:
+        return max(1, self.T // self.control_hop)
+
+    @property
+    def NC(self) -> int:
+        return self.K + 2 + self.NF
+
+    @property
+    def M(self) -> int:
+        return self.B * self.F
+
+    def param_count(self) -> int:
+        n, fan = 0, self.din
+        for _ in range(self.layers):
+            n += fan * self.hidden + self.hidden
+            fan = self.hidden
+        return n + self.hidden * self.NC + self.NC
+
+    def weights(self, seed: int | None = None) -> np.ndarray:
+        """Parameter blob in the order W1 b1 ... WL bL Wh bh; head columns are
+        W_harm | W_gain | W_noise | W_noiseFilter.  Initialisation follows
+        HarmonicDecoderModel.init (Examples/HarmonicE2E/Model.swift:36-83),
+        drawing the tensors in the reference's order."""
+        rng = SplitMix64(self.weight_seed if seed is None else seed)
+        parts = []
+        fan = self.din
+        for _ in range(self.layers):
+            scale = np.float32(math.sqrt(2.0 / fan) * 0.5)
+            parts.append(reference_random_array(rng, fan * self.hidden, scale))
+            parts.append(np.zeros(self.hidden, np.float32))
+            fan = self.hidden
+        H, K, NF = self.hidden, self.K, self.NF
+        w_harm = reference_random_array(rng, H * K, 0.06).reshape(H, K)
+        w_gain = reference_random_array(rng, H, 0.05).reshape(H, 1)
+        w_noise = reference_random_array(rng, H, 0.05).reshape(H, 1)
+        w_nf = reference_random_array(rng, H * NF, 0.05).reshape(H, NF)
+        parts.append(np.concatenate([w_harm, w_gain, w_noise, w_nf], axis=1).reshape(-1))
+        bh = np.zeros(self.NC, np.float32)
+        bh[K + 1] = -3.0  # b_noise init (Model.swift:77)
+        parts.append(bh)
+        return np.concatenate(parts).astype(np.float32)
+
+    def data(self):
+        """f0 [F][B] (Hz), uv [F][B], features X [B*F][din] (row = b*F + f).
+
+        f0: log-uniform start in [60, 1000] Hz, then a Gaussian log-domain
+        random walk (sigma 0.01 per control frame); loudness ~ U[0,1].
+        Features follow makeConditioningData (Examples/HarmonicE2E/Trainer.swift:588-616):
+        f0_norm = (log(max(f0,minF0)) - log(minF0)) / (log(maxF0) - log(minF0)),
+        loudness as given; uv = 1 (voiced)."""
+        rng = SplitMix64(self.data_seed)
+        B, F = self.B, self.F
+        start = math.log(60.0) + rng.uniform(B) * (math.log(1000.0) - math.log(60.0))
+        walk = np.cumsum(rng.normal(F * B).reshape(F, B) * 0.01, axis=0)
+        walk -= walk[0:1]
+        f0 = np.exp(start[None, :] + walk).astype(np.float32)
+        loud = rng.uniform(F * B).reshape(F, B).astype(np.float32)
+        uv = np.ones((F, B), np.float32)
+        lo, hi = math.log(self.min_f0), math.log(max(self.max_f0, self.min_f0 + 1))
+        f0n = ((np.log(np.maximum(f0.astype(np.float64), self.min_f0)) - lo) / max(1e-6, hi - lo)).astype(np.float32)
+        X = np.zeros((B * F, self.din), np.float32)
+        X[:, 0] = f0n.T.reshape(-1)
+        if self.din > 1:
+            X[:, 1] = loud.T.reshape(-1)
+        if self.din > 2:
+            X[:, 2] = uv.T.reshape(-1)
+        return f0, uv, X

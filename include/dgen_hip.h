@@ -1,0 +1,245 @@
+/*
+ * dgen_hip.h -- C ABI of libdgen_hip.so, the MI355X (gfx950) execution backend
+ * for DGen schedules.
+ *
+ * The library plays the two roles the reference splits between a Renderer
+ * and a LazyRuntime:
+ *   - it accepts a *schedule*: an ordered list of kernel-class launches over
+ *     cells of one flat float arena (the reference's `memory`, addressed by
+ *     cell offsets), i.e. what a renderer emits as [CompiledKernel]
+ *     (reference: Sources/DGen/Renderer/Renderer.swift:134-143, 203-226);
+ *   - it owns the device arena, a pinned host mirror, the HIP streams and the
+ *     per-kernel timing, mirroring the LazyRuntime protocol
+ *     (Sources/DGenLazy/Realize.swift:12-19) and MetalCompiledKernel
+ *     (Sources/DGen/MetalRuntime.swift:5-893).
+ *
+ * Conventions (shared by every entry point):
+ *   - Every function returns 0 on success or a negative DGEN_HIP_E_* code.
+ *     Nothing aborts across the ABI; the message of the last failure on the
+ *     calling thread is returned by dgen_hip_last_error().
+ *   - Offsets and lengths are in floats (4-byte cells) of the arena.
+ *   - One context per thread; calls on one context must be serialised
+ *     (the reference is single-threaded per graph, LazyGraph.swift:255).
+ *   - No torch or HIP types appear in this header.
+ */
+#ifndef DGEN_HIP_H
+#define DGEN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DGEN_HIP_ABI_VERSION 1
+
+/* ---- status codes ------------------------------------------------------ */
+#define DGEN_HIP_OK 0
+#define DGEN_HIP_E_INVALID (-1)   /* bad argument / shape / offset        */
+#define DGEN_HIP_E_DEVICE (-2)    /* HIP runtime error                    */
+#define DGEN_HIP_E_STATE (-3)     /* call out of order (e.g. run before configure) */
+#define DGEN_HIP_E_RANGE (-4)     /* frame_count > max_frames, cell out of arena */
+#define DGEN_HIP_E_NOMEM (-5)     /* device or pinned allocation failed   */
+
+typedef struct dgen_hip_ctx dgen_hip_ctx;
+
+/* ---- kernel classes ----------------------------------------------------
+ * Argument meaning per class is documented at each class below.
+ * "cell" = arena offset in floats; "n" = element count.                   */
+enum dgen_hip_kernel {
+  /* Accumulator table (static block): out[t] = min(max(accum_t, lo), hi),
+   * accum_t the pre-increment output of u_accum(step, reset 0, min, max)
+   * evaluated sequentially in fp32 (Definitions.swift:215-246).
+   * arg: [0]=out cell [1]=frames   farg: [0]=step [1]=min [2]=max [3]=lo [4]=hi */
+  DGEN_HIP_K_ACCUM_TABLE = 1,
+
+  /* First MLP layer for a small fan-in: H = tanh(X W + b).
+   * arg: [0]=X [1]=W [2]=b [3]=H (cells) [4]=rows [5]=fan_in [6]=width */
+  DGEN_HIP_K_DENSE_SMALL = 2,
+
+  /* fp32 MFMA GEMM  C[M][N] = op(A) op(B) with fused epilogue.
+   * arg: [0]=A [1]=B [2]=C [3]=M [4]=N [5]=K [6]=lda [7]=ldb [8]=ldc
+   *      [9]=a_layout (0: A stored [M][K], 1: A stored [K][M])
+   *      [10]=b_layout (0: B stored [K][N], 1: B stored [N][K])
+   *      [11]=epilogue (DGEN_HIP_EPI_*) [12]=bias cell (-1 none)
+   *      [13]=aux cell (tanh output for EPI_TANH_GRAD, -1 none) [14]=ld aux
+   *      [15]=split_k (1 = none; >1: partial sums in [16]) [16]=workspace cell */
+  DGEN_HIP_K_GEMM = 3,
+
+  /* Head activations of HarmonicDecoderModel (Model.swift:100-114):
+   * amps = softplus/sum, gain/noise gain = softplus, taps = tanh/sum|.|.
+   * arg: [0]=Z [1]=ctrl [2]=rows [3]=K [4]=NF */
+  DGEN_HIP_K_HEADS_FWD = 4,
+
+  /* Sequential tensor-phasor carry pass (Emit+State.swift:322-369) for
+   * lanes (b,k), freq = (k+1) * lerp(f0 rows at the playhead); stores the
+   * phase at the start of every segment.
+   * arg: [0]=playhead cell [1]=f0 cell ([F][B]) [2]=checkpoints cell
+   *      ([nseg][B][K]) [3]=B [4]=K [5]=F [6]=T [7]=segment length
+   * farg: [0]=sample rate */
+  DGEN_HIP_K_PHASOR_CARRY = 5,
+
+  /* Batched harmonic + FIR-noise synth forward
+   * (Examples/HarmonicE2E/Synth.swift:47-102).
+   * arg: [0]=ctrl [1]=f0 [2]=uv [3]=playhead [4]=checkpoints [5]=y ([B][T])
+   *      [6]=B [7]=K [8]=NF [9]=F [10]=T [11]=segment length
+   * farg: [0]=sample rate [1]=harmonic scale [2]=noise scale */
+  DGEN_HIP_K_SYNTH_FWD = 6,
+
+  /* Multi-scale batched spectral loss, forward + gradient spectrum + IFFT for
+   * one FFT size (Emit+SpectralLoss.swift:719-1160).
+   * arg: [0]=x ([B][T]) [1]=target ([B][T]) [2]=per-window loss cell
+   *      ([nwin][B][2]: lin, log) [3]=per-window time-gradient cell
+   *      ([nwin][B][N]) [4]=B [5]=T [6]=N [7]=hop
+   * farg: [0]=lin upstream grad per window (w_lin/nsizes/maxFrames/B)
+   *       [1]=log upstream grad per window */
+  DGEN_HIP_K_SPECTRAL_LOSS = 7,
+
+  /* Gather of hop-window time gradients into d x (Emit+SpectralLoss.swift:
+   * 1163-1235) summed over up to 8 FFT sizes, plus the per-frame loss signal.
+   * arg: [0]=dx ([B][T]) [1]=loss frames ([T]) [2]=B [3]=T [4]=n_sizes
+   *      [5..12]=N_s [13..20]=window-gradient cells [21..28] per-window loss
+   *      cells [29]=hop divisor
+   * farg: [0]=lin weight per size * 1/(B*maxFrames) [1]=log weight likewise */
+  DGEN_HIP_K_SPECTRAL_GATHER = 8,
+
+  /* Synth backward: d ctrl row partials per segment.
+   * arg: as DGEN_HIP_K_SYNTH_FWD with [5]=dy ([B][T]) [12]=partials cell */
+  DGEN_HIP_K_SYNTH_BWD = 9,
+
+  /* Deterministic reduction of synth-backward segment partials into d ctrl.
+   * arg: [0]=partials [1]=playhead [2]=dctrl [3]=B [4]=NC [5]=F [6]=T [7]=seg */
+  DGEN_HIP_K_SYNTH_BWD_REDUCE = 10,
+
+  /* Head backward: dZ from d ctrl and Z.  arg: [0]=Z [1]=dctrl [2]=dZ
+   * [3]=rows [4]=K [5]=NF */
+  DGEN_HIP_K_HEADS_BWD = 11,
+
+  /* Column sums (bias gradients): out[n] = sum_m A[m][n].
+   * arg: [0]=A [1]=out [2]=M [3]=N [4]=lda [5]=workspace cell */
+  DGEN_HIP_K_COLSUM = 12,
+
+  /* First-layer weight gradient for a small fan-in: dW[i][j] = sum_m X[m][i]
+   * dZ[m][j]. arg: [0]=X [1]=dZ [2]=dW [3]=rows [4]=fan_in [5]=width
+   * [6]=workspace cell */
+  DGEN_HIP_K_DENSE_SMALL_WGRAD = 13,
+
+  /* Adam.step over a flat parameter blob (Optimizers.swift:164-204).
+   * arg: [0]=params [1]=grads [2]=m [3]=v [4]=n [5]=step-counter cell
+   * farg: [0]=lr [1]=beta1 [2]=beta2 [3]=eps */
+  DGEN_HIP_K_ADAM = 14,
+
+  /* Deterministic phasor bank -> sum -> one-pole (config 1).
+   * arg: [0]=freqs [1]=amps [2]=out [3]=n_osc [4]=frames [5]=workspace cell
+   * farg: [0]=sample rate [1]=pole */
+  DGEN_HIP_K_OSC_BANK = 15,
+
+  /* xorshift32 noise stream of a zeroed cell (CRenderer.swift:685-693), a
+   * static table.  arg: [0]=out cell [1]=frames */
+  DGEN_HIP_K_NOISE_TABLE = 16,
+
+  /* Row schedule of a sampleRow read (Emit+RowSelection.swift:164-197) from a
+   * playhead table, a static table set.  arg: [0]=playhead [1]=lerp ([T][8]:
+   * lo, hi, frac, 1-frac, slot(lo), slot(hi), 0, 0) [2]=segment rows
+   * ([nseg][4]) [3]=row entries ([F][8]) [4]=status flag cell [5]=F [6]=T
+   * [7]=segment length.  The flag is 0 when every segment touches <= 4 rows
+   * and every row has <= 8 (segment, slot) entries. */
+  DGEN_HIP_K_ROW_SCHEDULE = 17,
+
+  /* Spectral-loss tables for one FFT size (HigherOps.swift:71-99):
+   * hann[N] | twre[N-1] | twim[N-1].  arg: [0]=out cell [1]=N */
+  DGEN_HIP_K_FFT_TABLES = 18,
+};
+
+/* GEMM epilogues */
+enum dgen_hip_epilogue {
+  DGEN_HIP_EPI_NONE = 0,       /* C = acc                                   */
+  DGEN_HIP_EPI_BIAS = 1,       /* C = acc + bias[n]                         */
+  DGEN_HIP_EPI_BIAS_TANH = 2,  /* C = tanh(acc + bias[n])                   */
+  DGEN_HIP_EPI_TANH_GRAD = 3,  /* C = acc * (1 - aux[m][n]^2)               */
+};
+
+/* op flags */
+#define DGEN_HIP_OP_STATIC 1u /* run once, at configure (static temporality) */
+#define DGEN_HIP_OP_SIDE 2u   /* launch on the side stream (overlaps stream 0) */
+#define DGEN_HIP_OP_JOIN 4u   /* stream 0 waits for the side stream first    */
+
+#define DGEN_HIP_OP_NARG 32
+#define DGEN_HIP_OP_NFARG 8
+
+typedef struct dgen_hip_op {
+  uint32_t kernel; /* enum dgen_hip_kernel */
+  uint32_t flags;  /* DGEN_HIP_OP_* */
+  int64_t arg[DGEN_HIP_OP_NARG];
+  float farg[DGEN_HIP_OP_NFARG];
+} dgen_hip_op;
+
+typedef struct dgen_hip_kernel_time {
+  uint32_t index;  /* position in the schedule */
+  uint32_t kernel; /* enum dgen_hip_kernel */
+  float gpu_ms;    /* hipEvent time of the op's launches */
+} dgen_hip_kernel_time;
+
+/* ---- runtime ----------------------------------------------------------- */
+
+/* ABI version (DGEN_HIP_ABI_VERSION) and the device count. No device init
+ * beyond hipGetDeviceCount. */
+int dgen_hip_abi_version(void);
+int dgen_hip_device_count(int* out);
+
+/* Create a context on `device`: streams and events; no arena yet.
+ * Mirrors MetalCompiledKernel.init (MetalRuntime.swift:30-206). */
+int dgen_hip_create(int device, dgen_hip_ctx** out);
+/* Release everything the context owns (MetalRuntime.swift:572-588). */
+int dgen_hip_destroy(dgen_hip_ctx* ctx);
+/* Message of the last failing call on this thread ("" if none). */
+const char* dgen_hip_last_error(void);
+
+/* Allocate the device arena (memory_floats floats, zeroed) and its pinned
+ * host mirror, copy the schedule (the caller keeps ownership of `ops`),
+ * validate every op's cells against the arena, and run the STATIC ops.
+ * Mirrors initializeBuffers + kernel creation (MetalRuntime.swift:221-254).
+ * max_frames bounds dgen_hip_run's frame_count (maxFrameCount). */
+int dgen_hip_configure(dgen_hip_ctx* ctx, const dgen_hip_op* ops, uint32_t n_ops, uint64_t memory_floats,
+                       uint32_t max_frames);
+
+/* Host mirror of the arena (LazyRuntime.memoryPointer, Realize.swift:16).
+ * Valid until the next configure/destroy. */
+float* dgen_hip_host_memory(dgen_hip_ctx* ctx);
+/* Copy [off, off+n) host mirror -> device now (injectTensorData,
+ * Realize.swift:257-282). */
+int dgen_hip_upload(dgen_hip_ctx* ctx, uint64_t off, uint64_t n);
+/* Copy [off, off+n) device -> host mirror now (readOutputs / readGradients,
+ * Realize.swift:298-306, Backward.swift:132-165). */
+int dgen_hip_download(dgen_hip_ctx* ctx, uint64_t off, uint64_t n);
+/* Zero [off, off+n) on the device (n = 0: the whole arena); mirrors
+ * zeroAllBuffers (MetalRuntime.swift:265-281). */
+int dgen_hip_zero(dgen_hip_ctx* ctx, uint64_t off, uint64_t n);
+
+/* Enqueue every non-static op in schedule order and wait for completion
+ * (runNoCopy -> run, MetalRuntime.swift:283-342,676-698: synchronous on
+ * return).  Fails with DGEN_HIP_E_RANGE if frame_count > max_frames. */
+int dgen_hip_run(dgen_hip_ctx* ctx, uint32_t frame_count);
+/* As dgen_hip_run but returns without waiting; dgen_hip_sync waits. */
+int dgen_hip_run_async(dgen_hip_ctx* ctx, uint32_t frame_count);
+int dgen_hip_sync(dgen_hip_ctx* ctx);
+
+/* Run once with a hipEvent pair around every op; fills up to `cap` entries
+ * and sets *n_out.  Mirrors profileKernels (MetalRuntime.swift:397-425). */
+int dgen_hip_profile(dgen_hip_ctx* ctx, uint32_t frame_count, dgen_hip_kernel_time* out, size_t cap,
+                     size_t* n_out);
+
+/* Time `iters` back-to-back runs (after `warmup` untimed runs) with one
+ * hipEvent pair on stream 0; *ms_out = total milliseconds. */
+int dgen_hip_time_runs(dgen_hip_ctx* ctx, uint32_t frame_count, int warmup, int iters, double* ms_out);
+
+/* Average duration of the launches of schedule op `op_index` over `iters`
+ * runs, timed with hipEvents recorded on the stream that op launches on. */
+int dgen_hip_time_op(dgen_hip_ctx* ctx, uint32_t frame_count, uint32_t op_index, int iters, double* ms_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DGEN_HIP_H */

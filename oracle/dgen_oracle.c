@@ -1,0 +1,766 @@
+/*
+ * dgen_oracle.c -- CPU restatement of the DGen reference C-backend semantics
+ * for the five workloads served by the HIP backend.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the parity checker: only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.  The
+ * product path (libdgen_hip.so) never links, calls or falls back to it.
+ *
+ * One source, two builds:
+ *   -DREAL=float  -DSFX=_f32   emission-faithful fp32 (IEEE, no contraction):
+ *                              the forward parity reference and the CPU baseline
+ *   -DREAL=double -DSFX=_f64   the same program in fp64, for central finite
+ *                              differences of sum_frames(loss)
+ * Constants that the reference computes in Float (steps, windows, twiddles,
+ * 2*pi, noise samples) are rounded to fp32 in BOTH builds, so the f64 build is
+ * the exact-arithmetic version of the same fp32 program.
+ *
+ * Every function cites the reference file:line it restates (paths relative to
+ * the universalsequences/dgen-audio repository root).
+ *
+ * Pinning (see tests/test_oracle_*.py):
+ *   deterministic phasor  closed form + CBackendTests.swift:46-76 known answers
+ *   one-pole              impulse response 0.9^n (closed form)
+ *   stateful phasor       fp64 closed-form phase sum, pre-increment output
+ *   xorshift32 noise      bit-exact brute force of the published recurrence
+ *   sampleRow             closed-form linear interpolation with wrap
+ *   radix-2 FFT           brute-force DFT, impulse/DC/cosine, Parseval
+ *   spectral loss         identical signals -> 0, brute-force DFT magnitudes
+ *   MLP / heads           numpy restatement + finite differences
+ *   all analytic grads    central finite differences of the f64 build
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifndef REAL
+#define REAL float
+#define SFX _f32
+#endif
+
+#define CAT2(a, b) a##b
+#define CAT(a, b) CAT2(a, b)
+#define FN(name) CAT(name, SFX)
+
+#define IS_F32 (sizeof(REAL) == 4)
+#define R_SIN(x) (IS_F32 ? (REAL)sinf((float)(x)) : (REAL)sin((double)(x)))
+#define R_SQRT(x) (IS_F32 ? (REAL)sqrtf((float)(x)) : (REAL)sqrt((double)(x)))
+#define R_LOG(x) (IS_F32 ? (REAL)logf((float)(x)) : (REAL)log((double)(x)))
+#define R_EXP(x) (IS_F32 ? (REAL)expf((float)(x)) : (REAL)exp((double)(x)))
+#define R_TANH(x) (IS_F32 ? (REAL)tanhf((float)(x)) : (REAL)tanh((double)(x)))
+#define R_FLOOR(x) (IS_F32 ? (REAL)floorf((float)(x)) : (REAL)floor((double)(x)))
+#define R_FMOD(x, y) (IS_F32 ? (REAL)fmodf((float)(x), (float)(y)) : (REAL)fmod((double)(x), (double)(y)))
+#define R_ABS(x) (IS_F32 ? (REAL)fabsf((float)(x)) : (REAL)fabs((double)(x)))
+
+static inline REAL r_sign(REAL x) { return x > 0 ? (REAL)1 : (x < 0 ? (REAL)-1 : (REAL)0); }
+static inline REAL r_max(REAL a, REAL b) { return a >= b ? a : b; }
+static inline REAL r_min(REAL a, REAL b) { return a <= b ? a : b; }
+
+/* 2*Float.pi as Swift computes it in Float. */
+#define TWO_PI_F32 ((REAL)(2.0f * 3.14159265358979323846f))
+
+/* ------------------------------------------------------------------------ */
+/* Shared helpers (compiled once per build; names carry the suffix).        */
+/* ------------------------------------------------------------------------ */
+
+/* Non-finite output containment: toolchain/include/dgen_runtime.h:58-85,
+ * Sources/DGen/Renderer/CRenderer.swift:1021-1039 (every `out` store). */
+static inline REAL sanitize(REAL v) { return isfinite(v) ? v : (REAL)0; }
+
+/* u_accum: Sources/DGen/Definitions.swift:215-246.  Returns the
+ * pre-increment value and updates *state. */
+static inline REAL accum_step(REAL* state, REAL incr, REAL reset, REAL mn, REAL mx) {
+  REAL acc = *state;
+  REAL span = mx - mn;
+  REAL next = reset > 0 ? mn : acc + incr;
+  REAL k = R_FLOOR((next - mn) / span);
+  REAL w = next - k * span;
+  if (w >= mx) w = w - span;
+  if (reset > 0) w = mn;
+  *state = w;
+  return acc;
+}
+
+/* Tensor stateful phasor: Sources/DGen/Emit+State.swift:322-369
+ * (incr = freq / sampleRate; floor-wrap; >=1 correction; pre-increment out).
+ * Always fp32: the phase depends on no parameter (f0 is data). */
+static inline float phasor_step(float* state, float freq, float sr) {
+  float prev = *state;
+  float incr = freq / sr;
+  float next = prev + incr;
+  float w = next - floorf(next);
+  if (w >= 1.0f) w = w - 1.0f;
+  *state = w;
+  return prev;
+}
+
+/* xorshift32 noise: Sources/DGen/Renderer/CRenderer.swift:685-693.  The state
+ * lives in a zeroed float cell; 0 is replaced by 1 before the update. */
+static inline float noise_step(uint32_t* s) {
+  uint32_t x = *s;
+  if (x == 0u) x = 1u;
+  x ^= x << 13;
+  x ^= x >> 17;
+  x ^= x << 5;
+  *s = x;
+  return (float)x / 4294967296.0f;
+}
+
+/* sampleInline row lookup: Sources/DGen/Emit+RowSelection.swift:164-197.
+ * The row index and weights depend on no parameter: fp32 in both builds. */
+typedef struct {
+  int lo, hi;
+  float frac, omf;
+} RowLerp;
+static inline RowLerp row_lerp(float index, int rows) {
+  RowLerp r;
+  float nr = (float)rows;
+  float w = fmodf(index, nr);
+  if (w < 0) w = w + nr;
+  float fl = floorf(w);
+  float ce = fl + 1.0f;
+  if (ce >= nr) ce = 0;
+  r.frac = w - fl;
+  r.omf = 1.0f - r.frac;
+  r.lo = (int)fl;
+  r.hi = (int)ce;
+  return r;
+}
+/* Interpolated read of a parameter-dependent value (REAL arithmetic). */
+static inline REAL lerp_rows(const RowLerp* r, REAL a, REAL b) { return (REAL)r->omf * a + (REAL)r->frac * b; }
+/* Interpolated read of data (f0, uv): fp32 in both builds. */
+static inline float lerp_data(const RowLerp* r, float a, float b) { return r->omf * a + r->frac * b; }
+
+/* ------------------------------------------------------------------------ */
+/* Config 1: deterministic phasor bank -> sum -> one-pole history.          */
+/* ------------------------------------------------------------------------ */
+
+/* deterministicPhasor: Sources/DGen/Emit+State.swift:370-387;
+ * Signal.phasor(Tensor): Sources/DGenLazy/SignalTensor.swift:67-80.
+ * sin(phase * 2pi): Sources/DGen/Renderer/CRenderer.swift:825-827.
+ * history one-pole y = x + 0.9*y[n-1]: Sources/DGen/Emit+State.swift:150-224
+ * (read returns the previous frame's write). */
+void FN(dgen_oracle_oscbank)(const float* freqs, const float* amps, int n_osc, float sr, float pole,
+                             int frames, float* out) {
+  REAL y = 0;
+  for (int n = 0; n < frames; ++n) {
+    REAL x = 0;
+    for (int k = 0; k < n_osc; ++k) {
+      REAL inc = (REAL)freqs[k] / (REAL)sr;
+      REAL raw = inc * (REAL)n;
+      REAL phase = raw - R_FLOOR(raw);
+      x = x + R_SIN(phase * TWO_PI_F32) * (REAL)amps[k];
+    }
+    y = x + (REAL)pole * y;
+    out[n] = (float)sanitize(y);
+  }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Config 3: batched harmonic + FIR-noise synth, MLP decoder, MSS loss.      */
+/* ------------------------------------------------------------------------ */
+
+/* Control layout: one row of NC = K + 2 + NF floats per (b, f), row index
+ * m = b*F + f (reference: controls.reshape([B, F, ...]),
+ * Examples/HarmonicE2E/Synth.swift:72-75).  Columns: [0,K) harmonic amps,
+ * K harmonic gain, K+1 noise gain, [K+2, K+2+NF) FIR taps. */
+
+/* The playhead of Examples/HarmonicE2E/Synth.swift:60-71: accum of
+ * step = (F-1)/(T-1) wrapping at F-1, clipped to [0, F-1-1e-4].  It depends
+ * on no parameter, so both builds evaluate it in fp32 exactly as the C backend
+ * does (the fp32 accumulation drifts and can wrap to row 0 in the last frames
+ * of long runs; that is reference behaviour). */
+static void playhead_real(int F, int T, REAL* out) {
+  float fmaxi = (float)(F > 1 ? F - 1 : 0);
+  float denom = (float)(T > 2 ? T - 1 : 1);
+  float step = fmaxi / denom;
+  float hi = fmaxi - 1e-4f > 0.f ? fmaxi - 1e-4f : 0.f;
+  float st = 0;
+  for (int t = 0; t < T; ++t) {
+    float acc = st;
+    float next = acc + step;
+    float k = floorf(next / fmaxi);
+    float w = next - k * fmaxi;
+    if (w >= fmaxi) w = w - fmaxi;
+    st = w;
+    float p = acc < 0.f ? 0.f : acc;
+    out[t] = (REAL)(p > hi ? hi : p);
+  }
+}
+void FN(dgen_oracle_playhead)(int F, int T, float* out) {
+  REAL* p = (REAL*)malloc(sizeof(REAL) * T);
+  playhead_real(F, T, p);
+  for (int t = 0; t < T; ++t) out[t] = (float)p[t];
+  free(p);
+}
+
+/* The shared xorshift32 stream of Signal.noise() for T frames, starting from
+ * a zeroed cell (CRenderer.swift:685-693).  Precision-independent: emitted
+ * once, by the fp32 build. */
+void dgen_oracle_noise_stream(int T, float* out);
+#ifdef ORACLE_COMMON
+void dgen_oracle_noise_stream(int T, float* out) {
+  uint32_t s = 0;
+  for (int t = 0; t < T; ++t) out[t] = noise_step(&s);
+}
+#endif
+
+/* Forward synth: HarmonicSynth.renderBatchedSignal,
+ * Examples/HarmonicE2E/Synth.swift:47-102, with nyquistNormalizedHarmonicsBatched
+ * (:158-167).  ctrl: [B*F][NC]; f0, uv: [F][B]; y: [B][T] (lane-major).
+ * Frame-sequential exactly like the C backend: per frame the playhead accum,
+ * the sampleRow reads, the tensor phasor update and the noise buffer write.
+ * With dy != NULL it instead accumulates the adjoint into dctrl (the graph AD
+ * of the same expressions: Gradients.swift rules for mul/div/sum and the
+ * sampleInline gradient scatter, Emit+RowSelection.swift:100-141; f0, uv and
+ * noise are data and carry no gradient). */
+static void synth_core(const REAL* ctrl, const float* f0, const float* uv, int B, int F, int T, int K, int NF,
+                       float sr, float hscale, float nscale, REAL* y, const REAL* dy, REAL* dctrl) {
+  const int NC = K + 2 + NF;
+  REAL* play = (REAL*)malloc(sizeof(REAL) * T);
+  float* noise = (float*)malloc(sizeof(float) * T);
+  float* ph = (float*)calloc((size_t)B * K, sizeof(float));
+  float* freq = (float*)malloc(sizeof(float) * K);
+  REAL* masked = (REAL*)malloc(sizeof(REAL) * K);
+  REAL* sines = (REAL*)malloc(sizeof(REAL) * K);
+  playhead_real(F, T, play);
+  dgen_oracle_noise_stream(T, noise);
+  if (dctrl) memset(dctrl, 0, sizeof(REAL) * (size_t)B * F * NC);
+  const float nyq = sr * 0.5f;
+  for (int t = 0; t < T; ++t) {
+    RowLerp r = row_lerp((float)play[t], F);
+    for (int b = 0; b < B; ++b) {
+      const REAL* c0 = ctrl + (size_t)(b * F + r.lo) * NC;
+      const REAL* c1 = ctrl + (size_t)(b * F + r.hi) * NC;
+      float f0i = lerp_data(&r, f0[r.lo * B + b], f0[r.hi * B + b]);
+      REAL uvi = (REAL)lerp_data(&r, uv[r.lo * B + b], uv[r.hi * B + b]);
+      REAL den = 0;
+      for (int k = 0; k < K; ++k) {
+        freq[k] = (float)(k + 1) * f0i;
+        REAL a = lerp_rows(&r, c0[k], c1[k]);
+        masked[k] = a * (freq[k] < nyq ? (REAL)1 : (REAL)0);
+        den = den + masked[k];
+      }
+      den = den + (REAL)1e-8f;
+      REAL hsum = 0;
+      for (int k = 0; k < K; ++k) {
+        float p = phasor_step(&ph[b * K + k], freq[k], sr);
+        sines[k] = R_SIN((REAL)(p * (2.0f * 3.14159265358979323846f)));
+        hsum = hsum + sines[k] * (masked[k] / den);
+      }
+      REAL gain = lerp_rows(&r, c0[K], c1[K]);
+      REAL ngain = lerp_rows(&r, c0[K + 1], c1[K + 1]);
+      /* bufferView window: oldest first, ends at the current frame, zero
+       * before frame 0 (HigherOps.swift:738-792). */
+      REAL filt = 0;
+      for (int i = 0; i < NF; ++i) {
+        int tt = t - (NF - 1) + i;
+        REAL w = tt >= 0 ? (REAL)noise[tt] : (REAL)0;
+        filt = filt + w * lerp_rows(&r, c0[K + 2 + i], c1[K + 2 + i]);
+      }
+      REAL hout = ((hsum * gain) * uvi) * (REAL)hscale;
+      REAL nout = ((filt * ngain) * (REAL)0.12f) * (REAL)nscale;
+      if (y) y[(size_t)b * T + t] = sanitize(hout + nout);
+      if (!dy) continue;
+      REAL* d0 = dctrl + (size_t)(b * F + r.lo) * NC;
+      REAL* d1 = dctrl + (size_t)(b * F + r.hi) * NC;
+      const REAL omf = (REAL)r.omf, frac = (REAL)r.frac;
+      REAL g = dy[(size_t)b * T + t];
+      REAL dhsum = g * gain * uvi * (REAL)hscale;
+      REAL dgain = g * hsum * uvi * (REAL)hscale;
+      /* amps = masked/den:  d masked_k = (dA_k - sum_j dA_j amps_j) / den */
+      REAL dot = 0;
+      for (int k = 0; k < K; ++k) dot = dot + dhsum * sines[k] * (masked[k] / den);
+      for (int k = 0; k < K; ++k) {
+        REAL mk = freq[k] < nyq ? (REAL)1 : (REAL)0;
+        REAL dm = (dhsum * sines[k] - dot) / den * mk;
+        d0[k] += omf * dm;
+        d1[k] += frac * dm;
+      }
+      d0[K] += omf * dgain;
+      d1[K] += frac * dgain;
+      REAL dfilt = g * ngain * (REAL)0.12f * (REAL)nscale;
+      REAL dngain = g * filt * (REAL)0.12f * (REAL)nscale;
+      d0[K + 1] += omf * dngain;
+      d1[K + 1] += frac * dngain;
+      for (int i = 0; i < NF; ++i) {
+        int tt = t - (NF - 1) + i;
+        REAL w = tt >= 0 ? (REAL)noise[tt] : (REAL)0;
+        d0[K + 2 + i] += omf * (dfilt * w);
+        d1[K + 2 + i] += frac * (dfilt * w);
+      }
+    }
+  }
+  free(play);
+  free(noise);
+  free(ph);
+  free(freq);
+  free(masked);
+  free(sines);
+}
+
+static REAL* to_real(const float* a, size_t n) {
+  REAL* r = (REAL*)malloc(sizeof(REAL) * (n ? n : 1));
+  for (size_t i = 0; i < n; ++i) r[i] = (REAL)a[i];
+  return r;
+}
+static void to_float(const REAL* a, size_t n, float* out) {
+  for (size_t i = 0; i < n; ++i) out[i] = (float)a[i];
+}
+
+void FN(dgen_oracle_synth_fwd)(const float* ctrl, const float* f0, const float* uv, int B, int F, int T, int K,
+                               int NF, float sr, float hscale, float nscale, float* y) {
+  size_t nc = (size_t)B * F * (K + 2 + NF);
+  REAL* c = to_real(ctrl, nc);
+  REAL* yr = (REAL*)malloc(sizeof(REAL) * (size_t)B * T);
+  synth_core(c, f0, uv, B, F, T, K, NF, sr, hscale, nscale, yr, NULL, NULL);
+  to_float(yr, (size_t)B * T, y);
+  free(c);
+  free(yr);
+}
+
+void FN(dgen_oracle_synth_bwd)(const float* ctrl, const float* f0, const float* uv, const float* dy, int B, int F,
+                               int T, int K, int NF, float sr, float hscale, float nscale, float* dctrl) {
+  size_t nc = (size_t)B * F * (K + 2 + NF);
+  REAL* c = to_real(ctrl, nc);
+  REAL* d = to_real(dy, (size_t)B * T);
+  REAL* dc = (REAL*)malloc(sizeof(REAL) * nc);
+  synth_core(c, f0, uv, B, F, T, K, NF, sr, hscale, nscale, NULL, d, dc);
+  to_float(dc, nc, dctrl);
+  free(c);
+  free(d);
+  free(dc);
+}
+
+/* softplus(x) = max(x,0) + log(1 + exp(-|x|)): Examples/HarmonicE2E/Model.swift:153-157. */
+static inline REAL softplus(REAL x) { return r_max(x, 0) + R_LOG((REAL)1 + R_EXP(-R_ABS(x))); }
+/* Its derivative through the reference's AD rules (Gradients.swift:398-408 max,
+ * :429-433 abs, :479-490 exp/log): [x>=0] - sign(x)*e^{-|x|}/(1+e^{-|x|}). */
+static inline REAL softplus_grad(REAL x) {
+  REAL e = R_EXP(-R_ABS(x));
+  return (x >= 0 ? (REAL)1 : (REAL)0) - r_sign(x) * (e / ((REAL)1 + e));
+}
+
+/* Parameter blob layout (floats, this order): W1[DIN][H] b1[H] W2[H][H] b2[H]
+ * ... (L trunk layers), then Wh[H][NC] bh[NC], where the head columns
+ * concatenate W_harm | W_gain | W_noise | W_noiseFilter
+ * (Examples/HarmonicE2E/Model.swift:36-83). */
+static size_t mlp_param_count(int din, int hid, int layers, int nc) {
+  size_t n = 0;
+  for (int l = 0; l < layers; ++l) n += (size_t)(l == 0 ? din : hid) * hid + hid;
+  return n + (size_t)hid * nc + nc;
+}
+size_t FN(dgen_oracle_mlp_param_count)(int din, int hid, int layers, int nc) {
+  return mlp_param_count(din, hid, layers, nc);
+}
+
+/* HarmonicDecoderModel.forward: Examples/HarmonicE2E/Model.swift:96-120.
+ * X: [M][DIN].  acts (optional, L*M*H) keeps the trunk outputs for the
+ * backward; zh (optional): head pre-activations [M][NC]; ctrl: [M][NC]. */
+static void mlp_forward(const float* X, const REAL* P, int M, int din, int hid, int layers, int K, int NF,
+                        REAL* acts, REAL* zh, REAL* ctrl) {
+  const int NC = K + 2 + NF;
+  REAL* h = (REAL*)malloc(sizeof(REAL) * (hid > din ? hid : din));
+  REAL* hn = (REAL*)malloc(sizeof(REAL) * hid);
+  REAL* z = (REAL*)malloc(sizeof(REAL) * NC);
+  for (int m = 0; m < M; ++m) {
+    const REAL* p = P;
+    int fan = din;
+    for (int i = 0; i < din; ++i) h[i] = (REAL)X[(size_t)m * din + i];
+    for (int l = 0; l < layers; ++l) {
+      const REAL* W = p;
+      const REAL* bb = p + (size_t)fan * hid;
+      for (int j = 0; j < hid; ++j) {
+        REAL s = 0;
+        for (int i = 0; i < fan; ++i) s = s + h[i] * W[(size_t)i * hid + j];
+        hn[j] = R_TANH(s + bb[j]);
+      }
+      memcpy(h, hn, sizeof(REAL) * hid);
+      if (acts) memcpy(acts + ((size_t)l * M + m) * hid, h, sizeof(REAL) * hid);
+      p += (size_t)fan * hid + hid;
+      fan = hid;
+    }
+    const REAL* Wh = p;
+    const REAL* bh = p + (size_t)hid * NC;
+    for (int c = 0; c < NC; ++c) {
+      REAL s = 0;
+      for (int i = 0; i < hid; ++i) s = s + h[i] * Wh[(size_t)i * NC + c];
+      z[c] = s + bh[c];
+      if (zh) zh[(size_t)m * NC + c] = z[c];
+    }
+    REAL* out = ctrl + (size_t)m * NC;
+    /* harmonic amps: softplus, normalised by sum + 1e-6 (Model.swift:102-106) */
+    REAL den = 0;
+    for (int k = 0; k < K; ++k) den = den + softplus(z[k]);
+    den = den + (REAL)1e-6f;
+    for (int k = 0; k < K; ++k) out[k] = softplus(z[k]) / den;
+    out[K] = softplus(z[K]);         /* harmonic gain (:107) */
+    out[K + 1] = softplus(z[K + 1]); /* noise gain (:108) */
+    /* FIR taps: tanh, normalised by sum|.| + 1e-4 (:109-113) */
+    REAL nrm = 0;
+    for (int i = 0; i < NF; ++i) nrm = nrm + R_ABS(R_TANH(z[K + 2 + i]));
+    nrm = nrm + (REAL)1e-4f;
+    for (int i = 0; i < NF; ++i) out[K + 2 + i] = R_TANH(z[K + 2 + i]) / nrm;
+  }
+  free(h);
+  free(hn);
+  free(z);
+}
+
+/* Backward of the MLP + heads (graph AD of Model.swift:96-120 with the rules
+ * of Gradients.swift: matmul/sum, tanh :470-477, softplus via max/abs/exp/log).
+ * dctrl: [M][NC]; dP: same layout as P (overwritten). */
+static void mlp_backward(const float* X, const REAL* P, const REAL* dctrl, int M, int din, int hid, int layers,
+                         int K, int NF, REAL* dP) {
+  const int NC = K + 2 + NF;
+  size_t np = mlp_param_count(din, hid, layers, NC);
+  REAL* acts = (REAL*)malloc(sizeof(REAL) * (size_t)layers * M * hid);
+  REAL* zh = (REAL*)malloc(sizeof(REAL) * (size_t)M * NC);
+  REAL* ctrl = (REAL*)malloc(sizeof(REAL) * (size_t)M * NC);
+  memset(dP, 0, sizeof(REAL) * np);
+  mlp_forward(X, P, M, din, hid, layers, K, NF, acts, zh, ctrl);
+  size_t* woff = (size_t*)malloc(sizeof(size_t) * (layers + 1));
+  size_t off = 0;
+  for (int l = 0; l < layers; ++l) {
+    woff[l] = off;
+    off += (size_t)(l == 0 ? din : hid) * hid + hid;
+  }
+  woff[layers] = off;
+  REAL* dz = (REAL*)malloc(sizeof(REAL) * NC);
+  REAL* dh = (REAL*)malloc(sizeof(REAL) * hid);
+  REAL* dhp = (REAL*)malloc(sizeof(REAL) * hid);
+  for (int m = 0; m < M; ++m) {
+    const REAL* z = zh + (size_t)m * NC;
+    const REAL* dc = dctrl + (size_t)m * NC;
+    REAL den = 0;
+    for (int k = 0; k < K; ++k) den = den + softplus(z[k]);
+    den = den + (REAL)1e-6f;
+    REAL dot = 0;
+    for (int k = 0; k < K; ++k) dot = dot + dc[k] * (softplus(z[k]) / den);
+    for (int k = 0; k < K; ++k) dz[k] = (dc[k] - dot) / den * softplus_grad(z[k]);
+    dz[K] = dc[K] * softplus_grad(z[K]);
+    dz[K + 1] = dc[K + 1] * softplus_grad(z[K + 1]);
+    REAL nrm = 0;
+    for (int i = 0; i < NF; ++i) nrm = nrm + R_ABS(R_TANH(z[K + 2 + i]));
+    nrm = nrm + (REAL)1e-4f;
+    REAL dot2 = 0;
+    for (int i = 0; i < NF; ++i) dot2 = dot2 + dc[K + 2 + i] * (R_TANH(z[K + 2 + i]) / nrm);
+    for (int i = 0; i < NF; ++i) {
+      REAL s = R_TANH(z[K + 2 + i]);
+      REAL ds = (dc[K + 2 + i] - r_sign(s) * dot2) / nrm;
+      dz[K + 2 + i] = ds * ((REAL)1 - s * s);
+    }
+    const REAL* h3 = acts + ((size_t)(layers - 1) * M + m) * hid;
+    const REAL* Wh = P + woff[layers];
+    REAL* dWh = dP + woff[layers];
+    REAL* dbh = dWh + (size_t)hid * NC;
+    for (int c = 0; c < NC; ++c) dbh[c] += dz[c];
+    for (int i = 0; i < hid; ++i) {
+      REAL s = 0;
+      for (int c = 0; c < NC; ++c) {
+        dWh[(size_t)i * NC + c] += h3[i] * dz[c];
+        s = s + dz[c] * Wh[(size_t)i * NC + c];
+      }
+      dh[i] = s;
+    }
+    for (int l = layers - 1; l >= 0; --l) {
+      int fan = l == 0 ? din : hid;
+      const REAL* hl = acts + ((size_t)l * M + m) * hid;
+      const REAL* W = P + woff[l];
+      REAL* dW = dP + woff[l];
+      REAL* db = dW + (size_t)fan * hid;
+      for (int j = 0; j < hid; ++j) dh[j] = dh[j] * ((REAL)1 - hl[j] * hl[j]);
+      for (int j = 0; j < hid; ++j) db[j] += dh[j];
+      for (int i = 0; i < fan; ++i) {
+        REAL hin = l == 0 ? (REAL)X[(size_t)m * din + i] : acts[((size_t)(l - 1) * M + m) * hid + i];
+        REAL s = 0;
+        for (int j = 0; j < hid; ++j) {
+          dW[(size_t)i * hid + j] += hin * dh[j];
+          s = s + dh[j] * W[(size_t)i * hid + j];
+        }
+        if (l > 0) dhp[i] = s;
+      }
+      if (l > 0) memcpy(dh, dhp, sizeof(REAL) * hid);
+    }
+  }
+  free(acts);
+  free(zh);
+  free(ctrl);
+  free(woff);
+  free(dz);
+  free(dh);
+  free(dhp);
+}
+
+void FN(dgen_oracle_mlp_fwd)(const float* X, const float* P, int M, int din, int hid, int layers, int K, int NF,
+                             float* ctrl) {
+  size_t np = mlp_param_count(din, hid, layers, K + 2 + NF);
+  REAL* p = to_real(P, np);
+  REAL* c = (REAL*)malloc(sizeof(REAL) * (size_t)M * (K + 2 + NF));
+  mlp_forward(X, p, M, din, hid, layers, K, NF, NULL, NULL, c);
+  to_float(c, (size_t)M * (K + 2 + NF), ctrl);
+  free(p);
+  free(c);
+}
+
+void FN(dgen_oracle_mlp_bwd)(const float* X, const float* P, const float* dctrl, int M, int din, int hid,
+                             int layers, int K, int NF, float* dP_out) {
+  size_t np = mlp_param_count(din, hid, layers, K + 2 + NF);
+  REAL* p = to_real(P, np);
+  REAL* dc = to_real(dctrl, (size_t)M * (K + 2 + NF));
+  REAL* dp = (REAL*)malloc(sizeof(REAL) * np);
+  mlp_backward(X, p, dc, M, din, hid, layers, K, NF, dp);
+  to_float(dp, np, dP_out);
+  free(p);
+  free(dc);
+  free(dp);
+}
+
+/* ---- radix-2 FFT exactly as the spectral-loss kernels emit it ----------- */
+/* Tables: Sources/DGen/HigherOps.swift:71-99 (symmetric Hann over N-1, Float
+ * twiddles cos/sin(2*pi*k/(2*half)) at offset half-1, bit reversal).        */
+typedef struct {
+  int n, stages;
+  float* hann;
+  float* twre;
+  float* twim;
+  int* bitrev;
+} FftTables;
+
+static void fft_tables_init(FftTables* t, int n) {
+  t->n = n;
+  t->stages = 0;
+  while ((1 << t->stages) < n) t->stages++;
+  t->hann = (float*)malloc(sizeof(float) * n);
+  t->twre = (float*)malloc(sizeof(float) * (n > 1 ? n - 1 : 1));
+  t->twim = (float*)malloc(sizeof(float) * (n > 1 ? n - 1 : 1));
+  t->bitrev = (int*)malloc(sizeof(int) * n);
+  for (int i = 0; i < n; ++i) t->hann[i] = (float)(0.5 * (1.0 - cos(2.0 * M_PI * (double)i / (double)(n - 1))));
+  for (int s = 0; s < t->stages; ++s) {
+    int half = 1 << s;
+    for (int k = 0; k < half; ++k) {
+      double ang = 2.0 * M_PI * (double)k / (double)(2 * half);
+      t->twre[half - 1 + k] = (float)cos(ang);
+      t->twim[half - 1 + k] = (float)sin(ang);
+    }
+  }
+  for (int i = 0; i < n; ++i) {
+    int rev = 0, bits = i;
+    for (int s = 0; s < t->stages; ++s) {
+      rev = rev * 2 + (bits & 1);
+      bits >>= 1;
+    }
+    t->bitrev[i] = rev;
+  }
+}
+static void fft_tables_free(FftTables* t) {
+  free(t->hann);
+  free(t->twre);
+  free(t->twim);
+  free(t->bitrev);
+}
+
+/* In-place radix-2 DIT, forward (twiddle exp(-i...)) when sign<0, inverse
+ * without 1/N when sign>0: Emit+SpectralLoss.swift:802-848 (forward),
+ * :1085-1160 (gradient IFFT). */
+static void fft_inplace(const FftTables* t, REAL* re, REAL* im, int sign) {
+  int n = t->n;
+  for (int i = 0; i < n; ++i) {
+    int r = t->bitrev[i];
+    if (i < r) {
+      REAL a = re[i];
+      re[i] = re[r];
+      re[r] = a;
+      a = im[i];
+      im[i] = im[r];
+      im[r] = a;
+    }
+  }
+  for (int s = 0; s < t->stages; ++s) {
+    int half = 1 << s, size = half * 2;
+    for (int g = 0; g < n / size; ++g) {
+      for (int k = 0; k < half; ++k) {
+        REAL wr = (REAL)t->twre[half - 1 + k];
+        REAL wi = sign < 0 ? -(REAL)t->twim[half - 1 + k] : (REAL)t->twim[half - 1 + k];
+        int i = g * size + k, j = i + half;
+        REAL tr = wr * re[j] - wi * im[j];
+        REAL ti = wr * im[j] + wi * re[j];
+        REAL ar = re[i], ai = im[i];
+        re[i] = ar + tr;
+        im[i] = ai + ti;
+        re[j] = ar - tr;
+        im[j] = ai - ti;
+      }
+    }
+  }
+}
+
+/* Forward FFT of one hop window ending at frame f (window covers f-N+1..f,
+ * zero outside [0,T)): Emit+SpectralLoss.swift:776-800. */
+static void window_fft(const FftTables* tb, const REAL* x, int T, int f, REAL* re, REAL* im) {
+  int n = tb->n;
+  for (int i = 0; i < n; ++i) {
+    int tt = f - (n - 1) + i;
+    REAL s = (tt >= 0 && tt < T) ? x[tt] : (REAL)0;
+    re[i] = s * (REAL)tb->hann[i];
+    im[i] = 0;
+  }
+  fft_inplace(tb, re, im, -1);
+}
+
+#define LOG_EPS ((REAL)1e-8f) /* DGenSpectralConfig.logMagnitudeEpsilon, GradientConfig.swift:38 */
+
+/* Multi-scale spectral loss, HarmonicE2E Trainer.fullBatchedLoss
+ * (Examples/HarmonicE2E/Trainer.swift:538-583) over spectralLossFFTBatched +
+ * BatchedReduce (Emit+SpectralLoss.swift:719-938) with normalize
+ * (Sources/DGenLazy/Functions.swift:945-955: / maxFrameCount).
+ * x, tgt: [B][T].  lf[T]: the per-frame loss signal.
+ * With dx != NULL also writes d sum_frames(loss) / d x: GradSpec
+ * (Emit+SpectralLoss.swift:940-1030: sign(diff), /(mag+eps) for log,
+ * * X/max(|X|,1e-8), bins above N/2 zeroed), unnormalised positive-twiddle
+ * IFFT (:1032-1160), window multiply, and the per-sample gather over the hop
+ * windows containing it (:1163-1235). */
+static double mss_core(const REAL* x, const REAL* tgt, int B, int T, const int* sizes, int n_sizes, int hop_div,
+                       float w_lin, float w_log, float max_frames, REAL* lf, REAL* dx) {
+  memset(lf, 0, sizeof(REAL) * T);
+  if (dx) memset(dx, 0, sizeof(REAL) * (size_t)B * T);
+  for (int si = 0; si < n_sizes; ++si) {
+    int N = sizes[si], H = N / hop_div > 0 ? N / hop_div : 1;
+    FftTables tb;
+    fft_tables_init(&tb, N);
+    REAL *r1 = (REAL*)malloc(sizeof(REAL) * N), *i1 = (REAL*)malloc(sizeof(REAL) * N);
+    REAL *r2 = (REAL*)malloc(sizeof(REAL) * N), *i2 = (REAL*)malloc(sizeof(REAL) * N);
+    REAL *gr = (REAL*)malloc(sizeof(REAL) * N), *gi = (REAL*)malloc(sizeof(REAL) * N);
+    REAL wl = (REAL)(w_lin / (float)n_sizes), wg = (REAL)(w_log / (float)n_sizes);
+    /* upstream gradient of each batched spectral node, scaled by 1/B (:960) */
+    REAL gl = wl / (REAL)max_frames / (REAL)B;
+    REAL gg = wg / (REAL)max_frames / (REAL)B;
+    for (int f = 0; f < T; f += H) {
+      REAL lin = 0, lg = 0;
+      for (int b = 0; b < B; ++b) {
+        window_fft(&tb, x + (size_t)b * T, T, f, r1, i1);
+        window_fft(&tb, tgt + (size_t)b * T, T, f, r2, i2);
+        REAL bl = 0, bg = 0;
+        for (int k = 0; k < N; ++k) gr[k] = gi[k] = 0;
+        for (int k = 0; k <= N / 2; ++k) {
+          REAL m1 = R_SQRT(r1[k] * r1[k] + i1[k] * i1[k]);
+          REAL m2 = R_SQRT(r2[k] * r2[k] + i2[k] * i2[k]);
+          REAL dlog = R_LOG(m1 + LOG_EPS) - R_LOG(m2 + LOG_EPS);
+          bl = bl + R_ABS(m1 - m2);
+          bg = bg + R_ABS(dlog);
+          if (dx) {
+            REAL dmag = gl * r_sign(m1 - m2) + gg * r_sign(dlog) / (m1 + LOG_EPS);
+            REAL sm = r_max(m1, (REAL)1e-8f);
+            gr[k] = dmag * r1[k] / sm;
+            gi[k] = dmag * i1[k] / sm;
+          }
+        }
+        lin = lin + bl;
+        lg = lg + bg;
+        if (dx) {
+          fft_inplace(&tb, gr, gi, +1);
+          for (int i = 0; i < N; ++i) {
+            int tt = f - (N - 1) + i;
+            if (tt >= 0 && tt < T) dx[(size_t)b * T + tt] += gr[i] * (REAL)tb.hann[i];
+          }
+        }
+      }
+      lin = lin / (REAL)B / (REAL)max_frames;
+      lg = lg / (REAL)B / (REAL)max_frames;
+      lf[f] = lf[f] + lin * wl + lg * wg;
+    }
+    free(r1);
+    free(i1);
+    free(r2);
+    free(i2);
+    free(gr);
+    free(gi);
+    fft_tables_free(&tb);
+  }
+  double total = 0;
+  for (int t = 0; t < T; ++t) total += (double)lf[t];
+  return total;
+}
+
+double FN(dgen_oracle_mss_fwd)(const float* x, const float* tgt, int B, int T, const int* sizes, int n_sizes,
+                               int hop_div, float w_lin, float w_log, float max_frames, float* loss_frames) {
+  REAL* xr = to_real(x, (size_t)B * T);
+  REAL* tr = to_real(tgt, (size_t)B * T);
+  REAL* lf = (REAL*)malloc(sizeof(REAL) * T);
+  double tot = mss_core(xr, tr, B, T, sizes, n_sizes, hop_div, w_lin, w_log, max_frames, lf, NULL);
+  if (loss_frames) to_float(lf, T, loss_frames);
+  free(xr);
+  free(tr);
+  free(lf);
+  return tot;
+}
+
+void FN(dgen_oracle_mss_bwd)(const float* x, const float* tgt, int B, int T, const int* sizes, int n_sizes,
+                             int hop_div, float w_lin, float w_log, float max_frames, float* dx_out) {
+  REAL* xr = to_real(x, (size_t)B * T);
+  REAL* tr = to_real(tgt, (size_t)B * T);
+  REAL* lf = (REAL*)malloc(sizeof(REAL) * T);
+  REAL* dx = (REAL*)malloc(sizeof(REAL) * (size_t)B * T);
+  mss_core(xr, tr, B, T, sizes, n_sizes, hop_div, w_lin, w_log, max_frames, lf, dx);
+  to_float(dx, (size_t)B * T, dx_out);
+  free(xr);
+  free(tr);
+  free(lf);
+  free(dx);
+}
+
+/* One whole config-3 training step in this build's precision: MLP -> synth ->
+ * MSS loss, and (dP != NULL) the full backward to the parameters.  P and dP
+ * use REAL (double in the fp64 build), so finite differences can perturb the
+ * parameters far below fp32 resolution.  tgt: [B][T].  y_out (optional): the
+ * prediction.  Returns sum_frames(loss). */
+double FN(dgen_oracle_harmonic_step)(const float* X, const REAL* P, const float* f0, const float* uv,
+                                     const float* tgt, int B, int F, int T, int K, int NF, int din, int hid,
+                                     int layers, float sr, float hscale, float nscale, const int* sizes,
+                                     int n_sizes, int hop_div, float w_lin, float w_log, float max_frames,
+                                     REAL* dP, float* y_out) {
+  const int NC = K + 2 + NF;
+  const int M = B * F;
+  REAL* ctrl = (REAL*)malloc(sizeof(REAL) * (size_t)M * NC);
+  REAL* y = (REAL*)malloc(sizeof(REAL) * (size_t)B * T);
+  REAL* tr = to_real(tgt, (size_t)B * T);
+  REAL* lf = (REAL*)malloc(sizeof(REAL) * T);
+  mlp_forward(X, P, M, din, hid, layers, K, NF, NULL, NULL, ctrl);
+  synth_core(ctrl, f0, uv, B, F, T, K, NF, sr, hscale, nscale, y, NULL, NULL);
+  if (y_out) to_float(y, (size_t)B * T, y_out);
+  double tot;
+  if (dP) {
+    REAL* dy = (REAL*)malloc(sizeof(REAL) * (size_t)B * T);
+    REAL* dc = (REAL*)malloc(sizeof(REAL) * (size_t)M * NC);
+    tot = mss_core(y, tr, B, T, sizes, n_sizes, hop_div, w_lin, w_log, max_frames, lf, dy);
+    synth_core(ctrl, f0, uv, B, F, T, K, NF, sr, hscale, nscale, NULL, dy, dc);
+    mlp_backward(X, P, dc, M, din, hid, layers, K, NF, dP);
+    free(dy);
+    free(dc);
+  } else {
+    tot = mss_core(y, tr, B, T, sizes, n_sizes, hop_div, w_lin, w_log, max_frames, lf, NULL);
+  }
+  free(ctrl);
+  free(y);
+  free(tr);
+  free(lf);
+  return tot;
+}
+
+/* Adam.step: Sources/DGenLazy/Optimizers.swift:164-204 (bias corrections in
+ * Float, update p -= lr*mHat/(sqrt(vHat)+eps)). step = t after increment. */
+void FN(dgen_oracle_adam)(float* p, const float* g, float* m, float* v, size_t n, float lr, float b1, float b2,
+                          float eps, int step) {
+  float bc1 = 1.0f - powf(b1, (float)step);
+  float bc2 = 1.0f - powf(b2, (float)step);
+  for (size_t j = 0; j < n; ++j) {
+    REAL gj = g[j];
+    REAL mj = (REAL)b1 * (REAL)m[j] + ((REAL)1 - (REAL)b1) * gj;
+    REAL vj = (REAL)b2 * (REAL)v[j] + ((REAL)1 - (REAL)b2) * gj * gj;
+    REAL mh = mj / (REAL)bc1, vh = vj / (REAL)bc2;
+    p[j] = (float)((REAL)p[j] - (REAL)lr * mh / (R_SQRT(vh) + (REAL)eps));
+    m[j] = (float)mj;
+    v[j] = (float)vj;
+  }
+}

@@ -1,0 +1,163 @@
+"""ctypes view of the CPU oracle (``liboracle.so``).
+
+TEST INFRASTRUCTURE ONLY: the parity checker for the HIP backend.  Only the
+test suite, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` import this module; the product library never calls it.
+
+Each wrapper takes/returns numpy float32 arrays and selects the fp32
+(emission-faithful) or fp64 (finite-difference) build with ``prec``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIBS: dict[str, ctypes.CDLL] = {}
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+_c_int, _c_float, _c_size = ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+
+
+def build() -> None:
+    """Compile liboracle.so / liboracle_bench.so with the committed Makefile."""
+    subprocess.run(["make", "-s", "-C", _HERE, "all"], check=True)
+
+
+def lib(name: str = "liboracle.so") -> ctypes.CDLL:
+    if name not in _LIBS:
+        path = os.path.join(_HERE, name)
+        if not os.path.exists(path):
+            build()
+        L = ctypes.CDLL(path)
+        for sfx in ("_f32", "_f64"):
+            if not hasattr(L, "dgen_oracle_oscbank" + sfx):
+                continue
+            _sig(L, "dgen_oracle_oscbank" + sfx, [_f32p, _f32p, _c_int, _c_float, _c_float, _c_int, _f32p])
+            _sig(L, "dgen_oracle_playhead" + sfx, [_c_int, _c_int, _f32p])
+            syn = [_f32p, _f32p, _f32p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_float, _c_float, _f32p]
+            _sig(L, "dgen_oracle_synth_fwd" + sfx, syn)
+            _sig(L, "dgen_oracle_synth_bwd" + sfx, syn[:3] + [_f32p] + syn[3:])
+            _sig(L, "dgen_oracle_mlp_param_count" + sfx, [_c_int] * 4, _c_size)
+            _sig(L, "dgen_oracle_mlp_fwd" + sfx, [_f32p, _f32p] + [_c_int] * 6 + [_f32p])
+            _sig(L, "dgen_oracle_mlp_bwd" + sfx, [_f32p, _f32p, _f32p] + [_c_int] * 6 + [_f32p])
+            mss = [_f32p, _f32p, _c_int, _c_int, _i32p, _c_int, _c_int, _c_float, _c_float, _c_float]
+            _sig(L, "dgen_oracle_mss_fwd" + sfx, mss + [ctypes.c_void_p], ctypes.c_double)
+            _sig(L, "dgen_oracle_mss_bwd" + sfx, mss + [_f32p])
+            rp = _f32p if sfx == "_f32" else np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
+            _sig(L, "dgen_oracle_harmonic_step" + sfx,
+                 [_f32p, rp, _f32p, _f32p, _f32p] + [_c_int] * 8 + [_c_float] * 3 + [_i32p, _c_int, _c_int]
+                 + [_c_float] * 3 + [ctypes.c_void_p, ctypes.c_void_p], ctypes.c_double)
+            _sig(L, "dgen_oracle_adam" + sfx, [_f32p, _f32p, _f32p, _f32p, _c_size] + [_c_float] * 4 + [_c_int])
+        _sig(L, "dgen_oracle_noise_stream", [_c_int, _f32p])
+        _LIBS[name] = L
+    return _LIBS[name]
+
+
+def _sig(L, name, args, res=None):
+    fn = getattr(L, name)
+    fn.argtypes = args
+    fn.restype = res
+
+
+def _f(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _fn(name: str, prec: str, libname: str = "liboracle.so"):
+    return getattr(lib(libname), f"{name}_{prec}")
+
+
+# -- config 1 -------------------------------------------------------------
+def oscbank(freqs, amps, sr, pole, frames, prec="f32", libname="liboracle.so"):
+    out = np.zeros(frames, np.float32)
+    _fn("dgen_oracle_oscbank", prec, libname)(_f(freqs), _f(amps), len(freqs), sr, pole, frames, out)
+    return out
+
+
+# -- config 3 -------------------------------------------------------------
+def playhead(F, T, prec="f32"):
+    out = np.zeros(T, np.float32)
+    _fn("dgen_oracle_playhead", prec)(F, T, out)
+    return out
+
+
+def noise_stream(T):
+    out = np.zeros(T, np.float32)
+    lib().dgen_oracle_noise_stream(T, out)
+    return out
+
+
+def synth_fwd(ctrl, f0, uv, B, F, T, K, NF, sr, hscale=1.0, nscale=1.0, prec="f32", libname="liboracle.so"):
+    y = np.zeros((B, T), np.float32)
+    _fn("dgen_oracle_synth_fwd", prec, libname)(_f(ctrl), _f(f0), _f(uv), B, F, T, K, NF, sr, hscale, nscale, y)
+    return y
+
+
+def synth_bwd(ctrl, f0, uv, dy, B, F, T, K, NF, sr, hscale=1.0, nscale=1.0, prec="f32"):
+    NC = K + 2 + NF
+    d = np.zeros((B * F, NC), np.float32)
+    _fn("dgen_oracle_synth_bwd", prec)(_f(ctrl), _f(f0), _f(uv), _f(dy), B, F, T, K, NF, sr, hscale, nscale, d)
+    return d
+
+
+def mlp_param_count(din, hid, layers, nc):
+    return int(lib().dgen_oracle_mlp_param_count_f32(din, hid, layers, nc))
+
+
+def mlp_fwd(X, P, M, din, hid, layers, K, NF, prec="f32", libname="liboracle.so"):
+    ctrl = np.zeros((M, K + 2 + NF), np.float32)
+    _fn("dgen_oracle_mlp_fwd", prec, libname)(_f(X), _f(P), M, din, hid, layers, K, NF, ctrl)
+    return ctrl
+
+
+def mlp_bwd(X, P, dctrl, M, din, hid, layers, K, NF, prec="f32"):
+    dP = np.zeros(len(P), np.float32)
+    _fn("dgen_oracle_mlp_bwd", prec)(_f(X), _f(P), _f(dctrl), M, din, hid, layers, K, NF, dP)
+    return dP
+
+
+def mss_fwd(x, tgt, B, T, sizes, hop_div, w_lin, w_log, max_frames, prec="f32", frames=False,
+            libname="liboracle.so"):
+    sizes = np.ascontiguousarray(sizes, np.int32)
+    lf = np.zeros(T, np.float32) if frames else None
+    ptr = lf.ctypes.data_as(ctypes.c_void_p) if frames else None
+    tot = _fn("dgen_oracle_mss_fwd", prec, libname)(_f(x), _f(tgt), B, T, sizes, len(sizes), hop_div, w_lin,
+                                                    w_log, max_frames, ptr)
+    return (tot, lf) if frames else tot
+
+
+def mss_bwd(x, tgt, B, T, sizes, hop_div, w_lin, w_log, max_frames, prec="f32"):
+    sizes = np.ascontiguousarray(sizes, np.int32)
+    dx = np.zeros((B, T), np.float32)
+    _fn("dgen_oracle_mss_bwd", prec)(_f(x), _f(tgt), B, T, sizes, len(sizes), hop_div, w_lin, w_log,
+                                     max_frames, dx)
+    return dx
+
+
+def adam(p, g, m, v, lr, b1, b2, eps, step, prec="f32"):
+    p, m, v = _f(p).copy(), _f(m).copy(), _f(v).copy()
+    _fn("dgen_oracle_adam", prec)(p, _f(g), m, v, len(p), lr, b1, b2, eps, step)
+    return p, m, v
+
+
+def harmonic_step(cfg, X, P, f0, uv, tgt, grad=True, want_y=False, prec="f64"):
+    """Whole config-3 step (MLP -> synth -> MSS loss [-> backward]) in one
+    oracle call.  For prec="f64" the parameters are float64, so finite
+    differences can use steps far below fp32 resolution.
+    Returns (loss, dP or None, y or None)."""
+    dt = np.float32 if prec == "f32" else np.float64
+    P = np.ascontiguousarray(P, dtype=dt)
+    dP = np.zeros(len(P), dt) if grad else None
+    y = np.zeros((cfg.B, cfg.T), np.float32) if want_y else None
+    sizes = np.ascontiguousarray(cfg.fft_sizes, np.int32)
+    fn = _fn("dgen_oracle_harmonic_step", prec)
+    loss = fn(_f(X), P, _f(f0), _f(uv), _f(tgt), cfg.B, cfg.F, cfg.T, cfg.K, cfg.NF, cfg.din, cfg.hidden,
+              cfg.layers, cfg.sr, cfg.hscale, cfg.nscale, sizes, len(sizes), cfg.hop_div, cfg.w_lin, cfg.w_log,
+              float(cfg.T), dP.ctypes.data_as(ctypes.c_void_p) if grad else None,
+              y.ctypes.data_as(ctypes.c_void_p) if want_y else None)
+    return loss, dP, y
