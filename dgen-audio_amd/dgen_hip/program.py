@@ -28,6 +28,9 @@ class Op:
     flags: int = 0
     label: str = ""
     dispatch: str = ""
+    bytes: float = 0.0   # algorithmic HBM bytes per launch (interface read once + written once)
+    flops: float = 0.0   # algorithmic flops per launch
+    bound: str = "hbm"   # roof that bounds the op: "hbm", "mfma" (fp32 matrix) or "valu" (fp32 vector)
 
 
 @dataclass
@@ -53,13 +56,16 @@ class Program:
     def off(self, name: str) -> int:
         return self.cells[name].off
 
-    def add(self, kernel: int, arg, farg=(), flags: int = 0, label: str = "", dispatch: str = "") -> int:
+    def add(self, kernel: int, arg, farg=(), flags: int = 0, label: str = "", dispatch: str = "",
+            bytes: float = 0.0, flops: float = 0.0, bound: str = "hbm") -> int:
         arg = [int(a) for a in arg]
         farg = [float(a) for a in farg]
         if len(arg) > 32 or len(farg) > 8:
             raise ValueError("too many op arguments")
+        if bound not in ("hbm", "mfma", "valu"):
+            raise ValueError(f"unknown bound {bound}")
         self.ops.append(Op(kernel, arg + [0] * (32 - len(arg)), farg + [0.0] * (8 - len(farg)), flags, label,
-                           dispatch))
+                           dispatch, float(bytes), float(flops), bound))
         return len(self.ops) - 1
 
     def find(self, label: str) -> int:

@@ -95,21 +95,33 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     y = p.alloc("y", B * T)
 
     # ---- forward
+    f4 = 4.0
+    ctrl_b = M * NC * f4                      # one pass over the control rows
+    lerp_b = T * 8 * f4
+    ck_b = nseg * B * K * f4
+    data_b = 2 * F * B * f4 + T * f4          # f0, uv, noise
     p.add(R.K_PHASOR_CARRY, [lerp, f0, ck, B, K, F, T, SEG], [cfg.sr], flags=R.OP_SIDE, label="phasor_carry",
-          dispatch=f"fixedWithFrameLoop({B * K})")
+          dispatch=f"fixedWithFrameLoop({B * K})", bytes=lerp_b + F * B * f4 + ck_b, flops=5.0 * B * K * T,
+          bound="valu")
     W1, b1 = woff[0]
-    p.add(R.K_DENSE_SMALL, [X, W1, b1, Hs[0], M, din, Hd], label="mlp_in", dispatch="gemmSmall")
+    p.add(R.K_DENSE_SMALL, [X, W1, b1, Hs[0], M, din, Hd], label="mlp_in", dispatch="gemmSmall",
+          bytes=(M * din + din * Hd + Hd + M * Hd) * f4, flops=2.0 * M * din * Hd)
+    gemm_hh = dict(flops=2.0 * M * Hd * Hd, bound="mfma")
     for l in range(1, Lyr):
         W, b = woff[l]
         p.add(R.K_GEMM, [Hs[l - 1], W, Hs[l], M, Hd, Hd, Hd, Hd, Hd, 0, 0, R.EPI_BIAS_TANH, b, -1, 0, 1, 0],
-              label=f"mlp_l{l + 1}", dispatch="gemm")
+              label=f"mlp_l{l + 1}", dispatch="gemm", bytes=(2 * M * Hd + Hd * Hd + Hd) * f4, **gemm_hh)
     p.add(R.K_GEMM, [Hs[-1], Wh, Z, M, NC, Hd, Hd, NC, LDC, 0, 0, R.EPI_BIAS, bh, -1, 0, 1, 0], label="mlp_heads",
-          dispatch="gemm")
-    p.add(R.K_HEADS_FWD, [Z, ctrl, M, K, NF, LDC], label="heads", dispatch=f"perFrameScaled({M})")
+          dispatch="gemm", bytes=(M * Hd + Hd * NC + NC + M * NC) * f4, flops=2.0 * M * Hd * NC, bound="mfma")
+    p.add(R.K_HEADS_FWD, [Z, ctrl, M, K, NF, LDC], label="heads", dispatch=f"perFrameScaled({M})",
+          bytes=2 * M * NC * f4, flops=M * (K * 12.0 + NF * 8.0))
     synth_args = [ctrl, f0, uv, lerp, ck, y, B, K, NF, F, T, SEG, -1, noise, LDC]
     hs, ns = cfg.hscale, cfg.nscale
+    # per (b, t): K harmonics x (phase 4 + sin 20 + lerp 3 + mask/div 3 + sum 1 + normaliser 4), NF taps x 5
+    synth_flops = float(B) * T * (35.0 * K + 5.0 * NF)
     p.add(R.K_SYNTH_FWD, synth_args, [cfg.sr, hs, ns], flags=R.OP_JOIN, label="synth_fwd",
-          dispatch=f"perFrameScaled({B})")
+          dispatch=f"perFrameScaled({B})", bytes=ctrl_b + lerp_b + ck_b + data_b + B * T * f4, flops=synth_flops,
+          bound="valu")
     p.output_cell = "y"
     if not train:
         return p
@@ -128,6 +140,7 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     gl = wl / maxf / np.float32(B)
     gg = wg / maxf / np.float32(B)
     wgrad_cells, wloss_cells = [], []
+    gather_b = 0.0
     for N in sizes:
         hop = max(1, N // cfg.hop_div)
         nwin = (T + hop - 1) // hop
@@ -135,24 +148,34 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
         p.add(R.K_FFT_TABLES, [tab, N], flags=R.OP_STATIC, label=f"fft_tables_{N}", dispatch="static")
         wlc = p.alloc(f"win_loss_{N}", nwin * B * 2)
         wgc = p.alloc(f"win_grad_{N}", nwin * B * N)
+        lg = int(np.log2(N))
+        # two forward transforms + one inverse (5 N log2 N each), window and bin math
         p.add(R.K_SPECTRAL_LOSS, [y, target, wlc, wgc, B, T, N, hop, tab], [gl, gg], label=f"spectral_{N}",
-              dispatch=f"perFrameScaledThreadgroup1({B}) hop {hop}")
+              dispatch=f"perFrameScaledThreadgroup1({B}) hop {hop}",
+              bytes=(2 * B * T + nwin * B * (N + 2)) * f4, flops=nwin * B * (15.0 * N * lg + 40.0 * N),
+              bound="valu")
+        gather_b += nwin * B * (N + 2) * f4
         wgrad_cells.append(wgc)
         wloss_cells.append(wlc)
     garg = [dy, lossf, B, T, len(sizes)] + (sizes + [0] * 8)[:8] + (wgrad_cells + [0] * 8)[:8] \
         + (wloss_cells + [0] * 8)[:8] + [cfg.hop_div]
-    p.add(R.K_SPECTRAL_GATHER, garg, [wl, wg, maxf], label="spectral_gather", dispatch=f"perFrameScaled({B})")
+    p.add(R.K_SPECTRAL_GATHER, garg, [wl, wg, maxf], label="spectral_gather", dispatch=f"perFrameScaled({B})",
+          bytes=gather_b + (B * T + T) * f4, flops=gather_b / f4)
 
     part = p.alloc("synth_partials", B * nseg * SLOTS * LDC)
     dctrl = p.alloc("dctrl", M * LDC)
     bargs = list(synth_args)
     bargs[5] = dy
     bargs[12] = part
-    p.add(R.K_SYNTH_BWD, bargs, [cfg.sr, hs, ns], label="synth_bwd", dispatch=f"selfManagedThreads({B})")
+    part_b = B * nseg * SLOTS * NC * f4
+    p.add(R.K_SYNTH_BWD, bargs, [cfg.sr, hs, ns], label="synth_bwd", dispatch=f"selfManagedThreads({B})",
+          bytes=ctrl_b + lerp_b + ck_b + data_b + B * T * f4 + part_b,
+          flops=synth_flops + float(B) * T * (6.0 * K + 4.0 * NC), bound="valu")
     p.add(R.K_SYNTH_BWD_REDUCE, [part, rowlist, dctrl, B, NC, F, T, SEG, LDC], label="synth_bwd_reduce",
-          dispatch=f"perFrameScaled({M})")
+          dispatch=f"perFrameScaled({M})", bytes=part_b + F * ROW_ENTRIES * f4 + M * NC * f4, flops=part_b / f4)
     dZ = p.alloc("dZ", M * LDC)
-    p.add(R.K_HEADS_BWD, [Z, dctrl, dZ, M, K, NF, LDC], label="heads_bwd", dispatch=f"perFrameScaled({M})")
+    p.add(R.K_HEADS_BWD, [Z, dctrl, dZ, M, K, NF, LDC], label="heads_bwd", dispatch=f"perFrameScaled({M})",
+          bytes=3 * M * NC * f4, flops=M * (K * 20.0 + NF * 14.0))
 
     G = p.alloc("grads", npar)
     split = max(1, (M + SPLITK_ROWS - 1) // SPLITK_ROWS)
@@ -163,29 +186,34 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     gWh, gbh = G + (Wh - P), G + (bh - P)
     # heads: dWh = H_L^T dZ ; dbh = colsum(dZ) ; dH_L = (dZ Wh^T) * (1 - H_L^2)
     p.add(R.K_GEMM, [Hs[-1], dZ, gWh, Hd, NC, M, Hd, LDC, NC, 1, 0, R.EPI_NONE, -1, -1, 0, split, ws_gemm],
-          label="dW_heads", dispatch="gemmChunkPartials")
-    p.add(R.K_COLSUM, [dZ, gbh, M, NC, LDC, ws_col], label="db_heads", dispatch="chunkPartialsReduceToCell")
+          label="dW_heads", dispatch="gemmChunkPartials", bytes=(M * Hd + M * NC + Hd * NC) * f4,
+          flops=2.0 * M * Hd * NC, bound="mfma")
+    p.add(R.K_COLSUM, [dZ, gbh, M, NC, LDC, ws_col], label="db_heads", dispatch="chunkPartialsReduceToCell",
+          bytes=(M * NC + NC) * f4, flops=float(M * NC))
     dH = [p.alloc(f"dZ{l + 1}", M * Hd) for l in range(Lyr)]
     p.add(R.K_GEMM, [dZ, Wh, dH[-1], M, Hd, NC, LDC, NC, Hd, 0, 1, R.EPI_TANH_GRAD, -1, Hs[-1], Hd, 1, 0],
-          label=f"dX_heads", dispatch="gemm")
+          label=f"dX_heads", dispatch="gemm", bytes=(M * NC + Hd * NC + 2 * M * Hd) * f4, flops=2.0 * M * Hd * NC,
+          bound="mfma")
     for l in range(Lyr - 1, 0, -1):
         W, _b = woff[l]
         gw, gb = gW[l]
         p.add(R.K_GEMM, [Hs[l - 1], dH[l], gw, Hd, Hd, M, Hd, Hd, Hd, 1, 0, R.EPI_NONE, -1, -1, 0, split, ws_gemm],
-              label=f"dW_l{l + 1}", dispatch="gemmChunkPartials")
-        p.add(R.K_COLSUM, [dH[l], gb, M, Hd, Hd, ws_col], label=f"db_l{l + 1}", dispatch="chunkPartialsReduceToCell")
+              label=f"dW_l{l + 1}", dispatch="gemmChunkPartials", bytes=(2 * M * Hd + Hd * Hd) * f4, **gemm_hh)
+        p.add(R.K_COLSUM, [dH[l], gb, M, Hd, Hd, ws_col], label=f"db_l{l + 1}", dispatch="chunkPartialsReduceToCell",
+              bytes=(M * Hd + Hd) * f4, flops=float(M * Hd))
         p.add(R.K_GEMM, [dH[l], W, dH[l - 1], M, Hd, Hd, Hd, Hd, Hd, 0, 1, R.EPI_TANH_GRAD, -1, Hs[l - 1], Hd, 1, 0],
-              label=f"dX_l{l + 1}", dispatch="gemm")
+              label=f"dX_l{l + 1}", dispatch="gemm", bytes=(3 * M * Hd + Hd * Hd) * f4, **gemm_hh)
     gw1, gb1 = gW[0]
     p.add(R.K_DENSE_SMALL_WGRAD, [X, dH[0], gw1, M, din, Hd, ws_col], label="dW_l1",
-          dispatch="chunkPartialsReduceToCell")
-    p.add(R.K_COLSUM, [dH[0], gb1, M, Hd, Hd, ws_col], label="db_l1", dispatch="chunkPartialsReduceToCell")
+          dispatch="chunkPartialsReduceToCell", bytes=(M * din + M * Hd + din * Hd) * f4, flops=2.0 * M * din * Hd)
+    p.add(R.K_COLSUM, [dH[0], gb1, M, Hd, Hd, ws_col], label="db_l1", dispatch="chunkPartialsReduceToCell",
+          bytes=(M * Hd + Hd) * f4, flops=float(M * Hd))
     if optimizer:
         m = p.alloc("adam_m", npar)
         v = p.alloc("adam_v", npar)
         tcell = p.alloc("adam_t", 1)
         p.add(R.K_ADAM, [P, G, m, v, npar, tcell], [cfg.lr, 0.9, 0.999, 1e-8], label="adam",
-              dispatch=f"staticThreads({npar})")
+              dispatch=f"staticThreads({npar})", bytes=7.0 * npar * f4, flops=12.0 * npar)
     p.output_cell = "y"
     return p
 

@@ -145,7 +145,7 @@ def adam(p, g, m, v, lr, b1, b2, eps, step, prec="f32"):
     return p, m, v
 
 
-def harmonic_step(cfg, X, P, f0, uv, tgt, grad=True, want_y=False, prec="f64"):
+def harmonic_step(cfg, X, P, f0, uv, tgt, grad=True, want_y=False, prec="f64", libname="liboracle.so"):
     """Whole config-3 step (MLP -> synth -> MSS loss [-> backward]) in one
     oracle call.  For prec="f64" the parameters are float64, so finite
     differences can use steps far below fp32 resolution.
@@ -155,7 +155,7 @@ def harmonic_step(cfg, X, P, f0, uv, tgt, grad=True, want_y=False, prec="f64"):
     dP = np.zeros(len(P), dt) if grad else None
     y = np.zeros((cfg.B, cfg.T), np.float32) if want_y else None
     sizes = np.ascontiguousarray(cfg.fft_sizes, np.int32)
-    fn = _fn("dgen_oracle_harmonic_step", prec)
+    fn = _fn("dgen_oracle_harmonic_step", prec, libname)
     loss = fn(_f(X), P, _f(f0), _f(uv), _f(tgt), cfg.B, cfg.F, cfg.T, cfg.K, cfg.NF, cfg.din, cfg.hidden,
               cfg.layers, cfg.sr, cfg.hscale, cfg.nscale, sizes, len(sizes), cfg.hop_div, cfg.w_lin, cfg.w_log,
               float(cfg.T), dP.ctypes.data_as(ctypes.c_void_p) if grad else None,
