@@ -58,6 +58,13 @@ inline float* cell(const Launch& L, int64_t off) { return L.arena + off; }
 
 using Launcher = int (*)(const Launch&, const dgen_hip_op&);
 
+// Workgroup barrier that orders LDS only: waits for the wave's own LDS
+// operations, not for its outstanding global memory operations (HIP's
+// __syncthreads() also waits for those, which exposes prefetch latency).
+// Kernels use it only where no global-memory ordering between threads of
+// the workgroup is needed.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 int launch_accum_table(const Launch&, const dgen_hip_op&);
 int launch_dense_small(const Launch&, const dgen_hip_op&);
 int launch_dense_small_wgrad(const Launch&, const dgen_hip_op&);
@@ -76,5 +83,6 @@ int launch_osc_bank(const Launch&, const dgen_hip_op&);
 int launch_noise_table(const Launch&, const dgen_hip_op&);
 int launch_row_schedule(const Launch&, const dgen_hip_op&);
 int launch_fft_tables(const Launch&, const dgen_hip_op&);
+int launch_lerp_frames(const Launch&, const dgen_hip_op&);
 
 }  // namespace dgen

@@ -1,275 +1,641 @@
 // Batched harmonic + FIR-noise synth (HarmonicSynth.renderBatchedSignal,
 // Examples/HarmonicE2E/Synth.swift:47-102) and its adjoint.
 //
-// Time is cut into segments of `seg` (<= 64) frames.  The only true
-// recurrence is the tensor phasor (Sources/DGen/Emit+State.swift:322-369):
-// one lane per (batch, harmonic) accumulates phase sequentially in fp32.
-// k_phasor_carry runs that chain once over the whole signal (lane = wave
-// lane, phase in a VGPR) and stores the phase at each segment start; every
-// other kernel restarts the chain from those checkpoints, so all remaining
-// work is parallel over (segment, batch) and bit-identical to the sequential
-// evaluation.  The chain, the sampleRow interpolation and every sum are
-// evaluated in the reference's operation order with contraction disabled.
+// Time is cut into segments of kSeg = 64 frames.  The only true recurrence
+// is the tensor phasor (Sources/DGen/Emit+State.swift:322-369): one lane per
+// (batch, harmonic) accumulates phase sequentially in fp32.  k_phasor_carry
+// runs that chain once over the whole signal and stores the phase at every
+// segment start; the synth kernels restart the chain from those checkpoints,
+// so all remaining work is parallel over (segment, batch) and the phases are
+// bit-identical to one sequential evaluation.
 //
-// Layouts: ctrl rows [B*F][ldc] (row = b*F + f); f0, uv [F][B]; y, dy
-// [B][T]; lerp table [T][8] = lo, hi, frac, 1-frac, slot(lo), slot(hi);
-// checkpoints [nseg][B][K]; noise [T].
+// The chain step is the reference's u_accum/phasor order:
+//   inc = freq / sr;  next = ph + inc;  w = next - floor(next);  if (w >= 1) w -= 1
+// - freq / sr uses the fma-corrected reciprocal product (q0 = x*r,
+//   e = fma(-q0, sr, x), q = fma(e, r, q0)), which equals the IEEE quotient
+//   for every normal |x| in [2^-20, 2^24) (checked exhaustively for the
+//   sample rates in use by tests/test_fastdiv.py); outside that range the
+//   kernel divides.
+// - for ph in [0,1) and a finite inc >= 0, next >= 0, next - floor(next) is
+//   exact and < 1, so the step is fract(ph + inc) (one v_fract_f32); chunks
+//   holding a negative or non-finite increment take the literal form.
+//
+// Layouts: ctrl rows [B*F][ldc] (row = b*F + f); f0f, uvf [B][T] (frame-rate
+// interpolated f0 and uv); lerp [T][8] = lo, hi, frac, 1-frac, slot(lo),
+// slot(hi); seg_rows [nseg][4]; checkpoints [nseg][B][K]; noise [T];
+// y, dy [B][T]; partials [B][nseg][4][ldc].
 #pragma clang fp contract(off)
+
+#include <type_traits>
 
 #include "internal.h"
 
 namespace dgen {
 
-constexpr int kMaxSeg = 64;   // frames per segment (one thread per frame)
+constexpr int kSeg = 64;      // frames per segment = checkpoint spacing
 constexpr int kMaxK = 64;     // harmonics (one lane per harmonic)
-constexpr int kMaxNC = 128;   // control columns (one thread per column)
+constexpr int kMaxNC = 128;   // control columns
 constexpr int kSlots = 4;     // distinct control rows a segment may touch
-constexpr float kTwoPi = 2.0f * 3.14159265358979323846f;  // 2*Float.pi
+constexpr int kLd = kSeg + 1; // LDS row stride of [frame][harmonic] tiles (bank-conflict free)
+constexpr int kMaxNoise = kSeg + kMaxNC;  // noise window of one segment
 
 __device__ __forceinline__ float phasor_wrap(float next) {
   float w = next - floorf(next);
   return w >= 1.0f ? w - 1.0f : w;
 }
 
+// x / sr for a constant sr with r = RN(1/sr): IEEE-exact on the validated range.
+__device__ __forceinline__ float div_sr(float x, float sr, float rsr) {
+  const float ax = fabsf(x);
+  if (ax >= 0x1p-20f && ax < 0x1p24f) {
+    const float q0 = x * rsr;
+    const float e = fmaf(-q0, sr, x);
+    return fmaf(e, rsr, q0);
+  }
+  return x / sr;
+}
+
+// sin(2*pi*p) for p in [0, 1): the gfx950 transcendental unit takes its
+// argument in revolutions (v_sin_f32).  Measured max abs error over a 2^24
+// point grid of [0,1): 1.3e-7, against 4.2e-7 for sinf(fl(p * 2pi_f32)), the
+// expression the reference evaluates (CRenderer.swift:825-827).
+__device__ __forceinline__ float sin2pi(float p) { return __builtin_amdgcn_sinf(p); }
+
+// ------------------------------------------------------------ frame-rate data
+// out[b][t] = (1-frac_t) * src[lo_t][b] + frac_t * src[hi_t][b]: the sampleRow
+// read of a [F][B] data table (Emit+RowSelection.swift:164-197).
+__global__ void k_lerp_frames(const float* __restrict__ src, const float* __restrict__ lerp, float* __restrict__ out,
+                              int B, int T) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  const int b = blockIdx.y;
+  if (t >= T) return;
+  const float4 e = *reinterpret_cast<const float4*>(lerp + (size_t)t * 8);
+  const int lo = (int)e.x, hi = (int)e.y;
+  out[(size_t)b * T + t] = e.w * src[(size_t)lo * B + b] + e.z * src[(size_t)hi * B + b];
+}
+
+int launch_lerp_frames(const Launch& L, const dgen_hip_op& op) {
+  // arg: [0]=src ([F][B]) [1]=lerp ([T][8]) [2]=out ([B][T]) [3]=B [4]=F [5]=T
+  const int64_t src = op.arg[0], lerp = op.arg[1], out = op.arg[2], B = op.arg[3], F = op.arg[4], T = op.arg[5];
+  DGEN_REQUIRE(B > 0 && B <= 65535 && F > 0 && T > 0 && T <= (1 << 26), "lerp_frames: B %lld F %lld T %lld",
+               (long long)B, (long long)F, (long long)T);
+  DGEN_REQUIRE(lerp % 4 == 0, "lerp_frames: lerp table must be 16-byte aligned");
+  DGEN_CHECK_CELL(L, src, F * B, "lerp_frames.src");
+  DGEN_CHECK_CELL(L, lerp, T * 8, "lerp_frames.lerp");
+  DGEN_CHECK_CELL(L, out, B * T, "lerp_frames.out");
+  if (L.dry) return 0;
+  hipLaunchKernelGGL(k_lerp_frames, dim3((unsigned)((T + 255) / 256), (unsigned)B), dim3(256), 0, L.stream,
+                     cell(L, src), cell(L, lerp), cell(L, out), (int)B, (int)T);
+  DGEN_LAUNCH_CHECK("k_lerp_frames");
+  return 0;
+}
+
 // ------------------------------------------------------------ carry pass
-__global__ __launch_bounds__(64) void k_phasor_carry(const float* __restrict__ lerp, const float* __restrict__ f0,
-                                                     float* __restrict__ ckpt, int B, int K, int T, int seg, float sr) {
-  const int lane = blockIdx.x * blockDim.x + threadIdx.x;
-  if (lane >= B * K) return;
-  const int b = lane / K;
-  const float kf = (float)(lane % K + 1);
-  const int BK = B * K;
-  float ph = 0.f;
-  int until = 0, s = 0;
-  for (int t = 0; t < T; ++t) {
-    if (t == until) {
-      ckpt[(size_t)s * BK + lane] = ph;
-      ++s;
-      until += seg;
+// One workgroup per batch lane b.  Wave 0 runs the K phase chains
+// (lane = k); at 2 dependent VALU ops per step its 64-step segment costs
+// ~128 issue slots, so everything else is kept off its path:
+// - waves 1..4 compute increments into a ring of kCarryBufs segment buffers,
+//   kIv segments per barrier interval, one interval ahead of the chain;
+//   producer waves own frames 0-23, 24-47 and 48-63 of a segment, lane = k
+//   (four waves: one per SIMD, so the chain wave's SIMD runs only it);
+// - increments are stored k-major ([k][frame], stride 68 floats), so the
+//   chain reads a lane's 64 increments with 16 ds_read_b128 and producers
+//   write them with ds_write_b128, both bank-conflict free;
+// - f0 is staged from global memory 16 segments at a time into a
+//   double-buffered LDS ring, so load latency is paid once per 16 segments;
+//   the fast-step test (every f0 of the block in the exact range) is voted
+//   once per block while loading it;
+// - the chain wave reads segment s+1's increments into registers while it
+//   steps segment s, and has issue priority on its SIMD.
+constexpr int kProducers = 3;
+constexpr int kCarryWaves = 1 + kProducers;
+constexpr int kIv = 3;                  // segments per barrier interval
+constexpr int kCarryBufs = 2 * kIv;     // increment ring
+constexpr int kRing = 16;               // segments per f0 block
+constexpr int kIncLd = kSeg + 4;        // k-major row stride (floats)
+
+__device__ __forceinline__ bool fast_f0(float f0) {
+  // every increment (k+1)*f0/sr, k < 64, is then computed by the exact
+  // reciprocal-product form and is finite and >= 0
+  return f0 == 0.0f || (f0 >= 0x1p-20f && f0 < 0x1p18f);
+}
+
+__global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* __restrict__ f0f,
+                                                                   float* __restrict__ ckpt, int B, int K, int T,
+                                                                   float sr, float rsr) {
+  __shared__ __align__(16) float s_inc[kCarryBufs][64 * kIncLd];  // [k][frame]
+  __shared__ __align__(16) float s_f0[2][kRing * kSeg];
+  __shared__ int s_flag[kCarryBufs][kCarryWaves];  // segment needs the literal wrap form
+  __shared__ int s_blkbad[2][kProducers];           // f0 block holds a value outside the fast range
+  const int b = blockIdx.x, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int nseg = (T + kSeg - 1) / kSeg;
+  const float* f0b = f0f + (size_t)b * T;
+  const int ptid = threadIdx.x - 64;  // producer thread index
+  auto load_block = [&](int blk) {
+    float* dst = s_f0[blk & 1];
+    const int t0 = blk * kRing * kSeg;
+    int bad = 0;
+    for (int i = ptid; i < kRing * kSeg; i += 64 * kProducers) {
+      const int t = t0 + i;
+      const float v = t < T ? f0b[t] : 0.0f;
+      bad |= !fast_f0(v);
+      dst[i] = v;
     }
-    const float* e = lerp + (size_t)t * 8;
-    const int lo = (int)e[0], hi = (int)e[1];
-    const float f0i = e[3] * f0[lo * B + b] + e[2] * f0[hi * B + b];
-    const float freq = kf * f0i;
-    ph = phasor_wrap(ph + freq / sr);
+    bad = __any(bad);
+    if (lane == 0) s_blkbad[blk & 1][wave - 1] = bad;
+  };
+  auto produce = [&](int s) {
+    const int buf = s % kCarryBufs;
+    const int i0 = (wave - 1) * 24;                 // frames i0 .. i0 + nf - 1
+    const int nf = wave == kProducers ? 16 : 24;
+    const float4* f4 = reinterpret_cast<const float4*>(&s_f0[(s / kRing) & 1][(s % kRing) * kSeg + i0]);
+    float f[24];
+#pragma unroll
+    for (int q = 0; q < 6; ++q) {
+      const float4 v = q < nf / 4 ? f4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+      f[4 * q] = v.x;
+      f[4 * q + 1] = v.y;
+      f[4 * q + 2] = v.z;
+      f[4 * q + 3] = v.w;
+    }
+    const float kf = (float)(lane + 1);
+    const int* bb = s_blkbad[(s / kRing) & 1];
+    int blkbad = 0;
+#pragma unroll
+    for (int w = 0; w < kProducers; ++w) blkbad |= bb[w];
+    const bool fast = !blkbad;
+    float inc[24];
+    if (fast) {
+#pragma unroll
+      for (int j = 0; j < 24; ++j) {
+        const float x = kf * f[j];
+        const float q0 = x * rsr;
+        inc[j] = fmaf(fmaf(-q0, sr, x), rsr, q0);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 24; ++j) inc[j] = div_sr(kf * f[j], sr, rsr);
+    }
+    float4* dst = reinterpret_cast<float4*>(&s_inc[buf][lane * kIncLd + i0]);
+#pragma unroll
+    for (int q = 0; q < 6; ++q)
+      if (q < nf / 4) dst[q] = make_float4(inc[4 * q], inc[4 * q + 1], inc[4 * q + 2], inc[4 * q + 3]);
+    if (lane == 0) s_flag[buf][wave] = fast ? 0 : 1;
+  };
+  // chain: v[32h .. 32h+31] <- half h of segment s's increments
+  auto fetch_half = [&](int s, float* v, int h) {
+    const float4* src = reinterpret_cast<const float4*>(&s_inc[s % kCarryBufs][lane * kIncLd]) + 8 * h;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const float4 u = src[q];
+      v[32 * h + 4 * q] = u.x;
+      v[32 * h + 4 * q + 1] = u.y;
+      v[32 * h + 4 * q + 2] = u.z;
+      v[32 * h + 4 * q + 3] = u.w;
+    }
+  };
+  // returns 1 if segment s needs the wrap form
+  auto seg_flag = [&](int s) -> int {
+    int flag = 0;
+#pragma unroll
+    for (int w = 1; w < kCarryWaves; ++w) flag |= s_flag[s % kCarryBufs][w];
+    return flag || (T - s * kSeg) < kSeg;
+  };
+  auto fetch = [&](int s, float* v) -> int {
+    fetch_half(s, v, 0);
+    fetch_half(s, v, 1);
+    return seg_flag(s);
+  };
+  float ph = 0.0f;  // the phasor state cell is zero at the start of every run
+  // steps segment s from v; if nv, loads segment s+1 into nv half by half in
+  // between so at most ~8 LDS reads are in flight
+  auto step_seg = [&](int s, const float* v, int slow, float* nv, auto has_next) {
+    constexpr bool kNext = decltype(has_next)::value;
+    if (lane < K) ckpt[((size_t)s * B + b) * K + lane] = ph;
+    if (!slow) {
+      if constexpr (kNext) fetch_half(s + 1, nv, 0);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < kSeg / 2; ++i) ph = __builtin_amdgcn_fractf(ph + v[i]);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (kNext) fetch_half(s + 1, nv, 1);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = kSeg / 2; i < kSeg; ++i) ph = __builtin_amdgcn_fractf(ph + v[i]);
+    } else {
+      if constexpr (kNext) {
+        fetch_half(s + 1, nv, 0);
+        fetch_half(s + 1, nv, 1);
+      }
+      const float* inc = &s_inc[s % kCarryBufs][lane * kIncLd];
+      const int nt = min(kSeg, T - s * kSeg);
+      for (int i = 0; i < nt; ++i) ph = phasor_wrap(ph + inc[i]);
+    }
+  };
+
+  const int nint = (nseg + kIv - 1) / kIv;
+  if (wave > 0) {
+    load_block(0);
+    load_block(1);
+  }
+  lds_barrier();
+  if (wave > 0)
+    for (int s = 0; s < kIv && s < nseg; ++s) produce(s);
+  lds_barrier();
+  if (wave == 0) __builtin_amdgcn_s_setprio(3);
+  for (int iv = 0; iv < nint; ++iv) {
+    const int s0 = iv * kIv;
+    if (wave == 0) {
+      float va[kSeg], vb[kSeg];
+      int fa = fetch(s0, va), fb = 0;
+#pragma unroll
+      for (int q = 0; q < kIv; ++q) {
+        const int s = s0 + q;
+        if (s >= nseg) break;
+        // the next segment's increments are loaded while this one steps
+        const bool more = q + 1 < kIv && s + 1 < nseg;
+        if (q % 2 == 0) {
+          if (more) {
+            fb = seg_flag(s + 1);
+            step_seg(s, va, fa, vb, std::true_type{});
+          } else {
+            step_seg(s, va, fa, vb, std::false_type{});
+          }
+        } else {
+          if (more) {
+            fa = seg_flag(s + 1);
+            step_seg(s, vb, fb, va, std::true_type{});
+          } else {
+            step_seg(s, vb, fb, va, std::false_type{});
+          }
+        }
+      }
+    } else {
+      // f0 block s/16 + 1 goes into the half whose segments are all produced
+      const int next = s0 + kIv;
+      for (int s = next; s < next + kIv && s < nseg; ++s) {
+        if (s % kRing == 0) load_block(s / kRing + 1);
+        produce(s);
+      }
+    }
+    lds_barrier();
   }
 }
 
 int launch_phasor_carry(const Launch& L, const dgen_hip_op& op) {
-  const int64_t lerp = op.arg[0], f0 = op.arg[1], ck = op.arg[2], B = op.arg[3], K = op.arg[4], F = op.arg[5],
-                T = op.arg[6], seg = op.arg[7];
-  DGEN_REQUIRE(B > 0 && K > 0 && F > 0 && T > 0 && seg > 0 && B * K <= (1 << 24) && T <= (1 << 26),
-               "phasor_carry: B %lld K %lld F %lld T %lld seg %lld", (long long)B, (long long)K, (long long)F,
-               (long long)T, (long long)seg);
-  const int64_t nseg = (T + seg - 1) / seg;
-  DGEN_CHECK_CELL(L, lerp, T * 8, "phasor_carry.lerp");
-  DGEN_CHECK_CELL(L, f0, F * B, "phasor_carry.f0");
+  // arg: [0]=f0f ([B][T]) [1]=checkpoints ([nseg][B][K]) [2]=B [3]=K [4]=T   farg: [0]=sr
+  const int64_t f0f = op.arg[0], ck = op.arg[1], B = op.arg[2], K = op.arg[3], T = op.arg[4];
+  DGEN_REQUIRE(B > 0 && B <= 65535 && K > 0 && K <= kMaxK && T > 0 && T <= (1 << 26),
+               "phasor_carry: B %lld K %lld T %lld", (long long)B, (long long)K, (long long)T);
+  DGEN_REQUIRE(op.farg[0] > 0.f && op.farg[0] < 1e30f, "phasor_carry: sample rate %g", (double)op.farg[0]);
+  const int64_t nseg = (T + kSeg - 1) / kSeg;
+  DGEN_CHECK_CELL(L, f0f, B * T, "phasor_carry.f0_frames");
   DGEN_CHECK_CELL(L, ck, nseg * B * K, "phasor_carry.checkpoints");
   if (L.dry) return 0;
-  hipLaunchKernelGGL(k_phasor_carry, dim3((unsigned)((B * K + 63) / 64)), dim3(64), 0, L.stream, cell(L, lerp),
-                     cell(L, f0), cell(L, ck), (int)B, (int)K, (int)T, (int)seg, op.farg[0]);
+  const float sr = op.farg[0], rsr = 1.0f / sr;
+  hipLaunchKernelGGL(k_phasor_carry, dim3((unsigned)B), dim3(64 * kCarryWaves), 0, L.stream, cell(L, f0f),
+                     cell(L, ck), (int)B, (int)K, (int)T, sr, rsr);
   DGEN_LAUNCH_CHECK("k_phasor_carry");
   return 0;
 }
 
-// ------------------------------------------------------------ shared per-frame prologue
-struct FrameRow {
-  int lo, hi, slo, shi;
-  float frac, omf;
-};
-
-__device__ __forceinline__ FrameRow frame_row(const float* __restrict__ lerp, int t) {
-  const float* e = lerp + (size_t)t * 8;
-  FrameRow r;
-  r.lo = (int)e[0];
-  r.hi = (int)e[1];
-  r.frac = e[2];
-  r.omf = e[3];
-  r.slo = (int)e[4];
-  r.shi = (int)e[5];
-  return r;
-}
-
+// ------------------------------------------------------------ shared pieces
 struct SynthArgs {
   const float* ctrl;
-  int ldc;
-  const float* f0;
-  const float* uv;
+  const float* f0f;
+  const float* uvf;
   const float* lerp;
+  const float* seg_rows;
   const float* noise;
   const float* ckpt;
-  int B, K, NF, F, T, seg;
-  float sr, hscale, nscale;
+  int ldc, B, K, NF, F, T;
+  float sr, rsr, hscale, nscale;
 };
 
-// ------------------------------------------------------------ forward
-__global__ __launch_bounds__(64) void k_synth_fwd(SynthArgs a, float* __restrict__ y) {
-  __shared__ float s_den[kMaxSeg], s_f0[kMaxSeg], s_omf[kMaxSeg], s_frac[kMaxSeg];
-  __shared__ int s_lo[kMaxSeg], s_hi[kMaxSeg];
-  __shared__ float s_contrib[kMaxSeg][kMaxK + 1];
-  const int s = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-  const int t0 = s * a.seg, nt = min(a.seg, a.T - t0);
-  const float nyq = a.sr * 0.5f;
+// Per-frame values of a segment, staged in LDS and read as broadcasts.
+struct FrameRec {
+  float f0, frac, omf;
+  int slots;  // slot(lo) | slot(hi) << 8
+};
 
-  if (tid < nt) {  // phase A: per-frame interpolation and harmonic normaliser
-    const int t = t0 + tid;
-    const FrameRow r = frame_row(a.lerp, t);
-    const float f0i = r.omf * a.f0[r.lo * a.B + b] + r.frac * a.f0[r.hi * a.B + b];
-    const float* c0 = a.ctrl + (size_t)(b * a.F + r.lo) * a.ldc;
-    const float* c1 = a.ctrl + (size_t)(b * a.F + r.hi) * a.ldc;
-    float den = 0.f;
-    for (int k = 0; k < a.K; ++k) {
-      const float freq = (float)(k + 1) * f0i;
-      const float amp = r.omf * c0[k] + r.frac * c1[k];
-      den = den + amp * (freq < nyq ? 1.0f : 0.0f);
+// Per-wave LDS of the synth kernels.
+struct SegLds {
+  FrameRec fr[kSeg];
+  float row[kSlots][kMaxNC];      // control rows touched by the segment
+  float pre[kSlots][kMaxK + 1];   // prefix sums of the harmonic columns of each row
+  float noise[kMaxNoise];         // noise[t0 - (NF-1) ... t0 + 63]
+  float hs[kSeg];                 // per-frame scalars of the backward
+  float coef[kSeg];
+  float dg[kSeg];
+  float dng[kSeg];
+  float dfl[kSeg];
+};
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Stage the segment's frame records, rows, their harmonic prefix sums (if
+// want_pre) and the noise window.  Returns 1 if every frame's f0 admits the
+// fast chain step.
+__device__ __forceinline__ int stage_segment(const SynthArgs& a, SegLds& L, int s, int b, int lane, int nt,
+                                             bool want_pre) {
+  const int t0 = s * kSeg;
+  const int NC = a.K + 2 + a.NF;
+  int ok = 1;
+  {
+    FrameRec r{0.f, 0.f, 1.f, 0};
+    if (lane < nt) {
+      const int t = t0 + lane;
+      const float4 e0 = *reinterpret_cast<const float4*>(a.lerp + (size_t)t * 8);
+      const float4 e1 = *reinterpret_cast<const float4*>(a.lerp + (size_t)t * 8 + 4);
+      r.f0 = a.f0f[(size_t)b * a.T + t];
+      r.frac = e0.z;
+      r.omf = e0.w;
+      r.slots = (int)e1.x | ((int)e1.y << 8);
+      ok = fast_f0(r.f0) ? 1 : 0;
     }
-    s_den[tid] = den + 1e-8f;
-    s_f0[tid] = f0i;
-    s_omf[tid] = r.omf;
-    s_frac[tid] = r.frac;
-    s_lo[tid] = r.lo;
-    s_hi[tid] = r.hi;
+    L.fr[lane] = r;
   }
-  __syncthreads();
-  if (tid < a.K) {  // phase B: one lane per harmonic runs the phasor from the checkpoint
-    const float kf = (float)(tid + 1);
-    float ph = a.ckpt[((size_t)s * a.B + b) * a.K + tid];
-    for (int i = 0; i < nt; ++i) {
-      const float freq = kf * s_f0[i];
+  int nslot = 0;
+  for (int j = 0; j < kSlots; ++j) {
+    const float r = a.seg_rows[(size_t)s * kSlots + j];
+    if (r < 0.0f) break;
+    const float* src = a.ctrl + ((size_t)b * a.F + (int)r) * a.ldc;
+    for (int c = lane; c < NC; c += 64) L.row[j][c] = src[c];
+    ++nslot;
+  }
+  for (int i = lane; i < a.NF - 1 + kSeg; i += 64) {
+    const int tt = t0 - (a.NF - 1) + i;
+    L.noise[i] = (tt >= 0 && tt < a.T) ? a.noise[tt] : 0.0f;
+  }
+  wave_sync();
+  if (want_pre) {
+    // inclusive wave scan of each row's first K columns -> pre[j][k+1]
+    for (int j = 0; j < nslot; ++j) {
+      float v = lane < a.K ? L.row[j][lane] : 0.0f;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const float u = __shfl_up(v, d, 64);
+        if (lane >= d) v += u;
+      }
+      if (lane < a.K) L.pre[j][lane + 1] = v;
+      if (lane == 0) L.pre[j][0] = 0.0f;
+    }
+    wave_sync();
+  }
+  return __all(ok) && nt == kSeg;
+}
+
+// Number of harmonics k < K with (k+1)*f0 < nyq (a prefix of k, since
+// (k+1)*f0 is monotone in k).
+__device__ __forceinline__ int below_nyquist(float f0, float nyq, int K) {
+  int lo = 0, hi = K;  // answer in [lo, hi]
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if ((float)mid * f0 < nyq) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+// Chain pass of one segment: lane = harmonic.  For every frame i writes
+// sin(2 pi phase) into sn[i][k] (SN) and sin * masked amplitude into
+// sc[i][k] (SC).  Steps run in blocks of 8 whose LDS reads (frame records,
+// row values) are all issued before the block's arithmetic.
+constexpr int kBlk = 8;
+
+template <bool FAST, bool SC, bool SN>
+__device__ __forceinline__ void chain_loop(const SynthArgs& a, const SegLds& L, float* sc, float* sn, int lane,
+                                           int nt, float ph) {
+  const float kf = (float)(lane + 1);
+  const float nyq = a.sr * 0.5f;
+  const int kk = lane < a.K ? lane : 0;
+  const int n = FAST ? kSeg : nt;
+  for (int i0 = 0; i0 < n; i0 += kBlk) {
+    FrameRec r[kBlk];
+    float al[kBlk], ah[kBlk];
+#pragma unroll
+    for (int j = 0; j < kBlk; ++j) r[j] = L.fr[i0 + j];
+    if (SC) {
+#pragma unroll
+      for (int j = 0; j < kBlk; ++j) {
+        al[j] = L.row[r[j].slots & 255][kk];
+        ah[j] = L.row[r[j].slots >> 8][kk];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kBlk; ++j) {
+      const int i = i0 + j;
+      if (!FAST && i >= nt) break;
+      const float freq = kf * r[j].f0;
+      float inc;
+      if (FAST) {
+        const float q0 = freq * a.rsr;
+        inc = fmaf(fmaf(-q0, a.sr, freq), a.rsr, q0);
+      } else {
+        inc = div_sr(freq, a.sr, a.rsr);
+      }
       const float p = ph;
-      ph = phasor_wrap(ph + freq / a.sr);
-      const float sn = sinf(p * kTwoPi);
-      const float* c0 = a.ctrl + (size_t)(b * a.F + s_lo[i]) * a.ldc;
-      const float* c1 = a.ctrl + (size_t)(b * a.F + s_hi[i]) * a.ldc;
-      const float masked = (s_omf[i] * c0[tid] + s_frac[i] * c1[tid]) * (freq < nyq ? 1.0f : 0.0f);
-      s_contrib[i][tid] = sn * (masked / s_den[i]);
+      ph = FAST ? __builtin_amdgcn_fractf(ph + inc) : phasor_wrap(ph + inc);
+      const float sv = sin2pi(p);
+      if (SC) {
+        const float amp = r[j].omf * al[j] + r[j].frac * ah[j];
+        sc[i * kLd + lane] = freq < nyq ? sv * amp : 0.0f;
+      }
+      if (SN) sn[i * kLd + lane] = sv;
     }
   }
-  __syncthreads();
-  if (tid < nt) {  // phase C: sum over harmonics, FIR noise, mix
-    const int t = t0 + tid;
-    const float omf = s_omf[tid], frac = s_frac[tid];
-    const float* c0 = a.ctrl + (size_t)(b * a.F + s_lo[tid]) * a.ldc;
-    const float* c1 = a.ctrl + (size_t)(b * a.F + s_hi[tid]) * a.ldc;
-    float hsum = 0.f;
-    for (int k = 0; k < a.K; ++k) hsum = hsum + s_contrib[tid][k];
-    const float gain = omf * c0[a.K] + frac * c1[a.K];
-    const float ngain = omf * c0[a.K + 1] + frac * c1[a.K + 1];
-    const float uvi = omf * a.uv[s_lo[tid] * a.B + b] + frac * a.uv[s_hi[tid] * a.B + b];
-    float filt = 0.f;
-    for (int i = 0; i < a.NF; ++i) {
-      const int tt = t - (a.NF - 1) + i;
-      const float w = tt >= 0 ? a.noise[tt] : 0.f;
-      filt = filt + w * (omf * c0[a.K + 2 + i] + frac * c1[a.K + 2 + i]);
-    }
-    const float hout = ((hsum * gain) * uvi) * a.hscale;
+}
+
+template <bool SC, bool SN>
+__device__ __forceinline__ void chain_pass(const SynthArgs& a, const SegLds& L, float* sc, float* sn, int s, int b,
+                                           int lane, int nt, int fast) {
+  const float ph = a.ckpt[((size_t)s * a.B + b) * a.K + (lane < a.K ? lane : 0)];
+  if (fast)
+    chain_loop<true, SC, SN>(a, L, sc, sn, lane, nt, ph);
+  else
+    chain_loop<false, SC, SN>(a, L, sc, sn, lane, nt, ph);
+}
+
+// FIR noise branch for frame i: sum_j noise[t-(NF-1)+j] * tap_j(t).
+__device__ __forceinline__ float frame_fir(const SynthArgs& a, const SegLds& L, int i, const FrameRec& r) {
+  const float* rl = &L.row[r.slots & 255][a.K + 2];
+  const float* rh = &L.row[r.slots >> 8][a.K + 2];
+  const float* w = &L.noise[i];
+  float flo = 0.0f, fhi = 0.0f;
+  for (int j = 0; j < a.NF; ++j) {
+    flo = fmaf(w[j], rl[j], flo);
+    fhi = fmaf(w[j], rh[j], fhi);
+  }
+  return r.omf * flo + r.frac * fhi;
+}
+
+// ------------------------------------------------------------ forward
+// Writes y and the per-frame tape aux = [hsum | den | filt] ([3][B][T]) that
+// the backward reuses.
+constexpr int kWavesFwd = 2;
+
+__global__ __launch_bounds__(64 * kWavesFwd) void k_synth_fwd(SynthArgs a, float* __restrict__ y,
+                                                              float* __restrict__ aux) {
+  __shared__ SegLds lds[kWavesFwd];
+  __shared__ float s_c[kWavesFwd][kSeg * kLd];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int nseg = (a.T + kSeg - 1) / kSeg;
+  const int s = blockIdx.x * kWavesFwd + wave, b = blockIdx.y;
+  if (s >= nseg) return;
+  SegLds& L = lds[wave];
+  float* sc = s_c[wave];
+  const int t0 = s * kSeg, nt = min(kSeg, a.T - t0);
+  const int fast = stage_segment(a, L, s, b, lane, nt, true);
+  chain_pass<true, false>(a, L, sc, nullptr, s, b, lane, nt, fast);
+  wave_sync();
+  if (lane < nt) {
+    const int t = t0 + lane;
+    const FrameRec r = L.fr[lane];
+    const int slo = r.slots & 255, shi = r.slots >> 8;
+    float num = 0.0f;
+    const float* row = sc + lane * kLd;
+    for (int k = 0; k < a.K; ++k) num += row[k];
+    const int n = below_nyquist(r.f0, a.sr * 0.5f, a.K);
+    const float den = r.omf * L.pre[slo][n] + r.frac * L.pre[shi][n] + 1e-8f;
+    const float hsum = num / den;
+    const float gain = r.omf * L.row[slo][a.K] + r.frac * L.row[shi][a.K];
+    const float ngain = r.omf * L.row[slo][a.K + 1] + r.frac * L.row[shi][a.K + 1];
+    const float filt = frame_fir(a, L, lane, r);
+    const float uv = a.uvf[(size_t)b * a.T + t];
+    const float hout = ((hsum * gain) * uv) * a.hscale;
     const float nout = ((filt * ngain) * 0.12f) * a.nscale;
-    const float v = hout + nout;
-    y[(size_t)b * a.T + t] = isfinite(v) ? v : 0.f;  // dgen_runtime.h:58-85 containment
+    const float o = hout + nout;
+    const size_t bt = (size_t)b * a.T + t, plane = (size_t)a.B * a.T;
+    y[bt] = isfinite(o) ? o : 0.0f;  // dgen_runtime.h:58-85 containment
+    if (aux) {
+      aux[bt] = hsum;
+      aux[plane + bt] = den;
+      aux[2 * plane + bt] = filt;
+    }
   }
 }
 
 // ------------------------------------------------------------ backward
-// Per (segment, batch): recompute the forward quantities, then one thread
-// per control column accumulates its gradient into <= 4 row slots.
-__global__ __launch_bounds__(128) void k_synth_bwd(SynthArgs a, const float* __restrict__ dy,
-                                                   float* __restrict__ part) {
-  __shared__ float s_den[kMaxSeg], s_f0[kMaxSeg], s_omf[kMaxSeg], s_frac[kMaxSeg];
-  __shared__ int s_lo[kMaxSeg], s_hi[kMaxSeg], s_slo[kMaxSeg], s_shi[kMaxSeg];
-  __shared__ float s_dhsum[kMaxSeg], s_dot[kMaxSeg], s_dgain[kMaxSeg], s_dngain[kMaxSeg], s_dfilt[kMaxSeg];
-  __shared__ float s_sin[kMaxSeg][kMaxK + 1];
-  __shared__ float s_amp[kMaxSeg][kMaxK + 1];
-  const int s = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-  const int t0 = s * a.seg, nt = min(a.seg, a.T - t0);
-  const int nseg = (a.T + a.seg - 1) / a.seg;
-  const float nyq = a.sr * 0.5f;
+// Per (segment, batch) wave: recompute the phases, then accumulate every
+// control column's gradient into <= 4 row slots:
+//   d amp_k = dhsum * (sin_k - hsum) / den * mask_k       (normalised amps)
+//   d gain  = g * hsum * uv * hscale,  d ngain = g * filt * 0.12 * nscale
+//   d tap_j = g * ngain * 0.12 * nscale * noise[t-(NF-1)+j]
+// each scattered to rows lo/hi with weights 1-frac / frac
+// (sampleInline gradient, Emit+RowSelection.swift:100-141).  Column c is
+// handled by lane c & 63 in pass c >> 6.
+constexpr int kWavesBwd = 2;
 
-  if (tid < nt) {
-    const int t = t0 + tid;
-    const FrameRow r = frame_row(a.lerp, t);
-    const float f0i = r.omf * a.f0[r.lo * a.B + b] + r.frac * a.f0[r.hi * a.B + b];
-    const float* c0 = a.ctrl + (size_t)(b * a.F + r.lo) * a.ldc;
-    const float* c1 = a.ctrl + (size_t)(b * a.F + r.hi) * a.ldc;
-    float den = 0.f;
-    for (int k = 0; k < a.K; ++k) {
-      const float freq = (float)(k + 1) * f0i;
-      den = den + (r.omf * c0[k] + r.frac * c1[k]) * (freq < nyq ? 1.0f : 0.0f);
-    }
-    s_den[tid] = den + 1e-8f;
-    s_f0[tid] = f0i;
-    s_omf[tid] = r.omf;
-    s_frac[tid] = r.frac;
-    s_lo[tid] = r.lo;
-    s_hi[tid] = r.hi;
-    s_slo[tid] = r.slo;
-    s_shi[tid] = r.shi;
+// Four row-slot accumulators of one control column.  Frames come in runs
+// with a constant slot pair; a run is summed in two registers and added to
+// the slots when the pair changes.
+struct SlotAcc {
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+  float sl = 0.f, sh = 0.f;
+  int cur = -1;
+  __device__ __forceinline__ void put(int slot, float v) {
+    a0 += slot == 0 ? v : 0.f;
+    a1 += slot == 1 ? v : 0.f;
+    a2 += slot == 2 ? v : 0.f;
+    a3 += slot == 3 ? v : 0.f;
   }
-  __syncthreads();
-  if (tid < a.K) {
-    const float kf = (float)(tid + 1);
-    float ph = a.ckpt[((size_t)s * a.B + b) * a.K + tid];
-    for (int i = 0; i < nt; ++i) {
-      const float freq = kf * s_f0[i];
-      const float p = ph;
-      ph = phasor_wrap(ph + freq / a.sr);
-      s_sin[i][tid] = sinf(p * kTwoPi);
-      const float* c0 = a.ctrl + (size_t)(b * a.F + s_lo[i]) * a.ldc;
-      const float* c1 = a.ctrl + (size_t)(b * a.F + s_hi[i]) * a.ldc;
-      const float masked = (s_omf[i] * c0[tid] + s_frac[i] * c1[tid]) * (freq < nyq ? 1.0f : 0.0f);
-      s_amp[i][tid] = masked / s_den[i];
+  __device__ __forceinline__ void flush() {
+    if (cur >= 0) {
+      put(cur & 255, sl);
+      put(cur >> 8, sh);
     }
+    sl = sh = 0.f;
   }
-  __syncthreads();
-  if (tid < nt) {
-    const int t = t0 + tid;
-    const float omf = s_omf[tid], frac = s_frac[tid];
-    const float* c0 = a.ctrl + (size_t)(b * a.F + s_lo[tid]) * a.ldc;
-    const float* c1 = a.ctrl + (size_t)(b * a.F + s_hi[tid]) * a.ldc;
-    float hsum = 0.f;
-    for (int k = 0; k < a.K; ++k) hsum = hsum + s_sin[tid][k] * s_amp[tid][k];
-    const float gain = omf * c0[a.K] + frac * c1[a.K];
-    const float ngain = omf * c0[a.K + 1] + frac * c1[a.K + 1];
-    const float uvi = omf * a.uv[s_lo[tid] * a.B + b] + frac * a.uv[s_hi[tid] * a.B + b];
-    float filt = 0.f;
-    for (int i = 0; i < a.NF; ++i) {
-      const int tt = t - (a.NF - 1) + i;
-      const float w = tt >= 0 ? a.noise[tt] : 0.f;
-      filt = filt + w * (omf * c0[a.K + 2 + i] + frac * c1[a.K + 2 + i]);
+  __device__ __forceinline__ void add(int slots, float wl, float wh) {
+    if (slots != cur) {
+      flush();
+      cur = slots;
     }
-    const float g = dy[(size_t)b * a.T + t];
-    const float dhsum = g * gain * uvi * a.hscale;
-    float dot = 0.f;
-    for (int k = 0; k < a.K; ++k) dot = dot + dhsum * s_sin[tid][k] * s_amp[tid][k];
-    s_dhsum[tid] = dhsum;
-    s_dot[tid] = dot;
-    s_dgain[tid] = g * hsum * uvi * a.hscale;
-    s_dfilt[tid] = g * ngain * 0.12f * a.nscale;
-    s_dngain[tid] = g * filt * 0.12f * a.nscale;
+    sl += wl;
+    sh += wh;
   }
-  __syncthreads();
+  __device__ __forceinline__ void store(float* out, int ldc, int c) {
+    flush();
+    out[0 * ldc + c] = a0;
+    out[1 * ldc + c] = a1;
+    out[2 * ldc + c] = a2;
+    out[3 * ldc + c] = a3;
+  }
+};
+
+__global__ __launch_bounds__(64 * kWavesBwd) void k_synth_bwd(SynthArgs a, const float* __restrict__ dy,
+                                                              const float* __restrict__ aux,
+                                                              float* __restrict__ part) {
+  __shared__ SegLds lds[kWavesBwd];
+  __shared__ float s_s[kWavesBwd][kSeg * kLd];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int nseg = (a.T + kSeg - 1) / kSeg;
+  const int s = blockIdx.x * kWavesBwd + wave, b = blockIdx.y;
+  if (s >= nseg) return;
+  SegLds& L = lds[wave];
+  float* sn = s_s[wave];
+  const int t0 = s * kSeg, nt = min(kSeg, a.T - t0);
+  const int fast = stage_segment(a, L, s, b, lane, nt, false);
+  chain_pass<false, true>(a, L, nullptr, sn, s, b, lane, nt, fast);
+  {
+    float hs = 0.f, coef = 0.f, dg = 0.f, dng = 0.f, dfl = 0.f;
+    if (lane < nt) {
+      const int t = t0 + lane;
+      const FrameRec r = L.fr[lane];
+      const int slo = r.slots & 255, shi = r.slots >> 8;
+      const size_t bt = (size_t)b * a.T + t, plane = (size_t)a.B * a.T;
+      const float hsum = aux[bt], den = aux[plane + bt], filt = aux[2 * plane + bt];
+      const float gain = r.omf * L.row[slo][a.K] + r.frac * L.row[shi][a.K];
+      const float ngain = r.omf * L.row[slo][a.K + 1] + r.frac * L.row[shi][a.K + 1];
+      const float uv = a.uvf[bt];
+      const float g = dy[bt];
+      hs = hsum;
+      coef = (((g * gain) * uv) * a.hscale) / den;
+      dg = ((g * hsum) * uv) * a.hscale;
+      dng = ((g * filt) * 0.12f) * a.nscale;
+      dfl = ((g * ngain) * 0.12f) * a.nscale;
+    }
+    L.hs[lane] = hs;
+    L.coef[lane] = coef;
+    L.dg[lane] = dg;
+    L.dng[lane] = dng;
+    L.dfl[lane] = dfl;
+  }
+  wave_sync();
+
   const int NC = a.K + 2 + a.NF;
-  if (tid < NC) {
-    float acc[kSlots] = {0.f, 0.f, 0.f, 0.f};
-    const float kf = (float)(tid + 1);
-    for (int i = 0; i < nt; ++i) {
-      float dm;
-      if (tid < a.K) {
-        const float mk = kf * s_f0[i] < nyq ? 1.0f : 0.0f;
-        dm = (s_dhsum[i] * s_sin[i][tid] - s_dot[i]) / s_den[i] * mk;
-      } else if (tid == a.K) {
-        dm = s_dgain[i];
-      } else if (tid == a.K + 1) {
-        dm = s_dngain[i];
-      } else {
-        const int tt = t0 + i - (a.NF - 1) + (tid - a.K - 2);
-        dm = s_dfilt[i] * (tt >= 0 ? a.noise[tt] : 0.f);
-      }
-      acc[s_slo[i]] += s_omf[i] * dm;
-      acc[s_shi[i]] += s_frac[i] * dm;
-    }
-    float* out = part + ((size_t)b * nseg + s) * kSlots * a.ldc;
+  const float nyq = a.sr * 0.5f;
+  float* out = part + ((size_t)b * nseg + s) * kSlots * a.ldc;
+  for (int c0 = 0; c0 < NC; c0 += 64) {
+    const int c = c0 + lane;
+    const bool harm = c < a.K;
+    const float kf = (float)(c + 1);
+    const int q = c - a.K;  // 0: gain, 1: noise gain, q >= 2: tap q-2
+    const int nidx = max(q - 2, 0);
+    SlotAcc acc;
+    for (int i0 = 0; i0 < nt; i0 += kBlk) {
+      FrameRec r[kBlk];
+      float sv[kBlk], hs[kBlk], cf[kBlk], ex[kBlk];
 #pragma unroll
-    for (int j = 0; j < kSlots; ++j) out[(size_t)j * a.ldc + tid] = acc[j];
+      for (int j = 0; j < kBlk; ++j) {
+        const int i = i0 + j;
+        r[j] = L.fr[i];
+        sv[j] = sn[i * kLd + lane];
+        hs[j] = L.hs[i];
+        cf[j] = L.coef[i];
+        ex[j] = q == 0 ? L.dg[i] : (q == 1 ? L.dng[i] : L.dfl[i] * L.noise[i + nidx]);
+      }
+#pragma unroll
+      for (int j = 0; j < kBlk; ++j) {
+        if (i0 + j >= nt) break;
+        const float dm = harm ? (kf * r[j].f0 < nyq ? (sv[j] - hs[j]) * cf[j] : 0.0f) : ex[j];
+        acc.add(r[j].slots, r[j].omf * dm, r[j].frac * dm);
+      }
+    }
+    if (c < NC) acc.store(out, a.ldc, c);
   }
 }
 
@@ -294,38 +660,41 @@ __global__ void k_synth_bwd_reduce(const float* __restrict__ part, const float* 
 }
 
 static int synth_args(const Launch& L, const dgen_hip_op& op, SynthArgs& a, const char* who) {
-  // arg: [0]=ctrl [1]=f0 [2]=uv [3]=lerp [4]=checkpoints [5]=y/dy [6]=B [7]=K [8]=NF [9]=F [10]=T [11]=seg
-  //      [12]=partials (bwd) [13]=noise [14]=ldc
+  // arg: [0]=ctrl [1]=f0 frames [2]=uv frames [3]=lerp [4]=checkpoints [5]=y/dy [6]=B [7]=K [8]=NF [9]=F [10]=T
+  //      [11]=seg (64) [12]=partials (bwd) [13]=noise [14]=ldc [15]=seg_rows
   const int64_t B = op.arg[6], K = op.arg[7], NF = op.arg[8], F = op.arg[9], T = op.arg[10], seg = op.arg[11];
   const int64_t ldc = op.arg[14];
   DGEN_REQUIRE(B > 0 && B <= 65535 && K > 0 && K <= kMaxK && NF > 0 && F > 0 && T > 0 && T <= (1 << 26) &&
-                   seg > 0 && seg <= kMaxSeg && K + 2 + NF <= kMaxNC && ldc >= K + 2 + NF,
+                   seg == kSeg && K + 2 + NF <= kMaxNC && ldc >= K + 2 + NF,
                "%s: B %lld K %lld NF %lld F %lld T %lld seg %lld ldc %lld", who, (long long)B, (long long)K,
                (long long)NF, (long long)F, (long long)T, (long long)seg, (long long)ldc);
+  DGEN_REQUIRE(op.farg[0] > 0.f && op.farg[0] < 1e30f, "%s: sample rate %g", who, (double)op.farg[0]);
+  DGEN_REQUIRE(op.arg[3] % 4 == 0, "%s: lerp table must be 16-byte aligned", who);
   const int64_t nseg = (T + seg - 1) / seg;
-  DGEN_REQUIRE(nseg <= 2147483647ll, "%s: too many segments", who);
   DGEN_CHECK_CELL(L, op.arg[0], B * F * ldc, "synth.ctrl");
-  DGEN_CHECK_CELL(L, op.arg[1], F * B, "synth.f0");
-  DGEN_CHECK_CELL(L, op.arg[2], F * B, "synth.uv");
+  DGEN_CHECK_CELL(L, op.arg[1], B * T, "synth.f0_frames");
+  DGEN_CHECK_CELL(L, op.arg[2], B * T, "synth.uv_frames");
   DGEN_CHECK_CELL(L, op.arg[3], T * 8, "synth.lerp");
   DGEN_CHECK_CELL(L, op.arg[4], nseg * B * K, "synth.checkpoints");
   DGEN_CHECK_CELL(L, op.arg[5], B * T, "synth.y");
   DGEN_CHECK_CELL(L, op.arg[13], T, "synth.noise");
+  DGEN_CHECK_CELL(L, op.arg[15], nseg * kSlots, "synth.seg_rows");
   if (L.dry) return 0;
   a.ctrl = cell(L, op.arg[0]);
-  a.ldc = (int)ldc;
-  a.f0 = cell(L, op.arg[1]);
-  a.uv = cell(L, op.arg[2]);
+  a.f0f = cell(L, op.arg[1]);
+  a.uvf = cell(L, op.arg[2]);
   a.lerp = cell(L, op.arg[3]);
   a.ckpt = cell(L, op.arg[4]);
   a.noise = cell(L, op.arg[13]);
+  a.seg_rows = cell(L, op.arg[15]);
+  a.ldc = (int)ldc;
   a.B = (int)B;
   a.K = (int)K;
   a.NF = (int)NF;
   a.F = (int)F;
   a.T = (int)T;
-  a.seg = (int)seg;
   a.sr = op.farg[0];
+  a.rsr = 1.0f / a.sr;
   a.hscale = op.farg[1];
   a.nscale = op.farg[2];
   return 0;
@@ -334,9 +703,13 @@ static int synth_args(const Launch& L, const dgen_hip_op& op, SynthArgs& a, cons
 int launch_synth_fwd(const Launch& L, const dgen_hip_op& op) {
   SynthArgs a{};
   int rc = synth_args(L, op, a, "synth_fwd");
-  if (rc || L.dry) return rc;
-  const int nseg = (a.T + a.seg - 1) / a.seg;
-  hipLaunchKernelGGL(k_synth_fwd, dim3((unsigned)nseg, (unsigned)a.B), dim3(64), 0, L.stream, a, cell(L, op.arg[5]));
+  if (rc) return rc;
+  if (op.arg[12] >= 0) DGEN_CHECK_CELL(L, op.arg[12], 3 * op.arg[6] * op.arg[10], "synth_fwd.aux");
+  if (L.dry) return 0;
+  const int nseg = (a.T + kSeg - 1) / kSeg;
+  hipLaunchKernelGGL(k_synth_fwd, dim3((unsigned)((nseg + kWavesFwd - 1) / kWavesFwd), (unsigned)a.B),
+                     dim3(64 * kWavesFwd), 0, L.stream, a, cell(L, op.arg[5]),
+                     op.arg[12] >= 0 ? cell(L, op.arg[12]) : nullptr);
   DGEN_LAUNCH_CHECK("k_synth_fwd");
   return 0;
 }
@@ -345,12 +718,14 @@ int launch_synth_bwd(const Launch& L, const dgen_hip_op& op) {
   SynthArgs a{};
   int rc = synth_args(L, op, a, "synth_bwd");
   if (rc) return rc;
-  const int64_t T = op.arg[10], seg = op.arg[11], B = op.arg[6], ldc = op.arg[14];
-  const int64_t nseg = (T + seg - 1) / seg;
+  const int64_t T = op.arg[10], B = op.arg[6], ldc = op.arg[14];
+  const int64_t nseg = (T + kSeg - 1) / kSeg;
   DGEN_CHECK_CELL(L, op.arg[12], B * nseg * kSlots * ldc, "synth_bwd.partials");
+  DGEN_CHECK_CELL(L, op.arg[16], 3 * B * T, "synth_bwd.aux");
   if (L.dry) return 0;
-  hipLaunchKernelGGL(k_synth_bwd, dim3((unsigned)nseg, (unsigned)a.B), dim3(128), 0, L.stream, a,
-                     cell(L, op.arg[5]), cell(L, op.arg[12]));
+  hipLaunchKernelGGL(k_synth_bwd, dim3((unsigned)((nseg + kWavesBwd - 1) / kWavesBwd), (unsigned)a.B),
+                     dim3(64 * kWavesBwd), 0, L.stream, a, cell(L, op.arg[5]), cell(L, op.arg[16]),
+                     cell(L, op.arg[12]));
   DGEN_LAUNCH_CHECK("k_synth_bwd");
   return 0;
 }
@@ -359,7 +734,7 @@ int launch_synth_bwd_reduce(const Launch& L, const dgen_hip_op& op) {
   // arg: [0]=partials [1]=row_list [2]=dctrl [3]=B [4]=NC [5]=F [6]=T [7]=seg [8]=ldc
   const int64_t part = op.arg[0], rl = op.arg[1], dc = op.arg[2], B = op.arg[3], NC = op.arg[4], F = op.arg[5],
                 T = op.arg[6], seg = op.arg[7], ldc = op.arg[8];
-  DGEN_REQUIRE(B > 0 && B <= 65535 && NC > 0 && ldc >= NC && ldc <= 1024 && F > 0 && T > 0 && seg > 0,
+  DGEN_REQUIRE(B > 0 && B <= 65535 && NC > 0 && ldc >= NC && ldc <= 1024 && F > 0 && T > 0 && seg == kSeg,
                "synth_bwd_reduce: B %lld NC %lld F %lld T %lld seg %lld ldc %lld", (long long)B, (long long)NC,
                (long long)F, (long long)T, (long long)seg, (long long)ldc);
   const int64_t nseg = (T + seg - 1) / seg;

@@ -48,77 +48,119 @@ int launch_dense_small(const Launch& L, const dgen_hip_op& op) {
   return 0;
 }
 
-// Two-stage column reduction: partial[c][n] = sum over row chunk c of
-// scale_row(m) * A[m][n]; out[n] = sum_c partial[c][n] in chunk order.
+// Deterministic two-stage column reductions over the row (batch) axis:
+//   out_q[n] = sum_m w_q(m) * A[m][n],  w_q(m) = X[m][q] for q < nw, 1 for q = nw
+// Stage 1: workgroup (column block of 64, row chunk c); its 4 waves stride the
+// chunk's rows, lanes read 64 consecutive columns (256-byte rows), and the
+// waves' sums are combined in LDS in wave order -> part[c][q][n].
+// Stage 2: one workgroup per 64 columns sums the chunk partials in chunk order
+// (4 waves over interleaved chunks, then wave order).
 constexpr int kColChunks = 256;
+constexpr int kMaxW = 4;  // weighted sums besides the plain one
 
-__global__ void k_colsum_partial(const float* __restrict__ A, int lda, const float* __restrict__ X, int ldx,
-                                 int xcol, float* __restrict__ part, int rows, int cols, int chunk) {
-  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+__global__ __launch_bounds__(256) void k_colsum_partial(const float* __restrict__ A, int lda,
+                                                        const float* __restrict__ X, int nw, int rows, int cols,
+                                                        int chunk, float* __restrict__ part, int want_plain) {
+  __shared__ float red[4][kMaxW + 1][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 64 + lane;
   const int c = blockIdx.y;
-  if (n >= cols) return;
   const int m0 = c * chunk, m1 = min(rows, m0 + chunk);
-  float s = 0.f;
-  if (X) {
-    for (int m = m0; m < m1; ++m) s += X[(size_t)m * ldx + xcol] * A[(size_t)m * lda + n];
-  } else {
-    for (int m = m0; m < m1; ++m) s += A[(size_t)m * lda + n];
+  float acc[kMaxW + 1];
+#pragma unroll
+  for (int q = 0; q <= kMaxW; ++q) acc[q] = 0.f;
+  if (n < cols) {
+#pragma unroll 4
+    for (int m = m0 + wave; m < m1; m += 4) {
+      const float v = A[(size_t)m * lda + n];
+#pragma unroll
+      for (int q = 0; q < kMaxW; ++q)
+        if (q < nw) acc[q] += X[(size_t)m * nw + q] * v;
+      acc[kMaxW] += v;
+    }
   }
-  part[(size_t)c * cols + n] = s;
+#pragma unroll
+  for (int q = 0; q <= kMaxW; ++q) red[wave][q][lane] = acc[q];
+  __syncthreads();
+  if (wave == 0 && n < cols) {
+    const int nq = nw + (want_plain ? 1 : 0);
+    for (int q = 0; q < nq; ++q) {
+      const int src = q < nw ? q : kMaxW;
+      const float v = ((red[0][src][lane] + red[1][src][lane]) + red[2][src][lane]) + red[3][src][lane];
+      part[((size_t)c * nq + q) * cols + n] = v;
+    }
+  }
 }
 
-__global__ void k_colsum_final(const float* __restrict__ part, float* __restrict__ out, int chunks, int cols) {
-  const int n = blockIdx.x * blockDim.x + threadIdx.x;
-  if (n >= cols) return;
+__global__ __launch_bounds__(256) void k_colsum_final(const float* __restrict__ part, int chunks, int nq, int cols,
+                                                      float* __restrict__ out0, int ld_out0,
+                                                      float* __restrict__ plain_out, int want_plain) {
+  __shared__ float red[4][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 64 + lane;
+  const int q = blockIdx.y;
   float s = 0.f;
-  for (int c = 0; c < chunks; ++c) s += part[(size_t)c * cols + n];
-  out[n] = s;
+  if (n < cols)
+    for (int c = wave; c < chunks; c += 4) s += part[((size_t)c * nq + q) * cols + n];
+  red[wave][lane] = s;
+  __syncthreads();
+  if (wave == 0 && n < cols) {
+    const float v = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+    if (want_plain && q == nq - 1)
+      plain_out[n] = v;
+    else
+      out0[(size_t)q * ld_out0 + n] = v;
+  }
 }
 
-static int colsum_chunks(int64_t rows) { return (int)std::min<int64_t>(kColChunks, std::max<int64_t>(1, rows / 16)); }
+static int colsum_chunks(int64_t rows) { return (int)std::min<int64_t>(kColChunks, std::max<int64_t>(1, rows / 32)); }
+
+// out_q (q < nw) rows of out0 (stride ld_out0) and the plain sum into plain_out.
+static int colsum_launch(const Launch& L, const float* A, int lda, const float* X, int nw, int rows, int cols,
+                         float* ws, float* out0, int ld_out0, float* plain_out) {
+  const int chunks = colsum_chunks(rows);
+  const int chunk = (rows + chunks - 1) / chunks;
+  const int want_plain = plain_out != nullptr;
+  const int nq = nw + want_plain;
+  hipLaunchKernelGGL(k_colsum_partial, dim3((unsigned)((cols + 63) / 64), (unsigned)chunks), dim3(256), 0, L.stream,
+                     A, lda, X, nw, rows, cols, chunk, ws, want_plain);
+  DGEN_LAUNCH_CHECK("k_colsum_partial");
+  hipLaunchKernelGGL(k_colsum_final, dim3((unsigned)((cols + 63) / 64), (unsigned)nq), dim3(256), 0, L.stream, ws,
+                     chunks, nq, cols, out0, ld_out0, plain_out, want_plain);
+  DGEN_LAUNCH_CHECK("k_colsum_final");
+  return 0;
+}
 
 int launch_colsum(const Launch& L, const dgen_hip_op& op) {
   const int64_t A = op.arg[0], out = op.arg[1], rows = op.arg[2], cols = op.arg[3], lda = op.arg[4], ws = op.arg[5];
-  DGEN_REQUIRE(rows > 0 && cols > 0 && lda >= cols && cols <= 65536, "colsum: rows %lld cols %lld lda %lld",
-               (long long)rows, (long long)cols, (long long)lda);
+  DGEN_REQUIRE(rows > 0 && rows < (1ll << 31) && cols > 0 && lda >= cols && cols <= 65536,
+               "colsum: rows %lld cols %lld lda %lld", (long long)rows, (long long)cols, (long long)lda);
   const int chunks = colsum_chunks(rows);
   DGEN_CHECK_CELL(L, A, (rows - 1) * lda + cols, "colsum.A");
   DGEN_CHECK_CELL(L, out, cols, "colsum.out");
   DGEN_CHECK_CELL(L, ws, (int64_t)chunks * cols, "colsum.workspace");
   if (L.dry) return 0;
-  const int chunk = (int)((rows + chunks - 1) / chunks);
-  hipLaunchKernelGGL(k_colsum_partial, dim3((unsigned)((cols + 63) / 64), chunks), dim3(64), 0, L.stream, cell(L, A),
-                     (int)lda, nullptr, 0, 0, cell(L, ws), (int)rows, (int)cols, chunk);
-  DGEN_LAUNCH_CHECK("k_colsum_partial");
-  hipLaunchKernelGGL(k_colsum_final, dim3((unsigned)((cols + 255) / 256)), dim3(256), 0, L.stream, cell(L, ws),
-                     cell(L, out), chunks, (int)cols);
-  DGEN_LAUNCH_CHECK("k_colsum_final");
-  return 0;
+  return colsum_launch(L, cell(L, A), (int)lda, nullptr, 0, (int)rows, (int)cols, cell(L, ws), nullptr, 0,
+                       cell(L, out));
 }
 
-// dW[i][j] = sum_m X[m][i] dZ[m][j] for a small fan-in (first layer).
+// dW[i][j] = sum_m X[m][i] dZ[m][j] for a small fan-in (first layer), and
+// optionally the bias gradient db[j] = sum_m dZ[m][j] from the same pass.
 int launch_dense_small_wgrad(const Launch& L, const dgen_hip_op& op) {
   const int64_t X = op.arg[0], dZ = op.arg[1], dW = op.arg[2], rows = op.arg[3], fan = op.arg[4],
-                width = op.arg[5], ws = op.arg[6];
-  DGEN_REQUIRE(rows > 0 && fan > 0 && fan <= 64 && width > 0 && width <= 65536,
+                width = op.arg[5], ws = op.arg[6], db = op.arg[7];
+  DGEN_REQUIRE(rows > 0 && rows < (1ll << 31) && fan > 0 && fan <= kMaxW && width > 0 && width <= 65536,
                "dense_small_wgrad: rows %lld fan %lld width %lld", (long long)rows, (long long)fan,
                (long long)width);
   const int chunks = colsum_chunks(rows);
   DGEN_CHECK_CELL(L, X, rows * fan, "dense_small_wgrad.X");
   DGEN_CHECK_CELL(L, dZ, rows * width, "dense_small_wgrad.dZ");
   DGEN_CHECK_CELL(L, dW, fan * width, "dense_small_wgrad.dW");
-  DGEN_CHECK_CELL(L, ws, (int64_t)chunks * width, "dense_small_wgrad.workspace");
+  if (db >= 0) DGEN_CHECK_CELL(L, db, width, "dense_small_wgrad.db");
+  DGEN_CHECK_CELL(L, ws, (int64_t)chunks * (fan + 1) * width, "dense_small_wgrad.workspace");
   if (L.dry) return 0;
-  const int chunk = (int)((rows + chunks - 1) / chunks);
-  for (int i = 0; i < fan; ++i) {
-    hipLaunchKernelGGL(k_colsum_partial, dim3((unsigned)((width + 63) / 64), chunks), dim3(64), 0, L.stream,
-                       cell(L, dZ), (int)width, cell(L, X), (int)fan, i, cell(L, ws), (int)rows, (int)width, chunk);
-    DGEN_LAUNCH_CHECK("k_colsum_partial");
-    hipLaunchKernelGGL(k_colsum_final, dim3((unsigned)((width + 255) / 256)), dim3(256), 0, L.stream, cell(L, ws),
-                       cell(L, dW) + (size_t)i * width, chunks, (int)width);
-    DGEN_LAUNCH_CHECK("k_colsum_final");
-  }
-  return 0;
+  return colsum_launch(L, cell(L, dZ), (int)width, cell(L, X), (int)fan, (int)rows, (int)width, cell(L, ws),
+                       cell(L, dW), (int)width, db >= 0 ? cell(L, db) : nullptr);
 }
 
 // ---------------------------------------------------------------- heads

@@ -1,181 +1,461 @@
-// Hop-gated batched spectral loss (spectralLossFFTBatched + BatchedReduce and
-// the GradSpec / GradIFFT / GradRead backward chain,
-// Sources/DGen/Emit+SpectralLoss.swift:719-1235) for one FFT size per launch.
+// Hop-gated batched multi-scale spectral loss and its gradient, all FFT
+// sizes fused (spectralLossFFTBatched + BatchedReduce and the GradSpec /
+// GradIFFT / GradRead chain, Sources/DGen/Emit+SpectralLoss.swift:719-1235;
+// HarmonicE2E's fullBatchedLoss, Examples/HarmonicE2E/Trainer.swift:538-583).
 //
-// The reference runs one thread per (frame, batch) with a serial N-point FFT
-// in threadgroup scratch and idles on non-hop frames.  Here one workgroup
-// owns one (hop window, batch) pair: the window is read once, multiplied by
-// the symmetric Hann table and scattered in bit-reversed order into LDS; the
-// prediction and target spectra are transformed together (radix-2 stages,
-// all butterflies of a stage in parallel); magnitudes, the L1 and log-L1
-// terms and the gradient spectrum are formed in place; the unnormalised
-// inverse transform and the window multiply produce the window's time
-// gradient.  A gather kernel then sums, for every sample, the <= N/H+1
-// windows that contain it (atomic-free, fixed order) and forms the
-// per-frame loss signal.
+// Per FFT size N (hop H = N/4) and hop frame f = w*H the reference windows
+// x[f-N+1 .. f] (zero outside [0,T)) with the symmetric Hann
+// 0.5*(1 - cos(2 pi i/(N-1))), transforms prediction and target, and over the
+// bins k = 0..N/2 accumulates |m1 - m2| and |log(m1+eps) - log(m2+eps)|.
+// Its gradient spectrum G_k = dmag_k * X_k / max(m1, eps) (bins above N/2
+// zero) goes through an unnormalised inverse transform whose real part,
+// times the window, is added to dx over the window's samples.
+//
+// Work decomposition (one workgroup = 256 threads):
+// - the workgroup owns an output tile [a, a+4096) of one batch lane and all
+//   windows whose hop frame lies in it, for every size;
+// - a real N-point transform is an N/2-point complex Stockham FFT of
+//   z[n] = s[2n] + i s[2n+1] plus the even/odd split; the real-output
+//   inverse is the mirror image (Hermitian pre-processing, N/2-point inverse
+//   FFT giving g[2n] + i g[2n+1]);
+// - windows processed together are 4 hops (= N samples) apart, so their
+//   overlap-add into the tile's LDS accumulator never collides; groups run
+//   in a fixed order, so the sums are deterministic and atomic-free;
+// - the accumulator spans [a-2047, a+4096); the part left of a belongs to the
+//   previous tile and is added by k_mss_combine, which also forms the
+//   per-frame loss signal.
+// FFT passes follow the Stockham autosort formulation of Govindaraju et al.,
+// "High Performance Discrete Fourier Transforms on Graphics Processors"
+// (SC 2008): pass with radix R and span Ns reads v_r = in[j + r*M/R],
+// twiddles by exp(-+2 pi i r (j mod Ns)/(Ns R)), does an R-point DFT and
+// writes out[(j/Ns)*Ns*R + j mod Ns + r*Ns].
 #include "internal.h"
 
 namespace dgen {
 
-constexpr float kLogEps = 1e-8f;  // DGenSpectralConfig.logMagnitudeEpsilon (GradientConfig.swift:38)
-constexpr float kMagEps = 1e-8f;  // safeMag = max(mag, 1e-8) (Emit+SpectralLoss.swift:1005-1006)
+constexpr int kTile = 4096;        // output samples owned by a workgroup
+constexpr int kHalo = 2047;        // largest N - 1
+constexpr int kAcc = kTile + kHalo;
+constexpr int kThreads = 256;
 constexpr int kMaxSizes = 8;
+constexpr float kLogEps = 1e-8f;   // DGenSpectralConfig.logMagnitudeEpsilon (GradientConfig.swift:38)
+constexpr float kMagEps = 1e-8f;   // safeMag = max(mag, 1e-8) (Emit+SpectralLoss.swift:1005-1006)
 
-__device__ __forceinline__ float sgn(float v) { return v > 0.f ? 1.f : (v < 0.f ? -1.f : 0.f); }
+struct MssArgs {
+  const float* x;
+  const float* tgt;
+  float* part;                     // [B][ntiles][kAcc]
+  float* wloss[kMaxSizes];         // per size: [nwin][B][2] (lin, log)
+  const float* hann[kMaxSizes];    // per size: symmetric Hann table [N] (double-evaluated)
+  int logn[kMaxSizes];
+  int nsizes, B, T, ntiles;
+  float gl, gg;                    // upstream gradient of each window's lin / log sum
+};
 
-__device__ __forceinline__ void fft_stages(float* re0, float* im0, float* re1, float* im1, const float* twre,
-                                           const float* twim, int n, int logn, float dir, bool two) {
-  for (int s = 0; s < logn; ++s) {
-    const int half = 1 << s;
-    for (int idx = threadIdx.x; idx < n / 2; idx += blockDim.x) {
-      const int g = idx >> s, k = idx & (half - 1);
-      const int i = (g << (s + 1)) + k, j = i + half;
-      const float wr = twre[half - 1 + k];
-      const float wi = dir * twim[half - 1 + k];
-      {
-        const float br = re0[j], bi = im0[j];
-        const float tr = wr * br - wi * bi, ti = wr * bi + wi * br;
-        const float ar = re0[i], ai = im0[i];
-        re0[i] = ar + tr;
-        im0[i] = ai + ti;
-        re0[j] = ar - tr;
-        im0[j] = ai - ti;
-      }
-      if (two) {
-        const float br = re1[j], bi = im1[j];
-        const float tr = wr * br - wi * bi, ti = wr * bi + wi * br;
-        const float ar = re1[i], ai = im1[i];
-        re1[i] = ar + tr;
-        im1[i] = ai + ti;
-        re1[j] = ar - tr;
-        im1[j] = ai - ti;
+struct c2 {
+  float x, y;
+};
+__device__ __forceinline__ c2 cadd(c2 a, c2 b) { return {a.x + b.x, a.y + b.y}; }
+__device__ __forceinline__ c2 csub(c2 a, c2 b) { return {a.x - b.x, a.y - b.y}; }
+__device__ __forceinline__ c2 cmul(c2 a, c2 b) { return {fmaf(a.x, b.x, -a.y * b.y), fmaf(a.x, b.y, a.y * b.x)}; }
+__device__ __forceinline__ c2 cconj(c2 a) { return {a.x, -a.y}; }
+// multiply by -i (forward) or +i (inverse)
+template <bool INV>
+__device__ __forceinline__ c2 mul_mi(c2 a) { return INV ? c2{-a.y, a.x} : c2{a.y, -a.x}; }
+// exp(sgn * 2 pi i * rev), rev in revolutions (v_cos/v_sin take revolutions)
+__device__ __forceinline__ c2 cis(float rev) { return {__builtin_amdgcn_cosf(rev), __builtin_amdgcn_sinf(rev)}; }
+
+template <bool INV>
+__device__ __forceinline__ void dft2(c2* v) {
+  const c2 a = v[0], b = v[1];
+  v[0] = cadd(a, b);
+  v[1] = csub(a, b);
+}
+
+template <bool INV>
+__device__ __forceinline__ void dft4(c2* v) {
+  const c2 s02 = cadd(v[0], v[2]), d02 = csub(v[0], v[2]);
+  const c2 s13 = cadd(v[1], v[3]), d13 = mul_mi<INV>(csub(v[1], v[3]));
+  v[0] = cadd(s02, s13);
+  v[2] = csub(s02, s13);
+  v[1] = cadd(d02, d13);
+  v[3] = csub(d02, d13);
+}
+
+template <bool INV>
+__device__ __forceinline__ void dft8(c2* v) {
+  c2 e[4] = {v[0], v[2], v[4], v[6]};
+  c2 o[4] = {v[1], v[3], v[5], v[7]};
+  dft4<INV>(e);
+  dft4<INV>(o);
+  constexpr float h = 0.70710678118654752f;
+  // o_k *= w8^k, w8 = exp(-+2 pi i / 8)
+  o[1] = INV ? c2{h * (o[1].x - o[1].y), h * (o[1].x + o[1].y)} : c2{h * (o[1].x + o[1].y), h * (o[1].y - o[1].x)};
+  o[2] = mul_mi<INV>(o[2]);
+  o[3] = INV ? c2{-h * (o[3].x + o[3].y), h * (o[3].x - o[3].y)} : c2{h * (o[3].y - o[3].x), -h * (o[3].x + o[3].y)};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    v[k] = cadd(e[k], o[k]);
+    v[k + 4] = csub(e[k], o[k]);
+  }
+}
+
+template <int R, bool INV>
+__device__ __forceinline__ void dftR(c2* v) {
+  if (R == 8) dft8<INV>(v);
+  else if (R == 4) dft4<INV>(v);
+  else dft2<INV>(v);
+}
+
+// Radix of pass p for an M-point transform: 8s first, then one 4 or 2.
+__host__ __device__ constexpr int pass_radix(int logm, int p) {
+  return (logm - 3 * p) >= 3 ? 8 : (logm - 3 * p == 2 ? 4 : 2);
+}
+__host__ __device__ constexpr int pass_count(int logm) { return (logm + 2) / 3; }
+__host__ __device__ constexpr int pass_span(int logm, int p) {
+  return p == 0 ? 1 : pass_span(logm, p - 1) * pass_radix(logm, p - 1);
+}
+
+// One Stockham pass over this thread's 8 values v (already read): twiddle,
+// R-point DFTs, and the output positions.  j = thread index within the
+// window; butterfly u of the thread is bj = j + u*M/8.
+template <int M, int R, int NS, bool INV>
+__device__ __forceinline__ void pass_compute(c2* v, int j, int* outpos) {
+  constexpr int BPT = 8 / R;
+#pragma unroll
+  for (int u = 0; u < BPT; ++u) {
+    const int bj = j + u * (M / 8);
+    const int k = bj % NS;
+    c2* w = v + u * R;
+    if (NS > 1) {
+      const float rev = (INV ? 1.0f : -1.0f) * (float)k / (float)(NS * R);
+      const c2 t1 = cis(rev);
+      c2 t = t1;
+#pragma unroll
+      for (int r = 1; r < R; ++r) {
+        w[r] = cmul(w[r], t);
+        if (r + 1 < R) t = cmul(t, t1);
       }
     }
-    __syncthreads();
+    dftR<R, INV>(w);
+    const int base = (bj / NS) * NS * R + k;
+#pragma unroll
+    for (int r = 0; r < R; ++r) outpos[u * R + r] = base + r * NS;
   }
 }
 
-__device__ __forceinline__ float block_sum(float v, float* red) {
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  if ((threadIdx.x & 63) == 0) red[w] = v;
-  __syncthreads();
-  float s = 0.f;
-  for (int i = 0; i < nw; ++i) s += red[i];
-  __syncthreads();
-  return s;
+// Input positions of pass with radix R: element u*R + r <- bj + r*M/R.
+template <int M, int R>
+__device__ __forceinline__ int in_pos(int j, int e) {
+  const int u = e / R, r = e % R;
+  return j + u * (M / 8) + r * (M / R);
 }
 
-// tables = hann[N] | twre[N-1] | twim[N-1]
-__global__ void k_spectral_loss(const float* __restrict__ x, const float* __restrict__ tgt,
-                                const float* __restrict__ tables, float* __restrict__ wloss, float* __restrict__ wgrad,
-                                int B, int T, int n, int logn, int hop, float gl, float gg) {
-  extern __shared__ float sm[];
-  float* re1 = sm;
-  float* im1 = re1 + n;
-  float* re2 = im1 + n;
-  float* im2 = re2 + n;
-  float* scale = im2 + n;          // n/2 + 1
-  float* red = scale + n / 2 + 1;  // 16
-  const float* hann = tables;
-  const float* twre = tables + n;
-  const float* twim = tables + 2 * n - 1;
-  const int w = blockIdx.x, b = blockIdx.y;
-  const int f = w * hop;  // the hop frame whose window ends here
-  const float* xs = x + (size_t)b * T;
-  const float* ts = tgt + (size_t)b * T;
+// Middle passes 1 .. npass-2 in LDS (in place; a barrier separates each
+// pass's reads from its writes).
+template <int LOGM, int P, bool INV>
+__device__ __forceinline__ void mid_passes(c2* buf, int j, c2* v) {
+  constexpr int M = 1 << LOGM;
+  if constexpr (P < pass_count(LOGM) - 1) {
+    constexpr int R = pass_radix(LOGM, P), NS = pass_span(LOGM, P);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = buf[in_pos<M, R>(j, e)];
+    lds_barrier();
+    int op[8];
+    pass_compute<M, R, NS, INV>(v, j, op);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) buf[op[e]] = v[e];
+    lds_barrier();
+    mid_passes<LOGM, P + 1, INV>(buf, j, v);
+  }
+}
 
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    const int tt = f - (n - 1) + i;
-    const bool in = tt >= 0 && tt < T;
-    const float hw = hann[i];
-    const int p = (int)(__brev((unsigned)i) >> (32 - logn));
-    re1[p] = (in ? xs[tt] : 0.f) * hw;
-    im1[p] = 0.f;
-    re2[p] = (in ? ts[tt] : 0.f) * hw;
-    im2[p] = 0.f;
+// Full M-point FFT: v holds the first pass's inputs (v[e] = input at
+// in_pos of pass 0); on return v holds the last pass's outputs at positions
+// op[e].  Uses buf (M complex, this window's slot) between passes.
+template <int LOGM, bool INV>
+__device__ __forceinline__ void fft(c2* buf, int j, c2* v, int* op) {
+  constexpr int M = 1 << LOGM;
+  constexpr int NP = pass_count(LOGM);
+  {
+    constexpr int R = pass_radix(LOGM, 0);
+    pass_compute<M, R, 1, INV>(v, j, op);
   }
-  __syncthreads();
-  fft_stages(re1, im1, re2, im2, twre, twim, n, logn, -1.f, true);
+  if constexpr (NP > 1) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) buf[op[e]] = v[e];
+    lds_barrier();
+    mid_passes<LOGM, 1, INV>(buf, j, v);
+    constexpr int RL = pass_radix(LOGM, NP - 1), NSL = pass_span(LOGM, NP - 1);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = buf[in_pos<M, RL>(j, e)];
+    lds_barrier();
+    pass_compute<M, RL, NSL, INV>(v, j, op);
+  }
+}
 
-  float lin = 0.f, lg = 0.f;
-  for (int k = threadIdx.x; k <= n / 2; k += blockDim.x) {
-    const float m1 = sqrtf(re1[k] * re1[k] + im1[k] * im1[k]);
-    const float m2 = sqrtf(re2[k] * re2[k] + im2[k] * im2[k]);
-    const float dlog = logf(m1 + kLogEps) - logf(m2 + kLogEps);
-    lin += fabsf(m1 - m2);
-    lg += fabsf(dlog);
-    const float dmag = gl * sgn(m1 - m2) + gg * sgn(dlog) / (m1 + kLogEps);
-    scale[k] = dmag / fmaxf(m1, kMagEps);
+__device__ __forceinline__ float sgn(float v) { return v > 0.f ? 1.f : (v < 0.f ? -1.f : 0.f); }
+// Hardware square root, natural log (via log2) and reciprocal, each within
+// ~1 ulp; the loss and its gradient are checked against the fp64 oracle.
+__device__ __forceinline__ float hw_sqrt(float v) { return __builtin_amdgcn_sqrtf(v); }
+__device__ __forceinline__ float hw_log(float v) { return __builtin_amdgcn_logf(v) * 0.69314718055994531f; }
+__device__ __forceinline__ float hw_rcp(float v) { return __builtin_amdgcn_rcpf(v); }
+
+struct MssLds {
+  float acc[kAcc];                 // dx of samples [a - kHalo, a + kTile)
+  c2 buf[2048];                    // FFT slots: (4096/N windows) x (N/2)
+  c2 aux[2048];                    // second signal's spectrum / gradient spectrum
+  float red[kThreads / 64][2];
+  float hann[2048];                // this size's window
+};
+
+// One FFT size: 4 groups of 4096/N windows, windows in a group 4 hops apart.
+template <int LOGN>
+__device__ __forceinline__ void mss_size(const MssArgs& a, MssLds& L, int si, int b, int tile) {
+  constexpr int N = 1 << LOGN, M = N / 2, LOGM = LOGN - 1, H = N / 4, P = M / 8, W = kThreads / P;
+  static_assert(W * M == 2048, "window slots must fill the FFT buffer");
+  const int tid = threadIdx.x;
+  const int slot = tid / P, j = tid % P;
+  c2* buf = L.buf + slot * M;
+  c2* spec = L.aux + slot * M;
+  const int a0 = tile * kTile;
+  const int nwin = (a.T + H - 1) / H;
+  const float* xs = a.x + (size_t)b * a.T;
+  const float* ts = a.tgt + (size_t)b * a.T;
+  for (int i = tid; i < N; i += kThreads) L.hann[i] = a.hann[si][i];
+  lds_barrier();
+  // window samples of group g for this thread: element e of the first pass
+  // needs samples s0 + 2n and s0 + 2n + 1, n = in_pos(j, e)
+  float pt[16], px[16];
+  auto fetch = [&](int g) {
+    const int w = a0 / H + g + 4 * slot;
+    const bool live = w < nwin && w * H < a0 + kTile;
+    const int s0 = w * H - N + 1;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int n = in_pos<M, pass_radix(LOGM, 0)>(j, e);
+      const int t0 = s0 + 2 * n, t1 = t0 + 1;
+      const bool i0 = live && t0 >= 0 && t0 < a.T, i1 = live && t1 >= 0 && t1 < a.T;
+      pt[2 * e] = i0 ? ts[t0] : 0.0f;
+      pt[2 * e + 1] = i1 ? ts[t1] : 0.0f;
+      px[2 * e] = i0 ? xs[t0] : 0.0f;
+      px[2 * e + 1] = i1 ? xs[t1] : 0.0f;
+    }
+  };
+  fetch(0);
+#pragma unroll 1
+  for (int g = 0; g < 4; ++g) {
+    const int w = a0 / H + g + 4 * slot;
+    const bool live = w < nwin && w * H < a0 + kTile;
+    const int f = w * H;
+    const int s0 = f - N + 1;  // first sample of the window
+    c2 v[8];
+    int op[8];
+    // ---- forward transform of the target, then of the prediction; the
+    //      target's half-size spectrum is kept in spec
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int n = in_pos<M, pass_radix(LOGM, 0)>(j, e);
+        const float h0 = L.hann[2 * n], h1 = L.hann[2 * n + 1];
+        v[e] = pass == 0 ? c2{pt[2 * e] * h0, pt[2 * e + 1] * h1} : c2{px[2 * e] * h0, px[2 * e + 1] * h1};
+      }
+      fft<LOGM, false>(buf, j, v, op);
+      c2* dst = pass == 0 ? spec : buf;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dst[op[e]] = v[e];
+      lds_barrier();
+    }
+    if (g + 1 < 4) fetch(g + 1);  // overlaps the bins and the inverse transform
+    // ---- bins: pair (k, M-k) for k = 0..M/2 gives every bin 0..N/2
+    float lin = 0.f, lg = 0.f;
+#pragma unroll 1
+    for (int k = j; k <= M / 2; k += P) {
+      const int km = (M - k) & (M - 1);
+      const c2 zx = buf[k], zxm = buf[km], zt = spec[k], ztm = spec[km];
+      // even/odd split: E = (Z_k + conj Z_{M-k})/2, O = (Z_k - conj Z_{M-k})/(2i)
+      const c2 ex = {0.5f * (zx.x + zxm.x), 0.5f * (zx.y - zxm.y)};
+      const c2 ox = {0.5f * (zx.y + zxm.y), 0.5f * (zxm.x - zx.x)};
+      const c2 et = {0.5f * (zt.x + ztm.x), 0.5f * (zt.y - ztm.y)};
+      const c2 ot = {0.5f * (zt.y + ztm.y), 0.5f * (ztm.x - zt.x)};
+      const c2 wk = cis(-(float)k / (float)N);  // W_N^k
+      const c2 wox = cmul(wk, ox), wot = cmul(wk, ot);
+      // X_k = E + W^k O ; X_{M-k} = conj(E - W^k O)   (k = 0: X_0 and X_M)
+      c2 X[2] = {cadd(ex, wox), cconj(csub(ex, wox))};
+      c2 Tt[2] = {cadd(et, wot), cconj(csub(et, wot))};
+      if (k == 0) {  // X_M = E_0 - O_0 (real parts; imaginary parts vanish)
+        X[1] = {ex.x - ox.x, 0.f};
+        Tt[1] = {et.x - ot.x, 0.f};
+      }
+      const int nb = (k == M / 2) ? 1 : 2;  // k = M/2 is its own mirror
+      c2 G[2] = {{0.f, 0.f}, {0.f, 0.f}};
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        if (q >= nb) break;
+        const float m1 = hw_sqrt(X[q].x * X[q].x + X[q].y * X[q].y);
+        const float m2 = hw_sqrt(Tt[q].x * Tt[q].x + Tt[q].y * Tt[q].y);
+        const float dlog = hw_log(m1 + kLogEps) - hw_log(m2 + kLogEps);
+        lin += fabsf(m1 - m2);
+        lg += fabsf(dlog);
+        const float dmag = a.gl * sgn(m1 - m2) + a.gg * sgn(dlog) * hw_rcp(m1 + kLogEps);
+        const float sc = dmag * hw_rcp(fmaxf(m1, kMagEps));
+        G[q] = {sc * X[q].x, sc * X[q].y};
+      }
+      // inverse pre-processing (Hermitian extension of the one-sided G):
+      //   E'_k = (G_k + conj G_{M-k})/2, O'_k = (G_k - conj G_{M-k})/2 * W_N^{-k},
+      //   z'_k = E'_k + i O'_k ; bin 0: E' = Re G_0 + Re G_M, O' = Re G_0 - Re G_M
+      if (k == 0) {
+        const float e0 = G[0].x + G[1].x, o0 = G[0].x - G[1].x;
+        spec[0] = {e0, o0};
+      } else {
+        const c2 gk = G[0], gm = nb == 2 ? G[1] : G[0];
+        const c2 winv = cconj(wk);
+        const c2 e1 = {0.5f * (gk.x + gm.x), 0.5f * (gk.y - gm.y)};
+        const c2 o1 = cmul(c2{0.5f * (gk.x - gm.x), 0.5f * (gk.y + gm.y)}, winv);
+        spec[k] = {e1.x - o1.y, e1.y + o1.x};
+        if (nb == 2) {
+          // index M-k: G_{M-k} = gm, mirror gk, twiddle W_N^{-(M-k)} = -W_N^{k}
+          const c2 e2 = {0.5f * (gm.x + gk.x), 0.5f * (gm.y - gk.y)};
+          const c2 o2 = cmul(c2{0.5f * (gm.x - gk.x), 0.5f * (gm.y + gk.y)}, c2{-wk.x, -wk.y});
+          spec[M - k] = {e2.x - o2.y, e2.y + o2.x};
+        }
+      }
+    }
+    // ---- per-window loss sums over the window's P threads
+#pragma unroll
+    for (int off = 1; off < (P < 64 ? P : 64); off <<= 1) {
+      lin += __shfl_xor(lin, off, 64);
+      lg += __shfl_xor(lg, off, 64);
+    }
+    if (P > 64) {
+      const int wv = tid >> 6;
+      if ((tid & 63) == 0) {
+        L.red[wv][0] = lin;
+        L.red[wv][1] = lg;
+      }
+    }
+    lds_barrier();
+    if (j == 0 && live) {
+      float sl = lin, sg = lg;
+      if (P > 64) {
+        const int w0 = (slot * P) >> 6;
+        sl = 0.f;
+        sg = 0.f;
+        for (int q = 0; q < P / 64; ++q) {
+          sl += L.red[w0 + q][0];
+          sg += L.red[w0 + q][1];
+        }
+      }
+      float* wl = a.wloss[si] + ((size_t)w * a.B + b) * 2;
+      wl[0] = sl;
+      wl[1] = sg;
+    }
+    // ---- real-output inverse transform and windowed overlap-add
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = spec[in_pos<M, pass_radix(LOGM, 0)>(j, e)];
+    fft<LOGM, true>(buf, j, v, op);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int n0 = 2 * op[e], n1 = n0 + 1;
+      const int t0 = s0 + n0, t1 = t0 + 1;
+      const float h0 = L.hann[n0], h1 = L.hann[n1];
+      if (live && t0 >= 0 && t0 < a.T) L.acc[t0 - (a0 - kHalo)] += v[e].x * h0;
+      if (live && t1 >= 0 && t1 < a.T) L.acc[t1 - (a0 - kHalo)] += v[e].y * h1;
+    }
+    lds_barrier();
   }
-  lin = block_sum(lin, red);
-  lg = block_sum(lg, red);
-  if (threadIdx.x == 0) {
-    wloss[((size_t)w * B + b) * 2 + 0] = lin;
-    wloss[((size_t)w * B + b) * 2 + 1] = lg;
-  }
-  // gradient spectrum, bins above N/2 zeroed, scattered bit-reversed
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    const int p = (int)(__brev((unsigned)i) >> (32 - logn));
-    const bool keep = i <= n / 2;
-    re2[p] = keep ? scale[i] * re1[i] : 0.f;
-    im2[p] = keep ? scale[i] * im1[i] : 0.f;
-  }
-  __syncthreads();
-  fft_stages(re2, im2, nullptr, nullptr, twre, twim, n, logn, 1.f, false);
-  float* out = wgrad + ((size_t)w * B + b) * n;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = re2[i] * hann[i];
+}
+
+// One launch per FFT size (each size gets its own register allocation); the
+// tile accumulator starts at zero for the first size and is carried in the
+// tile partials between launches, which run in the op's size order.
+template <int LOGN>
+__global__ __launch_bounds__(kThreads) void k_mss(MssArgs a, int si, int first) {
+  extern __shared__ float smem[];
+  MssLds& L = *reinterpret_cast<MssLds*>(smem);
+  const int tile = blockIdx.x, b = blockIdx.y;
+  float* part = a.part + ((size_t)b * a.ntiles + tile) * kAcc;
+  for (int i = threadIdx.x; i < kAcc; i += kThreads) L.acc[i] = first ? 0.f : part[i];
+  lds_barrier();
+  mss_size<LOGN>(a, L, si, b, tile);
+  for (int i = threadIdx.x; i < kAcc; i += kThreads) part[i] = L.acc[i];
 }
 
 int launch_spectral_loss(const Launch& L, const dgen_hip_op& op) {
-  const int64_t x = op.arg[0], tgt = op.arg[1], wl = op.arg[2], wg = op.arg[3], B = op.arg[4], T = op.arg[5],
-                n = op.arg[6], hop = op.arg[7], tab = op.arg[8];
-  DGEN_REQUIRE(B > 0 && B <= 65535 && T > 0 && n >= 2 && n <= 8192 && (n & (n - 1)) == 0 && hop >= 1,
-               "spectral_loss: B %lld T %lld N %lld hop %lld", (long long)B, (long long)T, (long long)n,
-               (long long)hop);
-  const int64_t nwin = (T + hop - 1) / hop;
+  // arg: [0]=x ([B][T]) [1]=target ([B][T]) [2]=tile partials ([B][ntiles][6143]) [3]=B [4]=T [5]=n_sizes
+  //      [6..13]=N_s [14..21]=per-window loss cells ([nwin_s][B][2]) [22..29]=Hann tables ([N_s])
+  // farg: [0]=lin upstream grad per window [1]=log upstream grad per window
+  const int64_t x = op.arg[0], tgt = op.arg[1], part = op.arg[2], B = op.arg[3], T = op.arg[4], ns = op.arg[5];
+  DGEN_REQUIRE(B > 0 && B <= 65535 && T > 0 && T <= (1 << 26) && ns >= 1 && ns <= kMaxSizes,
+               "spectral_loss: B %lld T %lld sizes %lld", (long long)B, (long long)T, (long long)ns);
+  const int64_t ntiles = (T + kTile - 1) / kTile;
   DGEN_CHECK_CELL(L, x, B * T, "spectral_loss.x");
   DGEN_CHECK_CELL(L, tgt, B * T, "spectral_loss.target");
-  DGEN_CHECK_CELL(L, wl, nwin * B * 2, "spectral_loss.window_loss");
-  DGEN_CHECK_CELL(L, wg, nwin * B * n, "spectral_loss.window_grad");
-  DGEN_CHECK_CELL(L, tab, 3 * n - 2, "spectral_loss.tables");
+  DGEN_CHECK_CELL(L, part, B * ntiles * kAcc, "spectral_loss.tile_partials");
+  MssArgs a{};
+  for (int s = 0; s < ns; ++s) {
+    const int64_t n = op.arg[6 + s];
+    int lg = 0;
+    while ((1ll << lg) < n) ++lg;
+    DGEN_REQUIRE((1ll << lg) == n && lg >= 6 && lg <= 11, "spectral_loss: size %lld not a power of two in [64, 2048]",
+                 (long long)n);
+    const int64_t nwin = (T + n / 4 - 1) / (n / 4);
+    DGEN_CHECK_CELL(L, op.arg[14 + s], nwin * B * 2, "spectral_loss.window_loss");
+    DGEN_CHECK_CELL(L, op.arg[22 + s], n, "spectral_loss.hann");
+    a.logn[s] = lg;
+    if (!L.dry) {
+      a.wloss[s] = cell(L, op.arg[14 + s]);
+      a.hann[s] = cell(L, op.arg[22 + s]);
+    }
+  }
   if (L.dry) return 0;
-  int logn = 0;
-  while ((1ll << logn) < n) ++logn;
-  const int threads = (int)std::min<int64_t>(256, std::max<int64_t>(64, n / 2));
-  const size_t lds = (size_t)(4 * n + n / 2 + 1 + 16) * sizeof(float);
-  hipLaunchKernelGGL(k_spectral_loss, dim3((unsigned)nwin, (unsigned)B), dim3(threads), lds, L.stream, cell(L, x),
-                     cell(L, tgt), cell(L, tab), cell(L, wl), cell(L, wg), (int)B, (int)T, (int)n, logn, (int)hop,
-                     op.farg[0], op.farg[1]);
-  DGEN_LAUNCH_CHECK("k_spectral_loss");
+  a.x = cell(L, x);
+  a.tgt = cell(L, tgt);
+  a.part = cell(L, part);
+  a.nsizes = (int)ns;
+  a.B = (int)B;
+  a.T = (int)T;
+  a.ntiles = (int)ntiles;
+  a.gl = op.farg[0];
+  a.gg = op.farg[1];
+  const dim3 grid((unsigned)ntiles, (unsigned)B);
+  for (int s = 0; s < ns; ++s) {
+    const int first = s == 0;
+    switch (a.logn[s]) {
+      case 6: hipLaunchKernelGGL(k_mss<6>, grid, dim3(kThreads), sizeof(MssLds), L.stream, a, s, first); break;
+      case 7: hipLaunchKernelGGL(k_mss<7>, grid, dim3(kThreads), sizeof(MssLds), L.stream, a, s, first); break;
+      case 8: hipLaunchKernelGGL(k_mss<8>, grid, dim3(kThreads), sizeof(MssLds), L.stream, a, s, first); break;
+      case 9: hipLaunchKernelGGL(k_mss<9>, grid, dim3(kThreads), sizeof(MssLds), L.stream, a, s, first); break;
+      case 10: hipLaunchKernelGGL(k_mss<10>, grid, dim3(kThreads), sizeof(MssLds), L.stream, a, s, first); break;
+      default: hipLaunchKernelGGL(k_mss<11>, grid, dim3(kThreads), sizeof(MssLds), L.stream, a, s, first); break;
+    }
+    DGEN_LAUNCH_CHECK("k_mss");
+  }
   return 0;
 }
 
-struct GatherArgs {
+// dx[b][t] = the owning tile's accumulator + the next tile's halo part, and
+// the per-frame loss signal (Emit+SpectralLoss.swift:914-938 batch mean,
+// Functions.swift:945-955 normalize by maxFrameCount).
+struct CombineArgs {
   int nsizes;
-  int n[kMaxSizes];
   int hop[kMaxSizes];
-  const float* wgrad[kMaxSizes];
   const float* wloss[kMaxSizes];
 };
 
-__global__ void k_spectral_gather(GatherArgs g, float* __restrict__ dx, float* __restrict__ lossf, int B, int T,
-                                  float wl, float wg, float max_frames) {
+__global__ void k_mss_combine(CombineArgs g, const float* __restrict__ part, float* __restrict__ dx,
+                              float* __restrict__ lossf, int B, int T, int ntiles, float wl, float wg,
+                              float max_frames) {
   const int t = blockIdx.x * blockDim.x + threadIdx.x;
   const int b = blockIdx.y;
   if (t >= T) return;
-  float acc = 0.f;
-  for (int s = 0; s < g.nsizes; ++s) {
-    const int n = g.n[s], hop = g.hop[s];
-    const int nwin = (T + hop - 1) / hop;
-    const int wlo = (t + hop - 1) / hop;
-    const int whi = min(nwin - 1, (t + n - 1) / hop);
-    for (int w = wlo; w <= whi; ++w) {
-      const int off = t - (w * hop - n + 1);
-      acc += g.wgrad[s][((size_t)w * B + b) * n + off];
-    }
-  }
-  dx[(size_t)b * T + t] = acc;
+  const int tile = t / kTile, a0 = tile * kTile;
+  const float* p = part + ((size_t)b * ntiles + tile) * kAcc;
+  float v = p[t - a0 + kHalo];
+  const int a1 = a0 + kTile;
+  if (tile + 1 < ntiles && t >= a1 - kHalo) v += p[kAcc + (t - a1 + kHalo)];
+  dx[(size_t)b * T + t] = v;
   if (b == 0 && lossf) {
     float lf = 0.f;
     for (int s = 0; s < g.nsizes; ++s) {
@@ -196,34 +476,35 @@ __global__ void k_spectral_gather(GatherArgs g, float* __restrict__ dx, float* _
 }
 
 int launch_spectral_gather(const Launch& L, const dgen_hip_op& op) {
+  // arg: [0]=dx ([B][T]) [1]=loss frames ([T]) or -1 [2]=B [3]=T [4]=n_sizes [5..12]=N_s
+  //      [13]=tile partials [21..28]=per-window loss cells
+  // farg: [0]=lin weight per size [1]=log weight per size [2]=maxFrameCount
   const int64_t dx = op.arg[0], lossf = op.arg[1], B = op.arg[2], T = op.arg[3], ns = op.arg[4];
-  const int64_t hop_div = op.arg[29];
-  DGEN_REQUIRE(B > 0 && B <= 65535 && T > 0 && ns >= 1 && ns <= kMaxSizes && hop_div >= 1,
-               "spectral_gather: B %lld T %lld sizes %lld hop_div %lld", (long long)B, (long long)T, (long long)ns,
-               (long long)hop_div);
+  const int64_t part = op.arg[13];
+  DGEN_REQUIRE(B > 0 && B <= 65535 && T > 0 && T <= (1 << 26) && ns >= 1 && ns <= kMaxSizes,
+               "spectral_gather: B %lld T %lld sizes %lld", (long long)B, (long long)T, (long long)ns);
+  const int64_t ntiles = (T + kTile - 1) / kTile;
   DGEN_CHECK_CELL(L, dx, B * T, "spectral_gather.dx");
   if (lossf >= 0) DGEN_CHECK_CELL(L, lossf, T, "spectral_gather.loss_frames");
-  GatherArgs g{};
+  DGEN_CHECK_CELL(L, part, B * ntiles * kAcc, "spectral_gather.tile_partials");
+  CombineArgs g{};
   g.nsizes = (int)ns;
   for (int s = 0; s < ns; ++s) {
     const int64_t n = op.arg[5 + s];
-    DGEN_REQUIRE(n >= 2 && (n & (n - 1)) == 0 && n <= 8192, "spectral_gather: size %lld", (long long)n);
-    const int64_t hop = std::max<int64_t>(1, n / hop_div);
+    DGEN_REQUIRE(n >= 64 && n <= 2048 && (n & (n - 1)) == 0, "spectral_gather: size %lld", (long long)n);
+    const int64_t hop = n / 4;
     const int64_t nwin = (T + hop - 1) / hop;
-    DGEN_CHECK_CELL(L, op.arg[13 + s], nwin * B * n, "spectral_gather.window_grad");
     DGEN_CHECK_CELL(L, op.arg[21 + s], nwin * B * 2, "spectral_gather.window_loss");
     if (!L.dry) {
-      g.n[s] = (int)n;
       g.hop[s] = (int)hop;
-      g.wgrad[s] = cell(L, op.arg[13 + s]);
       g.wloss[s] = cell(L, op.arg[21 + s]);
     }
   }
   if (L.dry) return 0;
-  hipLaunchKernelGGL(k_spectral_gather, dim3((unsigned)((T + 255) / 256), (unsigned)B), dim3(256), 0, L.stream, g,
-                     cell(L, dx), lossf >= 0 ? cell(L, lossf) : nullptr, (int)B, (int)T, op.farg[0], op.farg[1],
-                     op.farg[2]);
-  DGEN_LAUNCH_CHECK("k_spectral_gather");
+  hipLaunchKernelGGL(k_mss_combine, dim3((unsigned)((T + 255) / 256), (unsigned)B), dim3(256), 0, L.stream, g,
+                     cell(L, part), cell(L, dx), lossf >= 0 ? cell(L, lossf) : nullptr, (int)B, (int)T, (int)ntiles,
+                     op.farg[0], op.farg[1], op.farg[2]);
+  DGEN_LAUNCH_CHECK("k_mss_combine");
   return 0;
 }
 

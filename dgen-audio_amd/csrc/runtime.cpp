@@ -61,6 +61,7 @@ static Launcher launcher_for(uint32_t k) {
     case DGEN_HIP_K_NOISE_TABLE: return launch_noise_table;
     case DGEN_HIP_K_ROW_SCHEDULE: return launch_row_schedule;
     case DGEN_HIP_K_FFT_TABLES: return launch_fft_tables;
+    case DGEN_HIP_K_LERP_FRAMES: return launch_lerp_frames;
     default: return nullptr;
   }
 }

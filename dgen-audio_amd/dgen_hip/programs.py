@@ -18,6 +18,7 @@ SLOTS = 4         # control rows a segment may touch
 ROW_ENTRIES = 8   # (segment, slot) entries per control row
 LDC = 128         # padded control-row stride (K + 2 + NF <= 128)
 SPLITK_ROWS = 1024  # rows per split of the weight-gradient GEMMs
+MSS_TILE = 4096     # output samples per spectral-loss workgroup
 
 
 def _f32(x) -> float:
@@ -40,12 +41,17 @@ def oscbank_program(cfg: OscBankConfig) -> Program:
 
 
 # ------------------------------------------------------------------ config 3
-def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = True) -> Program:
+def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = True,
+                     side_stream: bool = True) -> Program:
     """Batched harmonic + noise synth with MLP decoder and MSS loss.
 
     ``train=False`` builds the forward render only (controls -> audio), used
     to render targets.  With ``train=True`` the schedule is forward, loss,
-    backward to every parameter and (``optimizer``) one Adam step."""
+    backward to every parameter and (``optimizer``) one Adam step.  With
+    ``side_stream`` the phase-carry chain (which depends only on f0) runs on a
+    second stream, overlapping the control-network forward."""
+    SIDE = R.OP_SIDE if side_stream else 0
+    JOIN = R.OP_JOIN if side_stream else 0
     B, T, F, K, NF, NC, M = cfg.B, cfg.T, cfg.F, cfg.K, cfg.NF, cfg.NC, cfg.M
     Hd, din, Lyr = cfg.hidden, cfg.din, cfg.layers
     if NC > LDC:
@@ -92,6 +98,8 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     Z = p.alloc("Z", M * LDC)
     ctrl = p.alloc("ctrl", M * LDC)
     ck = p.alloc("checkpoints", nseg * B * K)
+    f0f = p.alloc("f0_frames", B * T)
+    uvf = p.alloc("uv_frames", B * T)
     y = p.alloc("y", B * T)
 
     # ---- forward
@@ -99,10 +107,14 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     ctrl_b = M * NC * f4                      # one pass over the control rows
     lerp_b = T * 8 * f4
     ck_b = nseg * B * K * f4
-    data_b = 2 * F * B * f4 + T * f4          # f0, uv, noise
-    p.add(R.K_PHASOR_CARRY, [lerp, f0, ck, B, K, F, T, SEG], [cfg.sr], flags=R.OP_SIDE, label="phasor_carry",
-          dispatch=f"fixedWithFrameLoop({B * K})", bytes=lerp_b + F * B * f4 + ck_b, flops=5.0 * B * K * T,
-          bound="valu")
+    data_b = 2 * B * T * f4 + T * f4 + nseg * SLOTS * f4  # f0 and uv frames, noise, segment rows
+    frames_b = lerp_b + F * B * f4 + B * T * f4
+    p.add(R.K_LERP_FRAMES, [f0, lerp, f0f, B, F, T], flags=SIDE, label="f0_frames",
+          dispatch=f"perFrameScaled({B})", bytes=frames_b, flops=3.0 * B * T)
+    p.add(R.K_PHASOR_CARRY, [f0f, ck, B, K, T], [cfg.sr], flags=SIDE, label="phasor_carry",
+          dispatch=f"fixedWithFrameLoop({B * K})", bytes=B * T * f4 + ck_b, flops=6.0 * B * K * T, bound="valu")
+    p.add(R.K_LERP_FRAMES, [uv, lerp, uvf, B, F, T], label="uv_frames", dispatch=f"perFrameScaled({B})",
+          bytes=frames_b, flops=3.0 * B * T)
     W1, b1 = woff[0]
     p.add(R.K_DENSE_SMALL, [X, W1, b1, Hs[0], M, din, Hd], label="mlp_in", dispatch="gemmSmall",
           bytes=(M * din + din * Hd + Hd + M * Hd) * f4, flops=2.0 * M * din * Hd)
@@ -115,13 +127,14 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
           dispatch="gemm", bytes=(M * Hd + Hd * NC + NC + M * NC) * f4, flops=2.0 * M * Hd * NC, bound="mfma")
     p.add(R.K_HEADS_FWD, [Z, ctrl, M, K, NF, LDC], label="heads", dispatch=f"perFrameScaled({M})",
           bytes=2 * M * NC * f4, flops=M * (K * 12.0 + NF * 8.0))
-    synth_args = [ctrl, f0, uv, lerp, ck, y, B, K, NF, F, T, SEG, -1, noise, LDC]
+    aux = p.alloc("synth_tape", 3 * B * T) if train else -1
+    synth_args = [ctrl, f0f, uvf, lerp, ck, y, B, K, NF, F, T, SEG, aux, noise, LDC, segrows]
     hs, ns = cfg.hscale, cfg.nscale
     # per (b, t): K harmonics x (phase 4 + sin 20 + lerp 3 + mask/div 3 + sum 1 + normaliser 4), NF taps x 5
     synth_flops = float(B) * T * (35.0 * K + 5.0 * NF)
-    p.add(R.K_SYNTH_FWD, synth_args, [cfg.sr, hs, ns], flags=R.OP_JOIN, label="synth_fwd",
-          dispatch=f"perFrameScaled({B})", bytes=ctrl_b + lerp_b + ck_b + data_b + B * T * f4, flops=synth_flops,
-          bound="valu")
+    p.add(R.K_SYNTH_FWD, synth_args, [cfg.sr, hs, ns], flags=JOIN, label="synth_fwd",
+          dispatch=f"perFrameScaled({B})", bytes=ctrl_b + lerp_b + ck_b + data_b + B * T * f4 * (4 if train else 1),
+          flops=synth_flops, bound="valu")
     p.output_cell = "y"
     if not train:
         return p
@@ -139,37 +152,39 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     maxf = np.float32(T)
     gl = wl / maxf / np.float32(B)
     gg = wg / maxf / np.float32(B)
-    wgrad_cells, wloss_cells = [], []
-    gather_b = 0.0
+    if any(N not in (64, 128, 256, 512, 1024, 2048) for N in sizes) or cfg.hop_div != 4:
+        raise ValueError("spectral loss sizes must be powers of two in [64, 2048] with hop N/4")
+    ntiles = (T + MSS_TILE - 1) // MSS_TILE
+    mss_part = p.alloc("mss_tiles", B * ntiles * (MSS_TILE + 2047))
+    wloss_cells, hann_cells, mss_flops = [], [], 0.0
     for N in sizes:
-        hop = max(1, N // cfg.hop_div)
+        hop = N // 4
         nwin = (T + hop - 1) // hop
+        wloss_cells.append(p.alloc(f"win_loss_{N}", nwin * B * 2))
         tab = p.alloc(f"fft_tables_{N}", 3 * N - 2)
         p.add(R.K_FFT_TABLES, [tab, N], flags=R.OP_STATIC, label=f"fft_tables_{N}", dispatch="static")
-        wlc = p.alloc(f"win_loss_{N}", nwin * B * 2)
-        wgc = p.alloc(f"win_grad_{N}", nwin * B * N)
-        lg = int(np.log2(N))
-        # two forward transforms + one inverse (5 N log2 N each), window and bin math
-        p.add(R.K_SPECTRAL_LOSS, [y, target, wlc, wgc, B, T, N, hop, tab], [gl, gg], label=f"spectral_{N}",
-              dispatch=f"perFrameScaledThreadgroup1({B}) hop {hop}",
-              bytes=(2 * B * T + nwin * B * (N + 2)) * f4, flops=nwin * B * (15.0 * N * lg + 40.0 * N),
-              bound="valu")
-        gather_b += nwin * B * (N + 2) * f4
-        wgrad_cells.append(wgc)
-        wloss_cells.append(wlc)
-    garg = [dy, lossf, B, T, len(sizes)] + (sizes + [0] * 8)[:8] + (wgrad_cells + [0] * 8)[:8] \
-        + (wloss_cells + [0] * 8)[:8] + [cfg.hop_div]
-    p.add(R.K_SPECTRAL_GATHER, garg, [wl, wg, maxf], label="spectral_gather", dispatch=f"perFrameScaled({B})",
-          bytes=gather_b + (B * T + T) * f4, flops=gather_b / f4)
+        hann_cells.append(tab)
+        # two real forward transforms + one real-output inverse (2.5 N log2 N each) + bin math
+        mss_flops += nwin * B * (7.5 * N * np.log2(N) + 30.0 * N)
+    larg = [y, target, mss_part, B, T, len(sizes)] + (sizes + [0] * 8)[:8] + (wloss_cells + [0] * 8)[:8] \
+        + (hann_cells + [0] * 8)[:8]
+    p.add(R.K_SPECTRAL_LOSS, larg, [gl, gg], label="spectral_mss",
+          dispatch=f"perFrameScaledThreadgroup1({B}) x {len(sizes)} sizes",
+          bytes=(2 * B * T + B * ntiles * (MSS_TILE + 2047) + sum((T + N // 4 - 1) // (N // 4) for N in sizes) * B * 2)
+          * f4, flops=mss_flops, bound="valu")
+    garg = [dy, lossf, B, T, len(sizes)] + (sizes + [0] * 8)[:8] + [mss_part] + [0] * 7 + (wloss_cells + [0] * 8)[:8]
+    p.add(R.K_SPECTRAL_GATHER, garg, [wl, wg, maxf], label="spectral_combine", dispatch=f"perFrameScaled({B})",
+          bytes=(B * ntiles * (MSS_TILE + 2047) + B * T + T) * f4, flops=float(B * T))
 
     part = p.alloc("synth_partials", B * nseg * SLOTS * LDC)
     dctrl = p.alloc("dctrl", M * LDC)
     bargs = list(synth_args)
     bargs[5] = dy
     bargs[12] = part
+    bargs.append(aux)
     part_b = B * nseg * SLOTS * NC * f4
     p.add(R.K_SYNTH_BWD, bargs, [cfg.sr, hs, ns], label="synth_bwd", dispatch=f"selfManagedThreads({B})",
-          bytes=ctrl_b + lerp_b + ck_b + data_b + B * T * f4 + part_b,
+          bytes=ctrl_b + lerp_b + ck_b + data_b + 4 * B * T * f4 + part_b,
           flops=synth_flops + float(B) * T * (6.0 * K + 4.0 * NC), bound="valu")
     p.add(R.K_SYNTH_BWD_REDUCE, [part, rowlist, dctrl, B, NC, F, T, SEG, LDC], label="synth_bwd_reduce",
           dispatch=f"perFrameScaled({M})", bytes=part_b + F * ROW_ENTRIES * f4 + M * NC * f4, flops=part_b / f4)
@@ -180,8 +195,8 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     G = p.alloc("grads", npar)
     split = max(1, (M + SPLITK_ROWS - 1) // SPLITK_ROWS)
     ws_gemm = p.alloc("splitk_ws", split * Hd * max(Hd, NC))
-    chunks = min(256, max(1, M // 16))
-    ws_col = p.alloc("colsum_ws", chunks * max(Hd, NC))
+    chunks = min(256, max(1, M // 32))
+    ws_col = p.alloc("colsum_ws", chunks * (din + 1) * max(Hd, NC))
     gW = [(G + (w - P), G + (b - P)) for (w, b) in woff]
     gWh, gbh = G + (Wh - P), G + (bh - P)
     # heads: dWh = H_L^T dZ ; dbh = colsum(dZ) ; dH_L = (dZ Wh^T) * (1 - H_L^2)
@@ -204,10 +219,9 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
         p.add(R.K_GEMM, [dH[l], W, dH[l - 1], M, Hd, Hd, Hd, Hd, Hd, 0, 1, R.EPI_TANH_GRAD, -1, Hs[l - 1], Hd, 1, 0],
               label=f"dX_l{l + 1}", dispatch="gemm", bytes=(3 * M * Hd + Hd * Hd) * f4, **gemm_hh)
     gw1, gb1 = gW[0]
-    p.add(R.K_DENSE_SMALL_WGRAD, [X, dH[0], gw1, M, din, Hd, ws_col], label="dW_l1",
-          dispatch="chunkPartialsReduceToCell", bytes=(M * din + M * Hd + din * Hd) * f4, flops=2.0 * M * din * Hd)
-    p.add(R.K_COLSUM, [dH[0], gb1, M, Hd, Hd, ws_col], label="db_l1", dispatch="chunkPartialsReduceToCell",
-          bytes=(M * Hd + Hd) * f4, flops=float(M * Hd))
+    p.add(R.K_DENSE_SMALL_WGRAD, [X, dH[0], gw1, M, din, Hd, ws_col, gb1], label="dWb_l1",
+          dispatch="chunkPartialsReduceToCell", bytes=(M * din + M * Hd + (din + 1) * Hd) * f4,
+          flops=2.0 * M * (din + 1) * Hd)
     if optimizer:
         m = p.alloc("adam_m", npar)
         v = p.alloc("adam_v", npar)
@@ -231,7 +245,8 @@ class HarmonicSession:
     HarmonicConfig.  Inputs are staged once; every ``step()`` is one
     forward+backward(+Adam) pass with all data resident in HBM."""
 
-    def __init__(self, cfg: HarmonicConfig, device: int = 0, optimizer: bool = True, target=None):
+    def __init__(self, cfg: HarmonicConfig, device: int = 0, optimizer: bool = True, target=None,
+                 side_stream: bool = True):
         self.cfg = cfg
         f0, uv, X = cfg.data()
         self.f0, self.uv, self.X = f0, uv, X
@@ -239,7 +254,7 @@ class HarmonicSession:
         if target is None:
             target = self.render(cfg.weights(seed=cfg.target_seed), device)
         self.target = np.ascontiguousarray(target, np.float32).reshape(cfg.B, cfg.T)
-        self.program = harmonic_program(cfg, train=True, optimizer=optimizer)
+        self.program = harmonic_program(cfg, train=True, optimizer=optimizer, side_stream=side_stream)
         self.rt = R.HIPLazyRuntime(self.program, device)
         check_row_schedule(self.rt)
         self.rt.write("X", X)

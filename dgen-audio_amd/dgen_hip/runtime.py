@@ -41,6 +41,7 @@ K_OSC_BANK = 15
 K_NOISE_TABLE = 16
 K_ROW_SCHEDULE = 17
 K_FFT_TABLES = 18
+K_LERP_FRAMES = 19
 
 KERNEL_NAMES = {v: k[2:].lower() for k, v in globals().items() if k.startswith("K_")}
 

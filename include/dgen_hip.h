@@ -73,39 +73,46 @@ enum dgen_hip_kernel {
   DGEN_HIP_K_HEADS_FWD = 4,
 
   /* Sequential tensor-phasor carry pass (Emit+State.swift:322-369) for
-   * lanes (b,k), freq = (k+1) * lerp(f0 rows at the playhead); stores the
-   * phase at the start of every segment.
-   * arg: [0]=playhead cell [1]=f0 cell ([F][B]) [2]=checkpoints cell
-   *      ([nseg][B][K]) [3]=B [4]=K [5]=F [6]=T [7]=segment length
+   * lanes (b,k), freq = (k+1) * f0 frames[b][t]; stores the phase at the
+   * start of every 64-frame segment.
+   * arg: [0]=f0 frames cell ([B][T], from DGEN_HIP_K_LERP_FRAMES)
+   *      [1]=checkpoints cell ([nseg][B][K]) [2]=B [3]=K [4]=T
    * farg: [0]=sample rate */
   DGEN_HIP_K_PHASOR_CARRY = 5,
 
   /* Batched harmonic + FIR-noise synth forward
    * (Examples/HarmonicE2E/Synth.swift:47-102).
-   * arg: [0]=ctrl [1]=f0 [2]=uv [3]=playhead [4]=checkpoints [5]=y ([B][T])
-   *      [6]=B [7]=K [8]=NF [9]=F [10]=T [11]=segment length
+   * arg: [0]=ctrl ([B*F][ldc]) [1]=f0 frames ([B][T]) [2]=uv frames ([B][T])
+   *      [3]=lerp table ([T][8]) [4]=checkpoints [5]=y ([B][T]) [6]=B [7]=K
+   *      [8]=NF [9]=F [10]=T [11]=segment length (64) [12]=per-frame tape
+   *      ([3][B][T]: harmonic sum, normaliser, FIR output) or -1
+   *      [13]=noise ([T]) [14]=ldc [15]=segment rows ([nseg][4])
    * farg: [0]=sample rate [1]=harmonic scale [2]=noise scale */
   DGEN_HIP_K_SYNTH_FWD = 6,
 
-  /* Multi-scale batched spectral loss, forward + gradient spectrum + IFFT for
-   * one FFT size (Emit+SpectralLoss.swift:719-1160).
-   * arg: [0]=x ([B][T]) [1]=target ([B][T]) [2]=per-window loss cell
-   *      ([nwin][B][2]: lin, log) [3]=per-window time-gradient cell
-   *      ([nwin][B][N]) [4]=B [5]=T [6]=N [7]=hop
+  /* Multi-scale batched spectral loss and its gradient, every FFT size in
+   * one launch (Emit+SpectralLoss.swift:719-1235).  Sizes are powers of two
+   * in [64, 2048] with hop N/4.  Each workgroup owns a 4096-sample tile of
+   * one lane; the tile's dx (samples a-2047 .. a+4095) goes to the tile
+   * partials, the per-window (lin, log) sums to the window-loss cells.
+   * arg: [0]=x ([B][T]) [1]=target ([B][T]) [2]=tile partials
+   *      ([B][ceil(T/4096)][6143]) [3]=B [4]=T [5]=n_sizes [6..13]=N_s
+   *      [14..21]=window-loss cells ([ceil(T/hop)][B][2])
+   *      [22..29]=Hann tables (DGEN_HIP_K_FFT_TABLES output, first N floats)
    * farg: [0]=lin upstream grad per window (w_lin/nsizes/maxFrames/B)
    *       [1]=log upstream grad per window */
   DGEN_HIP_K_SPECTRAL_LOSS = 7,
 
-  /* Gather of hop-window time gradients into d x (Emit+SpectralLoss.swift:
-   * 1163-1235) summed over up to 8 FFT sizes, plus the per-frame loss signal.
-   * arg: [0]=dx ([B][T]) [1]=loss frames ([T]) [2]=B [3]=T [4]=n_sizes
-   *      [5..12]=N_s [13..20]=window-gradient cells [21..28] per-window loss
-   *      cells [29]=hop divisor
-   * farg: [0]=lin weight per size * 1/(B*maxFrames) [1]=log weight likewise */
+  /* dx from the spectral-loss tile partials (owning tile + next tile's
+   * halo) and the per-frame loss signal (batch mean, / maxFrameCount).
+   * arg: [0]=dx ([B][T]) [1]=loss frames ([T]) or -1 [2]=B [3]=T
+   *      [4]=n_sizes [5..12]=N_s [13]=tile partials [21..28]=window-loss cells
+   * farg: [0]=lin weight per size [1]=log weight per size [2]=maxFrameCount */
   DGEN_HIP_K_SPECTRAL_GATHER = 8,
 
   /* Synth backward: d ctrl row partials per segment.
-   * arg: as DGEN_HIP_K_SYNTH_FWD with [5]=dy ([B][T]) [12]=partials cell */
+   * arg: as DGEN_HIP_K_SYNTH_FWD with [5]=dy ([B][T]) [12]=partials cell
+   *      ([B][nseg][4][ldc]) [16]=the forward's per-frame tape */
   DGEN_HIP_K_SYNTH_BWD = 9,
 
   /* Deterministic reduction of synth-backward segment partials into d ctrl.
@@ -116,13 +123,16 @@ enum dgen_hip_kernel {
    * [3]=rows [4]=K [5]=NF */
   DGEN_HIP_K_HEADS_BWD = 11,
 
-  /* Column sums (bias gradients): out[n] = sum_m A[m][n].
-   * arg: [0]=A [1]=out [2]=M [3]=N [4]=lda [5]=workspace cell */
+  /* Column sums (bias gradients): out[n] = sum_m A[m][n], deterministic
+   * two-stage order.  arg: [0]=A [1]=out [2]=M [3]=N [4]=lda [5]=workspace
+   * cell (min(256, M/32) * N floats) */
   DGEN_HIP_K_COLSUM = 12,
 
-  /* First-layer weight gradient for a small fan-in: dW[i][j] = sum_m X[m][i]
-   * dZ[m][j]. arg: [0]=X [1]=dZ [2]=dW [3]=rows [4]=fan_in [5]=width
-   * [6]=workspace cell */
+  /* First-layer weight gradient for a small fan-in (<= 4): dW[i][j] =
+   * sum_m X[m][i] dZ[m][j], and with [7] >= 0 the bias gradient
+   * db[j] = sum_m dZ[m][j] from the same pass.  arg: [0]=X [1]=dZ [2]=dW
+   * [3]=rows [4]=fan_in [5]=width [6]=workspace cell
+   * (min(256, rows/32) * (fan_in+1) * width floats) [7]=db cell or -1 */
   DGEN_HIP_K_DENSE_SMALL_WGRAD = 13,
 
   /* Adam.step over a flat parameter blob (Optimizers.swift:164-204).
@@ -147,9 +157,15 @@ enum dgen_hip_kernel {
    * and every row has <= 8 (segment, slot) entries. */
   DGEN_HIP_K_ROW_SCHEDULE = 17,
 
-  /* Spectral-loss tables for one FFT size (HigherOps.swift:71-99):
-   * hann[N] | twre[N-1] | twim[N-1].  arg: [0]=out cell [1]=N */
+  /* Radix-2 spectral-loss tables for one FFT size (HigherOps.swift:71-99):
+   * symmetric hann[N] | twre[N-1] | twim[N-1].  arg: [0]=out cell [1]=N */
   DGEN_HIP_K_FFT_TABLES = 18,
+
+  /* Frame-rate sampleRow read of a [F][B] data table through a lerp table
+   * (Emit+RowSelection.swift:164-197): out[b][t] = (1-frac) src[lo][b] +
+   * frac src[hi][b].  arg: [0]=src [1]=lerp ([T][8]) [2]=out ([B][T]) [3]=B
+   * [4]=F [5]=T */
+  DGEN_HIP_K_LERP_FRAMES = 19,
 };
 
 /* GEMM epilogues */

@@ -49,7 +49,11 @@ def test_synth_forward_matches_oracle(small):
     ctrl = out["ctrl"].reshape(cfg.M, 128)[:, :cfg.NC]
     y = out["y"].reshape(cfg.B, cfg.T)
     ref = O.synth_fwd(ctrl, f0, uv, cfg.B, cfg.F, cfg.T, cfg.K, cfg.NF, cfg.sr)
-    assert np.abs(y - ref).max() < 2e-6
+    # the kernel evaluates sin(2 pi p) to ~2e-7 abs where the oracle takes
+    # sinf(fl(p * 2pi_f32)); the end-to-end bar (1e-4) is tested below
+    err = np.abs(y - ref).max()
+    print(f"synth forward max|y - oracle| = {err:.3e}")
+    assert err < 1e-5
 
 
 def test_forward_end_to_end_within_1e4(small):
@@ -59,11 +63,38 @@ def test_forward_end_to_end_within_1e4(small):
 
 
 def test_loss_frames_match_oracle(small):
+    """Total loss within 1e-5 relative; per-frame loss no further from the
+    fp64 oracle than twice the fp32 oracle's own distance (the log term of
+    near-silent windows is ill-conditioned in fp32)."""
     cfg, X, f0, uv, tgt, out = small
     y = out["y"].reshape(cfg.B, cfg.T)
-    tot, lf = O.mss_fwd(y, tgt, cfg.B, cfg.T, cfg.fft_sizes, cfg.hop_div, cfg.w_lin, cfg.w_log, cfg.T, frames=True)
-    assert abs(out["loss_frames"].astype(np.float64).sum() - tot) / tot < 1e-5
-    assert np.abs(out["loss_frames"] - lf).max() <= 1e-5 * np.abs(lf).max()
+    args = (y, tgt, cfg.B, cfg.T, cfg.fft_sizes, cfg.hop_div, cfg.w_lin, cfg.w_log, cfg.T)
+    tot, lf = O.mss_fwd(*args, frames=True)
+    tot64, lf64 = O.mss_fwd(*args, prec="f64", frames=True)
+    got = out["loss_frames"].astype(np.float64)
+    assert abs(got.sum() - tot) / tot < 1e-5
+    e_gpu = np.abs(got - lf64).max()
+    e_o32 = np.abs(lf.astype(np.float64) - lf64).max()
+    print(f"per-frame loss max abs vs fp64: HIP {e_gpu:.3e}, fp32 oracle {e_o32:.3e}")
+    assert e_gpu <= 2.0 * e_o32 + 1e-9 * np.abs(lf64).max()
+
+
+def test_spectral_gradient_matches_oracle(small):
+    """dL/dy of the 6-scale spectral loss at the GPU's own y.  The L1 terms
+    flip sign where |X| ~ |T| and the log term scales like 1/|X|, so an fp32
+    evaluation carries ~0.4% (L2) noise even in the oracle; the bar is that
+    the HIP gradient is no noisier, against the fp64 oracle, than the fp32
+    oracle is."""
+    cfg, X, f0, uv, tgt, out = small
+    y = out["y"].reshape(cfg.B, cfg.T)
+    args = (y, tgt, cfg.B, cfg.T, cfg.fft_sizes, cfg.hop_div, cfg.w_lin, cfg.w_log, cfg.T)
+    ref64 = O.mss_bwd(*args, prec="f64")
+    ref32 = O.mss_bwd(*args, prec="f32")
+    got = out["dy"].reshape(cfg.B, cfg.T)
+    e_gpu, e_o32 = rel(got, ref64), rel(ref32, ref64)
+    print(f"spectral dL/dy rel L2 vs fp64 oracle: HIP {e_gpu:.3e}, fp32 oracle {e_o32:.3e}; "
+          f"HIP vs fp32 oracle {rel(got, ref32):.3e}")
+    assert e_gpu <= 1.5 * e_o32 + 1e-4
 
 
 def test_synth_backward_matches_oracle(small):
