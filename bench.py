@@ -7,8 +7,11 @@ parameters, and the Adam update, with every input resident in HBM.
 
 Prints ONE JSON line (rank 0):
   value         audio samples/s over the timed steps (B*T per step)
-  roofline      the dominant kernel's achieved rate against its own roof,
+  roofline      the dominant kernel (largest roofline time = algorithmic
+                cost; ties broken by measured time) against its own roof,
                 timed with HIP events on the stream it launches on
+  longest_kernel / kernels   the longest op by measured time and the top
+                ops, each against its own bound (hbm, mfma or fp32 valu)
   step_roofline sum of per-op roofline times / measured step time
   cpu_baseline  the CPU oracle forward (fp32, -O3 -ffast-math) on a bounded
                 sample of the same workload, timed on this host
@@ -114,7 +117,8 @@ def main() -> int:
         log("bench: per-op profile")
         prof = rt.profileKernels()
         rows = table(sess.program, prof)
-        dom = max(rows, key=lambda r: r.meas_ms)
+        dom = max(rows, key=lambda r: (round(r.roof_ms, 6), r.meas_ms))
+        longest = max(rows, key=lambda r: r.meas_ms)
         dom_ms = rt.time_op(dom.index, args.op_iters)
         dom.meas_ms = dom_ms
         ach, peak, unit = dom.achieved()
@@ -150,8 +154,12 @@ def main() -> int:
                                "loss, fwd+bwd+Adam", "B": cfg.B, "T": cfg.T, "sr": cfg.sr, "harmonics": cfg.K,
                    "noise_taps": cfg.NF, "fft_sizes": list(cfg.fft_sizes), "mlp": [cfg.din] + [cfg.hidden] * cfg.layers
                    + [cfg.NC], "parallelism": "single GPU"},
-        "roofline": {"kernel": dom.label, "bound": "hbm" if dom.bound == "hbm" else "mfma",
-                     "achieved": ach, "peak": peak, "unit": unit, "frac": ach / peak, "traffic": None},
+        "roofline": {"kernel": dom.label, "bound": dom.bound, "achieved": ach, "peak": peak, "unit": unit,
+                     "frac": ach / peak, "traffic": None, "ms": dom_ms},
+        "longest_kernel": {"kernel": longest.label, "bound": longest.bound, "ms": longest.meas_ms,
+                           "frac": longest.frac},
+        "kernels": [{"kernel": r.label, "bound": r.bound, "ms": round(r.meas_ms, 4), "roof_ms": round(r.roof_ms, 4),
+                     "frac": round(r.frac, 4)} for r in sorted(rows, key=lambda r: -r.meas_ms)[:10]],
         "step_roofline": {"roof_ms": roof_ms, "measured_ms": ms_per_step, "frac": roof_ms / ms_per_step,
                           "kernel_sum_ms": meas_sum},
         "loss": loss,

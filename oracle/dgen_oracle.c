@@ -188,6 +188,14 @@ static void playhead_real(int F, int T, REAL* out) {
     out[t] = (REAL)(p > hi ? hi : p);
   }
 }
+#ifdef ORACLE_COMMON
+static void playhead_real_f32(int F, int T, float* out) {
+  REAL* p = (REAL*)malloc(sizeof(REAL) * T);
+  playhead_real(F, T, p);
+  for (int t = 0; t < T; ++t) out[t] = (float)p[t];
+  free(p);
+}
+#endif
 void FN(dgen_oracle_playhead)(int F, int T, float* out) {
   REAL* p = (REAL*)malloc(sizeof(REAL) * T);
   playhead_real(F, T, p);
@@ -203,6 +211,46 @@ void dgen_oracle_noise_stream(int T, float* out);
 void dgen_oracle_noise_stream(int T, float* out) {
   uint32_t s = 0;
   for (int t = 0; t < T; ++t) out[t] = noise_step(&s);
+}
+#endif
+
+/* Stateful phasor (pre-increment output) driven by a per-frame frequency:
+ * Sources/DGen/Definitions.swift:96-102,215-246 (u_phasor / u_accum order),
+ * Sources/DGenLazy/Signal.swift:183-225.  Precision-independent (fp32). */
+void dgen_oracle_phasor(const float* freq, int T, float sr, float* out);
+/* Frame-rate sampleRow read of a [F][B] data table through the playhead of
+ * Examples/HarmonicE2E/Synth.swift:60-71 (Emit+RowSelection.swift:164-197):
+ * out[b][t].  Precision-independent (fp32). */
+void dgen_oracle_lerp_frames(const float* src, int B, int F, int T, float* out);
+/* Phase of harmonic lane (b, k), freq = (k+1) * f0f[b][t], at the start of
+ * every seg-frame segment: out[s][b][k] (the tensor phasor of
+ * Emit+State.swift:322-369 evaluated sequentially in fp32). */
+void dgen_oracle_phase_checkpoints(const float* f0f, int B, int K, int T, float sr, int seg, float* out);
+#ifdef ORACLE_COMMON
+void dgen_oracle_phasor(const float* freq, int T, float sr, float* out) {
+  float st = 0.0f;
+  for (int t = 0; t < T; ++t) out[t] = phasor_step(&st, freq[t], sr);
+}
+void dgen_oracle_lerp_frames(const float* src, int B, int F, int T, float* out) {
+  float* play = (float*)malloc(sizeof(float) * T);
+  playhead_real_f32(F, T, play);
+  for (int t = 0; t < T; ++t) {
+    RowLerp r = row_lerp(play[t], F);
+    for (int b = 0; b < B; ++b) out[(size_t)b * T + t] = lerp_data(&r, src[r.lo * B + b], src[r.hi * B + b]);
+  }
+  free(play);
+}
+void dgen_oracle_phase_checkpoints(const float* f0f, int B, int K, int T, float sr, int seg, float* out) {
+  const int nseg = (T + seg - 1) / seg;
+  for (int b = 0; b < B; ++b)
+    for (int k = 0; k < K; ++k) {
+      float ph = 0.0f;
+      for (int t = 0; t < T; ++t) {
+        if (t % seg == 0) out[((size_t)(t / seg) * B + b) * K + k] = ph;
+        (void)phasor_step(&ph, (float)(k + 1) * f0f[(size_t)b * T + t], sr);
+      }
+    }
+  (void)nseg;
 }
 #endif
 
@@ -691,6 +739,18 @@ double FN(dgen_oracle_mss_fwd)(const float* x, const float* tgt, int B, int T, c
   double tot = mss_core(xr, tr, B, T, sizes, n_sizes, hop_div, w_lin, w_log, max_frames, lf, NULL);
   if (loss_frames) to_float(lf, T, loss_frames);
   free(xr);
+  free(tr);
+  free(lf);
+  return tot;
+}
+
+/* As dgen_oracle_mss_fwd with the prediction in this build's precision, so
+ * finite differences can perturb it below fp32 resolution. */
+double FN(dgen_oracle_mss_fwd_real)(const REAL* x, const float* tgt, int B, int T, const int* sizes, int n_sizes,
+                                    int hop_div, float w_lin, float w_log, float max_frames) {
+  REAL* tr = to_real(tgt, (size_t)B * T);
+  REAL* lf = (REAL*)malloc(sizeof(REAL) * T);
+  double tot = mss_core(x, tr, B, T, sizes, n_sizes, hop_div, w_lin, w_log, max_frames, lf, NULL);
   free(tr);
   free(lf);
   return tot;

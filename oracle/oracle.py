@@ -21,6 +21,12 @@ _LIBS: dict[str, ctypes.CDLL] = {}
 _f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
 _i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
 _c_int, _c_float, _c_size = ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+_f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
+
+
+def rp_(sfx):
+    """Pointer type of the build's REAL arrays."""
+    return _f32p if sfx == "_f32" else _f64p
 
 
 def build() -> None:
@@ -48,12 +54,17 @@ def lib(name: str = "liboracle.so") -> ctypes.CDLL:
             mss = [_f32p, _f32p, _c_int, _c_int, _i32p, _c_int, _c_int, _c_float, _c_float, _c_float]
             _sig(L, "dgen_oracle_mss_fwd" + sfx, mss + [ctypes.c_void_p], ctypes.c_double)
             _sig(L, "dgen_oracle_mss_bwd" + sfx, mss + [_f32p])
+            _sig(L, "dgen_oracle_mss_fwd_real" + sfx, [rp_(sfx), _f32p] + mss[2:], ctypes.c_double)
             rp = _f32p if sfx == "_f32" else np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
             _sig(L, "dgen_oracle_harmonic_step" + sfx,
                  [_f32p, rp, _f32p, _f32p, _f32p] + [_c_int] * 8 + [_c_float] * 3 + [_i32p, _c_int, _c_int]
                  + [_c_float] * 3 + [ctypes.c_void_p, ctypes.c_void_p], ctypes.c_double)
             _sig(L, "dgen_oracle_adam" + sfx, [_f32p, _f32p, _f32p, _f32p, _c_size] + [_c_float] * 4 + [_c_int])
-        _sig(L, "dgen_oracle_noise_stream", [_c_int, _f32p])
+        if hasattr(L, "dgen_oracle_noise_stream"):
+            _sig(L, "dgen_oracle_noise_stream", [_c_int, _f32p])
+            _sig(L, "dgen_oracle_phasor", [_f32p, _c_int, _c_float, _f32p])
+            _sig(L, "dgen_oracle_lerp_frames", [_f32p, _c_int, _c_int, _c_int, _f32p])
+            _sig(L, "dgen_oracle_phase_checkpoints", [_f32p, _c_int, _c_int, _c_int, _c_float, _c_int, _f32p])
         _LIBS[name] = L
     return _LIBS[name]
 
@@ -89,6 +100,29 @@ def playhead(F, T, prec="f32"):
 def noise_stream(T):
     out = np.zeros(T, np.float32)
     lib().dgen_oracle_noise_stream(T, out)
+    return out
+
+
+def phasor(freq, sr):
+    """Stateful phasor outputs (pre-increment) for a per-frame frequency."""
+    freq = _f(freq)
+    out = np.zeros(len(freq), np.float32)
+    lib().dgen_oracle_phasor(freq, len(freq), sr, out)
+    return out
+
+
+def lerp_frames(src, B, F, T):
+    """[B][T] frame-rate interpolation of a [F][B] data table along the playhead."""
+    out = np.zeros((B, T), np.float32)
+    lib().dgen_oracle_lerp_frames(_f(src), B, F, T, out)
+    return out
+
+
+def phase_checkpoints(f0f, B, K, T, sr, seg=64):
+    """[nseg][B][K] harmonic phases at every segment start."""
+    nseg = (T + seg - 1) // seg
+    out = np.zeros((nseg, B, K), np.float32)
+    lib().dgen_oracle_phase_checkpoints(_f(f0f), B, K, T, sr, seg, out)
     return out
 
 
@@ -129,6 +163,13 @@ def mss_fwd(x, tgt, B, T, sizes, hop_div, w_lin, w_log, max_frames, prec="f32", 
     tot = _fn("dgen_oracle_mss_fwd", prec, libname)(_f(x), _f(tgt), B, T, sizes, len(sizes), hop_div, w_lin,
                                                     w_log, max_frames, ptr)
     return (tot, lf) if frames else tot
+
+
+def mss_fwd_x64(x, tgt, B, T, sizes, hop_div, w_lin, w_log, max_frames):
+    """fp64 spectral loss with a float64 prediction (finite differences)."""
+    sizes = np.ascontiguousarray(sizes, np.int32)
+    return lib().dgen_oracle_mss_fwd_real_f64(np.ascontiguousarray(x, np.float64), _f(tgt), B, T, sizes, len(sizes),
+                                              hop_div, w_lin, w_log, max_frames)
 
 
 def mss_bwd(x, tgt, B, T, sizes, hop_div, w_lin, w_log, max_frames, prec="f32"):

@@ -1,0 +1,54 @@
+"""The C ABI of libdgen_hip.so on a host without a GPU: the library loads,
+exports every entry point include/dgen_hip.h declares, and reports errors
+through status codes and dgen_hip_last_error() instead of aborting."""
+import ctypes
+import os
+import re
+
+import dgen_hip
+from dgen_hip import runtime as R
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "dgen_hip.h")
+
+
+def declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(dgen_hip_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_runtime_interface():
+    names = declared()
+    for n in ("dgen_hip_create", "dgen_hip_configure", "dgen_hip_run", "dgen_hip_host_memory", "dgen_hip_profile",
+              "dgen_hip_last_error", "dgen_hip_destroy"):
+        assert n in names
+    assert set(names) == set(R.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(R.LIB_PATH)
+    missing = [n for n in declared() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_kernel_class_ids_match_header():
+    text = open(HEADER).read()
+    ids = dict((k, int(v)) for k, v in re.findall(r"DGEN_HIP_K_(\w+)\s*=\s*(\d+)", text))
+    for name, v in ids.items():
+        assert getattr(R, "K_" + name) == v, name
+
+
+def test_errors_are_status_codes_not_aborts():
+    L = dgen_hip.load_library()
+    assert L.dgen_hip_abi_version() == 1
+    rc = L.dgen_hip_run(None, 16)
+    assert rc == -3 and b"not configured" in L.dgen_hip_last_error()
+    rc = L.dgen_hip_configure(None, None, 0, 0, 0)
+    assert rc == -1 and L.dgen_hip_last_error()
+    n = ctypes.c_int(-1)
+    rc = L.dgen_hip_device_count(ctypes.byref(n))
+    assert (rc == 0 and n.value >= 0) or (rc == -2 and n.value == 0)
+    if rc != 0 or n.value == 0:
+        ctx = ctypes.c_void_p()
+        assert L.dgen_hip_create(0, ctypes.byref(ctx)) < 0 and ctx.value is None
+        assert dgen_hip.device_count() == 0

@@ -1,0 +1,92 @@
+"""Host-side schedule construction: cell layout, operand shapes and the cost
+model the roofline figures come from.  CPU only."""
+import numpy as np
+import pytest
+
+from dgen_hip import HarmonicConfig
+from dgen_hip import runtime as R
+from dgen_hip.program import ALIGN, Program
+from dgen_hip.programs import harmonic_program, oscbank_program
+from dgen_hip.roofline import roof_seconds, step_roof_ms
+from dgen_hip.workloads import OscBankConfig, SplitMix64
+
+
+def test_cells_are_aligned_and_disjoint():
+    p = harmonic_program(HarmonicConfig())
+    cells = sorted(p.cells.values(), key=lambda c: c.off)
+    for a, b in zip(cells, cells[1:]):
+        assert a.off % ALIGN == 0 and a.off + a.n <= b.off
+    assert cells[-1].off + cells[-1].n == p.size
+
+
+def test_op_operands_lie_in_cells():
+    p = harmonic_program(HarmonicConfig(B=4, T=4096))
+    starts = {c.off: c for c in p.cells.values()}
+    for op in p.ops:
+        # every cell-typed operand the schedule passes starts a cell
+        for a in op.arg[:3]:
+            if a > 0 and a in starts:
+                assert starts[a].off + starts[a].n <= p.size
+
+
+def test_train_schedule_order():
+    labels = [op.label for op in harmonic_program(HarmonicConfig()).ops if not op.flags & R.OP_STATIC]
+    assert labels.index("phasor_carry") < labels.index("synth_fwd") < labels.index("spectral_mss")
+    assert labels.index("spectral_combine") < labels.index("synth_bwd") < labels.index("heads_bwd")
+    assert labels[-1] == "adam"
+
+
+def test_roofline_model_config3():
+    p = harmonic_program(HarmonicConfig())
+    gemm = [op for op in p.ops if op.bound == "mfma"]
+    flops = sum(op.flops for op in gemm)
+    # 3 x 512 MLP over 32000 rows: forward + two backward GEMMs per layer
+    assert abs(flops - 2 * 32000 * (2 * 512 * 512 * 3 + 512 * 127 * 3)) < 1e6
+    assert 0.5 < step_roof_ms(p) < 2.0
+    assert all(roof_seconds(op) >= 0 for op in p.ops)
+
+
+def test_invalid_configs_raise():
+    with pytest.raises(ValueError):
+        harmonic_program(HarmonicConfig(K=65))
+    with pytest.raises(ValueError):
+        harmonic_program(HarmonicConfig(NF=70))
+    with pytest.raises(ValueError):
+        harmonic_program(HarmonicConfig(fft_sizes=(4096,)))
+    with pytest.raises(ValueError):
+        Program().alloc("x", 0)
+
+
+def test_splitmix_matches_reference_sequence():
+    # SplitMix64 with seed 0 replaced by the golden-ratio increment
+    # (Examples/HarmonicE2E/Config.swift:245-259); vector and scalar agree
+    a, b = SplitMix64(5), SplitMix64(5)
+    v = a.next_array(100)
+    s = np.array([b.next() for _ in range(100)], np.uint64)
+    np.testing.assert_array_equal(v, s)
+    # first output of seed 1 (the published SplitMix64 test value)
+    assert SplitMix64(1).next() == 0x910A2DEC89025CC1
+
+
+def test_weights_follow_reference_init():
+    cfg = HarmonicConfig()
+    w = cfg.weights()
+    assert w.dtype == np.float32 and len(w) == cfg.param_count()
+    # b_noise starts at -3 (Model.swift:77), every other bias at 0
+    bh = w[-cfg.NC:]
+    assert bh[cfg.K + 1] == -3.0 and np.count_nonzero(bh) == 1
+    # trunk layer 1 scale sqrt(2/fan)*0.5
+    w1 = w[:cfg.din * cfg.hidden]
+    assert np.abs(w1).max() <= np.sqrt(2 / cfg.din) * 0.5 + 1e-6
+
+
+def test_oscbank_program():
+    cfg = OscBankConfig()
+    p = oscbank_program(cfg)
+    assert p.output_cell == "out" and p.cells["out"].n == cfg.frames
+
+
+def test_oscbank_inputs_follow_config():
+    freqs, amps = OscBankConfig().inputs()
+    np.testing.assert_array_equal(freqs, (np.arange(1, 17) * 220.0).astype(np.float32))
+    assert abs(float(amps.sum()) - 1.0) < 1e-6
