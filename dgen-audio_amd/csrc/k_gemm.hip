@@ -16,7 +16,9 @@
 
 namespace dgen {
 
-constexpr int BM = 128, BN = 128, BK = 16, LDSROW = BM + 4;
+constexpr int BM = 128, BN = 128, BK = 32, LDSROW = BM + 4;
+// float4 loads per thread per operand tile: BM*BK / 4 / 256
+constexpr int LPT = BM * BK / 4 / 256;
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
@@ -71,30 +73,30 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-  float4 ra[2], rb[2];
+  float4 ra[LPT], rb[LPT];
 
   auto load_tile = [&](int k0) {
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
+    for (int p = 0; p < LPT; ++p) {
       const int q = tid + p * 256;
-      if (!A_KMAJ) {  // [M][K]: float4 along k
-        const int i = q >> 2, kq = (q & 3) * 4;
+      if (!A_KMAJ) {  // [M][K]: float4 along k, BK/4 per row
+        const int i = q / (BK / 4), kq = (q % (BK / 4)) * 4;
         const int row = m0 + i, k = k0 + kq;
         int valid = (row < M) ? min(4, kend - k) : 0;
         ra[p] = load4<VEC>(A + (size_t)row * lda + k, valid);
       } else {  // [K][M]: float4 along m
-        const int kk = q >> 5, iq = (q & 31) * 4;
+        const int kk = q / (BM / 4), iq = (q % (BM / 4)) * 4;
         const int k = k0 + kk, col = m0 + iq;
         int valid = (k < kend) ? min(4, M - col) : 0;
         ra[p] = load4<VEC>(A + (size_t)k * lda + col, valid);
       }
       if (!B_NK) {  // [K][N]: float4 along n
-        const int kk = q >> 5, jq = (q & 31) * 4;
+        const int kk = q / (BN / 4), jq = (q % (BN / 4)) * 4;
         const int k = k0 + kk, col = n0 + jq;
         int valid = (k < kend) ? min(4, N - col) : 0;
         rb[p] = load4<VEC>(B + (size_t)k * ldb + col, valid);
       } else {  // [N][K]: float4 along k
-        const int j = q >> 2, kq = (q & 3) * 4;
+        const int j = q / (BK / 4), kq = (q % (BK / 4)) * 4;
         const int col = n0 + j, k = k0 + kq;
         int valid = (col < N) ? min(4, kend - k) : 0;
         rb[p] = load4<VEC>(B + (size_t)col * ldb + k, valid);
@@ -103,23 +105,23 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const
   };
   auto store_tile = [&](int buf) {
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
+    for (int p = 0; p < LPT; ++p) {
       const int q = tid + p * 256;
       if (!A_KMAJ) {
-        const int i = q >> 2, kq = (q & 3) * 4;
+        const int i = q / (BK / 4), kq = (q % (BK / 4)) * 4;
         As[buf][kq + 0][i] = ra[p].x;
         As[buf][kq + 1][i] = ra[p].y;
         As[buf][kq + 2][i] = ra[p].z;
         As[buf][kq + 3][i] = ra[p].w;
       } else {
-        const int kk = q >> 5, iq = (q & 31) * 4;
+        const int kk = q / (BM / 4), iq = (q % (BM / 4)) * 4;
         *reinterpret_cast<float4*>(&As[buf][kk][iq]) = ra[p];
       }
       if (!B_NK) {
-        const int kk = q >> 5, jq = (q & 31) * 4;
+        const int kk = q / (BN / 4), jq = (q % (BN / 4)) * 4;
         *reinterpret_cast<float4*>(&Bs[buf][kk][jq]) = rb[p];
       } else {
-        const int j = q >> 2, kq = (q & 3) * 4;
+        const int j = q / (BK / 4), kq = (q % (BK / 4)) * 4;
         Bs[buf][kq + 0][j] = rb[p].x;
         Bs[buf][kq + 1][j] = rb[p].y;
         Bs[buf][kq + 2][j] = rb[p].z;
@@ -137,17 +139,28 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const
   for (int k0 = kbeg; k0 < kend; k0 += BK) {
     const bool more = k0 + BK < kend;
     if (more) load_tile(k0 + BK);
+    // operand fragments double-buffered in registers: step s+1's LDS reads
+    // are issued before step s's four MFMAs
+    float fa0[2], fa1[2], fb0[2], fb1[2];
+    auto frag = [&](int st, int slot) {
+      const int k = 2 * st + h;
+      fa0[slot] = As[buf][k][wm + r];
+      fa1[slot] = As[buf][k][wm + 32 + r];
+      fb0[slot] = Bs[buf][k][wn + r];
+      fb1[slot] = Bs[buf][k][wn + 32 + r];
+    };
+    frag(0, 0);
 #pragma unroll
-    for (int s = 0; s < BK / 2; ++s) {
-      const int k = 2 * s + h;
-      float a0 = As[buf][k][wm + r];
-      float a1 = As[buf][k][wm + 32 + r];
-      float b0 = Bs[buf][k][wn + r];
-      float b1 = Bs[buf][k][wn + 32 + r];
-      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
-      acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
-      acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
-      acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+    for (int st = 0; st < BK / 2; ++st) {
+      const int cur = st & 1;
+      if (st + 1 < BK / 2) frag(st + 1, cur ^ 1);
+      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa0[cur], fb0[cur], acc[0][0], 0, 0, 0);
+      acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa0[cur], fb1[cur], acc[0][1], 0, 0, 0);
+      acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa1[cur], fb0[cur], acc[1][0], 0, 0, 0);
+      acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa1[cur], fb1[cur], acc[1][1], 0, 0, 0);
+      // keep the reads for the next step ahead of this step's MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS read
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // MFMA
     }
     if (more) store_tile(buf ^ 1);
     __syncthreads();
