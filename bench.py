@@ -16,7 +16,11 @@ Prints ONE JSON line (rank 0):
   cpu_baseline  the CPU oracle forward (fp32, -O3 -ffast-math) on a bounded
                 sample of the same workload, timed on this host
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+With ``--workload biquad`` the same line is printed for BASELINE config 4
+(256-lane x 2^18 tensor biquad bank, forward + loss + BPTT + Adam) instead;
+the default workload is the headline config 3.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--workload harmonic|biquad]
 """
 from __future__ import annotations
 
@@ -31,6 +35,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "dgen-audio_amd"))
 
 METRIC = "fwd+bwd audio samples/sec, batch-32 harmonic synth + MSS loss; % HBM peak"
+BIQUAD_METRIC = "fwd+bwd lane-samples/sec, 256-lane x 2^18 tensor biquad bank with BPTT"
 
 
 def log(msg: str) -> None:
@@ -77,6 +82,109 @@ def cpu_baseline(cfg, lanes: int, repeats: int) -> dict:
     }
 
 
+def time_session(rt, program, args):
+    """Warm up, time args.steps back-to-back runs, then profile every op and
+    time the dominant one (largest roofline time) with HIP events."""
+    from dgen_hip.roofline import step_roof_ms, table
+    log(f"bench: warmup {args.warmup}")
+    for _ in range(args.warmup):
+        rt.run_async()
+    rt.sync()
+    log(f"bench: timing {args.steps} steps")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        rt.run_async()
+    rt.sync()
+    wall = time.perf_counter() - t0
+    log("bench: per-op profile")
+    rows = table(program, rt.profileKernels())
+    dom = max(rows, key=lambda r: (round(r.roof_ms, 6), r.meas_ms))
+    dom.meas_ms = rt.time_op(dom.index, args.op_iters)
+    for r in sorted(rows, key=lambda r: -r.meas_ms):
+        log(f"  {r.label:18s} {r.bound:5s} meas {r.meas_ms * 1e3:9.1f} us  roof {r.roof_ms * 1e3:8.1f} us  "
+            f"frac {r.frac:6.3f}")
+    return wall, rows, dom, step_roof_ms(program)
+
+
+def roofline_fields(rows, dom, roof_ms, ms_per_step):
+    longest = max(rows, key=lambda r: r.meas_ms)
+    ach, peak, unit = dom.achieved()
+    return {
+        "roofline": {"kernel": dom.label, "bound": dom.bound, "achieved": ach, "peak": peak, "unit": unit,
+                     "frac": ach / peak, "traffic": None, "ms": dom.meas_ms},
+        "longest_kernel": {"kernel": longest.label, "bound": longest.bound, "ms": longest.meas_ms,
+                           "frac": longest.frac},
+        "kernels": [{"kernel": r.label, "bound": r.bound, "ms": round(r.meas_ms, 4), "roof_ms": round(r.roof_ms, 4),
+                     "frac": round(r.frac, 4)} for r in sorted(rows, key=lambda r: -r.meas_ms)[:10]],
+        "step_roofline": {"roof_ms": roof_ms, "measured_ms": ms_per_step, "frac": roof_ms / ms_per_step,
+                          "kernel_sum_ms": sum(r.meas_ms for r in rows)},
+    }
+
+
+def biquad_cpu_baseline(cfg, repeats: int) -> dict:
+    """The oracle's fp32 biquad step (forward, loss and BPTT backward; built
+    with the reference C backend's -O3 -ffast-math policy) over the whole
+    config-4 workload, single thread.  Median of `repeats` after a warm-up."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    x, m, p = cfg.inputs(), cfg.modulation(), cfg.params()
+    tgt = O.biquad_fwd(x, None, cfg.target_params()[:cfg.B], cfg.target_params()[cfg.B:])
+    fn = O._fn("dgen_oracle_biquad_step", "f32", "liboracle_bench.so")
+    import ctypes
+    import numpy as np
+    g = np.zeros(2 * cfg.B, np.float32)
+    times = []
+    for i in range(repeats + 1):
+        t0 = time.perf_counter()
+        fn(x, m.ctypes.data_as(ctypes.c_void_p), np.ascontiguousarray(p[:cfg.B]), np.ascontiguousarray(p[cfg.B:]),
+           tgt, cfg.B, cfg.T, None, g.ctypes.data_as(ctypes.c_void_p))
+        dt = time.perf_counter() - t0
+        if i:
+            times.append(dt)
+    times.sort()
+    med = times[len(times) // 2]
+    return {
+        "value": cfg.B * cfg.T / med,
+        "unit": "lane-samples/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"whole workload ({cfg.B} lanes x {cfg.T} frames): sequential fp32 forward, loss and BPTT "
+                   f"backward (no Adam); median of {repeats} after 1 warm-up; host "
+                   f"{platform.processor() or platform.machine()}, nproc {os.cpu_count()}"),
+    }
+
+
+def run_biquad(args) -> dict:
+    from dgen_hip import BiquadConfig
+    from dgen_hip.programs import BiquadSession
+    cfg = BiquadConfig()
+    log(f"bench: biquad session B={cfg.B} T={cfg.T} chunk={args.chunk}")
+    sess = BiquadSession(cfg, device=0, optimizer=True, chunk=args.chunk)
+    try:
+        wall, rows, dom, roof_ms = time_session(sess.rt, sess.program, args)
+        loss = sess.loss()
+    finally:
+        sess.close()
+    ms_per_step = wall * 1e3 / args.steps
+    cpu = None
+    if not args.no_cpu:
+        log("bench: cpu baseline (biquad)")
+        cpu = biquad_cpu_baseline(cfg, args.cpu_repeats)
+    out = {
+        "metric": BIQUAD_METRIC, "value": cfg.B * cfg.T * args.steps / wall, "unit": "lane-samples/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (U[-1,1] SplitMix64 input per lane, 2 Hz geometric cutoff sweep)",
+        "config": {"workload": "config 4: tensor biquad bank, RBJ low-pass with per-sample coefficients, MSE vs "
+                               "fixed bank, BPTT to base cutoff and Q, Adam", "B": cfg.B, "T": cfg.T, "sr": cfg.sr,
+                   "chunk": args.chunk, "parallelism": "single GPU"},
+    }
+    out.update(roofline_fields(rows, dom, roof_ms, ms_per_step))
+    out["loss"] = loss
+    out["cpu_baseline"] = cpu
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
@@ -86,60 +194,41 @@ def main() -> int:
     ap.add_argument("--cpu-lanes", type=int, default=4)
     ap.add_argument("--cpu-repeats", type=int, default=3)
     ap.add_argument("--op-iters", type=int, default=10, help="runs averaged for the dominant kernel's time")
+    ap.add_argument("--workload", choices=("harmonic", "biquad"), default="harmonic")
+    ap.add_argument("--chunk", type=int, default=256, help="biquad scan chunk length (frames)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this backend runs on one GPU; the multi-GPU "
               f"design (lane sharding + one gradient all-reduce) is not built.", file=sys.stderr)
         return 2
+    if args.workload == "biquad":
+        print(json.dumps(run_biquad(args)), flush=True)
+        return 0
 
+    print(json.dumps(run_harmonic(args)), flush=True)
+    return 0
+
+
+def run_harmonic(args) -> dict:
     from dgen_hip import HarmonicConfig
     from dgen_hip.programs import HarmonicSession
-    from dgen_hip.roofline import step_roof_ms, table
 
     cfg = HarmonicConfig()  # B=32, T=64000 @ 16 kHz, K=60, NF=65, MLP 3x512, FFT 2048..64
     log(f"bench: building session B={cfg.B} T={cfg.T} K={cfg.K} hidden={cfg.hidden}")
     sess = HarmonicSession(cfg, device=0, optimizer=True)
-    rt = sess.rt
     try:
-        log(f"bench: warmup {args.warmup}")
-        for _ in range(args.warmup):
-            rt.run_async()
-        rt.sync()
-        log(f"bench: timing {args.steps} steps")
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            rt.run_async()
-        rt.sync()
-        wall = time.perf_counter() - t0
-        ms_per_step = wall * 1e3 / args.steps
-        value = cfg.B * cfg.T * args.steps / wall
-
-        log("bench: per-op profile")
-        prof = rt.profileKernels()
-        rows = table(sess.program, prof)
-        dom = max(rows, key=lambda r: (round(r.roof_ms, 6), r.meas_ms))
-        longest = max(rows, key=lambda r: r.meas_ms)
-        dom_ms = rt.time_op(dom.index, args.op_iters)
-        dom.meas_ms = dom_ms
-        ach, peak, unit = dom.achieved()
-        roof_ms = step_roof_ms(sess.program)
-        meas_sum = sum(r.meas_ms for r in rows)
+        wall, rows, dom, roof_ms = time_session(sess.rt, sess.program, args)
         loss = sess.loss()
     finally:
         sess.close()
-
-    for r in sorted(rows, key=lambda r: -r.meas_ms):
-        log(f"  {r.label:18s} {r.bound:5s} meas {r.meas_ms * 1e3:9.1f} us  roof {r.roof_ms * 1e3:8.1f} us  "
-            f"frac {r.frac:6.3f}")
-
+    ms_per_step = wall * 1e3 / args.steps
     cpu = None
     if not args.no_cpu:
         log(f"bench: cpu baseline ({args.cpu_lanes} lanes)")
         cpu = cpu_baseline(cfg, args.cpu_lanes, args.cpu_repeats)
-
     out = {
         "metric": METRIC,
-        "value": value,
+        "value": cfg.B * cfg.T * args.steps / wall,
         "unit": "audio samples/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -154,19 +243,11 @@ def main() -> int:
                                "loss, fwd+bwd+Adam", "B": cfg.B, "T": cfg.T, "sr": cfg.sr, "harmonics": cfg.K,
                    "noise_taps": cfg.NF, "fft_sizes": list(cfg.fft_sizes), "mlp": [cfg.din] + [cfg.hidden] * cfg.layers
                    + [cfg.NC], "parallelism": "single GPU"},
-        "roofline": {"kernel": dom.label, "bound": dom.bound, "achieved": ach, "peak": peak, "unit": unit,
-                     "frac": ach / peak, "traffic": None, "ms": dom_ms},
-        "longest_kernel": {"kernel": longest.label, "bound": longest.bound, "ms": longest.meas_ms,
-                           "frac": longest.frac},
-        "kernels": [{"kernel": r.label, "bound": r.bound, "ms": round(r.meas_ms, 4), "roof_ms": round(r.roof_ms, 4),
-                     "frac": round(r.frac, 4)} for r in sorted(rows, key=lambda r: -r.meas_ms)[:10]],
-        "step_roofline": {"roof_ms": roof_ms, "measured_ms": ms_per_step, "frac": roof_ms / ms_per_step,
-                          "kernel_sum_ms": meas_sum},
-        "loss": loss,
-        "cpu_baseline": cpu,
     }
-    print(json.dumps(out), flush=True)
-    return 0
+    out.update(roofline_fields(rows, dom, roof_ms, ms_per_step))
+    out["loss"] = loss
+    out["cpu_baseline"] = cpu
+    return out
 
 
 if __name__ == "__main__":

@@ -84,5 +84,10 @@ int launch_noise_table(const Launch&, const dgen_hip_op&);
 int launch_row_schedule(const Launch&, const dgen_hip_op&);
 int launch_fft_tables(const Launch&, const dgen_hip_op&);
 int launch_lerp_frames(const Launch&, const dgen_hip_op&);
+int launch_biquad_chunk(const Launch&, const dgen_hip_op&);
+int launch_biquad_carry(const Launch&, const dgen_hip_op&);
+int launch_biquad_fwd(const Launch&, const dgen_hip_op&);
+int launch_biquad_adj_chunk(const Launch&, const dgen_hip_op&);
+int launch_biquad_bwd(const Launch&, const dgen_hip_op&);
 
 }  // namespace dgen

@@ -62,6 +62,11 @@ static Launcher launcher_for(uint32_t k) {
     case DGEN_HIP_K_ROW_SCHEDULE: return launch_row_schedule;
     case DGEN_HIP_K_FFT_TABLES: return launch_fft_tables;
     case DGEN_HIP_K_LERP_FRAMES: return launch_lerp_frames;
+    case DGEN_HIP_K_BIQUAD_CHUNK: return launch_biquad_chunk;
+    case DGEN_HIP_K_BIQUAD_CARRY: return launch_biquad_carry;
+    case DGEN_HIP_K_BIQUAD_FWD: return launch_biquad_fwd;
+    case DGEN_HIP_K_BIQUAD_ADJ_CHUNK: return launch_biquad_adj_chunk;
+    case DGEN_HIP_K_BIQUAD_BWD: return launch_biquad_bwd;
     default: return nullptr;
   }
 }

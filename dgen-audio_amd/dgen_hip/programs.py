@@ -11,7 +11,7 @@ import numpy as np
 
 from . import runtime as R
 from .program import Program
-from .workloads import HarmonicConfig, OscBankConfig
+from .workloads import BiquadConfig, HarmonicConfig, OscBankConfig
 
 SEG = 64          # frames per synth segment (checkpoint spacing)
 SLOTS = 4         # control rows a segment may touch
@@ -19,6 +19,7 @@ ROW_ENTRIES = 8   # (segment, slot) entries per control row
 LDC = 128         # padded control-row stride (K + 2 + NF <= 128)
 SPLITK_ROWS = 1024  # rows per split of the weight-gradient GEMMs
 MSS_TILE = 4096     # output samples per spectral-loss workgroup
+BQ_CHUNK = 256      # frames per biquad scan chunk
 
 
 def _f32(x) -> float:
@@ -279,6 +280,124 @@ class HarmonicSession:
 
     def loss(self) -> float:
         return float(self.rt.read("loss_frames").astype(np.float64).sum())
+
+    def close(self):
+        self.rt.close()
+
+
+# ------------------------------------------------------------------ config 4
+def _colsum_ws(rows: int, cols: int) -> int:
+    return max(1, min(256, rows // 32)) * cols
+
+
+def biquad_program(cfg: BiquadConfig, train: bool = True, optimizer: bool = True, modulated: bool = True,
+                   chunk: int = BQ_CHUNK) -> Program:
+    """Tensor biquad bank: x -> RBJ low-pass with cutoff base[k]*mod[n] and Q[k].
+
+    ``train=False`` builds the forward render only (used for the fixed target
+    bank, ``modulated=False``).  With ``train=True``: forward, loss
+    sum (y - target)^2, BPTT to (base, Q), and (``optimizer``) one Adam step.
+    Each recurrence runs as a chunked scan (chunk summaries, per-lane carry
+    composition, replay) forward and, for the adjoint, backward."""
+    B, T, L = cfg.B, cfg.T, int(chunk)
+    if L <= 0:
+        raise ValueError("chunk length must be positive")
+    C = (T + L - 1) // L
+    f4 = 4.0
+    p = Program(max_frames=T)
+    p.meta.update(cfg=cfg, chunk=L, chunks=C, train=train)
+    x = p.alloc("x", T * B)
+    mod = p.alloc("mod", T) if modulated else -1
+    P = p.alloc("params", 2 * B)
+    y = p.alloc("y", T * B)
+    summ = p.alloc("summary", 12 * C * B)  # fp64
+    init = p.alloc("init", 2 * C * B)
+    # algorithmic cost per lane-frame: coefficients (|.|, cos, sin, 2 div, 9 mul/add) ~ 16 flops,
+    # one Direct Form I step 9 flops
+    n = float(T * B)
+    mod_b = float(T) * f4 if modulated else 0.0
+    sfx = "" if modulated else " (fixed cutoff)"
+    p.add(R.K_BIQUAD_CHUNK, [x, mod, P, summ, B, T, L], label="bq_chunk", dispatch=f"chunk summaries {C}x{B}{sfx}",
+          bytes=n * f4 + mod_b + 12.0 * C * B * f4, flops=n * (16 + 3 * 9))
+    p.add(R.K_BIQUAD_CARRY, [summ, init, B, C, 0], label="bq_carry", dispatch=f"per-lane scan of {C} chunk maps",
+          bytes=(12.0 + 2.0) * C * B * f4, flops=24.0 * C * B)
+    if not train:
+        p.add(R.K_BIQUAD_FWD, [x, mod, P, init, y, B, T, L, -1, -1], label="bq_fwd", dispatch=f"chunk replay{sfx}",
+              bytes=2 * n * f4 + mod_b + 2.0 * C * B * f4, flops=n * (16 + 9))
+        p.output_cell = "y"
+        return p
+    tgt = p.alloc("target", T * B)
+    lossp = p.alloc("loss_partials", C * B)
+    lane_loss = p.alloc("lane_loss", B)
+    loss = p.alloc("loss", 1)
+    asumm = p.alloc("adj_summary", 12 * C * B)  # fp64
+    ainit = p.alloc("adj_init", 2 * C * B)
+    gpart = p.alloc("grad_partials", 2 * C * B)
+    G = p.alloc("grads", 2 * B)
+    ws = p.alloc("colsum_ws", max(_colsum_ws(C, 2 * B), _colsum_ws(C, B), _colsum_ws(B, 1)))
+    p.add(R.K_BIQUAD_FWD, [x, mod, P, init, y, B, T, L, tgt, lossp], label="bq_fwd",
+          dispatch="chunk replay + loss partials", bytes=3 * n * f4 + mod_b + 3.0 * C * B * f4,
+          flops=n * (16 + 9 + 3))
+    p.add(R.K_COLSUM, [lossp, lane_loss, C, B, B, ws], label="loss_lanes", dispatch="chunkPartialsReduceToCell",
+          bytes=(C * B + B) * f4, flops=float(C * B))
+    p.add(R.K_COLSUM, [lane_loss, loss, B, 1, 1, ws], label="loss_sum", dispatch="chunkPartialsReduceToCell",
+          bytes=(B + 1) * f4, flops=float(B))
+    p.add(R.K_BIQUAD_ADJ_CHUNK, [mod, P, y, tgt, asumm, B, T, L], label="bq_adj_chunk",
+          dispatch=f"reverse chunk summaries {C}x{B}", bytes=2 * n * f4 + mod_b + 12.0 * C * B * f4,
+          flops=n * (16 + 3 * 6))
+    p.add(R.K_BIQUAD_CARRY, [asumm, ainit, B, C, 1], label="bq_adj_carry", dispatch=f"reverse scan of {C} maps",
+          bytes=(12.0 + 2.0) * C * B * f4, flops=24.0 * C * B)
+    p.add(R.K_BIQUAD_BWD, [x, mod, P, y, tgt, ainit, gpart, B, T, L], label="bq_bwd",
+          dispatch="reverse chunk replay + gradient partials", bytes=3 * n * f4 + mod_b + 4.0 * C * B * f4,
+          flops=n * (16 + 6 + 30))
+    p.add(R.K_COLSUM, [gpart, G, C, 2 * B, 2 * B, ws], label="grad_sum", dispatch="chunkPartialsReduceToCell",
+          bytes=(2.0 * C * B + 2 * B) * f4, flops=2.0 * C * B)
+    if optimizer:
+        m = p.alloc("adam_m", 2 * B)
+        v = p.alloc("adam_v", 2 * B)
+        tcell = p.alloc("adam_t", 1)
+        p.add(R.K_ADAM, [P, G, m, v, 2 * B, tcell], [cfg.lr, 0.9, 0.999, 1e-8], label="adam",
+              dispatch=f"staticThreads({2 * B})", bytes=7.0 * 2 * B * f4, flops=12.0 * 2 * B)
+    p.output_cell = "y"
+    return p
+
+
+class BiquadSession:
+    """Config-4 training runtime: the target bank is rendered once by a
+    forward-only program with the fixed (tgt_fc, tgt_Q) coefficients, then
+    every ``step()`` is forward + loss + BPTT (+ Adam) with all data in HBM."""
+
+    def __init__(self, cfg: BiquadConfig, device: int = 0, optimizer: bool = True, chunk: int = BQ_CHUNK,
+                 target=None):
+        self.cfg = cfg
+        self.x = cfg.inputs()
+        self.mod = cfg.modulation()
+        self.params0 = cfg.params()
+        if target is None:
+            target = self.render(cfg.target_params(), device, modulated=False, chunk=chunk)
+        self.target = np.ascontiguousarray(target, np.float32).reshape(cfg.T, cfg.B)
+        self.program = biquad_program(cfg, train=True, optimizer=optimizer, chunk=chunk)
+        self.rt = R.HIPLazyRuntime(self.program, device)
+        self.rt.write("x", self.x)
+        self.rt.write("mod", self.mod)
+        self.rt.write("params", self.params0)
+        self.rt.write("target", self.target)
+
+    def render(self, params, device: int = 0, modulated: bool = True, chunk: int = BQ_CHUNK) -> np.ndarray:
+        prog = biquad_program(self.cfg, train=False, modulated=modulated, chunk=chunk)
+        with R.HIPLazyRuntime(prog, device) as rt:
+            rt.write("x", self.x)
+            if modulated:
+                rt.write("mod", self.mod)
+            rt.write("params", params)
+            rt.runNoCopy()
+            return rt.read("y").reshape(self.cfg.T, self.cfg.B)
+
+    def step(self) -> None:
+        self.rt.runNoCopy()
+
+    def loss(self) -> float:
+        return float(self.rt.read("loss")[0])
 
     def close(self):
         self.rt.close()

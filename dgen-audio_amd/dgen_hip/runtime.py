@@ -42,6 +42,11 @@ K_NOISE_TABLE = 16
 K_ROW_SCHEDULE = 17
 K_FFT_TABLES = 18
 K_LERP_FRAMES = 19
+K_BIQUAD_CHUNK = 20
+K_BIQUAD_CARRY = 21
+K_BIQUAD_FWD = 22
+K_BIQUAD_ADJ_CHUNK = 23
+K_BIQUAD_BWD = 24
 
 KERNEL_NAMES = {v: k[2:].lower() for k, v in globals().items() if k.startswith("K_")}
 

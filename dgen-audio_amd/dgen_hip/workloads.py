@@ -172,3 +172,50 @@ class HarmonicConfig:
         if self.din > 2:
             X[:, 2] = uv.T.reshape(-1)
         return f0, uv, X
+
+
+# ---------------------------------------------------------------- config 4
+@dataclass
+class BiquadConfig:
+    """Tensor biquad bank with BPTT: B lanes x T samples of U[-1,1] noise
+    through an RBJ low-pass whose cutoff base[k] * m[n] follows a geometric
+    f_lo -> f_hi sweep driven by a sine LFO; loss = sum (y - y_target)^2
+    against a fixed (tgt_fc, tgt_Q) bank; gradients w.r.t. base and Q."""
+    B: int = 256
+    T: int = 1 << 18
+    sr: float = 44100.0
+    lfo_hz: float = 2.0
+    f_lo: float = 200.0
+    f_hi: float = 4000.0
+    base0: float = 200.0
+    Q0: float = 0.707
+    tgt_fc: float = 1000.0
+    tgt_Q: float = 0.707
+    seed: int = 40
+    lr: float = 1e-3
+
+    def inputs(self) -> np.ndarray:
+        """x [T][B]: lane k is U[-1,1] drawn from SplitMix64(seed + k)."""
+        x = np.empty((self.T, self.B), np.float32)
+        for k in range(self.B):
+            x[:, k] = (SplitMix64(self.seed + k).uniform(self.T) * 2.0 - 1.0).astype(np.float32)
+        return x
+
+    def modulation(self) -> np.ndarray:
+        """m [T] in fp32, so that base[k] * m[n] sweeps geometrically between
+        base*1 and base*(f_hi/f_lo): the LFO is the deterministic phasor
+        frac((lfo/sr) * n) (Sources/DGen/Emit+State.swift:382-386) through
+        sin(2 pi p), mapped to m = (f_hi/f_lo)^(0.5 + 0.5 sin)."""
+        n = np.arange(self.T, dtype=np.float32)
+        r = np.float32(self.lfo_hz / self.sr) * n
+        ph = (r - np.floor(r)).astype(np.float32)
+        s = np.sin(np.float32(2.0 * math.pi) * ph, dtype=np.float32)
+        e = (np.float32(0.5) + np.float32(0.5) * s).astype(np.float32)
+        return np.exp2(np.float32(math.log2(self.f_hi / self.f_lo)) * e, dtype=np.float32).astype(np.float32)
+
+    def params(self) -> np.ndarray:
+        """Parameter blob [2][B] = base | Q."""
+        return np.concatenate([np.full(self.B, self.base0, np.float32), np.full(self.B, self.Q0, np.float32)])
+
+    def target_params(self) -> np.ndarray:
+        return np.concatenate([np.full(self.B, self.tgt_fc, np.float32), np.full(self.B, self.tgt_Q, np.float32)])

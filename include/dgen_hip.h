@@ -166,6 +166,41 @@ enum dgen_hip_kernel {
    * frac src[hi][b].  arg: [0]=src [1]=lerp ([T][8]) [2]=out ([B][T]) [3]=B
    * [4]=F [5]=T */
   DGEN_HIP_K_LERP_FRAMES = 19,
+
+  /* ---- tensor biquad bank (HigherOps.swift:401-570, RBJ low-pass, mode 0,
+   * gain 1, coefficients recomputed every frame from cutoff base[k]*mod[n]
+   * and Q[k]).  x, y, target: [T][B]; params: [2][B] = base | Q; mod: [T] or
+   * -1 (unmodulated).  Time is cut into C = ceil(T/L) chunks of L frames.
+   *
+   * Forward part 1: per (lane, chunk) the zero-state response and the
+   * responses to the unit initial states, summary [C][6][B] in fp64 (12*C*B
+   * floats, even cell offset).
+   * arg: [0]=x [1]=mod [2]=params [3]=summary [4]=B [5]=T [6]=L */
+  DGEN_HIP_K_BIQUAD_CHUNK = 20,
+
+  /* Compose the fp64 chunk summaries per lane (ascending chunks, or
+   * descending when reverse = 1, for the adjoint): init [C][2][B] (fp32) =
+   * the state entering each chunk.  arg: [0]=summary [1]=init [2]=B [3]=C [4]=reverse */
+  DGEN_HIP_K_BIQUAD_CARRY = 21,
+
+  /* Forward part 2: each chunk re-run from its initial state; writes y and,
+   * when a target is given, per-chunk partial sums of (y - target)^2.
+   * arg: [0]=x [1]=mod [2]=params [3]=init [4]=y [5]=B [6]=T [7]=L
+   *      [8]=target or -1 [9]=loss partials [C][B] (with a target) or -1 */
+  DGEN_HIP_K_BIQUAD_FWD = 22,
+
+  /* BPTT part 1 (BPTTEmission.swift:133-160): per (lane, chunk), the reverse
+   * adjoint recurrence's zero-carry result and its responses to the unit
+   * carries, summary [C][6][B] fp64 (then DGEN_HIP_K_BIQUAD_CARRY, reverse 1).
+   * arg: [0]=mod [1]=params [2]=y [3]=target [4]=summary [5]=B [6]=T [7]=L */
+  DGEN_HIP_K_BIQUAD_ADJ_CHUNK = 23,
+
+  /* BPTT part 2: each chunk's adjoint from its carry, chained through the
+   * coefficients to per-chunk gradient partials [C][2][B] (d/d base,
+   * d/d Q), summed over chunks by DGEN_HIP_K_COLSUM.
+   * arg: [0]=x [1]=mod [2]=params [3]=y [4]=target [5]=adjoint init
+   *      [6]=grad partials [7]=B [8]=T [9]=L */
+  DGEN_HIP_K_BIQUAD_BWD = 24,
 };
 
 /* GEMM epilogues */

@@ -824,3 +824,163 @@ void FN(dgen_oracle_adam)(float* p, const float* g, float* m, float* v, size_t n
     v[j] = (float)vj;
   }
 }
+
+/* ------------------------------------------------------------------------ */
+/* Config 4: tensor biquad bank, forward and BPTT adjoint.                  */
+/* ------------------------------------------------------------------------ */
+
+#define R_COS(x) (IS_F32 ? (REAL)cosf((float)(x)) : (REAL)cos((double)(x)))
+
+/* w0 per Hz: the reference hardcodes 2*pi/44100 as a Float constant
+ * (Sources/DGen/HigherOps.swift:446-447), whatever the graph's sample rate. */
+#define BQ_W0_PER_HZ ((REAL)0.00014247585730565955f)
+
+typedef struct {
+  REAL c, s, q, alpha, r, P, D;  /* cos, sin, |Q|, div18, recip24, div11, add10 */
+  REAL b0, b1, b2, a1, a2;
+} BqCoef;
+
+/* RBJ low-pass coefficients (mode 0, gain 1) in the reference graph's
+ * operation order, node names as in Sources/DGen/HigherOps.swift:443-556:
+ * selector(mode+1 == 1, ...) picks the first option and the shelf branch
+ * (mode >= 6) is not taken.  mult26 = recip24 * gain with gain = 1. */
+static inline void bq_coef(REAL fc, REAL Q, BqCoef* k) {
+  REAL abs6 = R_ABS(fc);
+  REAL mult7 = abs6 * BQ_W0_PER_HZ;
+  REAL cos8 = R_COS(mult7);
+  REAL mult9 = cos8 * (REAL)-1;
+  REAL add10 = mult9 + (REAL)1;
+  REAL div11 = add10 / (REAL)2;
+  REAL sin14 = R_SIN(mult7);
+  REAL mult15 = sin14 * (REAL)0.5;
+  REAL abs17 = R_ABS(Q);
+  REAL div18 = mult15 / abs17;
+  REAL add22 = div18 + (REAL)1;
+  REAL recip24 = (REAL)1 / add22;
+  REAL mult26 = recip24 * (REAL)1;
+  REAL mult31 = mult9 * (REAL)2;
+  REAL not_sub35 = (REAL)1 - div18;
+  k->c = cos8;
+  k->s = sin14;
+  k->q = abs17;
+  k->alpha = div18;
+  k->r = recip24;
+  k->P = div11;
+  k->D = add10;
+  k->b2 = div11 * mult26;           /* selector23 -> b2_scaled */
+  k->b1 = add10 * mult26;           /* selector32 -> b1_scaled */
+  k->b0 = div11 * mult26;           /* selector36 -> b0_scaled */
+  k->a2 = not_sub35 * recip24;      /* a2_orig */
+  k->a1 = mult31 * recip24;         /* a1_orig */
+}
+
+/* One Direct Form I step, HigherOps.swift:535-568: history3 = x[n-2],
+ * history2 = x[n-1], history0 = y[n-2], history1 = y[n-1]. */
+static inline REAL bq_step(const BqCoef* k, REAL x0, REAL x1, REAL x2, REAL y1, REAL y2) {
+  REAL mult28 = x2 * k->b2;
+  REAL mult34 = x1 * k->b1;
+  REAL mult38 = x0 * k->b0;
+  REAL add39 = (mult28 + mult34) + mult38;
+  REAL mult42 = y2 * k->a2;
+  REAL mult44 = y1 * k->a1;
+  REAL add45 = mult42 + mult44;
+  return add39 - add45;
+}
+
+/* cutoff[n][k] = base[k] * m[n] (the per-lane base times the shared
+ * modulation signal; m == NULL means unmodulated).  The product is the
+ * graph's `mul` node, so it is rounded in this build's precision. */
+static inline REAL bq_cutoff(const float* m, const REAL* base, int n, int k) {
+  return m ? base[k] * (REAL)m[n] : base[k];
+}
+
+/* Forward of the bank: x, y are [T][B] (frame-major, lane-minor).  State
+ * starts at zero (history cells zeroed by zeroAllBuffers). */
+static void bq_forward(const float* x, const float* m, const REAL* base, const REAL* Q, int B, int T, REAL* y) {
+  REAL* st = (REAL*)calloc((size_t)4 * B, sizeof(REAL)); /* x1 x2 y1 y2 per lane */
+  for (int n = 0; n < T; ++n) {
+    for (int k = 0; k < B; ++k) {
+      REAL* s = st + 4 * k;
+      BqCoef c;
+      bq_coef(bq_cutoff(m, base, n, k), Q[k], &c);
+      REAL x0 = (REAL)x[(size_t)n * B + k];
+      REAL v = bq_step(&c, x0, s[0], s[1], s[2], s[3]);
+      s[1] = s[0];
+      s[0] = x0;
+      s[3] = s[2];
+      s[2] = v;
+      y[(size_t)n * B + k] = v;
+    }
+  }
+  free(st);
+}
+
+void FN(dgen_oracle_biquad_fwd)(const float* x, const float* m, const REAL* base, const REAL* Q, int B, int T,
+                                float* y_out) {
+  REAL* y = (REAL*)malloc(sizeof(REAL) * (size_t)B * T);
+  bq_forward(x, m, base, Q, B, T, y);
+  to_float(y, (size_t)B * T, y_out);
+  free(y);
+}
+
+/* One config-4 training step in this build's precision: forward, loss
+ * sum_n sum_k (y - tgt)^2 (u_mse per element, Sources/DGen/Definitions.swift:
+ * 206-213, summed over lanes and frames), and (grad != NULL) the BPTT
+ * gradient [2][B] = (d/d base_k, d/d Q_k).
+ *
+ * Adjoint: with g[n] = 2 (y[n] - tgt[n]) and lambda[n] = dL/dy[n] in total,
+ *   lambda[n] = g[n] - a1[n+1] lambda[n+1] - a2[n+2] lambda[n+2],
+ * run backwards with two carries (v1, v2) = the contributions already owed
+ * to lambda[n-1] and lambda[n-2].  The coefficient derivatives follow the
+ * chain rule through the nodes of bq_coef (pinned by finite differences of
+ * this function's fp64 build). */
+double FN(dgen_oracle_biquad_step)(const float* x, const float* m, const REAL* base, const REAL* Q,
+                                   const float* tgt, int B, int T, float* y_out, REAL* grad) {
+  const size_t N = (size_t)B * T;
+  REAL* y = (REAL*)malloc(sizeof(REAL) * N);
+  bq_forward(x, m, base, Q, B, T, y);
+  if (y_out) to_float(y, N, y_out);
+  double loss = 0.0;
+  for (size_t i = 0; i < N; ++i) {
+    REAL d = y[i] - (REAL)tgt[i];
+    loss += (double)(d * d);
+  }
+  if (grad) {
+    REAL* v = (REAL*)calloc((size_t)2 * B, sizeof(REAL));
+    for (int k = 0; k < 2 * B; ++k) grad[k] = 0;
+    for (int n = T - 1; n >= 0; --n) {
+      for (int k = 0; k < B; ++k) {
+        const size_t i = (size_t)n * B + k;
+        REAL fc = bq_cutoff(m, base, n, k);
+        BqCoef c;
+        bq_coef(fc, Q[k], &c);
+        REAL x0 = (REAL)x[i];
+        REAL x1 = n >= 1 ? (REAL)x[i - B] : 0;
+        REAL x2 = n >= 2 ? (REAL)x[i - 2 * (size_t)B] : 0;
+        REAL y1 = n >= 1 ? y[i - B] : 0;
+        REAL y2 = n >= 2 ? y[i - 2 * (size_t)B] : 0;
+        REAL lam = (REAL)2 * (y[i] - (REAL)tgt[i]) + v[2 * k];
+        v[2 * k] = v[2 * k + 1] - c.a1 * lam;
+        v[2 * k + 1] = -c.a2 * lam;
+        /* dL/d(coefficient) at this frame */
+        REAL gb0 = lam * x0, gb2 = lam * x2, gb1 = lam * x1;
+        REAL ga1 = -lam * y1, ga2 = -lam * y2;
+        /* b0 = b2 = P r, b1 = D r, a1 = (-2c) r, a2 = (1 - alpha) r */
+        REAL dr = (gb0 + gb2) * c.P + gb1 * c.D + ga1 * ((REAL)-2 * c.c) + ga2 * ((REAL)1 - c.alpha);
+        REAL dP = (gb0 + gb2) * c.r;
+        REAL dD = gb1 * c.r + dP / (REAL)2;
+        REAL dc = -dD + ga1 * ((REAL)-2 * c.r);
+        REAL dalpha = -ga2 * c.r - dr * c.r * c.r;
+        REAL ds = dalpha * (REAL)0.5 / c.q;
+        REAL dq = -dalpha * c.alpha / c.q;
+        REAL dw = -c.s * dc + c.c * ds;
+        REAL dfc = dw * BQ_W0_PER_HZ * r_sign(fc);
+        grad[k] += dfc * (m ? (REAL)m[n] : (REAL)1);
+        grad[B + k] += dq * r_sign(Q[k]);
+      }
+    }
+    free(v);
+  }
+  free(y);
+  return loss;
+}

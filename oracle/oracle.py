@@ -60,6 +60,10 @@ def lib(name: str = "liboracle.so") -> ctypes.CDLL:
                  [_f32p, rp, _f32p, _f32p, _f32p] + [_c_int] * 8 + [_c_float] * 3 + [_i32p, _c_int, _c_int]
                  + [_c_float] * 3 + [ctypes.c_void_p, ctypes.c_void_p], ctypes.c_double)
             _sig(L, "dgen_oracle_adam" + sfx, [_f32p, _f32p, _f32p, _f32p, _c_size] + [_c_float] * 4 + [_c_int])
+            vp = ctypes.c_void_p
+            _sig(L, "dgen_oracle_biquad_fwd" + sfx, [_f32p, vp, rp, rp, _c_int, _c_int, _f32p])
+            _sig(L, "dgen_oracle_biquad_step" + sfx, [_f32p, vp, rp, rp, _f32p, _c_int, _c_int, vp, vp],
+                 ctypes.c_double)
         if hasattr(L, "dgen_oracle_noise_stream"):
             _sig(L, "dgen_oracle_noise_stream", [_c_int, _f32p])
             _sig(L, "dgen_oracle_phasor", [_f32p, _c_int, _c_float, _f32p])
@@ -202,3 +206,41 @@ def harmonic_step(cfg, X, P, f0, uv, tgt, grad=True, want_y=False, prec="f64", l
               float(cfg.T), dP.ctypes.data_as(ctypes.c_void_p) if grad else None,
               y.ctypes.data_as(ctypes.c_void_p) if want_y else None)
     return loss, dP, y
+
+
+# -- config 4 -------------------------------------------------------------
+def _mod_ptr(m, T):
+    if m is None:
+        return None, None
+    m = _f(m)
+    if m.shape != (T,):
+        raise ValueError(f"modulation must have shape ({T},)")
+    return m, m.ctypes.data_as(ctypes.c_void_p)
+
+
+def biquad_fwd(x, m, base, Q, prec="f32"):
+    """Biquad bank forward: x [T][B] -> y [T][B]; cutoff[n][k] = base[k]*m[n]
+    (m None: unmodulated)."""
+    x = _f(x)
+    T, B = x.shape
+    dt = np.float32 if prec == "f32" else np.float64
+    m, mp = _mod_ptr(m, T)
+    y = np.zeros((T, B), np.float32)
+    _fn("dgen_oracle_biquad_fwd", prec)(x, mp, np.ascontiguousarray(base, dt), np.ascontiguousarray(Q, dt), B, T, y)
+    return y
+
+
+def biquad_step(x, m, base, Q, tgt, grad=True, want_y=False, prec="f64"):
+    """Config-4 step: forward, loss sum (y - tgt)^2, and (grad) the BPTT
+    gradient [2][B] = (d/d base, d/d Q) in the build's precision.
+    Returns (loss, grad or None, y or None)."""
+    x = _f(x)
+    T, B = x.shape
+    dt = np.float32 if prec == "f32" else np.float64
+    m, mp = _mod_ptr(m, T)
+    g = np.zeros(2 * B, dt) if grad else None
+    y = np.zeros((T, B), np.float32) if want_y else None
+    loss = _fn("dgen_oracle_biquad_step", prec)(
+        x, mp, np.ascontiguousarray(base, dt), np.ascontiguousarray(Q, dt), _f(tgt).reshape(T, B), B, T,
+        y.ctypes.data_as(ctypes.c_void_p) if want_y else None, g.ctypes.data_as(ctypes.c_void_p) if grad else None)
+    return loss, g, y
