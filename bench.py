@@ -17,10 +17,12 @@ Prints ONE JSON line (rank 0):
                 sample of the same workload, timed on this host
 
 With ``--workload biquad`` the same line is printed for BASELINE config 4
-(256-lane x 2^18 tensor biquad bank, forward + loss + BPTT + Adam) instead;
-the default workload is the headline config 3.
+(256-lane x 2^18 tensor biquad bank, forward + loss + BPTT + Adam) and with
+``--workload stft`` for config 2 (8 x 2^20 STFT round trip with per-bin
+gains, forward + loss + gain gradient + Adam) instead; the default workload
+is the headline config 3.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--workload harmonic|biquad]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--workload harmonic|biquad|stft]
 """
 from __future__ import annotations
 
@@ -36,6 +38,7 @@ sys.path.insert(0, os.path.join(ROOT, "dgen-audio_amd"))
 
 METRIC = "fwd+bwd audio samples/sec, batch-32 harmonic synth + MSS loss; % HBM peak"
 BIQUAD_METRIC = "fwd+bwd lane-samples/sec, 256-lane x 2^18 tensor biquad bank with BPTT"
+STFT_METRIC = "fwd+bwd input samples/sec, 8 x 2^20 hop-gated STFT round trip with 513 learnable gains"
 
 
 def log(msg: str) -> None:
@@ -185,6 +188,72 @@ def run_biquad(args) -> dict:
     return out
 
 
+def stft_cpu_baseline(cfg, signals: int, repeats: int) -> dict:
+    """The oracle's fp32 STFT step (forward, loss and gain gradient; built
+    with the reference C backend's -O3 -ffast-math policy) on `signals` of the
+    config-2 signals at full length, single thread."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import ctypes
+
+    import numpy as np
+
+    import oracle as O
+    from dgen_hip import StftConfig
+    sub = StftConfig(**{**cfg.__dict__, "S": signals})
+    x = sub.inputs()
+    fn = O._fn("dgen_oracle_stft_step", "f32", "liboracle_bench.so")
+    dg = np.zeros(cfg.bins, np.float32)
+    times = []
+    for i in range(repeats + 1):
+        t0 = time.perf_counter()
+        fn(x, signals, cfg.T, cfg.N, cfg.H, cfg.window(), cfg.gains(), None, dg.ctypes.data_as(ctypes.c_void_p))
+        dt = time.perf_counter() - t0
+        if i:
+            times.append(dt)
+    times.sort()
+    med = times[len(times) // 2]
+    return {
+        "value": signals * cfg.T / med,
+        "unit": "input samples/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"{signals} of {cfg.S} signals x {cfg.T} samples: radix-2 tensorFFT forward, gains, IFFT, "
+                   f"overlap-add, loss and gain gradient (no Adam); median of {repeats} after 1 warm-up; host "
+                   f"{platform.processor() or platform.machine()}, nproc {os.cpu_count()}"),
+    }
+
+
+def run_stft(args) -> dict:
+    from dgen_hip import StftConfig
+    from dgen_hip.programs import StftSession
+    cfg = StftConfig()
+    log(f"bench: stft session S={cfg.S} T={cfg.T} N={cfg.N} H={cfg.H}")
+    sess = StftSession(cfg, device=0, optimizer=True)
+    try:
+        wall, rows, dom, roof_ms = time_session(sess.rt, sess.program, args)
+        loss = sess.loss()
+    finally:
+        sess.close()
+    ms_per_step = wall * 1e3 / args.steps
+    cpu = None
+    if not args.no_cpu:
+        log("bench: cpu baseline (stft)")
+        cpu = stft_cpu_baseline(cfg, cfg.S, args.cpu_repeats)
+    out = {
+        "metric": STFT_METRIC, "value": cfg.S * cfg.T * args.steps / wall, "unit": "input samples/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (N(0, 0.25) SplitMix64 noise per signal)",
+        "config": {"workload": "config 2: buffer N=1024 hop 256, periodic Hann, FFT, per-bin gains, IFFT, "
+                               "overlapAdd, MSE vs input, gain gradient, Adam", "S": cfg.S, "T": cfg.T, "N": cfg.N,
+                   "H": cfg.H, "parallelism": "single GPU"},
+    }
+    out.update(roofline_fields(rows, dom, roof_ms, ms_per_step))
+    out["loss"] = loss
+    out["cpu_baseline"] = cpu
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
@@ -194,7 +263,7 @@ def main() -> int:
     ap.add_argument("--cpu-lanes", type=int, default=4)
     ap.add_argument("--cpu-repeats", type=int, default=3)
     ap.add_argument("--op-iters", type=int, default=10, help="runs averaged for the dominant kernel's time")
-    ap.add_argument("--workload", choices=("harmonic", "biquad"), default="harmonic")
+    ap.add_argument("--workload", choices=("harmonic", "biquad", "stft"), default="harmonic")
     ap.add_argument("--chunk", type=int, default=256, help="biquad scan chunk length (frames)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -203,6 +272,9 @@ def main() -> int:
         return 2
     if args.workload == "biquad":
         print(json.dumps(run_biquad(args)), flush=True)
+        return 0
+    if args.workload == "stft":
+        print(json.dumps(run_stft(args)), flush=True)
         return 0
 
     print(json.dumps(run_harmonic(args)), flush=True)

@@ -24,12 +24,8 @@
 // - the accumulator spans [a-2047, a+4096); the part left of a belongs to the
 //   previous tile and is added by k_mss_combine, which also forms the
 //   per-frame loss signal.
-// FFT passes follow the Stockham autosort formulation of Govindaraju et al.,
-// "High Performance Discrete Fourier Transforms on Graphics Processors"
-// (SC 2008): pass with radix R and span Ns reads v_r = in[j + r*M/R],
-// twiddles by exp(-+2 pi i r (j mod Ns)/(Ns R)), does an R-point DFT and
-// writes out[(j/Ns)*Ns*R + j mod Ns + r*Ns].
-#include "internal.h"
+// The FFT passes are the shared LDS Stockham transform of fft_lds.h.
+#include "fft_lds.h"
 
 namespace dgen {
 
@@ -51,148 +47,6 @@ struct MssArgs {
   int nsizes, B, T, ntiles;
   float gl, gg;                    // upstream gradient of each window's lin / log sum
 };
-
-struct c2 {
-  float x, y;
-};
-__device__ __forceinline__ c2 cadd(c2 a, c2 b) { return {a.x + b.x, a.y + b.y}; }
-__device__ __forceinline__ c2 csub(c2 a, c2 b) { return {a.x - b.x, a.y - b.y}; }
-__device__ __forceinline__ c2 cmul(c2 a, c2 b) { return {fmaf(a.x, b.x, -a.y * b.y), fmaf(a.x, b.y, a.y * b.x)}; }
-__device__ __forceinline__ c2 cconj(c2 a) { return {a.x, -a.y}; }
-// multiply by -i (forward) or +i (inverse)
-template <bool INV>
-__device__ __forceinline__ c2 mul_mi(c2 a) { return INV ? c2{-a.y, a.x} : c2{a.y, -a.x}; }
-// exp(sgn * 2 pi i * rev), rev in revolutions (v_cos/v_sin take revolutions)
-__device__ __forceinline__ c2 cis(float rev) { return {__builtin_amdgcn_cosf(rev), __builtin_amdgcn_sinf(rev)}; }
-
-template <bool INV>
-__device__ __forceinline__ void dft2(c2* v) {
-  const c2 a = v[0], b = v[1];
-  v[0] = cadd(a, b);
-  v[1] = csub(a, b);
-}
-
-template <bool INV>
-__device__ __forceinline__ void dft4(c2* v) {
-  const c2 s02 = cadd(v[0], v[2]), d02 = csub(v[0], v[2]);
-  const c2 s13 = cadd(v[1], v[3]), d13 = mul_mi<INV>(csub(v[1], v[3]));
-  v[0] = cadd(s02, s13);
-  v[2] = csub(s02, s13);
-  v[1] = cadd(d02, d13);
-  v[3] = csub(d02, d13);
-}
-
-template <bool INV>
-__device__ __forceinline__ void dft8(c2* v) {
-  c2 e[4] = {v[0], v[2], v[4], v[6]};
-  c2 o[4] = {v[1], v[3], v[5], v[7]};
-  dft4<INV>(e);
-  dft4<INV>(o);
-  constexpr float h = 0.70710678118654752f;
-  // o_k *= w8^k, w8 = exp(-+2 pi i / 8)
-  o[1] = INV ? c2{h * (o[1].x - o[1].y), h * (o[1].x + o[1].y)} : c2{h * (o[1].x + o[1].y), h * (o[1].y - o[1].x)};
-  o[2] = mul_mi<INV>(o[2]);
-  o[3] = INV ? c2{-h * (o[3].x + o[3].y), h * (o[3].x - o[3].y)} : c2{h * (o[3].y - o[3].x), -h * (o[3].x + o[3].y)};
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    v[k] = cadd(e[k], o[k]);
-    v[k + 4] = csub(e[k], o[k]);
-  }
-}
-
-template <int R, bool INV>
-__device__ __forceinline__ void dftR(c2* v) {
-  if (R == 8) dft8<INV>(v);
-  else if (R == 4) dft4<INV>(v);
-  else dft2<INV>(v);
-}
-
-// Radix of pass p for an M-point transform: 8s first, then one 4 or 2.
-__host__ __device__ constexpr int pass_radix(int logm, int p) {
-  return (logm - 3 * p) >= 3 ? 8 : (logm - 3 * p == 2 ? 4 : 2);
-}
-__host__ __device__ constexpr int pass_count(int logm) { return (logm + 2) / 3; }
-__host__ __device__ constexpr int pass_span(int logm, int p) {
-  return p == 0 ? 1 : pass_span(logm, p - 1) * pass_radix(logm, p - 1);
-}
-
-// One Stockham pass over this thread's 8 values v (already read): twiddle,
-// R-point DFTs, and the output positions.  j = thread index within the
-// window; butterfly u of the thread is bj = j + u*M/8.
-template <int M, int R, int NS, bool INV>
-__device__ __forceinline__ void pass_compute(c2* v, int j, int* outpos) {
-  constexpr int BPT = 8 / R;
-#pragma unroll
-  for (int u = 0; u < BPT; ++u) {
-    const int bj = j + u * (M / 8);
-    const int k = bj % NS;
-    c2* w = v + u * R;
-    if (NS > 1) {
-      const float rev = (INV ? 1.0f : -1.0f) * (float)k / (float)(NS * R);
-      const c2 t1 = cis(rev);
-      c2 t = t1;
-#pragma unroll
-      for (int r = 1; r < R; ++r) {
-        w[r] = cmul(w[r], t);
-        if (r + 1 < R) t = cmul(t, t1);
-      }
-    }
-    dftR<R, INV>(w);
-    const int base = (bj / NS) * NS * R + k;
-#pragma unroll
-    for (int r = 0; r < R; ++r) outpos[u * R + r] = base + r * NS;
-  }
-}
-
-// Input positions of pass with radix R: element u*R + r <- bj + r*M/R.
-template <int M, int R>
-__device__ __forceinline__ int in_pos(int j, int e) {
-  const int u = e / R, r = e % R;
-  return j + u * (M / 8) + r * (M / R);
-}
-
-// Middle passes 1 .. npass-2 in LDS (in place; a barrier separates each
-// pass's reads from its writes).
-template <int LOGM, int P, bool INV>
-__device__ __forceinline__ void mid_passes(c2* buf, int j, c2* v) {
-  constexpr int M = 1 << LOGM;
-  if constexpr (P < pass_count(LOGM) - 1) {
-    constexpr int R = pass_radix(LOGM, P), NS = pass_span(LOGM, P);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = buf[in_pos<M, R>(j, e)];
-    lds_barrier();
-    int op[8];
-    pass_compute<M, R, NS, INV>(v, j, op);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) buf[op[e]] = v[e];
-    lds_barrier();
-    mid_passes<LOGM, P + 1, INV>(buf, j, v);
-  }
-}
-
-// Full M-point FFT: v holds the first pass's inputs (v[e] = input at
-// in_pos of pass 0); on return v holds the last pass's outputs at positions
-// op[e].  Uses buf (M complex, this window's slot) between passes.
-template <int LOGM, bool INV>
-__device__ __forceinline__ void fft(c2* buf, int j, c2* v, int* op) {
-  constexpr int M = 1 << LOGM;
-  constexpr int NP = pass_count(LOGM);
-  {
-    constexpr int R = pass_radix(LOGM, 0);
-    pass_compute<M, R, 1, INV>(v, j, op);
-  }
-  if constexpr (NP > 1) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) buf[op[e]] = v[e];
-    lds_barrier();
-    mid_passes<LOGM, 1, INV>(buf, j, v);
-    constexpr int RL = pass_radix(LOGM, NP - 1), NSL = pass_span(LOGM, NP - 1);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = buf[in_pos<M, RL>(j, e)];
-    lds_barrier();
-    pass_compute<M, RL, NSL, INV>(v, j, op);
-  }
-}
 
 __device__ __forceinline__ float sgn(float v) { return v > 0.f ? 1.f : (v < 0.f ? -1.f : 0.f); }
 // Hardware square root, natural log (via log2) and reciprocal, each within

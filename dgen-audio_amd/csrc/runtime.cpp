@@ -67,6 +67,8 @@ static Launcher launcher_for(uint32_t k) {
     case DGEN_HIP_K_BIQUAD_FWD: return launch_biquad_fwd;
     case DGEN_HIP_K_BIQUAD_ADJ_CHUNK: return launch_biquad_adj_chunk;
     case DGEN_HIP_K_BIQUAD_BWD: return launch_biquad_bwd;
+    case DGEN_HIP_K_STFT_FWD: return launch_stft_fwd;
+    case DGEN_HIP_K_STFT_BWD: return launch_stft_bwd;
     default: return nullptr;
   }
 }

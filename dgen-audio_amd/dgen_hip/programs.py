@@ -11,7 +11,7 @@ import numpy as np
 
 from . import runtime as R
 from .program import Program
-from .workloads import BiquadConfig, HarmonicConfig, OscBankConfig
+from .workloads import BiquadConfig, HarmonicConfig, OscBankConfig, StftConfig
 
 SEG = 64          # frames per synth segment (checkpoint spacing)
 SLOTS = 4         # control rows a segment may touch
@@ -20,6 +20,7 @@ LDC = 128         # padded control-row stride (K + 2 + NF <= 128)
 SPLITK_ROWS = 1024  # rows per split of the weight-gradient GEMMs
 MSS_TILE = 4096     # output samples per spectral-loss workgroup
 BQ_CHUNK = 256      # frames per biquad scan chunk
+STFT_TILE = 8192    # output samples per STFT forward workgroup
 
 
 def _f32(x) -> float:
@@ -392,6 +393,88 @@ class BiquadSession:
             rt.write("params", params)
             rt.runNoCopy()
             return rt.read("y").reshape(self.cfg.T, self.cfg.B)
+
+    def step(self) -> None:
+        self.rt.runNoCopy()
+
+    def loss(self) -> float:
+        return float(self.rt.read("loss")[0])
+
+    def close(self):
+        self.rt.close()
+
+
+# ------------------------------------------------------------------ config 2
+def stft_windows_per_block(N: int) -> int:
+    """Windows summed by one gain-gradient workgroup (8 rounds of 4096/N)."""
+    return 8 * (4096 // N)
+
+
+def stft_program(cfg: StftConfig, train: bool = True, optimizer: bool = True) -> Program:
+    """x.buffer(N, hop H) * hann -> FFT -> gains -> IFFT -> overlapAdd, loss
+    sum (y - x)^2 / T against the raw input, gradient to the N/2+1 gains
+    (``train``) and one Adam step (``optimizer``)."""
+    S, T, N, H, nb = cfg.S, cfg.T, cfg.N, cfg.H, cfg.bins
+    ntiles = (T + STFT_TILE - 1) // STFT_TILE
+    nwin = (T + H - 1) // H
+    nblk = (nwin + stft_windows_per_block(N) - 1) // stft_windows_per_block(N)
+    f4 = 4.0
+    p = Program(max_frames=T)
+    p.meta.update(cfg=cfg, ntiles=ntiles, nblk=nblk, train=train)
+    x = p.alloc("x", S * T)
+    win = p.alloc("window", N)
+    g = p.alloc("gains", nb)
+    y = p.alloc("y", S * T)
+    lognn = float(np.log2(N))
+    fft_flops = 2.5 * N * lognn  # one real N-point transform (split-radix estimate)
+    windows = float(S * nwin)
+    halo = 1.0 + (N - H) / STFT_TILE  # windows recomputed at tile edges
+    if not train:
+        p.add(R.K_STFT_FWD, [x, win, g, y, -1, -1, S, T, N, H], label="stft_fwd",
+              dispatch=f"tiles {ntiles}x{S}, windows {nwin}/signal", bytes=2.0 * S * T * f4,
+              flops=windows * halo * 2 * fft_flops)
+        p.output_cell = "y"
+        return p
+    dy = p.alloc("dy", S * T)
+    lossp = p.alloc("loss_partials", S * ntiles)
+    loss = p.alloc("loss", 1)
+    gpart = p.alloc("grad_partials", S * nblk * nb)
+    G = p.alloc("grads", nb)
+    ws = p.alloc("colsum_ws", max(_colsum_ws(S * ntiles, 1), _colsum_ws(S * nblk, nb)))
+    p.add(R.K_STFT_FWD, [x, win, g, y, dy, lossp, S, T, N, H], label="stft_fwd",
+          dispatch=f"tiles {ntiles}x{S}, windows {nwin}/signal", bytes=3.0 * S * T * f4,
+          flops=windows * halo * 2 * fft_flops)
+    p.add(R.K_COLSUM, [lossp, loss, S * ntiles, 1, 1, ws], label="loss_sum", dispatch="chunkPartialsReduceToCell",
+          bytes=(S * ntiles + 1) * f4, flops=float(S * ntiles))
+    p.add(R.K_STFT_BWD, [x, win, dy, gpart, S, T, N, H], label="stft_bwd",
+          dispatch=f"window runs {nblk}x{S}", bytes=2.0 * S * T * f4 + S * nblk * nb * f4,
+          flops=windows * (2 * fft_flops + 4 * nb))
+    p.add(R.K_COLSUM, [gpart, G, S * nblk, nb, nb, ws], label="grad_sum", dispatch="chunkPartialsReduceToCell",
+          bytes=(S * nblk * nb + nb) * f4, flops=float(S * nblk * nb))
+    if optimizer:
+        m = p.alloc("adam_m", nb)
+        v = p.alloc("adam_v", nb)
+        tcell = p.alloc("adam_t", 1)
+        p.add(R.K_ADAM, [g, G, m, v, nb, tcell], [cfg.lr, 0.9, 0.999, 1e-8], label="adam",
+              dispatch=f"staticThreads({nb})", bytes=7.0 * nb * f4, flops=12.0 * nb)
+    p.output_cell = "y"
+    return p
+
+
+class StftSession:
+    """Config-2 training runtime: x, the window and the gains staged once;
+    every ``step()`` is forward + loss + gain gradient (+ Adam) in HBM."""
+
+    def __init__(self, cfg: StftConfig, device: int = 0, optimizer: bool = True, gains=None):
+        self.cfg = cfg
+        self.x = cfg.inputs()
+        self.window = cfg.window()
+        self.gains0 = cfg.gains() if gains is None else np.ascontiguousarray(gains, np.float32)
+        self.program = stft_program(cfg, train=True, optimizer=optimizer)
+        self.rt = R.HIPLazyRuntime(self.program, device)
+        self.rt.write("x", self.x)
+        self.rt.write("window", self.window)
+        self.rt.write("gains", self.gains0)
 
     def step(self) -> None:
         self.rt.runNoCopy()

@@ -47,6 +47,8 @@ K_BIQUAD_CARRY = 21
 K_BIQUAD_FWD = 22
 K_BIQUAD_ADJ_CHUNK = 23
 K_BIQUAD_BWD = 24
+K_STFT_FWD = 25
+K_STFT_BWD = 26
 
 KERNEL_NAMES = {v: k[2:].lower() for k, v in globals().items() if k.startswith("K_")}
 

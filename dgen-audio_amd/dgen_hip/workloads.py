@@ -219,3 +219,40 @@ class BiquadConfig:
 
     def target_params(self) -> np.ndarray:
         return np.concatenate([np.full(self.B, self.tgt_fc, np.float32), np.full(self.B, self.tgt_Q, np.float32)])
+
+
+# ---------------------------------------------------------------- config 2
+@dataclass
+class StftConfig:
+    """Hop-gated STFT round trip: S signals x [S][T] of N(0, sigma^2) noise,
+    buffer N / hop H, periodic Hann (DGenLazy hann(N)), FFT, per-bin gains
+    g[N/2+1] (init 1.0) on the one-sided spectrum, IFFT, overlapAdd; loss
+    sum (y - x)^2 / T against the raw input; gradient w.r.t. g."""
+    S: int = 8
+    T: int = 1 << 20
+    N: int = 1024
+    H: int = 256
+    sigma: float = 0.5
+    seed: int = 20
+    lr: float = 1e-3
+
+    @property
+    def bins(self) -> int:
+        return self.N // 2 + 1
+
+    def inputs(self) -> np.ndarray:
+        """x [S][T]: signal s is N(0, sigma^2) from SplitMix64(seed + s)."""
+        x = np.empty((self.S, self.T), np.float32)
+        for s in range(self.S):
+            x[s] = (SplitMix64(self.seed + s).normal(self.T) * self.sigma).astype(np.float32)
+        return x
+
+    def window(self) -> np.ndarray:
+        """hann(N) of Sources/DGenLazy/SpectralTensorOps.swift:42-49, in fp32:
+        scale = 2*Float.pi/Float(N); w[i] = 0.5 - 0.5*cos(scale*Float(i))."""
+        scale = np.float32(np.float32(2.0) * np.float32(math.pi)) / np.float32(self.N)
+        arg = (scale * np.arange(self.N, dtype=np.float32)).astype(np.float32)
+        return (np.float32(0.5) - np.float32(0.5) * np.cos(arg, dtype=np.float32)).astype(np.float32)
+
+    def gains(self) -> np.ndarray:
+        return np.ones(self.bins, np.float32)

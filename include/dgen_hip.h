@@ -201,6 +201,26 @@ enum dgen_hip_kernel {
    * arg: [0]=x [1]=mod [2]=params [3]=y [4]=target [5]=adjoint init
    *      [6]=grad partials [7]=B [8]=T [9]=L */
   DGEN_HIP_K_BIQUAD_BWD = 24,
+
+  /* ---- hop-gated STFT round trip (bufferView -> * window -> tensorFFT ->
+   * per-bin gains -> tensorIFFT -> overlapAdd; HigherOps.swift:738-813,
+   * HigherOps+FFT.swift:16-123, Emit+FFT.swift:6-62).  x, y, dy: [S][T];
+   * window: [N] (N a power of two in [64, 2048]); gains: [N/2+1] applied to
+   * bins k and N-k; hop H in [1, N].
+   *
+   * Forward: y, dL/dy = 2 (y - x)/T and per-8192-sample-tile loss partials
+   * sum (y - x)^2 / T.  arg: [0]=x [1]=window [2]=gains [3]=y or -1
+   * [4]=dy or -1 [5]=loss partials ([S][ceil(T/8192)]) or -1 [6]=S [7]=T
+   * [8]=N [9]=H */
+  DGEN_HIP_K_STFT_FWD = 25,
+
+  /* Gain gradient partials: row (s, b) sums (c_k/N) Re(X_k conj(E_k)) over
+   * a run of 8*4096/N windows of signal s (X: window spectrum, E: spectrum
+   * of dy over the window's outputs, c_k = 1 at k = 0, N/2, else 2); the
+   * rows are reduced by DGEN_HIP_K_COLSUM.  arg: [0]=x [1]=window [2]=dy
+   * [3]=grad partials ([S][nblk][N/2+1], nblk = ceil(ceil(T/H) / (8*4096/N)))
+   * [4]=S [5]=T [6]=N [7]=H */
+  DGEN_HIP_K_STFT_BWD = 26,
 };
 
 /* GEMM epilogues */

@@ -984,3 +984,180 @@ double FN(dgen_oracle_biquad_step)(const float* x, const float* m, const REAL* b
   free(y);
   return loss;
 }
+
+/* ------------------------------------------------------------------------ */
+/* Config 2: hop-gated STFT round trip with learnable per-bin gains.        */
+/* ------------------------------------------------------------------------ */
+
+/* tensorFFT / tensorIFFT (Sources/DGen/HigherOps+FFT.swift:16-123): bit
+ * reversal by reshape/transpose, then log2 N radix-2 stages on blocks
+ * [blocks][2][half] with twiddle w[j] = (cos a, sin a),
+ * a = sign * 2 * Float.pi * Float(j) / Float(2*half) evaluated in Float
+ * (:84-91); t = odd * w, top = even + t, bot = even - t. */
+typedef struct {
+  int n, stages;
+  float* twre; /* [stage half-1 + j], cos a (same for both signs) */
+  float* twim; /* sin a for the positive (inverse) angle */
+  int* bitrev;
+} TfPlan;
+
+static void tf_plan_init(TfPlan* p, int n) {
+  p->n = n;
+  p->stages = 0;
+  while ((1 << p->stages) < n) p->stages++;
+  p->twre = (float*)malloc(sizeof(float) * (n > 1 ? n - 1 : 1));
+  p->twim = (float*)malloc(sizeof(float) * (n > 1 ? n - 1 : 1));
+  p->bitrev = (int*)malloc(sizeof(int) * n);
+  const float two_pi = 2.0f * 3.14159265358979323846f;
+  for (int s = 0; s < p->stages; ++s) {
+    int half = 1 << s;
+    for (int j = 0; j < half; ++j) {
+      float ang = two_pi * (float)j / (float)(2 * half);
+      p->twre[half - 1 + j] = cosf(ang);
+      p->twim[half - 1 + j] = sinf(ang);
+    }
+  }
+  for (int i = 0; i < n; ++i) {
+    int rev = 0, bits = i;
+    for (int s = 0; s < p->stages; ++s) {
+      rev = rev * 2 + (bits & 1);
+      bits >>= 1;
+    }
+    p->bitrev[i] = rev;
+  }
+}
+
+static void tf_plan_free(TfPlan* p) {
+  free(p->twre);
+  free(p->twim);
+  free(p->bitrev);
+}
+
+/* In place; inverse: positive angles and the 1/N scale of tensorIFFT. */
+static void tf_fft(const TfPlan* p, REAL* re, REAL* im, int inverse) {
+  const int n = p->n;
+  for (int i = 0; i < n; ++i) {
+    int r = p->bitrev[i];
+    if (i < r) {
+      REAL a = re[i];
+      re[i] = re[r];
+      re[r] = a;
+      a = im[i];
+      im[i] = im[r];
+      im[r] = a;
+    }
+  }
+  for (int s = 0; s < p->stages; ++s) {
+    const int half = 1 << s, size = 2 * half;
+    for (int b = 0; b < n / size; ++b) {
+      for (int j = 0; j < half; ++j) {
+        const REAL wr = (REAL)p->twre[half - 1 + j];
+        const REAL wi = inverse ? (REAL)p->twim[half - 1 + j] : -(REAL)p->twim[half - 1 + j];
+        const int e = b * size + j, o = e + half;
+        const REAL t_re = re[o] * wr - im[o] * wi;
+        const REAL t_im = re[o] * wi + im[o] * wr;
+        const REAL er = re[e], ei = im[e];
+        re[e] = er + t_re;
+        im[e] = ei + t_im;
+        re[o] = er - t_re;
+        im[o] = ei - t_im;
+      }
+    }
+  }
+  if (inverse) {
+    const REAL sc = (REAL)(1.0f / (float)n);
+    for (int i = 0; i < n; ++i) {
+      re[i] *= sc;
+      im[i] *= sc;
+    }
+  }
+}
+
+void FN(dgen_oracle_tensor_fft)(int n, int inverse, REAL* re, REAL* im) {
+  TfPlan p;
+  tf_plan_init(&p, n);
+  tf_fft(&p, re, im, inverse);
+  tf_plan_free(&p);
+}
+
+/* The gain applied to bin k of the full N-point spectrum: the one-sided
+ * Hermitian reconstruction g0, 2 g_k (0 < k < N/2), g_{N/2}, 0 above. */
+static inline REAL stft_gain(const REAL* g, int N, int k) {
+  if (k == 0 || k == N / 2) return g[k];
+  return k < N / 2 ? (REAL)2 * g[k] : (REAL)0;
+}
+
+/* One config-2 step over S signals x [S][T]:
+ *   hop frames h = 0, H, 2H, ... < T (bufferView's counter fires on 0,
+ *   HigherOps.swift:770-783); window a[i] = win[i] * x[h-N+1+i], zero before
+ *   frame 0 (the ring starts zeroed, HigherOps.swift:738-765);
+ *   X = tensorFFT(a); X'[k] = X[k] * stft_gain(k); z = tensorIFFT(X');
+ *   overlapAdd (Emit+FFT.swift:6-62): y[t] = sum_h z_h[t-h], 0 <= t-h < N.
+ * loss = sum_s sum_t (y - x)^2 / T.  dg (optional, [N/2+1]):
+ *   dL/dg_k = sum_h (c_k/N) Re(X_h[k] conj(E_h[k])), E_h = tensorFFT of the
+ *   output gradient over the window's outputs, c_k = 1 (k = 0, N/2) or 2:
+ * the derivative of the forward above (pinned by finite differences).  The
+ * reference's own overlapAdd backward reads element 0's gradient from frame
+ * h+N instead of h (Emit+FFT.swift:93-97); this function does not follow it. */
+double FN(dgen_oracle_stft_step)(const float* x, int S, int T, int N, int H, const float* win, const REAL* g,
+                                 float* y_out, REAL* dg) {
+  TfPlan p;
+  tf_plan_init(&p, N);
+  REAL* re = (REAL*)malloc(sizeof(REAL) * N);
+  REAL* im = (REAL*)malloc(sizeof(REAL) * N);
+  REAL* y = (REAL*)malloc(sizeof(REAL) * (size_t)T);
+  REAL* ere = dg ? (REAL*)malloc(sizeof(REAL) * N) : NULL;
+  REAL* eim = dg ? (REAL*)malloc(sizeof(REAL) * N) : NULL;
+  if (dg)
+    for (int k = 0; k <= N / 2; ++k) dg[k] = 0;
+  double loss = 0.0;
+  for (int s = 0; s < S; ++s) {
+    const float* xs = x + (size_t)s * T;
+    for (int t = 0; t < T; ++t) y[t] = 0;
+    for (int h = 0; h < T; h += H) {
+      for (int i = 0; i < N; ++i) {
+        const int t = h - N + 1 + i;
+        re[i] = (REAL)win[i] * (t >= 0 ? (REAL)xs[t] : (REAL)0);
+        im[i] = 0;
+      }
+      tf_fft(&p, re, im, 0);
+      for (int k = 0; k < N; ++k) {
+        const REAL gk = stft_gain(g, N, k);
+        re[k] *= gk;
+        im[k] *= gk;
+      }
+      tf_fft(&p, re, im, 1);
+      for (int i = 0; i < N && h + i < T; ++i) y[h + i] += re[i];
+    }
+    for (int t = 0; t < T; ++t) {
+      const REAL d = y[t] - (REAL)xs[t];
+      loss += (double)(d * d) / (double)T;
+      if (y_out) y_out[(size_t)s * T + t] = (float)y[t];
+    }
+    if (!dg) continue;
+    /* dL/dy = 2 (y - x) / T; recompute each window's spectrum */
+    for (int h = 0; h < T; h += H) {
+      for (int i = 0; i < N; ++i) {
+        const int t = h - N + 1 + i;
+        re[i] = (REAL)win[i] * (t >= 0 ? (REAL)xs[t] : (REAL)0);
+        im[i] = 0;
+        const int u = h + i;
+        ere[i] = u < T ? (REAL)2 * (y[u] - (REAL)xs[u]) / (REAL)T : (REAL)0;
+        eim[i] = 0;
+      }
+      tf_fft(&p, re, im, 0);
+      tf_fft(&p, ere, eim, 0);
+      for (int k = 0; k <= N / 2; ++k) {
+        const REAL ck = (k == 0 || k == N / 2) ? (REAL)1 : (REAL)2;
+        dg[k] += ck / (REAL)N * (re[k] * ere[k] + im[k] * eim[k]);
+      }
+    }
+  }
+  free(re);
+  free(im);
+  free(y);
+  free(ere);
+  free(eim);
+  tf_plan_free(&p);
+  return loss;
+}

@@ -64,6 +64,9 @@ def lib(name: str = "liboracle.so") -> ctypes.CDLL:
             _sig(L, "dgen_oracle_biquad_fwd" + sfx, [_f32p, vp, rp, rp, _c_int, _c_int, _f32p])
             _sig(L, "dgen_oracle_biquad_step" + sfx, [_f32p, vp, rp, rp, _f32p, _c_int, _c_int, vp, vp],
                  ctypes.c_double)
+            _sig(L, "dgen_oracle_tensor_fft" + sfx, [_c_int, _c_int, rp, rp])
+            _sig(L, "dgen_oracle_stft_step" + sfx, [_f32p, _c_int, _c_int, _c_int, _c_int, _f32p, rp, vp, vp],
+                 ctypes.c_double)
         if hasattr(L, "dgen_oracle_noise_stream"):
             _sig(L, "dgen_oracle_noise_stream", [_c_int, _f32p])
             _sig(L, "dgen_oracle_phasor", [_f32p, _c_int, _c_float, _f32p])
@@ -244,3 +247,31 @@ def biquad_step(x, m, base, Q, tgt, grad=True, want_y=False, prec="f64"):
         x, mp, np.ascontiguousarray(base, dt), np.ascontiguousarray(Q, dt), _f(tgt).reshape(T, B), B, T,
         y.ctypes.data_as(ctypes.c_void_p) if want_y else None, g.ctypes.data_as(ctypes.c_void_p) if grad else None)
     return loss, g, y
+
+
+# -- config 2 -------------------------------------------------------------
+def tensor_fft(re, im=None, inverse=False, prec="f64"):
+    """tensorFFT (inverse=False) or tensorIFFT without taking the real part
+    (inverse=True, includes the 1/N scale).  Returns (re, im)."""
+    dt = np.float32 if prec == "f32" else np.float64
+    re = np.array(re, dtype=dt)
+    im = np.zeros_like(re) if im is None else np.array(im, dtype=dt)
+    _fn("dgen_oracle_tensor_fft", prec)(len(re), int(inverse), re, im)
+    return re, im
+
+
+def stft_step(x, N, H, win, g, grad=True, want_y=False, prec="f64"):
+    """Config-2 step over x [S][T]: window -> FFT -> gains -> IFFT ->
+    overlap-add; loss sum (y - x)^2 / T.  Returns (loss, dg or None, y or None)."""
+    x = _f(x)
+    S, T = x.shape
+    dt = np.float32 if prec == "f32" else np.float64
+    g = np.ascontiguousarray(g, dtype=dt)
+    if g.shape != (N // 2 + 1,):
+        raise ValueError(f"gains must have shape ({N // 2 + 1},)")
+    dg = np.zeros(N // 2 + 1, dt) if grad else None
+    y = np.zeros((S, T), np.float32) if want_y else None
+    loss = _fn("dgen_oracle_stft_step", prec)(x, S, T, N, H, _f(win), g,
+                                               y.ctypes.data_as(ctypes.c_void_p) if want_y else None,
+                                               dg.ctypes.data_as(ctypes.c_void_p) if grad else None)
+    return loss, dg, y
