@@ -19,10 +19,12 @@ Prints ONE JSON line (rank 0):
 With ``--workload biquad`` the same line is printed for BASELINE config 4
 (256-lane x 2^18 tensor biquad bank, forward + loss + BPTT + Adam) and with
 ``--workload stft`` for config 2 (8 x 2^20 STFT round trip with per-bin
-gains, forward + loss + gain gradient + Adam) instead; the default workload
-is the headline config 3.
+gains, forward + loss + gain gradient + Adam) and with ``--workload
+membrane`` for config 5 (512^2 membrane, 4800 steps, forward + loss + adjoint
++ Adam) instead; the default workload is the headline config 3.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--workload harmonic|biquad|stft]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+                       [--workload harmonic|biquad|stft|membrane]
 """
 from __future__ import annotations
 
@@ -39,6 +41,7 @@ sys.path.insert(0, os.path.join(ROOT, "dgen-audio_amd"))
 METRIC = "fwd+bwd audio samples/sec, batch-32 harmonic synth + MSS loss; % HBM peak"
 BIQUAD_METRIC = "fwd+bwd lane-samples/sec, 256-lane x 2^18 tensor biquad bank with BPTT"
 STFT_METRIC = "fwd+bwd input samples/sec, 8 x 2^20 hop-gated STFT round trip with 513 learnable gains"
+MEMBRANE_METRIC = "fwd+bwd cell-steps/sec, 512^2 membrane x 4800 steps with BPTT to (c2, d)"
 
 
 def log(msg: str) -> None:
@@ -254,6 +257,72 @@ def run_stft(args) -> dict:
     return out
 
 
+def membrane_cpu_baseline(cfg, frames: int, repeats: int) -> dict:
+    """The oracle's fp32 membrane step (forward, loss and adjoint with
+    checkpoint recomputation; -O3 -ffast-math build) on the full grid for
+    the first `frames` frames, single thread."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import ctypes
+
+    import numpy as np
+
+    import oracle as O
+    u0 = cfg.bump()
+    tgt = np.zeros(frames, np.float32)
+    fn = O._fn("dgen_oracle_membrane_step", "f32", "liboracle_bench.so")
+    g = np.zeros(2, np.float32)
+    py, px = cfg.pickup
+    times = []
+    for i in range(repeats + 1):
+        t0 = time.perf_counter()
+        fn(u0, cfg.R, cfg.C, frames, cfg.c2, cfg.d, py, px, tgt, None, g.ctypes.data_as(ctypes.c_void_p))
+        dt = time.perf_counter() - t0
+        if i:
+            times.append(dt)
+    times.sort()
+    med = times[len(times) // 2]
+    return {
+        "value": cfg.R * cfg.C * frames / med,
+        "unit": "cell-steps/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"{cfg.R}x{cfg.C} grid, first {frames} of {cfg.T} frames: sequential fp32 forward, loss and "
+                   f"adjoint with checkpoint recomputation (no Adam); median of {repeats} after 1 warm-up; host "
+                   f"{platform.processor() or platform.machine()}, nproc {os.cpu_count()}"),
+    }
+
+
+def run_membrane(args) -> dict:
+    from dgen_hip import MembraneConfig
+    from dgen_hip.programs import MembraneSession
+    cfg = MembraneConfig()
+    log(f"bench: membrane session {cfg.R}x{cfg.C} T={cfg.T} steps/launch={args.mem_steps}")
+    sess = MembraneSession(cfg, device=0, optimizer=True, steps=args.mem_steps)
+    try:
+        wall, rows, dom, roof_ms = time_session(sess.rt, sess.program, args)
+        loss = sess.loss()
+    finally:
+        sess.close()
+    ms_per_step = wall * 1e3 / args.steps
+    cpu = None
+    if not args.no_cpu:
+        log("bench: cpu baseline (membrane)")
+        cpu = membrane_cpu_baseline(cfg, cfg.T // 10, args.cpu_repeats)
+    out = {
+        "metric": MEMBRANE_METRIC, "value": cfg.R * cfg.C * cfg.T * args.steps / wall, "unit": "cell-steps/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (Gaussian bump at a SplitMix64 position)",
+        "config": {"workload": "config 5: damped 2D wave equation, 3x3 Laplacian, pickup MSE vs (0.25, 0.002) "
+                               "target, adjoint to (c2, d), Adam", "R": cfg.R, "C": cfg.C, "T": cfg.T,
+                   "steps_per_launch": args.mem_steps, "parallelism": "single GPU"},
+    }
+    out.update(roofline_fields(rows, dom, roof_ms, ms_per_step))
+    out["loss"] = loss
+    out["cpu_baseline"] = cpu
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
@@ -263,7 +332,8 @@ def main() -> int:
     ap.add_argument("--cpu-lanes", type=int, default=4)
     ap.add_argument("--cpu-repeats", type=int, default=3)
     ap.add_argument("--op-iters", type=int, default=10, help="runs averaged for the dominant kernel's time")
-    ap.add_argument("--workload", choices=("harmonic", "biquad", "stft"), default="harmonic")
+    ap.add_argument("--workload", choices=("harmonic", "biquad", "stft", "membrane"), default="harmonic")
+    ap.add_argument("--mem-steps", type=int, default=16, help="membrane frames per time-blocked launch")
     ap.add_argument("--chunk", type=int, default=256, help="biquad scan chunk length (frames)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -275,6 +345,9 @@ def main() -> int:
         return 0
     if args.workload == "stft":
         print(json.dumps(run_stft(args)), flush=True)
+        return 0
+    if args.workload == "membrane":
+        print(json.dumps(run_membrane(args)), flush=True)
         return 0
 
     print(json.dumps(run_harmonic(args)), flush=True)

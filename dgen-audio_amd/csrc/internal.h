@@ -91,5 +91,7 @@ int launch_biquad_adj_chunk(const Launch&, const dgen_hip_op&);
 int launch_biquad_bwd(const Launch&, const dgen_hip_op&);
 int launch_stft_fwd(const Launch&, const dgen_hip_op&);
 int launch_stft_bwd(const Launch&, const dgen_hip_op&);
+int launch_membrane_fwd(const Launch&, const dgen_hip_op&);
+int launch_membrane_bwd(const Launch&, const dgen_hip_op&);
 
 }  // namespace dgen

@@ -69,6 +69,8 @@ static Launcher launcher_for(uint32_t k) {
     case DGEN_HIP_K_BIQUAD_BWD: return launch_biquad_bwd;
     case DGEN_HIP_K_STFT_FWD: return launch_stft_fwd;
     case DGEN_HIP_K_STFT_BWD: return launch_stft_bwd;
+    case DGEN_HIP_K_MEMBRANE_FWD: return launch_membrane_fwd;
+    case DGEN_HIP_K_MEMBRANE_BWD: return launch_membrane_bwd;
     default: return nullptr;
   }
 }

@@ -11,7 +11,7 @@ import numpy as np
 
 from . import runtime as R
 from .program import Program
-from .workloads import BiquadConfig, HarmonicConfig, OscBankConfig, StftConfig
+from .workloads import BiquadConfig, HarmonicConfig, MembraneConfig, OscBankConfig, StftConfig
 
 SEG = 64          # frames per synth segment (checkpoint spacing)
 SLOTS = 4         # control rows a segment may touch
@@ -21,6 +21,8 @@ SPLITK_ROWS = 1024  # rows per split of the weight-gradient GEMMs
 MSS_TILE = 4096     # output samples per spectral-loss workgroup
 BQ_CHUNK = 256      # frames per biquad scan chunk
 STFT_TILE = 8192    # output samples per STFT forward workgroup
+MEM_STEPS = 16      # membrane frames per time-blocked launch
+MEM_TILE = 32       # membrane cells per workgroup tile side
 
 
 def _f32(x) -> float:
@@ -475,6 +477,91 @@ class StftSession:
         self.rt.write("x", self.x)
         self.rt.write("window", self.window)
         self.rt.write("gains", self.gains0)
+
+    def step(self) -> None:
+        self.rt.runNoCopy()
+
+    def loss(self) -> float:
+        return float(self.rt.read("loss")[0])
+
+    def close(self):
+        self.rt.close()
+
+
+# ------------------------------------------------------------------ config 5
+def membrane_program(cfg: MembraneConfig, train: bool = True, optimizer: bool = True,
+                     steps: int = MEM_STEPS) -> Program:
+    """Damped 2D wave equation on an R x C grid for T frames with a point
+    pickup; with ``train`` the loss sum (out - target)^2, the discrete adjoint
+    to (c2, d) and (``optimizer``) one Adam step.  Every forward state stays
+    in HBM for the adjoint: (T + 2) fields of R x C floats."""
+    rows, cols, T = cfg.R, cfg.C, cfg.T
+    G = rows * cols
+    py, px = cfg.pickup
+    tiles = ((rows + MEM_TILE - 1) // MEM_TILE) * ((cols + MEM_TILE - 1) // MEM_TILE)
+    f4 = 4.0
+    p = Program(max_frames=T)
+    p.meta.update(cfg=cfg, steps=steps, tiles=tiles, train=train)
+    u0 = p.alloc("u0", G)
+    P = p.alloc("params", 2)
+    out = p.alloc("pickup", T)
+    S = p.alloc("states", (T + 2) * G)
+    cell_steps = float(G) * T
+    # per cell-step: read u_n and u_{n-1}, write u_{n+1} (12 B); ~10 flops
+    p.add(R.K_MEMBRANE_FWD, [S, u0, P, out, rows, cols, T, py, px, steps], label="membrane_fwd",
+          dispatch=f"{(T + steps - 1) // steps} time-blocked launches x {tiles} tiles",
+          bytes=12.0 * cell_steps, flops=10.0 * cell_steps)
+    if not train:
+        p.output_cell = "pickup"
+        return p
+    tgt = p.alloc("target", T)
+    lam = p.alloc("adjoint_fields", 4 * G)
+    gpart = p.alloc("grad_partials", 4 * tiles)  # fp64
+    lt = p.alloc("loss_terms", T)
+    loss = p.alloc("loss", 1)
+    Gc = p.alloc("grads", 2)
+    ws = p.alloc("colsum_ws", _colsum_ws(T, 1))
+    # per cell-step: read lambda_{n+1}, lambda_{n+2}, u_n, u_{n-1}, write lambda_n (20 B); ~14 flops
+    p.add(R.K_MEMBRANE_BWD, [S, P, out, tgt, lam, gpart, lt, rows, cols, T, py, px, steps, Gc], label="membrane_bwd",
+          dispatch=f"{T // steps + 1} time-blocked adjoint launches x {tiles} tiles",
+          bytes=20.0 * cell_steps, flops=14.0 * cell_steps)
+    p.add(R.K_COLSUM, [lt, loss, T, 1, 1, ws], label="loss_sum", dispatch="chunkPartialsReduceToCell",
+          bytes=(T + 1) * f4, flops=float(T))
+    if optimizer:
+        m = p.alloc("adam_m", 2)
+        v = p.alloc("adam_v", 2)
+        tcell = p.alloc("adam_t", 1)
+        p.add(R.K_ADAM, [P, Gc, m, v, 2, tcell], [cfg.lr, 0.9, 0.999, 1e-8], label="adam",
+              dispatch="staticThreads(2)", bytes=14.0 * f4, flops=24.0)
+    p.output_cell = "pickup"
+    return p
+
+
+class MembraneSession:
+    """Config-5 training runtime: the target pickup series is rendered once
+    with (tgt_c2, tgt_d); every ``step()`` is forward + loss + adjoint
+    (+ Adam) with all states in HBM."""
+
+    def __init__(self, cfg: MembraneConfig, device: int = 0, optimizer: bool = True, steps: int = MEM_STEPS,
+                 target=None):
+        self.cfg = cfg
+        self.u0 = cfg.bump()
+        self.params0 = cfg.params()
+        if target is None:
+            target = self.render(cfg.target_params(), device, steps)
+        self.target = np.ascontiguousarray(target, np.float32).reshape(cfg.T)
+        self.program = membrane_program(cfg, train=True, optimizer=optimizer, steps=steps)
+        self.rt = R.HIPLazyRuntime(self.program, device)
+        self.rt.write("u0", self.u0)
+        self.rt.write("params", self.params0)
+        self.rt.write("target", self.target)
+
+    def render(self, params, device: int = 0, steps: int = MEM_STEPS) -> np.ndarray:
+        with R.HIPLazyRuntime(membrane_program(self.cfg, train=False, steps=steps), device) as rt:
+            rt.write("u0", self.u0)
+            rt.write("params", params)
+            rt.runNoCopy()
+            return rt.read("pickup")
 
     def step(self) -> None:
         self.rt.runNoCopy()

@@ -49,6 +49,8 @@ K_BIQUAD_ADJ_CHUNK = 23
 K_BIQUAD_BWD = 24
 K_STFT_FWD = 25
 K_STFT_BWD = 26
+K_MEMBRANE_FWD = 27
+K_MEMBRANE_BWD = 28
 
 KERNEL_NAMES = {v: k[2:].lower() for k, v in globals().items() if k.startswith("K_")}
 

@@ -256,3 +256,45 @@ class StftConfig:
 
     def gains(self) -> np.ndarray:
         return np.ones(self.bins, np.float32)
+
+
+# ---------------------------------------------------------------- config 5
+@dataclass
+class MembraneConfig:
+    """2D membrane: R x C grid, u_{t+1} = 2u_t - u_{t-1} + c2 L(u_t)
+    - d (u_t - u_{t-1}) with the 3x3 zero-padded Laplacian, Gaussian-bump
+    initial displacement (u_{-1} = u_0), T steps, pickup out[n] = u_{n+1}[p];
+    loss sum (out - out_target)^2 against the same model with (tgt_c2, tgt_d);
+    gradients w.r.t. (c2, d)."""
+    R: int = 512
+    C: int = 512
+    T: int = 4800
+    c2: float = 0.2
+    d: float = 0.001
+    tgt_c2: float = 0.25
+    tgt_d: float = 0.002
+    sigma: float = 4.0
+    seed: int = 50
+    lr: float = 1e-3
+
+    @property
+    def pickup(self) -> tuple:
+        return (self.R // 2, (self.C * 300) // 512)
+
+    def bump(self) -> np.ndarray:
+        """u_0: unit Gaussian (sigma cells) centred at a SplitMix64(seed)
+        position at least R/8 (C/8) cells inside the edges."""
+        rng = SplitMix64(self.seed)
+        my, mx = self.R // 8, self.C // 8
+        cy = my + int(rng.next() % max(1, self.R - 2 * my))
+        cx = mx + int(rng.next() % max(1, self.C - 2 * mx))
+        y = np.arange(self.R, dtype=np.float64)[:, None]
+        x = np.arange(self.C, dtype=np.float64)[None, :]
+        r2 = (y - cy) ** 2 + (x - cx) ** 2
+        return np.exp(-r2 / (2.0 * self.sigma ** 2)).astype(np.float32)
+
+    def params(self) -> np.ndarray:
+        return np.array([self.c2, self.d], np.float32)
+
+    def target_params(self) -> np.ndarray:
+        return np.array([self.tgt_c2, self.tgt_d], np.float32)

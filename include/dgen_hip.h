@@ -221,6 +221,26 @@ enum dgen_hip_kernel {
    * [3]=grad partials ([S][nblk][N/2+1], nblk = ceil(ceil(T/H) / (8*4096/N)))
    * [4]=S [5]=T [6]=N [7]=H */
   DGEN_HIP_K_STFT_BWD = 26,
+
+  /* ---- 2D membrane (Examples/BendingMetal/main.swift:96-169 idiom):
+   * u_{n+1} = 2u_n - u_{n-1} + c2 L(u_n) - d (u_n - u_{n-1}), L the 3x3
+   * zero-padded Laplacian, u_{-1} = u_0; pickup out[n] = u_{n+1}[py][px].
+   * states: [(T+2)][R][C] with S[0] = u_{-1}, S[1] = u_0, S[n+1] = u_n;
+   * params: (c2, d).  Time-blocked: one launch per `steps` (<= 16) frames.
+   *
+   * Forward: copies u0 into S[0], S[1], then fills S and the pickup.
+   * arg: [0]=states [1]=u0 ([R][C]) [2]=params [3]=pickup ([T]) [4]=R [5]=C
+   *      [6]=T [7]=py [8]=px [9]=steps per launch */
+  DGEN_HIP_K_MEMBRANE_FWD = 27,
+
+  /* Discrete adjoint of the forward against a target pickup series: the
+   * gradient (d/d c2, d/d d), accumulated in fp64 per tile
+   * ([ceil(R/32)*ceil(C/32)][2] doubles, even cell offset) and summed in
+   * tile order, and the loss terms (out - tgt)^2 ([T]).
+   * arg: [0]=states [1]=params [2]=pickup [3]=target ([T]) [4]=adjoint
+   *      boundary fields ([4][R][C]) [5]=grad partials [6]=loss terms
+   *      [7]=R [8]=C [9]=T [10]=py [11]=px [12]=steps per launch [13]=grads */
+  DGEN_HIP_K_MEMBRANE_BWD = 28,
 };
 
 /* GEMM epilogues */

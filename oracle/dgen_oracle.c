@@ -1161,3 +1161,122 @@ double FN(dgen_oracle_stft_step)(const float* x, int S, int T, int N, int H, con
   tf_plan_free(&p);
   return loss;
 }
+
+/* ------------------------------------------------------------------------ */
+/* Config 5: 2D membrane (damped wave equation on an R x C grid).           */
+/* ------------------------------------------------------------------------ */
+
+/* 3x3 Laplacian [[0,1,0],[1,-4,1],[0,1,0]] as conv2d "same" with zero
+ * padding (Sources/DGen/Emit+Tensor.swift:173-205; the pad + conv2d form of
+ * Examples/BendingMetal/main.swift:114-121 gives the same values): the taps
+ * accumulate ky-major from 0; zero taps add nothing. */
+static inline REAL mem_lap(const REAL* u, int R, int C, int y, int x) {
+  const size_t i = (size_t)y * C + x;
+  REAL n = y > 0 ? u[i - C] : (REAL)0;
+  REAL w = x > 0 ? u[i - 1] : (REAL)0;
+  REAL e = x + 1 < C ? u[i + 1] : (REAL)0;
+  REAL s = y + 1 < R ? u[i + C] : (REAL)0;
+  return (((n + w) + u[i] * (REAL)-4) + e) + s;
+}
+
+/* u_next = 2 u - u1 + c2 L(u) - d (u - u1), evaluated left to right as the
+ * graph states it: ((u*2 - u1) + L*c2) - (u - u1)*d. */
+static void mem_step(const REAL* u, const REAL* u1, REAL* un, int R, int C, REAL c2, REAL d) {
+  for (int y = 0; y < R; ++y)
+    for (int x = 0; x < C; ++x) {
+      const size_t i = (size_t)y * C + x;
+      const REAL b = u[i] * (REAL)2 - u1[i];
+      const REAL c = mem_lap(u, R, C, y, x) * c2;
+      const REAL g = (u[i] - u1[i]) * d;
+      un[i] = (b + c) - g;
+    }
+}
+
+/* One config-5 training step in this build's precision.  The state history
+ * starts at u_{-1} = u_0 = u0 (TensorHistory initial data); frame n reads
+ * u_n, u_{n-1} and writes u_{n+1}; the pickup output is out[n] = u_{n+1}[p]
+ * (Examples/BendingMetal/main.swift:96-169).  loss = sum_n (out[n] - tgt[n])^2.
+ *
+ * grad (optional, [2] = d/d c2, d/d d): discrete adjoint.  With L symmetric,
+ *   lambda_n = g_n + (2-d) lambda_{n+1} + c2 L lambda_{n+1} - (1-d) lambda_{n+2},
+ *   g_n = 2 (out[n-1] - tgt[n-1]) at p, lambda_{T+1} = lambda_{T+2} = 0;
+ *   dL/dc2 = sum_n <lambda_n, L u_{n-1}>, dL/dd = sum_n <lambda_n, u_{n-2} - u_{n-1}>
+ * for n = T..1.  The states are recomputed from checkpoints every `ck`
+ * steps (memory ~ (T/ck + ck) fields). */
+double FN(dgen_oracle_membrane_step)(const float* u0, int R, int C, int T, REAL c2, REAL d, int py, int px,
+                                     const float* tgt, float* out, REAL* grad) {
+  const size_t G = (size_t)R * C;
+  const size_t ip = (size_t)py * C + px;
+  REAL* a = (REAL*)malloc(sizeof(REAL) * G);
+  REAL* b = (REAL*)malloc(sizeof(REAL) * G);
+  REAL* cbuf = (REAL*)malloc(sizeof(REAL) * G);
+  for (size_t i = 0; i < G; ++i) a[i] = b[i] = (REAL)u0[i];
+  int ck = 1;
+  while ((long)ck * ck < T) ++ck;
+  const int nck = (T + ck - 1) / ck + 1;
+  REAL* cks = grad ? (REAL*)malloc(sizeof(REAL) * G * 2 * nck) : NULL; /* (u_{m-1}, u_m) at m = j*ck */
+  REAL* o = (REAL*)malloc(sizeof(REAL) * (T > 0 ? T : 1));
+  REAL *um1 = a, *u = b, *un = cbuf;  /* u_{n-1}, u_n, u_{n+1} */
+  for (int n = 0; n < T; ++n) {
+    if (grad && n % ck == 0) {
+      memcpy(cks + G * 2 * (n / ck), um1, sizeof(REAL) * G);
+      memcpy(cks + G * (2 * (n / ck) + 1), u, sizeof(REAL) * G);
+    }
+    mem_step(u, um1, un, R, C, c2, d);
+    o[n] = un[ip];
+    REAL* t = um1;
+    um1 = u;
+    u = un;
+    un = t;
+  }
+  double loss = 0.0;
+  for (int n = 0; n < T; ++n) {
+    if (out) out[n] = (float)o[n];
+    const REAL e = o[n] - (REAL)tgt[n];
+    loss += (double)(e * e);
+  }
+  if (grad) {
+    grad[0] = grad[1] = 0;
+    REAL* l1 = (REAL*)calloc(G, sizeof(REAL)); /* lambda_{n+1} */
+    REAL* l2 = (REAL*)calloc(G, sizeof(REAL)); /* lambda_{n+2} */
+    REAL* seg = (REAL*)malloc(sizeof(REAL) * G * (ck + 1));  /* u_{m-1} .. u_{m+ck-1} */
+    for (int m = ((T - 1) / ck) * ck; m >= 0; m -= ck) {
+      const int len = (m + ck <= T ? ck : T - m);
+      /* states u_{m-1} .. u_{m+len-1} of this segment */
+      memcpy(seg, cks + G * 2 * (m / ck), sizeof(REAL) * G);
+      memcpy(seg + G, cks + G * (2 * (m / ck) + 1), sizeof(REAL) * G);
+      for (int q = 1; q < len; ++q) mem_step(seg + G * q, seg + G * (q - 1), seg + G * (q + 1), R, C, c2, d);
+      /* lambda_n for n = m+len .. m+1 needs u_{n-1} = seg[n-m], u_{n-2} = seg[n-1-m] */
+      for (int n = m + len; n >= m + 1; --n) {
+        const REAL* v1 = seg + G * (size_t)(n - m);
+        const REAL* v2 = seg + G * (size_t)(n - 1 - m);
+        for (int y = 0; y < R; ++y)
+          for (int x = 0; x < C; ++x) {
+            const size_t i = (size_t)y * C + x;
+            REAL lam = ((REAL)2 - d) * l1[i] + c2 * mem_lap(l1, R, C, y, x) - ((REAL)1 - d) * l2[i];
+            if (i == ip) lam += (REAL)2 * (o[n - 1] - (REAL)tgt[n - 1]);
+            cbuf[i] = lam;
+          }
+        for (int y = 0; y < R; ++y)
+          for (int x = 0; x < C; ++x) {
+            const size_t i = (size_t)y * C + x;
+            grad[0] += cbuf[i] * mem_lap(v1, R, C, y, x);
+            grad[1] += cbuf[i] * (v2[i] - v1[i]);
+          }
+        REAL* t = l2;
+        l2 = l1;
+        l1 = cbuf;
+        cbuf = t;
+      }
+    }
+    free(l1);
+    free(l2);
+    free(seg);
+  }
+  free(a);
+  free(b);
+  free(cbuf);
+  free(cks);
+  free(o);
+  return loss;
+}

@@ -65,6 +65,9 @@ def lib(name: str = "liboracle.so") -> ctypes.CDLL:
             _sig(L, "dgen_oracle_biquad_step" + sfx, [_f32p, vp, rp, rp, _f32p, _c_int, _c_int, vp, vp],
                  ctypes.c_double)
             _sig(L, "dgen_oracle_tensor_fft" + sfx, [_c_int, _c_int, rp, rp])
+            rs = ctypes.c_float if sfx == "_f32" else ctypes.c_double
+            _sig(L, "dgen_oracle_membrane_step" + sfx, [_f32p, _c_int, _c_int, _c_int, rs, rs, _c_int, _c_int, _f32p,
+                                                        vp, vp], ctypes.c_double)
             _sig(L, "dgen_oracle_stft_step" + sfx, [_f32p, _c_int, _c_int, _c_int, _c_int, _f32p, rp, vp, vp],
                  ctypes.c_double)
         if hasattr(L, "dgen_oracle_noise_stream"):
@@ -275,3 +278,20 @@ def stft_step(x, N, H, win, g, grad=True, want_y=False, prec="f64"):
                                                y.ctypes.data_as(ctypes.c_void_p) if want_y else None,
                                                dg.ctypes.data_as(ctypes.c_void_p) if grad else None)
     return loss, dg, y
+
+
+# -- config 5 -------------------------------------------------------------
+def membrane_step(u0, T, c2, d, pickup, tgt, grad=True, want_out=False, prec="f64"):
+    """Config-5 step on the grid u0 [R][C]: T steps of the damped wave
+    equation, pickup out[n] = u_{n+1}[p], loss sum (out - tgt)^2.
+    Returns (loss, grad [2] = (d/dc2, d/dd) or None, out [T] or None)."""
+    u0 = _f(u0)
+    R, C = u0.shape
+    dt = np.float32 if prec == "f32" else np.float64
+    g = np.zeros(2, dt) if grad else None
+    out = np.zeros(T, np.float32) if want_out else None
+    loss = _fn("dgen_oracle_membrane_step", prec)(
+        u0, R, C, T, float(c2), float(d), int(pickup[0]), int(pickup[1]), _f(tgt).reshape(-1)[:T].copy()
+        if tgt is not None else np.zeros(T, np.float32),
+        out.ctypes.data_as(ctypes.c_void_p) if want_out else None, g.ctypes.data_as(ctypes.c_void_p) if grad else None)
+    return loss, g, out
