@@ -35,11 +35,29 @@ __device__ __forceinline__ float4 load4(const float* __restrict__ p, int valid) 
   return v;
 }
 
+// tanh within a few ulp at a fraction of the libm cost: for |x| < 0.55 the
+// odd Taylor series to x^15 (truncation below 5e-8 relative; the series
+// converges for |x| < pi/2), otherwise 1 - 2/(e^{2|x|} + 1) on the hardware
+// exp2 and reciprocal (no cancellation there: 2/(e^{2|x|}+1) <= 0.5).
+__device__ __forceinline__ float fast_tanh(float x) {
+  const float ax = fabsf(x), x2 = x * x;
+  float p = fmaf(x2, -929569.0f / 638512875.0f, 21844.0f / 6081075.0f);
+  p = fmaf(x2, p, -1382.0f / 155925.0f);
+  p = fmaf(x2, p, 62.0f / 2835.0f);
+  p = fmaf(x2, p, -17.0f / 315.0f);
+  p = fmaf(x2, p, 2.0f / 15.0f);
+  p = fmaf(x2, p, -1.0f / 3.0f);
+  const float small = fmaf(x * x2, p, x);
+  const float e = __builtin_amdgcn_exp2f(ax * 2.8853900817779268f);  // e^{2|x|}
+  const float big = 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
+  return ax < 0.55f ? small : copysignf(big, x);
+}
+
 __device__ __forceinline__ float apply_epi(int epi, float acc, int row, int col, const float* __restrict__ bias,
                                            const float* __restrict__ aux, int ldaux) {
   switch (epi) {
     case EPI_BIAS: return acc + bias[col];
-    case EPI_BIAS_TANH: return tanhf(acc + bias[col]);
+    case EPI_BIAS_TANH: return fast_tanh(acc + bias[col]);
     case EPI_TANH_GRAD: {
       float h = aux[(size_t)row * ldaux + col];
       return acc * (1.f - h * h);
@@ -61,7 +79,20 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const
   const int wave = tid >> 6, lane = tid & 63;
   const int h = lane >> 5, r = lane & 31;
   const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  // Workgroups are dealt to the 8 XCDs round-robin by launch order; renumber
+  // them so that each XCD runs a contiguous run of tiles (the N tiles of one
+  // row block share their A rows in that XCD's L2).
+  int bx = blockIdx.x, by = blockIdx.y;
+  {
+    const int tiles = gridDim.x * gridDim.y;
+    if (tiles % 8 == 0) {
+      const int hw = blockIdx.y * gridDim.x + blockIdx.x;
+      const int lg = (hw % 8) * (tiles / 8) + hw / 8;
+      bx = lg % gridDim.x;
+      by = lg / gridDim.x;
+    }
+  }
+  const int m0 = by * BM, n0 = bx * BN;
   const int kbeg = blockIdx.z * kchunk;
   const int kend = min(K, kbeg + kchunk);
 
@@ -169,21 +200,55 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const
 
   // Accumulator layout of a 32x32 MFMA block: register v of lane l holds
   // row 8*(v/4) + 4*(l/32) + v%4, column l%32.
+  if (!ws && epi == EPI_TANH_GRAD) {
+    // issue all 64 loads of the tanh outputs before using any
+    float hv[2][2][16];
 #pragma unroll
-  for (int ti = 0; ti < 2; ++ti)
+    for (int ti = 0; ti < 2; ++ti)
 #pragma unroll
-    for (int tj = 0; tj < 2; ++tj)
+      for (int tj = 0; tj < 2; ++tj)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int row = m0 + wm + ti * 32 + (v >> 2) * 8 + h * 4 + (v & 3);
+        for (int v = 0; v < 16; ++v) {
+          const int row = m0 + wm + ti * 32 + (v >> 2) * 8 + h * 4 + (v & 3);
+          const int col = n0 + wn + tj * 32 + r;
+          hv[ti][tj][v] = (row < M && col < N) ? aux[(size_t)row * ldaux + col] : 0.f;
+        }
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+      for (int tj = 0; tj < 2; ++tj)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int row = m0 + wm + ti * 32 + (v >> 2) * 8 + h * 4 + (v & 3);
+          const int col = n0 + wn + tj * 32 + r;
+          const float hh = hv[ti][tj][v];
+          if (row < M && col < N) C[(size_t)row * ldc + col] = acc[ti][tj][v] * (1.f - hh * hh);
+        }
+    return;
+  }
+  // one uniform branch per epilogue kind, then a straight store loop
+  auto store_all = [&](auto f) {
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+      for (int tj = 0; tj < 2; ++tj) {
         const int col = n0 + wn + tj * 32 + r;
-        if (row < M && col < N) {
-          if (ws)
-            ws[((size_t)blockIdx.z * M + row) * N + col] = acc[ti][tj][v];
-          else
-            C[(size_t)row * ldc + col] = apply_epi(epi, acc[ti][tj][v], row, col, bias, aux, ldaux);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int row = m0 + wm + ti * 32 + (v >> 2) * 8 + h * 4 + (v & 3);
+          if (row < M && col < N) f(row, col, acc[ti][tj][v]);
         }
       }
+  };
+  if (ws) {
+    store_all([&](int row, int col, float a) { ws[((size_t)blockIdx.z * M + row) * N + col] = a; });
+  } else if (epi == EPI_BIAS_TANH) {
+    store_all([&](int row, int col, float a) { C[(size_t)row * ldc + col] = fast_tanh(a + bias[col]); });
+  } else if (epi == EPI_BIAS) {
+    store_all([&](int row, int col, float a) { C[(size_t)row * ldc + col] = a + bias[col]; });
+  } else {
+    store_all([&](int row, int col, float a) { C[(size_t)row * ldc + col] = a; });
+  }
 }
 
 __global__ void k_splitk_reduce(const float* __restrict__ ws, float* __restrict__ C, int M, int N, int ldc, int splits,

@@ -18,6 +18,7 @@ SLOTS = 4         # control rows a segment may touch
 ROW_ENTRIES = 8   # (segment, slot) entries per control row
 LDC = 128         # padded control-row stride (K + 2 + NF <= 128)
 SPLITK_ROWS = 1024  # rows per split of the weight-gradient GEMMs
+SPLITK_ROWS_HEADS = 512  # the heads' weight gradient has one 128-wide column tile: split finer to fill the chip
 MSS_TILE = 4096     # output samples per spectral-loss workgroup
 BQ_CHUNK = 256      # frames per biquad scan chunk
 STFT_TILE = 8192    # output samples per STFT forward workgroup
@@ -198,13 +199,14 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
 
     G = p.alloc("grads", npar)
     split = max(1, (M + SPLITK_ROWS - 1) // SPLITK_ROWS)
-    ws_gemm = p.alloc("splitk_ws", split * Hd * max(Hd, NC))
+    split_h = max(1, (M + SPLITK_ROWS_HEADS - 1) // SPLITK_ROWS_HEADS)
+    ws_gemm = p.alloc("splitk_ws", max(split * Hd * Hd, split_h * Hd * NC))
     chunks = min(256, max(1, M // 32))
     ws_col = p.alloc("colsum_ws", chunks * (din + 1) * max(Hd, NC))
     gW = [(G + (w - P), G + (b - P)) for (w, b) in woff]
     gWh, gbh = G + (Wh - P), G + (bh - P)
     # heads: dWh = H_L^T dZ ; dbh = colsum(dZ) ; dH_L = (dZ Wh^T) * (1 - H_L^2)
-    p.add(R.K_GEMM, [Hs[-1], dZ, gWh, Hd, NC, M, Hd, LDC, NC, 1, 0, R.EPI_NONE, -1, -1, 0, split, ws_gemm],
+    p.add(R.K_GEMM, [Hs[-1], dZ, gWh, Hd, NC, M, Hd, LDC, NC, 1, 0, R.EPI_NONE, -1, -1, 0, split_h, ws_gemm],
           label="dW_heads", dispatch="gemmChunkPartials", bytes=(M * Hd + M * NC + Hd * NC) * f4,
           flops=2.0 * M * Hd * NC, bound="mfma")
     p.add(R.K_COLSUM, [dZ, gbh, M, NC, LDC, ws_col], label="db_heads", dispatch="chunkPartialsReduceToCell",
