@@ -566,20 +566,61 @@ struct SlotAcc {
   }
 };
 
+// Column passes of the backward.  Pass 1 runs the phase chain (lane =
+// harmonic k, the forward's chain bit for bit) and accumulates harmonic
+// column k in the same loop, so no per-frame sine table is staged; lanes
+// k >= K take the non-harmonic columns lane + 64.  Pass 2 takes columns
+// K + lane.  Together they cover every column c < K + 128 >= NC.
+template <bool FAST>
+__device__ __forceinline__ void bwd_harmonic_pass(const SynthArgs& a, const SegLds& L, SlotAcc& acc, int lane,
+                                                  int nt, float ph, int nidx_spare) {
+  const float kf = (float)(lane + 1);
+  const float nyq = a.sr * 0.5f;
+  const bool harm = lane < a.K;
+  const int n = FAST ? kSeg : nt;
+  for (int i0 = 0; i0 < n; i0 += kBlk) {
+    FrameRec r[kBlk];
+    float hs[kBlk], cf[kBlk], ex[kBlk];
+#pragma unroll
+    for (int j = 0; j < kBlk; ++j) {
+      const int i = i0 + j;
+      r[j] = L.fr[i];
+      hs[j] = L.hs[i];
+      cf[j] = L.coef[i];
+      ex[j] = L.dfl[i] * L.noise[i + nidx_spare];
+    }
+#pragma unroll
+    for (int j = 0; j < kBlk; ++j) {
+      const int i = i0 + j;
+      if (!FAST && i >= nt) break;
+      const float freq = kf * r[j].f0;
+      float inc;
+      if (FAST) {
+        const float q0 = freq * a.rsr;
+        inc = fmaf(fmaf(-q0, a.sr, freq), a.rsr, q0);
+      } else {
+        inc = div_sr(freq, a.sr, a.rsr);
+      }
+      const float p = ph;
+      ph = FAST ? __builtin_amdgcn_fractf(ph + inc) : phasor_wrap(ph + inc);
+      const float sv = sin2pi(p);
+      const float dm = harm ? (freq < nyq ? (sv - hs[j]) * cf[j] : 0.0f) : ex[j];
+      acc.add(r[j].slots, r[j].omf * dm, r[j].frac * dm);
+    }
+  }
+}
+
 __global__ __launch_bounds__(64 * kWavesBwd) void k_synth_bwd(SynthArgs a, const float* __restrict__ dy,
                                                               const float* __restrict__ aux,
                                                               float* __restrict__ part) {
   __shared__ SegLds lds[kWavesBwd];
-  __shared__ float s_s[kWavesBwd][kSeg * kLd];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int nseg = (a.T + kSeg - 1) / kSeg;
   const int s = blockIdx.x * kWavesBwd + wave, b = blockIdx.y;
   if (s >= nseg) return;
   SegLds& L = lds[wave];
-  float* sn = s_s[wave];
   const int t0 = s * kSeg, nt = min(kSeg, a.T - t0);
   const int fast = stage_segment(a, L, s, b, lane, nt, false);
-  chain_pass<false, true>(a, L, nullptr, sn, s, b, lane, nt, fast);
   {
     float hs = 0.f, coef = 0.f, dg = 0.f, dng = 0.f, dfl = 0.f;
     if (lane < nt) {
@@ -607,32 +648,38 @@ __global__ __launch_bounds__(64 * kWavesBwd) void k_synth_bwd(SynthArgs a, const
   wave_sync();
 
   const int NC = a.K + 2 + a.NF;
-  const float nyq = a.sr * 0.5f;
   float* out = part + ((size_t)b * nseg + s) * kSlots * a.ldc;
-  for (int c0 = 0; c0 < NC; c0 += 64) {
-    const int c = c0 + lane;
-    const bool harm = c < a.K;
-    const float kf = (float)(c + 1);
-    const int q = c - a.K;  // 0: gain, 1: noise gain, q >= 2: tap q-2
+  {
+    // pass 1: harmonic k = lane, or (lane >= K) the tap column lane + 64
+    const int c = lane < a.K ? lane : lane + 64;
+    const int nidx = lane < a.K ? 0 : c - a.K - 2;
+    const float ph = a.ckpt[((size_t)s * a.B + b) * a.K + (lane < a.K ? lane : 0)];
+    SlotAcc acc;
+    if (fast)
+      bwd_harmonic_pass<true>(a, L, acc, lane, nt, ph, nidx);
+    else
+      bwd_harmonic_pass<false>(a, L, acc, lane, nt, ph, nidx);
+    if (c < NC) acc.store(out, a.ldc, c);
+  }
+  {
+    // pass 2: column K + lane (gain, noise gain, taps 0..61)
+    const int c = a.K + lane;
+    const int q = lane;  // 0: gain, 1: noise gain, q >= 2: tap q-2
     const int nidx = max(q - 2, 0);
     SlotAcc acc;
     for (int i0 = 0; i0 < nt; i0 += kBlk) {
       FrameRec r[kBlk];
-      float sv[kBlk], hs[kBlk], cf[kBlk], ex[kBlk];
+      float ex[kBlk];
 #pragma unroll
       for (int j = 0; j < kBlk; ++j) {
         const int i = i0 + j;
         r[j] = L.fr[i];
-        sv[j] = sn[i * kLd + lane];
-        hs[j] = L.hs[i];
-        cf[j] = L.coef[i];
         ex[j] = q == 0 ? L.dg[i] : (q == 1 ? L.dng[i] : L.dfl[i] * L.noise[i + nidx]);
       }
 #pragma unroll
       for (int j = 0; j < kBlk; ++j) {
         if (i0 + j >= nt) break;
-        const float dm = harm ? (kf * r[j].f0 < nyq ? (sv[j] - hs[j]) * cf[j] : 0.0f) : ex[j];
-        acc.add(r[j].slots, r[j].omf * dm, r[j].frac * dm);
+        acc.add(r[j].slots, r[j].omf * ex[j], r[j].frac * ex[j]);
       }
     }
     if (c < NC) acc.store(out, a.ldc, c);
