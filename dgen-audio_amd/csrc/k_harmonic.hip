@@ -36,7 +36,6 @@ constexpr int kSeg = 64;      // frames per segment = checkpoint spacing
 constexpr int kMaxK = 64;     // harmonics (one lane per harmonic)
 constexpr int kMaxNC = 128;   // control columns
 constexpr int kSlots = 4;     // distinct control rows a segment may touch
-constexpr int kLd = kSeg + 1; // LDS row stride of [frame][harmonic] tiles (bank-conflict free)
 constexpr int kMaxNoise = kSeg + kMaxNC;  // noise window of one segment
 
 __device__ __forceinline__ float phasor_wrap(float next) {
@@ -400,64 +399,9 @@ __device__ __forceinline__ int below_nyquist(float f0, float nyq, int K) {
   return lo;
 }
 
-// Chain pass of one segment: lane = harmonic.  For every frame i writes
-// sin(2 pi phase) into sn[i][k] (SN) and sin * masked amplitude into
-// sc[i][k] (SC).  Steps run in blocks of 8 whose LDS reads (frame records,
-// row values) are all issued before the block's arithmetic.
+// The phase chain runs in blocks of kBlk steps whose LDS reads (frame
+// records, row values) are all issued before the block's arithmetic.
 constexpr int kBlk = 8;
-
-template <bool FAST, bool SC, bool SN>
-__device__ __forceinline__ void chain_loop(const SynthArgs& a, const SegLds& L, float* sc, float* sn, int lane,
-                                           int nt, float ph) {
-  const float kf = (float)(lane + 1);
-  const float nyq = a.sr * 0.5f;
-  const int kk = lane < a.K ? lane : 0;
-  const int n = FAST ? kSeg : nt;
-  for (int i0 = 0; i0 < n; i0 += kBlk) {
-    FrameRec r[kBlk];
-    float al[kBlk], ah[kBlk];
-#pragma unroll
-    for (int j = 0; j < kBlk; ++j) r[j] = L.fr[i0 + j];
-    if (SC) {
-#pragma unroll
-      for (int j = 0; j < kBlk; ++j) {
-        al[j] = L.row[r[j].slots & 255][kk];
-        ah[j] = L.row[r[j].slots >> 8][kk];
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < kBlk; ++j) {
-      const int i = i0 + j;
-      if (!FAST && i >= nt) break;
-      const float freq = kf * r[j].f0;
-      float inc;
-      if (FAST) {
-        const float q0 = freq * a.rsr;
-        inc = fmaf(fmaf(-q0, a.sr, freq), a.rsr, q0);
-      } else {
-        inc = div_sr(freq, a.sr, a.rsr);
-      }
-      const float p = ph;
-      ph = FAST ? __builtin_amdgcn_fractf(ph + inc) : phasor_wrap(ph + inc);
-      const float sv = sin2pi(p);
-      if (SC) {
-        const float amp = r[j].omf * al[j] + r[j].frac * ah[j];
-        sc[i * kLd + lane] = freq < nyq ? sv * amp : 0.0f;
-      }
-      if (SN) sn[i * kLd + lane] = sv;
-    }
-  }
-}
-
-template <bool SC, bool SN>
-__device__ __forceinline__ void chain_pass(const SynthArgs& a, const SegLds& L, float* sc, float* sn, int s, int b,
-                                           int lane, int nt, int fast) {
-  const float ph = a.ckpt[((size_t)s * a.B + b) * a.K + (lane < a.K ? lane : 0)];
-  if (fast)
-    chain_loop<true, SC, SN>(a, L, sc, sn, lane, nt, ph);
-  else
-    chain_loop<false, SC, SN>(a, L, sc, sn, lane, nt, ph);
-}
 
 // FIR noise branch for frame i: sum_j noise[t-(NF-1)+j] * tap_j(t).
 __device__ __forceinline__ float frame_fir(const SynthArgs& a, const SegLds& L, int i, const FrameRec& r) {
@@ -477,27 +421,100 @@ __device__ __forceinline__ float frame_fir(const SynthArgs& a, const SegLds& L, 
 // the backward reuses.
 constexpr int kWavesFwd = 2;
 
+// Chain pass of the forward held in registers: v[i] = sin(2 pi phase_k(i)) *
+// masked amplitude for frame i of this lane's harmonic k (0 for lanes >= K
+// and frames >= nt).  The phase steps are those of the reference's stateful
+// phasor (pre-increment output, wrap), the backward's pass repeats them bit
+// for bit.
+template <bool FAST>
+__device__ __forceinline__ void chain_regs(const SynthArgs& a, const SegLds& L, float (&v)[kSeg], int lane, int nt,
+                                           float ph) {
+  const float kf = (float)(lane + 1);
+  const float nyq = a.sr * 0.5f;
+  const bool harm = lane < a.K;
+  const int kk = harm ? lane : 0;
+#pragma unroll
+  for (int i0 = 0; i0 < kSeg; i0 += kBlk) {
+    FrameRec r[kBlk];
+    float al[kBlk], ah[kBlk];
+#pragma unroll
+    for (int j = 0; j < kBlk; ++j) {
+      r[j] = L.fr[i0 + j];
+      al[j] = L.row[r[j].slots & 255][kk];
+      ah[j] = L.row[r[j].slots >> 8][kk];
+    }
+#pragma unroll
+    for (int j = 0; j < kBlk; ++j) {
+      const int i = i0 + j;
+      if (!FAST && i >= nt) {
+        v[i] = 0.0f;
+        continue;
+      }
+      const float freq = kf * r[j].f0;
+      float inc;
+      if (FAST) {
+        const float q0 = freq * a.rsr;
+        inc = fmaf(fmaf(-q0, a.sr, freq), a.rsr, q0);
+      } else {
+        inc = div_sr(freq, a.sr, a.rsr);
+      }
+      const float p = ph;
+      ph = FAST ? __builtin_amdgcn_fractf(ph + inc) : phasor_wrap(ph + inc);
+      const float amp = r[j].omf * al[j] + r[j].frac * ah[j];
+      v[i] = (harm && freq < nyq) ? sin2pi(p) * amp : 0.0f;
+    }
+  }
+}
+
+// Butterfly reduce-scatter across the wave: on entry v[i] is this lane's
+// term of frame i; on return v[0] is the sum over all 64 lanes of frame
+// `lane`'s terms.  Stage D keeps the half of the frames selected by bit D
+// of the lane and adds the partner lane's (lane ^ D) copy of that half.
+template <int D>
+__device__ __forceinline__ void rs_stage(float (&v)[kSeg], int lane) {
+  const bool up = (lane & D) != 0;
+#pragma unroll
+  for (int j = 0; j < D; ++j) {
+    const float send = up ? v[j] : v[j + D];
+    const float keep = up ? v[j + D] : v[j];
+    v[j] = keep + __shfl_xor(send, D, 64);
+  }
+}
+
+__device__ __forceinline__ float reduce_scatter64(float (&v)[kSeg], int lane) {
+  static_assert(kSeg == 64, "one frame per lane");
+  rs_stage<32>(v, lane);
+  rs_stage<16>(v, lane);
+  rs_stage<8>(v, lane);
+  rs_stage<4>(v, lane);
+  rs_stage<2>(v, lane);
+  rs_stage<1>(v, lane);
+  return v[0];
+}
+
 __global__ __launch_bounds__(64 * kWavesFwd) void k_synth_fwd(SynthArgs a, float* __restrict__ y,
                                                               float* __restrict__ aux) {
   __shared__ SegLds lds[kWavesFwd];
-  __shared__ float s_c[kWavesFwd][kSeg * kLd];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int nseg = (a.T + kSeg - 1) / kSeg;
   const int s = blockIdx.x * kWavesFwd + wave, b = blockIdx.y;
   if (s >= nseg) return;
   SegLds& L = lds[wave];
-  float* sc = s_c[wave];
   const int t0 = s * kSeg, nt = min(kSeg, a.T - t0);
   const int fast = stage_segment(a, L, s, b, lane, nt, true);
-  chain_pass<true, false>(a, L, sc, nullptr, s, b, lane, nt, fast);
-  wave_sync();
+  float v[kSeg];
+  {
+    const float ph = a.ckpt[((size_t)s * a.B + b) * a.K + (lane < a.K ? lane : 0)];
+    if (fast)
+      chain_regs<true>(a, L, v, lane, nt, ph);
+    else
+      chain_regs<false>(a, L, v, lane, nt, ph);
+  }
+  const float num = reduce_scatter64(v, lane);  // frame = lane
   if (lane < nt) {
     const int t = t0 + lane;
     const FrameRec r = L.fr[lane];
     const int slo = r.slots & 255, shi = r.slots >> 8;
-    float num = 0.0f;
-    const float* row = sc + lane * kLd;
-    for (int k = 0; k < a.K; ++k) num += row[k];
     const int n = below_nyquist(r.f0, a.sr * 0.5f, a.K);
     const float den = r.omf * L.pre[slo][n] + r.frac * L.pre[shi][n] + 1e-8f;
     const float hsum = num / den;
