@@ -9,6 +9,12 @@
 // out[(j/Ns)*Ns*R + j mod Ns + r*Ns].  Radix 8 passes first, then one 4 or 2.
 // Every thread of the workgroup must call fft() together (it contains
 // workgroup barriers); each group of M/8 threads works on its own buffer.
+//
+// Buffers are padded: complex value i lives at i + i/8.  A Stockham pass
+// writes R consecutive values per thread, a stride of 8R bytes across the
+// wave, which on the 32-bank LDS would put most lanes of a store on the same
+// bank pair; the pad spreads them over 16 pairs and keeps the passes' reads
+// (consecutive indices) contiguous.
 #pragma once
 
 #include "internal.h"
@@ -17,6 +23,15 @@ namespace dgen {
 
 struct c2 {
   float x, y;
+};
+
+// Storage (in complex values) for n padded values, n a multiple of 8.
+__host__ __device__ constexpr int lds_pad(int n) { return n + n / 8; }
+
+// View of one padded FFT buffer.
+struct PadBuf {
+  c2* p;
+  __device__ __forceinline__ c2& operator[](int i) const { return p[i + (i >> 3)]; }
 };
 __device__ __forceinline__ c2 cadd(c2 a, c2 b) { return {a.x + b.x, a.y + b.y}; }
 __device__ __forceinline__ c2 csub(c2 a, c2 b) { return {a.x - b.x, a.y - b.y}; }
@@ -117,7 +132,7 @@ __device__ __forceinline__ int in_pos(int j, int e) {
 // Middle passes 1 .. npass-2 in LDS (in place; a barrier separates each
 // pass's reads from its writes).
 template <int LOGM, int P, bool INV>
-__device__ __forceinline__ void mid_passes(c2* buf, int j, c2* v) {
+__device__ __forceinline__ void mid_passes(PadBuf buf, int j, c2* v) {
   constexpr int M = 1 << LOGM;
   if constexpr (P < pass_count(LOGM) - 1) {
     constexpr int R = pass_radix(LOGM, P), NS = pass_span(LOGM, P);
@@ -137,7 +152,7 @@ __device__ __forceinline__ void mid_passes(c2* buf, int j, c2* v) {
 // in_pos of pass 0); on return v holds the last pass's outputs at positions
 // op[e].  Uses buf (M complex, this window's slot) between passes.
 template <int LOGM, bool INV>
-__device__ __forceinline__ void fft(c2* buf, int j, c2* v, int* op) {
+__device__ __forceinline__ void fft(PadBuf buf, int j, c2* v, int* op) {
   constexpr int M = 1 << LOGM;
   constexpr int NP = pass_count(LOGM);
   {

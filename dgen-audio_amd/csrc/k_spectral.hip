@@ -57,8 +57,8 @@ __device__ __forceinline__ float hw_rcp(float v) { return __builtin_amdgcn_rcpf(
 
 struct MssLds {
   float acc[kAcc];                 // dx of samples [a - kHalo, a + kTile)
-  c2 buf[2048];                    // FFT slots: (4096/N windows) x (N/2)
-  c2 aux[2048];                    // second signal's spectrum / gradient spectrum
+  c2 buf[lds_pad(2048)];           // FFT slots: (4096/N windows) x (N/2), padded
+  c2 aux[lds_pad(2048)];           // second signal's spectrum / gradient spectrum
   float red[kThreads / 64][2];
   float hann[2048];                // this size's window
 };
@@ -70,8 +70,8 @@ __device__ __forceinline__ void mss_size(const MssArgs& a, MssLds& L, int si, in
   static_assert(W * M == 2048, "window slots must fill the FFT buffer");
   const int tid = threadIdx.x;
   const int slot = tid / P, j = tid % P;
-  c2* buf = L.buf + slot * M;
-  c2* spec = L.aux + slot * M;
+  const PadBuf buf{L.buf + slot * lds_pad(M)};
+  const PadBuf spec{L.aux + slot * lds_pad(M)};
   const int a0 = tile * kTile;
   const int nwin = (a.T + H - 1) / H;
   const float* xs = a.x + (size_t)b * a.T;
@@ -116,7 +116,7 @@ __device__ __forceinline__ void mss_size(const MssArgs& a, MssLds& L, int si, in
         v[e] = pass == 0 ? c2{pt[2 * e] * h0, pt[2 * e + 1] * h1} : c2{px[2 * e] * h0, px[2 * e + 1] * h1};
       }
       fft<LOGM, false>(buf, j, v, op);
-      c2* dst = pass == 0 ? spec : buf;
+      const PadBuf dst = pass == 0 ? spec : buf;
 #pragma unroll
       for (int e = 0; e < 8; ++e) dst[op[e]] = v[e];
       lds_barrier();

@@ -51,7 +51,7 @@ struct StftArgs {
 
 // Real N-point spectrum bins k and M-k (k = 0: bins 0 and M) from the
 // N/2-point complex transform Z of the even/odd-packed signal.
-__device__ __forceinline__ void split_bins(const c2* Z, int k, int M, float invN, c2& Xk, c2& Xm) {
+__device__ __forceinline__ void split_bins(PadBuf Z, int k, int M, float invN, c2& Xk, c2& Xm) {
   const int km = (M - k) & (M - 1);
   const c2 zk = Z[k], zm = Z[km];
   const c2 e = {0.5f * (zk.x + zm.x), 0.5f * (zk.y - zm.y)};
@@ -76,7 +76,7 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 
 struct FwdLds {
   float acc[kTile];
-  c2 buf[2048];
+  c2 buf[lds_pad(2048)];
   float win[2048];
   float gain[1025];
   float red[kThreads / 64];
@@ -98,8 +98,11 @@ __global__ __launch_bounds__(kThreads) void k_stft_fwd(StftArgs a) {
   const int w_lo = a0 - N < 0 ? 0 : (a0 - N) / H + 1;
   const int w_hi = (a1 - 1) / H;
   const int nw = w_hi - w_lo + 1;
-  c2* buf = L.buf + slot * M;
-  const float* zs = reinterpret_cast<const float*>(L.buf);  // slot q's outputs at zs + q*N
+  const PadBuf buf{L.buf + slot * lds_pad(M)};
+  // after the inverse transform a slot's region holds its N real outputs,
+  // unpadded: slot q's at zs + q * 2 * lds_pad(M)
+  const float* zs = reinterpret_cast<const float*>(L.buf);
+  constexpr int kZStride = 2 * lds_pad(M);
   constexpr float invN = 1.0f / (float)N;
   __syncthreads();
   for (int r0 = 0; r0 < nw; r0 += W) {
@@ -147,7 +150,7 @@ __global__ __launch_bounds__(kThreads) void k_stft_fwd(StftArgs a) {
     lds_barrier();
     fft<LOGM, true>(buf, j, v, op);
     // complex output q holds samples 2q, 2q+1 (unnormalised): scale by 1/N
-    float* zb = reinterpret_cast<float*>(buf);
+    float* zb = reinterpret_cast<float*>(buf.p);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       zb[2 * op[e]] = v[e].x * invN;
@@ -164,7 +167,7 @@ __global__ __launch_bounds__(kThreads) void k_stft_fwd(StftArgs a) {
       float sum = 0.0f;
       for (int q = 0; q < nq; ++q) {
         const int i = p - q * H;
-        if (i >= 0 && i < N) sum += zs[q * N + i];
+        if (i >= 0 && i < N) sum += zs[q * kZStride + i];
       }
       L.acc[t - a0] += sum;
     }
@@ -186,8 +189,8 @@ __global__ __launch_bounds__(kThreads) void k_stft_fwd(StftArgs a) {
 }
 
 struct BwdLds {
-  c2 buf[2048];
-  c2 aux[2048];
+  c2 buf[lds_pad(2048)];
+  c2 aux[lds_pad(2048)];
   float win[2048];
 };
 
@@ -204,8 +207,8 @@ __global__ __launch_bounds__(kThreads) void k_stft_bwd(StftArgs a) {
   const float* xs = a.x + (size_t)s * a.T;
   const float* gs = a.dyin + (size_t)s * a.T;
   for (int i = tid; i < N; i += kThreads) L.win[i] = a.win[i];
-  c2* buf = L.buf + slot * M;
-  c2* spec = L.aux + slot * M;
+  const PadBuf buf{L.buf + slot * lds_pad(M)};
+  const PadBuf spec{L.aux + slot * lds_pad(M)};
   constexpr float invN = 1.0f / (float)N;
   float acc_k[U], acc_m[U];
 #pragma unroll
@@ -233,7 +236,7 @@ __global__ __launch_bounds__(kThreads) void k_stft_bwd(StftArgs a) {
         }
       }
       fft<LOGM, false>(buf, j, v, op);
-      c2* dst = pass == 0 ? spec : buf;
+      const PadBuf dst = pass == 0 ? spec : buf;
 #pragma unroll
       for (int e = 0; e < 8; ++e) dst[op[e]] = v[e];
       lds_barrier();
