@@ -17,6 +17,11 @@
 namespace dgen {
 
 constexpr int BM = 128, BN = 128, BK = 32, LDSROW = BM + 4;
+// Row stride of an operand tile that is stored transposed (scalar writes of
+// four k values per thread): 130 floats puts the 8 k-groups of a wave's store
+// on distinct banks (132 would put them 4-way on 16 banks); a tile stored
+// as float4 rows keeps 132 for 16-byte alignment.
+constexpr int LDSROW_T = BM + 2;
 // float4 loads per thread per operand tile: BM*BK / 4 / 256
 constexpr int LPT = BM * BK / 4 / 256;
 
@@ -33,24 +38,6 @@ __device__ __forceinline__ float4 load4(const float* __restrict__ p, int valid) 
   if (valid > 2) v.z = p[2];
   if (valid > 3) v.w = p[3];
   return v;
-}
-
-// tanh within a few ulp at a fraction of the libm cost: for |x| < 0.55 the
-// odd Taylor series to x^15 (truncation below 5e-8 relative; the series
-// converges for |x| < pi/2), otherwise 1 - 2/(e^{2|x|} + 1) on the hardware
-// exp2 and reciprocal (no cancellation there: 2/(e^{2|x|}+1) <= 0.5).
-__device__ __forceinline__ float fast_tanh(float x) {
-  const float ax = fabsf(x), x2 = x * x;
-  float p = fmaf(x2, -929569.0f / 638512875.0f, 21844.0f / 6081075.0f);
-  p = fmaf(x2, p, -1382.0f / 155925.0f);
-  p = fmaf(x2, p, 62.0f / 2835.0f);
-  p = fmaf(x2, p, -17.0f / 315.0f);
-  p = fmaf(x2, p, 2.0f / 15.0f);
-  p = fmaf(x2, p, -1.0f / 3.0f);
-  const float small = fmaf(x * x2, p, x);
-  const float e = __builtin_amdgcn_exp2f(ax * 2.8853900817779268f);  // e^{2|x|}
-  const float big = 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
-  return ax < 0.55f ? small : copysignf(big, x);
 }
 
 __device__ __forceinline__ float apply_epi(int epi, float acc, int row, int col, const float* __restrict__ bias,
@@ -72,8 +59,12 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const
                                               float* __restrict__ C, int M, int N, int K, int lda, int ldb, int ldc,
                                               int epi, const float* __restrict__ bias, const float* __restrict__ aux,
                                               int ldaux, int kchunk, float* __restrict__ ws) {
-  __shared__ float As[2][BK][LDSROW];
-  __shared__ float Bs[2][BK][LDSROW];
+  __shared__ float As_[2][BK * LDSROW];
+  __shared__ float Bs_[2][BK * LDSROW];
+  constexpr int RA = A_KMAJ ? LDSROW : LDSROW_T;  // A is transposed when stored [M][K]
+  constexpr int RB = B_NK ? LDSROW_T : LDSROW;    // B is transposed when stored [N][K]
+  auto As = [&](int b, int k, int m) -> float& { return As_[b][k * RA + m]; };
+  auto Bs = [&](int b, int k, int n) -> float& { return Bs_[b][k * RB + n]; };
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -140,23 +131,23 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const
       const int q = tid + p * 256;
       if (!A_KMAJ) {
         const int i = q / (BK / 4), kq = (q % (BK / 4)) * 4;
-        As[buf][kq + 0][i] = ra[p].x;
-        As[buf][kq + 1][i] = ra[p].y;
-        As[buf][kq + 2][i] = ra[p].z;
-        As[buf][kq + 3][i] = ra[p].w;
+        As(buf, kq + 0, i) = ra[p].x;
+        As(buf, kq + 1, i) = ra[p].y;
+        As(buf, kq + 2, i) = ra[p].z;
+        As(buf, kq + 3, i) = ra[p].w;
       } else {
         const int kk = q / (BM / 4), iq = (q % (BM / 4)) * 4;
-        *reinterpret_cast<float4*>(&As[buf][kk][iq]) = ra[p];
+        *reinterpret_cast<float4*>(&As(buf, kk, iq)) = ra[p];
       }
       if (!B_NK) {
         const int kk = q / (BN / 4), jq = (q % (BN / 4)) * 4;
-        *reinterpret_cast<float4*>(&Bs[buf][kk][jq]) = rb[p];
+        *reinterpret_cast<float4*>(&Bs(buf, kk, jq)) = rb[p];
       } else {
         const int j = q / (BK / 4), kq = (q % (BK / 4)) * 4;
-        Bs[buf][kq + 0][j] = rb[p].x;
-        Bs[buf][kq + 1][j] = rb[p].y;
-        Bs[buf][kq + 2][j] = rb[p].z;
-        Bs[buf][kq + 3][j] = rb[p].w;
+        Bs(buf, kq + 0, j) = rb[p].x;
+        Bs(buf, kq + 1, j) = rb[p].y;
+        Bs(buf, kq + 2, j) = rb[p].z;
+        Bs(buf, kq + 3, j) = rb[p].w;
       }
     }
   };
@@ -175,10 +166,10 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const
     float fa0[2], fa1[2], fb0[2], fb1[2];
     auto frag = [&](int st, int slot) {
       const int k = 2 * st + h;
-      fa0[slot] = As[buf][k][wm + r];
-      fa1[slot] = As[buf][k][wm + 32 + r];
-      fb0[slot] = Bs[buf][k][wn + r];
-      fb1[slot] = Bs[buf][k][wn + 32 + r];
+      fa0[slot] = As(buf, k, wm + r);
+      fa1[slot] = As(buf, k, wm + 32 + r);
+      fb0[slot] = Bs(buf, k, wn + r);
+      fb1[slot] = Bs(buf, k, wn + 32 + r);
     };
     frag(0, 0);
 #pragma unroll

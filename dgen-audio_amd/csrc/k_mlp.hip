@@ -21,29 +21,45 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 // ---------------------------------------------------------------- layer 1
 // H[m][j] = tanh(sum_i X[m][i] W[i][j] + b[j]) for a fan-in of a few inputs.
-__global__ void k_dense_small(const float* __restrict__ X, const float* __restrict__ W, const float* __restrict__ b,
-                              float* __restrict__ H, int rows, int fan, int width) {
-  const int j = blockIdx.x * blockDim.x + threadIdx.x;
-  const int m = blockIdx.y;
-  if (j >= width || m >= rows) return;
-  float s = 0.f;
-  for (int i = 0; i < fan; ++i) s += X[(size_t)m * fan + i] * W[(size_t)i * width + j];
-  H[(size_t)m * width + j] = tanhf(s + b[j]);
+// Each thread writes 4 consecutive outputs of a row (width % 4 == 0), grid-
+// strided over rows.
+__global__ __launch_bounds__(256) void k_dense_small(const float* __restrict__ X, const float* __restrict__ W,
+                                                     const float* __restrict__ b, float* __restrict__ H, int rows,
+                                                     int fan, int width) {
+  const int qw = width / 4;
+  const size_t total = (size_t)rows * qw;
+  for (size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x; g < total; g += (size_t)gridDim.x * blockDim.x) {
+    const int m = (int)(g / qw), j = (int)(g % qw) * 4;
+    float4 s = *reinterpret_cast<const float4*>(b + j);
+    for (int i = 0; i < fan; ++i) {
+      const float x = X[(size_t)m * fan + i];
+      const float4 w = *reinterpret_cast<const float4*>(W + (size_t)i * width + j);
+      s.x = fmaf(x, w.x, s.x);
+      s.y = fmaf(x, w.y, s.y);
+      s.z = fmaf(x, w.z, s.z);
+      s.w = fmaf(x, w.w, s.w);
+    }
+    *reinterpret_cast<float4*>(H + (size_t)m * width + j) =
+        make_float4(fast_tanh(s.x), fast_tanh(s.y), fast_tanh(s.z), fast_tanh(s.w));
+  }
 }
 
 int launch_dense_small(const Launch& L, const dgen_hip_op& op) {
   const int64_t X = op.arg[0], W = op.arg[1], b = op.arg[2], H = op.arg[3];
   const int64_t rows = op.arg[4], fan = op.arg[5], width = op.arg[6];
-  DGEN_REQUIRE(rows > 0 && rows <= 65535 * 64 && fan > 0 && fan <= 64 && width > 0 && width <= 65536,
+  DGEN_REQUIRE(rows > 0 && rows < (1ll << 31) && fan > 0 && fan <= 64 && width > 0 && width <= 65536,
                "dense_small: rows %lld fan %lld width %lld", (long long)rows, (long long)fan, (long long)width);
   DGEN_CHECK_CELL(L, X, rows * fan, "dense_small.X");
   DGEN_CHECK_CELL(L, W, fan * width, "dense_small.W");
   DGEN_CHECK_CELL(L, b, width, "dense_small.b");
   DGEN_CHECK_CELL(L, H, rows * width, "dense_small.H");
+  DGEN_REQUIRE(width % 4 == 0 && W % 4 == 0 && b % 4 == 0 && H % 4 == 0,
+               "dense_small: width %lld and the W, b, H cells must be multiples of 4", (long long)width);
   if (L.dry) return 0;
-  DGEN_REQUIRE(rows <= 65535, "dense_small: rows %lld exceed grid y", (long long)rows);
-  hipLaunchKernelGGL(k_dense_small, dim3((unsigned)((width + 255) / 256), (unsigned)rows), dim3(256), 0, L.stream,
-                     cell(L, X), cell(L, W), cell(L, b), cell(L, H), (int)rows, (int)fan, (int)width);
+  const int64_t quads = rows * (width / 4);
+  const unsigned blocks = (unsigned)std::min<int64_t>((quads + 255) / 256, (int64_t)L.cu_count * 16);
+  hipLaunchKernelGGL(k_dense_small, dim3(blocks), dim3(256), 0, L.stream, cell(L, X), cell(L, W), cell(L, b),
+                     cell(L, H), (int)rows, (int)fan, (int)width);
   DGEN_LAUNCH_CHECK("k_dense_small");
   return 0;
 }
@@ -55,39 +71,67 @@ int launch_dense_small(const Launch& L, const dgen_hip_op& op) {
 // waves' sums are combined in LDS in wave order -> part[c][q][n].
 // Stage 2: one workgroup per 64 columns sums the chunk partials in chunk order
 // (4 waves over interleaved chunks, then wave order).
-constexpr int kColChunks = 256;
+constexpr int kColChunks = 128;
 constexpr int kMaxW = 4;  // weighted sums besides the plain one
 
+// V4: each lane reads 4 consecutive columns (float4; cols, lda and the base
+// are multiples of 4), so a workgroup covers 256 columns; else 64 columns.
+template <bool V4>
 __global__ __launch_bounds__(256) void k_colsum_partial(const float* __restrict__ A, int lda,
                                                         const float* __restrict__ X, int nw, int rows, int cols,
                                                         int chunk, float* __restrict__ part, int want_plain) {
-  __shared__ float red[4][kMaxW + 1][64];
+  constexpr int CW = V4 ? 4 : 1;  // columns per lane
+  __shared__ float red[4][kMaxW + 1][64 * CW];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int n = blockIdx.x * 64 + lane;
+  const int n = (blockIdx.x * 64 + lane) * CW;
   const int c = blockIdx.y;
   const int m0 = c * chunk, m1 = min(rows, m0 + chunk);
-  float acc[kMaxW + 1];
+  float acc[kMaxW + 1][CW];
 #pragma unroll
-  for (int q = 0; q <= kMaxW; ++q) acc[q] = 0.f;
+  for (int q = 0; q <= kMaxW; ++q)
+#pragma unroll
+    for (int e = 0; e < CW; ++e) acc[q][e] = 0.f;
   if (n < cols) {
-#pragma unroll 4
+#pragma unroll 8
     for (int m = m0 + wave; m < m1; m += 4) {
-      const float v = A[(size_t)m * lda + n];
+      float v[CW];
+      if constexpr (V4) {
+        const float4 t = *reinterpret_cast<const float4*>(A + (size_t)m * lda + n);
+        v[0] = t.x;
+        v[1] = t.y;
+        v[2] = t.z;
+        v[3] = t.w;
+      } else {
+        v[0] = A[(size_t)m * lda + n];
+      }
 #pragma unroll
       for (int q = 0; q < kMaxW; ++q)
-        if (q < nw) acc[q] += X[(size_t)m * nw + q] * v;
-      acc[kMaxW] += v;
+        if (q < nw) {
+          const float x = X[(size_t)m * nw + q];
+#pragma unroll
+          for (int e = 0; e < CW; ++e) acc[q][e] += x * v[e];
+        }
+#pragma unroll
+      for (int e = 0; e < CW; ++e) acc[kMaxW][e] += v[e];
     }
   }
 #pragma unroll
-  for (int q = 0; q <= kMaxW; ++q) red[wave][q][lane] = acc[q];
+  for (int q = 0; q <= kMaxW; ++q)
+#pragma unroll
+    for (int e = 0; e < CW; ++e) red[wave][q][lane * CW + e] = acc[q][e];
   __syncthreads();
-  if (wave == 0 && n < cols) {
+  if (wave == 0) {
     const int nq = nw + (want_plain ? 1 : 0);
     for (int q = 0; q < nq; ++q) {
       const int src = q < nw ? q : kMaxW;
-      const float v = ((red[0][src][lane] + red[1][src][lane]) + red[2][src][lane]) + red[3][src][lane];
-      part[((size_t)c * nq + q) * cols + n] = v;
+#pragma unroll
+      for (int e = 0; e < CW; ++e) {
+        const int col = n + e;
+        if (col >= cols) continue;
+        const int li = lane * CW + e;
+        const float v = ((red[0][src][li] + red[1][src][li]) + red[2][src][li]) + red[3][src][li];
+        part[((size_t)c * nq + q) * cols + col] = v;
+      }
     }
   }
 }
@@ -100,8 +144,11 @@ __global__ __launch_bounds__(256) void k_colsum_final(const float* __restrict__ 
   const int n = blockIdx.x * 64 + lane;
   const int q = blockIdx.y;
   float s = 0.f;
-  if (n < cols)
+  if (n < cols) {
+    // loads issued 8 at a time; the adds keep the fixed chunk order
+#pragma unroll 8
     for (int c = wave; c < chunks; c += 4) s += part[((size_t)c * nq + q) * cols + n];
+  }
   red[wave][lane] = s;
   __syncthreads();
   if (wave == 0 && n < cols) {
@@ -113,17 +160,26 @@ __global__ __launch_bounds__(256) void k_colsum_final(const float* __restrict__ 
   }
 }
 
-static int colsum_chunks(int64_t rows) { return (int)std::min<int64_t>(kColChunks, std::max<int64_t>(1, rows / 32)); }
+// Row chunks of stage 1: weighted sums do more work per row, so they use
+// twice as many (shorter) chunks.
+static int colsum_chunks(int64_t rows, int nw = 0) {
+  return (int)std::min<int64_t>(nw > 0 ? 2 * kColChunks : kColChunks, std::max<int64_t>(1, rows / 32));
+}
 
 // out_q (q < nw) rows of out0 (stride ld_out0) and the plain sum into plain_out.
 static int colsum_launch(const Launch& L, const float* A, int lda, const float* X, int nw, int rows, int cols,
                          float* ws, float* out0, int ld_out0, float* plain_out) {
-  const int chunks = colsum_chunks(rows);
+  const int chunks = colsum_chunks(rows, nw);
   const int chunk = (rows + chunks - 1) / chunks;
   const int want_plain = plain_out != nullptr;
   const int nq = nw + want_plain;
-  hipLaunchKernelGGL(k_colsum_partial, dim3((unsigned)((cols + 63) / 64), (unsigned)chunks), dim3(256), 0, L.stream,
-                     A, lda, X, nw, rows, cols, chunk, ws, want_plain);
+  const bool v4 = cols % 4 == 0 && lda % 4 == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0;
+  if (v4)
+    hipLaunchKernelGGL(k_colsum_partial<true>, dim3((unsigned)((cols + 255) / 256), (unsigned)chunks), dim3(256), 0,
+                       L.stream, A, lda, X, nw, rows, cols, chunk, ws, want_plain);
+  else
+    hipLaunchKernelGGL(k_colsum_partial<false>, dim3((unsigned)((cols + 63) / 64), (unsigned)chunks), dim3(256), 0,
+                       L.stream, A, lda, X, nw, rows, cols, chunk, ws, want_plain);
   DGEN_LAUNCH_CHECK("k_colsum_partial");
   hipLaunchKernelGGL(k_colsum_final, dim3((unsigned)((cols + 63) / 64), (unsigned)nq), dim3(256), 0, L.stream, ws,
                      chunks, nq, cols, out0, ld_out0, plain_out, want_plain);
@@ -152,7 +208,7 @@ int launch_dense_small_wgrad(const Launch& L, const dgen_hip_op& op) {
   DGEN_REQUIRE(rows > 0 && rows < (1ll << 31) && fan > 0 && fan <= kMaxW && width > 0 && width <= 65536,
                "dense_small_wgrad: rows %lld fan %lld width %lld", (long long)rows, (long long)fan,
                (long long)width);
-  const int chunks = colsum_chunks(rows);
+  const int chunks = colsum_chunks(rows, (int)fan);
   DGEN_CHECK_CELL(L, X, rows * fan, "dense_small_wgrad.X");
   DGEN_CHECK_CELL(L, dZ, rows * width, "dense_small_wgrad.dZ");
   DGEN_CHECK_CELL(L, dW, fan * width, "dense_small_wgrad.dW");
