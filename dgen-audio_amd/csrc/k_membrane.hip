@@ -12,13 +12,21 @@
 // S[n+1] = u_n, so the backward reads every forward state instead of
 // recomputing it (4801 fields of 1 MB at 512^2 x 4800).
 //
-// Temporal blocking: a workgroup owns a kTile x kTile tile and keeps a
-// kSide x kSide region (the tile plus a kHalo ring) of the two live fields
-// in LDS.  One launch advances ks <= kHalo steps: step s is valid on a band
-// that shrinks by one cell per step, so after ks steps the owned tile is
-// exact and no workgroup needs another's data until the next launch.  The
-// update is in place: u_{n+1}[i] overwrites u_{n-1}[i] (only that cell
-// reads it), so one workgroup barrier per step suffices.
+// Temporal blocking: a workgroup owns a kTile x kTile tile and advances a
+// kSide x kSide region (the tile plus a kHalo ring) of the two live fields.
+// One launch advances ks <= kHalo steps: values near the region edge go
+// wrong (their outside neighbours read as zero) but the error front moves one
+// cell per step, so after ks steps the owned tile is still exact and no
+// workgroup needs another's data until the next launch.
+//
+// Register strips: the region is 64 columns wide, one per wavefront lane;
+// wave w holds rows kRows*w .. kRows*w + kRows - 1 of its lane's column for
+// both live fields in registers.  Vertical neighbours come from the thread's
+// own registers (the strip's first and last rows from the waves above and
+// below, through a small double-buffered LDS edge table: one barrier per
+// step); horizontal neighbours from the adjacent lanes by DPP wave shifts.
+// Every cell of the region is updated each step; cells outside the grid are
+// then reset to zero (the conv2d zero padding).
 //
 // Adjoint (L is symmetric): lambda_n = g_n + (2-d) lambda_{n+1}
 // + c2 L lambda_{n+1} - (1-d) lambda_{n+2}, g_n = 2 (out[n-1] - tgt[n-1]) at
@@ -31,12 +39,14 @@
 namespace dgen {
 namespace {
 
-constexpr int kThreads = 256;
 constexpr int kTile = 32;
 constexpr int kHalo = 16;
-constexpr int kSide = kTile + 2 * kHalo;  // 64
-constexpr int kCells = kSide * kSide / kThreads;  // 16 cells per thread
-static_assert(kSide == 64, "thread mapping assumes a 64-wide region");
+constexpr int kSide = kTile + 2 * kHalo;  // 64: one wavefront lane per region column
+constexpr int kRows = 16;                 // region rows per thread
+constexpr int kWaves = kSide / kRows;
+constexpr int kThreads = 64 * kWaves;
+static_assert(kSide == 64, "one region column per wavefront lane");
+static_assert(kHalo % kRows == 0 && kTile % kRows == 0, "owned rows must fill whole strips");
 
 struct MemArgs {
   float* S;           // state store [(T + 2)][R][C]
@@ -48,180 +58,287 @@ struct MemArgs {
   int R, C, T, py, px;
 };
 
-// Cell j of thread t: column t & 63, row (t >> 6) + 4 j.
-__device__ __forceinline__ int cell_row(int j) { return (threadIdx.x >> 6) + 4 * j; }
-__device__ __forceinline__ int cell_col() { return threadIdx.x & 63; }
-
-__device__ __forceinline__ float lap5(const float* f, int i) {
-  return (((f[i - kSide] + f[i - 1]) + f[i] * -4.0f) + f[i + 1]) + f[i + kSide];
+// Value of lane c - 1 (0 at lane 0) and of lane c + 1 (0 at lane 63):
+// DPP wave_shr:1 / wave_shl:1.
+__device__ __forceinline__ float from_left(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x138, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float from_right(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x130, 0xf, 0xf, false));
 }
 
-// Loads the region of fields a (-> A) and b (-> B) around the tile; cells
-// outside the grid are zero (the conv2d zero padding) and stay zero.
-__device__ __forceinline__ void load_region(const MemArgs& a, const float* fa, const float* fb, float* A, float* B,
-                                            int ry0, int rx0) {
-  const int c = cell_col(), gx = rx0 + c;
-  const bool cin = gx >= 0 && gx < a.C;
-#pragma unroll
-  for (int j = 0; j < kCells; ++j) {
-    const int r = cell_row(j), gy = ry0 + r;
-    const bool in = cin && gy >= 0 && gy < a.R;
-    const size_t gi = in ? (size_t)gy * a.C + gx : 0;
-    A[r * kSide + c] = (in && fa) ? fa[gi] : 0.0f;
-    B[r * kSide + c] = (in && fb) ? fb[gi] : 0.0f;
+// Where this thread's strip lies in the grid.
+struct Strip {
+  int lane, w;
+  int gx, gy0;    // grid column; grid row of strip row 0
+  int qlo, qhi;   // strip rows [qlo, qhi) are inside the grid (uniform per wave)
+  int off0;       // gy0 * C + gx: field offset of strip row 0 (used for rows inside the grid)
+  bool cin;       // column inside the grid
+  bool own_w;     // the strip holds owned rows (uniform per wave)
+  bool own;       // owned cells: an owned strip and an owned column inside the grid
+  int prow;       // strip row of the pickup cell in this lane, or -1
+  int pw;         // strip row of the pickup cell if its row lies in this strip and its column in the region, else -1 (uniform per wave)
+
+  __device__ Strip(const MemArgs& a) {
+    lane = threadIdx.x & 63;
+    w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    gx = blockIdx.x * kTile - kHalo + lane;
+    gy0 = blockIdx.y * kTile - kHalo + kRows * w;
+    qlo = max(0, -gy0);
+    qhi = min(kRows, a.R - gy0);
+    off0 = gy0 * a.C + gx;
+    cin = gx >= 0 && gx < a.C;
+    own_w = kRows * w >= kHalo && kRows * w < kHalo + kTile;
+    own = own_w && cin && lane >= kHalo && lane < kHalo + kTile;
+    prow = (gx == a.px && a.py - gy0 >= 0 && a.py - gy0 < kRows) ? a.py - gy0 : -1;
+    const int px_lane = a.px - (blockIdx.x * kTile - kHalo);
+    pw = (px_lane >= 0 && px_lane < 64 && a.py - gy0 >= 0 && a.py - gy0 < kRows) ? a.py - gy0 : -1;
   }
+  __device__ bool in(int q) const { return cin && q >= qlo && q < qhi; }
+  // Field offset of row q (grids hold at most 2^28 cells: 32 bits suffice).
+  __device__ unsigned at(int q, int C) const { return (unsigned)(off0 + q * C); }
+};
+
+// Reads rows of field f at this strip; rows outside the grid read cell 0,
+// so that the loads issue back to back with no branch or wait between them.
+__device__ __forceinline__ void load_rows(const Strip& st, const float* f, int C, float (&v)[kRows]) {
+#pragma unroll
+  for (int q = 0; q < kRows; ++q) v[q] = f[st.in(q) ? st.at(q, C) : 0u];
+}
+
+// load_rows, zero outside the grid (keep = 0 there).
+__device__ __forceinline__ void load_strip(const Strip& st, const float* f, int C, const float (&keep)[kRows],
+                                           float (&v)[kRows]) {
+  load_rows(st, f, C, v);
+#pragma unroll
+  for (int q = 0; q < kRows; ++q) v[q] *= keep[q];
+}
+
+// Publishes the strip's first and last rows of u and returns the row above
+// the strip and the row below it (zero at the region edge).
+__device__ __forceinline__ void exchange_edges(float (*e)[2][64], const Strip& st, const float (&u)[kRows], float& up,
+                                               float& dn) {
+  e[st.w][0][st.lane] = u[0];
+  e[st.w][1][st.lane] = u[kRows - 1];
+  lds_barrier();
+  up = st.w > 0 ? e[st.w - 1][1][st.lane] : 0.0f;
+  dn = st.w + 1 < kWaves ? e[st.w + 1][0][st.lane] : 0.0f;
+}
+
+// 5-point Laplacian at strip row q, in the reference's summation order
+// (up, left, centre, right, down).
+__device__ __forceinline__ float lap_row(const float (&u)[kRows], float up, float dn, int q) {
+  const float n = q == 0 ? up : u[q - 1];
+  const float s = q == kRows - 1 ? dn : u[q + 1];
+  return (((n + from_left(u[q])) + u[q] * -4.0f) + from_right(u[q])) + s;
+}
+
+// 1 for strip rows inside the grid, 0 outside: a multiplier rather than a
+// branch, so that every lane runs the stencil (the DPP shifts read all 64).
+// The kernels scale the Laplacian by it: a cell outside the grid starts at
+// zero and its update (2u - u_prev + c2 L u - d (u - u_prev) forward, the
+// same form backward) then stays exactly zero.
+__device__ __forceinline__ void keep_mask(const Strip& st, float (&keep)[kRows]) {
+#pragma unroll
+  for (int q = 0; q < kRows; ++q) keep[q] = st.in(q) ? 1.0f : 0.0f;
 }
 
 // Forward: frames n0 .. n0+ks-1 (u_{n0+1} .. u_{n0+ks}).
 __global__ __launch_bounds__(kThreads) void k_mem_fwd(MemArgs a, int n0, int ks) {
-  __shared__ float f[2][kSide * kSide];
-  const int y0 = blockIdx.y * kTile, x0 = blockIdx.x * kTile;
-  const int ry0 = y0 - kHalo, rx0 = x0 - kHalo;
+  __shared__ float edge[2][kWaves][2][64];
+  const Strip st(a);
   const size_t G = (size_t)a.R * a.C;
   const float c2 = a.prm[0], d = a.prm[1];
-  float* cur = f[0];
-  float* prv = f[1];
-  load_region(a, a.S + (size_t)(n0 + 1) * G, a.S + (size_t)n0 * G, cur, prv, ry0, rx0);
-  const int c = cell_col(), gx = rx0 + c;
-  const bool cin = gx >= 0 && gx < a.C;
-  __syncthreads();
-  for (int s = 0; s < ks; ++s) {
-    const int lo = kHalo + 1 - ks + s, hi = kHalo + kTile - 1 + ks - s;
-    if (cin && c >= lo && c < hi) {
+  float keep[kRows];
+  keep_mask(st, keep);
+  float u[kRows], v[kRows];  // u_n, u_{n-1}
+  load_strip(st, a.S + (size_t)(n0 + 1) * G, a.C, keep, u);
+  load_strip(st, a.S + (size_t)n0 * G, a.C, keep, v);
+  // (cur, prv) -> prv = the next state; owned cells -> S[n0+s+2], pickup -> out[n0+s]
+  auto step = [&](const float (&cur)[kRows], float (&prv)[kRows], int s) {
+    float up, dn;
+    exchange_edges(edge[s & 1], st, cur, up, dn);
+    auto row = [&](int q) {
+      const float lap = lap_row(cur, up, dn, q) * keep[q];
+      const float b = cur[q] * 2.0f - prv[q];
+      const float g = (cur[q] - prv[q]) * d;
+      prv[q] = (b + lap * c2) - g;
+    };
+    // interior rows first: they do not wait for the exchanged edge rows
 #pragma unroll
-      for (int j = 0; j < kCells; ++j) {
-        const int r = cell_row(j), gy = ry0 + r;
-        if (r < lo || r >= hi || gy < 0 || gy >= a.R) continue;
-        const int i = r * kSide + c;
-        const float u = cur[i], u1 = prv[i];
-        const float b = u * 2.0f - u1;
-        const float cc = lap5(cur, i) * c2;
-        const float g = (u - u1) * d;
-        prv[i] = (b + cc) - g;
+    for (int q = 1; q < kRows - 1; ++q) row(q);
+    row(0);
+    row(kRows - 1);
+    if (st.own) {
+      float* dst = a.S + (size_t)(n0 + s + 2) * G;
+      if (st.qhi == kRows) {  // owned strips start inside the grid; most end inside it too
+#pragma unroll
+        for (int q = 0; q < kRows; ++q) dst[st.at(q, a.C)] = prv[q];
+      } else {
+#pragma unroll
+        for (int q = 0; q < kRows; ++q)
+          if (q < st.qhi) dst[st.at(q, a.C)] = prv[q];
+      }
+      if (st.prow >= 0) {  // only the owned copy is exact at the region edge
+#pragma unroll
+        for (int q = 0; q < kRows; ++q)
+          if (q == st.prow) a.out[n0 + s] = prv[q];
       }
     }
-    lds_barrier();
-    float* t = cur;
-    cur = prv;
-    prv = t;
-    // owned cells of u_{n0+s+1} -> S[n0+s+2]; the pickup -> out[n0+s]
-    if (cin && c >= kHalo && c < kHalo + kTile) {
-      float* dst = a.S + (size_t)(n0 + s + 2) * G;
+  };
+  int s = 0;
+  for (; s + 1 < ks; s += 2) {
+    step(u, v, s);
+    step(v, u, s + 1);
+  }
+  if (s < ks) step(u, v, s);
+}
+
+// Backward: adjoint steps n = m_hi .. m_hi-ks+1 (n >= 0), from
+// (lambda_{m_hi+1}, lambda_{m_hi+2}) in lam set `src` (zeroed by the launcher
+// before the first launch) to set `dst`.  Step n computes lambda_n and, from the same stencil pass, the
+// gradient terms of lambda_{n+1} (L symmetric: <lambda, L u> = <L lambda, u>):
+//   dc2 += L(lambda_{n+1}) u_n,  dd += lambda_{n+1} (u_{n-1} - u_n)
+// over the owned cells.  In the waves that hold owned rows, the stored
+// states F_k = S[m_hi + 1 - k] (step s needs F_s = u_n and F_{s+1} = u_{n-1})
+// stream through a ring of four register strips, loaded three steps ahead.
+// Every lane of those waves loads (lanes outside the owned columns re-read
+// an owned column's cache lines, rows past the grid its last row), so that
+// with no branch around the loads each wait covers exactly the strip it
+// needs.  Rows outside the grid meet a zero Laplacian and a zero lambda.  The
+// source terms of the launch's steps are read once into LDS, so that no step
+// waits on a vector load.  The schedule runs n down to 0 so that lambda_1's
+// terms are included.
+struct BwdShared {
+  float edge[2][kWaves][2][64];
+  float srcv[kHalo];  // 2 (out[n-1] - tgt[n-1]) of step s, 0 for n = 0
+};
+
+template <bool OWNED>
+__device__ __forceinline__ void bwd_strip(const MemArgs& a, const Strip& st, BwdShared& sh, int m_hi, int ks, int src,
+                                          int dst, double& gc, double& gd) {
+  const size_t G = (size_t)a.R * a.C;
+  const float c2 = a.prm[0], d = a.prm[1];
+  const float ad = 2.0f - d, bd = 1.0f - d;
+  float keep[kRows];
+  keep_mask(st, keep);
+  float x[kRows], y[kRows];  // lambda_{n+1}, lambda_{n+2}
+  const float* ls = a.lam + (size_t)src * 2 * G;
+  load_rows(st, ls, a.C, x);
+  load_rows(st, ls + G, a.C, y);
+  // ring loads: the lane's column clamped to the owned columns inside the
+  // grid, the row clamped to the grid (byte offsets below 2^30)
+  const int x0 = blockIdx.x * kTile;
+  const unsigned colb = 4u * (unsigned)min(max(st.gx, x0), min(x0 + kTile, a.C) - 1);
+  auto fetch = [&](int k, float (&f)[kRows]) {
+    const char* base = reinterpret_cast<const char*>(a.S + (size_t)(m_hi + 1 - min(k, ks)) * G);
 #pragma unroll
-      for (int j = 0; j < kCells; ++j) {
-        const int r = cell_row(j), gy = ry0 + r;
-        if (r < kHalo || r >= kHalo + kTile || gy >= a.R) continue;
-        const float v = cur[r * kSide + c];
-        dst[(size_t)gy * a.C + gx] = v;
-        if (gy == a.py && gx == a.px) a.out[n0 + s] = v;
+    for (int q = 0; q < kRows; ++q) {
+      const unsigned rowb = 4u * (unsigned)(min(st.gy0 + q, a.R - 1) * a.C);
+      f[q] = *reinterpret_cast<const float*>(base + (rowb + colb));
+    }
+  };
+  float f0[kRows], f1[kRows], f2[kRows], f3[kRows];
+  if constexpr (OWNED) {
+    fetch(0, f0);
+    fetch(1, f1);
+    fetch(2, f2);
+    fetch(3, f3);
+  }
+  // all loads issued: now zero the adjoint outside the grid
+#pragma unroll
+  for (int q = 0; q < kRows; ++q) {
+    x[q] *= keep[q];
+    y[q] *= keep[q];
+  }
+  // (lambda_{n+1}, lambda_{n+2}) -> lam2 = lambda_n; fa = u_n, fb = u_{n-1};
+  // fa is then refilled with F_{s+4} (F_ks again past the launch's end).
+  auto step = [&](const float (&lam1)[kRows], float (&lam2)[kRows], float (&fa)[kRows], const float (&fb)[kRows],
+                  int s) {
+    float up, dn;
+    exchange_edges(sh.edge[s & 1], st, lam1, up, dn);
+    float lap[kRows];
+    auto row = [&](int q) {
+      lap[q] = lap_row(lam1, up, dn, q) * keep[q];
+      lam2[q] = (ad * lam1[q] + c2 * lap[q]) - bd * lam2[q];
+    };
+#pragma unroll
+    for (int q = 1; q < kRows - 1; ++q) row(q);
+    row(0);
+    row(kRows - 1);
+    if (st.pw >= 0) {  // uniform: only the wave holding the pickup row
+      const float src_lane = st.prow >= 0 ? sh.srcv[s] : 0.0f;
+#pragma unroll
+      for (int q = 0; q < kRows; ++q) lam2[q] += q == st.pw ? src_lane : 0.0f;
+    }
+    if constexpr (OWNED) {
+      if (st.own) {
+#pragma unroll
+        for (int q = 0; q < kRows; ++q) {
+          gc += (double)(lap[q] * fa[q]);
+          gd += (double)(lam1[q] * (fb[q] - fa[q]));
+        }
+      }
+      fetch(s + 4, fa);
+    }
+  };
+  // Whole groups of four steps, then the rest: no exit or store inside the
+  // pipelined loop, so the waits on the ring stay exact.
+  int s = 0;
+  for (; s + 4 <= ks; s += 4) {
+    step(x, y, f0, f1, s);
+    step(y, x, f1, f2, s + 1);
+    step(x, y, f2, f3, s + 2);
+    step(y, x, f3, f0, s + 3);
+  }
+  if (s < ks) {
+    step(x, y, f0, f1, s);
+    if (s + 1 < ks) {
+      step(y, x, f1, f2, s + 1);
+      if (s + 2 < ks) step(x, y, f2, f3, s + 2);
+    }
+  }
+  // boundary fields (lambda_{m_lo}, lambda_{m_lo+1}) of the owned cells -> set dst
+  if constexpr (OWNED) {
+    if (st.own) {
+      float* o = a.lam + (size_t)dst * 2 * G;
+      const bool odd = (ks & 1) != 0;  // an odd step count leaves the newest field in y
+#pragma unroll
+      for (int q = 0; q < kRows; ++q) {
+        if (q >= st.qhi) continue;
+        o[st.at(q, a.C)] = odd ? y[q] : x[q];
+        o[G + st.at(q, a.C)] = odd ? x[q] : y[q];
       }
     }
   }
 }
 
-// Backward: adjoint steps n = m_hi .. m_hi-ks+1 (n >= 0), from
-// (lambda_{m_hi+1}, lambda_{m_hi+2}) in lam set `src` (zero when src < 0) to
-// set `dst`.  Step n computes lambda_n and, from the same stencil pass, the
-// gradient terms of lambda_{n+1} (L symmetric: <lambda, L u> = <L lambda, u>):
-//   dc2 += L(lambda_{n+1}) u_n,  dd += lambda_{n+1} (u_{n-1} - u_n)
-// over the owned cells, whose two state values are prefetched a step ahead.
-// The schedule runs n down to 0 so that lambda_1's terms are included.
 __global__ __launch_bounds__(kThreads) void k_mem_bwd(MemArgs a, int m_hi, int ks, int src, int dst, int first) {
-  __shared__ float f[2][kSide * kSide];
-  __shared__ double red[2][kThreads / 64];
-  constexpr int kOwn = kTile / 4;  // owned cells per owning thread: rows j = 4 .. 11
-  const int y0 = blockIdx.y * kTile, x0 = blockIdx.x * kTile;
-  const int ry0 = y0 - kHalo, rx0 = x0 - kHalo;
-  const size_t G = (size_t)a.R * a.C;
-  const float c2 = a.prm[0], d = a.prm[1];
-  const float ad = 2.0f - d, bd = 1.0f - d;
-  float* cur = f[0];  // lambda_{n+1}
-  float* prv = f[1];  // lambda_{n+2}
-  const float* ls = src >= 0 ? a.lam + (size_t)src * 2 * G : nullptr;
-  load_region(a, ls, ls ? ls + G : nullptr, cur, prv, ry0, rx0);
-  const int c = cell_col(), gx = rx0 + c;
-  const bool cin = gx >= 0 && gx < a.C;
-  const bool own_col = cin && c >= kHalo && c < kHalo + kTile;
-  // owned cell q = row (t >> 6) + 4 (q + 4): grid index, or -1 outside the grid
-  size_t gi[kOwn];
-  bool gin[kOwn];
-#pragma unroll
-  for (int q = 0; q < kOwn; ++q) {
-    const int gy = ry0 + cell_row(q + 4);
-    gin[q] = own_col && gy < a.R;
-    gi[q] = gin[q] ? (size_t)gy * a.C + gx : 0;
+  __shared__ BwdShared sh;
+  __shared__ double red[2][kWaves];
+  if ((int)threadIdx.x < ks) {
+    const int n = m_hi - (int)threadIdx.x;
+    sh.srcv[threadIdx.x] = n >= 1 ? 2.0f * (a.out[n - 1] - a.tgt[n - 1]) : 0.0f;
   }
-  float ua[kOwn], ub[kOwn];  // u_n, u_{n-1} at the owned cells for the current step
-  auto fetch = [&](int n, float* va, float* vb) {
-    const float* sa = a.S + (size_t)(n + 1) * G;
-    const float* sb = a.S + (size_t)n * G;
-#pragma unroll
-    for (int q = 0; q < kOwn; ++q) {
-      va[q] = gin[q] ? sa[gi[q]] : 0.0f;
-      vb[q] = gin[q] ? sb[gi[q]] : 0.0f;
-    }
-  };
-  fetch(m_hi, ua, ub);
+  const Strip st(a);
   double gc = 0.0, gd = 0.0;
-  __syncthreads();
-  for (int s = 0; s < ks; ++s) {
-    const int n = m_hi - s;
-    float na[kOwn], nb[kOwn];
-    if (s + 1 < ks) fetch(n - 1, na, nb);
-    const int lo = kHalo + 1 - ks + s, hi = kHalo + kTile - 1 + ks - s;
-    const float src_val = n >= 1 ? 2.0f * (a.out[n - 1] - a.tgt[n - 1]) : 0.0f;
-    if (cin && c >= lo && c < hi) {
-#pragma unroll
-      for (int j = 0; j < kCells; ++j) {
-        const int r = cell_row(j), gy = ry0 + r;
-        if (r < lo || r >= hi || gy < 0 || gy >= a.R) continue;
-        const int i = r * kSide + c;
-        const float lap = lap5(cur, i);
-        float lam = (ad * cur[i] + c2 * lap) - bd * prv[i];
-        if (gy == a.py && gx == a.px) lam += src_val;
-        if (j >= 4 && j < 4 + kOwn && own_col) {
-          gc += (double)(lap * ua[j - 4]);
-          gd += (double)(cur[i] * (ub[j - 4] - ua[j - 4]));
-        }
-        prv[i] = lam;
-      }
-    }
-    lds_barrier();
-    float* t = cur;
-    cur = prv;
-    prv = t;
-    if (s + 1 < ks) {
-#pragma unroll
-      for (int q = 0; q < kOwn; ++q) {
-        ua[q] = na[q];
-        ub[q] = nb[q];
-      }
-    }
-  }
-  // boundary adjoint fields of this launch: (lambda_{m_lo}, lambda_{m_lo+1}) -> set dst
-  if (own_col) {
-    float* o = a.lam + (size_t)dst * 2 * G;
-#pragma unroll
-    for (int q = 0; q < kOwn; ++q) {
-      if (!gin[q]) continue;
-      const int i = cell_row(q + 4) * kSide + c;
-      o[gi[q]] = cur[i];
-      o[G + gi[q]] = prv[i];
-    }
-  }
+  if (st.own_w)
+    bwd_strip<true>(a, st, sh, m_hi, ks, src, dst, gc, gd);
+  else
+    bwd_strip<false>(a, st, sh, m_hi, ks, src, dst, gc, gd);
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
     gc += __shfl_xor(gc, off, 64);
     gd += __shfl_xor(gd, off, 64);
   }
-  if ((threadIdx.x & 63) == 0) {
-    red[0][threadIdx.x >> 6] = gc;
-    red[1][threadIdx.x >> 6] = gd;
+  if (st.lane == 0) {
+    red[0][st.w] = gc;
+    red[1][st.w] = gd;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
     double sc = 0.0, sd = 0.0;
-    for (int w = 0; w < kThreads / 64; ++w) {
+    for (int w = 0; w < kWaves; ++w) {
       sc += red[0][w];
       sd += red[1][w];
     }
@@ -238,6 +355,11 @@ __global__ void k_mem_init(const float* __restrict__ u0, float* __restrict__ S, 
     S[i] = v;
     S[G + i] = v;
   }
+}
+
+// f[i] = 0 for i < n.
+__global__ void k_mem_zero(float* __restrict__ f, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) f[i] = 0.0f;
 }
 
 // grads[q] = sum over tiles of the fp64 partials, in tile order.
@@ -333,7 +455,11 @@ int launch_membrane_bwd(const Launch& L, const dgen_hip_op& op) {
                      cell(L, lt), (int)T);
   DGEN_LAUNCH_CHECK("k_mem_loss_terms");
   const dim3 grid((unsigned)((C + kTile - 1) / kTile), (unsigned)((R + kTile - 1) / kTile));
-  int src = -1, dst = 0;
+  // (lambda_{T+1}, lambda_{T+2}) = 0: set 1 starts zeroed
+  const unsigned zb = (unsigned)std::min<int64_t>((2 * G + 255) / 256, (int64_t)L.cu_count * 8);
+  hipLaunchKernelGGL(k_mem_zero, dim3(zb), dim3(256), 0, L.stream, a.lam + 2 * G, (size_t)(2 * G));
+  DGEN_LAUNCH_CHECK("k_mem_zero");
+  int src = 1, dst = 0;
   bool first = true;
   for (int64_t m_hi = T; m_hi >= 0; m_hi -= ks) {
     const int n = (int)std::min<int64_t>(ks, m_hi + 1);
