@@ -13,11 +13,16 @@
 // recomputing it (4801 fields of 1 MB at 512^2 x 4800).
 //
 // Temporal blocking: a workgroup owns a kTile x kTile tile and advances a
-// kSide x kSide region (the tile plus a kHalo ring) of the two live fields.
-// One launch advances ks <= kHalo steps: values near the region edge go
-// wrong (their outside neighbours read as zero) but the error front moves one
-// cell per step, so after ks steps the owned tile is still exact and no
-// workgroup needs another's data until the next launch.
+// kSide x kSide region around it (the tile plus a kHalo ring where the grid
+// allows) of the two live fields.  One launch advances ks <= kHalo steps:
+// values next to a region edge that lies inside the grid go wrong (their
+// outside neighbours read as zero) but the error front moves one cell per
+// step, so after ks steps the owned tile is still exact and no workgroup
+// needs another's data until the next launch.  On grids of at least kSide
+// cells each way the region is placed inside the grid: a region edge that is
+// a grid edge then reads the exact zero padding and no cell needs a mask.
+// Smaller grids centre the region on the tile and zero the cells outside the
+// grid by a per-row mask.
 //
 // Register strips: the region is 64 columns wide, one per wavefront lane;
 // wave w holds rows kRows*w .. kRows*w + kRows - 1 of its lane's column for
@@ -25,8 +30,6 @@
 // own registers (the strip's first and last rows from the waves above and
 // below, through a small double-buffered LDS edge table: one barrier per
 // step); horizontal neighbours from the adjacent lanes by DPP wave shifts.
-// Every cell of the region is updated each step; cells outside the grid are
-// then reset to zero (the conv2d zero padding).
 //
 // Adjoint (L is symmetric): lambda_n = g_n + (2-d) lambda_{n+1}
 // + c2 L lambda_{n+1} - (1-d) lambda_{n+2}, g_n = 2 (out[n-1] - tgt[n-1]) at
@@ -42,11 +45,10 @@ namespace {
 constexpr int kTile = 32;
 constexpr int kHalo = 16;
 constexpr int kSide = kTile + 2 * kHalo;  // 64: one wavefront lane per region column
-constexpr int kRows = 16;                 // region rows per thread
+constexpr int kRows = 4;                  // region rows per thread (four waves per SIMD)
 constexpr int kWaves = kSide / kRows;
 constexpr int kThreads = 64 * kWaves;
 static_assert(kSide == 64, "one region column per wavefront lane");
-static_assert(kHalo % kRows == 0 && kTile % kRows == 0, "owned rows must fill whole strips");
 
 struct MemArgs {
   float* S;           // state store [(T + 2)][R][C]
@@ -67,57 +69,91 @@ __device__ __forceinline__ float from_right(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x130, 0xf, 0xf, false));
 }
 
-// Where this thread's strip lies in the grid.
+// Where this thread's strip lies in the grid (INSIDE: the region is placed
+// inside the grid).  Row offsets are uniform per wave; with the column's byte
+// offset they address a field as base + row + column.
+template <bool INSIDE>
 struct Strip {
   int lane, w;
   int gx, gy0;    // grid column; grid row of strip row 0
-  int qlo, qhi;   // strip rows [qlo, qhi) are inside the grid (uniform per wave)
-  int off0;       // gy0 * C + gx: field offset of strip row 0 (used for rows inside the grid)
-  bool cin;       // column inside the grid
-  bool own_w;     // the strip holds owned rows (uniform per wave)
-  bool own;       // owned cells: an owned strip and an owned column inside the grid
+  int R, C;
+  int oq0, oq1;   // owned strip rows [oq0, oq1) (uniform per wave)
+  bool own_lane;  // the lane's column is owned
   int prow;       // strip row of the pickup cell in this lane, or -1
-  int pw;         // strip row of the pickup cell if its row lies in this strip and its column in the region, else -1 (uniform per wave)
+  int pw;         // strip row of the pickup row if the pickup lies in this strip's rows and the region's columns, else -1
+  unsigned colb;  // 4 * column, clamped into the grid
+  unsigned ownb;  // 4 * column, clamped into the owned columns
 
-  __device__ Strip(const MemArgs& a) {
+  __device__ Strip(const MemArgs& a) : R(a.R), C(a.C) {
     lane = threadIdx.x & 63;
     w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
-    gx = blockIdx.x * kTile - kHalo + lane;
-    gy0 = blockIdx.y * kTile - kHalo + kRows * w;
-    qlo = max(0, -gy0);
-    qhi = min(kRows, a.R - gy0);
-    off0 = gy0 * a.C + gx;
-    cin = gx >= 0 && gx < a.C;
-    own_w = kRows * w >= kHalo && kRows * w < kHalo + kTile;
-    own = own_w && cin && lane >= kHalo && lane < kHalo + kTile;
-    prow = (gx == a.px && a.py - gy0 >= 0 && a.py - gy0 < kRows) ? a.py - gy0 : -1;
-    const int px_lane = a.px - (blockIdx.x * kTile - kHalo);
-    pw = (px_lane >= 0 && px_lane < 64 && a.py - gy0 >= 0 && a.py - gy0 < kRows) ? a.py - gy0 : -1;
+    const int tx0 = blockIdx.x * kTile, ty0 = blockIdx.y * kTile;
+    const int tx1 = min(tx0 + kTile, a.C), ty1 = min(ty0 + kTile, a.R);
+    int rx0 = tx0 - kHalo, ry0 = ty0 - kHalo;
+    if constexpr (INSIDE) {
+      rx0 = min(max(rx0, 0), a.C - kSide);
+      ry0 = min(max(ry0, 0), a.R - kSide);
+    }
+    gx = rx0 + lane;
+    gy0 = ry0 + kRows * w;
+    oq0 = min(max(ty0 - gy0, 0), kRows);
+    oq1 = min(max(ty1 - gy0, 0), kRows);
+    own_lane = gx >= tx0 && gx < tx1;
+    const int pq = a.py - gy0;
+    prow = (gx == a.px && pq >= 0 && pq < kRows) ? pq : -1;
+    pw = (a.px - rx0 >= 0 && a.px - rx0 < 64 && pq >= 0 && pq < kRows) ? pq : -1;
+    colb = 4u * (unsigned)min(max(gx, 0), a.C - 1);
+    ownb = 4u * (unsigned)min(max(gx, tx0), tx1 - 1);
   }
-  __device__ bool in(int q) const { return cin && q >= qlo && q < qhi; }
-  // Field offset of row q (grids hold at most 2^28 cells: 32 bits suffice).
-  __device__ unsigned at(int q, int C) const { return (unsigned)(off0 + q * C); }
+  __device__ bool own_rows() const { return oq0 < oq1; }
+  __device__ bool all_rows_owned() const { return oq0 == 0 && oq1 == kRows; }
+  // bit q set for owned strip rows
+  __device__ unsigned own_mask() const { return ((1u << oq1) - 1u) & ~((1u << oq0) - 1u); }
+  // cell (q, lane) is inside the grid
+  __device__ bool in(int q) const {
+    if constexpr (INSIDE) return true;
+    return gx >= 0 && gx < C && gy0 + q >= 0 && gy0 + q < R;
+  }
+  // byte offset of strip row q's grid row (clamped into the grid; below 2^30)
+  __device__ unsigned rowb(int q) const { return 4u * (unsigned)(min(max(gy0 + q, 0), R - 1) * C); }
 };
 
-// Reads rows of field f at this strip; rows outside the grid read cell 0,
-// so that the loads issue back to back with no branch or wait between them.
-__device__ __forceinline__ void load_rows(const Strip& st, const float* f, int C, float (&v)[kRows]) {
-#pragma unroll
-  for (int q = 0; q < kRows; ++q) v[q] = f[st.in(q) ? st.at(q, C) : 0u];
+// A field of R x C cells as a raw buffer: loads and stores address it by a
+// per-lane column offset plus a uniform row offset (an SGPR operand), and
+// the hardware drops any access past its G cells.
+using Field = __amdgpu_buffer_rsrc_t;
+__device__ __forceinline__ Field field(const float* f, size_t G) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(f), 0, (int)(G * sizeof(float)), 0x00020000);
+}
+__device__ __forceinline__ float fload(Field f, unsigned col, unsigned row) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(f, col, row, 0));
+}
+__device__ __forceinline__ void fstore(float v, Field f, unsigned col, unsigned row) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), f, col, row, 0);
 }
 
-// load_rows, zero outside the grid (keep = 0 there).
-__device__ __forceinline__ void load_strip(const Strip& st, const float* f, int C, const float (&keep)[kRows],
-                                           float (&v)[kRows]) {
-  load_rows(st, f, C, v);
+// Reads strip rows of field f (cells outside the grid read a clamped cell).
+template <bool INSIDE>
+__device__ __forceinline__ void load_rows(const Strip<INSIDE>& st, Field f, float (&v)[kRows]) {
 #pragma unroll
-  for (int q = 0; q < kRows; ++q) v[q] *= keep[q];
+  for (int q = 0; q < kRows; ++q) v[q] = fload(f, st.colb, st.rowb(q));
+}
+
+// 1 for cells inside the grid, 0 outside (centred regions only).  The
+// kernels scale the Laplacian by it: a cell outside the grid starts at zero
+// and its update (2u - u_prev + c2 L u - d (u - u_prev) forward, the same form
+// backward) then stays exactly zero.
+template <bool INSIDE>
+__device__ __forceinline__ void keep_mask(const Strip<INSIDE>& st, float (&keep)[kRows]) {
+#pragma unroll
+  for (int q = 0; q < kRows; ++q) keep[q] = st.in(q) ? 1.0f : 0.0f;
 }
 
 // Publishes the strip's first and last rows of u and returns the row above
 // the strip and the row below it (zero at the region edge).
-__device__ __forceinline__ void exchange_edges(float (*e)[2][64], const Strip& st, const float (&u)[kRows], float& up,
-                                               float& dn) {
+template <bool INSIDE>
+__device__ __forceinline__ void exchange_edges(float (*e)[2][64], const Strip<INSIDE>& st, const float (&u)[kRows],
+                                               float& up, float& dn) {
   e[st.w][0][st.lane] = u[0];
   e[st.w][1][st.lane] = u[kRows - 1];
   lds_barrier();
@@ -133,33 +169,34 @@ __device__ __forceinline__ float lap_row(const float (&u)[kRows], float up, floa
   return (((n + from_left(u[q])) + u[q] * -4.0f) + from_right(u[q])) + s;
 }
 
-// 1 for strip rows inside the grid, 0 outside: a multiplier rather than a
-// branch, so that every lane runs the stencil (the DPP shifts read all 64).
-// The kernels scale the Laplacian by it: a cell outside the grid starts at
-// zero and its update (2u - u_prev + c2 L u - d (u - u_prev) forward, the
-// same form backward) then stays exactly zero.
-__device__ __forceinline__ void keep_mask(const Strip& st, float (&keep)[kRows]) {
-#pragma unroll
-  for (int q = 0; q < kRows; ++q) keep[q] = st.in(q) ? 1.0f : 0.0f;
-}
-
 // Forward: frames n0 .. n0+ks-1 (u_{n0+1} .. u_{n0+ks}).
+template <bool INSIDE>
 __global__ __launch_bounds__(kThreads) void k_mem_fwd(MemArgs a, int n0, int ks) {
   __shared__ float edge[2][kWaves][2][64];
-  const Strip st(a);
+  const Strip<INSIDE> st(a);
   const size_t G = (size_t)a.R * a.C;
   const float c2 = a.prm[0], d = a.prm[1];
   float keep[kRows];
-  keep_mask(st, keep);
+  if constexpr (!INSIDE) keep_mask(st, keep);
   float u[kRows], v[kRows];  // u_n, u_{n-1}
-  load_strip(st, a.S + (size_t)(n0 + 1) * G, a.C, keep, u);
-  load_strip(st, a.S + (size_t)n0 * G, a.C, keep, v);
+  load_rows(st, field(a.S + (size_t)(n0 + 1) * G, G), u);
+  load_rows(st, field(a.S + (size_t)n0 * G, G), v);
+  if constexpr (!INSIDE) {
+#pragma unroll
+    for (int q = 0; q < kRows; ++q) {
+      u[q] *= keep[q];
+      v[q] *= keep[q];
+    }
+  }
+  // the owned copy of the pickup cell (copies next to a region edge go wrong)
+  const bool pick = st.own_lane && st.prow >= st.oq0 && st.prow < st.oq1;
   // (cur, prv) -> prv = the next state; owned cells -> S[n0+s+2], pickup -> out[n0+s]
   auto step = [&](const float (&cur)[kRows], float (&prv)[kRows], int s) {
     float up, dn;
     exchange_edges(edge[s & 1], st, cur, up, dn);
     auto row = [&](int q) {
-      const float lap = lap_row(cur, up, dn, q) * keep[q];
+      float lap = lap_row(cur, up, dn, q);
+      if constexpr (!INSIDE) lap *= keep[q];
       const float b = cur[q] * 2.0f - prv[q];
       const float g = (cur[q] - prv[q]) * d;
       prv[q] = (b + lap * c2) - g;
@@ -169,17 +206,20 @@ __global__ __launch_bounds__(kThreads) void k_mem_fwd(MemArgs a, int n0, int ks)
     for (int q = 1; q < kRows - 1; ++q) row(q);
     row(0);
     row(kRows - 1);
-    if (st.own) {
-      float* dst = a.S + (size_t)(n0 + s + 2) * G;
-      if (st.qhi == kRows) {  // owned strips start inside the grid; most end inside it too
+    if (st.own_rows()) {
+      const Field dst = field(a.S + (size_t)(n0 + s + 2) * G, G);
+      if (st.own_lane) {
+        if (st.all_rows_owned()) {
 #pragma unroll
-        for (int q = 0; q < kRows; ++q) dst[st.at(q, a.C)] = prv[q];
-      } else {
+          for (int q = 0; q < kRows; ++q) fstore(prv[q], dst, st.colb, st.rowb(q));
+        } else {
+          const unsigned m = st.own_mask();
 #pragma unroll
-        for (int q = 0; q < kRows; ++q)
-          if (q < st.qhi) dst[st.at(q, a.C)] = prv[q];
+          for (int q = 0; q < kRows; ++q)
+            if ((m >> q) & 1u) fstore(prv[q], dst, st.colb, st.rowb(q));
+        }
       }
-      if (st.prow >= 0) {  // only the owned copy is exact at the region edge
+      if (pick) {
 #pragma unroll
         for (int q = 0; q < kRows; ++q)
           if (q == st.prow) a.out[n0 + s] = prv[q];
@@ -196,60 +236,59 @@ __global__ __launch_bounds__(kThreads) void k_mem_fwd(MemArgs a, int n0, int ks)
 
 // Backward: adjoint steps n = m_hi .. m_hi-ks+1 (n >= 0), from
 // (lambda_{m_hi+1}, lambda_{m_hi+2}) in lam set `src` (zeroed by the launcher
-// before the first launch) to set `dst`.  Step n computes lambda_n and, from the same stencil pass, the
-// gradient terms of lambda_{n+1} (L symmetric: <lambda, L u> = <L lambda, u>):
+// before the first launch) to set `dst`.  Step n computes lambda_n and, from
+// the same stencil pass, the gradient terms of lambda_{n+1} (L symmetric:
+// <lambda, L u> = <L lambda, u>):
 //   dc2 += L(lambda_{n+1}) u_n,  dd += lambda_{n+1} (u_{n-1} - u_n)
-// over the owned cells.  In the waves that hold owned rows, the stored
-// states F_k = S[m_hi + 1 - k] (step s needs F_s = u_n and F_{s+1} = u_{n-1})
-// stream through a ring of four register strips, loaded three steps ahead.
-// Every lane of those waves loads (lanes outside the owned columns re-read
-// an owned column's cache lines, rows past the grid its last row), so that
-// with no branch around the loads each wait covers exactly the strip it
-// needs.  Rows outside the grid meet a zero Laplacian and a zero lambda.  The
-// source terms of the launch's steps are read once into LDS, so that no step
-// waits on a vector load.  The schedule runs n down to 0 so that lambda_1's
-// terms are included.
+// over the owned cells: per cell in fp32 over the launch's steps, then in
+// fp64 over cells, workgroup partials and launches.  In the waves that hold
+// owned rows, the stored states F_k = S[m_hi + 1 - k] (step s needs
+// F_s = u_n and F_{s+1} = u_{n-1}) stream through a ring of four register
+// strips, loaded three steps ahead.  Every lane and row of those waves loads
+// (from its owned column and grid row, clamped), so that with no branch
+// around the loads each wait covers exactly the strip it needs; the sums
+// keep only the owned cells.  The source terms of the launch's steps are read
+// once into LDS, so that no step waits on a vector load.  The schedule runs
+// n down to 0 so that lambda_1's terms are included.
 struct BwdShared {
   float edge[2][kWaves][2][64];
   float srcv[kHalo];  // 2 (out[n-1] - tgt[n-1]) of step s, 0 for n = 0
 };
 
-template <bool OWNED>
-__device__ __forceinline__ void bwd_strip(const MemArgs& a, const Strip& st, BwdShared& sh, int m_hi, int ks, int src,
-                                          int dst, double& gc, double& gd) {
+template <bool INSIDE, bool OWNED>
+__device__ __forceinline__ void bwd_strip(const MemArgs& a, const Strip<INSIDE>& st, BwdShared& sh, int m_hi, int ks,
+                                          int src, int dst, double& gc, double& gd) {
   const size_t G = (size_t)a.R * a.C;
   const float c2 = a.prm[0], d = a.prm[1];
   const float ad = 2.0f - d, bd = 1.0f - d;
   float keep[kRows];
-  keep_mask(st, keep);
+  if constexpr (!INSIDE) keep_mask(st, keep);
   float x[kRows], y[kRows];  // lambda_{n+1}, lambda_{n+2}
   const float* ls = a.lam + (size_t)src * 2 * G;
-  load_rows(st, ls, a.C, x);
-  load_rows(st, ls + G, a.C, y);
-  // ring loads: the lane's column clamped to the owned columns inside the
-  // grid, the row clamped to the grid (byte offsets below 2^30)
-  const int x0 = blockIdx.x * kTile;
-  const unsigned colb = 4u * (unsigned)min(max(st.gx, x0), min(x0 + kTile, a.C) - 1);
+  load_rows(st, field(ls, G), x);
+  load_rows(st, field(ls + G, G), y);
   auto fetch = [&](int k, float (&f)[kRows]) {
-    const char* base = reinterpret_cast<const char*>(a.S + (size_t)(m_hi + 1 - min(k, ks)) * G);
+    const Field F = field(a.S + (size_t)(m_hi + 1 - min(k, ks)) * G, G);
 #pragma unroll
-    for (int q = 0; q < kRows; ++q) {
-      const unsigned rowb = 4u * (unsigned)(min(st.gy0 + q, a.R - 1) * a.C);
-      f[q] = *reinterpret_cast<const float*>(base + (rowb + colb));
-    }
+    for (int q = 0; q < kRows; ++q) f[q] = fload(F, st.ownb, st.rowb(q));
   };
   float f0[kRows], f1[kRows], f2[kRows], f3[kRows];
+  float acc_c[kRows], acc_d[kRows];
   if constexpr (OWNED) {
     fetch(0, f0);
     fetch(1, f1);
     fetch(2, f2);
     fetch(3, f3);
+#pragma unroll
+    for (int q = 0; q < kRows; ++q) acc_c[q] = acc_d[q] = 0.0f;
   }
   // all loads issued: now zero the adjoint outside the grid
+  if constexpr (!INSIDE) {
 #pragma unroll
-  for (int q = 0; q < kRows; ++q) {
-    x[q] *= keep[q];
-    y[q] *= keep[q];
+    for (int q = 0; q < kRows; ++q) {
+      x[q] *= keep[q];
+      y[q] *= keep[q];
+    }
   }
   // (lambda_{n+1}, lambda_{n+2}) -> lam2 = lambda_n; fa = u_n, fb = u_{n-1};
   // fa is then refilled with F_{s+4} (F_ks again past the launch's end).
@@ -259,7 +298,8 @@ __device__ __forceinline__ void bwd_strip(const MemArgs& a, const Strip& st, Bwd
     exchange_edges(sh.edge[s & 1], st, lam1, up, dn);
     float lap[kRows];
     auto row = [&](int q) {
-      lap[q] = lap_row(lam1, up, dn, q) * keep[q];
+      lap[q] = lap_row(lam1, up, dn, q);
+      if constexpr (!INSIDE) lap[q] *= keep[q];
       lam2[q] = (ad * lam1[q] + c2 * lap[q]) - bd * lam2[q];
     };
 #pragma unroll
@@ -272,12 +312,10 @@ __device__ __forceinline__ void bwd_strip(const MemArgs& a, const Strip& st, Bwd
       for (int q = 0; q < kRows; ++q) lam2[q] += q == st.pw ? src_lane : 0.0f;
     }
     if constexpr (OWNED) {
-      if (st.own) {
 #pragma unroll
-        for (int q = 0; q < kRows; ++q) {
-          gc += (double)(lap[q] * fa[q]);
-          gd += (double)(lam1[q] * (fb[q] - fa[q]));
-        }
+      for (int q = 0; q < kRows; ++q) {
+        acc_c[q] = fmaf(lap[q], fa[q], acc_c[q]);
+        acc_d[q] = fmaf(lam1[q], fb[q] - fa[q], acc_d[q]);
       }
       fetch(s + 4, fa);
     }
@@ -298,38 +336,51 @@ __device__ __forceinline__ void bwd_strip(const MemArgs& a, const Strip& st, Bwd
       if (s + 2 < ks) step(x, y, f2, f3, s + 2);
     }
   }
-  // boundary fields (lambda_{m_lo}, lambda_{m_lo+1}) of the owned cells -> set dst
   if constexpr (OWNED) {
-    if (st.own) {
-      float* o = a.lam + (size_t)dst * 2 * G;
+    if (st.own_lane) {
+      // boundary fields (lambda_{m_lo}, lambda_{m_lo+1}) of the owned cells -> set dst
+      const float* o = a.lam + (size_t)dst * 2 * G;
+      const Field o0 = field(o, G), o1 = field(o + G, G);
       const bool odd = (ks & 1) != 0;  // an odd step count leaves the newest field in y
+      const unsigned m = st.own_mask();
 #pragma unroll
       for (int q = 0; q < kRows; ++q) {
-        if (q >= st.qhi) continue;
-        o[st.at(q, a.C)] = odd ? y[q] : x[q];
-        o[G + st.at(q, a.C)] = odd ? x[q] : y[q];
+        if (!((m >> q) & 1u)) continue;
+        fstore(odd ? y[q] : x[q], o0, st.colb, st.rowb(q));
+        fstore(odd ? x[q] : y[q], o1, st.colb, st.rowb(q));
+        gc += (double)acc_c[q];
+        gd += (double)acc_d[q];
       }
     }
   }
 }
 
+template <bool INSIDE>
 __global__ __launch_bounds__(kThreads) void k_mem_bwd(MemArgs a, int m_hi, int ks, int src, int dst, int first) {
   __shared__ BwdShared sh;
   __shared__ double red[2][kWaves];
+  double* gp = a.gpart + 2 * (blockIdx.y * gridDim.x + blockIdx.x);
+  double prev_c = 0.0, prev_d = 0.0;  // this tile's partials so far, read early
+  if (threadIdx.x == 0 && !first) {
+    prev_c = gp[0];
+    prev_d = gp[1];
+  }
   if ((int)threadIdx.x < ks) {
     const int n = m_hi - (int)threadIdx.x;
     sh.srcv[threadIdx.x] = n >= 1 ? 2.0f * (a.out[n - 1] - a.tgt[n - 1]) : 0.0f;
   }
-  const Strip st(a);
+  const Strip<INSIDE> st(a);
   double gc = 0.0, gd = 0.0;
-  if (st.own_w)
-    bwd_strip<true>(a, st, sh, m_hi, ks, src, dst, gc, gd);
+  if (st.own_rows())
+    bwd_strip<INSIDE, true>(a, st, sh, m_hi, ks, src, dst, gc, gd);
   else
-    bwd_strip<false>(a, st, sh, m_hi, ks, src, dst, gc, gd);
+    bwd_strip<INSIDE, false>(a, st, sh, m_hi, ks, src, dst, gc, gd);
+  if (st.own_rows()) {
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    gc += __shfl_xor(gc, off, 64);
-    gd += __shfl_xor(gd, off, 64);
+    for (int off = 32; off >= 1; off >>= 1) {
+      gc += __shfl_xor(gc, off, 64);
+      gd += __shfl_xor(gd, off, 64);
+    }
   }
   if (st.lane == 0) {
     red[0][st.w] = gc;
@@ -342,9 +393,8 @@ __global__ __launch_bounds__(kThreads) void k_mem_bwd(MemArgs a, int m_hi, int k
       sc += red[0][w];
       sd += red[1][w];
     }
-    double* gp = a.gpart + 2 * (blockIdx.y * gridDim.x + blockIdx.x);
-    gp[0] = first ? sc : gp[0] + sc;
-    gp[1] = first ? sd : gp[1] + sd;
+    gp[0] = prev_c + sc;
+    gp[1] = prev_d + sd;
   }
 }
 
@@ -415,8 +465,13 @@ int launch_membrane_fwd(const Launch& L, const dgen_hip_op& op) {
   hipLaunchKernelGGL(k_mem_init, dim3(ib), dim3(256), 0, L.stream, cell(L, u0), a.S, (size_t)G);
   DGEN_LAUNCH_CHECK("k_mem_init");
   const dim3 grid((unsigned)((C + kTile - 1) / kTile), (unsigned)((R + kTile - 1) / kTile));
+  const bool inside = R >= kSide && C >= kSide;  // regions placed inside the grid
   for (int64_t n0 = 0; n0 < T; n0 += ks) {
-    hipLaunchKernelGGL(k_mem_fwd, grid, dim3(kThreads), 0, L.stream, a, (int)n0, (int)std::min<int64_t>(ks, T - n0));
+    const int n = (int)std::min<int64_t>(ks, T - n0);
+    if (inside)
+      hipLaunchKernelGGL(k_mem_fwd<true>, grid, dim3(kThreads), 0, L.stream, a, (int)n0, n);
+    else
+      hipLaunchKernelGGL(k_mem_fwd<false>, grid, dim3(kThreads), 0, L.stream, a, (int)n0, n);
     DGEN_LAUNCH_CHECK("k_mem_fwd");
   }
   return 0;
@@ -459,11 +514,16 @@ int launch_membrane_bwd(const Launch& L, const dgen_hip_op& op) {
   const unsigned zb = (unsigned)std::min<int64_t>((2 * G + 255) / 256, (int64_t)L.cu_count * 8);
   hipLaunchKernelGGL(k_mem_zero, dim3(zb), dim3(256), 0, L.stream, a.lam + 2 * G, (size_t)(2 * G));
   DGEN_LAUNCH_CHECK("k_mem_zero");
+  const bool inside = R >= kSide && C >= kSide;  // regions placed inside the grid
   int src = 1, dst = 0;
   bool first = true;
   for (int64_t m_hi = T; m_hi >= 0; m_hi -= ks) {
     const int n = (int)std::min<int64_t>(ks, m_hi + 1);
-    hipLaunchKernelGGL(k_mem_bwd, grid, dim3(kThreads), 0, L.stream, a, (int)m_hi, n, src, dst, first ? 1 : 0);
+    if (inside)
+      hipLaunchKernelGGL(k_mem_bwd<true>, grid, dim3(kThreads), 0, L.stream, a, (int)m_hi, n, src, dst, first ? 1 : 0);
+    else
+      hipLaunchKernelGGL(k_mem_bwd<false>, grid, dim3(kThreads), 0, L.stream, a, (int)m_hi, n, src, dst,
+                         first ? 1 : 0);
     DGEN_LAUNCH_CHECK("k_mem_bwd");
     src = dst;
     dst ^= 1;
