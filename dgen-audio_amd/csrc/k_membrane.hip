@@ -125,11 +125,18 @@ using Field = __amdgpu_buffer_rsrc_t;
 __device__ __forceinline__ Field field(const float* f, size_t G) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(f), 0, (int)(G * sizeof(float)), 0x00020000);
 }
+// Cache policy operand: 0 = default, kStream = non-temporal (the gfx940
+// family's nt bit) for the forward's state stores: each state is written
+// once and read once, much later, by the backward, so its traffic need not
+// stay in the caches (non-temporal loads in the backward measured slower).
+constexpr int kStream = 2;
+template <int POLICY = 0>
 __device__ __forceinline__ float fload(Field f, unsigned col, unsigned row) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(f, col, row, 0));
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(f, col, row, POLICY));
 }
+template <int POLICY = 0>
 __device__ __forceinline__ void fstore(float v, Field f, unsigned col, unsigned row) {
-  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), f, col, row, 0);
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), f, col, row, POLICY);
 }
 
 // Reads strip rows of field f (cells outside the grid read a clamped cell).
@@ -211,12 +218,12 @@ __global__ __launch_bounds__(kThreads) void k_mem_fwd(MemArgs a, int n0, int ks)
       if (st.own_lane) {
         if (st.all_rows_owned()) {
 #pragma unroll
-          for (int q = 0; q < kRows; ++q) fstore(prv[q], dst, st.colb, st.rowb(q));
+          for (int q = 0; q < kRows; ++q) fstore<kStream>(prv[q], dst, st.colb, st.rowb(q));
         } else {
           const unsigned m = st.own_mask();
 #pragma unroll
           for (int q = 0; q < kRows; ++q)
-            if ((m >> q) & 1u) fstore(prv[q], dst, st.colb, st.rowb(q));
+            if ((m >> q) & 1u) fstore<kStream>(prv[q], dst, st.colb, st.rowb(q));
         }
       }
       if (pick) {
