@@ -92,7 +92,9 @@ def time_session(rt, program, args):
     """Warm up, time args.steps back-to-back runs, then profile every op and
     time the dominant one (largest roofline time) with HIP events."""
     from dgen_hip.roofline import step_roof_ms, table
-    log(f"bench: warmup {args.warmup}")
+    if args.graphs:
+        rt.set_graphs(True)
+    log(f"bench: warmup {args.warmup} (runs replayed as a HIP graph: {args.graphs})")
     for _ in range(args.warmup):
         rt.run_async()
     rt.sync()
@@ -332,6 +334,8 @@ def main() -> int:
     ap.add_argument("--cpu-lanes", type=int, default=4)
     ap.add_argument("--cpu-repeats", type=int, default=3)
     ap.add_argument("--op-iters", type=int, default=10, help="runs averaged for the dominant kernel's time")
+    ap.add_argument("--no-graphs", dest="graphs", action="store_false",
+                    help="enqueue every kernel from the host instead of replaying each step as a HIP graph")
     ap.add_argument("--workload", choices=("harmonic", "biquad", "stft", "membrane"), default="harmonic")
     ap.add_argument("--mem-steps", type=int, default=16, help="membrane frames per time-blocked launch")
     ap.add_argument("--chunk", type=int, default=256, help="biquad scan chunk length (frames)")

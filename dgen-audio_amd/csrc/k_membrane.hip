@@ -56,9 +56,19 @@ struct MemArgs {
   float* out;         // pickup [T]
   const float* tgt;   // target pickup [T] (backward)
   float* lam;         // adjoint boundary fields: 2 sets x (lambda_{m+1}, lambda_{m+2}) x [R][C]
-  double* gpart;      // [tiles][2] gradient partials (fp64: the terms cancel heavily)
+  double* gpart;      // [tiles][kTile * kTile][2] gradient partials (fp64: the terms cancel heavily)
   int R, C, T, py, px;
+  int tiles_x;        // tiles per grid row
 };
+
+// Tile of this workgroup.  Workgroups go to the eight XCDs in turn, so when
+// the tile count allows, block b takes tile (b % 8) * (tiles / 8) + b / 8:
+// each XCD then advances a contiguous band of tiles and the overlapping
+// regions of neighbouring tiles meet in that XCD's L2.
+__device__ __forceinline__ int tile_index() {
+  const int b = blockIdx.x, n = gridDim.x;
+  return (n % 8 == 0) ? (b % 8) * (n / 8) + b / 8 : b;
+}
 
 // Value of lane c - 1 (0 at lane 0) and of lane c + 1 (0 at lane 63):
 // DPP wave_shr:1 / wave_shl:1.
@@ -84,10 +94,14 @@ struct Strip {
   unsigned colb;  // 4 * column, clamped into the grid
   unsigned ownb;  // 4 * column, clamped into the owned columns
 
+  int tile;       // tile index (row-major)
+  int slot;       // this thread's gradient slot in the tile: (first owned row, column)
+
   __device__ Strip(const MemArgs& a) : R(a.R), C(a.C) {
     lane = threadIdx.x & 63;
     w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
-    const int tx0 = blockIdx.x * kTile, ty0 = blockIdx.y * kTile;
+    tile = tile_index();
+    const int tx0 = (tile % a.tiles_x) * kTile, ty0 = (tile / a.tiles_x) * kTile;
     const int tx1 = min(tx0 + kTile, a.C), ty1 = min(ty0 + kTile, a.R);
     int rx0 = tx0 - kHalo, ry0 = ty0 - kHalo;
     if constexpr (INSIDE) {
@@ -104,6 +118,7 @@ struct Strip {
     pw = (a.px - rx0 >= 0 && a.px - rx0 < 64 && pq >= 0 && pq < kRows) ? pq : -1;
     colb = 4u * (unsigned)min(max(gx, 0), a.C - 1);
     ownb = 4u * (unsigned)min(max(gx, tx0), tx1 - 1);
+    slot = (gy0 + oq0 - ty0) * kTile + (gx - tx0);
   }
   __device__ bool own_rows() const { return oq0 < oq1; }
   __device__ bool all_rows_owned() const { return oq0 == 0 && oq1 == kRows; }
@@ -362,46 +377,32 @@ __device__ __forceinline__ void bwd_strip(const MemArgs& a, const Strip<INSIDE>&
   }
 }
 
+// Each owning thread adds its cells' fp64 sums to its own slot of the
+// tile's partials (zeroed by the launcher), read at the start of the launch:
+// no reduction inside the launch, and a fixed summation order.
 template <bool INSIDE>
-__global__ __launch_bounds__(kThreads) void k_mem_bwd(MemArgs a, int m_hi, int ks, int src, int dst, int first) {
+__global__ __launch_bounds__(kThreads) void k_mem_bwd(MemArgs a, int m_hi, int ks, int src, int dst) {
   __shared__ BwdShared sh;
-  __shared__ double red[2][kWaves];
-  double* gp = a.gpart + 2 * (blockIdx.y * gridDim.x + blockIdx.x);
-  double prev_c = 0.0, prev_d = 0.0;  // this tile's partials so far, read early
-  if (threadIdx.x == 0 && !first) {
-    prev_c = gp[0];
-    prev_d = gp[1];
-  }
   if ((int)threadIdx.x < ks) {
     const int n = m_hi - (int)threadIdx.x;
     sh.srcv[threadIdx.x] = n >= 1 ? 2.0f * (a.out[n - 1] - a.tgt[n - 1]) : 0.0f;
   }
   const Strip<INSIDE> st(a);
   double gc = 0.0, gd = 0.0;
-  if (st.own_rows())
-    bwd_strip<INSIDE, true>(a, st, sh, m_hi, ks, src, dst, gc, gd);
-  else
-    bwd_strip<INSIDE, false>(a, st, sh, m_hi, ks, src, dst, gc, gd);
   if (st.own_rows()) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      gc += __shfl_xor(gc, off, 64);
-      gd += __shfl_xor(gd, off, 64);
+    double* gp = a.gpart + 2 * ((size_t)st.tile * (kTile * kTile) + st.slot);
+    double prev_c = 0.0, prev_d = 0.0;
+    if (st.own_lane) {
+      prev_c = gp[0];
+      prev_d = gp[1];
     }
-  }
-  if (st.lane == 0) {
-    red[0][st.w] = gc;
-    red[1][st.w] = gd;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    double sc = 0.0, sd = 0.0;
-    for (int w = 0; w < kWaves; ++w) {
-      sc += red[0][w];
-      sd += red[1][w];
+    bwd_strip<INSIDE, true>(a, st, sh, m_hi, ks, src, dst, gc, gd);
+    if (st.own_lane) {
+      gp[0] = prev_c + gc;
+      gp[1] = prev_d + gd;
     }
-    gp[0] = prev_c + sc;
-    gp[1] = prev_d + sd;
+  } else {
+    bwd_strip<INSIDE, false>(a, st, sh, m_hi, ks, src, dst, gc, gd);
   }
 }
 
@@ -419,13 +420,28 @@ __global__ void k_mem_zero(float* __restrict__ f, size_t n) {
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) f[i] = 0.0f;
 }
 
-// grads[q] = sum over tiles of the fp64 partials, in tile order.
-__global__ void k_mem_grad_final(const double* __restrict__ gpart, float* __restrict__ grads, int tiles) {
-  if (threadIdx.x < 2) {
-    double t = 0.0;
-    for (int i = 0; i < tiles; ++i) t += gpart[2 * i + threadIdx.x];
-    grads[threadIdx.x] = (float)t;
+// grads[q] = sum of the fp64 partials [n][2]: one workgroup of kFinal
+// threads, each summing a fixed stride of slots, then a fixed tree.
+constexpr int kFinal = 1024;
+__global__ __launch_bounds__(kFinal) void k_mem_grad_final(const double* __restrict__ gpart, float* __restrict__ grads,
+                                                           int n) {
+  __shared__ double red[2][kFinal];
+  double c = 0.0, d = 0.0;
+  for (int i = threadIdx.x; i < n; i += kFinal) {
+    c += gpart[2 * i];
+    d += gpart[2 * i + 1];
   }
+  red[0][threadIdx.x] = c;
+  red[1][threadIdx.x] = d;
+  __syncthreads();
+  for (int h = kFinal / 2; h >= 1; h >>= 1) {
+    if ((int)threadIdx.x < h) {
+      red[0][threadIdx.x] += red[0][threadIdx.x + h];
+      red[1][threadIdx.x] += red[1][threadIdx.x + h];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x < 2) grads[threadIdx.x] = (float)red[threadIdx.x][0];
 }
 
 // lt[n] = (out[n] - tgt[n])^2
@@ -471,7 +487,8 @@ int launch_membrane_fwd(const Launch& L, const dgen_hip_op& op) {
   const unsigned ib = (unsigned)std::min<int64_t>((G + 255) / 256, (int64_t)L.cu_count * 8);
   hipLaunchKernelGGL(k_mem_init, dim3(ib), dim3(256), 0, L.stream, cell(L, u0), a.S, (size_t)G);
   DGEN_LAUNCH_CHECK("k_mem_init");
-  const dim3 grid((unsigned)((C + kTile - 1) / kTile), (unsigned)((R + kTile - 1) / kTile));
+  a.tiles_x = (int)((C + kTile - 1) / kTile);
+  const dim3 grid((unsigned)(a.tiles_x * ((R + kTile - 1) / kTile)));
   const bool inside = R >= kSide && C >= kSide;  // regions placed inside the grid
   for (int64_t n0 = 0; n0 < T; n0 += ks) {
     const int n = (int)std::min<int64_t>(ks, T - n0);
@@ -496,7 +513,7 @@ int launch_membrane_bwd(const Launch& L, const dgen_hip_op& op) {
   DGEN_CHECK_CELL(L, out, T, "membrane_bwd.pickup");
   DGEN_CHECK_CELL(L, tgt, T, "membrane_bwd.target");
   DGEN_CHECK_CELL(L, lam, 4 * G, "membrane_bwd.adjoint_fields");
-  DGEN_CHECK_CELL(L, gpart, 4 * tiles, "membrane_bwd.grad_partials");
+  DGEN_CHECK_CELL(L, gpart, 4 * tiles * kTile * kTile, "membrane_bwd.grad_partials");
   DGEN_REQUIRE(gpart % 2 == 0, "membrane_bwd: grad partials cell must be 8-byte aligned");
   DGEN_CHECK_CELL(L, grads, 2, "membrane_bwd.grads");
   DGEN_CHECK_CELL(L, lt, T, "membrane_bwd.loss_terms");
@@ -516,27 +533,29 @@ int launch_membrane_bwd(const Launch& L, const dgen_hip_op& op) {
   hipLaunchKernelGGL(k_mem_loss_terms, dim3((unsigned)((T + 255) / 256)), dim3(256), 0, L.stream, a.out, a.tgt,
                      cell(L, lt), (int)T);
   DGEN_LAUNCH_CHECK("k_mem_loss_terms");
-  const dim3 grid((unsigned)((C + kTile - 1) / kTile), (unsigned)((R + kTile - 1) / kTile));
-  // (lambda_{T+1}, lambda_{T+2}) = 0: set 1 starts zeroed
+  a.tiles_x = (int)((C + kTile - 1) / kTile);
+  const dim3 grid((unsigned)tiles);
+  // (lambda_{T+1}, lambda_{T+2}) = 0: set 1 starts zeroed; so do the gradient slots
   const unsigned zb = (unsigned)std::min<int64_t>((2 * G + 255) / 256, (int64_t)L.cu_count * 8);
   hipLaunchKernelGGL(k_mem_zero, dim3(zb), dim3(256), 0, L.stream, a.lam + 2 * G, (size_t)(2 * G));
   DGEN_LAUNCH_CHECK("k_mem_zero");
+  const int64_t nslots = tiles * kTile * kTile;
+  hipLaunchKernelGGL(k_mem_zero, dim3(zb), dim3(256), 0, L.stream, reinterpret_cast<float*>(a.gpart),
+                     (size_t)(4 * nslots));
+  DGEN_LAUNCH_CHECK("k_mem_zero");
   const bool inside = R >= kSide && C >= kSide;  // regions placed inside the grid
   int src = 1, dst = 0;
-  bool first = true;
   for (int64_t m_hi = T; m_hi >= 0; m_hi -= ks) {
     const int n = (int)std::min<int64_t>(ks, m_hi + 1);
     if (inside)
-      hipLaunchKernelGGL(k_mem_bwd<true>, grid, dim3(kThreads), 0, L.stream, a, (int)m_hi, n, src, dst, first ? 1 : 0);
+      hipLaunchKernelGGL(k_mem_bwd<true>, grid, dim3(kThreads), 0, L.stream, a, (int)m_hi, n, src, dst);
     else
-      hipLaunchKernelGGL(k_mem_bwd<false>, grid, dim3(kThreads), 0, L.stream, a, (int)m_hi, n, src, dst,
-                         first ? 1 : 0);
+      hipLaunchKernelGGL(k_mem_bwd<false>, grid, dim3(kThreads), 0, L.stream, a, (int)m_hi, n, src, dst);
     DGEN_LAUNCH_CHECK("k_mem_bwd");
     src = dst;
     dst ^= 1;
-    first = false;
   }
-  hipLaunchKernelGGL(k_mem_grad_final, dim3(1), dim3(64), 0, L.stream, a.gpart, cell(L, grads), (int)tiles);
+  hipLaunchKernelGGL(k_mem_grad_final, dim3(1), dim3(kFinal), 0, L.stream, a.gpart, cell(L, grads), (int)nslots);
   DGEN_LAUNCH_CHECK("k_mem_grad_final");
   return 0;
 }

@@ -90,6 +90,10 @@ struct dgen_hip_ctx {
   uint32_t max_frames = 0;
   std::vector<dgen_hip_op> ops;
   bool configured = false;
+  // graph replay of the per-run schedule (dgen_hip_set_graphs)
+  bool use_graphs = false;
+  hipGraphExec_t graph = nullptr;
+  uint32_t graph_frames = 0;
 };
 
 static int set_device(dgen_hip_ctx* c) {
@@ -109,7 +113,14 @@ static Launch make_launch(dgen_hip_ctx* c, hipStream_t s, uint32_t frames, bool 
   return L;
 }
 
+static void drop_graph(dgen_hip_ctx* c) {
+  if (c->graph) (void)hipGraphExecDestroy(c->graph);
+  c->graph = nullptr;
+  c->graph_frames = 0;
+}
+
 static void release_arena(dgen_hip_ctx* c) {
+  drop_graph(c);
   if (c->d_arena) (void)hipFree(c->d_arena);
   if (c->h_arena) (void)hipHostFree(c->h_arena);
   c->d_arena = nullptr;
@@ -144,6 +155,35 @@ static int enqueue(dgen_hip_ctx* c, uint32_t frames, bool static_pass, std::vect
     DGEN_HIP_TRY(hipEventRecord(c->ev_side, c->s1));
     DGEN_HIP_TRY(hipStreamWaitEvent(c->s0, c->ev_side, 0));
   }
+  return 0;
+}
+
+// One run of the per-run schedule.  With graphs on, the schedule for this
+// frame count is captured once from both streams (the side stream joins the
+// capture through the fork event and is joined back before it ends) and
+// replayed with one launch; captures hold kernel launches and events only.
+static int launch_run(dgen_hip_ctx* c, uint32_t frames) {
+  if (!c->use_graphs) return enqueue(c, frames, false, nullptr);
+  if (!c->graph || c->graph_frames != frames) {
+    drop_graph(c);
+    DGEN_HIP_TRY(hipStreamBeginCapture(c->s0, hipStreamCaptureModeThreadLocal));
+    int rc = enqueue(c, frames, false, nullptr);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(c->s0, &g);
+    if (rc) {
+      if (g) (void)hipGraphDestroy(g);
+      return rc;
+    }
+    if (e != hipSuccess) return fail(DGEN_HIP_E_DEVICE, "run: graph capture failed: %s", hipGetErrorString(e));
+    e = hipGraphInstantiate(&c->graph, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) {
+      c->graph = nullptr;
+      return fail(DGEN_HIP_E_DEVICE, "run: graph instantiation failed: %s", hipGetErrorString(e));
+    }
+    c->graph_frames = frames;
+  }
+  DGEN_HIP_TRY(hipGraphLaunch(c->graph, c->s0));
   return 0;
 }
 
@@ -316,7 +356,18 @@ static int run_static(dgen_hip_ctx* c) {
 int dgen_hip_run_async(dgen_hip_ctx* c, uint32_t frame_count) {
   int rc = run_checks(c, frame_count);
   if (rc) return rc;
-  return enqueue(c, frame_count, false, nullptr);
+  return launch_run(c, frame_count);
+}
+
+int dgen_hip_set_graphs(dgen_hip_ctx* c, int enable) {
+  if (!c) return fail(DGEN_HIP_E_INVALID, "set_graphs: null context");
+  int rc = set_device(c);
+  if (rc) return rc;
+  DGEN_HIP_TRY(hipStreamSynchronize(c->s0));
+  DGEN_HIP_TRY(hipStreamSynchronize(c->s1));
+  drop_graph(c);
+  c->use_graphs = enable != 0;
+  return 0;
 }
 
 int dgen_hip_sync(dgen_hip_ctx* c) {
@@ -364,13 +415,13 @@ int dgen_hip_time_runs(dgen_hip_ctx* c, uint32_t frame_count, int warmup, int it
   int rc = run_checks(c, frame_count);
   if (rc) return rc;
   for (int i = 0; i < warmup; ++i)
-    if ((rc = enqueue(c, frame_count, false, nullptr))) return rc;
+    if ((rc = launch_run(c, frame_count))) return rc;
   if ((rc = dgen_hip_sync(c))) return rc;
   hipEvent_t a, b;
   DGEN_HIP_TRY(hipEventCreate(&a));
   DGEN_HIP_TRY(hipEventCreate(&b));
   DGEN_HIP_TRY(hipEventRecord(a, c->s0));
-  for (int i = 0; i < iters && !rc; ++i) rc = enqueue(c, frame_count, false, nullptr);
+  for (int i = 0; i < iters && !rc; ++i) rc = launch_run(c, frame_count);
   DGEN_HIP_TRY(hipEventRecord(b, c->s0));
   int rc2 = dgen_hip_sync(c);
   float ms = 0.f;

@@ -518,7 +518,7 @@ def membrane_program(cfg: MembraneConfig, train: bool = True, optimizer: bool = 
         return p
     tgt = p.alloc("target", T)
     lam = p.alloc("adjoint_fields", 4 * G)
-    gpart = p.alloc("grad_partials", 4 * tiles)  # fp64
+    gpart = p.alloc("grad_partials", 4 * tiles * MEM_TILE * MEM_TILE)  # fp64, one (c2, d) slot per owned cell column strip
     lt = p.alloc("loss_terms", T)
     loss = p.alloc("loss", 1)
     Gc = p.alloc("grads", 2)

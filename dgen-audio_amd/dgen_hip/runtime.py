@@ -60,7 +60,7 @@ OP_STATIC, OP_SIDE, OP_JOIN = 1, 2, 4
 EXPORTED_SYMBOLS = (
     "dgen_hip_abi_version", "dgen_hip_device_count", "dgen_hip_create", "dgen_hip_destroy",
     "dgen_hip_last_error", "dgen_hip_configure", "dgen_hip_host_memory", "dgen_hip_upload",
-    "dgen_hip_download", "dgen_hip_zero", "dgen_hip_run", "dgen_hip_run_async", "dgen_hip_sync",
+    "dgen_hip_download", "dgen_hip_zero", "dgen_hip_run", "dgen_hip_run_async", "dgen_hip_sync", "dgen_hip_set_graphs",
     "dgen_hip_profile", "dgen_hip_time_runs", "dgen_hip_time_op",
 )
 
@@ -104,6 +104,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "dgen_hip_zero": ([vp, u64, u64], i32),
         "dgen_hip_run": ([vp, u32], i32),
         "dgen_hip_run_async": ([vp, u32], i32),
+        "dgen_hip_set_graphs": ([vp, i32], i32),
         "dgen_hip_sync": ([vp], i32),
         "dgen_hip_profile": ([vp, u32, ctypes.POINTER(CKernelTime), ctypes.c_size_t,
                               ctypes.POINTER(ctypes.c_size_t)], i32),
@@ -212,6 +213,10 @@ class HIPLazyRuntime:
         c = self.program.cells[name]
         self.download(name)
         return self._host[c.off:c.off + c.n].copy()
+
+    def set_graphs(self, enable: bool = True) -> None:
+        """Replay runs as a captured HIP graph (dgen_hip_set_graphs)."""
+        _check(self.L.dgen_hip_set_graphs(self._ctx, 1 if enable else 0), "dgen_hip_set_graphs")
 
     def run_async(self, frameCount: int | None = None) -> None:
         _check(self.L.dgen_hip_run_async(self._ctx, frameCount or self.program.max_frames), "dgen_hip_run_async")

@@ -234,9 +234,10 @@ enum dgen_hip_kernel {
   DGEN_HIP_K_MEMBRANE_FWD = 27,
 
   /* Discrete adjoint of the forward against a target pickup series: the
-   * gradient (d/d c2, d/d d), accumulated in fp64 per tile
-   * ([ceil(R/32)*ceil(C/32)][2] doubles, even cell offset) and summed in
-   * tile order, and the loss terms (out - tgt)^2 ([T]).
+   * gradient (d/d c2, d/d d), accumulated in fp64 per 32x32 tile and slot
+   * ([ceil(R/32)*ceil(C/32)][1024][2] doubles, even cell offset; zeroed
+   * by the call) and summed in a fixed order, and the loss terms
+   * (out - tgt)^2 ([T]).
    * arg: [0]=states [1]=params [2]=pickup [3]=target ([T]) [4]=adjoint
    *      boundary fields ([4][R][C]) [5]=grad partials [6]=loss terms
    *      [7]=R [8]=C [9]=T [10]=py [11]=px [12]=steps per launch [13]=grads */
@@ -315,6 +316,18 @@ int dgen_hip_run(dgen_hip_ctx* ctx, uint32_t frame_count);
 /* As dgen_hip_run but returns without waiting; dgen_hip_sync waits. */
 int dgen_hip_run_async(dgen_hip_ctx* ctx, uint32_t frame_count);
 int dgen_hip_sync(dgen_hip_ctx* ctx);
+
+/* Graph replay of runs (enable != 0): the per-run schedule for a frame count
+ * is captured once from both streams into a HIP graph and every later
+ * dgen_hip_run / dgen_hip_run_async / dgen_hip_time_runs with that frame
+ * count replays it with one launch, instead of enqueuing each kernel from
+ * the host.  Kernel arguments are fixed at capture; dgen_hip_configure and
+ * a change of frame count capture afresh.  dgen_hip_profile and
+ * dgen_hip_time_op always launch op by op.  Waits for outstanding work.
+ * The reference re-encodes its command buffers on every run
+ * (MetalRuntime.swift:676-698, runNoCopy -> run); this is the MI355X launch
+ * path for schedules of many short kernels (config 5: ~600 per step). */
+int dgen_hip_set_graphs(dgen_hip_ctx* ctx, int enable);
 
 /* Run once with a hipEvent pair around every op; fills up to `cap` entries
  * and sets *n_out.  Mirrors profileKernels (MetalRuntime.swift:397-425). */
