@@ -114,12 +114,63 @@ def time_session(rt, program, args):
     return wall, rows, dom, step_roof_ms(program)
 
 
-def roofline_fields(rows, dom, roof_ms, ms_per_step):
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+
+
+def measured_traffic(workload: str, label: str):
+    """HBM bytes per run of op `label`, from the rocprofv3 FETCH_SIZE /
+    WRITE_SIZE passes recorded by ``python -m dgen_hip.traffic`` (counters
+    scaled by a plain copy of known size), or None if not measured."""
+    try:
+        with open(TRAFFIC_FILE) as fh:
+            return json.load(fh)[workload][label]["bytes_per_run"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def traffic_run(sess, workload: str, runs: int) -> int:
+    """Driver for the traffic passes: one full run (so every cell holds
+    its values), then for each op with the largest roofline time a plain
+    1 GiB device-to-device copy (the HIP runtime's copy kernel: the counter
+    calibration, and a separator) and the op alone `runs` times.  Prints the
+    op labels as one JSON line."""
+    import ctypes
+
+    from dgen_hip.roofline import roof_seconds
+    from dgen_hip.runtime import OP_STATIC
+    prog = sess.program
+    per_run = [(i, roof_seconds(op)) for i, op in enumerate(prog.ops) if not op.flags & OP_STATIC]
+    top = max(r for _, r in per_run)
+    idx = [i for i, r in per_run if r >= top * (1.0 - 1e-9)]
+    sess.rt.runNoCopy()
+    hip = ctypes.CDLL("libamdhip64.so")  # the runtime libdgen_hip.so is linked against, already loaded
+    hip.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+    hip.hipMemcpyDtoD.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
+    hip.hipFree.argtypes = [ctypes.c_void_p]
+    n = 1 << 30
+    src, dst = ctypes.c_void_p(), ctypes.c_void_p()
+    if hip.hipMalloc(ctypes.byref(src), n) or hip.hipMalloc(ctypes.byref(dst), n):
+        raise RuntimeError("traffic run: hipMalloc of the calibration buffers failed")
+    try:
+        for i in idx:
+            if hip.hipMemcpyDtoD(dst, src, n) or hip.hipDeviceSynchronize():
+                raise RuntimeError("traffic run: calibration copy failed")
+            for _ in range(runs):
+                sess.rt.run_op(i)
+    finally:
+        hip.hipFree(src)
+        hip.hipFree(dst)
+    print(json.dumps({"traffic_ops": [prog.ops[i].label for i in idx], "runs": runs, "workload": workload}),
+          flush=True)
+    return 0
+
+
+def roofline_fields(rows, dom, roof_ms, ms_per_step, workload: str = "harmonic"):
     longest = max(rows, key=lambda r: r.meas_ms)
     ach, peak, unit = dom.achieved()
     return {
         "roofline": {"kernel": dom.label, "bound": dom.bound, "achieved": ach, "peak": peak, "unit": unit,
-                     "frac": ach / peak, "traffic": None, "ms": dom.meas_ms},
+                     "frac": ach / peak, "traffic": measured_traffic(workload, dom.label), "ms": dom.meas_ms},
         "longest_kernel": {"kernel": longest.label, "bound": longest.bound, "ms": longest.meas_ms,
                            "frac": longest.frac},
         "kernels": [{"kernel": r.label, "bound": r.bound, "ms": round(r.meas_ms, 4), "roof_ms": round(r.roof_ms, 4),
@@ -168,6 +219,12 @@ def run_biquad(args) -> dict:
     cfg = BiquadConfig()
     log(f"bench: biquad session B={cfg.B} T={cfg.T} chunk={args.chunk}")
     sess = BiquadSession(cfg, device=0, optimizer=True, chunk=args.chunk)
+    if args.traffic_runs:
+        try:
+            traffic_run(sess, "biquad", args.traffic_runs)
+        finally:
+            sess.close()
+        return None
     try:
         wall, rows, dom, roof_ms = time_session(sess.rt, sess.program, args)
         loss = sess.loss()
@@ -187,7 +244,7 @@ def run_biquad(args) -> dict:
                                "fixed bank, BPTT to base cutoff and Q, Adam", "B": cfg.B, "T": cfg.T, "sr": cfg.sr,
                    "chunk": args.chunk, "parallelism": "single GPU"},
     }
-    out.update(roofline_fields(rows, dom, roof_ms, ms_per_step))
+    out.update(roofline_fields(rows, dom, roof_ms, ms_per_step, "biquad"))
     out["loss"] = loss
     out["cpu_baseline"] = cpu
     return out
@@ -234,6 +291,12 @@ def run_stft(args) -> dict:
     cfg = StftConfig()
     log(f"bench: stft session S={cfg.S} T={cfg.T} N={cfg.N} H={cfg.H}")
     sess = StftSession(cfg, device=0, optimizer=True)
+    if args.traffic_runs:
+        try:
+            traffic_run(sess, "stft", args.traffic_runs)
+        finally:
+            sess.close()
+        return None
     try:
         wall, rows, dom, roof_ms = time_session(sess.rt, sess.program, args)
         loss = sess.loss()
@@ -253,7 +316,7 @@ def run_stft(args) -> dict:
                                "overlapAdd, MSE vs input, gain gradient, Adam", "S": cfg.S, "T": cfg.T, "N": cfg.N,
                    "H": cfg.H, "parallelism": "single GPU"},
     }
-    out.update(roofline_fields(rows, dom, roof_ms, ms_per_step))
+    out.update(roofline_fields(rows, dom, roof_ms, ms_per_step, "stft"))
     out["loss"] = loss
     out["cpu_baseline"] = cpu
     return out
@@ -300,6 +363,12 @@ def run_membrane(args) -> dict:
     cfg = MembraneConfig()
     log(f"bench: membrane session {cfg.R}x{cfg.C} T={cfg.T} steps/launch={args.mem_steps}")
     sess = MembraneSession(cfg, device=0, optimizer=True, steps=args.mem_steps)
+    if args.traffic_runs:
+        try:
+            traffic_run(sess, "membrane", args.traffic_runs)
+        finally:
+            sess.close()
+        return None
     try:
         wall, rows, dom, roof_ms = time_session(sess.rt, sess.program, args)
         loss = sess.loss()
@@ -319,7 +388,7 @@ def run_membrane(args) -> dict:
                                "target, adjoint to (c2, d), Adam", "R": cfg.R, "C": cfg.C, "T": cfg.T,
                    "steps_per_launch": args.mem_steps, "parallelism": "single GPU"},
     }
-    out.update(roofline_fields(rows, dom, roof_ms, ms_per_step))
+    out.update(roofline_fields(rows, dom, roof_ms, ms_per_step, "membrane"))
     out["loss"] = loss
     out["cpu_baseline"] = cpu
     return out
@@ -334,6 +403,8 @@ def main() -> int:
     ap.add_argument("--cpu-lanes", type=int, default=4)
     ap.add_argument("--cpu-repeats", type=int, default=3)
     ap.add_argument("--op-iters", type=int, default=10, help="runs averaged for the dominant kernel's time")
+    ap.add_argument("--traffic-runs", type=int, default=0,
+                    help="instead of timing: run the dominant op alone this many times (for rocprofv3 --pmc)")
     ap.add_argument("--no-graphs", dest="graphs", action="store_false",
                     help="enqueue every kernel from the host instead of replaying each step as a HIP graph")
     ap.add_argument("--workload", choices=("harmonic", "biquad", "stft", "membrane"), default="harmonic")
@@ -344,17 +415,10 @@ def main() -> int:
         print(f"bench.py: --gpus {args.gpus} is not supported: this backend runs on one GPU; the multi-GPU "
               f"design (lane sharding + one gradient all-reduce) is not built.", file=sys.stderr)
         return 2
-    if args.workload == "biquad":
-        print(json.dumps(run_biquad(args)), flush=True)
-        return 0
-    if args.workload == "stft":
-        print(json.dumps(run_stft(args)), flush=True)
-        return 0
-    if args.workload == "membrane":
-        print(json.dumps(run_membrane(args)), flush=True)
-        return 0
-
-    print(json.dumps(run_harmonic(args)), flush=True)
+    run = {"biquad": run_biquad, "stft": run_stft, "membrane": run_membrane, "harmonic": run_harmonic}[args.workload]
+    res = run(args)
+    if res is not None:
+        print(json.dumps(res), flush=True)
     return 0
 
 
@@ -365,6 +429,12 @@ def run_harmonic(args) -> dict:
     cfg = HarmonicConfig()  # B=32, T=64000 @ 16 kHz, K=60, NF=65, MLP 3x512, FFT 2048..64
     log(f"bench: building session B={cfg.B} T={cfg.T} K={cfg.K} hidden={cfg.hidden}")
     sess = HarmonicSession(cfg, device=0, optimizer=True)
+    if args.traffic_runs:
+        try:
+            traffic_run(sess, "harmonic", args.traffic_runs)
+        finally:
+            sess.close()
+        return None
     try:
         wall, rows, dom, roof_ms = time_session(sess.rt, sess.program, args)
         loss = sess.loss()
@@ -393,7 +463,7 @@ def run_harmonic(args) -> dict:
                    "noise_taps": cfg.NF, "fft_sizes": list(cfg.fft_sizes), "mlp": [cfg.din] + [cfg.hidden] * cfg.layers
                    + [cfg.NC], "parallelism": "single GPU"},
     }
-    out.update(roofline_fields(rows, dom, roof_ms, ms_per_step))
+    out.update(roofline_fields(rows, dom, roof_ms, ms_per_step, "harmonic"))
     out["loss"] = loss
     out["cpu_baseline"] = cpu
     return out

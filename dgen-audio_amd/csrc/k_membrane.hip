@@ -56,7 +56,7 @@ struct MemArgs {
   float* out;         // pickup [T]
   const float* tgt;   // target pickup [T] (backward)
   float* lam;         // adjoint boundary fields: 2 sets x (lambda_{m+1}, lambda_{m+2}) x [R][C]
-  double* gpart;      // [tiles][kTile * kTile][2] gradient partials (fp64: the terms cancel heavily)
+  double* gpart;      // [tiles][kWaves][2] gradient partials (fp64: the terms cancel heavily)
   int R, C, T, py, px;
   int tiles_x;        // tiles per grid row
 };
@@ -95,7 +95,6 @@ struct Strip {
   unsigned ownb;  // 4 * column, clamped into the owned columns
 
   int tile;       // tile index (row-major)
-  int slot;       // this thread's gradient slot in the tile: (first owned row, column)
 
   __device__ Strip(const MemArgs& a) : R(a.R), C(a.C) {
     lane = threadIdx.x & 63;
@@ -118,7 +117,6 @@ struct Strip {
     pw = (a.px - rx0 >= 0 && a.px - rx0 < 64 && pq >= 0 && pq < kRows) ? pq : -1;
     colb = 4u * (unsigned)min(max(gx, 0), a.C - 1);
     ownb = 4u * (unsigned)min(max(gx, tx0), tx1 - 1);
-    slot = (gy0 + oq0 - ty0) * kTile + (gx - tx0);
   }
   __device__ bool own_rows() const { return oq0 < oq1; }
   __device__ bool all_rows_owned() const { return oq0 == 0 && oq1 == kRows; }
@@ -377,9 +375,38 @@ __device__ __forceinline__ void bwd_strip(const MemArgs& a, const Strip<INSIDE>&
   }
 }
 
-// Each owning thread adds its cells' fp64 sums to its own slot of the
-// tile's partials (zeroed by the launcher), read at the start of the launch:
-// no reduction inside the launch, and a fixed summation order.
+// Value of lane i - K within the lane's row of 16 (0 for the first K lanes
+// of the row): DPP row_shr:K on both halves of a double.
+template <int K>
+__device__ __forceinline__ double row_shr(double v) {
+  const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)(unsigned)b, 0x110 + K, 0xf, 0xf, true);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(unsigned)(b >> 32), 0x110 + K, 0xf, 0xf, true);
+  return __builtin_bit_cast(double, (unsigned long long)(unsigned)lo | ((unsigned long long)(unsigned)hi << 32));
+}
+
+__device__ __forceinline__ double lane_value(double v, int lane) {
+  const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+  const unsigned lo = __builtin_amdgcn_readlane((int)(unsigned)b, lane);
+  const unsigned hi = __builtin_amdgcn_readlane((int)(unsigned)(b >> 32), lane);
+  return __builtin_bit_cast(double, (unsigned long long)lo | ((unsigned long long)hi << 32));
+}
+
+// Sum over the wave in a fixed order (uniform result): shift-and-add within
+// each row of 16 lanes leaves the row's sum in its last lane, then the four
+// row sums.
+__device__ __forceinline__ double wave_sum(double v) {
+  v += row_shr<1>(v);
+  v += row_shr<2>(v);
+  v += row_shr<4>(v);
+  v += row_shr<8>(v);
+  return (lane_value(v, 15) + lane_value(v, 31)) + (lane_value(v, 47) + lane_value(v, 63));
+}
+
+// Each wave holding owned rows sums its cells' fp64 terms over the wave and
+// adds them to its slot of the tile's partials (zeroed by the launcher),
+// read at the start of the launch: no barrier or LDS for the reduction, and
+// a fixed summation order.
 template <bool INSIDE>
 __global__ __launch_bounds__(kThreads) void k_mem_bwd(MemArgs a, int m_hi, int ks, int src, int dst) {
   __shared__ BwdShared sh;
@@ -390,14 +417,12 @@ __global__ __launch_bounds__(kThreads) void k_mem_bwd(MemArgs a, int m_hi, int k
   const Strip<INSIDE> st(a);
   double gc = 0.0, gd = 0.0;
   if (st.own_rows()) {
-    double* gp = a.gpart + 2 * ((size_t)st.tile * (kTile * kTile) + st.slot);
-    double prev_c = 0.0, prev_d = 0.0;
-    if (st.own_lane) {
-      prev_c = gp[0];
-      prev_d = gp[1];
-    }
+    double* gp = a.gpart + 2 * ((size_t)st.tile * kWaves + st.w);
+    const double prev_c = gp[0], prev_d = gp[1];
     bwd_strip<INSIDE, true>(a, st, sh, m_hi, ks, src, dst, gc, gd);
-    if (st.own_lane) {
+    gc = wave_sum(gc);
+    gd = wave_sum(gd);
+    if (st.lane == 0) {
       gp[0] = prev_c + gc;
       gp[1] = prev_d + gd;
     }
@@ -513,7 +538,7 @@ int launch_membrane_bwd(const Launch& L, const dgen_hip_op& op) {
   DGEN_CHECK_CELL(L, out, T, "membrane_bwd.pickup");
   DGEN_CHECK_CELL(L, tgt, T, "membrane_bwd.target");
   DGEN_CHECK_CELL(L, lam, 4 * G, "membrane_bwd.adjoint_fields");
-  DGEN_CHECK_CELL(L, gpart, 4 * tiles * kTile * kTile, "membrane_bwd.grad_partials");
+  DGEN_CHECK_CELL(L, gpart, 4 * tiles * kWaves, "membrane_bwd.grad_partials");
   DGEN_REQUIRE(gpart % 2 == 0, "membrane_bwd: grad partials cell must be 8-byte aligned");
   DGEN_CHECK_CELL(L, grads, 2, "membrane_bwd.grads");
   DGEN_CHECK_CELL(L, lt, T, "membrane_bwd.loss_terms");
@@ -539,7 +564,7 @@ int launch_membrane_bwd(const Launch& L, const dgen_hip_op& op) {
   const unsigned zb = (unsigned)std::min<int64_t>((2 * G + 255) / 256, (int64_t)L.cu_count * 8);
   hipLaunchKernelGGL(k_mem_zero, dim3(zb), dim3(256), 0, L.stream, a.lam + 2 * G, (size_t)(2 * G));
   DGEN_LAUNCH_CHECK("k_mem_zero");
-  const int64_t nslots = tiles * kTile * kTile;
+  const int64_t nslots = tiles * kWaves;
   hipLaunchKernelGGL(k_mem_zero, dim3(zb), dim3(256), 0, L.stream, reinterpret_cast<float*>(a.gpart),
                      (size_t)(4 * nslots));
   DGEN_LAUNCH_CHECK("k_mem_zero");

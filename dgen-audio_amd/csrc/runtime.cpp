@@ -432,6 +432,17 @@ int dgen_hip_time_runs(dgen_hip_ctx* c, uint32_t frame_count, int warmup, int it
   return rc ? rc : rc2;
 }
 
+int dgen_hip_run_op(dgen_hip_ctx* c, uint32_t frame_count, uint32_t op_index) {
+  int rc = run_checks(c, frame_count);
+  if (rc) return rc;
+  if (op_index >= c->ops.size()) return fail(DGEN_HIP_E_INVALID, "run_op: op %u of %zu", op_index, c->ops.size());
+  const dgen_hip_op& op = c->ops[op_index];
+  hipStream_t s = (op.flags & DGEN_HIP_OP_SIDE) ? c->s1 : c->s0;
+  rc = launcher_for(op.kernel)(make_launch(c, s, frame_count, false), op);
+  int rc2 = dgen_hip_sync(c);
+  return rc ? rc : rc2;
+}
+
 int dgen_hip_time_op(dgen_hip_ctx* c, uint32_t frame_count, uint32_t op_index, int iters, double* ms_out) {
   if (!ms_out || iters <= 0) return fail(DGEN_HIP_E_INVALID, "time_op: bad arguments");
   int rc = run_checks(c, frame_count);

@@ -24,6 +24,7 @@ BQ_CHUNK = 256      # frames per biquad scan chunk
 STFT_TILE = 8192    # output samples per STFT forward workgroup
 MEM_STEPS = 16      # membrane frames per time-blocked launch
 MEM_TILE = 32       # membrane cells per workgroup tile side
+MEM_WAVES = 16      # membrane waves per workgroup (4-row strips of a 64-row region)
 
 
 def _f32(x) -> float:
@@ -518,7 +519,7 @@ def membrane_program(cfg: MembraneConfig, train: bool = True, optimizer: bool = 
         return p
     tgt = p.alloc("target", T)
     lam = p.alloc("adjoint_fields", 4 * G)
-    gpart = p.alloc("grad_partials", 4 * tiles * MEM_TILE * MEM_TILE)  # fp64, one (c2, d) slot per owned cell column strip
+    gpart = p.alloc("grad_partials", 4 * tiles * MEM_WAVES)  # fp64 (c2, d) per tile and wave
     lt = p.alloc("loss_terms", T)
     loss = p.alloc("loss", 1)
     Gc = p.alloc("grads", 2)

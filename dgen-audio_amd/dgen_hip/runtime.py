@@ -61,7 +61,7 @@ EXPORTED_SYMBOLS = (
     "dgen_hip_abi_version", "dgen_hip_device_count", "dgen_hip_create", "dgen_hip_destroy",
     "dgen_hip_last_error", "dgen_hip_configure", "dgen_hip_host_memory", "dgen_hip_upload",
     "dgen_hip_download", "dgen_hip_zero", "dgen_hip_run", "dgen_hip_run_async", "dgen_hip_sync", "dgen_hip_set_graphs",
-    "dgen_hip_profile", "dgen_hip_time_runs", "dgen_hip_time_op",
+    "dgen_hip_profile", "dgen_hip_time_runs", "dgen_hip_time_op", "dgen_hip_run_op",
 )
 
 
@@ -110,6 +110,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
                               ctypes.POINTER(ctypes.c_size_t)], i32),
         "dgen_hip_time_runs": ([vp, u32, i32, i32, ctypes.POINTER(ctypes.c_double)], i32),
         "dgen_hip_time_op": ([vp, u32, u32, i32, ctypes.POINTER(ctypes.c_double)], i32),
+        "dgen_hip_run_op": ([vp, u32, u32], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -235,6 +236,10 @@ class HIPLazyRuntime:
         _check(self.L.dgen_hip_time_op(self._ctx, frameCount or self.program.max_frames, index, iters,
                                        ctypes.byref(ms)), "dgen_hip_time_op")
         return ms.value
+
+    def run_op(self, index: int, frameCount: int | None = None) -> None:
+        """Run schedule op `index` alone on the current cell contents."""
+        _check(self.L.dgen_hip_run_op(self._ctx, frameCount or self.program.max_frames, index), "dgen_hip_run_op")
 
     def close(self) -> None:
         if getattr(self, "_ctx", None):

@@ -234,9 +234,9 @@ enum dgen_hip_kernel {
   DGEN_HIP_K_MEMBRANE_FWD = 27,
 
   /* Discrete adjoint of the forward against a target pickup series: the
-   * gradient (d/d c2, d/d d), accumulated in fp64 per 32x32 tile and slot
-   * ([ceil(R/32)*ceil(C/32)][1024][2] doubles, even cell offset; zeroed
-   * by the call) and summed in a fixed order, and the loss terms
+   * gradient (d/d c2, d/d d), accumulated in fp64 per 32x32 tile and wave
+   * ([ceil(R/32)*ceil(C/32)][16][2] doubles, even cell offset; zeroed by
+   * the call) and summed in a fixed order, and the loss terms
    * (out - tgt)^2 ([T]).
    * arg: [0]=states [1]=params [2]=pickup [3]=target ([T]) [4]=adjoint
    *      boundary fields ([4][R][C]) [5]=grad partials [6]=loss terms
@@ -337,6 +337,12 @@ int dgen_hip_profile(dgen_hip_ctx* ctx, uint32_t frame_count, dgen_hip_kernel_ti
 /* Time `iters` back-to-back runs (after `warmup` untimed runs) with one
  * hipEvent pair on stream 0; *ms_out = total milliseconds. */
 int dgen_hip_time_runs(dgen_hip_ctx* ctx, uint32_t frame_count, int warmup, int iters, double* ms_out);
+
+/* Run schedule op `op_index` alone, once, on the arena's current contents,
+ * and wait: for measuring one op in isolation (its HBM traffic under a
+ * counter profiler).  The reference has no counterpart; its profileKernels
+ * (MetalRuntime.swift:397-425) times kernels inside a full run. */
+int dgen_hip_run_op(dgen_hip_ctx* ctx, uint32_t frame_count, uint32_t op_index);
 
 /* Average duration of the launches of schedule op `op_index` over `iters`
  * runs, timed with hipEvents recorded on the stream that op launches on. */
