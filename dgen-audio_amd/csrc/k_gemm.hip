@@ -71,20 +71,22 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const
   const int h = lane >> 5, r = lane & 31;
   const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
   // Workgroups are dealt to the 8 XCDs round-robin by launch order; renumber
-  // them so that each XCD runs a contiguous run of tiles (the N tiles of one
-  // row block share their A rows in that XCD's L2).
-  int bx = blockIdx.x, by = blockIdx.y;
+  // them (over the whole grid, split index outermost) so that each XCD runs a
+  // contiguous run of tiles: the N tiles of one row block share their A rows,
+  // and the tiles of one k-split share both operand chunks, in that XCD's L2.
+  int bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
   {
-    const int tiles = gridDim.x * gridDim.y;
-    if (tiles % 8 == 0) {
-      const int hw = blockIdx.y * gridDim.x + blockIdx.x;
-      const int lg = (hw % 8) * (tiles / 8) + hw / 8;
-      bx = lg % gridDim.x;
-      by = lg / gridDim.x;
+    const int tiles = gridDim.x * gridDim.y, total = tiles * gridDim.z;
+    if (total % 8 == 0) {
+      const int hw = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+      const int lg = (hw % 8) * (total / 8) + hw / 8;
+      bz = lg / tiles;
+      bx = (lg % tiles) % gridDim.x;
+      by = (lg % tiles) / gridDim.x;
     }
   }
   const int m0 = by * BM, n0 = bx * BN;
-  const int kbeg = blockIdx.z * kchunk;
+  const int kbeg = bz * kchunk;
   const int kend = min(K, kbeg + kchunk);
 
   floatx16 acc[2][2];
@@ -232,7 +234,7 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const
       }
   };
   if (ws) {
-    store_all([&](int row, int col, float a) { ws[((size_t)blockIdx.z * M + row) * N + col] = a; });
+    store_all([&](int row, int col, float a) { ws[((size_t)bz * M + row) * N + col] = a; });
   } else if (epi == EPI_BIAS_TANH) {
     store_all([&](int row, int col, float a) { C[(size_t)row * ldc + col] = fast_tanh(a + bias[col]); });
   } else if (epi == EPI_BIAS) {
