@@ -93,10 +93,13 @@ int launch_lerp_frames(const Launch& L, const dgen_hip_op& op) {
 // One workgroup per batch lane b.  Wave 0 runs the K phase chains
 // (lane = k); at 2 dependent VALU ops per step its 64-step segment costs
 // ~128 issue slots, so everything else is kept off its path:
-// - waves 1..4 compute increments into a ring of kCarryBufs segment buffers,
-//   kIv segments per barrier interval, one interval ahead of the chain;
-//   producer waves own frames 0-23, 24-47 and 48-63 of a segment, lane = k
-//   (four waves: one per SIMD, so the chain wave's SIMD runs only it);
+// - waves 1..kProducers compute increments into a ring of kCarryBufs
+//   segment buffers, kIv segments per barrier interval, one interval ahead
+//   of the chain; producer p owns frames 16p .. 16p+15 of a segment, lane = k
+//   (four producers: with three, one per SIMD, each producer's division
+//   work and LDS writes took longer than the chain's segment and the chain
+//   waited at every barrier; a fourth shares the chain's SIMD at lower
+//   priority);
 // - increments are stored k-major ([k][frame], stride 68 floats), so the
 //   chain reads a lane's 64 increments with 16 ds_read_b128 and producers
 //   write them with ds_write_b128, both bank-conflict free;
@@ -106,8 +109,10 @@ int launch_lerp_frames(const Launch& L, const dgen_hip_op& op) {
 //   once per block while loading it;
 // - the chain wave reads segment s+1's increments into registers while it
 //   steps segment s, and has issue priority on its SIMD.
-constexpr int kProducers = 3;
+constexpr int kProducers = 4;
 constexpr int kCarryWaves = 1 + kProducers;
+constexpr int kGroups = (kSeg / 4 + kProducers - 1) / kProducers;  // float4 frame groups per producer
+constexpr int kFrames = 4 * kGroups;
 constexpr int kIv = 3;                  // segments per barrier interval
 constexpr int kCarryBufs = 2 * kIv;     // increment ring
 constexpr int kRing = 16;               // segments per f0 block
@@ -130,28 +135,50 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
   const int nseg = (T + kSeg - 1) / kSeg;
   const float* f0b = f0f + (size_t)b * T;
   const int ptid = threadIdx.x - 64;  // producer thread index
-  auto load_block = [&](int blk) {
+  // An f0 block is loaded in two parts: issue (every load of the thread in
+  // flight at once, from in-bounds clamped addresses) and commit (registers
+  // -> LDS, and the fast-range vote), so that its latency overlaps the
+  // produce work of an interval.
+  constexpr int kBlkLoads = (kRing * kSeg + 64 * kProducers - 1) / (64 * kProducers);
+  float blk_v[kBlkLoads];
+  auto issue_block = [&](int blk) {
+    const int t0 = blk * kRing * kSeg;
+#pragma unroll
+    for (int j = 0; j < kBlkLoads; ++j) {
+      const int i = min(ptid + j * 64 * kProducers, kRing * kSeg - 1);
+      blk_v[j] = f0b[min(t0 + i, T - 1)];
+    }
+  };
+  auto commit_block = [&](int blk) {
     float* dst = s_f0[blk & 1];
     const int t0 = blk * kRing * kSeg;
     int bad = 0;
-    for (int i = ptid; i < kRing * kSeg; i += 64 * kProducers) {
-      const int t = t0 + i;
-      const float v = t < T ? f0b[t] : 0.0f;
-      bad |= !fast_f0(v);
-      dst[i] = v;
+#pragma unroll
+    for (int j = 0; j < kBlkLoads; ++j) {
+      const int i = ptid + j * 64 * kProducers;
+      if (i < kRing * kSeg) {
+        const float v = t0 + i < T ? blk_v[j] : 0.0f;
+        bad |= !fast_f0(v);
+        dst[i] = v;
+      }
     }
     bad = __any(bad);
     if (lane == 0) s_blkbad[blk & 1][wave - 1] = bad;
   };
+  auto load_block = [&](int blk) {
+    issue_block(blk);
+    commit_block(blk);
+  };
   auto produce = [&](int s) {
     const int buf = s % kCarryBufs;
-    const int i0 = (wave - 1) * 24;                 // frames i0 .. i0 + nf - 1
-    const int nf = wave == kProducers ? 16 : 24;
+    // producer p owns frames [4 kGroups p, 4 kGroups (p + 1)) of the segment
+    const int i0 = (wave - 1) * kFrames;
+    const int ng = min(kGroups, kSeg / 4 - (wave - 1) * kGroups);  // its float4 groups
     const float4* f4 = reinterpret_cast<const float4*>(&s_f0[(s / kRing) & 1][(s % kRing) * kSeg + i0]);
-    float f[24];
+    float f[kFrames];
 #pragma unroll
-    for (int q = 0; q < 6; ++q) {
-      const float4 v = q < nf / 4 ? f4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int q = 0; q < kGroups; ++q) {
+      const float4 v = q < ng ? f4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
       f[4 * q] = v.x;
       f[4 * q + 1] = v.y;
       f[4 * q + 2] = v.z;
@@ -163,22 +190,22 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
 #pragma unroll
     for (int w = 0; w < kProducers; ++w) blkbad |= bb[w];
     const bool fast = !blkbad;
-    float inc[24];
+    float inc[kFrames];
     if (fast) {
 #pragma unroll
-      for (int j = 0; j < 24; ++j) {
+      for (int j = 0; j < kFrames; ++j) {
         const float x = kf * f[j];
         const float q0 = x * rsr;
         inc[j] = fmaf(fmaf(-q0, sr, x), rsr, q0);
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < 24; ++j) inc[j] = div_sr(kf * f[j], sr, rsr);
+      for (int j = 0; j < kFrames; ++j) inc[j] = div_sr(kf * f[j], sr, rsr);
     }
     float4* dst = reinterpret_cast<float4*>(&s_inc[buf][lane * kIncLd + i0]);
 #pragma unroll
-    for (int q = 0; q < 6; ++q)
-      if (q < nf / 4) dst[q] = make_float4(inc[4 * q], inc[4 * q + 1], inc[4 * q + 2], inc[4 * q + 3]);
+    for (int q = 0; q < kGroups; ++q)
+      if (q < ng) dst[q] = make_float4(inc[4 * q], inc[4 * q + 1], inc[4 * q + 2], inc[4 * q + 3]);
     if (lane == 0) s_flag[buf][wave] = fast ? 0 : 1;
   };
   // chain: v[32h .. 32h+31] <- half h of segment s's increments
@@ -270,12 +297,19 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
         }
       }
     } else {
-      // f0 block s/16 + 1 goes into the half whose segments are all produced
+      // f0 block s/16 + 1 goes into the half whose segments are all
+      // produced; its loads are issued with segment s and committed after
+      // the interval's produce work (it is first read 16 segments later)
       const int next = s0 + kIv;
+      int pending = -1;
       for (int s = next; s < next + kIv && s < nseg; ++s) {
-        if (s % kRing == 0) load_block(s / kRing + 1);
+        if (s % kRing == 0) {
+          pending = s / kRing + 1;
+          issue_block(pending);
+        }
         produce(s);
       }
+      if (pending >= 0) commit_block(pending);
     }
     lds_barrier();
   }
