@@ -18,10 +18,11 @@ namespace dgen {
 
 constexpr int BM = 128, BN = 128, BK = 32, LDSROW = BM + 4;
 // Row stride of an operand tile that is stored transposed (scalar writes of
-// four k values per thread): 130 floats puts the 8 k-groups of a wave's store
-// on distinct banks (132 would put them 4-way on 16 banks); a tile stored
-// as float4 rows keeps 132 for 16-byte alignment.
-constexpr int LDSROW_T = BM + 2;
+// four k values per thread): an odd stride puts the 32 lanes of each store
+// pass (8 k-groups x 4 rows) on 32 distinct banks (130 folded the k-groups
+// onto 16 banks, 2-way; measured as bank-conflict cycles); a tile stored as
+// float4 rows keeps 132 for 16-byte alignment.
+constexpr int LDSROW_T = BM + 1;
 // float4 loads per thread per operand tile: BM*BK / 4 / 256
 constexpr int LPT = BM * BK / 4 / 256;
 
@@ -54,7 +55,14 @@ __device__ __forceinline__ float apply_epi(int epi, float acc, int row, int col,
 }
 
 // A_KMAJ: A stored [K][M] (else [M][K]); B_NK: B stored [N][K] (else [K][N]).
-template <bool A_KMAJ, bool B_NK, bool VEC>
+// VA / VB: the operand's rows are 16-byte aligned, so its tiles load as
+// float4 (the heads' 127-column weights are not, their activations are).
+// FULL: every tile and k-step lies inside the matrices and both operands
+// are aligned, with byte extents below 2^31: tiles load by raw buffer
+// loads, the thread's offset fixed in a VGPR and the k-step's in an SGPR,
+// with no bounds tests (the generic path spends ~80 VALU and SALU
+// instructions per k-step on them).
+template <bool A_KMAJ, bool B_NK, bool VA, bool VB, bool FULL = false>
 __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const float* __restrict__ B,
                                               float* __restrict__ C, int M, int N, int K, int lda, int ldb, int ldc,
                                               int epi, const float* __restrict__ bias, const float* __restrict__ aux,
@@ -99,7 +107,45 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const
 
   float4 ra[LPT], rb[LPT];
 
+  // FULL: per-thread byte offsets of its LPT float4 loads at k-step 0
+  unsigned va_off[LPT], vb_off[LPT];
+  if constexpr (FULL) {
+#pragma unroll
+    for (int p = 0; p < LPT; ++p) {
+      const int q = tid + p * 256;
+      if (!A_KMAJ) {
+        const int i = q / (BK / 4), kq = (q % (BK / 4)) * 4;
+        va_off[p] = 4u * (unsigned)((m0 + i) * lda + kq);
+      } else {
+        const int kk = q / (BM / 4), iq = (q % (BM / 4)) * 4;
+        va_off[p] = 4u * (unsigned)(kk * lda + m0 + iq);
+      }
+      if (!B_NK) {
+        const int kk = q / (BN / 4), jq = (q % (BN / 4)) * 4;
+        vb_off[p] = 4u * (unsigned)(kk * ldb + n0 + jq);
+      } else {
+        const int j = q / (BK / 4), kq = (q % (BK / 4)) * 4;
+        vb_off[p] = 4u * (unsigned)((n0 + j) * ldb + kq);
+      }
+    }
+  }
+
   auto load_tile = [&](int k0) {
+    if constexpr (FULL) {
+      const auto rsa = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(A), 0,
+                                                         (int)(4u * (unsigned)(A_KMAJ ? K * lda : M * lda)), 0x00020000);
+      const auto rsb = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(B), 0,
+                                                         (int)(4u * (unsigned)(B_NK ? N * ldb : K * ldb)), 0x00020000);
+      // k-step offset: along k within a row, or k rows down
+      const unsigned sa = 4u * (unsigned)(A_KMAJ ? k0 * lda : k0);
+      const unsigned sb = 4u * (unsigned)(B_NK ? k0 : k0 * ldb);
+#pragma unroll
+      for (int p = 0; p < LPT; ++p) {
+        ra[p] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rsa, va_off[p], sa, 0));
+        rb[p] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rsb, vb_off[p], sb, 0));
+      }
+      return;
+    }
 #pragma unroll
     for (int p = 0; p < LPT; ++p) {
       const int q = tid + p * 256;
@@ -107,23 +153,23 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const
         const int i = q / (BK / 4), kq = (q % (BK / 4)) * 4;
         const int row = m0 + i, k = k0 + kq;
         int valid = (row < M) ? min(4, kend - k) : 0;
-        ra[p] = load4<VEC>(A + (size_t)row * lda + k, valid);
+        ra[p] = load4<VA>(A + (size_t)row * lda + k, valid);
       } else {  // [K][M]: float4 along m
         const int kk = q / (BM / 4), iq = (q % (BM / 4)) * 4;
         const int k = k0 + kk, col = m0 + iq;
         int valid = (k < kend) ? min(4, M - col) : 0;
-        ra[p] = load4<VEC>(A + (size_t)k * lda + col, valid);
+        ra[p] = load4<VA>(A + (size_t)k * lda + col, valid);
       }
       if (!B_NK) {  // [K][N]: float4 along n
         const int kk = q / (BN / 4), jq = (q % (BN / 4)) * 4;
         const int k = k0 + kk, col = n0 + jq;
         int valid = (k < kend) ? min(4, N - col) : 0;
-        rb[p] = load4<VEC>(B + (size_t)k * ldb + col, valid);
+        rb[p] = load4<VB>(B + (size_t)k * ldb + col, valid);
       } else {  // [N][K]: float4 along k
         const int j = q / (BK / 4), kq = (q % (BK / 4)) * 4;
         const int col = n0 + j, k = k0 + kq;
         int valid = (col < N) ? min(4, kend - k) : 0;
-        rb[p] = load4<VEC>(B + (size_t)col * ldb + k, valid);
+        rb[p] = load4<VB>(B + (size_t)col * ldb + k, valid);
       }
     }
   };
@@ -254,16 +300,33 @@ __global__ void k_splitk_reduce(const float* __restrict__ ws, float* __restrict_
   C[(size_t)row * ldc + col] = apply_epi(epi, s, row, col, bias, aux, ldaux);
 }
 
-template <bool AK, bool BT>
-static void launch_variant(bool vec, dim3 g, hipStream_t s, const float* A, const float* B, float* C, int M, int N,
-                           int K, int lda, int ldb, int ldc, int epi, const float* bias, const float* aux, int ldaux,
-                           int kchunk, float* ws) {
-  if (vec)
-    hipLaunchKernelGGL((k_gemm<AK, BT, true>), g, dim3(256), 0, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias, aux,
+template <bool AK, bool BT, bool VA>
+static void launch_vb(bool vb, dim3 g, hipStream_t s, const float* A, const float* B, float* C, int M, int N, int K,
+                      int lda, int ldb, int ldc, int epi, const float* bias, const float* aux, int ldaux, int kchunk,
+                      float* ws, bool full) {
+  if constexpr (VA) {
+    if (vb && full) {
+      hipLaunchKernelGGL((k_gemm<AK, BT, true, true, true>), g, dim3(256), 0, s, A, B, C, M, N, K, lda, ldb, ldc, epi,
+                         bias, aux, ldaux, kchunk, ws);
+      return;
+    }
+  }
+  if (vb)
+    hipLaunchKernelGGL((k_gemm<AK, BT, VA, true>), g, dim3(256), 0, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias, aux,
                        ldaux, kchunk, ws);
   else
-    hipLaunchKernelGGL((k_gemm<AK, BT, false>), g, dim3(256), 0, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias, aux,
-                       ldaux, kchunk, ws);
+    hipLaunchKernelGGL((k_gemm<AK, BT, VA, false>), g, dim3(256), 0, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias,
+                       aux, ldaux, kchunk, ws);
+}
+
+template <bool AK, bool BT>
+static void launch_variant(bool va, bool vb, dim3 g, hipStream_t s, const float* A, const float* B, float* C, int M,
+                           int N, int K, int lda, int ldb, int ldc, int epi, const float* bias, const float* aux,
+                           int ldaux, int kchunk, float* ws, bool full) {
+  if (va)
+    launch_vb<AK, BT, true>(vb, g, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias, aux, ldaux, kchunk, ws, full);
+  else
+    launch_vb<AK, BT, false>(vb, g, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias, aux, ldaux, kchunk, ws, full);
 }
 
 int launch_gemm(const Launch& L, const dgen_hip_op& op) {
@@ -295,7 +358,11 @@ int launch_gemm(const Launch& L, const dgen_hip_op& op) {
   if (split > 1) DGEN_CHECK_CELL(L, ws, splits * M * N, "gemm.workspace");
   DGEN_REQUIRE((M + BM - 1) / BM <= 65535 && splits <= 65535, "gemm: grid too large");
   if (L.dry) return 0;
-  const bool vec = (lda % 4 == 0) && (ldb % 4 == 0) && (A % 4 == 0) && (Bc % 4 == 0);
+  const bool va = (lda % 4 == 0) && (A % 4 == 0), vb = (ldb % 4 == 0) && (Bc % 4 == 0);
+  // full tiles and k-steps, and byte extents that fit the buffer loads' 32-bit offsets
+  const int64_t ext_a = 4 * (alay ? K * lda : M * lda), ext_b = 4 * (blay ? N * ldb : K * ldb);
+  const bool full = va && vb && M % BM == 0 && N % BN == 0 && K % BK == 0 && ext_a < (1ll << 31) &&
+                    ext_b < (1ll << 31);
   dim3 g((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM), (unsigned)splits);
   const float* pa = cell(L, A);
   const float* pb = cell(L, Bc);
@@ -305,13 +372,17 @@ int launch_gemm(const Launch& L, const dgen_hip_op& op) {
   float* pws = split > 1 ? cell(L, ws) : nullptr;
   const int e = split > 1 ? EPI_NONE : (int)epi;
   if (alay == 0 && blay == 0)
-    launch_variant<false, false>(vec, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk, pws);
+    launch_variant<false, false>(va, vb, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk, pws,
+                                  full);
   else if (alay == 0 && blay == 1)
-    launch_variant<false, true>(vec, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk, pws);
+    launch_variant<false, true>(va, vb, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk, pws,
+                                  full);
   else if (alay == 1 && blay == 0)
-    launch_variant<true, false>(vec, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk, pws);
+    launch_variant<true, false>(va, vb, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk, pws,
+                                  full);
   else
-    launch_variant<true, true>(vec, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk, pws);
+    launch_variant<true, true>(va, vb, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk, pws,
+                                  full);
   DGEN_LAUNCH_CHECK("k_gemm");
   if (split > 1) {
     const size_t total = (size_t)M * N;
