@@ -66,7 +66,8 @@ template <bool A_KMAJ, bool B_NK, bool VA, bool VB, bool FULL = false>
 __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const float* __restrict__ B,
                                               float* __restrict__ C, int M, int N, int K, int lda, int ldb, int ldc,
                                               int epi, const float* __restrict__ bias, const float* __restrict__ aux,
-                                              int ldaux, int kchunk, float* __restrict__ ws) {
+                                              int ldaux, int kchunk, float* __restrict__ ws,
+                                              float* __restrict__ cs) {
   __shared__ float As_[2][BK * LDSROW];
   __shared__ float Bs_[2][BK * LDSROW];
   constexpr int RA = A_KMAJ ? LDSROW : LDSROW_T;  // A is transposed when stored [M][K]
@@ -261,8 +262,36 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const
           const int row = m0 + wm + ti * 32 + (v >> 2) * 8 + h * 4 + (v & 3);
           const int col = n0 + wn + tj * 32 + r;
           const float hh = hv[ti][tj][v];
-          if (row < M && col < N) C[(size_t)row * ldc + col] = acc[ti][tj][v] * (1.f - hh * hh);
+          acc[ti][tj][v] *= 1.f - hh * hh;
+          if (row < M && col < N) C[(size_t)row * ldc + col] = acc[ti][tj][v];
         }
+    if (cs) {
+      // column sums of the 128-row tile just stored: each lane sums its 32
+      // rows of column wn + tj*32 + r (rows past M excluded), lanes r and
+      // r+32 (the other four rows of every group of eight) are added, then
+      // the two waves sharing the columns, top half first
+      float s[2];
+#pragma unroll
+      for (int tj = 0; tj < 2; ++tj) {
+        s[tj] = 0.f;
+#pragma unroll
+        for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int row = m0 + wm + ti * 32 + (v >> 2) * 8 + h * 4 + (v & 3);
+            s[tj] += row < M ? acc[ti][tj][v] : 0.f;
+          }
+        s[tj] += __shfl_xor(s[tj], 32, 64);
+      }
+      // the k-loop's last barrier has retired every read of the operand tiles
+      float* red = As_[0];
+      red[wave * 64 + lane] = lane < 32 ? s[0] : s[1];
+      __syncthreads();
+      if (wave < 2) {
+        const int col = n0 + wn + lane;
+        if (col < N) cs[(size_t)by * N + col] = red[wave * 64 + lane] + red[(wave + 2) * 64 + lane];
+      }
+    }
     return;
   }
   // one uniform branch per epilogue kind, then a straight store loop
@@ -290,50 +319,81 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const
   }
 }
 
+// C = sum over the k-splits of the partial products, in split order, then
+// the epilogue.  V4: each thread owns four consecutive columns (N, ldc and the
+// workspace rows allow float4) and keeps 16 splits' loads in flight.
+template <bool V4>
 __global__ void k_splitk_reduce(const float* __restrict__ ws, float* __restrict__ C, int M, int N, int ldc, int splits,
                                 int epi, const float* __restrict__ bias, const float* __restrict__ aux, int ldaux) {
-  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  constexpr int CW = V4 ? 4 : 1;
+  const size_t idx = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * CW;
   if (idx >= (size_t)M * N) return;
   const int row = (int)(idx / N), col = (int)(idx % N);
-  float s = 0.f;
-  for (int z = 0; z < splits; ++z) s += ws[(size_t)z * M * N + idx];
-  C[(size_t)row * ldc + col] = apply_epi(epi, s, row, col, bias, aux, ldaux);
+  const size_t plane = (size_t)M * N;
+  float s[CW];
+#pragma unroll
+  for (int e = 0; e < CW; ++e) s[e] = 0.f;
+  int z = 0;
+  for (; z + 16 <= splits; z += 16) {
+    float v[16][CW];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      if constexpr (V4) {
+        const float4 t = *reinterpret_cast<const float4*>(ws + (size_t)(z + q) * plane + idx);
+        v[q][0] = t.x;
+        v[q][1] = t.y;
+        v[q][2] = t.z;
+        v[q][3] = t.w;
+      } else {
+        v[q][0] = ws[(size_t)(z + q) * plane + idx];
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 16; ++q)
+#pragma unroll
+      for (int e = 0; e < CW; ++e) s[e] += v[q][e];
+  }
+  for (; z < splits; ++z)
+#pragma unroll
+    for (int e = 0; e < CW; ++e) s[e] += ws[(size_t)z * plane + idx + e];
+#pragma unroll
+  for (int e = 0; e < CW; ++e) C[(size_t)row * ldc + col + e] = apply_epi(epi, s[e], row, col + e, bias, aux, ldaux);
 }
 
 template <bool AK, bool BT, bool VA>
 static void launch_vb(bool vb, dim3 g, hipStream_t s, const float* A, const float* B, float* C, int M, int N, int K,
                       int lda, int ldb, int ldc, int epi, const float* bias, const float* aux, int ldaux, int kchunk,
-                      float* ws, bool full) {
+                      float* ws, float* cs, bool full) {
   if constexpr (VA) {
     if (vb && full) {
       hipLaunchKernelGGL((k_gemm<AK, BT, true, true, true>), g, dim3(256), 0, s, A, B, C, M, N, K, lda, ldb, ldc, epi,
-                         bias, aux, ldaux, kchunk, ws);
+                         bias, aux, ldaux, kchunk, ws, cs);
       return;
     }
   }
   if (vb)
     hipLaunchKernelGGL((k_gemm<AK, BT, VA, true>), g, dim3(256), 0, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias, aux,
-                       ldaux, kchunk, ws);
+                       ldaux, kchunk, ws, cs);
   else
     hipLaunchKernelGGL((k_gemm<AK, BT, VA, false>), g, dim3(256), 0, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias,
-                       aux, ldaux, kchunk, ws);
+                       aux, ldaux, kchunk, ws, cs);
 }
 
 template <bool AK, bool BT>
 static void launch_variant(bool va, bool vb, dim3 g, hipStream_t s, const float* A, const float* B, float* C, int M,
                            int N, int K, int lda, int ldb, int ldc, int epi, const float* bias, const float* aux,
-                           int ldaux, int kchunk, float* ws, bool full) {
+                           int ldaux, int kchunk, float* ws, float* cs, bool full) {
   if (va)
-    launch_vb<AK, BT, true>(vb, g, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias, aux, ldaux, kchunk, ws, full);
+    launch_vb<AK, BT, true>(vb, g, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias, aux, ldaux, kchunk, ws, cs, full);
   else
-    launch_vb<AK, BT, false>(vb, g, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias, aux, ldaux, kchunk, ws, full);
+    launch_vb<AK, BT, false>(vb, g, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias, aux, ldaux, kchunk, ws, cs, full);
 }
 
 int launch_gemm(const Launch& L, const dgen_hip_op& op) {
   const int64_t A = op.arg[0], Bc = op.arg[1], Cc = op.arg[2], M = op.arg[3], N = op.arg[4], K = op.arg[5];
   const int64_t lda = op.arg[6], ldb = op.arg[7], ldc = op.arg[8], alay = op.arg[9], blay = op.arg[10];
   const int64_t epi = op.arg[11], bias = op.arg[12], aux = op.arg[13], ldaux = op.arg[14];
-  const int64_t split = op.arg[15], ws = op.arg[16];
+  const int64_t split = op.arg[15], ws = op.arg[16], colsum = op.arg[17];
   DGEN_REQUIRE(M > 0 && N > 0 && K > 0 && M < (1ll << 31) && N < (1ll << 31) && K < (1ll << 31),
                "gemm: M %lld N %lld K %lld", (long long)M, (long long)N, (long long)K);
   DGEN_REQUIRE(alay == 0 || alay == 1, "gemm: a_layout %lld", (long long)alay);
@@ -356,6 +416,10 @@ int launch_gemm(const Launch& L, const dgen_hip_op& op) {
   kchunk = (kchunk + BK - 1) / BK * BK;
   const int64_t splits = (K + kchunk - 1) / kchunk;
   if (split > 1) DGEN_CHECK_CELL(L, ws, splits * M * N, "gemm.workspace");
+  if (colsum >= 0) {
+    DGEN_REQUIRE(epi == EPI_TANH_GRAD && splits == 1, "gemm: column partials need the tanh-gradient epilogue, no split");
+    DGEN_CHECK_CELL(L, colsum, (M + BM - 1) / BM * N, "gemm.column_partials");
+  }
   DGEN_REQUIRE((M + BM - 1) / BM <= 65535 && splits <= 65535, "gemm: grid too large");
   if (L.dry) return 0;
   const bool va = (lda % 4 == 0) && (A % 4 == 0), vb = (ldb % 4 == 0) && (Bc % 4 == 0);
@@ -370,24 +434,29 @@ int launch_gemm(const Launch& L, const dgen_hip_op& op) {
   const float* pbias = (epi == EPI_BIAS || epi == EPI_BIAS_TANH) ? cell(L, bias) : nullptr;
   const float* paux = epi == EPI_TANH_GRAD ? cell(L, aux) : nullptr;
   float* pws = split > 1 ? cell(L, ws) : nullptr;
+  float* pcs = colsum >= 0 ? cell(L, colsum) : nullptr;
   const int e = split > 1 ? EPI_NONE : (int)epi;
   if (alay == 0 && blay == 0)
     launch_variant<false, false>(va, vb, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk, pws,
-                                  full);
+                                  pcs, full);
   else if (alay == 0 && blay == 1)
     launch_variant<false, true>(va, vb, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk, pws,
-                                  full);
+                                  pcs, full);
   else if (alay == 1 && blay == 0)
     launch_variant<true, false>(va, vb, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk, pws,
-                                  full);
+                                  pcs, full);
   else
     launch_variant<true, true>(va, vb, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk, pws,
-                                  full);
+                                  pcs, full);
   DGEN_LAUNCH_CHECK("k_gemm");
   if (split > 1) {
     const size_t total = (size_t)M * N;
-    hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, L.stream, pws, pc, (int)M,
-                       (int)N, (int)ldc, (int)splits, (int)epi, pbias, paux, (int)ldaux);
+    if (N % 4 == 0 && ws % 4 == 0)
+      hipLaunchKernelGGL(k_splitk_reduce<true>, dim3((unsigned)((total / 4 + 255) / 256)), dim3(256), 0, L.stream, pws,
+                         pc, (int)M, (int)N, (int)ldc, (int)splits, (int)epi, pbias, paux, (int)ldaux);
+    else
+      hipLaunchKernelGGL(k_splitk_reduce<false>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, L.stream, pws,
+                         pc, (int)M, (int)N, (int)ldc, (int)splits, (int)epi, pbias, paux, (int)ldaux);
     DGEN_LAUNCH_CHECK("k_splitk_reduce");
   }
   return 0;

@@ -18,6 +18,7 @@ SLOTS = 4         # control rows a segment may touch
 ROW_ENTRIES = 8   # (segment, slot) entries per control row
 LDC = 128         # padded control-row stride (K + 2 + NF <= 128)
 SPLITK_ROWS = 1024  # rows per split of the weight-gradient GEMMs
+GEMM_TILE_M = 128  # output rows per GEMM workgroup tile (k_gemm.hip BM)
 SPLITK_ROWS_HEADS = 512  # the heads' weight gradient has one 128-wide column tile: split finer to fill the chip
 MSS_TILE = 4096     # output samples per spectral-loss workgroup
 BQ_CHUNK = 256      # frames per biquad scan chunk
@@ -127,9 +128,10 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     gemm_hh = dict(flops=2.0 * M * Hd * Hd, bound="mfma")
     for l in range(1, Lyr):
         W, b = woff[l]
-        p.add(R.K_GEMM, [Hs[l - 1], W, Hs[l], M, Hd, Hd, Hd, Hd, Hd, 0, 0, R.EPI_BIAS_TANH, b, -1, 0, 1, 0],
+        p.add(R.K_GEMM, [Hs[l - 1], W, Hs[l], M, Hd, Hd, Hd, Hd, Hd, 0, 0, R.EPI_BIAS_TANH, b, -1, 0, 1, 0, -1],
               label=f"mlp_l{l + 1}", dispatch="gemm", bytes=(2 * M * Hd + Hd * Hd + Hd) * f4, **gemm_hh)
-    p.add(R.K_GEMM, [Hs[-1], Wh, Z, M, NC, Hd, Hd, NC, LDC, 0, 0, R.EPI_BIAS, bh, -1, 0, 1, 0], label="mlp_heads",
+    p.add(R.K_GEMM, [Hs[-1], Wh, Z, M, NC, Hd, Hd, NC, LDC, 0, 0, R.EPI_BIAS, bh, -1, 0, 1, 0, -1],
+          label="mlp_heads",
           dispatch="gemm", bytes=(M * Hd + Hd * NC + NC + M * NC) * f4, flops=2.0 * M * Hd * NC, bound="mfma")
     p.add(R.K_HEADS_FWD, [Z, ctrl, M, K, NF, LDC], label="heads", dispatch=f"perFrameScaled({M})",
           bytes=2 * M * NC * f4, flops=M * (K * 12.0 + NF * 8.0))
@@ -207,23 +209,28 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     gW = [(G + (w - P), G + (b - P)) for (w, b) in woff]
     gWh, gbh = G + (Wh - P), G + (bh - P)
     # heads: dWh = H_L^T dZ ; dbh = colsum(dZ) ; dH_L = (dZ Wh^T) * (1 - H_L^2)
-    p.add(R.K_GEMM, [Hs[-1], dZ, gWh, Hd, NC, M, Hd, LDC, NC, 1, 0, R.EPI_NONE, -1, -1, 0, split_h, ws_gemm],
+    p.add(R.K_GEMM, [Hs[-1], dZ, gWh, Hd, NC, M, Hd, LDC, NC, 1, 0, R.EPI_NONE, -1, -1, 0, split_h, ws_gemm, -1],
           label="dW_heads", dispatch="gemmChunkPartials", bytes=(M * Hd + M * NC + Hd * NC) * f4,
           flops=2.0 * M * Hd * NC, bound="mfma")
     p.add(R.K_COLSUM, [dZ, gbh, M, NC, LDC, ws_col], label="db_heads", dispatch="chunkPartialsReduceToCell",
           bytes=(M * NC + NC) * f4, flops=float(M * NC))
     dH = [p.alloc(f"dZ{l + 1}", M * Hd) for l in range(Lyr)]
-    p.add(R.K_GEMM, [dZ, Wh, dH[-1], M, Hd, NC, LDC, NC, Hd, 0, 1, R.EPI_TANH_GRAD, -1, Hs[-1], Hd, 1, 0],
+    # column sums of dH[l] per 128-row GEMM tile, written by the data GEMM
+    # that produces dH[l]; the bias gradient reduces these tile rows
+    mt = (M + GEMM_TILE_M - 1) // GEMM_TILE_M
+    dcol = [p.alloc(f"dZ{l + 1}_tile_colsums", mt * Hd) if l > 0 else -1 for l in range(Lyr)]
+    p.add(R.K_GEMM, [dZ, Wh, dH[-1], M, Hd, NC, LDC, NC, Hd, 0, 1, R.EPI_TANH_GRAD, -1, Hs[-1], Hd, 1, 0, dcol[-1]],
           label=f"dX_heads", dispatch="gemm", bytes=(M * NC + Hd * NC + 2 * M * Hd) * f4, flops=2.0 * M * Hd * NC,
           bound="mfma")
     for l in range(Lyr - 1, 0, -1):
         W, _b = woff[l]
         gw, gb = gW[l]
-        p.add(R.K_GEMM, [Hs[l - 1], dH[l], gw, Hd, Hd, M, Hd, Hd, Hd, 1, 0, R.EPI_NONE, -1, -1, 0, split, ws_gemm],
+        p.add(R.K_GEMM, [Hs[l - 1], dH[l], gw, Hd, Hd, M, Hd, Hd, Hd, 1, 0, R.EPI_NONE, -1, -1, 0, split, ws_gemm, -1],
               label=f"dW_l{l + 1}", dispatch="gemmChunkPartials", bytes=(2 * M * Hd + Hd * Hd) * f4, **gemm_hh)
-        p.add(R.K_COLSUM, [dH[l], gb, M, Hd, Hd, ws_col], label=f"db_l{l + 1}", dispatch="chunkPartialsReduceToCell",
-              bytes=(M * Hd + Hd) * f4, flops=float(M * Hd))
-        p.add(R.K_GEMM, [dH[l], W, dH[l - 1], M, Hd, Hd, Hd, Hd, Hd, 0, 1, R.EPI_TANH_GRAD, -1, Hs[l - 1], Hd, 1, 0],
+        p.add(R.K_COLSUM, [dcol[l], gb, mt, Hd, Hd, ws_col], label=f"db_l{l + 1}",
+              dispatch="chunkPartialsReduceToCell", bytes=(mt * Hd + Hd) * f4, flops=float(mt * Hd))
+        p.add(R.K_GEMM, [dH[l], W, dH[l - 1], M, Hd, Hd, Hd, Hd, Hd, 0, 1, R.EPI_TANH_GRAD, -1, Hs[l - 1], Hd, 1, 0,
+                         dcol[l - 1]],
               label=f"dX_l{l + 1}", dispatch="gemm", bytes=(3 * M * Hd + Hd * Hd) * f4, **gemm_hh)
     gw1, gb1 = gW[0]
     p.add(R.K_DENSE_SMALL_WGRAD, [X, dH[0], gw1, M, din, Hd, ws_col, gb1], label="dWb_l1",

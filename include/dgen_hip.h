@@ -64,7 +64,11 @@ enum dgen_hip_kernel {
    *      [10]=b_layout (0: B stored [K][N], 1: B stored [N][K])
    *      [11]=epilogue (DGEN_HIP_EPI_*) [12]=bias cell (-1 none)
    *      [13]=aux cell (tanh output for EPI_TANH_GRAD, -1 none) [14]=ld aux
-   *      [15]=split_k (1 = none; >1: partial sums in [16]) [16]=workspace cell */
+   *      [15]=split_k (1 = none; >1: partial sums in [16]) [16]=workspace cell
+   *      [17]=column-partials cell or -1: with EPI_TANH_GRAD and no split,
+   *           row t (t < ceil(M/128)) receives the column sums of output
+   *           rows [128t, 128t+128), so a bias gradient is a reduction over
+   *           ceil(M/128) rows instead of M (DGEN_HIP_K_COLSUM on the cell) */
   DGEN_HIP_K_GEMM = 3,
 
   /* Head activations of HarmonicDecoderModel (Model.swift:100-114):
