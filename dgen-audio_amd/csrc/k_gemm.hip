@@ -11,20 +11,33 @@
 // LDS holds both operand tiles k-major ([BK][BM] and [BK][BN]) so every
 // layout (A as [M][K] or [K][M], B as [K][N] or [N][K]) feeds the MFMA with
 // conflict-free single-float reads; tiles are double buffered with one
-// barrier per k-step.
+// barrier per k-step.  Two k-step depths:
+// - BK = 16: 33 KB of LDS and at most 128 registers per lane, so four
+//   workgroups share a CU (four waves per SIMD): a 1000-tile grid runs in one
+//   round on 256 CUs, and each SIMD has other waves' MFMAs to issue while one
+//   waits at its barrier (the backward GEMMs, 5-10% faster);
+// - BK = 32: 66 KB, two workgroups per CU.  The hidden forward layers (bias
+//   + tanh epilogue) use it: they run beside the phasor carry, whose serial
+//   chain is the step's critical path while they do; measured, the denser
+//   BK = 16 forward GEMMs slowed the carry by more (0.50 -> 0.62 ms) than
+//   they gained themselves.
 #include "internal.h"
 
 namespace dgen {
 
-constexpr int BM = 128, BN = 128, BK = 32, LDSROW = BM + 4;
+constexpr int BM = 128, BN = 128, LDSROW = BM + 4;
 // Row stride of an operand tile that is stored transposed (scalar writes of
-// four k values per thread): an odd stride puts the 32 lanes of each store
-// pass (8 k-groups x 4 rows) on 32 distinct banks (130 folded the k-groups
-// onto 16 banks, 2-way; measured as bank-conflict cycles); a tile stored as
-// float4 rows keeps 132 for 16-byte alignment.
-constexpr int LDSROW_T = BM + 1;
-// float4 loads per thread per operand tile: BM*BK / 4 / 256
-constexpr int LPT = BM * BK / 4 / 256;
+// four k values per thread).  The 32 lanes of a store pass cover BK/4
+// k-groups x 128/BK rows:
+// - BK = 16: 4 k-groups (k = 0, 4, 8, 12) x 8 rows; a stride of 2 mod 32
+//   puts them on 32 distinct banks (k-group g at banks 8g .. 8g+7);
+// - BK = 32: 8 k-groups x 4 rows; an odd stride does (2 mod 32 would fold
+//   the k-groups onto 16 banks, 2-way; measured as bank-conflict cycles).
+// The MFMA reads (one k, 32 consecutive rows per pass) are conflict-free
+// either way.  A tile stored as float4 rows keeps 132 for 16-byte alignment.
+template <int BK>
+constexpr int ldsrow_t() { return BK == 16 ? BM + 2 : BM + 1; }
+static_assert(ldsrow_t<16>() % 32 == 2 && ldsrow_t<32>() % 32 == 1, "transposed-store bank layout");
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
@@ -62,12 +75,16 @@ __device__ __forceinline__ float apply_epi(int epi, float acc, int row, int col,
 // loads, the thread's offset fixed in a VGPR and the k-step's in an SGPR,
 // with no bounds tests (the generic path spends ~80 VALU and SALU
 // instructions per k-step on them).
-template <bool A_KMAJ, bool B_NK, bool VA, bool VB, bool FULL = false>
-__global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const float* __restrict__ B,
+template <int BK, bool A_KMAJ, bool B_NK, bool VA, bool VB, bool FULL = false>
+__global__ __launch_bounds__(256, BK == 16 ? 4 : 2) void k_gemm(const float* __restrict__ A, const float* __restrict__ B,
                                               float* __restrict__ C, int M, int N, int K, int lda, int ldb, int ldc,
                                               int epi, const float* __restrict__ bias, const float* __restrict__ aux,
                                               int ldaux, int kchunk, float* __restrict__ ws,
                                               float* __restrict__ cs) {
+  static_assert(BK == 16 || BK == 32, "k-step depth");
+  // float4 loads per thread per operand tile
+  constexpr int LPT = BM * BK / 4 / 256;
+  constexpr int LDSROW_T = ldsrow_t<BK>();
   __shared__ float As_[2][BK * LDSROW];
   __shared__ float Bs_[2][BK * LDSROW];
   constexpr int RA = A_KMAJ ? LDSROW : LDSROW_T;  // A is transposed when stored [M][K]
@@ -241,30 +258,25 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, const
   // Accumulator layout of a 32x32 MFMA block: register v of lane l holds
   // row 8*(v/4) + 4*(l/32) + v%4, column l%32.
   if (!ws && epi == EPI_TANH_GRAD) {
-    // issue all 64 loads of the tanh outputs before using any
-    float hv[2][2][16];
+    // per 32x32 block: issue its 16 loads of the tanh outputs, then use them
 #pragma unroll
     for (int ti = 0; ti < 2; ++ti)
 #pragma unroll
-      for (int tj = 0; tj < 2; ++tj)
+      for (int tj = 0; tj < 2; ++tj) {
+        const int col = n0 + wn + tj * 32 + r;
+        float hv[16];
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int row = m0 + wm + ti * 32 + (v >> 2) * 8 + h * 4 + (v & 3);
-          const int col = n0 + wn + tj * 32 + r;
-          hv[ti][tj][v] = (row < M && col < N) ? aux[(size_t)row * ldaux + col] : 0.f;
+          hv[v] = (row < M && col < N) ? aux[(size_t)row * ldaux + col] : 0.f;
         }
 #pragma unroll
-    for (int ti = 0; ti < 2; ++ti)
-#pragma unroll
-      for (int tj = 0; tj < 2; ++tj)
-#pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int row = m0 + wm + ti * 32 + (v >> 2) * 8 + h * 4 + (v & 3);
-          const int col = n0 + wn + tj * 32 + r;
-          const float hh = hv[ti][tj][v];
-          acc[ti][tj][v] *= 1.f - hh * hh;
+          acc[ti][tj][v] *= 1.f - hv[v] * hv[v];
           if (row < M && col < N) C[(size_t)row * ldc + col] = acc[ti][tj][v];
         }
+      }
     if (cs) {
       // column sums of the 128-row tile just stored: each lane sums its 32
       // rows of column wn + tj*32 + r (rows past M excluded), lanes r and
@@ -360,33 +372,51 @@ __global__ void k_splitk_reduce(const float* __restrict__ ws, float* __restrict_
   for (int e = 0; e < CW; ++e) C[(size_t)row * ldc + col + e] = apply_epi(epi, s[e], row, col + e, bias, aux, ldaux);
 }
 
-template <bool AK, bool BT, bool VA>
+template <int BK, bool AK, bool BT, bool VA>
 static void launch_vb(bool vb, dim3 g, hipStream_t s, const float* A, const float* B, float* C, int M, int N, int K,
                       int lda, int ldb, int ldc, int epi, const float* bias, const float* aux, int ldaux, int kchunk,
                       float* ws, float* cs, bool full) {
   if constexpr (VA) {
     if (vb && full) {
-      hipLaunchKernelGGL((k_gemm<AK, BT, true, true, true>), g, dim3(256), 0, s, A, B, C, M, N, K, lda, ldb, ldc, epi,
-                         bias, aux, ldaux, kchunk, ws, cs);
+      hipLaunchKernelGGL((k_gemm<BK, AK, BT, true, true, true>), g, dim3(256), 0, s, A, B, C, M, N, K, lda, ldb, ldc,
+                         epi, bias, aux, ldaux, kchunk, ws, cs);
       return;
     }
   }
   if (vb)
-    hipLaunchKernelGGL((k_gemm<AK, BT, VA, true>), g, dim3(256), 0, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias, aux,
-                       ldaux, kchunk, ws, cs);
+    hipLaunchKernelGGL((k_gemm<BK, AK, BT, VA, true>), g, dim3(256), 0, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias,
+                       aux, ldaux, kchunk, ws, cs);
   else
-    hipLaunchKernelGGL((k_gemm<AK, BT, VA, false>), g, dim3(256), 0, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias,
+    hipLaunchKernelGGL((k_gemm<BK, AK, BT, VA, false>), g, dim3(256), 0, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias,
                        aux, ldaux, kchunk, ws, cs);
 }
 
-template <bool AK, bool BT>
+template <int BK, bool AK, bool BT>
 static void launch_variant(bool va, bool vb, dim3 g, hipStream_t s, const float* A, const float* B, float* C, int M,
                            int N, int K, int lda, int ldb, int ldc, int epi, const float* bias, const float* aux,
                            int ldaux, int kchunk, float* ws, float* cs, bool full) {
   if (va)
-    launch_vb<AK, BT, true>(vb, g, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias, aux, ldaux, kchunk, ws, cs, full);
+    launch_vb<BK, AK, BT, true>(vb, g, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias, aux, ldaux, kchunk, ws, cs, full);
   else
-    launch_vb<AK, BT, false>(vb, g, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias, aux, ldaux, kchunk, ws, cs, full);
+    launch_vb<BK, AK, BT, false>(vb, g, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias, aux, ldaux, kchunk, ws, cs, full);
+}
+
+template <int BK>
+static void launch_layout(int64_t alay, int64_t blay, bool va, bool vb, dim3 g, hipStream_t s, const float* A,
+                          const float* B, float* C, int M, int N, int K, int lda, int ldb, int ldc, int epi,
+                          const float* bias, const float* aux, int ldaux, int kchunk, float* ws, float* cs, bool full) {
+  if (alay == 0 && blay == 0)
+    launch_variant<BK, false, false>(va, vb, g, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias, aux, ldaux, kchunk, ws,
+                                     cs, full);
+  else if (alay == 0 && blay == 1)
+    launch_variant<BK, false, true>(va, vb, g, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias, aux, ldaux, kchunk, ws,
+                                    cs, full);
+  else if (alay == 1 && blay == 0)
+    launch_variant<BK, true, false>(va, vb, g, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias, aux, ldaux, kchunk, ws,
+                                    cs, full);
+  else
+    launch_variant<BK, true, true>(va, vb, g, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias, aux, ldaux, kchunk, ws,
+                                   cs, full);
 }
 
 int launch_gemm(const Launch& L, const dgen_hip_op& op) {
@@ -411,6 +441,9 @@ int launch_gemm(const Launch& L, const dgen_hip_op& op) {
     DGEN_REQUIRE(ldaux >= N, "gemm: ld aux %lld", (long long)ldaux);
     DGEN_CHECK_CELL(L, aux, (M - 1) * ldaux + N, "gemm.aux");
   }
+  // the hidden forward layers (bias + tanh) take the 32-deep k-step, every
+  // other GEMM the 16-deep one (see the header comment)
+  const int BK = epi == EPI_BIAS_TANH ? 32 : 16;
   // k-chunk per split, a multiple of BK
   int64_t kchunk = (K + split - 1) / split;
   kchunk = (kchunk + BK - 1) / BK * BK;
@@ -436,18 +469,12 @@ int launch_gemm(const Launch& L, const dgen_hip_op& op) {
   float* pws = split > 1 ? cell(L, ws) : nullptr;
   float* pcs = colsum >= 0 ? cell(L, colsum) : nullptr;
   const int e = split > 1 ? EPI_NONE : (int)epi;
-  if (alay == 0 && blay == 0)
-    launch_variant<false, false>(va, vb, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk, pws,
-                                  pcs, full);
-  else if (alay == 0 && blay == 1)
-    launch_variant<false, true>(va, vb, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk, pws,
-                                  pcs, full);
-  else if (alay == 1 && blay == 0)
-    launch_variant<true, false>(va, vb, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk, pws,
-                                  pcs, full);
+  if (BK == 32)
+    launch_layout<32>(alay, blay, va, vb, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk,
+                      pws, pcs, full);
   else
-    launch_variant<true, true>(va, vb, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk, pws,
-                                  pcs, full);
+    launch_layout<16>(alay, blay, va, vb, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk,
+                      pws, pcs, full);
   DGEN_LAUNCH_CHECK("k_gemm");
   if (split > 1) {
     const size_t total = (size_t)M * N;
