@@ -9,6 +9,9 @@
 // out[(j/Ns)*Ns*R + j mod Ns + r*Ns].  Radix 8 passes first, then one 4 or 2.
 // Every thread of the workgroup must call fft() together (it contains
 // workgroup barriers); each group of M/8 threads works on its own buffer.
+// With WAVE, the M/8 threads of every buffer lie in one wave and the passes
+// are ordered by wave_sync() instead of workgroup barriers (each wave then
+// runs its transforms without waiting for the others).
 //
 // Buffers are padded: complex value i lives at i + i/8.  A Stockham pass
 // writes R consecutive values per thread, a stride of 8R bytes across the
@@ -131,27 +134,27 @@ __device__ __forceinline__ int in_pos(int j, int e) {
 
 // Middle passes 1 .. npass-2 in LDS (in place; a barrier separates each
 // pass's reads from its writes).
-template <int LOGM, int P, bool INV>
+template <int LOGM, int P, bool INV, bool WAVE = false>
 __device__ __forceinline__ void mid_passes(PadBuf buf, int j, c2* v) {
   constexpr int M = 1 << LOGM;
   if constexpr (P < pass_count(LOGM) - 1) {
     constexpr int R = pass_radix(LOGM, P), NS = pass_span(LOGM, P);
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = buf[in_pos<M, R>(j, e)];
-    lds_barrier();
+    lds_sync<WAVE>();
     int op[8];
     pass_compute<M, R, NS, INV>(v, j, op);
 #pragma unroll
     for (int e = 0; e < 8; ++e) buf[op[e]] = v[e];
-    lds_barrier();
-    mid_passes<LOGM, P + 1, INV>(buf, j, v);
+    lds_sync<WAVE>();
+    mid_passes<LOGM, P + 1, INV, WAVE>(buf, j, v);
   }
 }
 
 // Full M-point FFT: v holds the first pass's inputs (v[e] = input at
 // in_pos of pass 0); on return v holds the last pass's outputs at positions
 // op[e].  Uses buf (M complex, this window's slot) between passes.
-template <int LOGM, bool INV>
+template <int LOGM, bool INV, bool WAVE = false>
 __device__ __forceinline__ void fft(PadBuf buf, int j, c2* v, int* op) {
   constexpr int M = 1 << LOGM;
   constexpr int NP = pass_count(LOGM);
@@ -162,12 +165,12 @@ __device__ __forceinline__ void fft(PadBuf buf, int j, c2* v, int* op) {
   if constexpr (NP > 1) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) buf[op[e]] = v[e];
-    lds_barrier();
-    mid_passes<LOGM, 1, INV>(buf, j, v);
+    lds_sync<WAVE>();
+    mid_passes<LOGM, 1, INV, WAVE>(buf, j, v);
     constexpr int RL = pass_radix(LOGM, NP - 1), NSL = pass_span(LOGM, NP - 1);
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = buf[in_pos<M, RL>(j, e)];
-    lds_barrier();
+    lds_sync<WAVE>();
     pass_compute<M, RL, NSL, INV>(v, j, op);
   }
 }

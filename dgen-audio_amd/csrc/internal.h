@@ -65,6 +65,24 @@ using Launcher = int (*)(const Launch&, const dgen_hip_op&);
 // the workgroup is needed.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// Orders one wave's LDS accesses around this point for every lane of the
+// wave: a wave's LDS instructions execute in issue order, so only the
+// compiler has to be kept from moving accesses across it (no hardware
+// barrier).
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Workgroup barrier, or the wave-level ordering above when every thread
+// that shares the LDS data lies in the calling wave.
+template <bool WAVE>
+__device__ __forceinline__ void lds_sync() {
+  if constexpr (WAVE) wave_sync();
+  else lds_barrier();
+}
+
 // tanh within a few ulp at a fraction of the libm cost: for |x| < 0.55 the
 // odd Taylor series to x^15 (truncation below 5e-8 relative; the series
 // converges for |x| < pi/2), otherwise 1 - 2/(e^{2|x|} + 1) on the hardware

@@ -364,12 +364,6 @@ struct SegLds {
   float dfl[kSeg];
 };
 
-__device__ __forceinline__ void wave_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 // Stage the segment's frame records, rows, their harmonic prefix sums (if
 // want_pre) and the noise window.  Returns 1 if every frame's f0 admits the
 // fast chain step.

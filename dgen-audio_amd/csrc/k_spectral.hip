@@ -24,7 +24,10 @@
 // - the accumulator spans [a-2047, a+4096); the part left of a belongs to the
 //   previous tile and is added by k_mss_combine, which also forms the
 //   per-frame loss signal.
-// The FFT passes are the shared LDS Stockham transform of fft_lds.h.
+// The FFT passes are the shared LDS Stockham transform of fft_lds.h.  For
+// N <= 1024 a window's N/16 threads lie in one wave, so its transforms and
+// bins are ordered by wave-level syncs and the waves run independently; one
+// workgroup barrier per group guards the shared accumulator.
 #include "fft_lds.h"
 
 namespace dgen {
@@ -68,6 +71,11 @@ template <int LOGN>
 __device__ __forceinline__ void mss_size(const MssArgs& a, MssLds& L, int si, int b, int tile) {
   constexpr int N = 1 << LOGN, M = N / 2, LOGM = LOGN - 1, H = N / 4, P = M / 8, W = kThreads / P;
   static_assert(W * M == 2048, "window slots must fill the FFT buffer");
+  // a window's P threads (and its FFT slots) lie in one wave when P <= 64:
+  // its transforms and bins then need only wave-level ordering; the
+  // workgroup barrier is kept for the shared accumulator (windows of
+  // consecutive groups overlap) and for the cross-wave loss sums (P > 64)
+  constexpr bool WL = P <= 64;
   const int tid = threadIdx.x;
   const int slot = tid / P, j = tid % P;
   const PadBuf buf{L.buf + slot * lds_pad(M)};
@@ -115,11 +123,11 @@ __device__ __forceinline__ void mss_size(const MssArgs& a, MssLds& L, int si, in
         const float h0 = L.hann[2 * n], h1 = L.hann[2 * n + 1];
         v[e] = pass == 0 ? c2{pt[2 * e] * h0, pt[2 * e + 1] * h1} : c2{px[2 * e] * h0, px[2 * e + 1] * h1};
       }
-      fft<LOGM, false>(buf, j, v, op);
+      fft<LOGM, false, WL>(buf, j, v, op);
       const PadBuf dst = pass == 0 ? spec : buf;
 #pragma unroll
       for (int e = 0; e < 8; ++e) dst[op[e]] = v[e];
-      lds_barrier();
+      lds_sync<WL>();
     }
     if (g + 1 < 4) fetch(g + 1);  // overlaps the bins and the inverse transform
     // ---- bins: pair (k, M-k) for k = 0..M/2 gives every bin 0..N/2
@@ -189,7 +197,7 @@ __device__ __forceinline__ void mss_size(const MssArgs& a, MssLds& L, int si, in
         L.red[wv][1] = lg;
       }
     }
-    lds_barrier();
+    lds_sync<WL>();
     if (j == 0 && live) {
       float sl = lin, sg = lg;
       if (P > 64) {
@@ -208,7 +216,7 @@ __device__ __forceinline__ void mss_size(const MssArgs& a, MssLds& L, int si, in
     // ---- real-output inverse transform and windowed overlap-add
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = spec[in_pos<M, pass_radix(LOGM, 0)>(j, e)];
-    fft<LOGM, true>(buf, j, v, op);
+    fft<LOGM, true, WL>(buf, j, v, op);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int n0 = 2 * op[e], n1 = n0 + 1;
@@ -217,6 +225,7 @@ __device__ __forceinline__ void mss_size(const MssArgs& a, MssLds& L, int si, in
       if (live && t0 >= 0 && t0 < a.T) L.acc[t0 - (a0 - kHalo)] += v[e].x * h0;
       if (live && t1 >= 0 && t1 < a.T) L.acc[t1 - (a0 - kHalo)] += v[e].y * h1;
     }
+    // every wave's overlap-add of group g lands before any of group g + 1
     lds_barrier();
   }
 }
