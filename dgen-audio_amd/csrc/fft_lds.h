@@ -175,4 +175,88 @@ __device__ __forceinline__ void fft(PadBuf buf, int j, c2* v, int* op) {
   }
 }
 
+// Two M-point transforms of the same direction in one pass sequence (a and
+// b in buffers bufa and bufb): each pass's twiddles, positions and LDS round
+// trip serve both, and the two butterflies give the scheduler independent
+// work.  Each signal's arithmetic is exactly that of fft().
+template <int M, int R, int NS, bool INV>
+__device__ __forceinline__ void pass_compute2(c2* va, c2* vb, int j, int* outpos) {
+  constexpr int BPT = 8 / R;
+#pragma unroll
+  for (int u = 0; u < BPT; ++u) {
+    const int bj = j + u * (M / 8);
+    const int k = bj % NS;
+    c2* wa = va + u * R;
+    c2* wb = vb + u * R;
+    if (NS > 1) {
+      const float rev = (INV ? 1.0f : -1.0f) * (float)k / (float)(NS * R);
+      const c2 t1 = cis(rev);
+      c2 t = t1;
+#pragma unroll
+      for (int r = 1; r < R; ++r) {
+        wa[r] = cmul(wa[r], t);
+        wb[r] = cmul(wb[r], t);
+        if (r + 1 < R) t = cmul(t, t1);
+      }
+    }
+    dftR<R, INV>(wa);
+    dftR<R, INV>(wb);
+    const int base = (bj / NS) * NS * R + k;
+#pragma unroll
+    for (int r = 0; r < R; ++r) outpos[u * R + r] = base + r * NS;
+  }
+}
+
+template <int LOGM, int P, bool INV, bool WAVE>
+__device__ __forceinline__ void mid_passes2(PadBuf bufa, PadBuf bufb, int j, c2* va, c2* vb) {
+  constexpr int M = 1 << LOGM;
+  if constexpr (P < pass_count(LOGM) - 1) {
+    constexpr int R = pass_radix(LOGM, P), NS = pass_span(LOGM, P);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      va[e] = bufa[in_pos<M, R>(j, e)];
+      vb[e] = bufb[in_pos<M, R>(j, e)];
+    }
+    lds_sync<WAVE>();
+    int op[8];
+    pass_compute2<M, R, NS, INV>(va, vb, j, op);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      bufa[op[e]] = va[e];
+      bufb[op[e]] = vb[e];
+    }
+    lds_sync<WAVE>();
+    mid_passes2<LOGM, P + 1, INV, WAVE>(bufa, bufb, j, va, vb);
+  }
+}
+
+// fft() of two signals at once: on return va / vb hold their last pass's
+// outputs at positions op[e].
+template <int LOGM, bool INV, bool WAVE = false>
+__device__ __forceinline__ void fft2(PadBuf bufa, PadBuf bufb, int j, c2* va, c2* vb, int* op) {
+  constexpr int M = 1 << LOGM;
+  constexpr int NP = pass_count(LOGM);
+  {
+    constexpr int R = pass_radix(LOGM, 0);
+    pass_compute2<M, R, 1, INV>(va, vb, j, op);
+  }
+  if constexpr (NP > 1) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      bufa[op[e]] = va[e];
+      bufb[op[e]] = vb[e];
+    }
+    lds_sync<WAVE>();
+    mid_passes2<LOGM, 1, INV, WAVE>(bufa, bufb, j, va, vb);
+    constexpr int RL = pass_radix(LOGM, NP - 1), NSL = pass_span(LOGM, NP - 1);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      va[e] = bufa[in_pos<M, RL>(j, e)];
+      vb[e] = bufb[in_pos<M, RL>(j, e)];
+    }
+    lds_sync<WAVE>();
+    pass_compute2<M, RL, NSL, INV>(va, vb, j, op);
+  }
+}
+
 }  // namespace dgen

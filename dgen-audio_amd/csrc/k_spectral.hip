@@ -84,7 +84,18 @@ __device__ __forceinline__ void mss_size(const MssArgs& a, MssLds& L, int si, in
   const int nwin = (a.T + H - 1) / H;
   const float* xs = a.x + (size_t)b * a.T;
   const float* ts = a.tgt + (size_t)b * a.T;
-  for (int i = tid; i < N; i += kThreads) L.hann[i] = a.hann[si][i];
+  {
+    // all of the thread's loads in flight before any LDS write (a loop that
+    // stored each load as it arrived waited out one memory latency per
+    // iteration)
+    constexpr int HP = (N + kThreads - 1) / kThreads;
+    float hv[HP];
+#pragma unroll
+    for (int q = 0; q < HP; ++q) hv[q] = a.hann[si][min(tid + q * kThreads, N - 1)];
+#pragma unroll
+    for (int q = 0; q < HP; ++q)
+      if (tid + q * kThreads < N) L.hann[tid + q * kThreads] = hv[q];
+  }
   lds_barrier();
   // window samples of group g for this thread: element e of the first pass
   // needs samples s0 + 2n and s0 + 2n + 1, n = in_pos(j, e)
@@ -113,20 +124,23 @@ __device__ __forceinline__ void mss_size(const MssArgs& a, MssLds& L, int si, in
     const int s0 = f - N + 1;  // first sample of the window
     c2 v[8];
     int op[8];
-    // ---- forward transform of the target, then of the prediction; the
-    //      target's half-size spectrum is kept in spec
-#pragma unroll
-    for (int pass = 0; pass < 2; ++pass) {
+    // ---- forward transforms of the target (in spec) and the prediction (in
+    //      buf), run together
+    {
+      c2 vt[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int n = in_pos<M, pass_radix(LOGM, 0)>(j, e);
         const float h0 = L.hann[2 * n], h1 = L.hann[2 * n + 1];
-        v[e] = pass == 0 ? c2{pt[2 * e] * h0, pt[2 * e + 1] * h1} : c2{px[2 * e] * h0, px[2 * e + 1] * h1};
+        vt[e] = c2{pt[2 * e] * h0, pt[2 * e + 1] * h1};
+        v[e] = c2{px[2 * e] * h0, px[2 * e + 1] * h1};
       }
-      fft<LOGM, false, WL>(buf, j, v, op);
-      const PadBuf dst = pass == 0 ? spec : buf;
+      fft2<LOGM, false, WL>(spec, buf, j, vt, v, op);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dst[op[e]] = v[e];
+      for (int e = 0; e < 8; ++e) {
+        spec[op[e]] = vt[e];
+        buf[op[e]] = v[e];
+      }
       lds_sync<WL>();
     }
     if (g + 1 < 4) fetch(g + 1);  // overlaps the bins and the inverse transform
@@ -239,7 +253,21 @@ __global__ __launch_bounds__(kThreads) void k_mss(MssArgs a, int si, int first) 
   MssLds& L = *reinterpret_cast<MssLds*>(smem);
   const int tile = blockIdx.x, b = blockIdx.y;
   float* part = a.part + ((size_t)b * a.ntiles + tile) * kAcc;
-  for (int i = threadIdx.x; i < kAcc; i += kThreads) L.acc[i] = first ? 0.f : part[i];
+  {
+    // the tile partials: every load in flight before the LDS writes
+    constexpr int AP = (kAcc + kThreads - 1) / kThreads;
+    float av[AP];
+    if (first) {
+#pragma unroll
+      for (int q = 0; q < AP; ++q) av[q] = 0.f;
+    } else {
+#pragma unroll
+      for (int q = 0; q < AP; ++q) av[q] = part[min((int)threadIdx.x + q * kThreads, kAcc - 1)];
+    }
+#pragma unroll
+    for (int q = 0; q < AP; ++q)
+      if ((int)threadIdx.x + q * kThreads < kAcc) L.acc[threadIdx.x + q * kThreads] = av[q];
+  }
   lds_barrier();
   mss_size<LOGN>(a, L, si, b, tile);
   for (int i = threadIdx.x; i < kAcc; i += kThreads) part[i] = L.acc[i];
