@@ -144,58 +144,80 @@ __device__ __forceinline__ void mss_size(const MssArgs& a, MssLds& L, int si, in
       lds_sync<WL>();
     }
     if (g + 1 < 4) fetch(g + 1);  // overlaps the bins and the inverse transform
-    // ---- bins: pair (k, M-k) for k = 0..M/2 gives every bin 0..N/2
+    // ---- bins: pair (k, M-k) for k = 0..M/2 gives every bin 0..N/2; each
+    //      thread owns the pairs k = j + i*P (i < NB)
     float lin = 0.f, lg = 0.f;
-#pragma unroll 1
-    for (int k = j; k <= M / 2; k += P) {
-      const int km = (M - k) & (M - 1);
-      const c2 zx = buf[k], zxm = buf[km], zt = spec[k], ztm = spec[km];
-      // even/odd split: E = (Z_k + conj Z_{M-k})/2, O = (Z_k - conj Z_{M-k})/(2i)
-      const c2 ex = {0.5f * (zx.x + zxm.x), 0.5f * (zx.y - zxm.y)};
-      const c2 ox = {0.5f * (zx.y + zxm.y), 0.5f * (zxm.x - zx.x)};
-      const c2 et = {0.5f * (zt.x + ztm.x), 0.5f * (zt.y - ztm.y)};
-      const c2 ot = {0.5f * (zt.y + ztm.y), 0.5f * (ztm.x - zt.x)};
-      const c2 wk = cis(-(float)k / (float)N);  // W_N^k
-      const c2 wox = cmul(wk, ox), wot = cmul(wk, ot);
-      // X_k = E + W^k O ; X_{M-k} = conj(E - W^k O)   (k = 0: X_0 and X_M)
-      c2 X[2] = {cadd(ex, wox), cconj(csub(ex, wox))};
-      c2 Tt[2] = {cadd(et, wot), cconj(csub(et, wot))};
-      if (k == 0) {  // X_M = E_0 - O_0 (real parts; imaginary parts vanish)
-        X[1] = {ex.x - ox.x, 0.f};
-        Tt[1] = {et.x - ot.x, 0.f};
-      }
-      const int nb = (k == M / 2) ? 1 : 2;  // k = M/2 is its own mirror
-      c2 G[2] = {{0.f, 0.f}, {0.f, 0.f}};
-#pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        if (q >= nb) break;
-        const float m1 = hw_sqrt(X[q].x * X[q].x + X[q].y * X[q].y);
-        const float m2 = hw_sqrt(Tt[q].x * Tt[q].x + Tt[q].y * Tt[q].y);
-        const float dlog = hw_log(m1 + kLogEps) - hw_log(m2 + kLogEps);
-        lin += fabsf(m1 - m2);
-        lg += fabsf(dlog);
-        const float dmag = a.gl * sgn(m1 - m2) + a.gg * sgn(dlog) * hw_rcp(m1 + kLogEps);
-        const float sc = dmag * hw_rcp(fmaxf(m1, kMagEps));
-        G[q] = {sc * X[q].x, sc * X[q].y};
-      }
-      // inverse pre-processing (Hermitian extension of the one-sided G):
-      //   E'_k = (G_k + conj G_{M-k})/2, O'_k = (G_k - conj G_{M-k})/2 * W_N^{-k},
-      //   z'_k = E'_k + i O'_k ; bin 0: E' = Re G_0 + Re G_M, O' = Re G_0 - Re G_M
-      if (k == 0) {
-        const float e0 = G[0].x + G[1].x, o0 = G[0].x - G[1].x;
-        spec[0] = {e0, o0};
-      } else {
-        const c2 gk = G[0], gm = nb == 2 ? G[1] : G[0];
-        const c2 winv = cconj(wk);
-        const c2 e1 = {0.5f * (gk.x + gm.x), 0.5f * (gk.y - gm.y)};
-        const c2 o1 = cmul(c2{0.5f * (gk.x - gm.x), 0.5f * (gk.y + gm.y)}, winv);
-        spec[k] = {e1.x - o1.y, e1.y + o1.x};
-        if (nb == 2) {
-          // index M-k: G_{M-k} = gm, mirror gk, twiddle W_N^{-(M-k)} = -W_N^{k}
-          const c2 e2 = {0.5f * (gm.x + gk.x), 0.5f * (gm.y - gk.y)};
-          const c2 o2 = cmul(c2{0.5f * (gm.x - gk.x), 0.5f * (gm.y + gk.y)}, c2{-wk.x, -wk.y});
-          spec[M - k] = {e2.x - o2.y, e2.y + o2.x};
+    auto bin_pair = [&](int k, c2 zx, c2 zxm, c2 zt, c2 ztm) {
+        // even/odd split: E = (Z_k + conj Z_{M-k})/2, O = (Z_k - conj Z_{M-k})/(2i)
+        const c2 ex = {0.5f * (zx.x + zxm.x), 0.5f * (zx.y - zxm.y)};
+        const c2 ox = {0.5f * (zx.y + zxm.y), 0.5f * (zxm.x - zx.x)};
+        const c2 et = {0.5f * (zt.x + ztm.x), 0.5f * (zt.y - ztm.y)};
+        const c2 ot = {0.5f * (zt.y + ztm.y), 0.5f * (ztm.x - zt.x)};
+        const c2 wk = cis(-(float)k / (float)N);  // W_N^k
+        const c2 wox = cmul(wk, ox), wot = cmul(wk, ot);
+        // X_k = E + W^k O ; X_{M-k} = conj(E - W^k O)   (k = 0: X_0 and X_M)
+        c2 X[2] = {cadd(ex, wox), cconj(csub(ex, wox))};
+        c2 Tt[2] = {cadd(et, wot), cconj(csub(et, wot))};
+        if (k == 0) {  // X_M = E_0 - O_0 (real parts; imaginary parts vanish)
+          X[1] = {ex.x - ox.x, 0.f};
+          Tt[1] = {et.x - ot.x, 0.f};
         }
+        const int nb = (k == M / 2) ? 1 : 2;  // k = M/2 is its own mirror
+        c2 G[2] = {{0.f, 0.f}, {0.f, 0.f}};
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          if (q >= nb) break;
+          const float m1 = hw_sqrt(X[q].x * X[q].x + X[q].y * X[q].y);
+          const float m2 = hw_sqrt(Tt[q].x * Tt[q].x + Tt[q].y * Tt[q].y);
+          const float dlog = hw_log(m1 + kLogEps) - hw_log(m2 + kLogEps);
+          lin += fabsf(m1 - m2);
+          lg += fabsf(dlog);
+          const float dmag = a.gl * sgn(m1 - m2) + a.gg * sgn(dlog) * hw_rcp(m1 + kLogEps);
+          const float sc = dmag * hw_rcp(fmaxf(m1, kMagEps));
+          G[q] = {sc * X[q].x, sc * X[q].y};
+        }
+        // inverse pre-processing (Hermitian extension of the one-sided G):
+        //   E'_k = (G_k + conj G_{M-k})/2, O'_k = (G_k - conj G_{M-k})/2 * W_N^{-k},
+        //   z'_k = E'_k + i O'_k ; bin 0: E' = Re G_0 + Re G_M, O' = Re G_0 - Re G_M
+        if (k == 0) {
+          const float e0 = G[0].x + G[1].x, o0 = G[0].x - G[1].x;
+          spec[0] = {e0, o0};
+        } else {
+          const c2 gk = G[0], gm = nb == 2 ? G[1] : G[0];
+          const c2 winv = cconj(wk);
+          const c2 e1 = {0.5f * (gk.x + gm.x), 0.5f * (gk.y - gm.y)};
+          const c2 o1 = cmul(c2{0.5f * (gk.x - gm.x), 0.5f * (gk.y + gm.y)}, winv);
+          spec[k] = {e1.x - o1.y, e1.y + o1.x};
+          if (nb == 2) {
+            // index M-k: G_{M-k} = gm, mirror gk, twiddle W_N^{-(M-k)} = -W_N^{k}
+            const c2 e2 = {0.5f * (gm.x + gk.x), 0.5f * (gm.y - gk.y)};
+            const c2 o2 = cmul(c2{0.5f * (gm.x - gk.x), 0.5f * (gm.y + gk.y)}, c2{-wk.x, -wk.y});
+            spec[M - k] = {e2.x - o2.y, e2.y + o2.x};
+          }
+        }
+    };
+    constexpr int NB = (M / 2) / P + 1;
+    if constexpr (WL) {
+      // every spectrum read issued before the first pair is processed (a
+      // one-pair loop waited out an LDS round trip per pair)
+      c2 zxa[NB], zxb[NB], zta[NB], ztb[NB];
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        const int k = min(j + i * P, M / 2), km = (M - k) & (M - 1);  // clamped: pairs past M/2 are skipped below
+        zxa[i] = buf[k];
+        zxb[i] = buf[km];
+        zta[i] = spec[k];
+        ztb[i] = spec[km];
+      }
+#pragma unroll
+      for (int i = 0; i < NB; ++i)
+        if (j + i * P <= M / 2) bin_pair(j + i * P, zxa[i], zxb[i], zta[i], ztb[i]);
+    } else {
+      // N = 2048: the hoisted reads would push the kernel past 256 registers
+#pragma unroll 1
+      for (int k = j; k <= M / 2; k += P) {
+        const int km = (M - k) & (M - 1);
+        bin_pair(k, buf[k], buf[km], spec[k], spec[km]);
       }
     }
     // ---- per-window loss sums over the window's P threads
