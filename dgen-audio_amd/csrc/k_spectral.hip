@@ -253,13 +253,31 @@ __device__ __forceinline__ void mss_size(const MssArgs& a, MssLds& L, int si, in
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = spec[in_pos<M, pass_radix(LOGM, 0)>(j, e)];
     fft<LOGM, true, WL>(buf, j, v, op);
+    // each accumulator element of a group belongs to one thread (the group's
+    // windows are disjoint), so all of the thread's reads are issued before
+    // its adds and writes; out-of-range samples read a clamped element and
+    // are not written
+    {
+      float ac[16];
+      int ai[16];
+      bool aw[16];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int n0 = 2 * op[e], n1 = n0 + 1;
-      const int t0 = s0 + n0, t1 = t0 + 1;
-      const float h0 = L.hann[n0], h1 = L.hann[n1];
-      if (live && t0 >= 0 && t0 < a.T) L.acc[t0 - (a0 - kHalo)] += v[e].x * h0;
-      if (live && t1 >= 0 && t1 < a.T) L.acc[t1 - (a0 - kHalo)] += v[e].y * h1;
+      for (int e = 0; e < 8; ++e) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int t = s0 + 2 * op[e] + h;
+          aw[2 * e + h] = live && t >= 0 && t < a.T;
+          ai[2 * e + h] = min(max(t - (a0 - kHalo), 0), kAcc - 1);
+          ac[2 * e + h] = L.acc[ai[2 * e + h]];
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int n0 = 2 * op[e];
+        const float h0 = L.hann[n0], h1 = L.hann[n0 + 1];
+        if (aw[2 * e]) L.acc[ai[2 * e]] = ac[2 * e] + v[e].x * h0;
+        if (aw[2 * e + 1]) L.acc[ai[2 * e + 1]] = ac[2 * e + 1] + v[e].y * h1;
+      }
     }
     // every wave's overlap-add of group g lands before any of group g + 1
     lds_barrier();
