@@ -106,7 +106,10 @@ def time_session(rt, program, args):
     wall = time.perf_counter() - t0
     log("bench: per-op profile")
     rows = table(program, rt.profileKernels())
-    dom = max(rows, key=lambda r: (round(r.roof_ms, 6), r.meas_ms))
+    # among ops of equal roofline time, prefer stream-0 ops: a side-stream
+    # op's event interval also covers the stream-0 work it overlaps
+    from dgen_hip.runtime import OP_SIDE
+    dom = max(rows, key=lambda r: (round(r.roof_ms, 6), not (program.ops[r.index].flags & OP_SIDE), r.meas_ms))
     dom.meas_ms = rt.time_op(dom.index, args.op_iters)
     for r in sorted(rows, key=lambda r: -r.meas_ms):
         log(f"  {r.label:18s} {r.bound:5s} meas {r.meas_ms * 1e3:9.1f} us  roof {r.roof_ms * 1e3:8.1f} us  "

@@ -8,8 +8,9 @@
 //   relies on host-coherent storage (MetalRuntime.swift:232); on discrete HBM
 //   the host mirror is pinned and moved only by explicit upload/download.
 // - Stream 0 carries the schedule; ops flagged SIDE run on a second stream
-//   (default priority) that first waits for the run's start event, and a JOIN
-//   op makes stream 0 wait for the side stream before it launches.
+//   (default priority) that first waits for the run's start event (or, for a
+//   SIDE|FORK op, for stream 0's work enqueued before it), and a JOIN op
+//   makes stream 0 wait for the side stream before it launches.
 // - run() is synchronous like MetalCompiledKernel.run (commit+wait,
 //   MetalRuntime.swift:334-337).
 #include <hip/hip_runtime.h>
@@ -83,7 +84,7 @@ struct dgen_hip_ctx {
   int device = 0;
   int cu_count = 256;
   hipStream_t s0 = nullptr, s1 = nullptr;
-  hipEvent_t ev_start = nullptr, ev_side = nullptr;
+  hipEvent_t ev_start = nullptr, ev_side = nullptr, ev_fork = nullptr;
   float* d_arena = nullptr;
   float* h_arena = nullptr;
   uint64_t floats = 0;
@@ -141,6 +142,13 @@ static int enqueue(dgen_hip_ctx* c, uint32_t frames, bool static_pass, std::vect
     if (op.flags & DGEN_HIP_OP_JOIN) {
       DGEN_HIP_TRY(hipEventRecord(c->ev_side, c->s1));
       DGEN_HIP_TRY(hipStreamWaitEvent(c->s0, c->ev_side, 0));
+    }
+    if ((op.flags & DGEN_HIP_OP_FORK) && (op.flags & DGEN_HIP_OP_SIDE)) {
+      // each wait is enqueued right after its record, so one event serves
+      // every fork point of the run (graph capture turns each pair into an
+      // edge from stream 0's last node)
+      DGEN_HIP_TRY(hipEventRecord(c->ev_fork, c->s0));
+      DGEN_HIP_TRY(hipStreamWaitEvent(c->s1, c->ev_fork, 0));
     }
     hipStream_t s = (op.flags & DGEN_HIP_OP_SIDE) ? c->s1 : c->s0;
     side_used |= (s == c->s1);
@@ -223,7 +231,8 @@ int dgen_hip_create(int device, dgen_hip_ctx** out) {
     if (hipStreamCreateWithFlags(&c->s0, hipStreamNonBlocking) != hipSuccess ||
         hipStreamCreateWithFlags(&c->s1, hipStreamNonBlocking) != hipSuccess ||
         hipEventCreateWithFlags(&c->ev_start, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&c->ev_side, hipEventDisableTiming) != hipSuccess)
+        hipEventCreateWithFlags(&c->ev_side, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming) != hipSuccess)
       rc = fail(DGEN_HIP_E_DEVICE, "create: stream/event creation failed");
   }
   if (rc) {
@@ -242,6 +251,7 @@ int dgen_hip_destroy(dgen_hip_ctx* c) {
   release_arena(c);
   if (c->ev_start) (void)hipEventDestroy(c->ev_start);
   if (c->ev_side) (void)hipEventDestroy(c->ev_side);
+  if (c->ev_fork) (void)hipEventDestroy(c->ev_fork);
   if (c->s0) (void)hipStreamDestroy(c->s0);
   if (c->s1) (void)hipStreamDestroy(c->s1);
   delete c;

@@ -56,9 +56,11 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     to render targets.  With ``train=True`` the schedule is forward, loss,
     backward to every parameter and (``optimizer``) one Adam step.  With
     ``side_stream`` the phase-carry chain (which depends only on f0) runs on a
-    second stream, overlapping the control-network forward."""
+    second stream, overlapping the control-network forward, and the weight
+    and bias gradients of the backward overlap its data-gradient chain."""
     SIDE = R.OP_SIDE if side_stream else 0
     JOIN = R.OP_JOIN if side_stream else 0
+    FORK = R.OP_FORK if side_stream else 0
     B, T, F, K, NF, NC, M = cfg.B, cfg.T, cfg.F, cfg.K, cfg.NF, cfg.NC, cfg.M
     Hd, din, Lyr = cfg.hidden, cfg.din, cfg.layers
     if NC > LDC:
@@ -206,14 +208,19 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     ws_gemm = p.alloc("splitk_ws", max(split * Hd * Hd, split_h * Hd * NC))
     chunks = min(256, max(1, M // 32))
     ws_col = p.alloc("colsum_ws", chunks * (din + 1) * max(Hd, NC))
+    # The weight and bias gradients of the heads and hidden layers run on the
+    # side stream, each forked after the data GEMM that produced its input, so
+    # they overlap the data-gradient chain (dX_heads -> dX_l3 -> dX_l2); they
+    # use their own column-sum workspace, and Adam joins them.
+    ws_col_side = p.alloc("colsum_ws_side", chunks * max(Hd, NC)) if side_stream else ws_col
     gW = [(G + (w - P), G + (b - P)) for (w, b) in woff]
     gWh, gbh = G + (Wh - P), G + (bh - P)
     # heads: dWh = H_L^T dZ ; dbh = colsum(dZ) ; dH_L = (dZ Wh^T) * (1 - H_L^2)
     p.add(R.K_GEMM, [Hs[-1], dZ, gWh, Hd, NC, M, Hd, LDC, NC, 1, 0, R.EPI_NONE, -1, -1, 0, split_h, ws_gemm, -1],
-          label="dW_heads", dispatch="gemmChunkPartials", bytes=(M * Hd + M * NC + Hd * NC) * f4,
+          flags=SIDE | FORK, label="dW_heads", dispatch="gemmChunkPartials", bytes=(M * Hd + M * NC + Hd * NC) * f4,
           flops=2.0 * M * Hd * NC, bound="mfma")
-    p.add(R.K_COLSUM, [dZ, gbh, M, NC, LDC, ws_col], label="db_heads", dispatch="chunkPartialsReduceToCell",
-          bytes=(M * NC + NC) * f4, flops=float(M * NC))
+    p.add(R.K_COLSUM, [dZ, gbh, M, NC, LDC, ws_col_side], flags=SIDE, label="db_heads",
+          dispatch="chunkPartialsReduceToCell", bytes=(M * NC + NC) * f4, flops=float(M * NC))
     dH = [p.alloc(f"dZ{l + 1}", M * Hd) for l in range(Lyr)]
     # column sums of dH[l] per 128-row GEMM tile, written by the data GEMM
     # that produces dH[l]; the bias gradient reduces these tile rows
@@ -226,8 +233,9 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
         W, _b = woff[l]
         gw, gb = gW[l]
         p.add(R.K_GEMM, [Hs[l - 1], dH[l], gw, Hd, Hd, M, Hd, Hd, Hd, 1, 0, R.EPI_NONE, -1, -1, 0, split, ws_gemm, -1],
-              label=f"dW_l{l + 1}", dispatch="gemmChunkPartials", bytes=(2 * M * Hd + Hd * Hd) * f4, **gemm_hh)
-        p.add(R.K_COLSUM, [dcol[l], gb, mt, Hd, Hd, ws_col], label=f"db_l{l + 1}",
+              flags=SIDE | FORK, label=f"dW_l{l + 1}", dispatch="gemmChunkPartials",
+              bytes=(2 * M * Hd + Hd * Hd) * f4, **gemm_hh)
+        p.add(R.K_COLSUM, [dcol[l], gb, mt, Hd, Hd, ws_col_side], flags=SIDE, label=f"db_l{l + 1}",
               dispatch="chunkPartialsReduceToCell", bytes=(mt * Hd + Hd) * f4, flops=float(mt * Hd))
         p.add(R.K_GEMM, [dH[l], W, dH[l - 1], M, Hd, Hd, Hd, Hd, Hd, 0, 1, R.EPI_TANH_GRAD, -1, Hs[l - 1], Hd, 1, 0,
                          dcol[l - 1]],
@@ -240,7 +248,7 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
         m = p.alloc("adam_m", npar)
         v = p.alloc("adam_v", npar)
         tcell = p.alloc("adam_t", 1)
-        p.add(R.K_ADAM, [P, G, m, v, npar, tcell], [cfg.lr, 0.9, 0.999, 1e-8], label="adam",
+        p.add(R.K_ADAM, [P, G, m, v, npar, tcell], [cfg.lr, 0.9, 0.999, 1e-8], flags=JOIN, label="adam",
               dispatch=f"staticThreads({npar})", bytes=7.0 * npar * f4, flops=12.0 * npar)
     p.output_cell = "y"
     return p

@@ -55,7 +55,7 @@ K_MEMBRANE_BWD = 28
 KERNEL_NAMES = {v: k[2:].lower() for k, v in globals().items() if k.startswith("K_")}
 
 EPI_NONE, EPI_BIAS, EPI_BIAS_TANH, EPI_TANH_GRAD = 0, 1, 2, 3
-OP_STATIC, OP_SIDE, OP_JOIN = 1, 2, 4
+OP_STATIC, OP_SIDE, OP_JOIN, OP_FORK = 1, 2, 4, 8
 
 EXPORTED_SYMBOLS = (
     "dgen_hip_abi_version", "dgen_hip_device_count", "dgen_hip_create", "dgen_hip_destroy",

@@ -260,6 +260,10 @@ enum dgen_hip_epilogue {
 #define DGEN_HIP_OP_STATIC 1u /* run once, at configure (static temporality) */
 #define DGEN_HIP_OP_SIDE 2u   /* launch on the side stream (overlaps stream 0) */
 #define DGEN_HIP_OP_JOIN 4u   /* stream 0 waits for the side stream first    */
+/* with SIDE: the side stream first waits for the stream-0 work enqueued
+ * before this op (a fork point); without it, side ops wait only for the
+ * start of the run */
+#define DGEN_HIP_OP_FORK 8u
 
 #define DGEN_HIP_OP_NARG 32
 #define DGEN_HIP_OP_NFARG 8
