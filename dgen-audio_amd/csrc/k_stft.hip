@@ -62,6 +62,30 @@ __device__ __forceinline__ void split_bins(PadBuf Z, int k, int M, float invN, c
   Xm = k == 0 ? c2{e.x - o.x, 0.0f} : cconj(csub(e, wo));
 }
 
+// split_bins on values already read: zk = Z[k], zm = Z[(M-k) mod M].
+__device__ __forceinline__ void split_pair(c2 zk, c2 zm, int k, float invN, c2& Xk, c2& Xm) {
+  const c2 e = {0.5f * (zk.x + zm.x), 0.5f * (zk.y - zm.y)};
+  const c2 o = {0.5f * (zk.y + zm.y), 0.5f * (zm.x - zk.x)};
+  const c2 wk = cis(-(float)k * invN);
+  const c2 wo = cmul(wk, o);
+  Xk = cadd(e, wo);
+  Xm = k == 0 ? c2{e.x - o.x, 0.0f} : cconj(csub(e, wo));
+}
+
+// dst[0..n) = src[0..n): every load of the thread in flight before its LDS
+// writes (a loop that stored each load as it arrived waited out one memory
+// latency per iteration).
+template <int n>
+__device__ __forceinline__ void stage(float* dst, const float* __restrict__ src, int tid) {
+  constexpr int Q = (n + kThreads - 1) / kThreads;
+  float v[Q];
+#pragma unroll
+  for (int q = 0; q < Q; ++q) v[q] = src[min(tid + q * kThreads, n - 1)];
+#pragma unroll
+  for (int q = 0; q < Q; ++q)
+    if (tid + q * kThreads < n) dst[tid + q * kThreads] = v[q];
+}
+
 __device__ __forceinline__ float block_sum(float v, float* red) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
@@ -85,14 +109,18 @@ struct FwdLds {
 template <int LOGN>
 __global__ __launch_bounds__(kThreads) void k_stft_fwd(StftArgs a) {
   constexpr int N = 1 << LOGN, M = N / 2, LOGM = LOGN - 1, P = M / 8, W = kThreads / P;
+  constexpr int U = M / 2 / P + 1;  // bin pairs per thread
+  // a window's P threads lie in one wave when P <= 64: its transforms and
+  // bins need only wave-level ordering; the gather reads every slot
+  constexpr bool WL = P <= 64;
   static_assert(W * M == 2048, "window slots must fill the FFT buffer");
   __shared__ FwdLds L;
   const int tid = threadIdx.x, slot = tid / P, j = tid % P;
   const int s = blockIdx.y, tile = blockIdx.x, H = a.H;
   const int a0 = tile * kTile, a1 = min(a.T, a0 + kTile);
   const float* xs = a.x + (size_t)s * a.T;
-  for (int i = tid; i < N; i += kThreads) L.win[i] = a.win[i];
-  for (int i = tid; i <= M; i += kThreads) L.gain[i] = a.gains[i];
+  stage<N>(L.win, a.win, tid);
+  stage<M + 1>(L.gain, a.gains, tid);
   for (int i = tid; i < kTile; i += kThreads) L.acc[i] = 0.0f;
   // windows h = w*H with outputs [h, h+N) meeting [a0, a1)
   const int w_lo = a0 - N < 0 ? 0 : (a0 - N) / H + 1;
@@ -119,16 +147,27 @@ __global__ __launch_bounds__(kThreads) void k_stft_fwd(StftArgs a) {
       const float x1 = live && t0 + 1 >= 0 ? xs[t0 + 1] : 0.0f;
       v[e] = c2{x0 * L.win[2 * n], x1 * L.win[2 * n + 1]};
     }
-    fft<LOGM, false>(buf, j, v, op);
+    fft<LOGM, false, WL>(buf, j, v, op);
 #pragma unroll
     for (int e = 0; e < 8; ++e) buf[op[e]] = v[e];
-    lds_barrier();
+    lds_sync<WL>();
     // gains on the one-sided spectrum, then the Hermitian inverse
     // pre-processing: z'_k = (G_k + conj G_{M-k}) + i (G_k - conj G_{M-k}) W_N^{-k}
-    // (each thread owns the pair k, M-k, so the update is in place)
-    for (int k = j; k <= M / 2; k += P) {
+    // (each thread owns the pairs k, M-k with k = j + u*P, so the update is
+    // in place; all of a thread's spectrum reads are issued first)
+    c2 zk[U], zm[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = min(j + u * P, M / 2);  // clamped: pairs past M/2 are skipped below
+      zk[u] = buf[k];
+      zm[u] = buf[(M - k) & (M - 1)];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = j + u * P;
+      if (k > M / 2) continue;
       c2 Xk, Xm;
-      split_bins(buf, k, M, invN, Xk, Xm);
+      split_pair(zk[u], zm[u], k, invN, Xk, Xm);
       const float gk = L.gain[k], gm = L.gain[M - k];
       Xk = c2{Xk.x * gk, Xk.y * gk};
       Xm = c2{Xm.x * gm, Xm.y * gm};
@@ -144,11 +183,11 @@ __global__ __launch_bounds__(kThreads) void k_stft_fwd(StftArgs a) {
         }
       }
     }
-    lds_barrier();
+    lds_sync<WL>();
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = buf[in_pos<M, pass_radix(LOGM, 0)>(j, e)];
-    lds_barrier();
-    fft<LOGM, true>(buf, j, v, op);
+    lds_sync<WL>();
+    fft<LOGM, true, WL>(buf, j, v, op);
     // complex output q holds samples 2q, 2q+1 (unnormalised): scale by 1/N
     float* zb = reinterpret_cast<float*>(buf.p);
 #pragma unroll
@@ -174,13 +213,22 @@ __global__ __launch_bounds__(kThreads) void k_stft_fwd(StftArgs a) {
     lds_barrier();
   }
   float ls = 0.0f;
-  for (int t = a0 + tid; t < a1; t += kThreads) {
-    const float yv = L.acc[t - a0];
-    const float d = yv - xs[t];
-    const size_t i = (size_t)s * a.T + t;
-    if (a.y) a.y[i] = yv;
-    if (a.dy) a.dy[i] = 2.0f * d * a.invT;
-    ls += d * d;
+  // the tile's input samples are loaded 8 at a time, all in flight before use
+  for (int t8 = a0 + tid; t8 < a1; t8 += 8 * kThreads) {
+    float xv[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) xv[q] = xs[min(t8 + q * kThreads, a1 - 1)];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int t = t8 + q * kThreads;
+      if (t >= a1) break;
+      const float yv = L.acc[t - a0];
+      const float d = yv - xv[q];
+      const size_t i = (size_t)s * a.T + t;
+      if (a.y) a.y[i] = yv;
+      if (a.dy) a.dy[i] = 2.0f * d * a.invT;
+      ls += d * d;
+    }
   }
   if (a.lossp) {
     const float tot = block_sum(ls, L.red);
@@ -198,6 +246,7 @@ template <int LOGN>
 __global__ __launch_bounds__(kThreads) void k_stft_bwd(StftArgs a) {
   constexpr int N = 1 << LOGN, M = N / 2, LOGM = LOGN - 1, P = M / 8, W = kThreads / P;
   constexpr int U = M / 2 / P + 1;  // bin pairs per thread
+  constexpr bool WL = P <= 64;       // a window's threads lie in one wave
   static_assert(W * M == 2048, "window slots must fill the FFT buffer");
   __shared__ BwdLds L;
   const int tid = threadIdx.x, slot = tid / P, j = tid % P;
@@ -206,7 +255,7 @@ __global__ __launch_bounds__(kThreads) void k_stft_bwd(StftArgs a) {
   const int wb = blk * kRounds * W, we = min(nwin, wb + kRounds * W);
   const float* xs = a.x + (size_t)s * a.T;
   const float* gs = a.dyin + (size_t)s * a.T;
-  for (int i = tid; i < N; i += kThreads) L.win[i] = a.win[i];
+  stage<N>(L.win, a.win, tid);
   const PadBuf buf{L.buf + slot * lds_pad(M)};
   const PadBuf spec{L.aux + slot * lds_pad(M)};
   constexpr float invN = 1.0f / (float)N;
@@ -218,28 +267,28 @@ __global__ __launch_bounds__(kThreads) void k_stft_bwd(StftArgs a) {
     const int w = wb + r0 + slot;
     const bool live = w < we;
     const int h = w * H;
-#pragma unroll
-    for (int pass = 0; pass < 2; ++pass) {
-      c2 v[8];
+    {
+      // the analysis window x[h-N+1 .. h] * hann (-> spec) and dL/dy over
+      // the window's outputs [h, h+N) (-> buf), transformed together
+      c2 vx[8], vg[8];
       int op[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int n = in_pos<M, pass_radix(LOGM, 0)>(j, e);
-        if (pass == 0) {  // the analysis window x[h-N+1 .. h] * hann
-          const int t0 = h - N + 1 + 2 * n;
-          const float x0 = live && t0 >= 0 ? xs[t0] : 0.0f;
-          const float x1 = live && t0 + 1 >= 0 ? xs[t0 + 1] : 0.0f;
-          v[e] = c2{x0 * L.win[2 * n], x1 * L.win[2 * n + 1]};
-        } else {  // dL/dy over the window's outputs [h, h+N)
-          const int t0 = h + 2 * n;
-          v[e] = c2{live && t0 < a.T ? gs[t0] : 0.0f, live && t0 + 1 < a.T ? gs[t0 + 1] : 0.0f};
-        }
+        const int t0 = h - N + 1 + 2 * n;
+        const float x0 = live && t0 >= 0 ? xs[t0] : 0.0f;
+        const float x1 = live && t0 + 1 >= 0 ? xs[t0 + 1] : 0.0f;
+        vx[e] = c2{x0 * L.win[2 * n], x1 * L.win[2 * n + 1]};
+        const int g0 = h + 2 * n;
+        vg[e] = c2{live && g0 < a.T ? gs[g0] : 0.0f, live && g0 + 1 < a.T ? gs[g0 + 1] : 0.0f};
       }
-      fft<LOGM, false>(buf, j, v, op);
-      const PadBuf dst = pass == 0 ? spec : buf;
+      fft2<LOGM, false, WL>(spec, buf, j, vx, vg, op);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dst[op[e]] = v[e];
-      lds_barrier();
+      for (int e = 0; e < 8; ++e) {
+        spec[op[e]] = vx[e];
+        buf[op[e]] = vg[e];
+      }
+      lds_sync<WL>();
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -251,8 +300,11 @@ __global__ __launch_bounds__(kThreads) void k_stft_bwd(StftArgs a) {
       acc_k[u] += Xk.x * Ek.x + Xk.y * Ek.y;
       acc_m[u] += Xm.x * Em.x + Xm.y * Em.y;
     }
-    lds_barrier();
+    // the next round overwrites this slot's buffers
+    lds_sync<WL>();
   }
+  // every slot's reads are done before the partial rows reuse the buffers
+  lds_barrier();
   // slots' partial sums -> one row: bins k (acc_k) and M-k (acc_m; bin M for k = 0)
   float* part = reinterpret_cast<float*>(L.buf);  // [W][M + 1]
 #pragma unroll
