@@ -132,22 +132,34 @@ __global__ __launch_bounds__(kThreads) void k_stft_fwd(StftArgs a) {
   const float* zs = reinterpret_cast<const float*>(L.buf);
   constexpr int kZStride = 2 * lds_pad(M);
   constexpr float invN = 1.0f / (float)N;
-  __syncthreads();
-  for (int r0 = 0; r0 < nw; r0 += W) {
+  // this thread's window samples of round r (element e of the first pass
+  // needs samples 2n and 2n+1 of the window, n = in_pos(j, e)); the next
+  // round's are loaded while this one is transformed and gathered
+  float px[16];
+  auto fetch = [&](int r0) {
     const int w = w_lo + r0 + slot;
     const bool live = w <= w_hi;
     const int h = w * H;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int n = in_pos<M, pass_radix(LOGM, 0)>(j, e);
+      const int t0 = h - N + 1 + 2 * n;
+      px[2 * e] = live && t0 >= 0 ? xs[t0] : 0.0f;
+      px[2 * e + 1] = live && t0 + 1 >= 0 ? xs[t0 + 1] : 0.0f;
+    }
+  };
+  __syncthreads();
+  fetch(0);
+  for (int r0 = 0; r0 < nw; r0 += W) {
     c2 v[8];
     int op[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int n = in_pos<M, pass_radix(LOGM, 0)>(j, e);
-      const int t0 = h - N + 1 + 2 * n;
-      const float x0 = live && t0 >= 0 ? xs[t0] : 0.0f;
-      const float x1 = live && t0 + 1 >= 0 ? xs[t0 + 1] : 0.0f;
-      v[e] = c2{x0 * L.win[2 * n], x1 * L.win[2 * n + 1]};
+      v[e] = c2{px[2 * e] * L.win[2 * n], px[2 * e + 1] * L.win[2 * n + 1]};
     }
     fft<LOGM, false, WL>(buf, j, v, op);
+    if (r0 + W < nw) fetch(r0 + W);
 #pragma unroll
     for (int e = 0; e < 8; ++e) buf[op[e]] = v[e];
     lds_sync<WL>();
@@ -200,15 +212,49 @@ __global__ __launch_bounds__(kThreads) void k_stft_fwd(StftArgs a) {
     const int wb = w_lo + r0, hb = wb * H;
     const int nq = min(W, w_hi - wb + 1);
     const int span = (nq - 1) * H + N;
-    for (int p = tid; p < span; p += kThreads) {
-      const int t = hb + p;
-      if (t < a0 || t >= a1) continue;
-      float sum = 0.0f;
-      for (int q = 0; q < nq; ++q) {
-        const int i = p - q * H;
-        if (i >= 0 && i < N) sum += zs[q * kZStride + i];
+    if constexpr (W <= 4) {
+      // span <= W*N = 4096 (H <= N): 16 positions per thread, gathered 4
+      // at a time with every slot read and accumulator read of a batch
+      // issued before its first sum (a position loop waited out LDS latency
+      // at every position); a slot that does not cover a position adds +0
+      // (exact)
+      constexpr int kPos = W * N / kThreads, kBatch = 4;
+#pragma unroll
+      for (int i0 = 0; i0 < kPos; i0 += kBatch) {
+        float z[kBatch][W], ac[kBatch];
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+          const int p = tid + (i0 + b) * kThreads;
+#pragma unroll
+          for (int q = 0; q < W; ++q) {
+            const int ii = p - q * H;
+            const bool ok = q < nq && ii >= 0 && ii < N;
+            z[b][q] = zs[q * kZStride + (ok ? ii : 0)];
+            z[b][q] = ok ? z[b][q] : 0.0f;
+          }
+          ac[b] = L.acc[min(max(hb + p - a0, 0), kTile - 1)];
+        }
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+          const int p = tid + (i0 + b) * kThreads, t = hb + p;
+          float sum = 0.0f;
+#pragma unroll
+          for (int q = 0; q < W; ++q) sum += z[b][q];
+          if (p < span && t >= a0 && t < a1) L.acc[t - a0] = ac[b] + sum;
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
-      L.acc[t - a0] += sum;
+    } else {
+      for (int p = tid; p < span; p += kThreads) {
+        const int t = hb + p;
+        if (t < a0 || t >= a1) continue;
+        float sum = 0.0f;
+        for (int q = 0; q < nq; ++q) {
+          const int i = p - q * H;
+          if (i >= 0 && i < N) sum += zs[q * kZStride + i];
+        }
+        L.acc[t - a0] += sum;
+      }
     }
     lds_barrier();
   }
