@@ -229,7 +229,12 @@ __device__ __forceinline__ float softplus_grad(float x) {
   return (x >= 0.f ? 1.f : 0.f) - sg * (e / (1.f + e));
 }
 
-// One wave per row; Z and ctrl rows have stride ldz / ldc.
+// One wave per row; Z and ctrl rows have stride ldz / ldc.  Lane l owns
+// elements l and l + 64 of each head group (K, NF <= 128), and every
+// softplus / tanh of a row is evaluated once, in registers (the sums add
+// the same terms in the same order as a per-group loop).
+constexpr int kHeadPer = 2;
+
 __global__ void k_heads_fwd(const float* __restrict__ Z, int ldz, float* __restrict__ C, int ldc, int rows, int K,
                             int NF) {
   const int m = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
@@ -237,18 +242,37 @@ __global__ void k_heads_fwd(const float* __restrict__ Z, int ldz, float* __restr
   if (m >= rows) return;
   const float* z = Z + (size_t)m * ldz;
   float* c = C + (size_t)m * ldc;
+  float sp[kHeadPer], th[kHeadPer];
   float den = 0.f;
-  for (int k = lane; k < K; k += kWave) den += softplus(z[k]);
+#pragma unroll
+  for (int q = 0; q < kHeadPer; ++q) {
+    const int k = lane + q * kWave;
+    sp[q] = k < K ? softplus(z[k]) : 0.f;
+    if (k < K) den += sp[q];
+  }
   den = wave_sum(den) + 1e-6f;
-  for (int k = lane; k < K; k += kWave) c[k] = softplus(z[k]) / den;
+#pragma unroll
+  for (int q = 0; q < kHeadPer; ++q) {
+    const int k = lane + q * kWave;
+    if (k < K) c[k] = sp[q] / den;
+  }
   if (lane == 0) {
     c[K] = softplus(z[K]);
     c[K + 1] = softplus(z[K + 1]);
   }
   float nrm = 0.f;
-  for (int i = lane; i < NF; i += kWave) nrm += fabsf(tanhf(z[K + 2 + i]));
+#pragma unroll
+  for (int q = 0; q < kHeadPer; ++q) {
+    const int i = lane + q * kWave;
+    th[q] = i < NF ? tanhf(z[K + 2 + i]) : 0.f;
+    if (i < NF) nrm += fabsf(th[q]);
+  }
   nrm = wave_sum(nrm) + 1e-4f;
-  for (int i = lane; i < NF; i += kWave) c[K + 2 + i] = tanhf(z[K + 2 + i]) / nrm;
+#pragma unroll
+  for (int q = 0; q < kHeadPer; ++q) {
+    const int i = lane + q * kWave;
+    if (i < NF) c[K + 2 + i] = th[q] / nrm;
+  }
 }
 
 __global__ void k_heads_bwd(const float* __restrict__ Z, int ldz, const float* __restrict__ dC, int ldc,
@@ -259,26 +283,54 @@ __global__ void k_heads_bwd(const float* __restrict__ Z, int ldz, const float* _
   const float* z = Z + (size_t)m * ldz;
   const float* dc = dC + (size_t)m * ldc;
   float* dz = dZ + (size_t)m * lddz;
+  float zk[kHeadPer], sp[kHeadPer], dk[kHeadPer];
   float den = 0.f;
-  for (int k = lane; k < K; k += kWave) den += softplus(z[k]);
+#pragma unroll
+  for (int q = 0; q < kHeadPer; ++q) {
+    const int k = lane + q * kWave;
+    zk[q] = k < K ? z[k] : 0.f;
+    dk[q] = k < K ? dc[k] : 0.f;
+    sp[q] = softplus(zk[q]);
+    if (k < K) den += sp[q];
+  }
   den = wave_sum(den) + 1e-6f;
   float dot = 0.f;
-  for (int k = lane; k < K; k += kWave) dot += dc[k] * (softplus(z[k]) / den);
+#pragma unroll
+  for (int q = 0; q < kHeadPer; ++q)
+    if (lane + q * kWave < K) dot += dk[q] * (sp[q] / den);
   dot = wave_sum(dot);
-  for (int k = lane; k < K; k += kWave) dz[k] = (dc[k] - dot) / den * softplus_grad(z[k]);
+#pragma unroll
+  for (int q = 0; q < kHeadPer; ++q) {
+    const int k = lane + q * kWave;
+    if (k < K) dz[k] = (dk[q] - dot) / den * softplus_grad(zk[q]);
+  }
   if (lane == 0) {
     dz[K] = dc[K] * softplus_grad(z[K]);
     dz[K + 1] = dc[K + 1] * softplus_grad(z[K + 1]);
   }
-  float nrm = 0.f, dot2 = 0.f;
-  for (int i = lane; i < NF; i += kWave) nrm += fabsf(tanhf(z[K + 2 + i]));
+  float th[kHeadPer], dt[kHeadPer];
+  float nrm = 0.f;
+#pragma unroll
+  for (int q = 0; q < kHeadPer; ++q) {
+    const int i = lane + q * kWave;
+    th[q] = i < NF ? tanhf(z[K + 2 + i]) : 0.f;
+    dt[q] = i < NF ? dc[K + 2 + i] : 0.f;
+    if (i < NF) nrm += fabsf(th[q]);
+  }
   nrm = wave_sum(nrm) + 1e-4f;
-  for (int i = lane; i < NF; i += kWave) dot2 += dc[K + 2 + i] * (tanhf(z[K + 2 + i]) / nrm);
+  float dot2 = 0.f;
+#pragma unroll
+  for (int q = 0; q < kHeadPer; ++q)
+    if (lane + q * kWave < NF) dot2 += dt[q] * (th[q] / nrm);
   dot2 = wave_sum(dot2);
-  for (int i = lane; i < NF; i += kWave) {
-    float s = tanhf(z[K + 2 + i]);
-    float sg = s > 0.f ? 1.f : (s < 0.f ? -1.f : 0.f);
-    dz[K + 2 + i] = (dc[K + 2 + i] - sg * dot2) / nrm * (1.f - s * s);
+#pragma unroll
+  for (int q = 0; q < kHeadPer; ++q) {
+    const int i = lane + q * kWave;
+    if (i < NF) {
+      const float s = th[q];
+      const float sg = s > 0.f ? 1.f : (s < 0.f ? -1.f : 0.f);
+      dz[K + 2 + i] = (dt[q] - sg * dot2) / nrm * (1.f - s * s);
+    }
   }
   // padding columns of the stored dZ row stay exactly zero
   for (int c = K + 2 + NF + lane; c < lddz; c += kWave) dz[c] = 0.f;
@@ -287,7 +339,8 @@ __global__ void k_heads_bwd(const float* __restrict__ Z, int ldz, const float* _
 int launch_heads_fwd(const Launch& L, const dgen_hip_op& op) {
   const int64_t Z = op.arg[0], C = op.arg[1], rows = op.arg[2], K = op.arg[3], NF = op.arg[4];
   const int64_t ld = op.arg[5];
-  DGEN_REQUIRE(rows > 0 && K > 0 && NF > 0 && ld >= K + 2 + NF, "heads_fwd: rows %lld K %lld NF %lld ld %lld",
+  DGEN_REQUIRE(rows > 0 && K > 0 && NF > 0 && K <= kHeadPer * kWave && NF <= kHeadPer * kWave && ld >= K + 2 + NF,
+               "heads_fwd: rows %lld K %lld NF %lld ld %lld",
                (long long)rows, (long long)K, (long long)NF, (long long)ld);
   DGEN_CHECK_CELL(L, Z, rows * ld, "heads_fwd.Z");
   DGEN_CHECK_CELL(L, C, rows * ld, "heads_fwd.ctrl");
@@ -301,7 +354,8 @@ int launch_heads_fwd(const Launch& L, const dgen_hip_op& op) {
 int launch_heads_bwd(const Launch& L, const dgen_hip_op& op) {
   const int64_t Z = op.arg[0], dC = op.arg[1], dZ = op.arg[2], rows = op.arg[3], K = op.arg[4], NF = op.arg[5];
   const int64_t ld = op.arg[6];
-  DGEN_REQUIRE(rows > 0 && K > 0 && NF > 0 && ld >= K + 2 + NF, "heads_bwd: rows %lld K %lld NF %lld ld %lld",
+  DGEN_REQUIRE(rows > 0 && K > 0 && NF > 0 && K <= kHeadPer * kWave && NF <= kHeadPer * kWave && ld >= K + 2 + NF,
+               "heads_bwd: rows %lld K %lld NF %lld ld %lld",
                (long long)rows, (long long)K, (long long)NF, (long long)ld);
   DGEN_CHECK_CELL(L, Z, rows * ld, "heads_bwd.Z");
   DGEN_CHECK_CELL(L, dC, rows * ld, "heads_bwd.dctrl");

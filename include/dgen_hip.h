@@ -73,7 +73,8 @@ enum dgen_hip_kernel {
 
   /* Head activations of HarmonicDecoderModel (Model.swift:100-114):
    * amps = softplus/sum, gain/noise gain = softplus, taps = tanh/sum|.|.
-   * arg: [0]=Z [1]=ctrl [2]=rows [3]=K [4]=NF */
+   * arg: [0]=Z [1]=ctrl [2]=rows [3]=K (<= 128) [4]=NF (<= 128)
+   *      [5]=row stride of Z and ctrl (>= K + 2 + NF) */
   DGEN_HIP_K_HEADS_FWD = 4,
 
   /* Sequential tensor-phasor carry pass (Emit+State.swift:322-369) for
@@ -124,7 +125,8 @@ enum dgen_hip_kernel {
   DGEN_HIP_K_SYNTH_BWD_REDUCE = 10,
 
   /* Head backward: dZ from d ctrl and Z.  arg: [0]=Z [1]=dctrl [2]=dZ
-   * [3]=rows [4]=K [5]=NF */
+   * [3]=rows [4]=K (<= 128) [5]=NF (<= 128) [6]=row stride (>= K + 2 + NF;
+   * dZ's padding columns are written as zero) */
   DGEN_HIP_K_HEADS_BWD = 11,
 
   /* Column sums (bias gradients): out[n] = sum_m A[m][n], deterministic
