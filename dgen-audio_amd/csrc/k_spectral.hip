@@ -381,12 +381,14 @@ __global__ void k_mss_combine(CombineArgs g, const float* __restrict__ part, flo
   const int t = blockIdx.x * blockDim.x + threadIdx.x;
   const int b = blockIdx.y;
   if (t >= T) return;
-  const int tile = t / kTile, a0 = tile * kTile;
-  const float* p = part + ((size_t)b * ntiles + tile) * kAcc;
-  float v = p[t - a0 + kHalo];
-  const int a1 = a0 + kTile;
-  if (tile + 1 < ntiles && t >= a1 - kHalo) v += p[kAcc + (t - a1 + kHalo)];
-  dx[(size_t)b * T + t] = v;
+  if (dx) {
+    const int tile = t / kTile, a0 = tile * kTile;
+    const float* p = part + ((size_t)b * ntiles + tile) * kAcc;
+    float v = p[t - a0 + kHalo];
+    const int a1 = a0 + kTile;
+    if (tile + 1 < ntiles && t >= a1 - kHalo) v += p[kAcc + (t - a1 + kHalo)];
+    dx[(size_t)b * T + t] = v;
+  }
   if (b == 0 && lossf) {
     float lf = 0.f;
     for (int s = 0; s < g.nsizes; ++s) {
@@ -394,6 +396,8 @@ __global__ void k_mss_combine(CombineArgs g, const float* __restrict__ part, flo
       if (t % hop) continue;
       const int w = t / hop;
       float lin = 0.f, lg = 0.f;
+      // loads of 8 lanes in flight at a time; the adds keep lane order
+#pragma unroll 8
       for (int bb = 0; bb < B; ++bb) {
         lin = lin + g.wloss[s][((size_t)w * B + bb) * 2 + 0];
         lg = lg + g.wloss[s][((size_t)w * B + bb) * 2 + 1];
@@ -407,15 +411,16 @@ __global__ void k_mss_combine(CombineArgs g, const float* __restrict__ part, flo
 }
 
 int launch_spectral_gather(const Launch& L, const dgen_hip_op& op) {
-  // arg: [0]=dx ([B][T]) [1]=loss frames ([T]) or -1 [2]=B [3]=T [4]=n_sizes [5..12]=N_s
+  // arg: [0]=dx ([B][T]) or -1 [1]=loss frames ([T]) or -1 [2]=B [3]=T [4]=n_sizes [5..12]=N_s
   //      [13]=tile partials [21..28]=per-window loss cells
   // farg: [0]=lin weight per size [1]=log weight per size [2]=maxFrameCount
   const int64_t dx = op.arg[0], lossf = op.arg[1], B = op.arg[2], T = op.arg[3], ns = op.arg[4];
+  DGEN_REQUIRE(dx >= 0 || lossf >= 0, "spectral_gather: neither dx nor loss frames requested");
   const int64_t part = op.arg[13];
   DGEN_REQUIRE(B > 0 && B <= 65535 && T > 0 && T <= (1 << 26) && ns >= 1 && ns <= kMaxSizes,
                "spectral_gather: B %lld T %lld sizes %lld", (long long)B, (long long)T, (long long)ns);
   const int64_t ntiles = (T + kTile - 1) / kTile;
-  DGEN_CHECK_CELL(L, dx, B * T, "spectral_gather.dx");
+  if (dx >= 0) DGEN_CHECK_CELL(L, dx, B * T, "spectral_gather.dx");
   if (lossf >= 0) DGEN_CHECK_CELL(L, lossf, T, "spectral_gather.loss_frames");
   DGEN_CHECK_CELL(L, part, B * ntiles * kAcc, "spectral_gather.tile_partials");
   CombineArgs g{};
@@ -432,9 +437,10 @@ int launch_spectral_gather(const Launch& L, const dgen_hip_op& op) {
     }
   }
   if (L.dry) return 0;
-  hipLaunchKernelGGL(k_mss_combine, dim3((unsigned)((T + 255) / 256), (unsigned)B), dim3(256), 0, L.stream, g,
-                     cell(L, part), cell(L, dx), lossf >= 0 ? cell(L, lossf) : nullptr, (int)B, (int)T, (int)ntiles,
-                     op.farg[0], op.farg[1], op.farg[2]);
+  // without dx only the lane-0 row of blocks (the loss signal) is launched
+  hipLaunchKernelGGL(k_mss_combine, dim3((unsigned)((T + 255) / 256), (unsigned)(dx >= 0 ? B : 1)), dim3(256), 0,
+                     L.stream, g, cell(L, part), dx >= 0 ? cell(L, dx) : nullptr, lossf >= 0 ? cell(L, lossf) : nullptr,
+                     (int)B, (int)T, (int)ntiles, op.farg[0], op.farg[1], op.farg[2]);
   DGEN_LAUNCH_CHECK("k_mss_combine");
   return 0;
 }

@@ -182,9 +182,17 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
           dispatch=f"perFrameScaledThreadgroup1({B}) x {len(sizes)} sizes",
           bytes=(2 * B * T + B * ntiles * (MSS_TILE + 2047) + sum((T + N // 4 - 1) // (N // 4) for N in sizes) * B * 2)
           * f4, flops=mss_flops, bound="valu")
-    garg = [dy, lossf, B, T, len(sizes)] + (sizes + [0] * 8)[:8] + [mss_part] + [0] * 7 + (wloss_cells + [0] * 8)[:8]
+    garg = [dy, -1, B, T, len(sizes)] + (sizes + [0] * 8)[:8] + [mss_part] + [0] * 7 + (wloss_cells + [0] * 8)[:8]
     p.add(R.K_SPECTRAL_GATHER, garg, [wl, wg, maxf], label="spectral_combine", dispatch=f"perFrameScaled({B})",
-          bytes=(B * ntiles * (MSS_TILE + 2047) + B * T + T) * f4, flops=float(B * T))
+          bytes=(B * ntiles * (MSS_TILE + 2047) + B * T) * f4, flops=float(B * T))
+    # the per-frame loss signal in a launch of its own (one row of blocks):
+    # folded into the combine, its blocks were the combine's tail (measured
+    # 25 -> 9 us + a separate 9 us); on the side stream the step measured
+    # 75 us slower
+    larg2 = [-1, lossf] + garg[2:]
+    nwin_all = sum((T + N // 4 - 1) // (N // 4) for N in sizes)
+    p.add(R.K_SPECTRAL_GATHER, larg2, [wl, wg, maxf], label="loss_frames",
+          dispatch="perFrame", bytes=(nwin_all * B * 2 + T) * f4, flops=float(nwin_all * B * 2))
 
     part = p.alloc("synth_partials", B * nseg * SLOTS * LDC)
     dctrl = p.alloc("dctrl", M * LDC)

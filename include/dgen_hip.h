@@ -110,7 +110,8 @@ enum dgen_hip_kernel {
 
   /* dx from the spectral-loss tile partials (owning tile + next tile's
    * halo) and the per-frame loss signal (batch mean, / maxFrameCount).
-   * arg: [0]=dx ([B][T]) [1]=loss frames ([T]) or -1 [2]=B [3]=T
+   * arg: [0]=dx ([B][T]) or -1 [1]=loss frames ([T]) or -1 (not both -1)
+   *      [2]=B [3]=T
    *      [4]=n_sizes [5..12]=N_s [13]=tile partials [21..28]=window-loss cells
    * farg: [0]=lin weight per size [1]=log weight per size [2]=maxFrameCount */
   DGEN_HIP_K_SPECTRAL_GATHER = 8,
