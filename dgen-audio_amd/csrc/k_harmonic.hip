@@ -739,13 +739,25 @@ __global__ void k_synth_bwd_reduce(const float* __restrict__ part, const float* 
   if (c >= ldc) return;
   float s = 0.f;
   if (c < NC) {
+    // the row's entries (a prefix of the 8, then -1), then every listed
+    // partial in flight at once; the adds keep the list order
     const float* lst = row_list + (size_t)f * 8;
+    float e[8], v[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) e[q] = lst[q];
+    bool live = true;
+#pragma unroll
     for (int q = 0; q < 8; ++q) {
-      const float e = lst[q];
-      if (e < 0.f) break;
-      const int ent = (int)e;
+      live = live && e[q] >= 0.f;
+      const int ent = live ? (int)e[q] : 0;
       const int seg = ent / kSlots, slot = ent % kSlots;
-      s += part[(((size_t)b * nseg + seg) * kSlots + slot) * ldc + c];
+      v[q] = live ? part[(((size_t)b * nseg + seg) * kSlots + slot) * ldc + c] : 0.f;
+    }
+    live = true;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      live = live && e[q] >= 0.f;
+      if (live) s += v[q];
     }
   }
   dctrl[((size_t)b * F + f) * ldc + c] = s;
