@@ -80,12 +80,12 @@ __global__ __launch_bounds__(256, BK == 16 ? 4 : 2) void k_gemm(const float* __r
                                               float* __restrict__ C, int M, int N, int K, int lda, int ldb, int ldc,
                                               int epi, const float* __restrict__ bias, const float* __restrict__ aux,
                                               int ldaux, int kchunk, float* __restrict__ ws,
-                                              float* __restrict__ cs) {
+                                              float* __restrict__ cs, const float* __restrict__ cw, int ncw) {
   static_assert(BK == 16 || BK == 32, "k-step depth");
   // float4 loads per thread per operand tile
   constexpr int LPT = BM * BK / 4 / 256;
   constexpr int LDSROW_T = ldsrow_t<BK>();
-  __shared__ float As_[2][BK * LDSROW];
+  __shared__ __align__(16) float As_[2][BK * LDSROW];
   __shared__ float Bs_[2][BK * LDSROW];
   constexpr int RA = A_KMAJ ? LDSROW : LDSROW_T;  // A is transposed when stored [M][K]
   constexpr int RB = B_NK ? LDSROW_T : LDSROW;    // B is transposed when stored [N][K]
@@ -278,10 +278,48 @@ __global__ __launch_bounds__(256, BK == 16 ? 4 : 2) void k_gemm(const float* __r
         }
       }
     if (cs) {
-      // column sums of the 128-row tile just stored: each lane sums its 32
-      // rows of column wn + tj*32 + r (rows past M excluded), lanes r and
-      // r+32 (the other four rows of every group of eight) are added, then
-      // the two waves sharing the columns, top half first
+      // column sums of the 128-row tile just stored, weighted by the ncw
+      // columns of cw ([M][ncw]) and plain: each lane sums its 32 rows of
+      // column wn + tj*32 + r, lanes r and r+32 (the other four rows of
+      // every group of eight) are added, then the two waves sharing the
+      // columns, top half first; the tile writes rows q < ncw (weighted by
+      // cw[.][q]) and ncw (plain) of its partials.  The k-loop's last
+      // barrier has retired every read of the operand tiles, so the
+      // weights are staged in one of them and the sums meet in the other.
+      float* red = As_[0];
+      if (ncw) {
+        // [q][BM] weights of the tile's rows, zero past M (where the
+        // accumulators are zero too: those A rows were loaded as zeros)
+        float* wt = As_[1];
+        for (int i = tid; i < ncw * BM; i += 256) {
+          const int rr = i / ncw, q = i - rr * ncw;
+          wt[q * BM + rr] = m0 + rr < M ? cw[(size_t)m0 * ncw + i] : 0.f;
+        }
+        __syncthreads();
+#pragma unroll 1
+        for (int q = 0; q < ncw; ++q) {
+          const float* wq = wt + q * BM + wm + h * 4;
+          float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+          for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              // rows 8g + e (e < 4) of this lane's 32-row block
+              const float4 w = *reinterpret_cast<const float4*>(wq + ti * 32 + g * 8);
+              s0 = fmaf(w.x, acc[ti][0][g * 4 + 0], s0);
+              s1 = fmaf(w.x, acc[ti][1][g * 4 + 0], s1);
+              s0 = fmaf(w.y, acc[ti][0][g * 4 + 1], s0);
+              s1 = fmaf(w.y, acc[ti][1][g * 4 + 1], s1);
+              s0 = fmaf(w.z, acc[ti][0][g * 4 + 2], s0);
+              s1 = fmaf(w.z, acc[ti][1][g * 4 + 2], s1);
+              s0 = fmaf(w.w, acc[ti][0][g * 4 + 3], s0);
+              s1 = fmaf(w.w, acc[ti][1][g * 4 + 3], s1);
+            }
+          s0 += __shfl_xor(s0, 32, 64);
+          s1 += __shfl_xor(s1, 32, 64);
+          red[(q * 4 + wave) * 64 + lane] = lane < 32 ? s0 : s1;
+        }
+      }
       float s[2];
 #pragma unroll
       for (int tj = 0; tj < 2; ++tj) {
@@ -295,13 +333,13 @@ __global__ __launch_bounds__(256, BK == 16 ? 4 : 2) void k_gemm(const float* __r
           }
         s[tj] += __shfl_xor(s[tj], 32, 64);
       }
-      // the k-loop's last barrier has retired every read of the operand tiles
-      float* red = As_[0];
-      red[wave * 64 + lane] = lane < 32 ? s[0] : s[1];
+      red[(ncw * 4 + wave) * 64 + lane] = lane < 32 ? s[0] : s[1];
       __syncthreads();
       if (wave < 2) {
         const int col = n0 + wn + lane;
-        if (col < N) cs[(size_t)by * N + col] = red[wave * 64 + lane] + red[(wave + 2) * 64 + lane];
+        if (col < N)
+          for (int q = 0; q <= ncw; ++q)
+            cs[((size_t)by * (ncw + 1) + q) * N + col] = red[(q * 4 + wave) * 64 + lane] + red[(q * 4 + wave + 2) * 64 + lane];
       }
     }
     return;
@@ -375,55 +413,56 @@ __global__ void k_splitk_reduce(const float* __restrict__ ws, float* __restrict_
 template <int BK, bool AK, bool BT, bool VA>
 static void launch_vb(bool vb, dim3 g, hipStream_t s, const float* A, const float* B, float* C, int M, int N, int K,
                       int lda, int ldb, int ldc, int epi, const float* bias, const float* aux, int ldaux, int kchunk,
-                      float* ws, float* cs, bool full) {
+                      float* ws, float* cs, const float* cw, int ncw, bool full) {
   if constexpr (VA) {
     if (vb && full) {
       hipLaunchKernelGGL((k_gemm<BK, AK, BT, true, true, true>), g, dim3(256), 0, s, A, B, C, M, N, K, lda, ldb, ldc,
-                         epi, bias, aux, ldaux, kchunk, ws, cs);
+                         epi, bias, aux, ldaux, kchunk, ws, cs, cw, ncw);
       return;
     }
   }
   if (vb)
     hipLaunchKernelGGL((k_gemm<BK, AK, BT, VA, true>), g, dim3(256), 0, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias,
-                       aux, ldaux, kchunk, ws, cs);
+                       aux, ldaux, kchunk, ws, cs, cw, ncw);
   else
     hipLaunchKernelGGL((k_gemm<BK, AK, BT, VA, false>), g, dim3(256), 0, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias,
-                       aux, ldaux, kchunk, ws, cs);
+                       aux, ldaux, kchunk, ws, cs, cw, ncw);
 }
 
 template <int BK, bool AK, bool BT>
 static void launch_variant(bool va, bool vb, dim3 g, hipStream_t s, const float* A, const float* B, float* C, int M,
                            int N, int K, int lda, int ldb, int ldc, int epi, const float* bias, const float* aux,
-                           int ldaux, int kchunk, float* ws, float* cs, bool full) {
+                           int ldaux, int kchunk, float* ws, float* cs, const float* cw, int ncw, bool full) {
   if (va)
-    launch_vb<BK, AK, BT, true>(vb, g, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias, aux, ldaux, kchunk, ws, cs, full);
+    launch_vb<BK, AK, BT, true>(vb, g, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias, aux, ldaux, kchunk, ws, cs, cw, ncw, full);
   else
-    launch_vb<BK, AK, BT, false>(vb, g, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias, aux, ldaux, kchunk, ws, cs, full);
+    launch_vb<BK, AK, BT, false>(vb, g, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias, aux, ldaux, kchunk, ws, cs, cw, ncw, full);
 }
 
 template <int BK>
 static void launch_layout(int64_t alay, int64_t blay, bool va, bool vb, dim3 g, hipStream_t s, const float* A,
                           const float* B, float* C, int M, int N, int K, int lda, int ldb, int ldc, int epi,
-                          const float* bias, const float* aux, int ldaux, int kchunk, float* ws, float* cs, bool full) {
+                          const float* bias, const float* aux, int ldaux, int kchunk, float* ws, float* cs,
+                          const float* cw, int ncw, bool full) {
   if (alay == 0 && blay == 0)
     launch_variant<BK, false, false>(va, vb, g, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias, aux, ldaux, kchunk, ws,
-                                     cs, full);
+                                     cs, cw, ncw, full);
   else if (alay == 0 && blay == 1)
     launch_variant<BK, false, true>(va, vb, g, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias, aux, ldaux, kchunk, ws,
-                                    cs, full);
+                                    cs, cw, ncw, full);
   else if (alay == 1 && blay == 0)
     launch_variant<BK, true, false>(va, vb, g, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias, aux, ldaux, kchunk, ws,
-                                    cs, full);
+                                    cs, cw, ncw, full);
   else
     launch_variant<BK, true, true>(va, vb, g, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias, aux, ldaux, kchunk, ws,
-                                   cs, full);
+                                   cs, cw, ncw, full);
 }
 
 int launch_gemm(const Launch& L, const dgen_hip_op& op) {
   const int64_t A = op.arg[0], Bc = op.arg[1], Cc = op.arg[2], M = op.arg[3], N = op.arg[4], K = op.arg[5];
   const int64_t lda = op.arg[6], ldb = op.arg[7], ldc = op.arg[8], alay = op.arg[9], blay = op.arg[10];
   const int64_t epi = op.arg[11], bias = op.arg[12], aux = op.arg[13], ldaux = op.arg[14];
-  const int64_t split = op.arg[15], ws = op.arg[16], colsum = op.arg[17];
+  const int64_t split = op.arg[15], ws = op.arg[16], colsum = op.arg[17], cwc = op.arg[18], ncw64 = op.arg[19];
   DGEN_REQUIRE(M > 0 && N > 0 && K > 0 && M < (1ll << 31) && N < (1ll << 31) && K < (1ll << 31),
                "gemm: M %lld N %lld K %lld", (long long)M, (long long)N, (long long)K);
   DGEN_REQUIRE(alay == 0 || alay == 1, "gemm: a_layout %lld", (long long)alay);
@@ -449,9 +488,12 @@ int launch_gemm(const Launch& L, const dgen_hip_op& op) {
   kchunk = (kchunk + BK - 1) / BK * BK;
   const int64_t splits = (K + kchunk - 1) / kchunk;
   if (split > 1) DGEN_CHECK_CELL(L, ws, splits * M * N, "gemm.workspace");
+  const int ncw = colsum >= 0 && ncw64 > 0 ? (int)ncw64 : 0;
   if (colsum >= 0) {
     DGEN_REQUIRE(epi == EPI_TANH_GRAD && splits == 1, "gemm: column partials need the tanh-gradient epilogue, no split");
-    DGEN_CHECK_CELL(L, colsum, (M + BM - 1) / BM * N, "gemm.column_partials");
+    DGEN_REQUIRE(ncw64 >= 0 && ncw64 <= 4, "gemm: %lld column-sum weights (0..4)", (long long)ncw64);
+    DGEN_CHECK_CELL(L, colsum, (M + BM - 1) / BM * (ncw + 1) * N, "gemm.column_partials");
+    if (ncw) DGEN_CHECK_CELL(L, cwc, M * ncw, "gemm.column_weights");
   }
   DGEN_REQUIRE((M + BM - 1) / BM <= 65535 && splits <= 65535, "gemm: grid too large");
   if (L.dry) return 0;
@@ -468,13 +510,14 @@ int launch_gemm(const Launch& L, const dgen_hip_op& op) {
   const float* paux = epi == EPI_TANH_GRAD ? cell(L, aux) : nullptr;
   float* pws = split > 1 ? cell(L, ws) : nullptr;
   float* pcs = colsum >= 0 ? cell(L, colsum) : nullptr;
+  const float* pcw = ncw ? cell(L, cwc) : nullptr;
   const int e = split > 1 ? EPI_NONE : (int)epi;
   if (BK == 32)
     launch_layout<32>(alay, blay, va, vb, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk,
-                      pws, pcs, full);
+                      pws, pcs, pcw, ncw, full);
   else
     launch_layout<16>(alay, blay, va, vb, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk,
-                      pws, pcs, full);
+                      pws, pcs, pcw, ncw, full);
   DGEN_LAUNCH_CHECK("k_gemm");
   if (split > 1) {
     const size_t total = (size_t)M * N;

@@ -231,10 +231,17 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
           dispatch="chunkPartialsReduceToCell", bytes=(M * NC + NC) * f4, flops=float(M * NC))
     dH = [p.alloc(f"dZ{l + 1}", M * Hd) for l in range(Lyr)]
     # column sums of dH[l] per 128-row GEMM tile, written by the data GEMM
-    # that produces dH[l]; the bias gradient reduces these tile rows
+    # that produces dH[l]; the bias gradient reduces these tile rows.  For
+    # the first layer the tile also writes the sums weighted by each input
+    # column of X, so W1 and b1 (contiguous in the parameters) reduce
+    # together from (din + 1) partial rows per tile.
     mt = (M + GEMM_TILE_M - 1) // GEMM_TILE_M
-    dcol = [p.alloc(f"dZ{l + 1}_tile_colsums", mt * Hd) if l > 0 else -1 for l in range(Lyr)]
-    p.add(R.K_GEMM, [dZ, Wh, dH[-1], M, Hd, NC, LDC, NC, Hd, 0, 1, R.EPI_TANH_GRAD, -1, Hs[-1], Hd, 1, 0, dcol[-1]],
+    if din > 4:
+        raise ValueError(f"first-layer fan-in {din} > 4")
+    dcol = [p.alloc(f"dZ{l + 1}_tile_colsums", mt * (din + 1 if l == 0 else 1) * Hd) for l in range(Lyr)]
+    wcol = [[X, din] if l == 0 else [-1, 0] for l in range(Lyr)]
+    p.add(R.K_GEMM, [dZ, Wh, dH[-1], M, Hd, NC, LDC, NC, Hd, 0, 1, R.EPI_TANH_GRAD, -1, Hs[-1], Hd, 1, 0, dcol[-1]]
+          + wcol[-1],
           label=f"dX_heads", dispatch="gemm", bytes=(M * NC + Hd * NC + 2 * M * Hd) * f4, flops=2.0 * M * Hd * NC,
           bound="mfma")
     for l in range(Lyr - 1, 0, -1):
@@ -246,12 +253,14 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
         p.add(R.K_COLSUM, [dcol[l], gb, mt, Hd, Hd, ws_col_side], flags=SIDE, label=f"db_l{l + 1}",
               dispatch="chunkPartialsReduceToCell", bytes=(mt * Hd + Hd) * f4, flops=float(mt * Hd))
         p.add(R.K_GEMM, [dH[l], W, dH[l - 1], M, Hd, Hd, Hd, Hd, Hd, 0, 1, R.EPI_TANH_GRAD, -1, Hs[l - 1], Hd, 1, 0,
-                         dcol[l - 1]],
+                         dcol[l - 1]] + wcol[l - 1],
               label=f"dX_l{l + 1}", dispatch="gemm", bytes=(3 * M * Hd + Hd * Hd) * f4, **gemm_hh)
     gw1, gb1 = gW[0]
-    p.add(R.K_DENSE_SMALL_WGRAD, [X, dH[0], gw1, M, din, Hd, ws_col, gb1], label="dWb_l1",
-          dispatch="chunkPartialsReduceToCell", bytes=(M * din + M * Hd + (din + 1) * Hd) * f4,
-          flops=2.0 * M * (din + 1) * Hd)
+    if gb1 != gw1 + din * Hd:
+        raise ValueError("first-layer weight and bias gradients are not contiguous")
+    p.add(R.K_COLSUM, [dcol[0], gw1, mt, (din + 1) * Hd, (din + 1) * Hd, ws_col], label="dWb_l1",
+          dispatch="chunkPartialsReduceToCell", bytes=(mt + 1) * (din + 1) * Hd * f4,
+          flops=float(mt * (din + 1) * Hd))
     if optimizer:
         m = p.alloc("adam_m", npar)
         v = p.alloc("adam_v", npar)

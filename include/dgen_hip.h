@@ -66,9 +66,13 @@ enum dgen_hip_kernel {
    *      [13]=aux cell (tanh output for EPI_TANH_GRAD, -1 none) [14]=ld aux
    *      [15]=split_k (1 = none; >1: partial sums in [16]) [16]=workspace cell
    *      [17]=column-partials cell or -1: with EPI_TANH_GRAD and no split,
-   *           row t (t < ceil(M/128)) receives the column sums of output
-   *           rows [128t, 128t+128), so a bias gradient is a reduction over
-   *           ceil(M/128) rows instead of M (DGEN_HIP_K_COLSUM on the cell) */
+   *           tile t (t < ceil(M/128)) covers output rows [128t, 128t+128)
+   *           and writes nw+1 rows of N partials at row t*(nw+1): for
+   *           q < nw the sums over its rows r of X[r][q]*C[r][n], then the
+   *           plain column sums, so the weight and bias gradients of a
+   *           layer fed by X are a reduction over ceil(M/128) rows instead
+   *           of M (DGEN_HIP_K_COLSUM on the cell)
+   *      [18]=X cell ([M][nw], read when nw > 0) [19]=nw (0..4) */
   DGEN_HIP_K_GEMM = 3,
 
   /* Head activations of HarmonicDecoderModel (Model.swift:100-114):

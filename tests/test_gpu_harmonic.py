@@ -114,3 +114,10 @@ def test_mlp_backward_matches_oracle(small):
     dctrl = out["dctrl"].reshape(cfg.M, 128)[:, :cfg.NC]
     ref = O.mlp_bwd(X, cfg.weights(), dctrl, cfg.M, cfg.din, cfg.hidden, cfg.layers, cfg.K, cfg.NF)
     assert rel(out["grads"], ref) < 1e-4
+    # first layer on its own (W1 then b1: reduced from the weighted tile
+    # partials of the GEMM that produces its input gradient), M not a
+    # multiple of the 128-row tile
+    assert cfg.M % 128
+    n1 = (cfg.din + 1) * cfg.hidden
+    assert rel(out["grads"][:cfg.din * cfg.hidden], ref[:cfg.din * cfg.hidden]) < 1e-4
+    assert rel(out["grads"][cfg.din * cfg.hidden:n1], ref[cfg.din * cfg.hidden:n1]) < 1e-4
