@@ -111,9 +111,10 @@ int launch_lerp_frames(const Launch& L, const dgen_hip_op& op) {
 //   steps segment s, and has issue priority on its SIMD.
 constexpr int kProducers = 4;
 constexpr int kCarryWaves = 1 + kProducers;
-constexpr int kGroups = (kSeg / 4 + kProducers - 1) / kProducers;  // float4 frame groups per producer
+constexpr int kGroups = kSeg / 4 / kProducers;  // float4 frame groups per producer
+static_assert(kGroups * kProducers * 4 == kSeg, "producers split a segment evenly");
 constexpr int kFrames = 4 * kGroups;
-constexpr int kIv = 3;                  // segments per barrier interval
+constexpr int kIv = 4;                  // segments per barrier interval
 constexpr int kCarryBufs = 2 * kIv;     // increment ring
 constexpr int kRing = 16;               // segments per f0 block
 constexpr int kIncLd = kSeg + 4;        // k-major row stride (floats)
@@ -129,7 +130,7 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
                                                                    float sr, float rsr) {
   __shared__ __align__(16) float s_inc[kCarryBufs][64 * kIncLd];  // [k][frame]
   __shared__ __align__(16) float s_f0[2][kRing * kSeg];
-  __shared__ int s_flag[kCarryBufs][kCarryWaves];  // segment needs the literal wrap form
+  __shared__ int s_flag[kCarryBufs * kProducers];  // [buf][producer]: segment needs the literal wrap form
   __shared__ int s_blkbad[2][kProducers];           // f0 block holds a value outside the fast range
   const int b = blockIdx.x, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int nseg = (T + kSeg - 1) / kSeg;
@@ -173,12 +174,11 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
     const int buf = s % kCarryBufs;
     // producer p owns frames [4 kGroups p, 4 kGroups (p + 1)) of the segment
     const int i0 = (wave - 1) * kFrames;
-    const int ng = min(kGroups, kSeg / 4 - (wave - 1) * kGroups);  // its float4 groups
     const float4* f4 = reinterpret_cast<const float4*>(&s_f0[(s / kRing) & 1][(s % kRing) * kSeg + i0]);
     float f[kFrames];
 #pragma unroll
     for (int q = 0; q < kGroups; ++q) {
-      const float4 v = q < ng ? f4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 v = f4[q];
       f[4 * q] = v.x;
       f[4 * q + 1] = v.y;
       f[4 * q + 2] = v.z;
@@ -191,7 +191,7 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
     for (int w = 0; w < kProducers; ++w) blkbad |= bb[w];
     const bool fast = !blkbad;
     float inc[kFrames];
-    if (fast) {
+    if (__builtin_expect(fast, 1)) {
 #pragma unroll
       for (int j = 0; j < kFrames; ++j) {
         const float x = kf * f[j];
@@ -204,9 +204,8 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
     }
     float4* dst = reinterpret_cast<float4*>(&s_inc[buf][lane * kIncLd + i0]);
 #pragma unroll
-    for (int q = 0; q < kGroups; ++q)
-      if (q < ng) dst[q] = make_float4(inc[4 * q], inc[4 * q + 1], inc[4 * q + 2], inc[4 * q + 3]);
-    if (lane == 0) s_flag[buf][wave] = fast ? 0 : 1;
+    for (int q = 0; q < kGroups; ++q) dst[q] = make_float4(inc[4 * q], inc[4 * q + 1], inc[4 * q + 2], inc[4 * q + 3]);
+    s_flag[buf * kProducers + wave - 1] = fast ? 0 : 1;  // every lane stores the same value: no branch
   };
   // chain: v[32h .. 32h+31] <- half h of segment s's increments
   auto fetch_half = [&](int s, float* v, int h) {
@@ -220,24 +219,22 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
       v[32 * h + 4 * q + 3] = u.w;
     }
   };
-  // returns 1 if segment s needs the wrap form
-  auto seg_flag = [&](int s) -> int {
-    int flag = 0;
-#pragma unroll
-    for (int w = 1; w < kCarryWaves; ++w) flag |= s_flag[s % kCarryBufs][w];
-    return flag || (T - s * kSeg) < kSeg;
-  };
-  auto fetch = [&](int s, float* v) -> int {
-    fetch_half(s, v, 0);
-    fetch_half(s, v, 1);
-    return seg_flag(s);
-  };
   float ph = 0.0f;  // the phasor state cell is zero at the start of every run
   // steps segment s from v; if nv, loads segment s+1 into nv half by half in
   // between so at most ~8 LDS reads are in flight
+  // checkpoint stores through a buffer resource bounded to this batch
+  // lane's rows: lanes >= K get an offset past the bound and the hardware
+  // drops their store, so the store needs no branch around it
+  const auto ck_rsrc = __builtin_amdgcn_make_buffer_rsrc(ckpt + (size_t)b * K, 0,
+                                                         (int)(4u * (unsigned)((nseg - 1) * B * K + K)), 0x00020000);
+  const unsigned ck_voff = lane < K ? 4u * (unsigned)lane : 0x80000000u;
+  auto store_ckpt = [&](int s) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, ph), ck_rsrc, ck_voff,
+                                          (int)(4u * (unsigned)(s * B * K)), 0);
+  };
   auto step_seg = [&](int s, const float* v, int slow, float* nv, auto has_next) {
     constexpr bool kNext = decltype(has_next)::value;
-    if (lane < K) ckpt[((size_t)s * B + b) * K + lane] = ph;
+    store_ckpt(s);
     if (!slow) {
       if constexpr (kNext) fetch_half(s + 1, nv, 0);
       __builtin_amdgcn_sched_barrier(0);
@@ -273,7 +270,66 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
     const int s0 = iv * kIv;
     if (wave == 0) {
       float va[kSeg], vb[kSeg];
-      int fa = fetch(s0, va), fb = 0;
+      // the interval's flags and its first segment's increments, one LDS
+      // round trip: the interval's buffers are consecutive in the ring, so
+      // lane q * kProducers + p reads producer p's flag for segment s0 + q
+      // and one ballot gathers them; a segment past the end or shorter than
+      // kSeg also takes the wrap form
+      static_assert(kCarryBufs % kIv == 0 && kIv * kProducers <= 64, "interval flags in one read");
+      const int fv = lane < kIv * kProducers ? s_flag[(s0 % kCarryBufs) * kProducers + lane] : 0;
+      fetch_half(s0, va, 0);
+      fetch_half(s0, va, 1);
+      const unsigned long long fm = __ballot(fv != 0);
+      int fl[kIv];
+#pragma unroll
+      for (int q = 0; q < kIv; ++q)
+        fl[q] = ((fm >> (q * kProducers)) & ((1ull << kProducers) - 1)) != 0 || (T - (s0 + q) * kSeg) < kSeg;
+      bool straight = true;
+#pragma unroll
+      for (int q = 0; q < kIv; ++q) straight = straight && !fl[q];
+      if (straight) {
+        // every segment full-length and in the fast form: one run of
+        // kIv * kSeg steps without a branch (a taken branch stalls the lone
+        // chain wave for its instruction refetch)
+        // Three rotating half-segment buffers X, Y, Z: each half steps
+        // while the half two ahead loads into the buffer the previous half
+        // freed (the empty asm statements keep every load at its place).
+        static_assert(kIv == 4, "the run below covers four segments");
+        float* X = va;
+        float* Y = va + kSeg / 2;
+        float* Z = vb;
+        auto ld = [&](int s, int h, float* d) {
+          asm volatile("" ::: "memory");
+          const float4* src = reinterpret_cast<const float4*>(&s_inc[s % kCarryBufs][lane * kIncLd]) + 8 * h;
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const float4 u = src[q];
+            d[4 * q] = u.x;
+            d[4 * q + 1] = u.y;
+            d[4 * q + 2] = u.z;
+            d[4 * q + 3] = u.w;
+          }
+          asm volatile("" ::: "memory");
+        };
+        auto st = [&](const float* v) {
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int i = 0; i < kSeg / 2; ++i) ph = __builtin_amdgcn_fractf(ph + v[i]);
+          __builtin_amdgcn_sched_barrier(0);
+        };
+        store_ckpt(s0);
+        ld(s0 + 1, 0, Z); st(X); ld(s0 + 1, 1, X); st(Y);
+        store_ckpt(s0 + 1);
+        ld(s0 + 2, 0, Y); st(Z); ld(s0 + 2, 1, Z); st(X);
+        store_ckpt(s0 + 2);
+        ld(s0 + 3, 0, X); st(Y); ld(s0 + 3, 1, Y); st(Z);
+        store_ckpt(s0 + 3);
+        st(X); st(Y);
+      } else {
+      // (loaded again: the run's registers stay its own)
+      fetch_half(s0, va, 0);
+      fetch_half(s0, va, 1);
+      int fa = fl[0], fb = 0;
 #pragma unroll
       for (int q = 0; q < kIv; ++q) {
         const int s = s0 + q;
@@ -282,32 +338,37 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
         const bool more = q + 1 < kIv && s + 1 < nseg;
         if (q % 2 == 0) {
           if (more) {
-            fb = seg_flag(s + 1);
+            fb = fl[q + 1];
             step_seg(s, va, fa, vb, std::true_type{});
           } else {
             step_seg(s, va, fa, vb, std::false_type{});
           }
         } else {
           if (more) {
-            fa = seg_flag(s + 1);
+            fa = fl[q + 1];
             step_seg(s, vb, fb, va, std::true_type{});
           } else {
             step_seg(s, vb, fb, va, std::false_type{});
           }
         }
       }
+      }
     } else {
-      // f0 block s/16 + 1 goes into the half whose segments are all
-      // produced; its loads are issued with segment s and committed after
-      // the interval's produce work (it is first read 16 segments later)
+      // f0 block s/16 + 1 (s the interval's segment at a block boundary)
+      // goes into the half whose segments are all produced; its loads are
+      // issued before the interval's produce work and committed after it
+      // (it is first read 16 segments later)
       const int next = s0 + kIv;
-      int pending = -1;
-      for (int s = next; s < next + kIv && s < nseg; ++s) {
-        if (s % kRing == 0) {
-          pending = s / kRing + 1;
-          issue_block(pending);
-        }
-        produce(s);
+      // at most one block boundary falls in an interval (kIv <= kRing)
+      static_assert(kIv <= kRing, "one f0 block boundary per interval");
+      const int sb = (next + kRing - 1) / kRing * kRing;
+      const int pending = sb < next + kIv && sb < nseg ? sb / kRing + 1 : -1;
+      if (pending >= 0) issue_block(pending);
+      if (__builtin_expect(next + kIv <= nseg, 1)) {
+#pragma unroll
+        for (int q = 0; q < kIv; ++q) produce(next + q);
+      } else {
+        for (int s = next; s < nseg; ++s) produce(s);
       }
       if (pending >= 0) commit_block(pending);
     }
@@ -324,6 +385,7 @@ int launch_phasor_carry(const Launch& L, const dgen_hip_op& op) {
   const int64_t nseg = (T + kSeg - 1) / kSeg;
   DGEN_CHECK_CELL(L, f0f, B * T, "phasor_carry.f0_frames");
   DGEN_CHECK_CELL(L, ck, nseg * B * K, "phasor_carry.checkpoints");
+  DGEN_REQUIRE(nseg * B * K < (1ll << 29), "phasor_carry: %lld checkpoints (< 2^29)", (long long)(nseg * B * K));
   if (L.dry) return 0;
   const float sr = op.farg[0], rsr = 1.0f / sr;
   hipLaunchKernelGGL(k_phasor_carry, dim3((unsigned)B), dim3(64 * kCarryWaves), 0, L.stream, cell(L, f0f),
