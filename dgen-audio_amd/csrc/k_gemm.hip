@@ -11,16 +11,13 @@
 // LDS holds both operand tiles k-major ([BK][BM] and [BK][BN]) so every
 // layout (A as [M][K] or [K][M], B as [K][N] or [N][K]) feeds the MFMA with
 // conflict-free single-float reads; tiles are double buffered with one
-// barrier per k-step.  Two k-step depths:
-// - BK = 16: 33 KB of LDS and at most 128 registers per lane, so four
-//   workgroups share a CU (four waves per SIMD): a 1000-tile grid runs in one
-//   round on 256 CUs, and each SIMD has other waves' MFMAs to issue while one
-//   waits at its barrier (the backward GEMMs, 5-10% faster);
-// - BK = 32: 66 KB, two workgroups per CU.  The hidden forward layers (bias
-//   + tanh epilogue) use it: they run beside the phasor carry, whose serial
-//   chain is the step's critical path while they do; measured, the denser
-//   BK = 16 forward GEMMs slowed the carry by more (0.50 -> 0.62 ms) than
-//   they gained themselves.
+// barrier per k-step.  The k-step depth is a template parameter (16 or 32);
+// every launch uses BK = 16: 33 KB of LDS and at most 128 registers per lane,
+// so four workgroups share a CU (four waves per SIMD): a 1000-tile grid runs
+// in one round on 256 CUs, and each SIMD has other waves' MFMAs to issue
+// while one waits at its barrier.  (BK = 32 takes 66 KB, two workgroups per
+// CU: 5-10% slower alone.  The phasor carry beside the forward layers holds
+// 148 KB of its CU's LDS, so no BK = 16 workgroup lands on its CUs either.)
 #include "internal.h"
 
 namespace dgen {
@@ -480,9 +477,7 @@ int launch_gemm(const Launch& L, const dgen_hip_op& op) {
     DGEN_REQUIRE(ldaux >= N, "gemm: ld aux %lld", (long long)ldaux);
     DGEN_CHECK_CELL(L, aux, (M - 1) * ldaux + N, "gemm.aux");
   }
-  // the hidden forward layers (bias + tanh) take the 32-deep k-step, every
-  // other GEMM the 16-deep one (see the header comment)
-  const int BK = epi == EPI_BIAS_TANH ? 32 : 16;
+  constexpr int BK = 16;
   // k-chunk per split, a multiple of BK
   int64_t kchunk = (K + split - 1) / split;
   kchunk = (kchunk + BK - 1) / BK * BK;
@@ -512,12 +507,8 @@ int launch_gemm(const Launch& L, const dgen_hip_op& op) {
   float* pcs = colsum >= 0 ? cell(L, colsum) : nullptr;
   const float* pcw = ncw ? cell(L, cwc) : nullptr;
   const int e = split > 1 ? EPI_NONE : (int)epi;
-  if (BK == 32)
-    launch_layout<32>(alay, blay, va, vb, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk,
-                      pws, pcs, pcw, ncw, full);
-  else
-    launch_layout<16>(alay, blay, va, vb, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk,
-                      pws, pcs, pcw, ncw, full);
+  launch_layout<BK>(alay, blay, va, vb, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk,
+                    pws, pcs, pcw, ncw, full);
   DGEN_LAUNCH_CHECK("k_gemm");
   if (split > 1) {
     const size_t total = (size_t)M * N;
