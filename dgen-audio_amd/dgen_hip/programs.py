@@ -247,11 +247,14 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     for l in range(Lyr - 1, 0, -1):
         W, _b = woff[l]
         gw, gb = gW[l]
-        p.add(R.K_GEMM, [Hs[l - 1], dH[l], gw, Hd, Hd, M, Hd, Hd, Hd, 1, 0, R.EPI_NONE, -1, -1, 0, split, ws_gemm, -1],
-              flags=SIDE | FORK, label=f"dW_l{l + 1}", dispatch="gemmChunkPartials",
-              bytes=(2 * M * Hd + Hd * Hd) * f4, **gemm_hh)
-        p.add(R.K_COLSUM, [dcol[l], gb, mt, Hd, Hd, ws_col_side], flags=SIDE, label=f"db_l{l + 1}",
+        # the bias gradient (a short reduce of tile partials) goes ahead of
+        # the weight GEMM on the side stream, so the last one is not left
+        # after the final weight GEMM
+        p.add(R.K_COLSUM, [dcol[l], gb, mt, Hd, Hd, ws_col_side], flags=SIDE | FORK, label=f"db_l{l + 1}",
               dispatch="chunkPartialsReduceToCell", bytes=(mt * Hd + Hd) * f4, flops=float(mt * Hd))
+        p.add(R.K_GEMM, [Hs[l - 1], dH[l], gw, Hd, Hd, M, Hd, Hd, Hd, 1, 0, R.EPI_NONE, -1, -1, 0, split, ws_gemm, -1],
+              flags=SIDE, label=f"dW_l{l + 1}", dispatch="gemmChunkPartials",
+              bytes=(2 * M * Hd + Hd * Hd) * f4, **gemm_hh)
         p.add(R.K_GEMM, [dH[l], W, dH[l - 1], M, Hd, Hd, Hd, Hd, Hd, 0, 1, R.EPI_TANH_GRAD, -1, Hs[l - 1], Hd, 1, 0,
                          dcol[l - 1]] + wcol[l - 1],
               label=f"dX_l{l + 1}", dispatch="gemm", bytes=(3 * M * Hd + Hd * Hd) * f4, **gemm_hh)
