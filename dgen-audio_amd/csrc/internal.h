@@ -130,4 +130,18 @@ int launch_stft_bwd(const Launch&, const dgen_hip_op&);
 int launch_membrane_fwd(const Launch&, const dgen_hip_op&);
 int launch_membrane_bwd(const Launch&, const dgen_hip_op&);
 
+// Sum over the 64 lanes of a wave (butterfly; every lane gets the total).
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+// softplus(x) = max(x,0) + log(1 + exp(-|x|))  (Model.swift:153-157)
+__device__ __forceinline__ float softplus(float x) { return fmaxf(x, 0.f) + logf(1.f + expf(-fabsf(x))); }
+// d softplus through the reference AD rules: [x>=0] - sign(x) e^{-|x|}/(1+e^{-|x|})
+__device__ __forceinline__ float softplus_grad(float x) {
+  float e = expf(-fabsf(x));
+  float sg = x > 0.f ? 1.f : (x < 0.f ? -1.f : 0.f);
+  return (x >= 0.f ? 1.f : 0.f) - sg * (e / (1.f + e));
+}
+
 }  // namespace dgen

@@ -794,11 +794,18 @@ __global__ __launch_bounds__(64 * kWavesBwd) void k_synth_bwd(SynthArgs a, const
 }
 
 // d ctrl[b*F+f][c] = sum over the (segment, slot) entries listed for row f.
+// With HEADS the workgroup also runs the head backward of its row (the
+// same rules as k_heads_bwd, Model.swift:100-114): thread c owns column c,
+// and the row sums (softplus over the K amplitudes, |tanh| over the NF
+// noise taps, then the two dot products) combine the waves' sums through
+// LDS in wave order.
+template <bool HEADS>
 __global__ void k_synth_bwd_reduce(const float* __restrict__ part, const float* __restrict__ row_list,
-                                   float* __restrict__ dctrl, int B, int NC, int ldc, int F, int nseg) {
+                                   float* __restrict__ dctrl, int B, int NC, int ldc, int F, int nseg,
+                                   const float* __restrict__ Z, float* __restrict__ dZ, int K, int NF) {
   const int c = threadIdx.x;
   const int f = blockIdx.x, b = blockIdx.y;
-  if (c >= ldc) return;
+  if (!HEADS && c >= ldc) return;
   float s = 0.f;
   if (c < NC) {
     // the row's entries (a prefix of the 8, then -1), then every listed
@@ -822,7 +829,51 @@ __global__ void k_synth_bwd_reduce(const float* __restrict__ part, const float* 
       if (live) s += v[q];
     }
   }
-  dctrl[((size_t)b * F + f) * ldc + c] = s;
+  const size_t row = (size_t)b * F + f;
+  if (c < ldc) dctrl[row * ldc + c] = s;
+  if constexpr (HEADS) {
+    __shared__ float red[16][4];  // per wave: sum sp, sum |th|, then the two dots
+    const int wave = c >> 6, lane = c & 63, nw = blockDim.x >> 6;
+    const bool amp = c < K, gain = c == K || c == K + 1, noise = c >= K + 2 && c < K + 2 + NF;
+    const float z = (amp || gain || noise) ? Z[row * ldc + c] : 0.f;
+    const float sp = amp ? softplus(z) : 0.f;
+    const float th = noise ? tanhf(z) : 0.f;
+    float r0 = wave_sum(sp), r1 = wave_sum(fabsf(th));
+    if (lane == 0) {
+      red[wave][0] = r0;
+      red[wave][1] = r1;
+    }
+    __syncthreads();
+    float den = 0.f, nrm = 0.f;
+    for (int w = 0; w < nw; ++w) {
+      den += red[w][0];
+      nrm += red[w][1];
+    }
+    den += 1e-6f;
+    nrm += 1e-4f;
+    r0 = wave_sum(amp ? s * (sp / den) : 0.f);
+    r1 = wave_sum(noise ? s * (th / nrm) : 0.f);
+    if (lane == 0) {
+      red[wave][2] = r0;
+      red[wave][3] = r1;
+    }
+    __syncthreads();
+    float dot = 0.f, dot2 = 0.f;
+    for (int w = 0; w < nw; ++w) {
+      dot += red[w][2];
+      dot2 += red[w][3];
+    }
+    float out = 0.f;  // padding columns stay exactly zero
+    if (amp) {
+      out = (s - dot) / den * softplus_grad(z);
+    } else if (gain) {
+      out = s * softplus_grad(z);
+    } else if (noise) {
+      const float sg = th > 0.f ? 1.f : (th < 0.f ? -1.f : 0.f);
+      out = (s - sg * dot2) / nrm * (1.f - th * th);
+    }
+    if (c < ldc) dZ[row * ldc + c] = out;
+  }
 }
 
 static int synth_args(const Launch& L, const dgen_hip_op& op, SynthArgs& a, const char* who) {
@@ -898,8 +949,11 @@ int launch_synth_bwd(const Launch& L, const dgen_hip_op& op) {
 
 int launch_synth_bwd_reduce(const Launch& L, const dgen_hip_op& op) {
   // arg: [0]=partials [1]=row_list [2]=dctrl [3]=B [4]=NC [5]=F [6]=T [7]=seg [8]=ldc
+  //      [9]=Z or -1 [10]=dZ [11]=K [12]=NF (with Z: the head backward too)
   const int64_t part = op.arg[0], rl = op.arg[1], dc = op.arg[2], B = op.arg[3], NC = op.arg[4], F = op.arg[5],
                 T = op.arg[6], seg = op.arg[7], ldc = op.arg[8];
+  const int64_t Zc = op.arg[9], dZc = op.arg[10], K = op.arg[11], NF = op.arg[12];
+  const bool heads = Zc >= 0;
   DGEN_REQUIRE(B > 0 && B <= 65535 && NC > 0 && ldc >= NC && ldc <= 1024 && F > 0 && T > 0 && seg == kSeg,
                "synth_bwd_reduce: B %lld NC %lld F %lld T %lld seg %lld ldc %lld", (long long)B, (long long)NC,
                (long long)F, (long long)T, (long long)seg, (long long)ldc);
@@ -907,9 +961,20 @@ int launch_synth_bwd_reduce(const Launch& L, const dgen_hip_op& op) {
   DGEN_CHECK_CELL(L, part, B * nseg * kSlots * ldc, "synth_bwd_reduce.partials");
   DGEN_CHECK_CELL(L, rl, F * 8, "synth_bwd_reduce.row_list");
   DGEN_CHECK_CELL(L, dc, B * F * ldc, "synth_bwd_reduce.dctrl");
+  if (heads) {
+    DGEN_REQUIRE(K > 0 && NF > 0 && K + 2 + NF == NC, "synth_bwd_reduce: heads K %lld NF %lld NC %lld", (long long)K,
+                 (long long)NF, (long long)NC);
+    DGEN_CHECK_CELL(L, Zc, B * F * ldc, "synth_bwd_reduce.Z");
+    DGEN_CHECK_CELL(L, dZc, B * F * ldc, "synth_bwd_reduce.dZ");
+  }
   if (L.dry) return 0;
-  hipLaunchKernelGGL(k_synth_bwd_reduce, dim3((unsigned)F, (unsigned)B), dim3((unsigned)((ldc + 63) / 64 * 64)), 0,
-                     L.stream, cell(L, part), cell(L, rl), cell(L, dc), (int)B, (int)NC, (int)ldc, (int)F, (int)nseg);
+  const dim3 grid((unsigned)F, (unsigned)B), block((unsigned)((ldc + 63) / 64 * 64));
+  if (heads)
+    hipLaunchKernelGGL(k_synth_bwd_reduce<true>, grid, block, 0, L.stream, cell(L, part), cell(L, rl), cell(L, dc),
+                       (int)B, (int)NC, (int)ldc, (int)F, (int)nseg, cell(L, Zc), cell(L, dZc), (int)K, (int)NF);
+  else
+    hipLaunchKernelGGL(k_synth_bwd_reduce<false>, grid, block, 0, L.stream, cell(L, part), cell(L, rl), cell(L, dc),
+                       (int)B, (int)NC, (int)ldc, (int)F, (int)nseg, nullptr, nullptr, 0, 0);
   DGEN_LAUNCH_CHECK("k_synth_bwd_reduce");
   return 0;
 }

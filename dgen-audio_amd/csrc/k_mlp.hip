@@ -14,10 +14,6 @@ namespace dgen {
 
 constexpr int kWave = 64;
 
-__device__ __forceinline__ float wave_sum(float v) {
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-  return v;
-}
 
 // ---------------------------------------------------------------- layer 1
 // H[m][j] = tanh(sum_i X[m][i] W[i][j] + b[j]) for a fan-in of a few inputs.
@@ -220,14 +216,6 @@ int launch_dense_small_wgrad(const Launch& L, const dgen_hip_op& op) {
 }
 
 // ---------------------------------------------------------------- heads
-// softplus(x) = max(x,0) + log(1 + exp(-|x|))  (Model.swift:153-157)
-__device__ __forceinline__ float softplus(float x) { return fmaxf(x, 0.f) + logf(1.f + expf(-fabsf(x))); }
-// d softplus through the reference AD rules: [x>=0] - sign(x) e^{-|x|}/(1+e^{-|x|})
-__device__ __forceinline__ float softplus_grad(float x) {
-  float e = expf(-fabsf(x));
-  float sg = x > 0.f ? 1.f : (x < 0.f ? -1.f : 0.f);
-  return (x >= 0.f ? 1.f : 0.f) - sg * (e / (1.f + e));
-}
 
 // One wave per row; Z and ctrl rows have stride ldz / ldc.  Lane l owns
 // elements l and l + 64 of each head group (K, NF <= 128), and every

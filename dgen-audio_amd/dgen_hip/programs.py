@@ -204,11 +204,11 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     p.add(R.K_SYNTH_BWD, bargs, [cfg.sr, hs, ns], label="synth_bwd", dispatch=f"selfManagedThreads({B})",
           bytes=ctrl_b + lerp_b + ck_b + data_b + 4 * B * T * f4 + part_b,
           flops=synth_flops + float(B) * T * (6.0 * K + 4.0 * NC), bound="valu")
-    p.add(R.K_SYNTH_BWD_REDUCE, [part, rowlist, dctrl, B, NC, F, T, SEG, LDC], label="synth_bwd_reduce",
-          dispatch=f"perFrameScaled({M})", bytes=part_b + F * ROW_ENTRIES * f4 + M * NC * f4, flops=part_b / f4)
+    # the row reduce also runs the head backward of its row (dZ from d ctrl and Z)
     dZ = p.alloc("dZ", M * LDC)
-    p.add(R.K_HEADS_BWD, [Z, dctrl, dZ, M, K, NF, LDC], label="heads_bwd", dispatch=f"perFrameScaled({M})",
-          bytes=3 * M * NC * f4, flops=M * (K * 20.0 + NF * 14.0))
+    p.add(R.K_SYNTH_BWD_REDUCE, [part, rowlist, dctrl, B, NC, F, T, SEG, LDC, Z, dZ, K, NF], label="synth_bwd_reduce",
+          dispatch=f"perFrameScaled({M})", bytes=part_b + F * ROW_ENTRIES * f4 + 3 * M * NC * f4,
+          flops=part_b / f4 + M * (K * 20.0 + NF * 14.0))
 
     G = p.alloc("grads", npar)
     split = max(1, (M + SPLITK_ROWS - 1) // SPLITK_ROWS)

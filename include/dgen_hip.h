@@ -126,7 +126,10 @@ enum dgen_hip_kernel {
   DGEN_HIP_K_SYNTH_BWD = 9,
 
   /* Deterministic reduction of synth-backward segment partials into d ctrl.
-   * arg: [0]=partials [1]=playhead [2]=dctrl [3]=B [4]=NC [5]=F [6]=T [7]=seg */
+   * arg: [0]=partials [1]=playhead [2]=dctrl [3]=B [4]=NC [5]=F [6]=T [7]=seg
+   *      [8]=row stride [9]=Z cell or -1: with Z, the head backward of each
+   *      row too (as DGEN_HIP_K_HEADS_BWD), into [10]=dZ, [11]=K [12]=NF
+   *      (K + 2 + NF = NC) */
   DGEN_HIP_K_SYNTH_BWD_REDUCE = 10,
 
   /* Head backward: dZ from d ctrl and Z.  arg: [0]=Z [1]=dctrl [2]=dZ
