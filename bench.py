@@ -21,10 +21,12 @@ With ``--workload biquad`` the same line is printed for BASELINE config 4
 ``--workload stft`` for config 2 (8 x 2^20 STFT round trip with per-bin
 gains, forward + loss + gain gradient + Adam) and with ``--workload
 membrane`` for config 5 (512^2 membrane, 4800 steps, forward + loss + adjoint
-+ Adam) instead; the default workload is the headline config 3.
++ Adam) and with ``--workload oscbank`` for config 1 (16-oscillator bank,
+65536 frames, forward only) instead; the default workload is the headline
+config 3.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                       [--workload harmonic|biquad|stft|membrane]
+                       [--workload harmonic|biquad|stft|membrane|oscbank]
 """
 from __future__ import annotations
 
@@ -48,6 +50,32 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+def host_cpu() -> str:
+    """The host's CPU model (first /proc/cpuinfo entry) and thread count."""
+    model = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return f"{model}, nproc {os.cpu_count()}"
+
+
+def median_time(fn, repeats: int) -> float:
+    """Median wall time of `repeats` calls of fn() after one warm-up call."""
+    fn()
+    times = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2]
+
+
 def cpu_baseline(cfg, lanes: int, repeats: int) -> dict:
     """Time the oracle's emission-faithful fp32 forward (built with the
     reference C backend's -O3 -ffast-math -ffp-contract=fast policy) on
@@ -67,24 +95,17 @@ def cpu_baseline(cfg, lanes: int, repeats: int) -> dict:
     uvs = np.ascontiguousarray(uv[:, :lanes])
     P = cfg.weights()
     tgt = np.zeros((lanes, cfg.T), np.float32)
-    times = []
-    for i in range(repeats + 1):
-        t0 = time.perf_counter()
-        O.harmonic_step(sub, Xs, P, f0s, uvs, tgt, grad=False, prec="f32", libname="liboracle_bench.so")
-        dt = time.perf_counter() - t0
-        if i:
-            times.append(dt)
-    times.sort()
-    med = times[len(times) // 2]
+    med = median_time(lambda: O.harmonic_step(sub, Xs, P, f0s, uvs, tgt, grad=False, prec="f32",
+                                              libname="liboracle_bench.so"), repeats)
     return {
         "value": lanes * cfg.T / med,
         "unit": "audio samples/s",
         "cores": 1,
         "kind": "port",
+        "host_cpu": host_cpu(),
         "sample": (f"forward only (the reference C backend has no backward): {lanes} of {cfg.B} lanes x "
                    f"T={cfg.T}, MLP {cfg.layers}x{cfg.hidden} + synth + {len(cfg.fft_sizes)}-scale spectral "
-                   f"loss; median of {repeats} after 1 warm-up; host {platform.processor() or platform.machine()}, "
-                   f"nproc {os.cpu_count()}"),
+                   f"loss; median of {repeats} after 1 warm-up; host {host_cpu()}"),
     }
 
 
@@ -195,24 +216,17 @@ def biquad_cpu_baseline(cfg, repeats: int) -> dict:
     import ctypes
     import numpy as np
     g = np.zeros(2 * cfg.B, np.float32)
-    times = []
-    for i in range(repeats + 1):
-        t0 = time.perf_counter()
-        fn(x, m.ctypes.data_as(ctypes.c_void_p), np.ascontiguousarray(p[:cfg.B]), np.ascontiguousarray(p[cfg.B:]),
-           tgt, cfg.B, cfg.T, None, g.ctypes.data_as(ctypes.c_void_p))
-        dt = time.perf_counter() - t0
-        if i:
-            times.append(dt)
-    times.sort()
-    med = times[len(times) // 2]
+    med = median_time(lambda: fn(x, m.ctypes.data_as(ctypes.c_void_p), np.ascontiguousarray(p[:cfg.B]),
+                                 np.ascontiguousarray(p[cfg.B:]), tgt, cfg.B, cfg.T, None,
+                                 g.ctypes.data_as(ctypes.c_void_p)), repeats)
     return {
         "value": cfg.B * cfg.T / med,
         "unit": "lane-samples/s",
         "cores": 1,
         "kind": "port",
+        "host_cpu": host_cpu(),
         "sample": (f"whole workload ({cfg.B} lanes x {cfg.T} frames): sequential fp32 forward, loss and BPTT "
-                   f"backward (no Adam); median of {repeats} after 1 warm-up; host "
-                   f"{platform.processor() or platform.machine()}, nproc {os.cpu_count()}"),
+                   f"backward (no Adam); median of {repeats} after 1 warm-up; host {host_cpu()}"),
     }
 
 
@@ -268,23 +282,18 @@ def stft_cpu_baseline(cfg, signals: int, repeats: int) -> dict:
     x = sub.inputs()
     fn = O._fn("dgen_oracle_stft_step", "f32", "liboracle_bench.so")
     dg = np.zeros(cfg.bins, np.float32)
-    times = []
-    for i in range(repeats + 1):
-        t0 = time.perf_counter()
-        fn(x, signals, cfg.T, cfg.N, cfg.H, cfg.window(), cfg.gains(), None, dg.ctypes.data_as(ctypes.c_void_p))
-        dt = time.perf_counter() - t0
-        if i:
-            times.append(dt)
-    times.sort()
-    med = times[len(times) // 2]
+    win, gains = cfg.window(), cfg.gains()
+    med = median_time(lambda: fn(x, signals, cfg.T, cfg.N, cfg.H, win, gains, None,
+                                 dg.ctypes.data_as(ctypes.c_void_p)), repeats)
     return {
         "value": signals * cfg.T / med,
         "unit": "input samples/s",
         "cores": 1,
         "kind": "port",
+        "host_cpu": host_cpu(),
         "sample": (f"{signals} of {cfg.S} signals x {cfg.T} samples: radix-2 tensorFFT forward, gains, IFFT, "
                    f"overlap-add, loss and gain gradient (no Adam); median of {repeats} after 1 warm-up; host "
-                   f"{platform.processor() or platform.machine()}, nproc {os.cpu_count()}"),
+                   f"{host_cpu()}"),
     }
 
 
@@ -340,23 +349,17 @@ def membrane_cpu_baseline(cfg, frames: int, repeats: int) -> dict:
     fn = O._fn("dgen_oracle_membrane_step", "f32", "liboracle_bench.so")
     g = np.zeros(2, np.float32)
     py, px = cfg.pickup
-    times = []
-    for i in range(repeats + 1):
-        t0 = time.perf_counter()
-        fn(u0, cfg.R, cfg.C, frames, cfg.c2, cfg.d, py, px, tgt, None, g.ctypes.data_as(ctypes.c_void_p))
-        dt = time.perf_counter() - t0
-        if i:
-            times.append(dt)
-    times.sort()
-    med = times[len(times) // 2]
+    med = median_time(lambda: fn(u0, cfg.R, cfg.C, frames, cfg.c2, cfg.d, py, px, tgt, None,
+                                 g.ctypes.data_as(ctypes.c_void_p)), repeats)
     return {
         "value": cfg.R * cfg.C * frames / med,
         "unit": "cell-steps/s",
         "cores": 1,
         "kind": "port",
+        "host_cpu": host_cpu(),
         "sample": (f"{cfg.R}x{cfg.C} grid, first {frames} of {cfg.T} frames: sequential fp32 forward, loss and "
                    f"adjoint with checkpoint recomputation (no Adam); median of {repeats} after 1 warm-up; host "
-                   f"{platform.processor() or platform.machine()}, nproc {os.cpu_count()}"),
+                   f"{host_cpu()}"),
     }
 
 
@@ -397,6 +400,59 @@ def run_membrane(args) -> dict:
     return out
 
 
+OSCBANK_METRIC = "output samples/sec, 16-oscillator deterministic phasor bank -> sum -> one-pole, 65536 frames"
+
+
+def oscbank_cpu_baseline(cfg, repeats: int) -> dict:
+    """The oracle's fp32 oscillator bank (-O3 -ffast-math build) over the
+    whole config-1 workload, single thread, like the reference C backend."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    freqs, amps = cfg.inputs()
+    med = median_time(lambda: O.oscbank(freqs, amps, cfg.sr, cfg.pole, cfg.frames, libname="liboracle_bench.so"),
+                      repeats)
+    return {
+        "value": cfg.frames / med,
+        "unit": "output samples/s",
+        "cores": 1,
+        "kind": "port",
+        "host_cpu": host_cpu(),
+        "sample": (f"whole workload ({cfg.n_osc} oscillators x {cfg.frames} frames): frame-sequential fp32 "
+                   f"phasors, sin, sum and one-pole; median of {repeats} after 1 warm-up; host {host_cpu()}"),
+    }
+
+
+def run_oscbank(args) -> dict:
+    from dgen_hip import OscBankConfig
+    from dgen_hip.programs import oscbank_program
+    from dgen_hip.runtime import HIPLazyRuntime
+    cfg = OscBankConfig()
+    log(f"bench: oscillator bank n_osc={cfg.n_osc} frames={cfg.frames}")
+    prog = oscbank_program(cfg)
+    freqs, amps = cfg.inputs()
+    with HIPLazyRuntime(prog, 0) as rt:
+        rt.write("freqs", freqs)
+        rt.write("amps", amps)
+        wall, rows, dom, roof_ms = time_session(rt, prog, args)
+    ms_per_step = wall * 1e3 / args.steps
+    cpu = None
+    if not args.no_cpu:
+        log("bench: cpu baseline (oscillator bank)")
+        cpu = oscbank_cpu_baseline(cfg, args.cpu_repeats)
+    out = {
+        "metric": OSCBANK_METRIC, "value": cfg.frames * args.steps / wall, "unit": "output samples/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (amplitudes U[0,1] from SplitMix64, normalised to sum 1)",
+        "config": {"workload": "config 1: 16 deterministic phasors at k*220 Hz, sin, amplitude sum, history "
+                               "one-pole 0.9, forward only", "n_osc": cfg.n_osc, "frames": cfg.frames, "sr": cfg.sr,
+                   "parallelism": "single GPU"},
+    }
+    out.update(roofline_fields(rows, dom, roof_ms, ms_per_step, "oscbank"))
+    out["cpu_baseline"] = cpu
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
@@ -404,13 +460,13 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-lanes", type=int, default=4)
-    ap.add_argument("--cpu-repeats", type=int, default=3)
+    ap.add_argument("--cpu-repeats", type=int, default=5)
     ap.add_argument("--op-iters", type=int, default=10, help="runs averaged for the dominant kernel's time")
     ap.add_argument("--traffic-runs", type=int, default=0,
                     help="instead of timing: run the dominant op alone this many times (for rocprofv3 --pmc)")
     ap.add_argument("--no-graphs", dest="graphs", action="store_false",
                     help="enqueue every kernel from the host instead of replaying each step as a HIP graph")
-    ap.add_argument("--workload", choices=("harmonic", "biquad", "stft", "membrane"), default="harmonic")
+    ap.add_argument("--workload", choices=("harmonic", "biquad", "stft", "membrane", "oscbank"), default="harmonic")
     ap.add_argument("--mem-steps", type=int, default=16, help="membrane frames per time-blocked launch")
     ap.add_argument("--chunk", type=int, default=256, help="biquad scan chunk length (frames)")
     args = ap.parse_args()
@@ -418,7 +474,8 @@ def main() -> int:
         print(f"bench.py: --gpus {args.gpus} is not supported: this backend runs on one GPU; the multi-GPU "
               f"design (lane sharding + one gradient all-reduce) is not built.", file=sys.stderr)
         return 2
-    run = {"biquad": run_biquad, "stft": run_stft, "membrane": run_membrane, "harmonic": run_harmonic}[args.workload]
+    run = {"biquad": run_biquad, "stft": run_stft, "membrane": run_membrane, "harmonic": run_harmonic,
+           "oscbank": run_oscbank}[args.workload]
     res = run(args)
     if res is not None:
         print(json.dumps(res), flush=True)

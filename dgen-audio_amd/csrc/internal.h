@@ -21,7 +21,14 @@ struct Launch {
   int device = 0;
   int cu_count = 256;
   bool dry = false;             // validate only
+  float host_sr = 0.f;          // host sample rate of this run; 0: each op's own
 };
+
+// Sample rate a phase increment divides by: the run's host sample rate when
+// one is set (u_phasor divides by hostSampleRate, Definitions.swift:96-102,
+// which the C backend takes from DGenProcessContextV1.sample_rate), else the
+// rate the op was rendered with.
+inline float host_rate(const Launch& L, float rendered) { return L.host_sr > 0.f ? L.host_sr : rendered; }
 
 // Thread-local last-error text; returns `code` for tail calls.
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));

@@ -387,7 +387,7 @@ int launch_phasor_carry(const Launch& L, const dgen_hip_op& op) {
   DGEN_CHECK_CELL(L, ck, nseg * B * K, "phasor_carry.checkpoints");
   DGEN_REQUIRE(nseg * B * K < (1ll << 29), "phasor_carry: %lld checkpoints (< 2^29)", (long long)(nseg * B * K));
   if (L.dry) return 0;
-  const float sr = op.farg[0], rsr = 1.0f / sr;
+  const float sr = host_rate(L, op.farg[0]), rsr = 1.0f / sr;
   hipLaunchKernelGGL(k_phasor_carry, dim3((unsigned)B), dim3(64 * kCarryWaves), 0, L.stream, cell(L, f0f),
                      cell(L, ck), (int)B, (int)K, (int)T, sr, rsr);
   DGEN_LAUNCH_CHECK("k_phasor_carry");
@@ -405,6 +405,7 @@ struct SynthArgs {
   const float* ckpt;
   int ldc, B, K, NF, F, T;
   float sr, rsr, hscale, nscale;
+  float nyq;  // half the graph's sample rate: the Nyquist mask (Synth.swift:158-167)
 };
 
 // Per-frame values of a segment, staged in LDS and read as broadcasts.
@@ -520,7 +521,7 @@ template <bool FAST>
 __device__ __forceinline__ void chain_regs(const SynthArgs& a, const SegLds& L, float (&v)[kSeg], int lane, int nt,
                                            float ph) {
   const float kf = (float)(lane + 1);
-  const float nyq = a.sr * 0.5f;
+  const float nyq = a.nyq;
   const bool harm = lane < a.K;
   const int kk = harm ? lane : 0;
 #pragma unroll
@@ -605,7 +606,7 @@ __global__ __launch_bounds__(64 * kWavesFwd) void k_synth_fwd(SynthArgs a, float
     const int t = t0 + lane;
     const FrameRec r = L.fr[lane];
     const int slo = r.slots & 255, shi = r.slots >> 8;
-    const int n = below_nyquist(r.f0, a.sr * 0.5f, a.K);
+    const int n = below_nyquist(r.f0, a.nyq, a.K);
     const float den = r.omf * L.pre[slo][n] + r.frac * L.pre[shi][n] + 1e-8f;
     const float hsum = num / den;
     const float gain = r.omf * L.row[slo][a.K] + r.frac * L.row[shi][a.K];
@@ -682,7 +683,7 @@ template <bool FAST>
 __device__ __forceinline__ void bwd_harmonic_pass(const SynthArgs& a, const SegLds& L, SlotAcc& acc, int lane,
                                                   int nt, float ph, int nidx_spare) {
   const float kf = (float)(lane + 1);
-  const float nyq = a.sr * 0.5f;
+  const float nyq = a.nyq;
   const bool harm = lane < a.K;
   const int n = FAST ? kSeg : nt;
   for (int i0 = 0; i0 < n; i0 += kBlk) {
@@ -910,8 +911,12 @@ static int synth_args(const Launch& L, const dgen_hip_op& op, SynthArgs& a, cons
   a.NF = (int)NF;
   a.F = (int)F;
   a.T = (int)T;
-  a.sr = op.farg[0];
+  // phase increments use the host sample rate (u_phasor divides by
+  // hostSampleRate, Definitions.swift:96-102); the Nyquist mask uses the
+  // graph's rate (DGenConfig.sampleRate, Synth.swift:158-167)
+  a.sr = host_rate(L, op.farg[0]);
   a.rsr = 1.0f / a.sr;
+  a.nyq = op.farg[0] * 0.5f;
   a.hscale = op.farg[1];
   a.nscale = op.farg[2];
   return 0;

@@ -2,100 +2,171 @@
 //
 // Signal.phasor(Tensor) lowers to the stateless deterministicPhasor
 // (Sources/DGenLazy/SignalTensor.swift:67-80, Sources/DGen/Emit+State.swift:
-// 370-387): phase = r - floor(r), r = (f / sr) * n, evaluated per frame, so
-// the oscillator sum is frame-parallel.  The history one-pole
-// y[n] = x[n] + pole * y[n-1] (Emit+State.swift:150-224) is a linear
-// recurrence; it is evaluated as a three-phase chunked scan: zero-state
-// chunk ends in parallel, a short sequential pass over chunk carries, then
-// every chunk re-runs its recurrence from the exact carry.  Within a chunk
-// the operation order is the reference's; only the carries are re-associated.
+// 370-387): phase = r - floor(r), r = (f / sr) * n with n the frame index in
+// this call, so the oscillator sum is frame-parallel.  The history one-pole
+// y[n] = x[n] + pole * y[n-1] (Emit+State.swift:150-224) is a first-order
+// linear recurrence, evaluated as a two-pass scan over 256-frame tiles:
+//   k_osc_tiles  one thread per frame: the oscillator sum, then the tile's
+//                zero-state response by a workgroup scan of the affine maps
+//                y -> pole*y + x[n]; writes it and the tile's map (pole^len,
+//                zero-state end);
+//   k_osc_apply  each workgroup composes the maps of the tiles before it
+//                (a workgroup scan over at most kMaxFusedTiles tiles) and adds
+//                pole^(i+1) * carry to its zero-state response.
+// Longer signals compose the tile maps in a single-workgroup pass
+// (k_osc_carries) between the two.  Every output store maps non-finite values
+// to 0 (CRenderer.swift:1021-1039).  The scan reassociates the recurrence's
+// fp32 sums; the oscillator sum keeps the reference's order over k.
 #pragma clang fp contract(off)
 
 #include "internal.h"
 
 namespace dgen {
 
-constexpr float kTwoPi = 2.0f * 3.14159265358979323846f;
-constexpr int kChunk = 256;
+constexpr int kTile = 256;             // frames per workgroup (one per thread)
+constexpr int kMaxFusedTiles = 1024;   // tiles k_osc_apply scans itself
+constexpr int kOscLds = 1024;          // oscillators staged in LDS per pass
 
-__global__ void k_osc_sum(const float* __restrict__ freqs, const float* __restrict__ amps, int nosc, float sr,
-                          int frames, float* __restrict__ x) {
-  const int n = blockIdx.x * blockDim.x + threadIdx.x;
-  if (n >= frames) return;
+// Affine map y -> a*y + b; compose(first, second) applies first, then second.
+struct Aff {
+  float a, b;
+};
+__device__ __forceinline__ Aff compose(Aff f, Aff s) { return Aff{f.a * s.a, s.a * f.b + s.b}; }
+
+// Inclusive scan of one map per thread over a 256-thread workgroup (four
+// waves): shuffles within each wave, then the wave totals through LDS.
+__device__ __forceinline__ Aff block_scan(Aff v, Aff* lds_tot) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    Aff u{__shfl_up(v.a, off, 64), __shfl_up(v.b, off, 64)};
+    if (lane >= off) v = compose(u, v);
+  }
+  if (lane == 63) lds_tot[w] = v;
+  __syncthreads();
+  Aff pre{1.f, 0.f};
+  for (int j = 0; j < w; ++j) pre = compose(pre, lds_tot[j]);
+  __syncthreads();
+  return w ? compose(pre, v) : v;
+}
+
+__global__ __launch_bounds__(kTile) void k_osc_tiles(const float* __restrict__ freqs, const float* __restrict__ amps,
+                                                     int nosc, float sr, int frames, float pole,
+                                                     float* __restrict__ zs, float2* __restrict__ tiles) {
+  __shared__ float s_inc[kOscLds], s_amp[kOscLds];
+  __shared__ Aff s_tot[kTile / 64];
+  const int n = blockIdx.x * kTile + threadIdx.x;
   const float fn = (float)n;
   float acc = 0.f;
-  for (int k = 0; k < nosc; ++k) {
-    const float inc = freqs[k] / sr;
-    const float r = inc * fn;
-    const float phase = r - floorf(r);
-    acc = acc + sinf(phase * kTwoPi) * amps[k];
+  for (int k0 = 0; k0 < nosc; k0 += kOscLds) {
+    const int kn = min(kOscLds, nosc - k0);
+    __syncthreads();
+    for (int k = threadIdx.x; k < kn; k += kTile) {
+      s_inc[k] = freqs[k0 + k] / sr;  // phaseIncrement = freq / sampleRate
+      s_amp[k] = amps[k0 + k];
+    }
+    __syncthreads();
+    for (int k = 0; k < kn; ++k) {
+      const float r = s_inc[k] * fn;
+      const float phase = r - floorf(r);
+      // sin(phase * 2pi): the transcendental unit takes revolutions
+      acc = acc + __builtin_amdgcn_sinf(phase) * s_amp[k];
+    }
   }
-  x[n] = acc;
+  const bool live = n < frames;
+  Aff v = block_scan(Aff{live ? pole : 1.f, live ? acc : 0.f}, s_tot);
+  if (live) zs[n] = v.b;
+  if (threadIdx.x == kTile - 1) tiles[blockIdx.x] = make_float2(v.a, v.b);
 }
 
-__global__ void k_onepole_ends(const float* __restrict__ x, float* __restrict__ ends, int frames, float pole) {
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  const int n0 = c * kChunk;
-  if (n0 >= frames) return;
-  const int n1 = min(frames, n0 + kChunk);
-  float z = 0.f;
-  for (int n = n0; n < n1; ++n) z = x[n] + pole * z;
-  ends[c] = z;
-}
-
-__global__ void k_onepole_carries(const float* __restrict__ ends, float* __restrict__ carry, int chunks, int frames,
-                                  float pole) {
-  if (blockIdx.x != 0 || threadIdx.x != 0) return;
-  float y = 0.f;
-  for (int c = 0; c < chunks; ++c) {
-    carry[c] = y;  // y[n0 - 1]
-    const int len = min(kChunk, frames - c * kChunk);
-    float pl = 1.f;
-    for (int i = 0; i < len; ++i) pl = pl * pole;
-    y = ends[c] + pl * y;
+// Carries of any number of tiles: one workgroup, blocks of 256 tile maps
+// scanned in parallel, the running carry composed block by block.
+__global__ __launch_bounds__(kTile) void k_osc_carries(const float2* __restrict__ tiles, float* __restrict__ carry,
+                                                       int ntiles) {
+  __shared__ Aff s_tot[kTile / 64];
+  __shared__ Aff s_inc[kTile];
+  float run = 0.f;  // y entering the block
+  for (int t0 = 0; t0 < ntiles; t0 += kTile) {
+    const int t = t0 + threadIdx.x;
+    const float2 m = t < ntiles ? tiles[t] : make_float2(1.f, 0.f);
+    const Aff inc = block_scan(Aff{m.x, m.y}, s_tot);
+    s_inc[threadIdx.x] = inc;
+    __syncthreads();
+    // carry into tile t: the maps of the block's tiles before t applied to `run`
+    const Aff ex = threadIdx.x ? s_inc[threadIdx.x - 1] : Aff{1.f, 0.f};
+    if (t < ntiles) carry[t] = ex.a * run + ex.b;
+    const Aff blk = s_inc[kTile - 1];
+    run = blk.a * run + blk.b;
+    __syncthreads();
   }
 }
 
-__global__ void k_onepole_apply(const float* __restrict__ x, const float* __restrict__ carry, float* __restrict__ out,
-                                int frames, float pole) {
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  const int n0 = c * kChunk;
-  if (n0 >= frames) return;
-  const int n1 = min(frames, n0 + kChunk);
-  float y = carry[c];
-  for (int n = n0; n < n1; ++n) {
-    y = x[n] + pole * y;
-    out[n] = isfinite(y) ? y : 0.f;
+template <bool FUSED>
+__global__ __launch_bounds__(kTile) void k_osc_apply(const float* __restrict__ zs, const float2* __restrict__ tiles,
+                                                     const float* __restrict__ carry, int frames, float pole,
+                                                     float* __restrict__ out) {
+  __shared__ Aff s_tot[kTile / 64];
+  __shared__ float s_carry;
+  const int g = blockIdx.x;
+  if constexpr (FUSED) {
+    // compose the maps of tiles 0 .. g-1 (g <= kMaxFusedTiles): four per thread
+    Aff v{1.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < kMaxFusedTiles / kTile; ++j) {
+      const int t = threadIdx.x * (kMaxFusedTiles / kTile) + j;
+      if (t < g) {
+        const float2 m = tiles[t];
+        v = compose(v, Aff{m.x, m.y});
+      }
+    }
+    v = block_scan(v, s_tot);
+    if (threadIdx.x == kTile - 1) s_carry = v.b;  // the composed maps applied to y[-1] = 0
+  } else {
+    if (threadIdx.x == 0) s_carry = carry[g];
   }
+  // pole^(i+1) for this thread's frame: the scan of the per-frame multipliers
+  Aff p = block_scan(Aff{pole, 0.f}, s_tot);
+  __syncthreads();
+  const int n = g * kTile + threadIdx.x;
+  if (n >= frames) return;
+  const float y = zs[n] + p.a * s_carry;
+  out[n] = isfinite(y) ? y : 0.f;
 }
 
 int launch_osc_bank(const Launch& L, const dgen_hip_op& op) {
-  // arg: [0]=freqs [1]=amps [2]=out [3]=n_osc [4]=frames [5]=workspace (frames + 2*chunks floats)
+  // arg: [0]=freqs [1]=amps [2]=out [3]=n_osc [4]=frames [5]=workspace
+  //      (frames + 1 + 3*tiles floats, tiles = ceil(frames/256), even cell)
   const int64_t fr = op.arg[0], am = op.arg[1], out = op.arg[2], nosc = op.arg[3], frames = op.arg[4],
                 ws = op.arg[5];
-  DGEN_REQUIRE(nosc > 0 && nosc <= 4096 && frames > 0 && frames <= (1 << 28), "osc_bank: n_osc %lld frames %lld",
-               (long long)nosc, (long long)frames);
-  const int64_t chunks = (frames + kChunk - 1) / kChunk;
+  DGEN_REQUIRE(nosc > 0 && nosc <= 65536 && frames > 0 && frames <= (1 << 28),
+               "osc_bank: n_osc %lld frames %lld", (long long)nosc, (long long)frames);
+  const int64_t tiles_cap = (frames + kTile - 1) / kTile;
   DGEN_CHECK_CELL(L, fr, nosc, "osc_bank.freqs");
   DGEN_CHECK_CELL(L, am, nosc, "osc_bank.amps");
   DGEN_CHECK_CELL(L, out, frames, "osc_bank.out");
-  DGEN_CHECK_CELL(L, ws, frames + 2 * chunks, "osc_bank.workspace");
+  DGEN_CHECK_CELL(L, ws, frames + 1 + 3 * tiles_cap, "osc_bank.workspace");
+  DGEN_REQUIRE(ws % 2 == 0, "osc_bank: workspace cell must be 8-byte aligned");
   if (L.dry) return 0;
-  float* x = cell(L, ws);
-  float* ends = x + frames;
-  float* carry = ends + chunks;
-  const float sr = op.farg[0], pole = op.farg[1];
-  hipLaunchKernelGGL(k_osc_sum, dim3((unsigned)((frames + 255) / 256)), dim3(256), 0, L.stream, cell(L, fr),
-                     cell(L, am), (int)nosc, sr, (int)frames, x);
-  DGEN_LAUNCH_CHECK("k_osc_sum");
-  hipLaunchKernelGGL(k_onepole_ends, dim3((unsigned)((chunks + 63) / 64)), dim3(64), 0, L.stream, x, ends,
-                     (int)frames, pole);
-  DGEN_LAUNCH_CHECK("k_onepole_ends");
-  hipLaunchKernelGGL(k_onepole_carries, dim3(1), dim3(64), 0, L.stream, ends, carry, (int)chunks, (int)frames, pole);
-  DGEN_LAUNCH_CHECK("k_onepole_carries");
-  hipLaunchKernelGGL(k_onepole_apply, dim3((unsigned)((chunks + 63) / 64)), dim3(64), 0, L.stream, x, carry,
-                     cell(L, out), (int)frames, pole);
-  DGEN_LAUNCH_CHECK("k_onepole_apply");
+  // a run of frame_count frames computes the first frame_count outputs
+  const int64_t n = std::min<int64_t>(frames, L.frames ? (int64_t)L.frames : frames);
+  const int64_t tiles = (n + kTile - 1) / kTile;
+  float* zs = cell(L, ws);
+  float2* tl = reinterpret_cast<float2*>(cell(L, ws) + ((frames + 1) & ~int64_t(1)));
+  float* carry = reinterpret_cast<float*>(tl + tiles_cap);
+  const float sr = host_rate(L, op.farg[0]), pole = op.farg[1];
+  hipLaunchKernelGGL(k_osc_tiles, dim3((unsigned)tiles), dim3(kTile), 0, L.stream, cell(L, fr), cell(L, am),
+                     (int)nosc, sr, (int)n, pole, zs, tl);
+  DGEN_LAUNCH_CHECK("k_osc_tiles");
+  if (tiles <= kMaxFusedTiles) {
+    hipLaunchKernelGGL(k_osc_apply<true>, dim3((unsigned)tiles), dim3(kTile), 0, L.stream, zs, tl, nullptr, (int)n,
+                       pole, cell(L, out));
+  } else {
+    hipLaunchKernelGGL(k_osc_carries, dim3(1), dim3(kTile), 0, L.stream, tl, carry, (int)tiles);
+    DGEN_LAUNCH_CHECK("k_osc_carries");
+    hipLaunchKernelGGL(k_osc_apply<false>, dim3((unsigned)tiles), dim3(kTile), 0, L.stream, zs, tl, carry, (int)n,
+                       pole, cell(L, out));
+  }
+  DGEN_LAUNCH_CHECK("k_osc_apply");
   return 0;
 }
 

@@ -95,6 +95,10 @@ struct dgen_hip_ctx {
   bool use_graphs = false;
   hipGraphExec_t graph = nullptr;
   uint32_t graph_frames = 0;
+  // host sample rate of the runs (dgen_hip_set_sample_rate; 0: each op's own)
+  float host_sr = 0.f;
+  // output cells (dgen_hip_set_outputs), downloaded by every dgen_hip_run
+  uint64_t out_off = 0, out_n = 0;
 };
 
 static int set_device(dgen_hip_ctx* c) {
@@ -111,6 +115,7 @@ static Launch make_launch(dgen_hip_ctx* c, hipStream_t s, uint32_t frames, bool 
   L.device = c->device;
   L.cu_count = c->cu_count;
   L.dry = dry;
+  L.host_sr = c->host_sr;
   return L;
 }
 
@@ -127,6 +132,7 @@ static void release_arena(dgen_hip_ctx* c) {
   c->d_arena = nullptr;
   c->h_arena = nullptr;
   c->floats = 0;
+  c->out_off = c->out_n = 0;
   c->configured = false;
 }
 
@@ -342,10 +348,52 @@ int dgen_hip_zero(dgen_hip_ctx* c, uint64_t off, uint64_t n) {
   return run_static(c);
 }
 
+// The frame-count argument of each per-run kernel class (index into
+// op.arg; -1: no frame dimension) and whether the class runs any frame_count
+// up to it (the first frame_count frames, as the reference's kernels loop
+// over [0, frameCount) of cells sized for maxFrameCount) or only the frame
+// count it was rendered for (its static tables, tiles and normalisation are
+// laid out for that count).
+struct FrameArg {
+  int index;
+  bool prefix;
+};
+static FrameArg frame_arg(uint32_t k) {
+  switch (k) {
+    case DGEN_HIP_K_PHASOR_CARRY: return {4, false};
+    case DGEN_HIP_K_SYNTH_FWD:
+    case DGEN_HIP_K_SYNTH_BWD: return {10, false};
+    case DGEN_HIP_K_SPECTRAL_LOSS: return {4, false};
+    case DGEN_HIP_K_SPECTRAL_GATHER: return {3, false};
+    case DGEN_HIP_K_SYNTH_BWD_REDUCE: return {6, false};
+    case DGEN_HIP_K_OSC_BANK: return {4, true};
+    case DGEN_HIP_K_LERP_FRAMES: return {5, false};
+    case DGEN_HIP_K_BIQUAD_CHUNK: return {5, false};
+    case DGEN_HIP_K_BIQUAD_FWD: return {6, false};
+    case DGEN_HIP_K_BIQUAD_ADJ_CHUNK: return {6, false};
+    case DGEN_HIP_K_BIQUAD_BWD: return {8, false};
+    case DGEN_HIP_K_STFT_FWD: return {7, false};
+    case DGEN_HIP_K_STFT_BWD: return {5, false};
+    case DGEN_HIP_K_MEMBRANE_FWD: return {6, false};
+    case DGEN_HIP_K_MEMBRANE_BWD: return {9, false};
+    default: return {-1, false};
+  }
+}
+
 static int run_checks(dgen_hip_ctx* c, uint32_t frame_count) {
   if (!c || !c->configured) return fail(DGEN_HIP_E_STATE, "run: context not configured");
-  if (frame_count > c->max_frames)
-    return fail(DGEN_HIP_E_RANGE, "run: frame_count %u > max_frames %u", frame_count, c->max_frames);
+  if (frame_count == 0 || frame_count > c->max_frames)
+    return fail(DGEN_HIP_E_RANGE, "run: frame_count %u outside [1, max_frames %u]", frame_count, c->max_frames);
+  for (size_t i = 0; i < c->ops.size(); ++i) {
+    const dgen_hip_op& op = c->ops[i];
+    if (op.flags & DGEN_HIP_OP_STATIC) continue;
+    const FrameArg fa = frame_arg(op.kernel);
+    if (fa.index < 0) continue;
+    const int64_t T = op.arg[fa.index];
+    if (fa.prefix ? (int64_t)frame_count > T : (int64_t)frame_count != T)
+      return fail(DGEN_HIP_E_RANGE, "run: op %zu (kernel %u) is rendered for %lld frames; frame_count %u %s", i,
+                  op.kernel, (long long)T, frame_count, fa.prefix ? "exceeds it" : "must equal it");
+  }
   return set_device(c);
 }
 
@@ -395,7 +443,39 @@ int dgen_hip_run(dgen_hip_ctx* c, uint32_t frame_count) {
     if (c) (void)dgen_hip_sync(c);
     return rc;
   }
-  return dgen_hip_sync(c);
+  if ((rc = dgen_hip_sync(c))) return rc;
+  // outputs are host-visible on return, as the reference's shared-storage
+  // outputs buffer is after run() (MetalRuntime.swift:232, 334-337)
+  return c->out_n ? dgen_hip_download(c, c->out_off, c->out_n) : 0;
+}
+
+int dgen_hip_set_outputs(dgen_hip_ctx* c, uint64_t off, uint64_t n) {
+  int rc = range_ok(c, off, n, "set_outputs");
+  if (rc) return rc;
+  c->out_off = off;
+  c->out_n = n;
+  return 0;
+}
+
+float* dgen_hip_host_outputs(dgen_hip_ctx* c, uint64_t* n_out) {
+  if (n_out) *n_out = (c && c->configured) ? c->out_n : 0;
+  if (!c || !c->configured || !c->out_n) return nullptr;
+  return c->h_arena + c->out_off;
+}
+
+int dgen_hip_set_sample_rate(dgen_hip_ctx* c, float sample_rate) {
+  if (!c) return fail(DGEN_HIP_E_INVALID, "set_sample_rate: null context");
+  // 0 restores each op's rendered rate; otherwise a rate the phase kernels'
+  // reciprocal-product division is exact for (normal quotients on [1, 1e7] Hz)
+  if (!(sample_rate == 0.f || (sample_rate >= 1.f && sample_rate <= 1e7f)))
+    return fail(DGEN_HIP_E_INVALID, "set_sample_rate: %g Hz outside [1, 1e7] (or 0)", (double)sample_rate);
+  int rc = set_device(c);
+  if (rc) return rc;
+  DGEN_HIP_TRY(hipStreamSynchronize(c->s0));
+  DGEN_HIP_TRY(hipStreamSynchronize(c->s1));
+  if (sample_rate != c->host_sr) drop_graph(c);  // captured launches hold the old rate
+  c->host_sr = sample_rate;
+  return 0;
 }
 
 int dgen_hip_profile(dgen_hip_ctx* c, uint32_t frame_count, dgen_hip_kernel_time* out, size_t cap, size_t* n_out) {

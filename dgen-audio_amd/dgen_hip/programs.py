@@ -39,10 +39,12 @@ def oscbank_program(cfg: OscBankConfig) -> Program:
     freqs = p.alloc("freqs", cfg.n_osc)
     amps = p.alloc("amps", cfg.n_osc)
     out = p.alloc("out", cfg.frames)
-    chunks = (cfg.frames + 255) // 256
-    ws = p.alloc("workspace", cfg.frames + 2 * chunks)
+    tiles = (cfg.frames + 255) // 256
+    ws = p.alloc("workspace", cfg.frames + 1 + 3 * tiles)
+    # per output sample: n_osc x (divide-free phase 4 + sin ~20 + mul-add 2) + the one-pole 2
     p.add(R.K_OSC_BANK, [freqs, amps, out, cfg.n_osc, cfg.frames, ws], [cfg.sr, cfg.pole], label="osc_bank",
-          dispatch=f"perFrame({cfg.frames}) + chunked scan")
+          dispatch=f"perFrame({cfg.frames}) + tile scan", bytes=4.0 * cfg.frames + 8.0 * cfg.n_osc,
+          flops=float(cfg.frames) * (26.0 * cfg.n_osc + 2.0), bound="valu")
     p.output_cell = "out"
     return p
 
@@ -545,10 +547,13 @@ def membrane_program(cfg: MembraneConfig, train: bool = True, optimizer: bool = 
     out = p.alloc("pickup", T)
     S = p.alloc("states", (T + 2) * G)
     cell_steps = float(G) * T
-    # per cell-step: read u_n and u_{n-1}, write u_{n+1} (12 B); ~10 flops
+    # Compulsory HBM traffic of the store-every-state design: the forward
+    # writes each state once (4 B per cell-step) for the adjoint, which reads
+    # each once (4 B); the two fields a step reads and the adjoint fields
+    # stay on chip inside a time-blocked launch.  ~10 flops per cell-step.
     p.add(R.K_MEMBRANE_FWD, [S, u0, P, out, rows, cols, T, py, px, steps], label="membrane_fwd",
           dispatch=f"{(T + steps - 1) // steps} time-blocked launches x {tiles} tiles",
-          bytes=12.0 * cell_steps, flops=10.0 * cell_steps)
+          bytes=4.0 * cell_steps, flops=10.0 * cell_steps)
     if not train:
         p.output_cell = "pickup"
         return p
@@ -559,10 +564,10 @@ def membrane_program(cfg: MembraneConfig, train: bool = True, optimizer: bool = 
     loss = p.alloc("loss", 1)
     Gc = p.alloc("grads", 2)
     ws = p.alloc("colsum_ws", _colsum_ws(T, 1))
-    # per cell-step: read lambda_{n+1}, lambda_{n+2}, u_n, u_{n-1}, write lambda_n (20 B); ~14 flops
+    # per cell-step: the stored state read once (4 B); ~14 flops
     p.add(R.K_MEMBRANE_BWD, [S, P, out, tgt, lam, gpart, lt, rows, cols, T, py, px, steps, Gc], label="membrane_bwd",
           dispatch=f"{T // steps + 1} time-blocked adjoint launches x {tiles} tiles",
-          bytes=20.0 * cell_steps, flops=14.0 * cell_steps)
+          bytes=4.0 * cell_steps, flops=14.0 * cell_steps)
     p.add(R.K_COLSUM, [lt, loss, T, 1, 1, ws], label="loss_sum", dispatch="chunkPartialsReduceToCell",
           bytes=(T + 1) * f4, flops=float(T))
     if optimizer:

@@ -61,7 +61,8 @@ EXPORTED_SYMBOLS = (
     "dgen_hip_abi_version", "dgen_hip_device_count", "dgen_hip_create", "dgen_hip_destroy",
     "dgen_hip_last_error", "dgen_hip_configure", "dgen_hip_host_memory", "dgen_hip_upload",
     "dgen_hip_download", "dgen_hip_zero", "dgen_hip_run", "dgen_hip_run_async", "dgen_hip_sync", "dgen_hip_set_graphs",
-    "dgen_hip_profile", "dgen_hip_time_runs", "dgen_hip_time_op", "dgen_hip_run_op",
+    "dgen_hip_profile", "dgen_hip_time_runs", "dgen_hip_time_op", "dgen_hip_run_op", "dgen_hip_set_outputs",
+    "dgen_hip_host_outputs", "dgen_hip_set_sample_rate",
 )
 
 
@@ -111,6 +112,9 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "dgen_hip_time_runs": ([vp, u32, i32, i32, ctypes.POINTER(ctypes.c_double)], i32),
         "dgen_hip_time_op": ([vp, u32, u32, i32, ctypes.POINTER(ctypes.c_double)], i32),
         "dgen_hip_run_op": ([vp, u32, u32], i32),
+        "dgen_hip_set_outputs": ([vp, u64, u64], i32),
+        "dgen_hip_host_outputs": ([vp, ctypes.POINTER(u64)], ctypes.POINTER(ctypes.c_float)),
+        "dgen_hip_set_sample_rate": ([vp, ctypes.c_float], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -167,28 +171,46 @@ class HIPLazyRuntime:
                "dgen_hip_configure")
         ptr = self.L.dgen_hip_host_memory(ctx)
         self._host = np.ctypeslib.as_array(ptr, shape=(program.size,))
+        if program.output_cell:
+            c = program.cells[program.output_cell]
+            _check(self.L.dgen_hip_set_outputs(ctx, c.off, c.n), "dgen_hip_set_outputs")
 
     # -- LazyRuntime protocol -------------------------------------------
     def zeroAllBuffers(self) -> None:
         _check(self.L.dgen_hip_zero(self._ctx, 0, 0), "dgen_hip_zero")
         self._host[:] = 0.0
 
+    def _frames(self, frameCount: int | None) -> int:
+        """None means the frame count the program was rendered for; any
+        other value goes to the library as is (it rejects what the schedule
+        cannot run, 0 included)."""
+        return self.program.max_frames if frameCount is None else int(frameCount)
+
     def runNoCopy(self, frameCount: int | None = None) -> None:
-        _check(self.L.dgen_hip_run(self._ctx, frameCount or self.program.max_frames), "dgen_hip_run")
+        _check(self.L.dgen_hip_run(self._ctx, self._frames(frameCount)), "dgen_hip_run")
 
     def memoryPointer(self) -> np.ndarray:
         return self._host
 
     def outputsPointer(self) -> np.ndarray:
-        c = self.program.cells[self.program.output_cell]
-        self.download(self.program.output_cell)
-        return self._host[c.off:c.off + c.n]
+        """The output cells in the host mirror, as the last run left them
+        (dgen_hip_run copies them back; dgen_hip_host_outputs)."""
+        n = ctypes.c_uint64(0)
+        ptr = self.L.dgen_hip_host_outputs(self._ctx, ctypes.byref(n))
+        if not ptr or n.value == 0:
+            raise HIPError("the program declares no output cells")
+        return np.ctypeslib.as_array(ptr, shape=(n.value,))
+
+    def setSampleRate(self, sample_rate: float) -> None:
+        """Host sample rate of later runs (0: the rendered rate); the
+        DGenProcessContextV1.sample_rate of the reference's C backend."""
+        _check(self.L.dgen_hip_set_sample_rate(self._ctx, float(sample_rate)), "dgen_hip_set_sample_rate")
 
     def profileKernels(self, frameCount: int | None = None) -> list[KernelTiming]:
         cap = len(self.program.ops)
         buf = (CKernelTime * max(1, cap))()
         n = ctypes.c_size_t(0)
-        _check(self.L.dgen_hip_profile(self._ctx, frameCount or self.program.max_frames, buf, cap,
+        _check(self.L.dgen_hip_profile(self._ctx, self._frames(frameCount), buf, cap,
                                        ctypes.byref(n)), "dgen_hip_profile")
         out = []
         for i in range(min(n.value, cap)):
@@ -220,26 +242,26 @@ class HIPLazyRuntime:
         _check(self.L.dgen_hip_set_graphs(self._ctx, 1 if enable else 0), "dgen_hip_set_graphs")
 
     def run_async(self, frameCount: int | None = None) -> None:
-        _check(self.L.dgen_hip_run_async(self._ctx, frameCount or self.program.max_frames), "dgen_hip_run_async")
+        _check(self.L.dgen_hip_run_async(self._ctx, self._frames(frameCount)), "dgen_hip_run_async")
 
     def sync(self) -> None:
         _check(self.L.dgen_hip_sync(self._ctx), "dgen_hip_sync")
 
     def time_runs(self, warmup: int, iters: int, frameCount: int | None = None) -> float:
         ms = ctypes.c_double(0.0)
-        _check(self.L.dgen_hip_time_runs(self._ctx, frameCount or self.program.max_frames, warmup, iters,
+        _check(self.L.dgen_hip_time_runs(self._ctx, self._frames(frameCount), warmup, iters,
                                          ctypes.byref(ms)), "dgen_hip_time_runs")
         return ms.value
 
     def time_op(self, index: int, iters: int, frameCount: int | None = None) -> float:
         ms = ctypes.c_double(0.0)
-        _check(self.L.dgen_hip_time_op(self._ctx, frameCount or self.program.max_frames, index, iters,
+        _check(self.L.dgen_hip_time_op(self._ctx, self._frames(frameCount), index, iters,
                                        ctypes.byref(ms)), "dgen_hip_time_op")
         return ms.value
 
     def run_op(self, index: int, frameCount: int | None = None) -> None:
         """Run schedule op `index` alone on the current cell contents."""
-        _check(self.L.dgen_hip_run_op(self._ctx, frameCount or self.program.max_frames, index), "dgen_hip_run_op")
+        _check(self.L.dgen_hip_run_op(self._ctx, self._frames(frameCount), index), "dgen_hip_run_op")
 
     def close(self) -> None:
         if getattr(self, "_ctx", None):

@@ -32,14 +32,14 @@
 extern "C" {
 #endif
 
-#define DGEN_HIP_ABI_VERSION 1
+#define DGEN_HIP_ABI_VERSION 2
 
 /* ---- status codes ------------------------------------------------------ */
 #define DGEN_HIP_OK 0
 #define DGEN_HIP_E_INVALID (-1)   /* bad argument / shape / offset        */
 #define DGEN_HIP_E_DEVICE (-2)    /* HIP runtime error                    */
 #define DGEN_HIP_E_STATE (-3)     /* call out of order (e.g. run before configure) */
-#define DGEN_HIP_E_RANGE (-4)     /* frame_count > max_frames, cell out of arena */
+#define DGEN_HIP_E_RANGE (-4)     /* frame count not runnable, cell out of arena */
 #define DGEN_HIP_E_NOMEM (-5)     /* device or pinned allocation failed   */
 
 typedef struct dgen_hip_ctx dgen_hip_ctx;
@@ -329,11 +329,39 @@ int dgen_hip_zero(dgen_hip_ctx* ctx, uint64_t off, uint64_t n);
 
 /* Enqueue every non-static op in schedule order and wait for completion
  * (runNoCopy -> run, MetalRuntime.swift:283-342,676-698: synchronous on
- * return).  Fails with DGEN_HIP_E_RANGE if frame_count > max_frames. */
+ * return); then the output cells (dgen_hip_set_outputs) are copied to the
+ * host mirror.
+ * frame_count must lie in [1, max_frames].  Each op is rendered for a frame
+ * count (its frame argument): the oscillator bank runs the first frame_count
+ * frames of it (the reference's kernels loop over [0, frameCount) of cells
+ * sized for maxFrameCount), every other frame-indexed class only the exact
+ * count it was rendered for (its static tables, tiles and loss normalisation
+ * are laid out for that count).  Any other frame_count fails with
+ * DGEN_HIP_E_RANGE before anything is enqueued. */
 int dgen_hip_run(dgen_hip_ctx* ctx, uint32_t frame_count);
 /* As dgen_hip_run but returns without waiting; dgen_hip_sync waits. */
 int dgen_hip_run_async(dgen_hip_ctx* ctx, uint32_t frame_count);
 int dgen_hip_sync(dgen_hip_ctx* ctx);
+
+/* Declare the output cells [off, off+n) of the schedule: every dgen_hip_run
+ * copies them to the host mirror after the run, and dgen_hip_host_outputs
+ * returns where they are (LazyRuntime.outputsPointer, Realize.swift:17;
+ * MetalCompiledKernel's host-visible outputs buffer, MetalRuntime.swift:
+ * 232-254).  n = 0 declares none.  Reset by dgen_hip_configure. */
+int dgen_hip_set_outputs(dgen_hip_ctx* ctx, uint64_t off, uint64_t n);
+/* Host pointer of the declared output cells (NULL if none); *n_out (if not
+ * NULL) receives their float count.  Valid until the next configure/destroy. */
+float* dgen_hip_host_outputs(dgen_hip_ctx* ctx, uint64_t* n_out);
+
+/* Host sample rate of later runs, in Hz: the divisor of every phase
+ * increment (u_phasor divides by hostSampleRate, Definitions.swift:96-102;
+ * the C backend reads it from DGenProcessContextV1.sample_rate,
+ * CRenderer.swift:357-359, defaulting to the graph's rate,
+ * Realize.swift:246-252).  Rates the graph itself fixes (the synth's
+ * Nyquist mask, Synth.swift:158-167) keep the rendered value.  0 restores
+ * the rate each op was rendered with; otherwise [1, 1e7].  Drops a captured
+ * graph. */
+int dgen_hip_set_sample_rate(dgen_hip_ctx* ctx, float sample_rate);
 
 /* Graph replay of runs (enable != 0): the per-run schedule for a frame count
  * is captured once from both streams into a HIP graph and every later

@@ -264,7 +264,7 @@ void dgen_oracle_phase_checkpoints(const float* f0f, int B, int K, int T, float 
  * sampleInline gradient scatter, Emit+RowSelection.swift:100-141; f0, uv and
  * noise are data and carry no gradient). */
 static void synth_core(const REAL* ctrl, const float* f0, const float* uv, int B, int F, int T, int K, int NF,
-                       float sr, float hscale, float nscale, REAL* y, const REAL* dy, REAL* dctrl) {
+                       float sr, float graph_sr, float hscale, float nscale, REAL* y, const REAL* dy, REAL* dctrl) {
   const int NC = K + 2 + NF;
   REAL* play = (REAL*)malloc(sizeof(REAL) * T);
   float* noise = (float*)malloc(sizeof(float) * T);
@@ -275,7 +275,10 @@ static void synth_core(const REAL* ctrl, const float* f0, const float* uv, int B
   playhead_real(F, T, play);
   dgen_oracle_noise_stream(T, noise);
   if (dctrl) memset(dctrl, 0, sizeof(REAL) * (size_t)B * F * NC);
-  const float nyq = sr * 0.5f;
+  /* phase increments divide by the host sample rate (u_phasor,
+   * Definitions.swift:96-102); the Nyquist mask uses the graph's
+   * DGenConfig.sampleRate (Synth.swift:158-167) */
+  const float nyq = graph_sr * 0.5f;
   for (int t = 0; t < T; ++t) {
     RowLerp r = row_lerp((float)play[t], F);
     for (int b = 0; b < B; ++b) {
@@ -362,7 +365,21 @@ void FN(dgen_oracle_synth_fwd)(const float* ctrl, const float* f0, const float* 
   size_t nc = (size_t)B * F * (K + 2 + NF);
   REAL* c = to_real(ctrl, nc);
   REAL* yr = (REAL*)malloc(sizeof(REAL) * (size_t)B * T);
-  synth_core(c, f0, uv, B, F, T, K, NF, sr, hscale, nscale, yr, NULL, NULL);
+  synth_core(c, f0, uv, B, F, T, K, NF, sr, sr, hscale, nscale, yr, NULL, NULL);
+  to_float(yr, (size_t)B * T, y);
+  free(c);
+  free(yr);
+}
+
+/* The forward with a host sample rate (phase increments) that differs from
+ * the graph's (the Nyquist mask): dgen_process_v1's context.sample_rate
+ * against DGenConfig.sampleRate. */
+void FN(dgen_oracle_synth_fwd_rates)(const float* ctrl, const float* f0, const float* uv, int B, int F, int T, int K,
+                                     int NF, float host_sr, float graph_sr, float hscale, float nscale, float* y) {
+  size_t nc = (size_t)B * F * (K + 2 + NF);
+  REAL* c = to_real(ctrl, nc);
+  REAL* yr = (REAL*)malloc(sizeof(REAL) * (size_t)B * T);
+  synth_core(c, f0, uv, B, F, T, K, NF, host_sr, graph_sr, hscale, nscale, yr, NULL, NULL);
   to_float(yr, (size_t)B * T, y);
   free(c);
   free(yr);
@@ -374,7 +391,7 @@ void FN(dgen_oracle_synth_bwd)(const float* ctrl, const float* f0, const float* 
   REAL* c = to_real(ctrl, nc);
   REAL* d = to_real(dy, (size_t)B * T);
   REAL* dc = (REAL*)malloc(sizeof(REAL) * nc);
-  synth_core(c, f0, uv, B, F, T, K, NF, sr, hscale, nscale, NULL, d, dc);
+  synth_core(c, f0, uv, B, F, T, K, NF, sr, sr, hscale, nscale, NULL, d, dc);
   to_float(dc, nc, dctrl);
   free(c);
   free(d);
@@ -787,14 +804,14 @@ double FN(dgen_oracle_harmonic_step)(const float* X, const REAL* P, const float*
   REAL* tr = to_real(tgt, (size_t)B * T);
   REAL* lf = (REAL*)malloc(sizeof(REAL) * T);
   mlp_forward(X, P, M, din, hid, layers, K, NF, NULL, NULL, ctrl);
-  synth_core(ctrl, f0, uv, B, F, T, K, NF, sr, hscale, nscale, y, NULL, NULL);
+  synth_core(ctrl, f0, uv, B, F, T, K, NF, sr, sr, hscale, nscale, y, NULL, NULL);
   if (y_out) to_float(y, (size_t)B * T, y_out);
   double tot;
   if (dP) {
     REAL* dy = (REAL*)malloc(sizeof(REAL) * (size_t)B * T);
     REAL* dc = (REAL*)malloc(sizeof(REAL) * (size_t)M * NC);
     tot = mss_core(y, tr, B, T, sizes, n_sizes, hop_div, w_lin, w_log, max_frames, lf, dy);
-    synth_core(ctrl, f0, uv, B, F, T, K, NF, sr, hscale, nscale, NULL, dy, dc);
+    synth_core(ctrl, f0, uv, B, F, T, K, NF, sr, sr, hscale, nscale, NULL, dy, dc);
     mlp_backward(X, P, dc, M, din, hid, layers, K, NF, dP);
     free(dy);
     free(dc);

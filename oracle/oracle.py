@@ -48,6 +48,7 @@ def lib(name: str = "liboracle.so") -> ctypes.CDLL:
             syn = [_f32p, _f32p, _f32p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_float, _c_float, _f32p]
             _sig(L, "dgen_oracle_synth_fwd" + sfx, syn)
             _sig(L, "dgen_oracle_synth_bwd" + sfx, syn[:3] + [_f32p] + syn[3:])
+            _sig(L, "dgen_oracle_synth_fwd_rates" + sfx, syn[:9] + [_c_float] + syn[9:])
             _sig(L, "dgen_oracle_mlp_param_count" + sfx, [_c_int] * 4, _c_size)
             _sig(L, "dgen_oracle_mlp_fwd" + sfx, [_f32p, _f32p] + [_c_int] * 6 + [_f32p])
             _sig(L, "dgen_oracle_mlp_bwd" + sfx, [_f32p, _f32p, _f32p] + [_c_int] * 6 + [_f32p])
@@ -139,6 +140,14 @@ def phase_checkpoints(f0f, B, K, T, sr, seg=64):
 def synth_fwd(ctrl, f0, uv, B, F, T, K, NF, sr, hscale=1.0, nscale=1.0, prec="f32", libname="liboracle.so"):
     y = np.zeros((B, T), np.float32)
     _fn("dgen_oracle_synth_fwd", prec, libname)(_f(ctrl), _f(f0), _f(uv), B, F, T, K, NF, sr, hscale, nscale, y)
+    return y
+
+
+def synth_fwd_rates(ctrl, f0, uv, B, F, T, K, NF, host_sr, graph_sr, hscale=1.0, nscale=1.0, prec="f32"):
+    """Synth forward with phase increments over host_sr and the Nyquist mask at graph_sr / 2."""
+    y = np.zeros((B, T), np.float32)
+    _fn("dgen_oracle_synth_fwd_rates", prec)(_f(ctrl), _f(f0), _f(uv), B, F, T, K, NF, host_sr, graph_sr, hscale,
+                                              nscale, y)
     return y
 
 

@@ -40,9 +40,13 @@ def test_kernel_class_ids_match_header():
 
 def test_errors_are_status_codes_not_aborts():
     L = dgen_hip.load_library()
-    assert L.dgen_hip_abi_version() == 1
+    assert L.dgen_hip_abi_version() == 2
     rc = L.dgen_hip_run(None, 16)
     assert rc == -3 and b"not configured" in L.dgen_hip_last_error()
+    assert L.dgen_hip_set_outputs(None, 0, 4) == -3
+    n = ctypes.c_uint64(7)
+    assert not L.dgen_hip_host_outputs(None, ctypes.byref(n)) and n.value == 0
+    assert L.dgen_hip_set_sample_rate(None, 44100.0) == -1
     rc = L.dgen_hip_configure(None, None, 0, 0, 0)
     assert rc == -1 and L.dgen_hip_last_error()
     n = ctypes.c_int(-1)

@@ -29,6 +29,9 @@ def test_exhaustive_for_workload_rates(checker):
 
 
 def test_sampled_for_common_rates(checker):
-    rates = ["8000", "11025", "22050", "24000", "32000", "48000", "88200", "96000", "192000", "1000", "4"]
+    # common rates, the ends of the host-rate range dgen_hip_set_sample_rate
+    # accepts ([1, 1e7] Hz) and a few arbitrary ones
+    rates = ["8000", "11025", "22050", "24000", "32000", "48000", "88200", "96000", "192000", "1000", "4", "1",
+             "10000000", "12345.678", "37011.5", "44099.99"]
     rc, res = run(checker, "sample", *rates)
     assert rc == 0 and all(v == 0 for v in res.values()) and len(res) == len(rates)

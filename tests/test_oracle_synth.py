@@ -221,3 +221,32 @@ def test_non_finite_control_row_zeroes_exactly_the_frames_that_read_it():
     inf[0 * F + 0, K] = np.inf
     yi = O.synth_fwd(inf, f0, uv, B, F, T, K, NF, SR)
     assert np.all(yi[0][(lo == 0) | (hi == 0)] == 0.0)
+
+
+def test_host_rate_drives_the_phase_and_graph_rate_the_nyquist_mask():
+    # dgen_process_v1's context.sample_rate divides the phase increments
+    # (u_phasor / hostSampleRate); the mask compares with the graph's
+    # DGenConfig.sampleRate / 2.  f0 = 4000: harmonics 4000, 8000, 12000 Hz.
+    B, F, T, K, NF = 1, 4, 256, 3, 5
+    c = _ctrl(B, F, K, NF, amps=[1.0, 1.0, 1.0], gain=1.0)
+    f0, uv = _data(B, F, 4000.0)
+    f0i = _f0_frames(f0, B, F, T)[0]
+
+    def sines(rate, k):
+        freq = (np.float32(k) * f0i).astype(np.float32)
+        return np.sin(2.0 * np.pi * O.phasor(freq, rate).astype(np.float64)), freq
+
+    # graph rate 16 kHz masks harmonics 2 and 3 wherever 2*f0 is exactly 8000
+    y = O.synth_fwd_rates(c, f0, uv, B, F, T, K, NF, 32000.0, 16000.0)[0].astype(np.float64)
+    s1, _ = sines(32000.0, 1)
+    s2, fr2 = sines(32000.0, 2)
+    on = fr2 == np.float32(8000.0)
+    assert on.sum() > T // 2
+    assert np.abs(y[on] - s1[on]).max() < 2e-6
+    # graph rate 32 kHz keeps harmonics 1..3 (all below 16 kHz)
+    y2 = O.synth_fwd_rates(c, f0, uv, B, F, T, K, NF, 32000.0, 32000.0)[0].astype(np.float64)
+    ref2 = (s1 + s2 + sines(32000.0, 3)[0]) / 3.0
+    assert np.abs(y2 - ref2).max() < 2e-6
+    # equal rates reduce to the plain forward
+    assert np.array_equal(O.synth_fwd_rates(c, f0, uv, B, F, T, K, NF, SR, SR), O.synth_fwd(c, f0, uv, B, F, T, K,
+                                                                                            NF, SR))
