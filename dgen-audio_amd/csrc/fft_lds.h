@@ -46,6 +46,33 @@ __device__ __forceinline__ c2 mul_mi(c2 a) { return INV ? c2{-a.y, a.x} : c2{a.y
 // exp(sgn * 2 pi i * rev), rev in revolutions (v_cos/v_sin take revolutions)
 __device__ __forceinline__ c2 cis(float rev) { return {__builtin_amdgcn_cosf(rev), __builtin_amdgcn_sinf(rev)}; }
 
+// Twiddle sources of the passes.  A pass of radix R and span NS multiplies
+// input r of butterfly k by W^(r k) with W = exp(-+2 pi i / (NS R)).
+// - HwTwiddle: W^1 from the hardware sin/cos (about 2 ulp), higher powers by
+//   complex products (up to six for radix 8);
+// - TableTwiddle: every power read from a table of correctly rounded values
+//   t[i] = exp(-2 pi i i / N), i < N/2 = M (the last radix-2 stage's row of
+//   the reference's Float twiddle table, HigherOps.swift:84-91), as
+//   W_M^e = W_N^(2e) = +-t[2e mod M].  The products' rounding compounds in
+//   windows whose spectrum spans many decades (the spectral loss's
+//   log-magnitude gradient amplifies it), so the spectral loss uses tables.
+struct HwTwiddle {
+  static constexpr bool kTable = false;
+  __device__ __forceinline__ c2 get(int) const { return {1.f, 0.f}; }
+};
+struct TableTwiddle {
+  static constexpr bool kTable = true;
+  const c2* t;  // M values, in LDS
+  int m;
+  // W_M^e for 0 <= e < M (forward sign)
+  __device__ __forceinline__ c2 get(int e) const {
+    const int i = 2 * e;
+    const bool hi = i >= m;
+    const c2 w = t[hi ? i - m : i];
+    return hi ? c2{-w.x, -w.y} : w;
+  }
+};
+
 template <bool INV>
 __device__ __forceinline__ void dft2(c2* v) {
   const c2 a = v[0], b = v[1];
@@ -100,24 +127,37 @@ __host__ __device__ constexpr int pass_span(int logm, int p) {
 // One Stockham pass over this thread's 8 values v (already read): twiddle,
 // R-point DFTs, and the output positions.  j = thread index within the
 // window; butterfly u of the thread is bj = j + u*M/8.
-template <int M, int R, int NS, bool INV>
-__device__ __forceinline__ void pass_compute(c2* v, int j, int* outpos) {
+// The twiddles of input r (1 <= r < R) of butterfly k: w[r] *= W^(r k).
+template <int M, int R, int NS, bool INV, class TW>
+__device__ __forceinline__ void twiddle(c2* w, int k, const TW& tw) {
+  if constexpr (TW::kTable) {
+    constexpr int S = M / (NS * R);  // W = W_M^S; r k S < M
+#pragma unroll
+    for (int r = 1; r < R; ++r) {
+      const c2 t = tw.get(r * k * S);
+      w[r] = cmul(w[r], INV ? cconj(t) : t);
+    }
+  } else {
+    const float rev = (INV ? 1.0f : -1.0f) * (float)k / (float)(NS * R);
+    const c2 t1 = cis(rev);
+    c2 t = t1;
+#pragma unroll
+    for (int r = 1; r < R; ++r) {
+      w[r] = cmul(w[r], t);
+      if (r + 1 < R) t = cmul(t, t1);
+    }
+  }
+}
+
+template <int M, int R, int NS, bool INV, class TW = HwTwiddle>
+__device__ __forceinline__ void pass_compute(c2* v, int j, int* outpos, const TW& tw = TW{}) {
   constexpr int BPT = 8 / R;
 #pragma unroll
   for (int u = 0; u < BPT; ++u) {
     const int bj = j + u * (M / 8);
     const int k = bj % NS;
     c2* w = v + u * R;
-    if (NS > 1) {
-      const float rev = (INV ? 1.0f : -1.0f) * (float)k / (float)(NS * R);
-      const c2 t1 = cis(rev);
-      c2 t = t1;
-#pragma unroll
-      for (int r = 1; r < R; ++r) {
-        w[r] = cmul(w[r], t);
-        if (r + 1 < R) t = cmul(t, t1);
-      }
-    }
+    if (NS > 1) twiddle<M, R, NS, INV>(w, k, tw);
     dftR<R, INV>(w);
     const int base = (bj / NS) * NS * R + k;
 #pragma unroll
@@ -134,8 +174,8 @@ __device__ __forceinline__ int in_pos(int j, int e) {
 
 // Middle passes 1 .. npass-2 in LDS (in place; a barrier separates each
 // pass's reads from its writes).
-template <int LOGM, int P, bool INV, bool WAVE = false>
-__device__ __forceinline__ void mid_passes(PadBuf buf, int j, c2* v) {
+template <int LOGM, int P, bool INV, bool WAVE = false, class TW = HwTwiddle>
+__device__ __forceinline__ void mid_passes(PadBuf buf, int j, c2* v, const TW& tw = TW{}) {
   constexpr int M = 1 << LOGM;
   if constexpr (P < pass_count(LOGM) - 1) {
     constexpr int R = pass_radix(LOGM, P), NS = pass_span(LOGM, P);
@@ -143,35 +183,35 @@ __device__ __forceinline__ void mid_passes(PadBuf buf, int j, c2* v) {
     for (int e = 0; e < 8; ++e) v[e] = buf[in_pos<M, R>(j, e)];
     lds_sync<WAVE>();
     int op[8];
-    pass_compute<M, R, NS, INV>(v, j, op);
+    pass_compute<M, R, NS, INV>(v, j, op, tw);
 #pragma unroll
     for (int e = 0; e < 8; ++e) buf[op[e]] = v[e];
     lds_sync<WAVE>();
-    mid_passes<LOGM, P + 1, INV, WAVE>(buf, j, v);
+    mid_passes<LOGM, P + 1, INV, WAVE>(buf, j, v, tw);
   }
 }
 
 // Full M-point FFT: v holds the first pass's inputs (v[e] = input at
 // in_pos of pass 0); on return v holds the last pass's outputs at positions
 // op[e].  Uses buf (M complex, this window's slot) between passes.
-template <int LOGM, bool INV, bool WAVE = false>
-__device__ __forceinline__ void fft(PadBuf buf, int j, c2* v, int* op) {
+template <int LOGM, bool INV, bool WAVE = false, class TW = HwTwiddle>
+__device__ __forceinline__ void fft(PadBuf buf, int j, c2* v, int* op, const TW& tw = TW{}) {
   constexpr int M = 1 << LOGM;
   constexpr int NP = pass_count(LOGM);
   {
     constexpr int R = pass_radix(LOGM, 0);
-    pass_compute<M, R, 1, INV>(v, j, op);
+    pass_compute<M, R, 1, INV>(v, j, op, tw);
   }
   if constexpr (NP > 1) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) buf[op[e]] = v[e];
     lds_sync<WAVE>();
-    mid_passes<LOGM, 1, INV, WAVE>(buf, j, v);
+    mid_passes<LOGM, 1, INV, WAVE>(buf, j, v, tw);
     constexpr int RL = pass_radix(LOGM, NP - 1), NSL = pass_span(LOGM, NP - 1);
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = buf[in_pos<M, RL>(j, e)];
     lds_sync<WAVE>();
-    pass_compute<M, RL, NSL, INV>(v, j, op);
+    pass_compute<M, RL, NSL, INV>(v, j, op, tw);
   }
 }
 
@@ -179,8 +219,8 @@ __device__ __forceinline__ void fft(PadBuf buf, int j, c2* v, int* op) {
 // b in buffers bufa and bufb): each pass's twiddles, positions and LDS round
 // trip serve both, and the two butterflies give the scheduler independent
 // work.  Each signal's arithmetic is exactly that of fft().
-template <int M, int R, int NS, bool INV>
-__device__ __forceinline__ void pass_compute2(c2* va, c2* vb, int j, int* outpos) {
+template <int M, int R, int NS, bool INV, class TW = HwTwiddle>
+__device__ __forceinline__ void pass_compute2(c2* va, c2* vb, int j, int* outpos, const TW& tw = TW{}) {
   constexpr int BPT = 8 / R;
 #pragma unroll
   for (int u = 0; u < BPT; ++u) {
@@ -189,14 +229,25 @@ __device__ __forceinline__ void pass_compute2(c2* va, c2* vb, int j, int* outpos
     c2* wa = va + u * R;
     c2* wb = vb + u * R;
     if (NS > 1) {
-      const float rev = (INV ? 1.0f : -1.0f) * (float)k / (float)(NS * R);
-      const c2 t1 = cis(rev);
-      c2 t = t1;
+      if constexpr (TW::kTable) {
+        constexpr int S = M / (NS * R);
 #pragma unroll
-      for (int r = 1; r < R; ++r) {
-        wa[r] = cmul(wa[r], t);
-        wb[r] = cmul(wb[r], t);
-        if (r + 1 < R) t = cmul(t, t1);
+        for (int r = 1; r < R; ++r) {
+          const c2 t0 = tw.get(r * k * S);
+          const c2 t = INV ? cconj(t0) : t0;
+          wa[r] = cmul(wa[r], t);
+          wb[r] = cmul(wb[r], t);
+        }
+      } else {
+        const float rev = (INV ? 1.0f : -1.0f) * (float)k / (float)(NS * R);
+        const c2 t1 = cis(rev);
+        c2 t = t1;
+#pragma unroll
+        for (int r = 1; r < R; ++r) {
+          wa[r] = cmul(wa[r], t);
+          wb[r] = cmul(wb[r], t);
+          if (r + 1 < R) t = cmul(t, t1);
+        }
       }
     }
     dftR<R, INV>(wa);
@@ -207,8 +258,8 @@ __device__ __forceinline__ void pass_compute2(c2* va, c2* vb, int j, int* outpos
   }
 }
 
-template <int LOGM, int P, bool INV, bool WAVE>
-__device__ __forceinline__ void mid_passes2(PadBuf bufa, PadBuf bufb, int j, c2* va, c2* vb) {
+template <int LOGM, int P, bool INV, bool WAVE, class TW = HwTwiddle>
+__device__ __forceinline__ void mid_passes2(PadBuf bufa, PadBuf bufb, int j, c2* va, c2* vb, const TW& tw = TW{}) {
   constexpr int M = 1 << LOGM;
   if constexpr (P < pass_count(LOGM) - 1) {
     constexpr int R = pass_radix(LOGM, P), NS = pass_span(LOGM, P);
@@ -219,26 +270,26 @@ __device__ __forceinline__ void mid_passes2(PadBuf bufa, PadBuf bufb, int j, c2*
     }
     lds_sync<WAVE>();
     int op[8];
-    pass_compute2<M, R, NS, INV>(va, vb, j, op);
+    pass_compute2<M, R, NS, INV>(va, vb, j, op, tw);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       bufa[op[e]] = va[e];
       bufb[op[e]] = vb[e];
     }
     lds_sync<WAVE>();
-    mid_passes2<LOGM, P + 1, INV, WAVE>(bufa, bufb, j, va, vb);
+    mid_passes2<LOGM, P + 1, INV, WAVE>(bufa, bufb, j, va, vb, tw);
   }
 }
 
 // fft() of two signals at once: on return va / vb hold their last pass's
 // outputs at positions op[e].
-template <int LOGM, bool INV, bool WAVE = false>
-__device__ __forceinline__ void fft2(PadBuf bufa, PadBuf bufb, int j, c2* va, c2* vb, int* op) {
+template <int LOGM, bool INV, bool WAVE = false, class TW = HwTwiddle>
+__device__ __forceinline__ void fft2(PadBuf bufa, PadBuf bufb, int j, c2* va, c2* vb, int* op, const TW& tw = TW{}) {
   constexpr int M = 1 << LOGM;
   constexpr int NP = pass_count(LOGM);
   {
     constexpr int R = pass_radix(LOGM, 0);
-    pass_compute2<M, R, 1, INV>(va, vb, j, op);
+    pass_compute2<M, R, 1, INV>(va, vb, j, op, tw);
   }
   if constexpr (NP > 1) {
 #pragma unroll
@@ -247,7 +298,7 @@ __device__ __forceinline__ void fft2(PadBuf bufa, PadBuf bufb, int j, c2* va, c2
       bufb[op[e]] = vb[e];
     }
     lds_sync<WAVE>();
-    mid_passes2<LOGM, 1, INV, WAVE>(bufa, bufb, j, va, vb);
+    mid_passes2<LOGM, 1, INV, WAVE>(bufa, bufb, j, va, vb, tw);
     constexpr int RL = pass_radix(LOGM, NP - 1), NSL = pass_span(LOGM, NP - 1);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -255,7 +306,7 @@ __device__ __forceinline__ void fft2(PadBuf bufa, PadBuf bufb, int j, c2* va, c2
       vb[e] = bufb[in_pos<M, RL>(j, e)];
     }
     lds_sync<WAVE>();
-    pass_compute2<M, RL, NSL, INV>(va, vb, j, op);
+    pass_compute2<M, RL, NSL, INV>(va, vb, j, op, tw);
   }
 }
 

@@ -45,7 +45,7 @@ struct MssArgs {
   const float* tgt;
   float* part;                     // [B][ntiles][kAcc]
   float* wloss[kMaxSizes];         // per size: [nwin][B][2] (lin, log)
-  const float* hann[kMaxSizes];    // per size: symmetric Hann table [N] (double-evaluated)
+  const float* hann[kMaxSizes];    // per size: DGEN_HIP_K_FFT_TABLES output (Hann [N], cos [N-1], sin [N-1])
   int logn[kMaxSizes];
   int nsizes, B, T, ntiles;
   float gl, gg;                    // upstream gradient of each window's lin / log sum
@@ -58,19 +58,26 @@ __device__ __forceinline__ float hw_sqrt(float v) { return __builtin_amdgcn_sqrt
 __device__ __forceinline__ float hw_log(float v) { return __builtin_amdgcn_logf(v) * 0.69314718055994531f; }
 __device__ __forceinline__ float hw_rcp(float v) { return __builtin_amdgcn_rcpf(v); }
 
+// LDS of one size's launch, sized for that size (smaller sizes fit more
+// workgroups per CU).
+template <int LOGN>
 struct MssLds {
-  float acc[kAcc];                 // dx of samples [a - kHalo, a + kTile)
+  static constexpr int N = 1 << LOGN, M = N / 2;
+  static constexpr int kAccN = kTile + N;  // dx of samples [a - (N-1), a + kTile), + 1 pad (even length)
+  float acc[kAccN];
   c2 buf[lds_pad(2048)];           // FFT slots: (4096/N windows) x (N/2), padded
   c2 aux[lds_pad(2048)];           // second signal's spectrum / gradient spectrum
   float red[kThreads / 64][2];
-  float hann[2048];                // this size's window
+  float hann[N];                   // this size's window
+  c2 tw[M];                        // exp(-2 pi i k / N), k < N/2, correctly rounded
 };
 
 // One FFT size: 4 groups of 4096/N windows, windows in a group 4 hops apart.
 template <int LOGN>
-__device__ __forceinline__ void mss_size(const MssArgs& a, MssLds& L, int si, int b, int tile) {
+__device__ __forceinline__ void mss_size(const MssArgs& a, MssLds<LOGN>& L, int si, int b, int tile) {
   constexpr int N = 1 << LOGN, M = N / 2, LOGM = LOGN - 1, H = N / 4, P = M / 8, W = kThreads / P;
   static_assert(W * M == 2048, "window slots must fill the FFT buffer");
+  const TableTwiddle tw{L.tw, M};
   // a window's P threads (and its FFT slots) lie in one wave when P <= 64:
   // its transforms and bins then need only wave-level ordering; the
   // workgroup barrier is kept for the shared accumulator (windows of
@@ -87,14 +94,27 @@ __device__ __forceinline__ void mss_size(const MssArgs& a, MssLds& L, int si, in
   {
     // all of the thread's loads in flight before any LDS write (a loop that
     // stored each load as it arrived waited out one memory latency per
-    // iteration)
+    // iteration).  The size's table cell holds hann[N] | cos[N-1] | sin[N-1]
+    // in the reference's radix-2 layout (stage with half-size h at h-1): the
+    // last stage's row is cos, sin(2 pi k / N), k < N/2.
     constexpr int HP = (N + kThreads - 1) / kThreads;
-    float hv[HP];
+    constexpr int TP = (M + kThreads - 1) / kThreads;
+    const float* tab = a.hann[si];
+    float hv[HP], cv[TP], sv[TP];
 #pragma unroll
-    for (int q = 0; q < HP; ++q) hv[q] = a.hann[si][min(tid + q * kThreads, N - 1)];
+    for (int q = 0; q < HP; ++q) hv[q] = tab[min(tid + q * kThreads, N - 1)];
+#pragma unroll
+    for (int q = 0; q < TP; ++q) {
+      const int k = min(tid + q * kThreads, M - 1);
+      cv[q] = tab[N + (M - 1) + k];
+      sv[q] = tab[2 * N - 1 + (M - 1) + k];
+    }
 #pragma unroll
     for (int q = 0; q < HP; ++q)
       if (tid + q * kThreads < N) L.hann[tid + q * kThreads] = hv[q];
+#pragma unroll
+    for (int q = 0; q < TP; ++q)
+      if (tid + q * kThreads < M) L.tw[tid + q * kThreads] = c2{cv[q], -sv[q]};
   }
   lds_barrier();
   // window samples of group g for this thread: element e of the first pass
@@ -131,11 +151,11 @@ __device__ __forceinline__ void mss_size(const MssArgs& a, MssLds& L, int si, in
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int n = in_pos<M, pass_radix(LOGM, 0)>(j, e);
-        const float h0 = L.hann[2 * n], h1 = L.hann[2 * n + 1];
-        vt[e] = c2{pt[2 * e] * h0, pt[2 * e + 1] * h1};
-        v[e] = c2{px[2 * e] * h0, px[2 * e + 1] * h1};
+        const float2 h = *reinterpret_cast<const float2*>(&L.hann[2 * n]);
+        vt[e] = c2{pt[2 * e] * h.x, pt[2 * e + 1] * h.y};
+        v[e] = c2{px[2 * e] * h.x, px[2 * e + 1] * h.y};
       }
-      fft2<LOGM, false, WL>(spec, buf, j, vt, v, op);
+      fft2<LOGM, false, WL>(spec, buf, j, vt, v, op, tw);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         spec[op[e]] = vt[e];
@@ -153,7 +173,7 @@ __device__ __forceinline__ void mss_size(const MssArgs& a, MssLds& L, int si, in
         const c2 ox = {0.5f * (zx.y + zxm.y), 0.5f * (zxm.x - zx.x)};
         const c2 et = {0.5f * (zt.x + ztm.x), 0.5f * (zt.y - ztm.y)};
         const c2 ot = {0.5f * (zt.y + ztm.y), 0.5f * (ztm.x - zt.x)};
-        const c2 wk = cis(-(float)k / (float)N);  // W_N^k
+        const c2 wk = L.tw[k];  // W_N^k (k <= N/4)
         const c2 wox = cmul(wk, ox), wot = cmul(wk, ot);
         // X_k = E + W^k O ; X_{M-k} = conj(E - W^k O)   (k = 0: X_0 and X_M)
         c2 X[2] = {cadd(ex, wox), cconj(csub(ex, wox))};
@@ -252,31 +272,34 @@ __device__ __forceinline__ void mss_size(const MssArgs& a, MssLds& L, int si, in
     // ---- real-output inverse transform and windowed overlap-add
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = spec[in_pos<M, pass_radix(LOGM, 0)>(j, e)];
-    fft<LOGM, true, WL>(buf, j, v, op);
+    fft<LOGM, true, WL>(buf, j, v, op, tw);
     // each accumulator element of a group belongs to one thread (the group's
     // windows are disjoint), so all of the thread's reads are issued before
-    // its adds and writes; out-of-range samples read a clamped element and
-    // are not written
+    // its adds and writes.  Output pair e holds samples t, t+1 with
+    // t = s0 + 2 op[e]; t - (a0 - (N-1)) = f - a0 + 2 op[e] is even, so the
+    // pair is one 8-byte LDS access.  Pairs outside the tile's range read a
+    // clamped element and are not written; a pair with one sample outside
+    // [0, T) writes only the other.
     {
-      float ac[16];
-      int ai[16];
-      bool aw[16];
+      constexpr int kAccN = MssLds<LOGN>::kAccN;
+      float2 ac[8];
+      int ai[8];
+      bool a0w[8], a1w[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int t = s0 + 2 * op[e] + h;
-          aw[2 * e + h] = live && t >= 0 && t < a.T;
-          ai[2 * e + h] = min(max(t - (a0 - kHalo), 0), kAcc - 1);
-          ac[2 * e + h] = L.acc[ai[2 * e + h]];
-        }
+        const int t = s0 + 2 * op[e];
+        a0w[e] = live && t >= 0 && t < a.T;
+        a1w[e] = live && t + 1 >= 0 && t + 1 < a.T;
+        ai[e] = min(max(t - (a0 - (N - 1)), 0), kAccN - 2);
+        ac[e] = *reinterpret_cast<const float2*>(&L.acc[ai[e]]);
       }
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int n0 = 2 * op[e];
-        const float h0 = L.hann[n0], h1 = L.hann[n0 + 1];
-        if (aw[2 * e]) L.acc[ai[2 * e]] = ac[2 * e] + v[e].x * h0;
-        if (aw[2 * e + 1]) L.acc[ai[2 * e + 1]] = ac[2 * e + 1] + v[e].y * h1;
+        const float2 h = *reinterpret_cast<const float2*>(&L.hann[2 * op[e]]);
+        const float2 r = {ac[e].x + v[e].x * h.x, ac[e].y + v[e].y * h.y};
+        if (a0w[e] && a1w[e]) *reinterpret_cast<float2*>(&L.acc[ai[e]]) = r;
+        else if (a0w[e]) L.acc[ai[e]] = r.x;
+        else if (a1w[e]) L.acc[ai[e] + 1] = r.y;
       }
     }
     // every wave's overlap-add of group g lands before any of group g + 1
@@ -289,33 +312,39 @@ __device__ __forceinline__ void mss_size(const MssArgs& a, MssLds& L, int si, in
 // tile partials between launches, which run in the op's size order.
 template <int LOGN>
 __global__ __launch_bounds__(kThreads) void k_mss(MssArgs a, int si, int first) {
-  extern __shared__ float smem[];
-  MssLds& L = *reinterpret_cast<MssLds*>(smem);
+  extern __shared__ float4 smem4[];
+  MssLds<LOGN>& L = *reinterpret_cast<MssLds<LOGN>*>(smem4);
+  constexpr int N = 1 << LOGN;
+  constexpr int kSpan = kTile + N - 1;  // samples [a - (N-1), a + kTile) of the tile row
+  constexpr int kOff = kHalo - (N - 1);  // their place in the row of kAcc
   const int tile = blockIdx.x, b = blockIdx.y;
   float* part = a.part + ((size_t)b * a.ntiles + tile) * kAcc;
   {
     // the tile partials: every load in flight before the LDS writes
-    constexpr int AP = (kAcc + kThreads - 1) / kThreads;
+    constexpr int AP = (kSpan + kThreads - 1) / kThreads;
     float av[AP];
     if (first) {
 #pragma unroll
       for (int q = 0; q < AP; ++q) av[q] = 0.f;
     } else {
 #pragma unroll
-      for (int q = 0; q < AP; ++q) av[q] = part[min((int)threadIdx.x + q * kThreads, kAcc - 1)];
+      for (int q = 0; q < AP; ++q) av[q] = part[kOff + min((int)threadIdx.x + q * kThreads, kSpan - 1)];
     }
 #pragma unroll
     for (int q = 0; q < AP; ++q)
-      if ((int)threadIdx.x + q * kThreads < kAcc) L.acc[threadIdx.x + q * kThreads] = av[q];
+      if ((int)threadIdx.x + q * kThreads < kSpan) L.acc[threadIdx.x + q * kThreads] = av[q];
   }
   lds_barrier();
   mss_size<LOGN>(a, L, si, b, tile);
-  for (int i = threadIdx.x; i < kAcc; i += kThreads) part[i] = L.acc[i];
+  for (int i = threadIdx.x; i < kSpan; i += kThreads) part[kOff + i] = L.acc[i];
+  // the first size also clears the row's part left of its own halo
+  if (first)
+    for (int i = threadIdx.x; i < kOff; i += kThreads) part[i] = 0.f;
 }
 
 int launch_spectral_loss(const Launch& L, const dgen_hip_op& op) {
   // arg: [0]=x ([B][T]) [1]=target ([B][T]) [2]=tile partials ([B][ntiles][6143]) [3]=B [4]=T [5]=n_sizes
-  //      [6..13]=N_s [14..21]=per-window loss cells ([nwin_s][B][2]) [22..29]=Hann tables ([N_s])
+  //      [6..13]=N_s [14..21]=per-window loss cells ([nwin_s][B][2]) [22..29]=FFT tables ([3 N_s - 2])
   // farg: [0]=lin upstream grad per window [1]=log upstream grad per window
   const int64_t x = op.arg[0], tgt = op.arg[1], part = op.arg[2], B = op.arg[3], T = op.arg[4], ns = op.arg[5];
   DGEN_REQUIRE(B > 0 && B <= 65535 && T > 0 && T <= (1 << 26) && ns >= 1 && ns <= kMaxSizes,
@@ -333,7 +362,7 @@ int launch_spectral_loss(const Launch& L, const dgen_hip_op& op) {
                  (long long)n);
     const int64_t nwin = (T + n / 4 - 1) / (n / 4);
     DGEN_CHECK_CELL(L, op.arg[14 + s], nwin * B * 2, "spectral_loss.window_loss");
-    DGEN_CHECK_CELL(L, op.arg[22 + s], n, "spectral_loss.hann");
+    DGEN_CHECK_CELL(L, op.arg[22 + s], 3 * n - 2, "spectral_loss.fft_tables");
     a.logn[s] = lg;
     if (!L.dry) {
       a.wloss[s] = cell(L, op.arg[14 + s]);
@@ -354,12 +383,12 @@ int launch_spectral_loss(const Launch& L, const dgen_hip_op& op) {
   for (int s = 0; s < ns; ++s) {
     const int first = s == 0;
     switch (a.logn[s]) {
-      case 6: hipLaunchKernelGGL(k_mss<6>, grid, dim3(kThreads), sizeof(MssLds), L.stream, a, s, first); break;
-      case 7: hipLaunchKernelGGL(k_mss<7>, grid, dim3(kThreads), sizeof(MssLds), L.stream, a, s, first); break;
-      case 8: hipLaunchKernelGGL(k_mss<8>, grid, dim3(kThreads), sizeof(MssLds), L.stream, a, s, first); break;
-      case 9: hipLaunchKernelGGL(k_mss<9>, grid, dim3(kThreads), sizeof(MssLds), L.stream, a, s, first); break;
-      case 10: hipLaunchKernelGGL(k_mss<10>, grid, dim3(kThreads), sizeof(MssLds), L.stream, a, s, first); break;
-      default: hipLaunchKernelGGL(k_mss<11>, grid, dim3(kThreads), sizeof(MssLds), L.stream, a, s, first); break;
+      case 6: hipLaunchKernelGGL(k_mss<6>, grid, dim3(kThreads), sizeof(MssLds<6>), L.stream, a, s, first); break;
+      case 7: hipLaunchKernelGGL(k_mss<7>, grid, dim3(kThreads), sizeof(MssLds<7>), L.stream, a, s, first); break;
+      case 8: hipLaunchKernelGGL(k_mss<8>, grid, dim3(kThreads), sizeof(MssLds<8>), L.stream, a, s, first); break;
+      case 9: hipLaunchKernelGGL(k_mss<9>, grid, dim3(kThreads), sizeof(MssLds<9>), L.stream, a, s, first); break;
+      case 10: hipLaunchKernelGGL(k_mss<10>, grid, dim3(kThreads), sizeof(MssLds<10>), L.stream, a, s, first); break;
+      default: hipLaunchKernelGGL(k_mss<11>, grid, dim3(kThreads), sizeof(MssLds<11>), L.stream, a, s, first); break;
     }
     DGEN_LAUNCH_CHECK("k_mss");
   }

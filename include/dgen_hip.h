@@ -107,7 +107,8 @@ enum dgen_hip_kernel {
    * arg: [0]=x ([B][T]) [1]=target ([B][T]) [2]=tile partials
    *      ([B][ceil(T/4096)][6143]) [3]=B [4]=T [5]=n_sizes [6..13]=N_s
    *      [14..21]=window-loss cells ([ceil(T/hop)][B][2])
-   *      [22..29]=Hann tables (DGEN_HIP_K_FFT_TABLES output, first N floats)
+   *      [22..29]=FFT tables (DGEN_HIP_K_FFT_TABLES output, 3N-2 floats: the
+   *      window and the transforms' twiddles)
    * farg: [0]=lin upstream grad per window (w_lin/nsizes/maxFrames/B)
    *       [1]=log upstream grad per window */
   DGEN_HIP_K_SPECTRAL_LOSS = 7,
