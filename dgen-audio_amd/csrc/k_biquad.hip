@@ -30,6 +30,8 @@
 // Layout: x, y, tgt are [T][B] (frame-major, lane-minor: a wave reads 256
 // contiguous bytes per frame); parameters are [2][B] = base | Q; the cutoff
 // of lane k at frame n is base[k] * m[n] (m: the shared modulation signal).
+#include <mutex>
+
 #include "internal.h"
 
 namespace dgen {
@@ -440,6 +442,33 @@ double* dcell(const Launch& L, int64_t off) { return reinterpret_cast<double*>(c
 
 dim3 bq_grid(const BqShape& s) { return dim3((unsigned)s.C, (unsigned)((s.B + kThreads - 1) / kThreads)); }
 
+// Enqueue the three passes of the forward on raw device pointers (shared by
+// the schedule's launchers and the no-allocation entry point).
+void bq_enqueue_chunk(hipStream_t st, const float* x, const float* mod, const float* prm, double* summ,
+                      const BqShape& s) {
+  if (mod)
+    hipLaunchKernelGGL(k_bq_chunk<true>, bq_grid(s), dim3(kThreads), 0, st, x, mod, prm, summ, (int)s.B, (int)s.T,
+                       (int)s.L);
+  else
+    hipLaunchKernelGGL(k_bq_chunk<false>, bq_grid(s), dim3(kThreads), 0, st, x, nullptr, prm, summ, (int)s.B,
+                       (int)s.T, (int)s.L);
+}
+void bq_enqueue_carry(hipStream_t st, const double* summ, float* init, int64_t B, int64_t C, int rev) {
+  hipLaunchKernelGGL(k_bq_carry, dim3((unsigned)((B + kCarryLanes - 1) / kCarryLanes)),
+                     dim3(kCarryLanes * kCarryGroups), 0, st, summ, init, (int)B, (int)C, rev);
+}
+void bq_enqueue_fwd(hipStream_t st, const float* x, const float* m, const float* prm, const float* init, float* y,
+                    const float* t, float* lp, const BqShape& s) {
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, bq_grid(s), dim3(kThreads), 0, st, x, m, prm, init, y, t, lp, (int)s.B, (int)s.T,
+                       (int)s.L);
+  };
+  if (m && t) go(k_bq_fwd<true, true>);
+  else if (m) go(k_bq_fwd<true, false>);
+  else if (t) go(k_bq_fwd<false, true>);
+  else go(k_bq_fwd<false, false>);
+}
+
 }  // namespace
 
 int launch_biquad_chunk(const Launch& L, const dgen_hip_op& op) {
@@ -452,12 +481,7 @@ int launch_biquad_chunk(const Launch& L, const dgen_hip_op& op) {
   DGEN_CHECK_CELL(L, summ, 12 * s.C * s.B, "biquad_chunk.summary");
   DGEN_REQUIRE(summ % 2 == 0, "biquad_chunk: summary cell must be 8-byte aligned");
   if (L.dry) return 0;
-  if (mod >= 0)
-    hipLaunchKernelGGL(k_bq_chunk<true>, bq_grid(s), dim3(kThreads), 0, L.stream, cell(L, x), cell(L, mod),
-                       cell(L, prm), dcell(L, summ), (int)s.B, (int)s.T, (int)s.L);
-  else
-    hipLaunchKernelGGL(k_bq_chunk<false>, bq_grid(s), dim3(kThreads), 0, L.stream, cell(L, x), nullptr, cell(L, prm),
-                       dcell(L, summ), (int)s.B, (int)s.T, (int)s.L);
+  bq_enqueue_chunk(L.stream, cell(L, x), mod >= 0 ? cell(L, mod) : nullptr, cell(L, prm), dcell(L, summ), s);
   DGEN_LAUNCH_CHECK("k_bq_chunk");
   return 0;
 }
@@ -470,9 +494,7 @@ int launch_biquad_carry(const Launch& L, const dgen_hip_op& op) {
   DGEN_REQUIRE(summ % 2 == 0, "biquad_carry: summary cell must be 8-byte aligned");
   DGEN_CHECK_CELL(L, init, 2 * C * B, "biquad_carry.init");
   if (L.dry) return 0;
-  hipLaunchKernelGGL(k_bq_carry, dim3((unsigned)((B + kCarryLanes - 1) / kCarryLanes)),
-                     dim3(kCarryLanes * kCarryGroups), 0, L.stream, dcell(L, summ), cell(L, init), (int)B, (int)C,
-                     (int)rev);
+  bq_enqueue_carry(L.stream, dcell(L, summ), cell(L, init), B, C, (int)rev);
   DGEN_LAUNCH_CHECK("k_bq_carry");
   return 0;
 }
@@ -493,17 +515,8 @@ int launch_biquad_fwd(const Launch& L, const dgen_hip_op& op) {
     DGEN_CHECK_CELL(L, lossp, s.C * s.B, "biquad_fwd.loss_partials");
   }
   if (L.dry) return 0;
-  const float* m = mod >= 0 ? cell(L, mod) : nullptr;
-  float* t = tgt >= 0 ? cell(L, tgt) : nullptr;
-  float* lp = lossp >= 0 ? cell(L, lossp) : nullptr;
-  auto go = [&](auto kern) {
-    hipLaunchKernelGGL(kern, bq_grid(s), dim3(kThreads), 0, L.stream, cell(L, x), m, cell(L, prm), cell(L, init),
-                       cell(L, y), t, lp, (int)s.B, (int)s.T, (int)s.L);
-  };
-  if (m && t) go(k_bq_fwd<true, true>);
-  else if (m) go(k_bq_fwd<true, false>);
-  else if (t) go(k_bq_fwd<false, true>);
-  else go(k_bq_fwd<false, false>);
+  bq_enqueue_fwd(L.stream, cell(L, x), mod >= 0 ? cell(L, mod) : nullptr, cell(L, prm), cell(L, init), cell(L, y),
+                 tgt >= 0 ? cell(L, tgt) : nullptr, lossp >= 0 ? cell(L, lossp) : nullptr, s);
   DGEN_LAUNCH_CHECK("k_bq_fwd");
   return 0;
 }
@@ -553,4 +566,72 @@ int launch_biquad_bwd(const Launch& L, const dgen_hip_op& op) {
   return 0;
 }
 
+// ---- the bank forward without allocation -----------------------------------
+// The chunk summaries ([C][6][B] fp64) and chunk initial states ([C][2][B]
+// fp32) of dgen_hip_biquad_forward_noalloc live in this fixed device array
+// (each GPU the library runs on holds its own copy until the process ends).
+// Host code never passes the array's name to a kernel: it is a host-side
+// stand-in, not a device address.  Each device's address comes from
+// hipGetSymbolAddress on that call's first use of the device, with the
+// device current.
+constexpr int64_t kNoAllocScratchBytes = 16ll << 20;
+static __device__ __align__(256) double scratch[kNoAllocScratchBytes / sizeof(double)];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+int scratch_on(int device, void** out) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(DGEN_HIP_E_DEVICE, "biquad_forward_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", device,
+                  hipGetErrorString(e));
+    g_scratch_ptr[device] = p;
+  }
+  *out = g_scratch_ptr[device];
+  return 0;
+}
+}  // namespace
+
 }  // namespace dgen
+
+extern "C" int dgen_hip_biquad_forward_noalloc(int device, const float* x, const float* mod, const float* params,
+                                               float* y, uint32_t B, uint32_t T, uint32_t chunk, void* stream) {
+  using namespace dgen;
+  if (!x || !params || !y) return fail(DGEN_HIP_E_INVALID, "biquad_forward_noalloc: null x, params or y");
+  const uint32_t L = chunk ? chunk : 256;
+  BqShape s;
+  if (int rc = bq_shape(B, T, L, s, "biquad_forward_noalloc")) return rc;
+  const int64_t need = (int64_t)sizeof(double) * 6 * s.C * s.B + (int64_t)sizeof(float) * 2 * s.C * s.B;
+  if (need > kNoAllocScratchBytes)
+    return fail(DGEN_HIP_E_RANGE,
+                "biquad_forward_noalloc: B=%u lanes x %lld chunks need %lld bytes of scratch; the fixed scratch holds "
+                "%lld (lanes x ceil(T/chunk) <= %lld; raise the chunk length or split the bank)",
+                B, (long long)s.C, (long long)need, (long long)kNoAllocScratchBytes,
+                (long long)(kNoAllocScratchBytes / 56));
+  int n = 0, prev = 0;
+  DGEN_HIP_TRY(hipGetDeviceCount(&n));
+  if (device < 0 || device >= n || device >= kMaxScratchDevices)
+    return fail(DGEN_HIP_E_INVALID, "biquad_forward_noalloc: device %d of %d", device, n);
+  DGEN_HIP_TRY(hipGetDevice(&prev));
+  DGEN_HIP_TRY(hipSetDevice(device));
+  void* base = nullptr;
+  int rc = scratch_on(device, &base);
+  if (!rc) {
+    double* summ = static_cast<double*>(base);
+    float* init = reinterpret_cast<float*>(summ + 6 * s.C * s.B);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    bq_enqueue_chunk(st, x, mod, params, summ, s);
+    bq_enqueue_carry(st, summ, init, s.B, s.C, 0);
+    bq_enqueue_fwd(st, x, mod, params, init, y, nullptr, nullptr, s);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+      rc = fail(DGEN_HIP_E_DEVICE, "biquad_forward_noalloc: launch failed: %s", hipGetErrorString(e));
+  }
+  (void)hipSetDevice(prev);
+  return rc;
+}

@@ -62,7 +62,7 @@ EXPORTED_SYMBOLS = (
     "dgen_hip_last_error", "dgen_hip_configure", "dgen_hip_host_memory", "dgen_hip_upload",
     "dgen_hip_download", "dgen_hip_zero", "dgen_hip_run", "dgen_hip_run_async", "dgen_hip_sync", "dgen_hip_set_graphs",
     "dgen_hip_profile", "dgen_hip_time_runs", "dgen_hip_time_op", "dgen_hip_run_op", "dgen_hip_set_outputs",
-    "dgen_hip_host_outputs", "dgen_hip_set_sample_rate",
+    "dgen_hip_host_outputs", "dgen_hip_set_sample_rate", "dgen_hip_biquad_forward_noalloc",
 )
 
 
@@ -115,6 +115,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "dgen_hip_set_outputs": ([vp, u64, u64], i32),
         "dgen_hip_host_outputs": ([vp, ctypes.POINTER(u64)], ctypes.POINTER(ctypes.c_float)),
         "dgen_hip_set_sample_rate": ([vp, ctypes.c_float], i32),
+        "dgen_hip_biquad_forward_noalloc": ([i32, vp, vp, vp, vp, u32, u32, u32, vp], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)

@@ -395,6 +395,25 @@ int dgen_hip_run_op(dgen_hip_ctx* ctx, uint32_t frame_count, uint32_t op_index);
  * runs, timed with hipEvents recorded on the stream that op launches on. */
 int dgen_hip_time_op(dgen_hip_ctx* ctx, uint32_t frame_count, uint32_t op_index, int iters, double* ms_out);
 
+/* ---- bank forward without allocation --------------------------------------
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, real-time render loops, hosts that
+ * forbid hipMalloc): the tensor biquad bank forward of the schedule classes
+ * DGEN_HIP_K_BIQUAD_CHUNK -> _CARRY -> _FWD (RBJ low-pass, cutoff
+ * base[k] * mod[n], Q[k], zero initial state) on caller-owned device buffers,
+ * with the chunk summaries in a fixed scratch array the library holds on each
+ * device (16 MiB: lanes x ceil(T/chunk) <= 299593; larger banks fail with
+ * DGEN_HIP_E_RANGE).  No device memory is allocated or freed.
+ *   x [T][B], y [T][B] (frame-major), params [2][B] = base | Q, mod [T] or
+ *   NULL (unmodulated); chunk = frames per scan chunk (0: 256); stream: a
+ *   hipStream_t, or NULL for the null stream.
+ * The work is enqueued on `stream` and the call returns without waiting.
+ * Every call on a device shares that device's scratch, so calls that can
+ * overlap on one device (other streams, other host threads) race: order them
+ * on one stream.  The caller's current device is restored on return. */
+int dgen_hip_biquad_forward_noalloc(int device, const float* x, const float* mod, const float* params, float* y,
+                                    uint32_t B, uint32_t T, uint32_t chunk, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
