@@ -22,6 +22,7 @@ struct Launch {
   int cu_count = 256;
   bool dry = false;             // validate only
   float host_sr = 0.f;          // host sample rate of this run; 0: each op's own
+  bool reset = false;           // streaming classes start from zero state (else the state cells)
 };
 
 // Sample rate a phase increment divides by: the run's host sample rate when
@@ -136,6 +137,8 @@ int launch_stft_fwd(const Launch&, const dgen_hip_op&);
 int launch_stft_bwd(const Launch&, const dgen_hip_op&);
 int launch_membrane_fwd(const Launch&, const dgen_hip_op&);
 int launch_membrane_bwd(const Launch&, const dgen_hip_op&);
+int launch_stream_osc_bank(const Launch&, const dgen_hip_op&);
+int launch_stream_biquad(const Launch&, const dgen_hip_op&);
 
 // Sum over the 64 lanes of a wave (butterfly; every lane gets the total).
 __device__ __forceinline__ float wave_sum(float v) {

@@ -566,6 +566,69 @@ int launch_biquad_bwd(const Launch& L, const dgen_hip_op& op) {
   return 0;
 }
 
+// ---- streaming bank: one thread per lane, history carried between runs ----
+// The reference's per-lane frame loop (StatefulTensorParallelPolicy.swift:
+// 21-74): lane k steps Direct Form I frame by frame in registers from the
+// history cells state[4][B] (x[n-1], x[n-2], y[n-1], y[n-2]) and writes them
+// back, so any split of a run into runs gives the same samples; frames are
+// read and written [frame][lane] (a wave's 64 lanes are 256 contiguous
+// bytes).  Out stores map non-finite values to 0 (CRenderer.swift:1021-1039).
+template <bool MOD>
+__global__ __launch_bounds__(kThreads) void k_stream_bq(const float* __restrict__ x, const float* __restrict__ mod,
+                                                        const float* __restrict__ prm, float* __restrict__ state,
+                                                        float* __restrict__ y, int B, int T, int reset) {
+  const int k = blockIdx.x * kThreads + threadIdx.x;
+  if (k >= B) return;
+  const float base = prm[k], q = fabsf(prm[B + k]), rq = 1.0f / q;
+  float x1 = 0.f, x2 = 0.f, y1 = 0.f, y2 = 0.f;
+  if (!reset) {
+    x1 = state[k];
+    x2 = state[B + k];
+    y1 = state[2 * B + k];
+    y2 = state[3 * B + k];
+  }
+  const float* const src[1] = {x};
+  walk_fwd<1, MOD>(src, mod, B, k, 0, T, [&](int n, const float* v, float m) {
+    const Coef K = coef(base * m, q, rq);
+    const float x0 = v[0];
+    const float out = ((x2 * K.b0 + x1 * K.b1) + x0 * K.b0) - (y2 * K.a2 + y1 * K.a1);
+    y[(size_t)n * B + k] = isfinite(out) ? out : 0.f;
+    y2 = y1;
+    y1 = out;
+    x2 = x1;
+    x1 = x0;
+  });
+  state[k] = x1;
+  state[B + k] = x2;
+  state[2 * B + k] = y1;
+  state[3 * B + k] = y2;
+}
+
+int launch_stream_biquad(const Launch& L, const dgen_hip_op& op) {
+  // arg: [0]=x ([frames][B]) [1]=mod ([frames]) or -1 [2]=params ([2][B]) [3]=state ([4][B]) [4]=y ([frames][B])
+  //      [5]=B [6]=frames (capacity)
+  const int64_t x = op.arg[0], mod = op.arg[1], prm = op.arg[2], st = op.arg[3], y = op.arg[4], B = op.arg[5],
+                T = op.arg[6];
+  DGEN_REQUIRE(B > 0 && B <= (1 << 20) && T > 0 && T < (1ll << 30) && B * T < (1ll << 40),
+               "stream_biquad: B %lld frames %lld", (long long)B, (long long)T);
+  DGEN_CHECK_CELL(L, x, B * T, "stream_biquad.x");
+  if (mod >= 0) DGEN_CHECK_CELL(L, mod, T, "stream_biquad.mod");
+  DGEN_CHECK_CELL(L, prm, 2 * B, "stream_biquad.params");
+  DGEN_CHECK_CELL(L, st, 4 * B, "stream_biquad.state");
+  DGEN_CHECK_CELL(L, y, B * T, "stream_biquad.y");
+  if (L.dry) return 0;
+  const int64_t n = std::min<int64_t>(T, L.frames ? (int64_t)L.frames : T);
+  const dim3 grid((unsigned)((B + kThreads - 1) / kThreads));
+  if (mod >= 0)
+    hipLaunchKernelGGL(k_stream_bq<true>, grid, dim3(kThreads), 0, L.stream, cell(L, x), cell(L, mod), cell(L, prm),
+                       cell(L, st), cell(L, y), (int)B, (int)n, L.reset ? 1 : 0);
+  else
+    hipLaunchKernelGGL(k_stream_bq<false>, grid, dim3(kThreads), 0, L.stream, cell(L, x), nullptr, cell(L, prm),
+                       cell(L, st), cell(L, y), (int)B, (int)n, L.reset ? 1 : 0);
+  DGEN_LAUNCH_CHECK("k_stream_bq");
+  return 0;
+}
+
 // ---- the bank forward without allocation -----------------------------------
 // The chunk summaries ([C][6][B] fp64) and chunk initial states ([C][2][B]
 // fp32) of dgen_hip_biquad_forward_noalloc live in this fixed device array

@@ -133,6 +133,91 @@ __global__ __launch_bounds__(kTile) void k_osc_apply(const float* __restrict__ z
   out[n] = isfinite(y) ? y : 0.f;
 }
 
+// ---- streaming bank: one wave, state carried between runs -----------------
+// The frame loop of the reference's C backend, one block of 64 frames at a
+// time: lane k (< n_osc) steps oscillator k's phase through the block (the
+// stateful u_phasor, or the deterministic phase of the frame index within
+// this run), lane i (< 64) sums frame i's oscillators in order, and the
+// one-pole runs frame by frame on every lane (the value is uniform; lane i
+// keeps frame i's).  The state cell holds the phases and y[n-1] across runs,
+// so any split of a run into runs gives the same samples.
+constexpr int kStreamBlk = 64;
+constexpr int kStreamMaxOsc = 64;
+
+__device__ __forceinline__ float stream_phasor_wrap(float next) {
+  const float w = next - floorf(next);
+  return w >= 1.0f ? w - 1.0f : w;
+}
+
+__global__ __launch_bounds__(64) void k_stream_osc(const float* __restrict__ freqs, const float* __restrict__ amps,
+                                                   float* __restrict__ out, int nosc, int frames,
+                                                   float* __restrict__ state, int stateful, float sr, float pole,
+                                                   int reset) {
+  __shared__ float s_ph[kStreamBlk][kStreamMaxOsc + 1];
+  __shared__ float s_amp[kStreamMaxOsc];
+  __shared__ float s_x[kStreamBlk];
+  const int lane = threadIdx.x;
+  const bool osc = lane < nosc;
+  const float inc = osc ? freqs[lane] / sr : 0.f;  // phaseIncrement = freq / sampleRate
+  if (osc) s_amp[lane] = amps[lane];
+  float ph = (osc && stateful && !reset) ? state[lane] : 0.f;
+  float y = reset ? 0.f : state[nosc];
+  for (int f0 = 0; f0 < frames; f0 += kStreamBlk) {
+    const int nb = min(kStreamBlk, frames - f0);
+    if (osc) {
+      if (stateful) {
+        for (int i = 0; i < nb; ++i) {
+          s_ph[i][lane] = ph;  // pre-increment output
+          ph = stream_phasor_wrap(ph + inc);
+        }
+      } else {
+        for (int i = 0; i < nb; ++i) {
+          const float r = inc * (float)(f0 + i);
+          s_ph[i][lane] = r - floorf(r);
+        }
+      }
+    }
+    wave_sync();
+    if (lane < nb) {
+      float x = 0.f;
+      for (int k = 0; k < nosc; ++k) x = x + __builtin_amdgcn_sinf(s_ph[lane][k]) * s_amp[k];
+      s_x[lane] = x;
+    }
+    wave_sync();
+    float mine = 0.f;
+    for (int i = 0; i < nb; ++i) {
+      y = s_x[i] + pole * y;
+      if (i == lane) mine = y;
+    }
+    if (lane < nb) out[f0 + lane] = isfinite(mine) ? mine : 0.f;
+    wave_sync();
+  }
+  if (osc && stateful) state[lane] = ph;
+  if (lane == 0) state[nosc] = y;
+}
+
+int launch_stream_osc_bank(const Launch& L, const dgen_hip_op& op) {
+  // arg: [0]=freqs [1]=amps [2]=out [3]=n_osc (<= 64) [4]=frames (capacity) [5]=state (n_osc + 1)
+  //      [6]=stateful (0: deterministic phasor, frame index from 0 in every run; 1: u_phasor state)
+  // farg: [0]=sample rate [1]=pole
+  const int64_t fr = op.arg[0], am = op.arg[1], out = op.arg[2], nosc = op.arg[3], frames = op.arg[4],
+                st = op.arg[5], stateful = op.arg[6];
+  DGEN_REQUIRE(nosc > 0 && nosc <= kStreamMaxOsc && frames > 0 && frames <= (1 << 28) && (stateful == 0 || stateful == 1),
+               "stream_osc_bank: n_osc %lld frames %lld stateful %lld", (long long)nosc, (long long)frames,
+               (long long)stateful);
+  DGEN_REQUIRE(op.farg[0] > 0.f && op.farg[0] < 1e30f, "stream_osc_bank: sample rate %g", (double)op.farg[0]);
+  DGEN_CHECK_CELL(L, fr, nosc, "stream_osc_bank.freqs");
+  DGEN_CHECK_CELL(L, am, nosc, "stream_osc_bank.amps");
+  DGEN_CHECK_CELL(L, out, frames, "stream_osc_bank.out");
+  DGEN_CHECK_CELL(L, st, nosc + 1, "stream_osc_bank.state");
+  if (L.dry) return 0;
+  const int64_t n = std::min<int64_t>(frames, L.frames ? (int64_t)L.frames : frames);
+  hipLaunchKernelGGL(k_stream_osc, dim3(1), dim3(64), 0, L.stream, cell(L, fr), cell(L, am), cell(L, out), (int)nosc,
+                     (int)n, cell(L, st), (int)stateful, host_rate(L, op.farg[0]), op.farg[1], L.reset ? 1 : 0);
+  DGEN_LAUNCH_CHECK("k_stream_osc");
+  return 0;
+}
+
 int launch_osc_bank(const Launch& L, const dgen_hip_op& op) {
   // arg: [0]=freqs [1]=amps [2]=out [3]=n_osc [4]=frames [5]=workspace
   //      (frames + 1 + 3*tiles floats, tiles = ceil(frames/256), even cell)

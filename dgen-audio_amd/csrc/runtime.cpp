@@ -15,7 +15,9 @@
 //   MetalRuntime.swift:334-337).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
+#include <cstdint>
 #include <cstring>
 #include <new>
 #include <string>
@@ -72,6 +74,8 @@ static Launcher launcher_for(uint32_t k) {
     case DGEN_HIP_K_STFT_BWD: return launch_stft_bwd;
     case DGEN_HIP_K_MEMBRANE_FWD: return launch_membrane_fwd;
     case DGEN_HIP_K_MEMBRANE_BWD: return launch_membrane_bwd;
+    case DGEN_HIP_K_STREAM_OSC_BANK: return launch_stream_osc_bank;
+    case DGEN_HIP_K_STREAM_BIQUAD: return launch_stream_biquad;
     default: return nullptr;
   }
 }
@@ -99,6 +103,12 @@ struct dgen_hip_ctx {
   float host_sr = 0.f;
   // output cells (dgen_hip_set_outputs), downloaded by every dgen_hip_run
   uint64_t out_off = 0, out_n = 0;
+  // process ports (dgen_hip_set_process_ports): channel c, frame i at cell
+  // in_cell[c] + i * in_stride[c] (inputs) / out_cell[c] + i * out_stride[c]
+  std::vector<uint64_t> in_cell, out_cell;
+  std::vector<uint32_t> in_stride, out_stride;
+  // the next enqueue starts the streaming classes from zero state
+  bool reset_next = false;
 };
 
 static int set_device(dgen_hip_ctx* c) {
@@ -116,6 +126,7 @@ static Launch make_launch(dgen_hip_ctx* c, hipStream_t s, uint32_t frames, bool 
   L.cu_count = c->cu_count;
   L.dry = dry;
   L.host_sr = c->host_sr;
+  L.reset = c->reset_next;
   return L;
 }
 
@@ -133,6 +144,10 @@ static void release_arena(dgen_hip_ctx* c) {
   c->h_arena = nullptr;
   c->floats = 0;
   c->out_off = c->out_n = 0;
+  c->in_cell.clear();
+  c->out_cell.clear();
+  c->in_stride.clear();
+  c->out_stride.clear();
   c->configured = false;
 }
 
@@ -376,6 +391,8 @@ static FrameArg frame_arg(uint32_t k) {
     case DGEN_HIP_K_STFT_BWD: return {5, false};
     case DGEN_HIP_K_MEMBRANE_FWD: return {6, false};
     case DGEN_HIP_K_MEMBRANE_BWD: return {9, false};
+    case DGEN_HIP_K_STREAM_OSC_BANK: return {4, true};
+    case DGEN_HIP_K_STREAM_BIQUAD: return {6, true};
     default: return {-1, false};
   }
 }
@@ -461,6 +478,100 @@ float* dgen_hip_host_outputs(dgen_hip_ctx* c, uint64_t* n_out) {
   if (n_out) *n_out = (c && c->configured) ? c->out_n : 0;
   if (!c || !c->configured || !c->out_n) return nullptr;
   return c->h_arena + c->out_off;
+}
+
+int dgen_hip_set_process_ports(dgen_hip_ctx* c, uint32_t n_in, const uint64_t* in_cells, const uint32_t* in_strides,
+                               uint32_t n_out, const uint64_t* out_cells, const uint32_t* out_strides) {
+  if (!c || !c->configured) return fail(DGEN_HIP_E_STATE, "set_process_ports: context not configured");
+  if ((n_in && (!in_cells || !in_strides)) || (n_out && (!out_cells || !out_strides)))
+    return fail(DGEN_HIP_E_INVALID, "set_process_ports: null port arrays");
+  auto check = [&](const uint64_t* cells, const uint32_t* strides, uint32_t n, const char* what) -> int {
+    for (uint32_t i = 0; i < n; ++i) {
+      if (strides[i] == 0)
+        return fail(DGEN_HIP_E_INVALID, "set_process_ports: %s channel %u has stride 0", what, i);
+      const uint64_t last = cells[i] + (uint64_t)(c->max_frames - 1) * strides[i];
+      if (cells[i] >= c->floats || last >= c->floats)
+        return fail(DGEN_HIP_E_RANGE, "set_process_ports: %s channel %u ([%llu, %llu] over %u frames) outside arena "
+                    "of %llu floats", what, i, (unsigned long long)cells[i], (unsigned long long)last, c->max_frames,
+                    (unsigned long long)c->floats);
+    }
+    return 0;
+  };
+  int rc = check(in_cells, in_strides, n_in, "input");
+  if (!rc) rc = check(out_cells, out_strides, n_out, "output");
+  if (rc) return rc;
+  c->in_cell.assign(in_cells, in_cells + n_in);
+  c->in_stride.assign(in_strides, in_strides + n_in);
+  c->out_cell.assign(out_cells, out_cells + n_out);
+  c->out_stride.assign(out_strides, out_strides + n_out);
+  return 0;
+}
+
+// Smallest cell range covering `n` frames of every channel of a port list.
+static void port_span(const std::vector<uint64_t>& cells, const std::vector<uint32_t>& strides, uint32_t n,
+                      uint64_t* lo, uint64_t* hi) {
+  *lo = UINT64_MAX;
+  *hi = 0;
+  for (size_t i = 0; i < cells.size(); ++i) {
+    *lo = std::min(*lo, cells[i]);
+    *hi = std::max(*hi, cells[i] + (uint64_t)(n - 1) * strides[i] + 1);
+  }
+}
+
+int dgen_hip_process_v1(dgen_hip_ctx* c, const float* const* inputs, float* const* outputs, uint32_t frame_count,
+                        const dgen_hip_process_context_v1* context) {
+  if (!c || !c->configured) return fail(DGEN_HIP_E_STATE, "process_v1: context not configured");
+  float sr = 0.f;
+  uint32_t flags = 0;
+  if (context) {
+    if (context->abi_version != DGEN_HIP_ABI_VERSION || context->struct_size < sizeof(dgen_hip_process_context_v1))
+      return fail(DGEN_HIP_E_INVALID, "process_v1: context abi %u size %u (expected %d, >= %zu)",
+                  context->abi_version, context->struct_size, DGEN_HIP_ABI_VERSION,
+                  sizeof(dgen_hip_process_context_v1));
+    sr = context->sample_rate;
+    flags = context->flags;
+    if (!(sr == 0.f || (sr >= 1.f && sr <= 1e7f)))
+      return fail(DGEN_HIP_E_INVALID, "process_v1: sample rate %g Hz outside [1, 1e7] (or 0)", (double)sr);
+  }
+  int rc = run_checks(c, frame_count);
+  if (rc) return rc;
+  if (!c->in_cell.empty() && !inputs) return fail(DGEN_HIP_E_INVALID, "process_v1: null inputs");
+  if (!c->out_cell.empty() && !outputs) return fail(DGEN_HIP_E_INVALID, "process_v1: null outputs");
+  for (size_t i = 0; i < c->in_cell.size(); ++i)
+    if (!inputs[i]) return fail(DGEN_HIP_E_INVALID, "process_v1: input channel %zu is null", i);
+  for (size_t i = 0; i < c->out_cell.size(); ++i)
+    if (!outputs[i]) return fail(DGEN_HIP_E_INVALID, "process_v1: output channel %zu is null", i);
+  // inputs -> host mirror -> device (one copy over the ports' span)
+  if (!c->in_cell.empty()) {
+    for (size_t i = 0; i < c->in_cell.size(); ++i) {
+      float* dst = c->h_arena + c->in_cell[i];
+      const uint32_t st = c->in_stride[i];
+      for (uint32_t f = 0; f < frame_count; ++f) dst[(size_t)f * st] = inputs[i][f];
+    }
+    uint64_t lo, hi;
+    port_span(c->in_cell, c->in_stride, frame_count, &lo, &hi);
+    if ((rc = dgen_hip_upload(c, lo, hi - lo))) return rc;
+  }
+  // the run, eagerly enqueued, at the call's host rate and reset flag
+  const float saved_sr = c->host_sr;
+  c->host_sr = sr;
+  c->reset_next = (flags & DGEN_HIP_PROCESS_RESET) != 0;
+  rc = enqueue(c, frame_count, false, nullptr);
+  c->host_sr = saved_sr;
+  c->reset_next = false;
+  const int rc2 = dgen_hip_sync(c);
+  if (rc || rc2) return rc ? rc : rc2;
+  if (!c->out_cell.empty()) {
+    uint64_t lo, hi;
+    port_span(c->out_cell, c->out_stride, frame_count, &lo, &hi);
+    if ((rc = dgen_hip_download(c, lo, hi - lo))) return rc;
+    for (size_t i = 0; i < c->out_cell.size(); ++i) {
+      const float* src = c->h_arena + c->out_cell[i];
+      const uint32_t st = c->out_stride[i];
+      for (uint32_t f = 0; f < frame_count; ++f) outputs[i][f] = src[(size_t)f * st];
+    }
+  }
+  return 0;
 }
 
 int dgen_hip_set_sample_rate(dgen_hip_ctx* c, float sample_rate) {

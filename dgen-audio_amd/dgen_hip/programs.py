@@ -49,6 +49,24 @@ def oscbank_program(cfg: OscBankConfig) -> Program:
     return p
 
 
+def stream_oscbank_program(cfg: OscBankConfig, stateful: bool = True, max_frames: int | None = None) -> Program:
+    """The config-1 graph as a streaming process (dgen_process_v1 with
+    preserved state): per call, frames [0, frame_count) of `out`; the
+    oscillator phases (stateful) and the one-pole's y[n-1] carry over."""
+    T = int(max_frames or cfg.frames)
+    p = Program(max_frames=T)
+    freqs = p.alloc("freqs", cfg.n_osc)
+    amps = p.alloc("amps", cfg.n_osc)
+    out = p.alloc("out", T)
+    st = p.alloc("state", cfg.n_osc + 1)
+    p.add(R.K_STREAM_OSC_BANK, [freqs, amps, out, cfg.n_osc, T, st, 1 if stateful else 0], [cfg.sr, cfg.pole],
+          label="stream_osc_bank", dispatch="singleThreaded frame loop (one wave)", bytes=4.0 * T,
+          flops=float(T) * (26.0 * cfg.n_osc + 2.0), bound="valu")
+    p.output_cell = "out"
+    p.meta.update(cfg=cfg, stateful=stateful, ports=([], [("out", 0, 1)]))
+    return p
+
+
 # ------------------------------------------------------------------ config 3
 def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = True,
                      side_stream: bool = True) -> Program:
@@ -402,6 +420,26 @@ def biquad_program(cfg: BiquadConfig, train: bool = True, optimizer: bool = True
         p.add(R.K_ADAM, [P, G, m, v, 2 * B, tcell], [cfg.lr, 0.9, 0.999, 1e-8], label="adam",
               dispatch=f"staticThreads({2 * B})", bytes=7.0 * 2 * B * f4, flops=12.0 * 2 * B)
     p.output_cell = "y"
+    return p
+
+
+def stream_biquad_program(cfg: BiquadConfig, max_frames: int | None = None, modulated: bool = True) -> Program:
+    """The config-4 bank as a streaming process: per call, B input channels
+    (and the modulation channel) in, B output channels out, the four history
+    cells of every lane carried over (StatefulTensorParallelPolicy's per-lane
+    frame loop)."""
+    B, T = cfg.B, int(max_frames or cfg.T)
+    p = Program(max_frames=T)
+    x = p.alloc("x", T * B)
+    mod = p.alloc("mod", T) if modulated else -1
+    P = p.alloc("params", 2 * B)
+    st = p.alloc("state", 4 * B)
+    y = p.alloc("y", T * B)
+    p.add(R.K_STREAM_BIQUAD, [x, mod, P, st, y, B, T], label="stream_biquad",
+          dispatch=f"fixedWithFrameLoop({B})", bytes=8.0 * T * B, flops=float(T * B) * (16 + 9), bound="valu")
+    p.output_cell = "y"
+    ins = [("x", k, B) for k in range(B)] + ([("mod", 0, 1)] if modulated else [])
+    p.meta.update(cfg=cfg, ports=(ins, [("y", k, B) for k in range(B)]))
     return p
 
 

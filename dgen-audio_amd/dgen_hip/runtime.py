@@ -51,6 +51,8 @@ K_STFT_FWD = 25
 K_STFT_BWD = 26
 K_MEMBRANE_FWD = 27
 K_MEMBRANE_BWD = 28
+K_STREAM_OSC_BANK = 29
+K_STREAM_BIQUAD = 30
 
 KERNEL_NAMES = {v: k[2:].lower() for k, v in globals().items() if k.startswith("K_")}
 
@@ -63,7 +65,9 @@ EXPORTED_SYMBOLS = (
     "dgen_hip_download", "dgen_hip_zero", "dgen_hip_run", "dgen_hip_run_async", "dgen_hip_sync", "dgen_hip_set_graphs",
     "dgen_hip_profile", "dgen_hip_time_runs", "dgen_hip_time_op", "dgen_hip_run_op", "dgen_hip_set_outputs",
     "dgen_hip_host_outputs", "dgen_hip_set_sample_rate", "dgen_hip_biquad_forward_noalloc",
+    "dgen_hip_set_process_ports", "dgen_hip_process_v1",
 )
+PROCESS_RESET = 1
 
 
 class HIPError(RuntimeError):
@@ -73,6 +77,11 @@ class HIPError(RuntimeError):
 class COp(ctypes.Structure):
     _fields_ = [("kernel", ctypes.c_uint32), ("flags", ctypes.c_uint32),
                 ("arg", ctypes.c_int64 * NARG), ("farg", ctypes.c_float * NFARG)]
+
+
+class CProcessContext(ctypes.Structure):
+    _fields_ = [("abi_version", ctypes.c_uint32), ("struct_size", ctypes.c_uint32), ("sample_rate", ctypes.c_float),
+                ("flags", ctypes.c_uint32)]
 
 
 class CKernelTime(ctypes.Structure):
@@ -116,6 +125,11 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "dgen_hip_host_outputs": ([vp, ctypes.POINTER(u64)], ctypes.POINTER(ctypes.c_float)),
         "dgen_hip_set_sample_rate": ([vp, ctypes.c_float], i32),
         "dgen_hip_biquad_forward_noalloc": ([i32, vp, vp, vp, vp, u32, u32, u32, vp], i32),
+        "dgen_hip_set_process_ports": ([vp, u32, ctypes.POINTER(u64), ctypes.POINTER(u32), u32,
+                                        ctypes.POINTER(u64), ctypes.POINTER(u32)], i32),
+        "dgen_hip_process_v1": ([vp, ctypes.POINTER(ctypes.POINTER(ctypes.c_float)),
+                                 ctypes.POINTER(ctypes.POINTER(ctypes.c_float)), u32, ctypes.POINTER(CProcessContext)],
+                                i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -237,6 +251,36 @@ class HIPLazyRuntime:
         c = self.program.cells[name]
         self.download(name)
         return self._host[c.off:c.off + c.n].copy()
+
+    # -- streaming process calls (dgen_process_v1) ----------------------
+    def setProcessPorts(self, inputs, outputs) -> None:
+        """Channels of process(): lists of (cell name, lane, lanes) for
+        [frames][lanes] cells (one channel per lane, stride lanes)."""
+        def cells(ports):
+            off = (ctypes.c_uint64 * max(1, len(ports)))()
+            st = (ctypes.c_uint32 * max(1, len(ports)))()
+            for i, (name, lane, lanes) in enumerate(ports):
+                off[i] = self.program.cells[name].off + lane
+                st[i] = lanes
+            return off, st
+        (io, ist), (oo, ost) = cells(inputs), cells(outputs)
+        self._ports = (len(inputs), len(outputs))
+        _check(self.L.dgen_hip_set_process_ports(self._ctx, len(inputs), io, ist, len(outputs), oo, ost),
+               "dgen_hip_set_process_ports")
+
+    def process(self, inputs, frames: int, sample_rate: float = 0.0, reset: bool = False) -> np.ndarray:
+        """One dgen_hip_process_v1 block: inputs [n_in][frames] -> outputs [n_out][frames]."""
+        n_in, n_out = self._ports
+        fp = ctypes.POINTER(ctypes.c_float)
+        ins = [np.ascontiguousarray(a, np.float32) for a in inputs]
+        if len(ins) != n_in or any(a.shape != (frames,) for a in ins):
+            raise ValueError(f"process: {n_in} input channels of {frames} frames expected")
+        outs = np.zeros((n_out, frames), np.float32)
+        ip = (fp * max(1, n_in))(*[a.ctypes.data_as(fp) for a in ins])
+        op = (fp * max(1, n_out))(*[outs[i].ctypes.data_as(fp) for i in range(n_out)])
+        ctxv = CProcessContext(2, ctypes.sizeof(CProcessContext), float(sample_rate), PROCESS_RESET if reset else 0)
+        _check(self.L.dgen_hip_process_v1(self._ctx, ip, op, int(frames), ctypes.byref(ctxv)), "dgen_hip_process_v1")
+        return outs
 
     def set_graphs(self, enable: bool = True) -> None:
         """Replay runs as a captured HIP graph (dgen_hip_set_graphs)."""

@@ -257,6 +257,28 @@ enum dgen_hip_kernel {
    *      boundary fields ([4][R][C]) [5]=grad partials [6]=loss terms
    *      [7]=R [8]=C [9]=T [10]=py [11]=px [12]=steps per launch [13]=grads */
   DGEN_HIP_K_MEMBRANE_BWD = 28,
+
+  /* ---- streaming classes (dgen_hip_process_v1 / dgen_hip_run with
+   * preserved state, Realize.swift:553-563).  A run of frame_count frames
+   * processes frames [0, frame_count) of the op's cells (any frame_count up
+   * to the op's frames) and carries the graph's state cells to the next run;
+   * a DGEN_HIP_PROCESS_RESET call starts from zero state.  Any split of a
+   * signal into runs gives the same samples.
+   *
+   * Oscillator bank -> sum -> history one-pole (config 1), frame-sequential
+   * like the C backend: arg: [0]=freqs [1]=amps [2]=out [3]=n_osc (<= 64)
+   * [4]=frames [5]=state (n_osc phases, then y[n-1]) [6]=stateful (0:
+   * Signal.phasor(Tensor), the deterministic phasor of the frame index within
+   * the run, Emit+State.swift:370-387; 1: stateful u_phasor accumulators,
+   * Definitions.swift:96-102)   farg: [0]=sample rate [1]=pole */
+  DGEN_HIP_K_STREAM_OSC_BANK = 29,
+
+  /* Tensor biquad bank, one lane per thread, Direct Form I history in the
+   * state cell ([4][B]: x[n-1], x[n-2], y[n-1], y[n-2]); coefficients as
+   * DGEN_HIP_K_BIQUAD_*.  arg: [0]=x ([frames][B]) [1]=mod ([frames]) or -1
+   * [2]=params ([2][B] base | Q) [3]=state [4]=y ([frames][B]) [5]=B
+   * [6]=frames */
+  DGEN_HIP_K_STREAM_BIQUAD = 30,
 };
 
 /* GEMM epilogues */
@@ -363,6 +385,33 @@ float* dgen_hip_host_outputs(dgen_hip_ctx* ctx, uint64_t* n_out);
  * the rate each op was rendered with; otherwise [1, 1e7].  Drops a captured
  * graph. */
 int dgen_hip_set_sample_rate(dgen_hip_ctx* ctx, float sample_rate);
+
+/* ---- streaming process calls (dgen_process_v1, dgen_runtime.h:252-291) -- */
+typedef struct dgen_hip_process_context_v1 {
+  uint32_t abi_version; /* DGEN_HIP_ABI_VERSION */
+  uint32_t struct_size; /* sizeof(dgen_hip_process_context_v1) */
+  float sample_rate;    /* host sample rate of this call (DGenProcessContextV1.sample_rate); 0: rendered */
+  uint32_t flags;       /* DGEN_HIP_PROCESS_* */
+} dgen_hip_process_context_v1;
+#define DGEN_HIP_PROCESS_RESET 1u /* streaming classes start this call from zero state */
+
+/* Declare the channels of dgen_hip_process_v1: input channel c's frame i is
+ * written to cell in_cells[c] + i * in_strides[c], output channel c's frame i
+ * read from out_cells[c] + i * out_strides[c] (a [frames][lanes] cell is one
+ * channel per lane with stride lanes).  Every channel must fit max_frames
+ * frames in the arena.  Reset by dgen_hip_configure. */
+int dgen_hip_set_process_ports(dgen_hip_ctx* ctx, uint32_t n_in, const uint64_t* in_cells, const uint32_t* in_strides,
+                               uint32_t n_out, const uint64_t* out_cells, const uint32_t* out_strides);
+
+/* One block of a streaming schedule (the reference's dgen_process_v1(inputs,
+ * outputs, frame_count, state, context, host)): the input channels'
+ * frame_count samples (host arrays) go to their cells, the per-run ops run
+ * on frame_count frames, carrying their state cells from the previous call
+ * (the context's state is the arena), and the output channels' samples come
+ * back to the host arrays.  Synchronous.  context may be NULL (rendered
+ * sample rate, no reset).  Ops are enqueued one by one (no graph replay). */
+int dgen_hip_process_v1(dgen_hip_ctx* ctx, const float* const* inputs, float* const* outputs, uint32_t frame_count,
+                        const dgen_hip_process_context_v1* context);
 
 /* Graph replay of runs (enable != 0): the per-run schedule for a frame count
  * is captured once from both streams into a HIP graph and every later

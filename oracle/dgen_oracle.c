@@ -157,6 +157,39 @@ void FN(dgen_oracle_oscbank)(const float* freqs, const float* amps, int n_osc, f
   }
 }
 
+/* One block of the bank as a streaming process call (dgen_process_v1 with
+ * realize(preserveState: true), Sources/DGenLazy/Realize.swift:553-563).
+ * state: [n_osc] phases, then y[n-1] of the history one-pole, carried from
+ * the previous call.  stateful = 0: Signal.phasor(Tensor), the deterministic
+ * phasor, whose frame index n restarts at 0 in every call
+ * (Emit+State.swift:370-387 uses the frame index of the call); stateful = 1:
+ * one Signal.phasor(Float) per oscillator, the u_phasor accumulator
+ * (Definitions.swift:96-102, 215-246) carried in state.  The sum over the
+ * oscillators keeps their order; out stores map non-finite values to 0. */
+void FN(dgen_oracle_oscbank_stream)(const float* freqs, const float* amps, int n_osc, float sr, float pole, int frames,
+                                    int stateful, REAL* state, float* out) {
+  REAL y = state[n_osc];
+  for (int n = 0; n < frames; ++n) {
+    REAL x = 0;
+    for (int k = 0; k < n_osc; ++k) {
+      REAL phase;
+      if (stateful) {
+        float ph = (float)state[k];
+        phase = (REAL)phasor_step(&ph, freqs[k], sr);
+        state[k] = (REAL)ph;
+      } else {
+        REAL inc = (REAL)freqs[k] / (REAL)sr;
+        REAL raw = inc * (REAL)n;
+        phase = raw - R_FLOOR(raw);
+      }
+      x = x + R_SIN(phase * TWO_PI_F32) * (REAL)amps[k];
+    }
+    y = x + (REAL)pole * y;
+    out[n] = (float)sanitize(y);
+  }
+  state[n_osc] = y;
+}
+
 /* ------------------------------------------------------------------------ */
 /* Config 3: batched harmonic + FIR-noise synth, MLP decoder, MSS loss.      */
 /* ------------------------------------------------------------------------ */
@@ -911,10 +944,11 @@ static inline REAL bq_cutoff(const float* m, const REAL* base, int n, int k) {
   return m ? base[k] * (REAL)m[n] : base[k];
 }
 
-/* Forward of the bank: x, y are [T][B] (frame-major, lane-minor).  State
- * starts at zero (history cells zeroed by zeroAllBuffers). */
-static void bq_forward(const float* x, const float* m, const REAL* base, const REAL* Q, int B, int T, REAL* y) {
-  REAL* st = (REAL*)calloc((size_t)4 * B, sizeof(REAL)); /* x1 x2 y1 y2 per lane */
+/* Forward of the bank from the history state st ([B][4]: x[n-1], x[n-2],
+ * y[n-1], y[n-2] per lane, updated in place): x, y are [T][B] (frame-major,
+ * lane-minor). */
+static void bq_forward_state(const float* x, const float* m, const REAL* base, const REAL* Q, int B, int T, REAL* st,
+                             REAL* y) {
   for (int n = 0; n < T; ++n) {
     for (int k = 0; k < B; ++k) {
       REAL* s = st + 4 * k;
@@ -929,7 +963,26 @@ static void bq_forward(const float* x, const float* m, const REAL* base, const R
       y[(size_t)n * B + k] = v;
     }
   }
+}
+
+/* From zero state (history cells zeroed by zeroAllBuffers). */
+static void bq_forward(const float* x, const float* m, const REAL* base, const REAL* Q, int B, int T, REAL* y) {
+  REAL* st = (REAL*)calloc((size_t)4 * B, sizeof(REAL)); /* x1 x2 y1 y2 per lane */
+  bq_forward_state(x, m, base, Q, B, T, st, y);
   free(st);
+}
+
+/* One block of the bank as a streaming process call (dgen_process_v1 with
+ * realize(preserveState: true), Sources/DGenLazy/Realize.swift:553-563): the
+ * history cells state[B][4] carry over from the previous call; m: this
+ * block's modulation (or NULL); y: the block's outputs, non-finite stored as
+ * 0 (CRenderer.swift:1021-1039) while the history keeps the raw value. */
+void FN(dgen_oracle_biquad_stream)(const float* x, const float* m, const REAL* base, const REAL* Q, int B, int T,
+                                   REAL* state, float* y_out) {
+  REAL* y = (REAL*)malloc(sizeof(REAL) * (size_t)B * T);
+  bq_forward_state(x, m, base, Q, B, T, state, y);
+  for (size_t i = 0; i < (size_t)B * T; ++i) y_out[i] = (float)sanitize(y[i]);
+  free(y);
 }
 
 void FN(dgen_oracle_biquad_fwd)(const float* x, const float* m, const REAL* base, const REAL* Q, int B, int T,

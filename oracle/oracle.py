@@ -44,6 +44,8 @@ def lib(name: str = "liboracle.so") -> ctypes.CDLL:
             if not hasattr(L, "dgen_oracle_oscbank" + sfx):
                 continue
             _sig(L, "dgen_oracle_oscbank" + sfx, [_f32p, _f32p, _c_int, _c_float, _c_float, _c_int, _f32p])
+            _sig(L, "dgen_oracle_oscbank_stream" + sfx,
+                 [_f32p, _f32p, _c_int, _c_float, _c_float, _c_int, _c_int, rp_(sfx), _f32p])
             _sig(L, "dgen_oracle_playhead" + sfx, [_c_int, _c_int, _f32p])
             syn = [_f32p, _f32p, _f32p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_float, _c_float, _f32p]
             _sig(L, "dgen_oracle_synth_fwd" + sfx, syn)
@@ -63,6 +65,7 @@ def lib(name: str = "liboracle.so") -> ctypes.CDLL:
             _sig(L, "dgen_oracle_adam" + sfx, [_f32p, _f32p, _f32p, _f32p, _c_size] + [_c_float] * 4 + [_c_int])
             vp = ctypes.c_void_p
             _sig(L, "dgen_oracle_biquad_fwd" + sfx, [_f32p, vp, rp, rp, _c_int, _c_int, _f32p])
+            _sig(L, "dgen_oracle_biquad_stream" + sfx, [_f32p, vp, rp, rp, _c_int, _c_int, rp, _f32p])
             _sig(L, "dgen_oracle_biquad_step" + sfx, [_f32p, vp, rp, rp, _f32p, _c_int, _c_int, vp, vp],
                  ctypes.c_double)
             _sig(L, "dgen_oracle_tensor_fft" + sfx, [_c_int, _c_int, rp, rp])
@@ -98,6 +101,15 @@ def _fn(name: str, prec: str, libname: str = "liboracle.so"):
 def oscbank(freqs, amps, sr, pole, frames, prec="f32", libname="liboracle.so"):
     out = np.zeros(frames, np.float32)
     _fn("dgen_oracle_oscbank", prec, libname)(_f(freqs), _f(amps), len(freqs), sr, pole, frames, out)
+    return out
+
+
+def oscbank_stream(freqs, amps, sr, pole, frames, stateful, state, prec="f32"):
+    """One streaming block of the bank; `state` ([n_osc] phases + y[n-1],
+    float32 for prec f32, float64 for f64) is updated in place."""
+    out = np.zeros(frames, np.float32)
+    _fn("dgen_oracle_oscbank_stream", prec)(_f(freqs), _f(amps), len(freqs), sr, pole, frames, int(stateful), state,
+                                            out)
     return out
 
 
@@ -242,6 +254,19 @@ def biquad_fwd(x, m, base, Q, prec="f32"):
     m, mp = _mod_ptr(m, T)
     y = np.zeros((T, B), np.float32)
     _fn("dgen_oracle_biquad_fwd", prec)(x, mp, np.ascontiguousarray(base, dt), np.ascontiguousarray(Q, dt), B, T, y)
+    return y
+
+
+def biquad_stream(x, m, base, Q, state, prec="f32"):
+    """One streaming block of the bank: x [T][B] -> y [T][B], the history
+    state [B][4] (x[n-1], x[n-2], y[n-1], y[n-2]) updated in place."""
+    x = _f(x)
+    T, B = x.shape
+    dt = np.float32 if prec == "f32" else np.float64
+    m, mp = _mod_ptr(m, T)
+    y = np.zeros((T, B), np.float32)
+    _fn("dgen_oracle_biquad_stream", prec)(x, mp, np.ascontiguousarray(base, dt), np.ascontiguousarray(Q, dt), B, T,
+                                           state, y)
     return y
 
 
