@@ -76,6 +76,8 @@ static Launcher launcher_for(uint32_t k) {
     case DGEN_HIP_K_MEMBRANE_BWD: return launch_membrane_bwd;
     case DGEN_HIP_K_STREAM_OSC_BANK: return launch_stream_osc_bank;
     case DGEN_HIP_K_STREAM_BIQUAD: return launch_stream_biquad;
+    case DGEN_HIP_K_TEMPORAL_GRAD_SCAN: return launch_temporal_grad_scan;
+    case DGEN_HIP_K_SWEPT_PHASOR: return launch_swept_phasor;
     default: return nullptr;
   }
 }
@@ -393,6 +395,8 @@ static FrameArg frame_arg(uint32_t k) {
     case DGEN_HIP_K_MEMBRANE_BWD: return {9, false};
     case DGEN_HIP_K_STREAM_OSC_BANK: return {4, true};
     case DGEN_HIP_K_STREAM_BIQUAD: return {6, true};
+    case DGEN_HIP_K_TEMPORAL_GRAD_SCAN: return {4, false};
+    case DGEN_HIP_K_SWEPT_PHASOR: return {7, false};
     default: return {-1, false};
   }
 }

@@ -11,7 +11,7 @@ import numpy as np
 
 from . import runtime as R
 from .program import Program
-from .workloads import BiquadConfig, HarmonicConfig, MembraneConfig, OscBankConfig, StftConfig
+from .workloads import BiquadConfig, HarmonicConfig, MembraneConfig, OscBankConfig, StftConfig, SweptPhasorConfig
 
 SEG = 64          # frames per synth segment (checkpoint spacing)
 SLOTS = 4         # control rows a segment may touch
@@ -473,6 +473,73 @@ class BiquadSession:
             rt.write("params", params)
             rt.runNoCopy()
             return rt.read("y").reshape(self.cfg.T, self.cfg.B)
+
+    def step(self) -> None:
+        self.rt.runNoCopy()
+
+    def loss(self) -> float:
+        return float(self.rt.read("loss")[0])
+
+    def close(self):
+        self.rt.close()
+
+
+# ------------------------------------------------- temporal gradient (a21)
+def swept_phasor_program(cfg: SweptPhasorConfig, optimizer: bool = True) -> Program:
+    """The swept-phasor bank forward, loss and backward to the sweep rates:
+    time = accum(1/sr) (a static table), the per-lane stateful phasor of
+    base + slope * time with the mse loss, the phasor's temporal gradient (the
+    reset-aware suffix scan, / sr) and d f / d slope = time summed over frames
+    (Gradients.swift:209-261), then (``optimizer``) one Adam step."""
+    E, T = cfg.E, cfg.T
+    C = (T + 255) // 256
+    f4 = 4.0
+    p = Program(max_frames=T)
+    p.meta.update(cfg=cfg)
+    slope = p.alloc("slope", E)
+    time = p.alloc("time", T)
+    reset = p.alloc("reset", T)
+    gup = p.alloc("upstream", T * E)
+    lossp = p.alloc("loss_partials", E)
+    loss = p.alloc("loss", 1)
+    dfreq = p.alloc("dfreq", T * E)
+    G = p.alloc("grads", E)
+    ws_scan = p.alloc("scan_ws", 2 * C * E + C)
+    chunks = min(256, max(1, T // 32))
+    ws_col = p.alloc("colsum_ws", max(chunks * 2 * E, _colsum_ws(E, 1)))
+    step = np.float32(np.float32(1.0) / np.float32(cfg.sr))
+    p.add(R.K_ACCUM_TABLE, [time, T], [step, 0.0, 1.0, 0.0, 1.0], flags=R.OP_STATIC, label="time",
+          dispatch="static singleThreaded")
+    n = float(T * E)
+    p.add(R.K_SWEPT_PHASOR, [slope, time, reset, -1, gup, lossp, E, T, int(cfg.smooth)], [cfg.sr, cfg.base, cfg.target],
+          label="swept_phasor", dispatch=f"fixedWithFrameLoop({E})", bytes=n * f4 + T * 2 * f4, flops=n * 10.0,
+          bound="valu")
+    p.add(R.K_COLSUM, [lossp, loss, E, 1, 1, ws_col], label="loss_sum", dispatch="chunkPartialsReduceToCell",
+          bytes=(E + 1) * f4, flops=float(E))
+    p.add(R.K_TEMPORAL_GRAD_SCAN, [gup, reset, dfreq, E, T, ws_scan, 1], [cfg.sr], label="temporal_scan",
+          dispatch=f"temporalGradScan({E}) chunked", bytes=2 * n * f4 + T * f4, flops=2.0 * n)
+    p.add(R.K_DENSE_SMALL_WGRAD, [time, dfreq, G, T, 1, E, ws_col, -1], label="dslope",
+          dispatch="chunkPartialsReduceToCell", bytes=(n + T + E) * f4, flops=2.0 * n)
+    if optimizer:
+        m = p.alloc("adam_m", E)
+        v = p.alloc("adam_v", E)
+        tcell = p.alloc("adam_t", 1)
+        p.add(R.K_ADAM, [slope, G, m, v, E, tcell], [cfg.lr, 0.9, 0.999, 1e-8], label="adam",
+              dispatch=f"staticThreads({E})", bytes=7.0 * E * f4, flops=12.0 * E)
+    p.output_cell = "loss"
+    return p
+
+
+class SweptPhasorSession:
+    """A swept-phasor bank runtime: slopes and the reset signal staged once,
+    every ``step()`` is forward + loss + temporal-gradient backward (+ Adam)."""
+
+    def __init__(self, cfg: SweptPhasorConfig, device: int = 0, optimizer: bool = True):
+        self.cfg = cfg
+        self.program = swept_phasor_program(cfg, optimizer=optimizer)
+        self.rt = R.HIPLazyRuntime(self.program, device)
+        self.rt.write("slope", cfg.slopes())
+        self.rt.write("reset", cfg.reset())
 
     def step(self) -> None:
         self.rt.runNoCopy()

@@ -53,6 +53,8 @@ K_MEMBRANE_FWD = 27
 K_MEMBRANE_BWD = 28
 K_STREAM_OSC_BANK = 29
 K_STREAM_BIQUAD = 30
+K_TEMPORAL_GRAD_SCAN = 31
+K_SWEPT_PHASOR = 32
 
 KERNEL_NAMES = {v: k[2:].lower() for k, v in globals().items() if k.startswith("K_")}
 

@@ -221,6 +221,39 @@ class BiquadConfig:
         return np.concatenate([np.full(self.B, self.tgt_fc, np.float32), np.full(self.B, self.tgt_Q, np.float32)])
 
 
+# ------------------------------------------------- temporal gradient (a21)
+@dataclass
+class SweptPhasorConfig:
+    """A bank of E swept phasors with learnable sweep rates: the graph of
+    Tests/DGenLazyTests/TemporalGradientTests.swift:24-60 per lane, f[n] =
+    base + slope[e] * time[n] with time = accum(1/sr), phase =
+    statefulPhasor(f, reset), loss = sum (phase - target)^2, or with
+    ``smooth`` sum (sin(2 pi phase) - target)^2 (continuous across the
+    phase's wraps, so finite differences of long runs are meaningful);
+    resets from frame reset_from on (-1: none)."""
+    E: int = 256
+    T: int = 1 << 16
+    sr: float = 44100.0
+    base: float = 80.0
+    target: float = 0.08
+    reset_from: int = -1
+    smooth: bool = True
+    slope_lo: float = 600.0
+    slope_hi: float = 24000.0
+    lr: float = 1e-3
+
+    def slopes(self) -> np.ndarray:
+        """Geometric sweep rates slope_lo .. slope_hi across the lanes."""
+        if self.E == 1:
+            return np.array([self.slope_lo], np.float32)
+        r = np.arange(self.E, dtype=np.float64) / (self.E - 1)
+        return (self.slope_lo * (self.slope_hi / self.slope_lo) ** r).astype(np.float32)
+
+    def reset(self) -> np.ndarray:
+        n = np.arange(self.T)
+        return ((n >= self.reset_from) & (self.reset_from >= 0)).astype(np.float32)
+
+
 # ---------------------------------------------------------------- config 2
 @dataclass
 class StftConfig:

@@ -279,6 +279,28 @@ enum dgen_hip_kernel {
    * [2]=params ([2][B] base | Q) [3]=state [4]=y ([frames][B]) [5]=B
    * [6]=frames */
   DGEN_HIP_K_STREAM_BIQUAD = 30,
+
+  /* ---- temporal gradient of stateful accumulators (phasor, accum):
+   * temporalIncrementGradient, Gradients.swift:209-261, and its three-phase
+   * emission, Emit+TemporalGradient.swift:15-105.  The reset-aware exclusive
+   * suffix scan of the output gradient, per element, from the last frame
+   * down: active = reset[n] > 0 ? 0 : carry; out[n] = active (/ sample rate
+   * for a phasor); carry = g[n] + active.  Chunked in time (the carries
+   * between 256-frame chunks are reassociated).
+   * arg: [0]=g ([T][E]) [1]=reset ([T]) or -1 [2]=out ([T][E]) [3]=E [4]=T
+   *      [5]=workspace (2*C*E + C floats, C = ceil(T/256)) [6]=divide by the
+   *      sample rate (0/1)   farg: [0]=sample rate */
+  DGEN_HIP_K_TEMPORAL_GRAD_SCAN = 31,
+
+  /* Swept-phasor bank forward and loss (TemporalGradientTests.swift:24-60),
+   * one lane per thread: f[n] = base + slope[e] * time[n], the stateful
+   * phasor of f with reset, mse of the phase (or, smooth, of sin(2 pi
+   * phase)) against target: loss partials per lane and the upstream gradient.
+   * arg: [0]=slope ([E]) [1]=time ([T]) [2]=reset ([T]) or -1 [3]=phase
+   *      ([T][E]) or -1 [4]=upstream ([T][E]) [5]=loss partials ([E]) [6]=E
+   *      [7]=T [8]=smooth (0/1)
+   * farg: [0]=sample rate [1]=base frequency [2]=target */
+  DGEN_HIP_K_SWEPT_PHASOR = 32,
 };
 
 /* GEMM epilogues */

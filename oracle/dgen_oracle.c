@@ -45,6 +45,7 @@
 
 #define IS_F32 (sizeof(REAL) == 4)
 #define R_SIN(x) (IS_F32 ? (REAL)sinf((float)(x)) : (REAL)sin((double)(x)))
+#define R_COS(x) (IS_F32 ? (REAL)cosf((float)(x)) : (REAL)cos((double)(x)))
 #define R_SQRT(x) (IS_F32 ? (REAL)sqrtf((float)(x)) : (REAL)sqrt((double)(x)))
 #define R_LOG(x) (IS_F32 ? (REAL)logf((float)(x)) : (REAL)log((double)(x)))
 #define R_EXP(x) (IS_F32 ? (REAL)expf((float)(x)) : (REAL)exp((double)(x)))
@@ -876,10 +877,99 @@ void FN(dgen_oracle_adam)(float* p, const float* g, float* m, float* v, size_t n
 }
 
 /* ------------------------------------------------------------------------ */
+/* Temporal gradient of stateful accumulators (phasor, accum).              */
+/* ------------------------------------------------------------------------ */
+
+/* The reset-aware exclusive suffix scan of Emit+TemporalGradient.swift:56-81
+ * (temporalIncrementGradient, Gradients.swift:209-261): per element, frames
+ * in reverse, active = reset[n] > 0 ? 0 : carry; out[n] = active;
+ * carry = g[n] + active.  out[n] is d(sum of g . y)/d increment[n] for an
+ * accumulator whose output y[n] is the state before frame n's increment.
+ * g, out: [T][E]; reset: [T] or NULL.  fp32, the reference's order. */
+void dgen_oracle_temporal_scan(const float* g, const float* reset, int T, int E, float* out);
+#ifdef ORACLE_COMMON
+void dgen_oracle_temporal_scan(const float* g, const float* reset, int T, int E, float* out) {
+  for (int e = 0; e < E; ++e) {
+    float carry = 0.0f;
+    for (int n = T - 1; n >= 0; --n) {
+      const float active = (reset && reset[n] > 0.0f) ? 0.0f : carry;
+      out[(size_t)n * E + e] = active;
+      carry = g[(size_t)n * E + e] + active;
+    }
+  }
+}
+#endif
+
+/* The swept-phasor bank of Tests/DGenLazyTests/TemporalGradientTests.swift:
+ * 24-60, per lane e: time = accum(1/sr) (fp32, data), frequency
+ * f[n] = base + slope[e] * time[n], phase = statefulPhasor(f, reset) (the
+ * u_phasor / u_accum order of Definitions.swift:96-102, 215-246, in this
+ * build's precision), loss = sum over frames and lanes of
+ * (phase - target)^2 (u_mse, Definitions.swift:206-213), or with smooth = 1 of
+ * (sin(2 pi phase) - target)^2.  reset[n] = 1 for
+ * n >= reset_from (reset_from < 0: never).  With grad != NULL the gradient
+ * d loss / d slope[e]: upstream 2 (phase - target), the temporal scan above
+ * (with the scan's increment gradient divided by sr, the phasor's
+ * scaleBySampleRate), times d f / d slope = time[n], summed over frames.
+ * phase_out (optional): [T][E].  Returns the loss. */
+double FN(dgen_oracle_swept_phasor_step)(const REAL* slope, int E, int T, float sr, float base, float target,
+                                         int reset_from, int smooth, REAL* grad, float* phase_out) {
+  float* time = (float*)malloc(sizeof(float) * T);
+  {
+    float st = 0.0f;
+    const float step = 1.0f / sr; /* Signal.constant(1.0 / sampleRate), a Float */
+    for (int n = 0; n < T; ++n) {
+      float acc = st;
+      float next = acc + step;
+      float w = next - floorf(next / 1.0f) * 1.0f;
+      if (w >= 1.0f) w = w - 1.0f;
+      st = w;
+      time[n] = acc;
+    }
+  }
+  REAL* gup = grad ? (REAL*)malloc(sizeof(REAL) * (size_t)T * E) : NULL;
+  double loss = 0.0;
+  for (int e = 0; e < E; ++e) {
+    REAL ph = 0;
+    for (int n = 0; n < T; ++n) {
+      const int rs = reset_from >= 0 && n >= reset_from;
+      const REAL f = (REAL)base + slope[e] * (REAL)time[n];
+      const REAL acc = ph;
+      REAL next = rs ? (REAL)0 : acc + f / (REAL)sr;
+      REAL w = next - R_FLOOR(next);
+      if (w >= (REAL)1) w = w - (REAL)1;
+      if (rs) w = 0;
+      ph = w;
+      /* smooth: the loss reads sin(2 pi phase) (CRenderer.swift:825-827),
+       * which the phase's wrap leaves continuous */
+      const REAL v = smooth ? R_SIN(acc * TWO_PI_F32) : acc;
+      const REAL d = v - (REAL)target;
+      loss += (double)(d * d);
+      if (phase_out) phase_out[(size_t)n * E + e] = (float)acc;
+      if (gup) gup[(size_t)n * E + e] = smooth ? (REAL)2 * d * (R_COS(acc * TWO_PI_F32) * TWO_PI_F32) : (REAL)2 * d;
+    }
+  }
+  if (grad) {
+    for (int e = 0; e < E; ++e) {
+      REAL carry = 0, sum = 0;
+      for (int n = T - 1; n >= 0; --n) {
+        const int rs = reset_from >= 0 && n >= reset_from;
+        const REAL active = rs ? (REAL)0 : carry;
+        sum = sum + (active / (REAL)sr) * (REAL)time[n];
+        carry = gup[(size_t)n * E + e] + active;
+      }
+      grad[e] = sum;
+    }
+    free(gup);
+  }
+  free(time);
+  return loss;
+}
+
+/* ------------------------------------------------------------------------ */
 /* Config 4: tensor biquad bank, forward and BPTT adjoint.                  */
 /* ------------------------------------------------------------------------ */
 
-#define R_COS(x) (IS_F32 ? (REAL)cosf((float)(x)) : (REAL)cos((double)(x)))
 
 /* w0 per Hz: the reference hardcodes 2*pi/44100 as a Float constant
  * (Sources/DGen/HigherOps.swift:446-447), whatever the graph's sample rate. */

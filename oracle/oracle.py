@@ -74,6 +74,12 @@ def lib(name: str = "liboracle.so") -> ctypes.CDLL:
                                                         vp, vp], ctypes.c_double)
             _sig(L, "dgen_oracle_stft_step" + sfx, [_f32p, _c_int, _c_int, _c_int, _c_int, _f32p, rp, vp, vp],
                  ctypes.c_double)
+            _sig(L, "dgen_oracle_swept_phasor_step" + sfx,
+                 [rp_(sfx), _c_int, _c_int, _c_float, _c_float, _c_float, _c_int, _c_int, ctypes.c_void_p,
+                  ctypes.c_void_p],
+                 ctypes.c_double)
+        if hasattr(L, "dgen_oracle_temporal_scan"):
+            _sig(L, "dgen_oracle_temporal_scan", [_f32p, ctypes.c_void_p, _c_int, _c_int, _f32p])
         if hasattr(L, "dgen_oracle_noise_stream"):
             _sig(L, "dgen_oracle_noise_stream", [_c_int, _f32p])
             _sig(L, "dgen_oracle_phasor", [_f32p, _c_int, _c_float, _f32p])
@@ -111,6 +117,32 @@ def oscbank_stream(freqs, amps, sr, pole, frames, stateful, state, prec="f32"):
     _fn("dgen_oracle_oscbank_stream", prec)(_f(freqs), _f(amps), len(freqs), sr, pole, frames, int(stateful), state,
                                             out)
     return out
+
+
+# -- temporal gradient of stateful accumulators -----------------------------
+def temporal_scan(g, reset=None):
+    """Reset-aware exclusive suffix scan of g [T][E] (reset [T] or None)."""
+    g = _f(g)
+    T, E = g.shape
+    out = np.zeros((T, E), np.float32)
+    r = None if reset is None else _f(reset)
+    lib().dgen_oracle_temporal_scan(g, None if r is None else r.ctypes.data_as(ctypes.c_void_p), T, E, out)
+    return out
+
+
+def swept_phasor_step(slope, T, sr, base, target, reset_from=-1, smooth=False, grad=True, want_phase=False,
+                      prec="f64"):
+    """Swept-phasor bank (loss on the phase, or with smooth on sin(2 pi
+    phase)): returns (loss, d loss / d slope or None, phase [T][E] or None)."""
+    dt = np.float32 if prec == "f32" else np.float64
+    slope = np.ascontiguousarray(slope, dt)
+    E = len(slope)
+    g = np.zeros(E, dt) if grad else None
+    ph = np.zeros((T, E), np.float32) if want_phase else None
+    loss = _fn("dgen_oracle_swept_phasor_step", prec)(slope, E, T, sr, base, target, reset_from, int(smooth),
+                                                      g.ctypes.data_as(ctypes.c_void_p) if grad else None,
+                                                      ph.ctypes.data_as(ctypes.c_void_p) if want_phase else None)
+    return loss, g, ph
 
 
 # -- config 3 -------------------------------------------------------------
