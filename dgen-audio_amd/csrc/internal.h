@@ -141,6 +141,11 @@ int launch_stream_osc_bank(const Launch&, const dgen_hip_op&);
 int launch_stream_biquad(const Launch&, const dgen_hip_op&);
 int launch_temporal_grad_scan(const Launch&, const dgen_hip_op&);
 int launch_swept_phasor(const Launch&, const dgen_hip_op&);
+int launch_svf_chunk(const Launch&, const dgen_hip_op&);
+int launch_svf_fwd(const Launch&, const dgen_hip_op&);
+int launch_svf_seq(const Launch&, const dgen_hip_op&);
+int launch_svf_adj_chunk(const Launch&, const dgen_hip_op&);
+int launch_svf_bwd(const Launch&, const dgen_hip_op&);
 
 // Sum over the 64 lanes of a wave (butterfly; every lane gets the total).
 __device__ __forceinline__ float wave_sum(float v) {

@@ -32,6 +32,7 @@
 // of lane k at frame n is base[k] * m[n] (m: the shared modulation signal).
 #include <mutex>
 
+#include "dev_math.h"
 #include "internal.h"
 
 namespace dgen {
@@ -45,16 +46,6 @@ constexpr int kCarryGroups = 32;  // chunk groups per lane in the carry scan
 // 2*pi/44100 as the Float constant the reference hardcodes
 // (HigherOps.swift:446-447), whatever the sample rate.
 constexpr float kW0PerHz = 0.00014247585730565955f;
-
-__device__ __forceinline__ float rcp_rn(float d) {
-  const float r = __builtin_amdgcn_rcpf(d);
-  return __builtin_fmaf(__builtin_fmaf(-d, r, 1.0f), r, r);
-}
-// x / d with rd = RN(1/d): one Markstein correction of x*rd.
-__device__ __forceinline__ float div_rn(float x, float d, float rd) {
-  const float q = x * rd;
-  return __builtin_fmaf(__builtin_fmaf(-q, d, x), rd, q);
-}
 
 struct Coef {
   float c, s, alpha, r, P, D;  // cos w, sin w, div18, recip24, div11, add10

@@ -1,0 +1,599 @@
+// Two-cell ZDF state-variable filter bank (low-pass) and its BPTT adjoint.
+//
+// Reference: the hand-rolled Cytomic/TPT SVF of the MonologueVoice filter,
+// Tests/DGenLazyTests/SVFBPTTScratchTests.swift:21-34 (history cells ic1,
+// ic2 with pass-through writes, saturation s = ic / (1 + |kSat ic|)), driven
+// as at :56-63: fc = (fBase [* m] + envelope).clip(20, 20000),
+// g = tan((pi * fc) / sr), kDamp = 1 / res.  Per lane and frame:
+//   a1 = 1 / (1 + g (g + kd)), a2 = g a1, v3 = x - s2, v1 = a1 s1 + a2 v3,
+//   ic1 <- 2 v1 - s1, v1p = (ic1 + s1) / 2, v2 = s2 + g v1p,
+//   ic2 <- 2 v2 - s2, y = (ic2 + s2) / 2.
+// The reference runs it as one sequential frame loop per lane and, for the
+// gradient, a reverse loop over stored per-frame values
+// (BPTTEmission.swift:133-160).
+//
+// Here, with kSat the constant 0 (a linear recurrence in (ic1, ic2)), time
+// is parallel like the biquad bank: frames cut into chunks of L,
+//   k_svf_chunk      per (lane, chunk): the chunk's zero-state result and its
+//                    responses to the two unit states, in fp64 on the fp32
+//                    coefficients (an affine 2x2 map per chunk)
+//   DGEN_HIP_K_BIQUAD_CARRY composes the maps per lane -> every chunk's state
+//   k_svf_fwd        each chunk re-run in fp32 from its state: y, the cells
+//                    entering every frame, per-chunk loss partials
+// With a learnable kSat the forward is not affine and runs one lane per
+// thread over all frames (k_svf_seq, the reference's schedule).  The adjoint
+// of the cells IS affine in both cases (its Jacobians read the stored
+// cells), so the backward is always chunked:
+//   k_svf_adj_chunk  per (lane, chunk), reverse: zero-carry adjoint and unit
+//                    responses (fp64), then the carry kernel in reverse
+//   k_svf_bwd        each chunk's adjoint replayed in fp32 from its carry,
+//                    chained through the coefficient nodes to per-chunk
+//                    gradient partials [C][P][B] (base, res[, kSat]) and
+//                    optionally d loss / d x.
+// Every frame computes in the reference graph's node order with IEEE fp32
+// (no contraction), like the CPU restatement it is checked against.
+//
+// Layout: x, y, target [T][B]; cells [2][T][B] (ic1 plane, ic2 plane);
+// params [P][B] = base | res (| kSat), P = 2 linear, 3 saturating; m and the
+// envelope are per-frame signals shared by all lanes ([T], optional).
+#pragma clang fp contract(off)
+
+#include "dev_math.h"
+#include "internal.h"
+
+namespace dgen {
+namespace {
+
+constexpr int kThreads = 256;   // lanes per workgroup of the chunked kernels
+constexpr int kSeqThreads = 64;  // lanes per workgroup of the sequential forward
+constexpr int kG = 8;           // frames per prefetch group
+constexpr float kPi = 3.14159265358979323846f;
+
+struct Ctl {
+  const float* m;    // [T] cutoff scale or null (1)
+  const float* env;  // [T] cutoff offset or null (0)
+};
+
+struct SvfK {
+  float g, a1, a2, u, Q;
+  bool pass;  // the clip passes the cutoff's gradient
+};
+
+// clip = max(min(v, 20000), 20) (Functions.swift:780-782); min passes its
+// input's gradient where v <= hi, max where min(v, hi) >= lo
+// (Gradients.swift:386-410).
+__device__ __forceinline__ SvfK svf_coef(float raw, float kd, float sr, float rsr) {
+  SvfK K;
+  const float lo = raw <= 20000.0f ? raw : 20000.0f;
+  const float fc = lo >= 20.0f ? lo : 20.0f;
+  K.pass = raw <= 20000.0f && lo >= 20.0f;
+  K.u = div_rn(kPi * fc, sr, rsr);
+  K.g = tanf(K.u);
+  K.Q = 1.0f + K.g * (K.g + kd);
+  K.a1 = rcp_rn(K.Q);
+  K.a2 = K.g * K.a1;
+  return K;
+}
+
+__device__ __forceinline__ float raw_cutoff(float base, float m, float e, const Ctl& ctl) {
+  const float v = base * m;
+  return ctl.env ? v + e : v;
+}
+
+// One frame of the fp32 program: cells (c1, c2) -> next; returns y.
+template <bool SAT>
+__device__ __forceinline__ float svf_step(const SvfK& K, float ks, float x, float& c1, float& c2) {
+  const float s1 = SAT ? c1 / (1.0f + fabsf(ks * c1)) : c1;
+  const float s2 = SAT ? c2 / (1.0f + fabsf(ks * c2)) : c2;
+  const float v3 = x - s2;
+  const float v1 = K.a1 * s1 + K.a2 * v3;
+  const float ic1 = 2.0f * v1 - s1;
+  const float v1p = (ic1 + s1) * 0.5f;
+  const float v2 = s2 + K.g * v1p;
+  const float ic2 = 2.0f * v2 - s2;
+  c1 = ic1;
+  c2 = ic2;
+  return (ic2 + s2) * 0.5f;
+}
+
+// Streams frames [n0, n1) forwards (REV: n1-1 down to n0): f(n, v, m, e)
+// with v[s] = src[s][n][k], m = m[n] (1) and e = env[n] (0).  The next
+// group's loads are issued before the current group is processed.
+template <int NS, bool REV, class F>
+__device__ __forceinline__ void walk(const float* const (&src)[NS], const Ctl& ctl, int B, int k, int n0, int n1,
+                                     F&& f) {
+  const int cnt = n1 - n0;
+  if (cnt <= 0) return;
+  auto frame = [&](int i) { return REV ? n1 - 1 - i : n0 + i; };
+  float cv[kG][NS], cm[kG], ce[kG];
+  auto load = [&](int i, float (&v)[kG][NS], float (&mv)[kG], float (&ev)[kG]) {
+#pragma unroll
+    for (int j = 0; j < kG; ++j) {
+      const int n = frame(min(i + j, cnt - 1));
+#pragma unroll
+      for (int s = 0; s < NS; ++s) v[j][s] = src[s][(size_t)n * B + k];
+      mv[j] = ctl.m ? ctl.m[n] : 1.0f;
+      ev[j] = ctl.env ? ctl.env[n] : 0.0f;
+    }
+  };
+  load(0, cv, cm, ce);
+  int i = 0;
+  for (; i + kG <= cnt; i += kG) {
+    float nv[kG][NS], nm[kG], ne[kG];
+    load(i + kG, nv, nm, ne);
+#pragma unroll
+    for (int j = 0; j < kG; ++j) f(frame(i + j), cv[j], cm[j], ce[j]);
+#pragma unroll
+    for (int j = 0; j < kG; ++j) {
+#pragma unroll
+      for (int s = 0; s < NS; ++s) cv[j][s] = nv[j][s];
+      cm[j] = nm[j];
+      ce[j] = ne[j];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kG; ++j)
+    if (i + j < cnt) f(frame(i + j), cv[j], cm[j], ce[j]);
+}
+
+struct Lane {
+  int k, c, n0, n1;
+  float base, res, kd, ks, rsr;
+};
+
+__device__ __forceinline__ bool lane_chunk(const float* __restrict__ prm, int B, int T, int L, float sr, bool sat,
+                                           Lane& l) {
+  l.k = blockIdx.y * kThreads + threadIdx.x;
+  if (l.k >= B) return false;
+  l.c = blockIdx.x;
+  l.n0 = l.c * L;
+  l.n1 = min(T, l.n0 + L);
+  l.base = prm[l.k];
+  l.res = prm[B + l.k];
+  l.kd = 1.0f / l.res;
+  l.ks = sat ? prm[2 * B + l.k] : 0.0f;
+  l.rsr = rcp_rn(sr);
+  return true;
+}
+
+// ------------------------------------------------------------ forward scan
+__global__ __launch_bounds__(kThreads) void k_svf_chunk(const float* __restrict__ x, Ctl ctl,
+                                                        const float* __restrict__ prm, double* __restrict__ summ,
+                                                        int B, int T, int L, float sr) {
+  Lane l;
+  if (!lane_chunk(prm, B, T, L, sr, false, l)) return;
+  double p1 = 0.0, p2 = 0.0, u1 = 1.0, u2 = 0.0, w1 = 0.0, w2 = 1.0;
+  auto adv = [](double a1, double a2, double g, double xx, double& c1, double& c2) {
+    const double v3 = xx - c2;
+    const double v1 = a1 * c1 + a2 * v3;
+    const double ic1 = 2.0 * v1 - c1;
+    const double v1p = (ic1 + c1) * 0.5;
+    const double v2 = c2 + g * v1p;
+    c1 = ic1;
+    c2 = 2.0 * v2 - c2;
+  };
+  const float* const src[1] = {x};
+  walk<1, false>(src, ctl, B, l.k, l.n0, l.n1, [&](int, const float* v, float m, float e) {
+    const SvfK K = svf_coef(raw_cutoff(l.base, m, e, ctl), l.kd, sr, l.rsr);
+    const double a1 = K.a1, a2 = K.a2, g = K.g;
+    adv(a1, a2, g, v[0], p1, p2);
+    adv(a1, a2, g, 0.0, u1, u2);
+    adv(a1, a2, g, 0.0, w1, w2);
+  });
+  double* o = summ + (size_t)l.c * 6 * B + l.k;
+  o[0] = p1;
+  o[(size_t)B] = p2;
+  o[(size_t)2 * B] = u1;
+  o[(size_t)3 * B] = u2;
+  o[(size_t)4 * B] = w1;
+  o[(size_t)5 * B] = w2;
+}
+
+template <bool LOSS>
+__global__ __launch_bounds__(kThreads) void k_svf_fwd(const float* __restrict__ x, Ctl ctl,
+                                                      const float* __restrict__ prm, const float* __restrict__ init,
+                                                      float* __restrict__ y, float* __restrict__ cells,
+                                                      const float* __restrict__ tgt, float* __restrict__ lossp, int B,
+                                                      int T, int L, float sr) {
+  Lane l;
+  if (!lane_chunk(prm, B, T, L, sr, false, l)) return;
+  const int k = l.k;
+  float c1 = init[(size_t)l.c * 2 * B + k], c2 = init[((size_t)l.c * 2 + 1) * B + k];
+  float ls = 0.0f;
+  const size_t plane = (size_t)T * B;
+  auto step = [&](int n, const float* v, float m, float e) {
+    const SvfK K = svf_coef(raw_cutoff(l.base, m, e, ctl), l.kd, sr, l.rsr);
+    const size_t i = (size_t)n * B + k;
+    if (cells) {
+      cells[i] = c1;
+      cells[plane + i] = c2;
+    }
+    const float out = svf_step<false>(K, 0.0f, v[0], c1, c2);
+    y[i] = out;
+    if constexpr (LOSS) {
+      const float d = out - v[1];
+      ls += d * d;
+    }
+  };
+  if constexpr (LOSS) {
+    const float* const src[2] = {x, tgt};
+    walk<2, false>(src, ctl, B, k, l.n0, l.n1, step);
+    lossp[(size_t)l.c * B + k] = ls;
+  } else {
+    const float* const src[1] = {x};
+    walk<1, false>(src, ctl, B, k, l.n0, l.n1, step);
+  }
+}
+
+// Saturating forward: one lane per thread over all frames, from the state
+// cell ([2][B], or zero) and back into it; loss partials per L-frame chunk.
+// sanitize: out stores map non-finite values to 0 (CRenderer.swift:1021-1039).
+template <bool LOSS>
+__global__ __launch_bounds__(kSeqThreads) void k_svf_seq(const float* __restrict__ x, Ctl ctl,
+                                                         const float* __restrict__ prm, float* __restrict__ state,
+                                                         int reset, float* __restrict__ y, float* __restrict__ cells,
+                                                         const float* __restrict__ tgt, float* __restrict__ lossp,
+                                                         int B, int T, int L, float sr, int sanitize) {
+  const int k = blockIdx.x * kSeqThreads + threadIdx.x;
+  if (k >= B) return;
+  const float base = prm[k], kd = 1.0f / prm[B + k], ks = prm[2 * B + k], rsr = rcp_rn(sr);
+  float c1 = 0.0f, c2 = 0.0f;
+  if (state && !reset) {
+    c1 = state[k];
+    c2 = state[B + k];
+  }
+  const size_t plane = (size_t)T * B;
+  const int C = (T + L - 1) / L;
+  for (int c = 0; c < C; ++c) {
+    float ls = 0.0f;
+    auto step = [&](int n, const float* v, float m, float e) {
+      const SvfK K = svf_coef(raw_cutoff(base, m, e, ctl), kd, sr, rsr);
+      const size_t i = (size_t)n * B + k;
+      if (cells) {
+        cells[i] = c1;
+        cells[plane + i] = c2;
+      }
+      const float out = svf_step<true>(K, ks, v[0], c1, c2);
+      y[i] = sanitize && !isfinite(out) ? 0.0f : out;
+      if constexpr (LOSS) {
+        const float d = out - v[1];
+        ls += d * d;
+      }
+    };
+    const int n0 = c * L, n1 = min(T, n0 + L);
+    if constexpr (LOSS) {
+      const float* const src[2] = {x, tgt};
+      walk<2, false>(src, ctl, B, k, n0, n1, step);
+      lossp[(size_t)c * B + k] = ls;
+    } else {
+      const float* const src[1] = {x};
+      walk<1, false>(src, ctl, B, k, n0, n1, step);
+    }
+  }
+  if (state) {
+    state[k] = c1;
+    state[B + k] = c2;
+  }
+}
+
+// ------------------------------------------------------------ adjoint scan
+// d s / d c for s = c / (1 + |ks c|): 1/D - (c/D^2) sgn(ks c) ks (1 when linear).
+__device__ __forceinline__ float sgn(float v) { return v > 0.0f ? 1.0f : (v < 0.0f ? -1.0f : 0.0f); }
+
+template <bool SAT>
+__global__ __launch_bounds__(kThreads) void k_svf_adj_chunk(Ctl ctl, const float* __restrict__ prm,
+                                                            const float* __restrict__ y,
+                                                            const float* __restrict__ tgt,
+                                                            const float* __restrict__ cells,
+                                                            double* __restrict__ summ, int B, int T, int L, float sr) {
+  Lane l;
+  if (!lane_chunk(prm, B, T, L, sr, SAT, l)) return;
+  double l1 = 0.0, l2 = 0.0, u1 = 1.0, u2 = 0.0, w1 = 0.0, w2 = 1.0;
+  // the cells' adjoint through one frame (the reverse of svf_step)
+  auto back = [](double a1, double a2, double g, double J1, double J2, double e, double& L1, double& L2) {
+    const double ic2_b = 0.5 * e + L2;
+    const double v2_b = 2.0 * ic2_b;
+    double s2_b = (0.5 * e - ic2_b) + v2_b;
+    const double v1p_b = v2_b * g;
+    const double ic1_b = L1 + 0.5 * v1p_b;
+    double s1_b = 0.5 * v1p_b - ic1_b;
+    const double v1_b = 2.0 * ic1_b;
+    s1_b += v1_b * a1;
+    s2_b -= v1_b * a2;
+    L1 = s1_b * J1;
+    L2 = s2_b * J2;
+  };
+  auto frame = [&](const float* v, float m, float e) {
+    const SvfK K = svf_coef(raw_cutoff(l.base, m, e, ctl), l.kd, sr, l.rsr);
+    double J1 = 1.0, J2 = 1.0;
+    if constexpr (SAT) {
+      const double ks = l.ks, c1 = v[2], c2 = v[3];
+      const double D1 = 1.0 + fabs(ks * c1), D2 = 1.0 + fabs(ks * c2);
+      J1 = 1.0 / D1 - (c1 / (D1 * D1)) * sgn(l.ks * v[2]) * ks;
+      J2 = 1.0 / D2 - (c2 / (D2 * D2)) * sgn(l.ks * v[3]) * ks;
+    }
+    const double a1 = K.a1, a2 = K.a2, g = K.g;
+    const double ee = 2.0 * ((double)v[0] - (double)v[1]);
+    back(a1, a2, g, J1, J2, ee, l1, l2);
+    back(a1, a2, g, J1, J2, 0.0, u1, u2);
+    back(a1, a2, g, J1, J2, 0.0, w1, w2);
+  };
+  const size_t plane = (size_t)T * B;
+  if constexpr (SAT) {
+    const float* const src[4] = {y, tgt, cells, cells + plane};
+    walk<4, true>(src, ctl, B, l.k, l.n0, l.n1, [&](int, const float* v, float m, float e) { frame(v, m, e); });
+  } else {
+    const float* const src[2] = {y, tgt};
+    walk<2, true>(src, ctl, B, l.k, l.n0, l.n1, [&](int, const float* v, float m, float e) { frame(v, m, e); });
+  }
+  double* o = summ + (size_t)l.c * 6 * B + l.k;
+  o[0] = l1;
+  o[(size_t)B] = l2;
+  o[(size_t)2 * B] = u1;
+  o[(size_t)3 * B] = u2;
+  o[(size_t)4 * B] = w1;
+  o[(size_t)5 * B] = w2;
+}
+
+// Each chunk's adjoint replayed from its carry in fp32 (node order of the
+// CPU restatement), with the chain rule through the coefficient nodes:
+// a2 = g a1, a1 = 1/Q, Q = 1 + g (g + kd), g = tan(u) (d/du = 1/(cos u)^2),
+// u = (pi fc) / sr, fc = clip(base m + env), kd = 1/res.
+// gpart[c][0][k] = d/d base, [1] = d/d res, [2] = d/d kSat (saturating).
+template <bool SAT>
+__global__ __launch_bounds__(kThreads) void k_svf_bwd(const float* __restrict__ x, Ctl ctl,
+                                                      const float* __restrict__ prm, const float* __restrict__ y,
+                                                      const float* __restrict__ tgt, const float* __restrict__ cells,
+                                                      const float* __restrict__ ainit, float* __restrict__ gpart,
+                                                      float* __restrict__ xbar, int B, int T, int L, float sr) {
+  Lane l;
+  if (!lane_chunk(prm, B, T, L, sr, SAT, l)) return;
+  const int k = l.k;
+  float L1 = ainit[(size_t)l.c * 2 * B + k], L2 = ainit[((size_t)l.c * 2 + 1) * B + k];
+  float gb = 0.0f, gkd = 0.0f, gks = 0.0f;
+  const float ks = l.ks;
+  const size_t plane = (size_t)T * B;
+  const float* const src[5] = {x, y, tgt, cells, cells + plane};
+  walk<5, true>(src, ctl, B, k, l.n0, l.n1, [&](int n, const float* v, float m, float e) {
+    const SvfK K = svf_coef(raw_cutoff(l.base, m, e, ctl), l.kd, sr, l.rsr);
+    const float c1 = v[3], c2 = v[4];
+    const float D1 = 1.0f + fabsf(ks * c1), D2 = 1.0f + fabsf(ks * c2);
+    const float s1 = SAT ? c1 / D1 : c1, s2 = SAT ? c2 / D2 : c2;
+    const float v3 = v[0] - s2;
+    const float v1 = K.a1 * s1 + K.a2 * v3;
+    const float ic1 = 2.0f * v1 - s1;
+    const float v1p = (ic1 + s1) * 0.5f;
+    const float ee = 2.0f * (v[1] - v[2]);
+    const float ic2_b = 0.5f * ee + L2;
+    float s2_b = 0.5f * ee - ic2_b;
+    const float v2_b = 2.0f * ic2_b;
+    s2_b += v2_b;
+    float g_b = v2_b * v1p;
+    const float v1p_b = v2_b * K.g;
+    const float ic1_b = L1 + 0.5f * v1p_b;
+    float s1_b = 0.5f * v1p_b - ic1_b;
+    const float v1_b = 2.0f * ic1_b;
+    float a1_b = v1_b * s1;
+    s1_b += v1_b * K.a1;
+    const float a2_b = v1_b * v3;
+    const float v3_b = v1_b * K.a2;
+    if (xbar) xbar[(size_t)n * B + k] = v3_b;
+    s2_b -= v3_b;
+    if constexpr (SAT) {
+      const float q1 = (c1 / (D1 * D1)) * sgn(ks * c1), q2 = (c2 / (D2 * D2)) * sgn(ks * c2);
+      L1 = s1_b * (1.0f / D1 - q1 * ks);
+      L2 = s2_b * (1.0f / D2 - q2 * ks);
+      gks += -(s1_b * q1 * c1) - s2_b * q2 * c2;
+    } else {
+      L1 = s1_b;
+      L2 = s2_b;
+    }
+    g_b += a2_b * K.a1;
+    a1_b += a2_b * K.g;
+    const float Q_b = -a1_b / (K.Q * K.Q);
+    g_b += Q_b * ((K.g + l.kd) + K.g);
+    gkd += Q_b * K.g;
+    const float cu = cosf(K.u);
+    const float u_b = g_b * (1.0f / (cu * cu));
+    const float fc_b = div_rn(u_b, sr, l.rsr) * kPi;
+    if (K.pass) gb += fc_b * m;
+  });
+  const int P = SAT ? 3 : 2;
+  gpart[((size_t)l.c * P) * B + k] = gb;
+  gpart[((size_t)l.c * P + 1) * B + k] = gkd * (-1.0f / (l.res * l.res));
+  if constexpr (SAT) gpart[((size_t)l.c * P + 2) * B + k] = gks;
+}
+
+struct SvfShape {
+  int64_t B, T, L, C;
+};
+
+int svf_shape(int64_t B, int64_t T, int64_t L, SvfShape& s, const char* who) {
+  DGEN_REQUIRE(B > 0 && B <= (1 << 20) && T > 0 && T < (1ll << 30) && L > 0 && L <= (1 << 20),
+               "%s: B %lld T %lld L %lld", who, (long long)B, (long long)T, (long long)L);
+  DGEN_REQUIRE(B * T < (1ll << 40), "%s: B*T too large", who);
+  s = SvfShape{B, T, L, (T + L - 1) / L};
+  DGEN_REQUIRE(s.C <= 65535, "%s: %lld chunks exceeds the grid limit (raise the chunk length)", who,
+               (long long)s.C);
+  return 0;
+}
+
+dim3 svf_grid(const SvfShape& s) { return dim3((unsigned)s.C, (unsigned)((s.B + kThreads - 1) / kThreads)); }
+
+double* dcell(const Launch& L, int64_t off) { return reinterpret_cast<double*>(cell(L, off)); }
+
+int svf_ctl(const Launch& L, int64_t m, int64_t env, int64_t T, const char* who, Ctl& ctl) {
+  if (m >= 0) DGEN_CHECK_CELL(L, m, T, who);
+  if (env >= 0) DGEN_CHECK_CELL(L, env, T, who);
+  ctl.m = m >= 0 ? cell(L, m) : nullptr;
+  ctl.env = env >= 0 ? cell(L, env) : nullptr;
+  return 0;
+}
+
+int svf_rate(const Launch& L, float rendered, const char* who, float& sr) {
+  sr = host_rate(L, rendered);
+  DGEN_REQUIRE(sr > 0.f && sr < 1e30f, "%s: sample rate %g", who, (double)sr);
+  return 0;
+}
+
+}  // namespace
+
+int launch_svf_chunk(const Launch& L, const dgen_hip_op& op) {
+  // arg: [0]=x [1]=mod or -1 [2]=env or -1 [3]=params ([2][B]) [4]=summary ([C][6][B] fp64) [5]=B [6]=T [7]=L
+  const int64_t x = op.arg[0], prm = op.arg[3], summ = op.arg[4];
+  SvfShape s;
+  if (int rc = svf_shape(op.arg[5], op.arg[6], op.arg[7], s, "svf_chunk")) return rc;
+  Ctl ctl{};
+  if (int rc = svf_ctl(L, op.arg[1], op.arg[2], s.T, "svf_chunk.mod/env", ctl)) return rc;
+  float sr;
+  if (int rc = svf_rate(L, op.farg[0], "svf_chunk", sr)) return rc;
+  DGEN_CHECK_CELL(L, x, s.B * s.T, "svf_chunk.x");
+  DGEN_CHECK_CELL(L, prm, 2 * s.B, "svf_chunk.params");
+  DGEN_CHECK_CELL(L, summ, 12 * s.C * s.B, "svf_chunk.summary");
+  DGEN_REQUIRE(summ % 2 == 0, "svf_chunk: summary cell must be 8-byte aligned");
+  if (L.dry) return 0;
+  hipLaunchKernelGGL(k_svf_chunk, svf_grid(s), dim3(kThreads), 0, L.stream, cell(L, x), ctl, cell(L, prm),
+                     dcell(L, summ), (int)s.B, (int)s.T, (int)s.L, sr);
+  DGEN_LAUNCH_CHECK("k_svf_chunk");
+  return 0;
+}
+
+int launch_svf_fwd(const Launch& L, const dgen_hip_op& op) {
+  // arg: [0]=x [1]=mod [2]=env [3]=params ([2][B]) [4]=init ([C][2][B]) [5]=y [6]=cells ([2][T][B]) or -1
+  //      [7]=target or -1 [8]=loss partials ([C][B]) or -1 [9]=B [10]=T [11]=L
+  const int64_t x = op.arg[0], prm = op.arg[3], init = op.arg[4], y = op.arg[5], cl = op.arg[6], tgt = op.arg[7],
+                lossp = op.arg[8];
+  SvfShape s;
+  if (int rc = svf_shape(op.arg[9], op.arg[10], op.arg[11], s, "svf_fwd")) return rc;
+  Ctl ctl{};
+  if (int rc = svf_ctl(L, op.arg[1], op.arg[2], s.T, "svf_fwd.mod/env", ctl)) return rc;
+  float sr;
+  if (int rc = svf_rate(L, op.farg[0], "svf_fwd", sr)) return rc;
+  DGEN_CHECK_CELL(L, x, s.B * s.T, "svf_fwd.x");
+  DGEN_CHECK_CELL(L, prm, 2 * s.B, "svf_fwd.params");
+  DGEN_CHECK_CELL(L, init, 2 * s.C * s.B, "svf_fwd.init");
+  DGEN_CHECK_CELL(L, y, s.B * s.T, "svf_fwd.y");
+  if (cl >= 0) DGEN_CHECK_CELL(L, cl, 2 * s.B * s.T, "svf_fwd.cells");
+  DGEN_REQUIRE((tgt >= 0) == (lossp >= 0), "svf_fwd: target and loss partials go together");
+  if (tgt >= 0) {
+    DGEN_CHECK_CELL(L, tgt, s.B * s.T, "svf_fwd.target");
+    DGEN_CHECK_CELL(L, lossp, s.C * s.B, "svf_fwd.loss_partials");
+  }
+  if (L.dry) return 0;
+  float* cp = cl >= 0 ? cell(L, cl) : nullptr;
+  if (tgt >= 0)
+    hipLaunchKernelGGL(k_svf_fwd<true>, svf_grid(s), dim3(kThreads), 0, L.stream, cell(L, x), ctl, cell(L, prm),
+                       cell(L, init), cell(L, y), cp, cell(L, tgt), cell(L, lossp), (int)s.B, (int)s.T, (int)s.L, sr);
+  else
+    hipLaunchKernelGGL(k_svf_fwd<false>, svf_grid(s), dim3(kThreads), 0, L.stream, cell(L, x), ctl, cell(L, prm),
+                       cell(L, init), cell(L, y), cp, nullptr, nullptr, (int)s.B, (int)s.T, (int)s.L, sr);
+  DGEN_LAUNCH_CHECK("k_svf_fwd");
+  return 0;
+}
+
+int launch_svf_seq(const Launch& L, const dgen_hip_op& op) {
+  // arg: [0]=x [1]=mod [2]=env [3]=params ([3][B]) [4]=state ([2][B]) or -1 [5]=y [6]=cells or -1
+  //      [7]=target or -1 [8]=loss partials ([C][B]) or -1 [9]=B [10]=T [11]=L [12]=sanitize
+  // As DGEN_HIP_K_STREAM_SVF: state required, no cells or loss, and a run
+  // processes the first frame_count frames.
+  const int64_t x = op.arg[0], prm = op.arg[3], st = op.arg[4], y = op.arg[5], cl = op.arg[6], tgt = op.arg[7],
+                lossp = op.arg[8];
+  const bool stream = op.kernel == DGEN_HIP_K_STREAM_SVF;
+  SvfShape s;
+  if (int rc = svf_shape(op.arg[9], op.arg[10], op.arg[11], s, "svf_seq")) return rc;
+  const int64_t T = stream ? std::min<int64_t>(s.T, L.frames) : s.T;
+  DGEN_REQUIRE(!stream || (st >= 0 && cl < 0 && tgt < 0), "stream_svf: needs a state cell, stores no cells or loss");
+  Ctl ctl{};
+  if (int rc = svf_ctl(L, op.arg[1], op.arg[2], s.T, "svf_seq.mod/env", ctl)) return rc;
+  float sr;
+  if (int rc = svf_rate(L, op.farg[0], "svf_seq", sr)) return rc;
+  DGEN_CHECK_CELL(L, x, s.B * s.T, "svf_seq.x");
+  DGEN_CHECK_CELL(L, prm, 3 * s.B, "svf_seq.params");
+  if (st >= 0) DGEN_CHECK_CELL(L, st, 2 * s.B, "svf_seq.state");
+  DGEN_CHECK_CELL(L, y, s.B * s.T, "svf_seq.y");
+  if (cl >= 0) DGEN_CHECK_CELL(L, cl, 2 * s.B * s.T, "svf_seq.cells");
+  DGEN_REQUIRE((tgt >= 0) == (lossp >= 0), "svf_seq: target and loss partials go together");
+  if (tgt >= 0) {
+    DGEN_CHECK_CELL(L, tgt, s.B * s.T, "svf_seq.target");
+    DGEN_CHECK_CELL(L, lossp, s.C * s.B, "svf_seq.loss_partials");
+  }
+  if (L.dry) return 0;
+  const dim3 grid((unsigned)((s.B + kSeqThreads - 1) / kSeqThreads));
+  float* sp = st >= 0 ? cell(L, st) : nullptr;
+  float* cp = cl >= 0 ? cell(L, cl) : nullptr;
+  const int reset = stream && L.reset ? 1 : 0, san = op.arg[12] ? 1 : 0;
+  if (tgt >= 0)
+    hipLaunchKernelGGL(k_svf_seq<true>, grid, dim3(kSeqThreads), 0, L.stream, cell(L, x), ctl, cell(L, prm), sp,
+                       reset, cell(L, y), cp, cell(L, tgt), cell(L, lossp), (int)s.B, (int)T, (int)s.L, sr, san);
+  else
+    hipLaunchKernelGGL(k_svf_seq<false>, grid, dim3(kSeqThreads), 0, L.stream, cell(L, x), ctl, cell(L, prm), sp,
+                       reset, cell(L, y), cp, nullptr, nullptr, (int)s.B, (int)T, (int)s.L, sr, san);
+  DGEN_LAUNCH_CHECK("k_svf_seq");
+  return 0;
+}
+
+int launch_svf_adj_chunk(const Launch& L, const dgen_hip_op& op) {
+  // arg: [0]=mod [1]=env [2]=params ([P][B]) [3]=y [4]=target [5]=cells (saturating) or -1 [6]=summary
+  //      [7]=B [8]=T [9]=L [10]=saturating
+  const int64_t prm = op.arg[2], y = op.arg[3], tgt = op.arg[4], cl = op.arg[5], summ = op.arg[6], sat = op.arg[10];
+  SvfShape s;
+  if (int rc = svf_shape(op.arg[7], op.arg[8], op.arg[9], s, "svf_adj_chunk")) return rc;
+  DGEN_REQUIRE(sat == 0 || sat == 1, "svf_adj_chunk: saturating %lld", (long long)sat);
+  Ctl ctl{};
+  if (int rc = svf_ctl(L, op.arg[0], op.arg[1], s.T, "svf_adj_chunk.mod/env", ctl)) return rc;
+  float sr;
+  if (int rc = svf_rate(L, op.farg[0], "svf_adj_chunk", sr)) return rc;
+  DGEN_CHECK_CELL(L, prm, (2 + sat) * s.B, "svf_adj_chunk.params");
+  DGEN_CHECK_CELL(L, y, s.B * s.T, "svf_adj_chunk.y");
+  DGEN_CHECK_CELL(L, tgt, s.B * s.T, "svf_adj_chunk.target");
+  DGEN_REQUIRE(!sat || cl >= 0, "svf_adj_chunk: the saturating adjoint reads the stored cells");
+  if (cl >= 0) DGEN_CHECK_CELL(L, cl, 2 * s.B * s.T, "svf_adj_chunk.cells");
+  DGEN_CHECK_CELL(L, summ, 12 * s.C * s.B, "svf_adj_chunk.summary");
+  DGEN_REQUIRE(summ % 2 == 0, "svf_adj_chunk: summary cell must be 8-byte aligned");
+  if (L.dry) return 0;
+  if (sat)
+    hipLaunchKernelGGL(k_svf_adj_chunk<true>, svf_grid(s), dim3(kThreads), 0, L.stream, ctl, cell(L, prm),
+                       cell(L, y), cell(L, tgt), cell(L, cl), dcell(L, summ), (int)s.B, (int)s.T, (int)s.L, sr);
+  else
+    hipLaunchKernelGGL(k_svf_adj_chunk<false>, svf_grid(s), dim3(kThreads), 0, L.stream, ctl, cell(L, prm),
+                       cell(L, y), cell(L, tgt), nullptr, dcell(L, summ), (int)s.B, (int)s.T, (int)s.L, sr);
+  DGEN_LAUNCH_CHECK("k_svf_adj_chunk");
+  return 0;
+}
+
+int launch_svf_bwd(const Launch& L, const dgen_hip_op& op) {
+  // arg: [0]=x [1]=mod [2]=env [3]=params ([P][B]) [4]=y [5]=target [6]=cells [7]=adjoint init ([C][2][B])
+  //      [8]=grad partials ([C][P][B]) [9]=xbar ([T][B]) or -1 [10]=B [11]=T [12]=L [13]=saturating
+  const int64_t x = op.arg[0], prm = op.arg[3], y = op.arg[4], tgt = op.arg[5], cl = op.arg[6], ainit = op.arg[7],
+                gpart = op.arg[8], xb = op.arg[9], sat = op.arg[13];
+  SvfShape s;
+  if (int rc = svf_shape(op.arg[10], op.arg[11], op.arg[12], s, "svf_bwd")) return rc;
+  DGEN_REQUIRE(sat == 0 || sat == 1, "svf_bwd: saturating %lld", (long long)sat);
+  Ctl ctl{};
+  if (int rc = svf_ctl(L, op.arg[1], op.arg[2], s.T, "svf_bwd.mod/env", ctl)) return rc;
+  float sr;
+  if (int rc = svf_rate(L, op.farg[0], "svf_bwd", sr)) return rc;
+  const int64_t P = 2 + sat;
+  DGEN_CHECK_CELL(L, x, s.B * s.T, "svf_bwd.x");
+  DGEN_CHECK_CELL(L, prm, P * s.B, "svf_bwd.params");
+  DGEN_CHECK_CELL(L, y, s.B * s.T, "svf_bwd.y");
+  DGEN_CHECK_CELL(L, tgt, s.B * s.T, "svf_bwd.target");
+  DGEN_CHECK_CELL(L, cl, 2 * s.B * s.T, "svf_bwd.cells");
+  DGEN_CHECK_CELL(L, ainit, 2 * s.C * s.B, "svf_bwd.adjoint_init");
+  DGEN_CHECK_CELL(L, gpart, P * s.C * s.B, "svf_bwd.grad_partials");
+  if (xb >= 0) DGEN_CHECK_CELL(L, xb, s.B * s.T, "svf_bwd.xbar");
+  if (L.dry) return 0;
+  float* xp = xb >= 0 ? cell(L, xb) : nullptr;
+  if (sat)
+    hipLaunchKernelGGL(k_svf_bwd<true>, svf_grid(s), dim3(kThreads), 0, L.stream, cell(L, x), ctl, cell(L, prm),
+                       cell(L, y), cell(L, tgt), cell(L, cl), cell(L, ainit), cell(L, gpart), xp, (int)s.B, (int)s.T,
+                       (int)s.L, sr);
+  else
+    hipLaunchKernelGGL(k_svf_bwd<false>, svf_grid(s), dim3(kThreads), 0, L.stream, cell(L, x), ctl, cell(L, prm),
+                       cell(L, y), cell(L, tgt), cell(L, cl), cell(L, ainit), cell(L, gpart), xp, (int)s.B, (int)s.T,
+                       (int)s.L, sr);
+  DGEN_LAUNCH_CHECK("k_svf_bwd");
+  return 0;
+}
+
+}  // namespace dgen

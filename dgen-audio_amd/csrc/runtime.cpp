@@ -78,6 +78,12 @@ static Launcher launcher_for(uint32_t k) {
     case DGEN_HIP_K_STREAM_BIQUAD: return launch_stream_biquad;
     case DGEN_HIP_K_TEMPORAL_GRAD_SCAN: return launch_temporal_grad_scan;
     case DGEN_HIP_K_SWEPT_PHASOR: return launch_swept_phasor;
+    case DGEN_HIP_K_SVF_CHUNK: return launch_svf_chunk;
+    case DGEN_HIP_K_SVF_FWD: return launch_svf_fwd;
+    case DGEN_HIP_K_SVF_SEQ:
+    case DGEN_HIP_K_STREAM_SVF: return launch_svf_seq;
+    case DGEN_HIP_K_SVF_ADJ_CHUNK: return launch_svf_adj_chunk;
+    case DGEN_HIP_K_SVF_BWD: return launch_svf_bwd;
     default: return nullptr;
   }
 }
@@ -397,6 +403,12 @@ static FrameArg frame_arg(uint32_t k) {
     case DGEN_HIP_K_STREAM_BIQUAD: return {6, true};
     case DGEN_HIP_K_TEMPORAL_GRAD_SCAN: return {4, false};
     case DGEN_HIP_K_SWEPT_PHASOR: return {7, false};
+    case DGEN_HIP_K_SVF_CHUNK: return {6, false};
+    case DGEN_HIP_K_SVF_FWD:
+    case DGEN_HIP_K_SVF_SEQ: return {10, false};
+    case DGEN_HIP_K_STREAM_SVF: return {10, true};
+    case DGEN_HIP_K_SVF_ADJ_CHUNK: return {8, false};
+    case DGEN_HIP_K_SVF_BWD: return {11, false};
     default: return {-1, false};
   }
 }

@@ -7,4 +7,4 @@ this package is the host-side mirror of the reference's runtime interface
 from .program import Program  # noqa: F401
 from .runtime import HIPError, HIPLazyRuntime, device_count, load_library  # noqa: F401
 from .workloads import (BiquadConfig, HarmonicConfig, MembraneConfig, OscBankConfig, SplitMix64,  # noqa: F401
-                        StftConfig, SweptPhasorConfig)
+                        StftConfig, SvfConfig, SweptPhasorConfig)

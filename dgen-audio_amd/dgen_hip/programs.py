@@ -11,7 +11,8 @@ import numpy as np
 
 from . import runtime as R
 from .program import Program
-from .workloads import BiquadConfig, HarmonicConfig, MembraneConfig, OscBankConfig, StftConfig, SweptPhasorConfig
+from .workloads import (BiquadConfig, HarmonicConfig, MembraneConfig, OscBankConfig, StftConfig, SvfConfig,
+                        SweptPhasorConfig)
 
 SEG = 64          # frames per synth segment (checkpoint spacing)
 SLOTS = 4         # control rows a segment may touch
@@ -22,6 +23,7 @@ GEMM_TILE_M = 128  # output rows per GEMM workgroup tile (k_gemm.hip BM)
 SPLITK_ROWS_HEADS = 512  # the heads' weight gradient has one 128-wide column tile: split finer to fill the chip
 MSS_TILE = 4096     # output samples per spectral-loss workgroup
 BQ_CHUNK = 256      # frames per biquad scan chunk
+SVF_CHUNK = 256     # frames per SVF scan chunk
 STFT_TILE = 8192    # output samples per STFT forward workgroup
 MEM_STEPS = 16      # membrane frames per time-blocked launch
 MEM_TILE = 32       # membrane cells per workgroup tile side
@@ -471,6 +473,149 @@ class BiquadSession:
             if modulated:
                 rt.write("mod", self.mod)
             rt.write("params", params)
+            rt.runNoCopy()
+            return rt.read("y").reshape(self.cfg.T, self.cfg.B)
+
+    def step(self) -> None:
+        self.rt.runNoCopy()
+
+    def loss(self) -> float:
+        return float(self.rt.read("loss")[0])
+
+    def close(self):
+        self.rt.close()
+
+
+# ------------------------------------------------------ ZDF SVF bank (BPTT)
+def svf_program(cfg: SvfConfig, train: bool = True, optimizer: bool = True, saturating: bool | None = None,
+                chunk: int = SVF_CHUNK, xbar: bool = False) -> Program:
+    """ZDF SVF low-pass bank: x -> y with cutoff clip(base[k]*mod[n] + env[n])
+    and res[k] (and, saturating, kSat[k]).
+
+    Linear (kSat the constant 0): the forward is a chunked scan (fp64 chunk
+    maps, per-lane carry composition, fp32 replay).  Saturating: one lane per
+    thread over all frames.  ``train=False`` renders y only.  With
+    ``train=True``: forward storing the cells entering every frame, loss
+    sum (y - target)^2, BPTT to the parameters as a chunked reverse scan
+    (``xbar``: also d loss / d x), and (``optimizer``) one Adam step."""
+    sat = cfg.saturating if saturating is None else bool(saturating)
+    B, T, L = cfg.B, cfg.T, int(chunk)
+    if L <= 0:
+        raise ValueError("chunk length must be positive")
+    P = 3 if sat else 2
+    C = (T + L - 1) // L
+    f4 = 4.0
+    n = float(T * B)
+    p = Program(max_frames=T)
+    p.meta.update(cfg=cfg, chunk=L, chunks=C, train=train, saturating=sat, P=P)
+    x = p.alloc("x", T * B)
+    mod = p.alloc("mod", T)
+    env = p.alloc("env", T)
+    prm = p.alloc("params", P * B)
+    y = p.alloc("y", T * B)
+    sr = [cfg.sr]
+    ctl_b = 2.0 * T * f4
+    cells = p.alloc("cells", 2 * T * B) if train else -1
+    tgt = p.alloc("target", T * B) if train else -1
+    lossp = p.alloc("loss_partials", C * B) if train else -1
+    # per lane-frame: coefficients (clip, div, tan, 1/Q, 4 mul/add) ~ 30 flops, one SVF frame 12
+    if sat:
+        p.add(R.K_SVF_SEQ, [x, mod, env, prm, -1, y, cells, tgt, lossp, B, T, L, 0], sr, label="svf_seq",
+              dispatch=f"fixedWithFrameLoop({B})", bytes=n * f4 * (5 if train else 2) + ctl_b,
+              flops=n * (30 + 18), bound="valu")
+    else:
+        summ = p.alloc("summary", 12 * C * B)  # fp64
+        init = p.alloc("init", 2 * C * B)
+        p.add(R.K_SVF_CHUNK, [x, mod, env, prm, summ, B, T, L], sr, label="svf_chunk",
+              dispatch=f"chunk summaries {C}x{B}", bytes=n * f4 + ctl_b + 12.0 * C * B * f4,
+              flops=n * (30 + 3 * 10))
+        p.add(R.K_BIQUAD_CARRY, [summ, init, B, C, 0], label="svf_carry", dispatch=f"per-lane scan of {C} chunk maps",
+              bytes=(12.0 + 2.0) * C * B * f4, flops=24.0 * C * B)
+        p.add(R.K_SVF_FWD, [x, mod, env, prm, init, y, cells, tgt, lossp, B, T, L], sr, label="svf_fwd",
+              dispatch="chunk replay" + (" + cells + loss partials" if train else ""),
+              bytes=n * f4 * (5 if train else 2) + ctl_b + 2.0 * C * B * f4, flops=n * (30 + 12))
+    if not train:
+        p.output_cell = "y"
+        return p
+    lane_loss = p.alloc("lane_loss", B)
+    loss = p.alloc("loss", 1)
+    asumm = p.alloc("adj_summary", 12 * C * B)  # fp64
+    ainit = p.alloc("adj_init", 2 * C * B)
+    gpart = p.alloc("grad_partials", P * C * B)
+    G = p.alloc("grads", P * B)
+    xb = p.alloc("xbar", T * B) if xbar else -1
+    ws = p.alloc("colsum_ws", max(_colsum_ws(C, P * B), _colsum_ws(C, B), _colsum_ws(B, 1)))
+    p.add(R.K_COLSUM, [lossp, lane_loss, C, B, B, ws], label="loss_lanes", dispatch="chunkPartialsReduceToCell",
+          bytes=(C * B + B) * f4, flops=float(C * B))
+    p.add(R.K_COLSUM, [lane_loss, loss, B, 1, 1, ws], label="loss_sum", dispatch="chunkPartialsReduceToCell",
+          bytes=(B + 1) * f4, flops=float(B))
+    p.add(R.K_SVF_ADJ_CHUNK, [mod, env, prm, y, tgt, cells if sat else -1, asumm, B, T, L, int(sat)], sr,
+          label="svf_adj_chunk", dispatch=f"reverse chunk summaries {C}x{B}",
+          bytes=n * f4 * (4 if sat else 2) + ctl_b + 12.0 * C * B * f4, flops=n * (30 + 3 * 12))
+    p.add(R.K_BIQUAD_CARRY, [asumm, ainit, B, C, 1], label="svf_adj_carry", dispatch=f"reverse scan of {C} maps",
+          bytes=(12.0 + 2.0) * C * B * f4, flops=24.0 * C * B)
+    p.add(R.K_SVF_BWD, [x, mod, env, prm, y, tgt, cells, ainit, gpart, xb, B, T, L, int(sat)], sr, label="svf_bwd",
+          dispatch="reverse chunk replay + gradient partials",
+          bytes=n * f4 * (5 + (1 if xbar else 0)) + ctl_b + (2.0 + P) * C * B * f4, flops=n * (30 + 12 + 40))
+    p.add(R.K_COLSUM, [gpart, G, C, P * B, P * B, ws], label="grad_sum", dispatch="chunkPartialsReduceToCell",
+          bytes=(P * C * B + P * B) * f4, flops=float(P * C * B))
+    if optimizer:
+        m = p.alloc("adam_m", P * B)
+        v = p.alloc("adam_v", P * B)
+        tcell = p.alloc("adam_t", 1)
+        p.add(R.K_ADAM, [prm, G, m, v, P * B, tcell], [cfg.lr, 0.9, 0.999, 1e-8], label="adam",
+              dispatch=f"staticThreads({P * B})", bytes=7.0 * P * B * f4, flops=12.0 * P * B)
+    p.output_cell = "y"
+    return p
+
+
+def stream_svf_program(cfg: SvfConfig, max_frames: int | None = None) -> Program:
+    """The SVF bank as a streaming process: per call, B input channels plus
+    the modulation and envelope channels in, B output channels out, each
+    lane's two cells carried over (params [3][B]; kSat 0 is the linear
+    filter).  Out stores map non-finite values to 0."""
+    B, T = cfg.B, int(max_frames or cfg.T)
+    p = Program(max_frames=T)
+    x = p.alloc("x", T * B)
+    mod = p.alloc("mod", T)
+    env = p.alloc("env", T)
+    prm = p.alloc("params", 3 * B)
+    st = p.alloc("state", 2 * B)
+    y = p.alloc("y", T * B)
+    p.add(R.K_STREAM_SVF, [x, mod, env, prm, st, y, -1, -1, -1, B, T, SVF_CHUNK, 1], [cfg.sr], label="stream_svf",
+          dispatch=f"fixedWithFrameLoop({B})", bytes=8.0 * T * B, flops=float(T * B) * (30 + 18), bound="valu")
+    p.output_cell = "y"
+    ins = [("x", k, B) for k in range(B)] + [("mod", 0, 1), ("env", 0, 1)]
+    p.meta.update(cfg=cfg, ports=(ins, [("y", k, B) for k in range(B)]))
+    return p
+
+
+class SvfSession:
+    """SVF-bank training runtime: the target bank is rendered once by a linear
+    forward-only program with (tgt_fc, tgt_res), then every ``step()`` is
+    forward + loss + BPTT (+ Adam) with all data in HBM."""
+
+    def __init__(self, cfg: SvfConfig, device: int = 0, optimizer: bool = True, chunk: int = SVF_CHUNK,
+                 target=None, xbar: bool = False):
+        self.cfg = cfg
+        self.x = cfg.inputs()
+        self.mod = cfg.modulation()
+        self.env = cfg.envelope()
+        self.params0 = cfg.params()
+        if target is None:
+            target = self.render(cfg.target_params(), device, saturating=False, chunk=chunk)
+        self.target = np.ascontiguousarray(target, np.float32).reshape(cfg.T, cfg.B)
+        self.program = svf_program(cfg, train=True, optimizer=optimizer, chunk=chunk, xbar=xbar)
+        self.rt = R.HIPLazyRuntime(self.program, device)
+        for name, a in (("x", self.x), ("mod", self.mod), ("env", self.env), ("params", self.params0),
+                        ("target", self.target)):
+            self.rt.write(name, a)
+
+    def render(self, params, device: int = 0, saturating: bool = False, chunk: int = SVF_CHUNK) -> np.ndarray:
+        prog = svf_program(self.cfg, train=False, saturating=saturating, chunk=chunk)
+        with R.HIPLazyRuntime(prog, device) as rt:
+            for name, a in (("x", self.x), ("mod", self.mod), ("env", self.env), ("params", params)):
+                rt.write(name, a)
             rt.runNoCopy()
             return rt.read("y").reshape(self.cfg.T, self.cfg.B)
 

@@ -55,6 +55,12 @@ K_STREAM_OSC_BANK = 29
 K_STREAM_BIQUAD = 30
 K_TEMPORAL_GRAD_SCAN = 31
 K_SWEPT_PHASOR = 32
+K_SVF_CHUNK = 33
+K_SVF_FWD = 34
+K_SVF_SEQ = 35
+K_SVF_ADJ_CHUNK = 36
+K_SVF_BWD = 37
+K_STREAM_SVF = 38
 
 KERNEL_NAMES = {v: k[2:].lower() for k, v in globals().items() if k.startswith("K_")}
 

@@ -221,6 +221,70 @@ class BiquadConfig:
         return np.concatenate([np.full(self.B, self.tgt_fc, np.float32), np.full(self.B, self.tgt_Q, np.float32)])
 
 
+# ------------------------------------------------------ ZDF SVF bank (BPTT)
+@dataclass
+class SvfConfig:
+    """Two-cell ZDF SVF low-pass bank with BPTT (the MonologueVoice filter of
+    Tests/DGenLazyTests/SVFBPTTScratchTests.swift:21-34, one per lane): B
+    lanes x T samples of U[-1,1] noise; the cutoff of lane k at frame n is
+    clip(base[k] * m[n] + env[n], 20, 20000) with m the config-4 LFO sweep
+    and env = env_depth * exp(-t / env_tau) (the reference's cutoff envelope,
+    :56-63); kDamp = 1 / res[k]; with ``saturating`` each lane also learns
+    its kSat.  Loss = sum (y - y_target)^2 against a linear bank with
+    (tgt_fc, tgt_res); gradients w.r.t. base, res (and kSat)."""
+    B: int = 256
+    T: int = 1 << 18
+    sr: float = 44100.0
+    lfo_hz: float = 2.0
+    f_lo: float = 200.0
+    f_hi: float = 4000.0
+    env_depth: float = 900.0
+    env_tau: float = 0.15
+    base_lo: float = 150.0
+    base_hi: float = 2500.0
+    res_lo: float = 0.6
+    res_hi: float = 3.0
+    ks_hi: float = 2.0
+    tgt_fc: float = 1000.0
+    tgt_res: float = 1.2
+    saturating: bool = False
+    seed: int = 40
+    lr: float = 1e-3
+
+    @property
+    def P(self) -> int:
+        """Parameters per lane: base, res (, kSat)."""
+        return 3 if self.saturating else 2
+
+    def inputs(self) -> np.ndarray:
+        """x [T][B]: lane k is U[-1,1] drawn from SplitMix64(seed + k)."""
+        x = np.empty((self.T, self.B), np.float32)
+        for k in range(self.B):
+            x[:, k] = (SplitMix64(self.seed + k).uniform(self.T) * 2.0 - 1.0).astype(np.float32)
+        return x
+
+    def modulation(self) -> np.ndarray:
+        """m [T]: the config-4 geometric LFO sweep (f_hi/f_lo)^(0.5 + 0.5 sin)."""
+        return BiquadConfig(T=self.T, sr=self.sr, lfo_hz=self.lfo_hz, f_lo=self.f_lo, f_hi=self.f_hi).modulation()
+
+    def envelope(self) -> np.ndarray:
+        """env [T] in fp32: env_depth * exp(-t / env_tau), t = n / sr."""
+        t = (np.arange(self.T, dtype=np.float64) / self.sr).astype(np.float32)
+        return (np.float32(self.env_depth) * np.exp(-t / np.float32(self.env_tau))).astype(np.float32)
+
+    def params(self) -> np.ndarray:
+        """Parameter blob [P][B] = base | res (| kSat), spread over the lanes."""
+        u = np.linspace(0.0, 1.0, self.B)
+        base = self.base_lo * (self.base_hi / self.base_lo) ** u
+        res = self.res_lo + (self.res_hi - self.res_lo) * u[::-1]
+        rows = [base, res] + ([self.ks_hi * u] if self.saturating else [])
+        return np.concatenate(rows).astype(np.float32)
+
+    def target_params(self) -> np.ndarray:
+        """The linear target bank's [2][B] = tgt_fc | tgt_res."""
+        return np.concatenate([np.full(self.B, self.tgt_fc, np.float32), np.full(self.B, self.tgt_res, np.float32)])
+
+
 # ------------------------------------------------- temporal gradient (a21)
 @dataclass
 class SweptPhasorConfig:

@@ -195,7 +195,9 @@ enum dgen_hip_kernel {
 
   /* Compose the fp64 chunk summaries per lane (ascending chunks, or
    * descending when reverse = 1, for the adjoint): init [C][2][B] (fp32) =
-   * the state entering each chunk.  arg: [0]=summary [1]=init [2]=B [3]=C [4]=reverse */
+   * the state entering each chunk.  Any two-cell affine chunk maps in this
+   * layout compose here (the SVF bank's too).
+   * arg: [0]=summary [1]=init [2]=B [3]=C [4]=reverse */
   DGEN_HIP_K_BIQUAD_CARRY = 21,
 
   /* Forward part 2: each chunk re-run from its initial state; writes y and,
@@ -301,6 +303,57 @@ enum dgen_hip_kernel {
    *      [7]=T [8]=smooth (0/1)
    * farg: [0]=sample rate [1]=base frequency [2]=target */
   DGEN_HIP_K_SWEPT_PHASOR = 32,
+
+  /* ---- ZDF state-variable filter bank (low-pass): the two-cell
+   * Cytomic/TPT SVF of SVFBPTTScratchTests.swift:21-34 per lane, cutoff
+   * fc = clip(base[k] * mod[n] + env[n], 20, 20000) (mod, env optional
+   * [T] signals), g = tan((pi fc) / sr), kDamp = 1 / res[k], saturation
+   * s = ic / (1 + |kSat[k] ic|).  x, y, target: [T][B]; cells: [2][T][B]
+   * (ic1 | ic2 entering every frame); params [P][B] = base | res (P = 2,
+   * kSat the constant 0) or base | res | kSat (P = 3).  Every class takes
+   * farg[0] = sample rate (the run's host rate when one is set).
+   *
+   * Linear forward part 1: per (lane, chunk of L frames) the chunk's
+   * zero-state result and unit-state responses as fp64 affine maps,
+   * summary [C][6][B] (C = ceil(T/L)); then DGEN_HIP_K_BIQUAD_CARRY.
+   * arg: [0]=x [1]=mod or -1 [2]=env or -1 [3]=params (P = 2) [4]=summary
+   *      [5]=B [6]=T [7]=L */
+  DGEN_HIP_K_SVF_CHUNK = 33,
+
+  /* Linear forward part 2: each chunk re-run from its state: y, the cells
+   * (or -1), per-chunk loss partials sum (y - target)^2 (with a target).
+   * arg: [0]=x [1]=mod [2]=env [3]=params (P = 2) [4]=init ([C][2][B])
+   *      [5]=y [6]=cells or -1 [7]=target or -1 [8]=loss partials ([C][B])
+   *      or -1 [9]=B [10]=T [11]=L */
+  DGEN_HIP_K_SVF_FWD = 34,
+
+  /* Saturating forward (P = 3), one lane per thread over all frames (the
+   * reference's per-lane frame loop); loss partials per L-frame chunk.
+   * arg: [0]=x [1]=mod [2]=env [3]=params [4]=state ([2][B]) or -1 [5]=y
+   *      [6]=cells or -1 [7]=target or -1 [8]=loss partials or -1 [9]=B
+   *      [10]=T [11]=L [12]=sanitize (non-finite out stores -> 0) */
+  DGEN_HIP_K_SVF_SEQ = 35,
+
+  /* BPTT part 1: per (lane, chunk), reverse, the cells' adjoint from a zero
+   * carry under the loss 2 (y - target) and its unit-carry responses
+   * (fp64, summary [C][6][B]; then DGEN_HIP_K_BIQUAD_CARRY, reverse 1).
+   * arg: [0]=mod [1]=env [2]=params [3]=y [4]=target [5]=cells (required
+   *      when saturating) or -1 [6]=summary [7]=B [8]=T [9]=L
+   *      [10]=saturating (0/1) */
+  DGEN_HIP_K_SVF_ADJ_CHUNK = 36,
+
+  /* BPTT part 2: each chunk's adjoint from its carry, chained through the
+   * coefficient nodes to gradient partials [C][P][B] (d/d base, d/d res,
+   * d/d kSat) for DGEN_HIP_K_COLSUM, and (optional) d loss / d x.
+   * arg: [0]=x [1]=mod [2]=env [3]=params [4]=y [5]=target [6]=cells
+   *      [7]=adjoint init ([C][2][B]) [8]=grad partials [9]=xbar ([T][B])
+   *      or -1 [10]=B [11]=T [12]=L [13]=saturating (0/1) */
+  DGEN_HIP_K_SVF_BWD = 37,
+
+  /* Streaming SVF bank: DGEN_HIP_K_SVF_SEQ's arguments with a state cell,
+   * no cells and no loss; a run processes frames [0, frame_count) and
+   * carries ic1, ic2 to the next (zero after a reset). */
+  DGEN_HIP_K_STREAM_SVF = 38,
 };
 
 /* GEMM epilogues */

@@ -27,6 +27,10 @@
  *   radix-2 FFT           brute-force DFT, impulse/DC/cosine, Parseval
  *   spectral loss         identical signals -> 0, brute-force DFT magnitudes
  *   MLP / heads           numpy restatement + finite differences
+ *   ZDF SVF               TPT low-pass response (|H| on a steady sinusoid,
+ *                         scipy lfilter of the bilinear transfer function),
+ *                         odd symmetry and the exact 2x scaling invariant of
+ *                         the saturation
  *   all analytic grads    central finite differences of the f64 build
  */
 #include <math.h>
@@ -53,6 +57,7 @@
 #define R_FLOOR(x) (IS_F32 ? (REAL)floorf((float)(x)) : (REAL)floor((double)(x)))
 #define R_FMOD(x, y) (IS_F32 ? (REAL)fmodf((float)(x), (float)(y)) : (REAL)fmod((double)(x), (double)(y)))
 #define R_ABS(x) (IS_F32 ? (REAL)fabsf((float)(x)) : (REAL)fabs((double)(x)))
+#define R_TAN(x) (IS_F32 ? (REAL)tanf((float)(x)) : (REAL)tan((double)(x)))
 
 static inline REAL r_sign(REAL x) { return x > 0 ? (REAL)1 : (x < 0 ? (REAL)-1 : (REAL)0); }
 static inline REAL r_max(REAL a, REAL b) { return a >= b ? a : b; }
@@ -1140,6 +1145,187 @@ double FN(dgen_oracle_biquad_step)(const float* x, const float* m, const REAL* b
       }
     }
     free(v);
+  }
+  free(y);
+  return loss;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Two-cell ZDF state-variable filter bank (low-pass) and its BPTT.         */
+/* ------------------------------------------------------------------------ */
+
+/* The hand-rolled Cytomic/TPT SVF of Tests/DGenLazyTests/
+ * SVFBPTTScratchTests.swift:21-34 (the MonologueVoice filter): two history
+ * cells ic1, ic2 written with pass-through values, soft saturation
+ * s = ic / (1 + |kSat ic|), and the cutoff drive of :56-63,
+ * (fBase + envelope).clip(20, 20000) -> g = tan((pi * fc) / sr).  Per lane k
+ * and frame n, in the graph's node order:
+ *   fc  = clip(base[k] * m[n] + env[n], 20, 20000)   (m = 1, env = 0 if absent;
+ *         clip = max(min(v, 20000), 20), Functions.swift:780-782)
+ *   g   = tan((pi * fc) / sr);  kd = 1 / res[k]
+ *   a1  = 1 / (1 + g * (g + kd));  a2 = g * a1
+ *   s1  = ic1 / (1 + |ks ic1|);  s2 = ic2 / (1 + |ks ic2|)
+ *   v3  = x - s2;  v1 = a1 s1 + a2 v3
+ *   ic1 <- 2 v1 - s1;  v1p = (ic1 + s1) * 0.5
+ *   v2  = s2 + g v1p;  ic2 <- 2 v2 - s2
+ *   y   = (ic2 + s2) * 0.5
+ * pi and sr enter as Float constants.  With ks = 0 this is the TPT low-pass
+ * H(s) = 1 / (s^2 + kd s + 1) under the prewarped bilinear transform. */
+typedef struct {
+  REAL g, kd, a1, a2, u, Q;
+  int pass; /* the clip passes its input's gradient */
+} SvfCoef;
+
+#define SVF_PI ((REAL)3.14159265358979323846f)
+
+static inline void svf_coef(REAL raw, REAL kd, float sr, SvfCoef* c) {
+  const REAL fc = r_max(r_min(raw, (REAL)20000), (REAL)20);
+  /* min passes for raw <= hi, max for min(raw, hi) >= lo (Gradients.swift:386-410) */
+  c->pass = raw <= (REAL)20000 && r_min(raw, (REAL)20000) >= (REAL)20;
+  c->u = (SVF_PI * fc) / (REAL)sr;
+  c->g = R_TAN(c->u);
+  c->kd = kd;
+  c->Q = (REAL)1 + c->g * (c->g + kd);
+  c->a1 = (REAL)1 / c->Q;
+  c->a2 = c->g * c->a1;
+}
+
+static inline REAL svf_raw_cutoff(const float* m, const float* env, REAL base, int n) {
+  REAL v = base * (m ? (REAL)m[n] : (REAL)1);
+  return env ? v + (REAL)env[n] : v;
+}
+
+static inline REAL svf_sat(REAL c, REAL ks) { return c / ((REAL)1 + R_ABS(ks * c)); }
+
+/* One frame: state (c1, c2) -> next state; returns y. */
+static inline REAL svf_frame(const SvfCoef* k, REAL ks, REAL x, REAL* c1, REAL* c2) {
+  const REAL s1 = svf_sat(*c1, ks), s2 = svf_sat(*c2, ks);
+  const REAL v3 = x - s2;
+  const REAL v1 = k->a1 * s1 + k->a2 * v3;
+  const REAL ic1 = (REAL)2 * v1 - s1;
+  const REAL v1p = (ic1 + s1) * (REAL)0.5;
+  const REAL v2 = s2 + k->g * v1p;
+  const REAL ic2 = (REAL)2 * v2 - s2;
+  *c1 = ic1;
+  *c2 = ic2;
+  return (ic2 + s2) * (REAL)0.5;
+}
+
+/* Forward over [T][B] lanes from state[2][B] (ic1 | ic2, updated in place;
+ * NULL: zero state).  ks NULL: kSat is the constant 0.  states (optional,
+ * [2][T][B]): the cells entering every frame. */
+static void svf_forward(const float* x, const float* m, const float* env, const REAL* base, const REAL* res,
+                        const REAL* ks, int B, int T, float sr, REAL* state, REAL* y, REAL* states) {
+  /* lanes are independent: each runs its frames in order on one thread */
+#pragma omp parallel for schedule(static)
+  for (int k = 0; k < B; ++k) {
+    REAL c1 = state ? state[k] : 0, c2 = state ? state[B + k] : 0;
+    const REAL kd = (REAL)1 / res[k];
+    const REAL kk = ks ? ks[k] : (REAL)0;
+    for (int n = 0; n < T; ++n) {
+      const size_t i = (size_t)n * B + k;
+      SvfCoef c;
+      svf_coef(svf_raw_cutoff(m, env, base[k], n), kd, sr, &c);
+      if (states) {
+        states[i] = c1;
+        states[(size_t)T * B + i] = c2;
+      }
+      y[i] = svf_frame(&c, kk, (REAL)x[i], &c1, &c2);
+    }
+    if (state) {
+      state[k] = c1;
+      state[B + k] = c2;
+    }
+  }
+}
+
+void FN(dgen_oracle_svf_fwd)(const float* x, const float* m, const float* env, const REAL* base, const REAL* res,
+                             const REAL* ks, int B, int T, float sr, REAL* state, float* y_out) {
+  REAL* y = (REAL*)malloc(sizeof(REAL) * (size_t)B * T);
+  svf_forward(x, m, env, base, res, ks, B, T, sr, state, y, NULL);
+  to_float(y, (size_t)B * T, y_out);
+  free(y);
+}
+
+/* Forward, loss = sum (y - tgt)^2 over frames and lanes, and (grad, [3][B] =
+ * d/d base | d/d res | d/d ks; the last is 0 when ks is NULL) the BPTT
+ * gradient: the reverse-time adjoint (lambda1, lambda2) of the two cells
+ * through every node above, reading the stored cells of each frame (the
+ * reference's stored-forward-value reverse loop, BPTTEmission.swift:133-160,
+ * with the per-node rules of Gradients.swift: abs -> sign, min/max ->
+ * pass masks, tan -> 1/(cos cos), div).  xbar (optional, [T][B]) = d loss /
+ * d x. */
+double FN(dgen_oracle_svf_step)(const float* x, const float* m, const float* env, const REAL* base,
+                                const REAL* res, const REAL* ks, const float* tgt, int B, int T, float sr,
+                                float* y_out, REAL* grad, REAL* xbar) {
+  const size_t N = (size_t)B * T;
+  REAL* y = (REAL*)malloc(sizeof(REAL) * N);
+  REAL* st = grad || xbar ? (REAL*)malloc(sizeof(REAL) * 2 * N) : NULL;
+  svf_forward(x, m, env, base, res, ks, B, T, sr, NULL, y, st);
+  if (y_out) to_float(y, N, y_out);
+  double loss = 0.0;
+  for (size_t i = 0; i < N; ++i) {
+    const REAL d = y[i] - (REAL)tgt[i];
+    loss += (double)(d * d);
+  }
+  if (st) {
+#pragma omp parallel for schedule(static)
+    for (int k = 0; k < B; ++k) {
+      const REAL kd = (REAL)1 / res[k];
+      const REAL kk = ks ? ks[k] : (REAL)0;
+      REAL l1 = 0, l2 = 0, gb = 0, gkd = 0, gks = 0;
+      for (int n = T - 1; n >= 0; --n) {
+        const size_t i = (size_t)n * B + k;
+        SvfCoef c;
+        svf_coef(svf_raw_cutoff(m, env, base[k], n), kd, sr, &c);
+        const REAL c1 = st[i], c2 = st[N + i];
+        const REAL D1 = (REAL)1 + R_ABS(kk * c1), D2 = (REAL)1 + R_ABS(kk * c2);
+        const REAL s1 = c1 / D1, s2 = c2 / D2;
+        const REAL v3 = (REAL)x[i] - s2;
+        const REAL v1 = c.a1 * s1 + c.a2 * v3;
+        const REAL ic1 = (REAL)2 * v1 - s1;
+        const REAL v1p = (ic1 + s1) * (REAL)0.5;
+        /* adjoints, last node first */
+        const REAL e = (REAL)2 * (y[i] - (REAL)tgt[i]);
+        const REAL ic2_b = (REAL)0.5 * e + l2;
+        REAL s2_b = (REAL)0.5 * e - ic2_b;
+        const REAL v2_b = (REAL)2 * ic2_b;
+        s2_b += v2_b;
+        REAL g_b = v2_b * v1p;
+        const REAL v1p_b = v2_b * c.g;
+        const REAL ic1_b = l1 + (REAL)0.5 * v1p_b;
+        REAL s1_b = (REAL)0.5 * v1p_b - ic1_b;
+        const REAL v1_b = (REAL)2 * ic1_b;
+        REAL a1_b = v1_b * s1;
+        s1_b += v1_b * c.a1;
+        const REAL a2_b = v1_b * v3;
+        const REAL v3_b = v1_b * c.a2;
+        if (xbar) xbar[i] = v3_b;
+        s2_b -= v3_b;
+        /* s = c / D, D = 1 + |ks c|: ds/dc = 1/D - (c/D^2) sgn(ks c) ks, ds/dks = -(c/D^2) sgn(ks c) c */
+        const REAL q1 = (c1 / (D1 * D1)) * r_sign(kk * c1), q2 = (c2 / (D2 * D2)) * r_sign(kk * c2);
+        l1 = s1_b * ((REAL)1 / D1 - q1 * kk);
+        l2 = s2_b * ((REAL)1 / D2 - q2 * kk);
+        gks += -(s1_b * q1 * c1) - s2_b * q2 * c2;
+        g_b += a2_b * c.a1;
+        a1_b += a2_b * c.g;
+        /* a1 = 1 / Q, Q = 1 + g (g + kd) */
+        const REAL Q_b = -a1_b / (c.Q * c.Q);
+        g_b += Q_b * ((c.g + c.kd) + c.g);
+        gkd += Q_b * c.g;
+        /* g = tan(u), u = (pi fc) / sr */
+        const REAL cu = R_COS(c.u);
+        const REAL u_b = g_b * ((REAL)1 / (cu * cu));
+        const REAL fc_b = (u_b / (REAL)sr) * SVF_PI;
+        if (c.pass) gb += fc_b * (m ? (REAL)m[n] : (REAL)1);
+      }
+      if (grad) {
+        grad[k] = gb;
+        grad[B + k] = gkd * (-(REAL)1 / (res[k] * res[k]));
+        grad[2 * B + k] = ks ? gks : (REAL)0;
+      }
+    }
+    free(st);
   }
   free(y);
   return loss;

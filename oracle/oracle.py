@@ -78,6 +78,9 @@ def lib(name: str = "liboracle.so") -> ctypes.CDLL:
                  [rp_(sfx), _c_int, _c_int, _c_float, _c_float, _c_float, _c_int, _c_int, ctypes.c_void_p,
                   ctypes.c_void_p],
                  ctypes.c_double)
+            _sig(L, "dgen_oracle_svf_fwd" + sfx, [_f32p, vp, vp, rp, rp, vp, _c_int, _c_int, _c_float, vp, _f32p])
+            _sig(L, "dgen_oracle_svf_step" + sfx,
+                 [_f32p, vp, vp, rp, rp, vp, _f32p, _c_int, _c_int, _c_float, vp, vp, vp], ctypes.c_double)
         if hasattr(L, "dgen_oracle_temporal_scan"):
             _sig(L, "dgen_oracle_temporal_scan", [_f32p, ctypes.c_void_p, _c_int, _c_int, _f32p])
         if hasattr(L, "dgen_oracle_noise_stream"):
@@ -316,6 +319,49 @@ def biquad_step(x, m, base, Q, tgt, grad=True, want_y=False, prec="f64"):
         x, mp, np.ascontiguousarray(base, dt), np.ascontiguousarray(Q, dt), _f(tgt).reshape(T, B), B, T,
         y.ctypes.data_as(ctypes.c_void_p) if want_y else None, g.ctypes.data_as(ctypes.c_void_p) if grad else None)
     return loss, g, y
+
+
+def _vp(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def svf_fwd(x, base, res, ks=None, m=None, env=None, sr=44100.0, state=None, prec="f32"):
+    """The ZDF SVF low-pass bank: x [T][B] -> y [T][B] (float32).  base, res,
+    ks [B] (ks None: kSat is the constant 0); m, env [T] or None (cutoff =
+    clip(base * m + env, 20, 20000)); state [2][B] (ic1 | ic2, the build's
+    precision) is carried in place when given."""
+    x = _f(x)
+    T, B = x.shape
+    dt = np.float32 if prec == "f32" else np.float64
+    ksa = None if ks is None else np.ascontiguousarray(ks, dt)
+    ma = None if m is None else _f(m)
+    ea = None if env is None else _f(env)
+    if state is not None:
+        assert state.dtype == dt and state.shape == (2, B) and state.flags.c_contiguous
+    y = np.zeros((T, B), np.float32)
+    _fn("dgen_oracle_svf_fwd", prec)(x, _vp(ma), _vp(ea), np.ascontiguousarray(base, dt),
+                                     np.ascontiguousarray(res, dt), _vp(ksa), B, T, sr, _vp(state), y)
+    return y
+
+
+def svf_step(x, base, res, tgt, ks=None, m=None, env=None, sr=44100.0, grad=True, want_y=False, want_xbar=False,
+             prec="f64"):
+    """SVF bank step: forward, loss sum (y - tgt)^2, and (grad) the BPTT
+    gradient [3][B] = (d/d base, d/d res, d/d ks).  Returns (loss, grad or
+    None, y or None, xbar or None)."""
+    x = _f(x)
+    T, B = x.shape
+    dt = np.float32 if prec == "f32" else np.float64
+    ksa = None if ks is None else np.ascontiguousarray(ks, dt)
+    ma = None if m is None else _f(m)
+    ea = None if env is None else _f(env)
+    g = np.zeros(3 * B, dt) if grad else None
+    y = np.zeros((T, B), np.float32) if want_y else None
+    xb = np.zeros((T, B), dt) if want_xbar else None
+    loss = _fn("dgen_oracle_svf_step", prec)(
+        x, _vp(ma), _vp(ea), np.ascontiguousarray(base, dt), np.ascontiguousarray(res, dt), _vp(ksa),
+        _f(tgt).reshape(T, B), B, T, sr, _vp(y), _vp(g), _vp(xb))
+    return loss, g, y, xb
 
 
 # -- config 2 -------------------------------------------------------------

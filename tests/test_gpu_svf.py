@@ -1,0 +1,119 @@
+"""ZDF SVF bank on the GPU against the oracle (dgen_oracle_svf_fwd / _step):
+the linear bank's chunked forward and the saturating bank's per-lane forward,
+the BPTT gradient to (base, res, kSat) and d loss / d x, at 256 lanes x 2^18
+frames (SvfConfig), and the streaming process path (any split of a signal
+into calls gives the same samples).  fp32 recurrences: the HIP results must
+stay within 2x the fp32 oracle's distance from the fp64 oracle.  Needs a GPU."""
+import numpy as np
+import pytest
+
+import oracle as O
+from dgen_hip import SvfConfig
+from dgen_hip.programs import SvfSession, stream_svf_program
+from dgen_hip.runtime import HIPLazyRuntime
+
+
+pytestmark = pytest.mark.gpu
+
+
+def oracle_args(cfg, params):
+    P = len(params) // cfg.B
+    p = params.reshape(P, cfg.B)
+    return dict(base=p[0], res=p[1], ks=p[2] if P == 3 else None, m=cfg.modulation(), env=cfg.envelope(), sr=cfg.sr)
+
+
+@pytest.fixture(scope="module", params=[False, True], ids=["linear", "saturating"])
+def svf_run(request):
+    cfg = SvfConfig(saturating=request.param)
+    print(f"SVF bank B={cfg.B} T={cfg.T} saturating={cfg.saturating}", flush=True)
+    s = SvfSession(cfg, optimizer=False)
+    try:
+        s.step()
+        out = dict(cfg=cfg, x=s.x, target=s.target, y=s.rt.read("y").reshape(cfg.T, cfg.B), loss=s.loss(),
+                   grads=s.rt.read("grads").astype(np.float64), params=s.params0)
+    finally:
+        s.close()
+    return out
+
+
+def test_target_bank_matches_the_oracle(svf_run):
+    cfg = svf_run["cfg"]
+    a = oracle_args(cfg, cfg.target_params())
+    a["ks"] = None
+    ref32 = O.svf_fwd(svf_run["x"], **a)
+    ref64 = O.svf_fwd(svf_run["x"], **a, prec="f64")
+    e_hip, e_o32 = np.abs(svf_run["target"] - ref64).max(), np.abs(ref32 - ref64).max()
+    print(f"target bank: max|y - fp64| HIP {e_hip:.3e}, fp32 oracle {e_o32:.3e}")
+    assert e_hip <= 2.0 * e_o32 + 1e-6
+
+
+def test_forward_loss_and_gradient_match_the_oracle(svf_run):
+    cfg, x, tgt = svf_run["cfg"], svf_run["x"], svf_run["target"]
+    a = oracle_args(cfg, svf_run["params"])
+    l64, g64, y64, _ = O.svf_step(x, tgt=tgt, want_y=True, **a)
+    l32, g32, y32, _ = O.svf_step(x, tgt=tgt, want_y=True, prec="f32", **a)
+    y = svf_run["y"]
+    e_hip, e_o32 = np.abs(y - y64).max(), np.abs(y32 - y64).max()
+    print(f"y: max|y - fp64| HIP {e_hip:.3e}, fp32 oracle {e_o32:.3e} (max |y| {np.abs(y64).max():.3f})")
+    assert e_hip <= 2.0 * e_o32 + 1e-6
+    loss = svf_run["loss"]
+    print(f"loss HIP {loss:.8e}, fp64 oracle {l64:.8e}, fp32 oracle {l32:.8e}")
+    assert abs(loss - l64) <= 2.0 * abs(l32 - l64) + 1e-5 * abs(l64)
+    g = svf_run["grads"]
+    P = cfg.P
+    for r, name in enumerate(["base", "res", "kSat"][:P]):
+        sl = slice(r * cfg.B, (r + 1) * cfg.B)
+        nrm = np.linalg.norm(g64[sl])
+        eh, eo = np.linalg.norm(g[sl] - g64[sl]) / nrm, np.linalg.norm(g32[sl] - g64[sl]) / nrm
+        print(f"d/d {name}: rel L2 vs fp64 HIP {eh:.3e}, fp32 oracle {eo:.3e}")
+        assert eh <= 2.0 * eo + 1e-5
+
+
+def test_input_gradient_matches_the_oracle():
+    for sat in (False, True):
+        cfg = SvfConfig(B=64, T=1 << 14, saturating=sat)
+        s = SvfSession(cfg, optimizer=False, xbar=True)
+        try:
+            s.step()
+            xb = s.rt.read("xbar").reshape(cfg.T, cfg.B).astype(np.float64)
+        finally:
+            s.close()
+        a = oracle_args(cfg, cfg.params())
+        _, _, _, xb64 = O.svf_step(s.x, tgt=s.target, want_xbar=True, grad=False, **a)
+        _, _, _, xb32 = O.svf_step(s.x, tgt=s.target, want_xbar=True, grad=False, prec="f32", **a)
+        nrm = np.linalg.norm(xb64)
+        eh, eo = np.linalg.norm(xb - xb64) / nrm, np.linalg.norm(xb32 - xb64) / nrm
+        print(f"saturating={sat}: d loss / d x rel L2 vs fp64 HIP {eh:.3e}, fp32 oracle {eo:.3e}")
+        assert eh <= 2.0 * eo + 1e-6
+
+
+def test_streaming_calls_carry_the_cells():
+    cfg = SvfConfig(B=64, T=1 << 15, saturating=True)
+    prog = stream_svf_program(cfg)
+    x, m, env, prm = cfg.inputs(), cfg.modulation(), cfg.envelope(), cfg.params()
+    rt = HIPLazyRuntime(prog, 0)
+    try:
+        rt.write("params", prm)
+        rt.setProcessPorts(*prog.meta["ports"])
+
+        def calls(sizes):
+            out, n0 = [], 0
+            for i, n in enumerate(sizes):
+                ins = [x[n0:n0 + n, k] for k in range(cfg.B)] + [m[n0:n0 + n], env[n0:n0 + n]]
+                out.append(rt.process(ins, n, reset=i == 0).T)
+                n0 += n
+            return np.concatenate(out)
+
+        one = calls([cfg.T])
+        for sizes in ([8192] * 4, [1, 4095, 20000, 8672]):
+            np.testing.assert_array_equal(calls(sizes), one)
+    finally:
+        rt.close()
+    a = oracle_args(cfg, prm)
+    st = np.zeros((2, cfg.B), np.float32)
+    ref = np.concatenate([O.svf_fwd(x[:9000], **{**a, "m": a["m"][:9000], "env": a["env"][:9000]}, state=st),
+                          O.svf_fwd(x[9000:], **{**a, "m": a["m"][9000:], "env": a["env"][9000:]}, state=st)])
+    ref64 = O.svf_fwd(x, **a, prec="f64")
+    print(f"stream: max|y - fp32 oracle| {np.abs(one - ref).max():.3e}, HIP vs fp64 {np.abs(one - ref64).max():.3e}, "
+          f"fp32 oracle vs fp64 {np.abs(ref - ref64).max():.3e}")
+    assert np.abs(one - ref64).max() <= 2.0 * np.abs(ref - ref64).max() + 1e-6
