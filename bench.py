@@ -22,11 +22,12 @@ With ``--workload biquad`` the same line is printed for BASELINE config 4
 gains, forward + loss + gain gradient + Adam) and with ``--workload
 membrane`` for config 5 (512^2 membrane, 4800 steps, forward + loss + adjoint
 + Adam) and with ``--workload oscbank`` for config 1 (16-oscillator bank,
-65536 frames, forward only) instead; the default workload is the headline
-config 3.
+65536 frames, forward only) and with ``--workload svf`` / ``svf-sat`` for
+the 256-lane x 2^18 ZDF SVF bank (linear / learnable saturation, forward +
+loss + BPTT + Adam) instead; the default workload is the headline config 3.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                       [--workload harmonic|biquad|stft|membrane|oscbank]
+                       [--workload harmonic|biquad|stft|membrane|oscbank|svf|svf-sat]
 """
 from __future__ import annotations
 
@@ -44,6 +45,7 @@ METRIC = "fwd+bwd audio samples/sec, batch-32 harmonic synth + MSS loss; % HBM p
 BIQUAD_METRIC = "fwd+bwd lane-samples/sec, 256-lane x 2^18 tensor biquad bank with BPTT"
 STFT_METRIC = "fwd+bwd input samples/sec, 8 x 2^20 hop-gated STFT round trip with 513 learnable gains"
 MEMBRANE_METRIC = "fwd+bwd cell-steps/sec, 512^2 membrane x 4800 steps with BPTT to (c2, d)"
+SVF_METRIC = "fwd+bwd lane-samples/sec, 256-lane x 2^18 ZDF SVF bank with BPTT"
 
 
 def log(msg: str) -> None:
@@ -267,6 +269,78 @@ def run_biquad(args) -> dict:
     return out
 
 
+def svf_cpu_baseline(cfg, lanes: int, repeats: int) -> dict:
+    """The oracle's fp32 SVF step (forward, loss and BPTT backward; built with
+    the reference C backend's -O3 -ffast-math policy, single thread) on
+    `lanes` of the bank's lanes over all frames.  Median of `repeats` after a
+    warm-up."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import ctypes
+
+    import numpy as np
+    import oracle as O
+    x = np.ascontiguousarray(cfg.inputs()[:, :lanes])
+    m, env = cfg.modulation(), cfg.envelope()
+    p = cfg.params().reshape(cfg.P, cfg.B)[:, :lanes]
+    tp = cfg.target_params().reshape(2, cfg.B)[:, :lanes]
+    tgt = O.svf_fwd(x, tp[0], tp[1], None, m, env, cfg.sr)
+    fn = O._fn("dgen_oracle_svf_step", "f32", "liboracle_bench.so")
+    base, res = np.ascontiguousarray(p[0]), np.ascontiguousarray(p[1])
+    ks = np.ascontiguousarray(p[2]) if cfg.saturating else None
+    g = np.zeros(3 * lanes, np.float32)
+    vp = lambda a: None if a is None else a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
+    med = median_time(lambda: fn(x, vp(m), vp(env), base, res, vp(ks), tgt, lanes, cfg.T, cfg.sr, None, vp(g), None),
+                      repeats)
+    return {
+        "value": lanes * cfg.T / med,
+        "unit": "lane-samples/s",
+        "cores": 1,
+        "kind": "port",
+        "host_cpu": host_cpu(),
+        "sample": (f"{lanes} of {cfg.B} lanes x {cfg.T} frames: sequential fp32 forward, loss and BPTT backward "
+                   f"(no Adam); median of {repeats} after 1 warm-up; host {host_cpu()}"),
+    }
+
+
+def run_svf(args, saturating: bool) -> dict:
+    from dgen_hip import SvfConfig
+    from dgen_hip.programs import SvfSession
+    cfg = SvfConfig(saturating=saturating)
+    name = "svf-sat" if saturating else "svf"
+    log(f"bench: SVF session B={cfg.B} T={cfg.T} saturating={saturating} chunk={args.chunk}")
+    sess = SvfSession(cfg, device=0, optimizer=True, chunk=args.chunk)
+    if args.traffic_runs:
+        try:
+            traffic_run(sess, name, args.traffic_runs)
+        finally:
+            sess.close()
+        return None
+    try:
+        wall, rows, dom, roof_ms = time_session(sess.rt, sess.program, args)
+        loss = sess.loss()
+    finally:
+        sess.close()
+    ms_per_step = wall * 1e3 / args.steps
+    cpu = None
+    if not args.no_cpu:
+        log("bench: cpu baseline (svf)")
+        cpu = svf_cpu_baseline(cfg, 32, args.cpu_repeats)
+    out = {
+        "metric": SVF_METRIC, "value": cfg.B * cfg.T * args.steps / wall, "unit": "lane-samples/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (U[-1,1] SplitMix64 input per lane, 2 Hz geometric cutoff sweep + 900 Hz envelope)",
+        "config": {"workload": "ZDF SVF bank (SVFBPTTScratchTests.swift:21-34 per lane), MSE vs a fixed linear bank, "
+                               "BPTT to base cutoff, res" + (" and kSat" if saturating else "") + ", Adam",
+                   "B": cfg.B, "T": cfg.T, "sr": cfg.sr, "saturating": saturating, "chunk": args.chunk,
+                   "parallelism": "single GPU"},
+    }
+    out.update(roofline_fields(rows, dom, roof_ms, ms_per_step, name))
+    out["loss"] = loss
+    out["cpu_baseline"] = cpu
+    return out
+
+
 def stft_cpu_baseline(cfg, signals: int, repeats: int) -> dict:
     """The oracle's fp32 STFT step (forward, loss and gain gradient; built
     with the reference C backend's -O3 -ffast-math policy) on `signals` of the
@@ -466,16 +540,18 @@ def main() -> int:
                     help="instead of timing: run the dominant op alone this many times (for rocprofv3 --pmc)")
     ap.add_argument("--no-graphs", dest="graphs", action="store_false",
                     help="enqueue every kernel from the host instead of replaying each step as a HIP graph")
-    ap.add_argument("--workload", choices=("harmonic", "biquad", "stft", "membrane", "oscbank"), default="harmonic")
+    ap.add_argument("--workload", choices=("harmonic", "biquad", "stft", "membrane", "oscbank", "svf", "svf-sat"),
+                    default="harmonic")
     ap.add_argument("--mem-steps", type=int, default=16, help="membrane frames per time-blocked launch")
-    ap.add_argument("--chunk", type=int, default=256, help="biquad scan chunk length (frames)")
+    ap.add_argument("--chunk", type=int, default=256, help="biquad / SVF scan chunk length (frames)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this backend runs on one GPU; the multi-GPU "
               f"design (lane sharding + one gradient all-reduce) is not built.", file=sys.stderr)
         return 2
     run = {"biquad": run_biquad, "stft": run_stft, "membrane": run_membrane, "harmonic": run_harmonic,
-           "oscbank": run_oscbank}[args.workload]
+           "oscbank": run_oscbank, "svf": lambda a: run_svf(a, False),
+           "svf-sat": lambda a: run_svf(a, True)}[args.workload]
     res = run(args)
     if res is not None:
         print(json.dumps(res), flush=True)

@@ -81,10 +81,21 @@ __device__ __forceinline__ float raw_cutoff(float base, float m, float e, const 
 }
 
 // One frame of the fp32 program: cells (c1, c2) -> next; returns y.
+// (the saturation's quotients: reciprocal + one correction, like 1/Q)
+template <bool SAT>
+__device__ __forceinline__ float sat_div(float c, float ks) {
+  if constexpr (!SAT) {
+    return c;
+  } else {
+    const float d = 1.0f + fabsf(ks * c);
+    return div_rn(c, d, rcp_rn(d));
+  }
+}
+
 template <bool SAT>
 __device__ __forceinline__ float svf_step(const SvfK& K, float ks, float x, float& c1, float& c2) {
-  const float s1 = SAT ? c1 / (1.0f + fabsf(ks * c1)) : c1;
-  const float s2 = SAT ? c2 / (1.0f + fabsf(ks * c2)) : c2;
+  const float s1 = sat_div<SAT>(c1, ks);
+  const float s2 = sat_div<SAT>(c2, ks);
   const float v3 = x - s2;
   const float v1 = K.a1 * s1 + K.a2 * v3;
   const float ic1 = 2.0f * v1 - s1;
@@ -225,15 +236,33 @@ __global__ __launch_bounds__(kThreads) void k_svf_fwd(const float* __restrict__ 
   }
 }
 
+// g = tan(pi fc / sr) of every (frame, lane) into a tape [T][B]: it does not
+// depend on the cells, so the saturating forward's sequential loop reads it
+// instead of evaluating tan (a1 and a2 follow from g in a few operations off
+// the loop's dependency chain).  One load per frame: the sequential loop is
+// bound by its outstanding memory operations, not by arithmetic.
+__global__ __launch_bounds__(kThreads) void k_svf_coef(Ctl ctl, const float* __restrict__ prm,
+                                                       float* __restrict__ tape, int B, int T, int L, float sr) {
+  Lane l;
+  if (!lane_chunk(prm, B, T, L, sr, false, l)) return;
+  for (int n = l.n0; n < l.n1; ++n) {
+    const SvfK K = svf_coef(raw_cutoff(l.base, ctl.m ? ctl.m[n] : 1.0f, ctl.env ? ctl.env[n] : 0.0f, ctl), l.kd,
+                            sr, l.rsr);
+    tape[(size_t)n * B + l.k] = K.g;
+  }
+}
+
 // Saturating forward: one lane per thread over all frames, from the state
 // cell ([2][B], or zero) and back into it; loss partials per L-frame chunk.
+// TAPE: coefficients from k_svf_coef's tape, else evaluated in the loop.
 // sanitize: out stores map non-finite values to 0 (CRenderer.swift:1021-1039).
-template <bool LOSS>
+template <bool LOSS, bool TAPE>
 __global__ __launch_bounds__(kSeqThreads) void k_svf_seq(const float* __restrict__ x, Ctl ctl,
-                                                         const float* __restrict__ prm, float* __restrict__ state,
-                                                         int reset, float* __restrict__ y, float* __restrict__ cells,
-                                                         const float* __restrict__ tgt, float* __restrict__ lossp,
-                                                         int B, int T, int L, float sr, int sanitize) {
+                                                         const float* __restrict__ prm, const float* __restrict__ tape,
+                                                         float* __restrict__ state, int reset, float* __restrict__ y,
+                                                         float* __restrict__ cells, const float* __restrict__ tgt,
+                                                         float* __restrict__ lossp, int B, int T, int L, float sr,
+                                                         int sanitize) {
   const int k = blockIdx.x * kSeqThreads + threadIdx.x;
   if (k >= B) return;
   const float base = prm[k], kd = 1.0f / prm[B + k], ks = prm[2 * B + k], rsr = rcp_rn(sr);
@@ -244,10 +273,25 @@ __global__ __launch_bounds__(kSeqThreads) void k_svf_seq(const float* __restrict
   }
   const size_t plane = (size_t)T * B;
   const int C = (T + L - 1) / L;
+  constexpr int NS = 1 + (LOSS ? 1 : 0) + (TAPE ? 1 : 0);
+  const float* src[NS];
+  src[0] = x;
+  if constexpr (LOSS) src[1] = tgt;
+  if constexpr (TAPE) src[NS - 1] = tape;
+  const float* const(&csrc)[NS] = src;
+  const Ctl none{nullptr, nullptr};
   for (int c = 0; c < C; ++c) {
     float ls = 0.0f;
     auto step = [&](int n, const float* v, float m, float e) {
-      const SvfK K = svf_coef(raw_cutoff(base, m, e, ctl), kd, sr, rsr);
+      SvfK K;
+      if constexpr (TAPE) {
+        K.g = v[NS - 1];
+        K.Q = 1.0f + K.g * (K.g + kd);
+        K.a1 = rcp_rn(K.Q);
+        K.a2 = K.g * K.a1;
+      } else {
+        K = svf_coef(raw_cutoff(base, m, e, ctl), kd, sr, rsr);
+      }
       const size_t i = (size_t)n * B + k;
       if (cells) {
         cells[i] = c1;
@@ -261,14 +305,8 @@ __global__ __launch_bounds__(kSeqThreads) void k_svf_seq(const float* __restrict
       }
     };
     const int n0 = c * L, n1 = min(T, n0 + L);
-    if constexpr (LOSS) {
-      const float* const src[2] = {x, tgt};
-      walk<2, false>(src, ctl, B, k, n0, n1, step);
-      lossp[(size_t)c * B + k] = ls;
-    } else {
-      const float* const src[1] = {x};
-      walk<1, false>(src, ctl, B, k, n0, n1, step);
-    }
+    walk<NS, false>(csrc, TAPE ? none : ctl, B, k, n0, n1, step);
+    if constexpr (LOSS) lossp[(size_t)c * B + k] = ls;
   }
   if (state) {
     state[k] = c1;
@@ -307,10 +345,10 @@ __global__ __launch_bounds__(kThreads) void k_svf_adj_chunk(Ctl ctl, const float
     const SvfK K = svf_coef(raw_cutoff(l.base, m, e, ctl), l.kd, sr, l.rsr);
     double J1 = 1.0, J2 = 1.0;
     if constexpr (SAT) {
-      const double ks = l.ks, c1 = v[2], c2 = v[3];
-      const double D1 = 1.0 + fabs(ks * c1), D2 = 1.0 + fabs(ks * c2);
-      J1 = 1.0 / D1 - (c1 / (D1 * D1)) * sgn(l.ks * v[2]) * ks;
-      J2 = 1.0 / D2 - (c2 / (D2 * D2)) * sgn(l.ks * v[3]) * ks;
+      // ds/dc = 1/D - (c/D^2) sgn(ks c) ks = (D - |ks c|)/D^2 = 1/D^2
+      const float r1 = rcp_rn(1.0f + fabsf(l.ks * v[2])), r2 = rcp_rn(1.0f + fabsf(l.ks * v[3]));
+      J1 = (double)r1 * (double)r1;
+      J2 = (double)r2 * (double)r2;
     }
     const double a1 = K.a1, a2 = K.a2, g = K.g;
     const double ee = 2.0 * ((double)v[0] - (double)v[1]);
@@ -358,7 +396,7 @@ __global__ __launch_bounds__(kThreads) void k_svf_bwd(const float* __restrict__ 
     const SvfK K = svf_coef(raw_cutoff(l.base, m, e, ctl), l.kd, sr, l.rsr);
     const float c1 = v[3], c2 = v[4];
     const float D1 = 1.0f + fabsf(ks * c1), D2 = 1.0f + fabsf(ks * c2);
-    const float s1 = SAT ? c1 / D1 : c1, s2 = SAT ? c2 / D2 : c2;
+    const float s1 = sat_div<SAT>(c1, ks), s2 = sat_div<SAT>(c2, ks);
     const float v3 = v[0] - s2;
     const float v1 = K.a1 * s1 + K.a2 * v3;
     const float ic1 = 2.0f * v1 - s1;
@@ -380,9 +418,11 @@ __global__ __launch_bounds__(kThreads) void k_svf_bwd(const float* __restrict__ 
     if (xbar) xbar[(size_t)n * B + k] = v3_b;
     s2_b -= v3_b;
     if constexpr (SAT) {
-      const float q1 = (c1 / (D1 * D1)) * sgn(ks * c1), q2 = (c2 / (D2 * D2)) * sgn(ks * c2);
-      L1 = s1_b * (1.0f / D1 - q1 * ks);
-      L2 = s2_b * (1.0f / D2 - q2 * ks);
+      // ds/dc = 1/D^2, ds/dks = -(c/D^2) sgn(ks c) c = -s |c| sgn(ks) / D
+      const float r1 = rcp_rn(D1), r2 = rcp_rn(D2);
+      const float q1 = (c1 * (r1 * r1)) * sgn(ks * c1), q2 = (c2 * (r2 * r2)) * sgn(ks * c2);
+      L1 = s1_b * (r1 * r1);
+      L2 = s2_b * (r2 * r2);
       gks += -(s1_b * q1 * c1) - s2_b * q2 * c2;
     } else {
       L1 = s1_b;
@@ -494,6 +534,7 @@ int launch_svf_fwd(const Launch& L, const dgen_hip_op& op) {
 int launch_svf_seq(const Launch& L, const dgen_hip_op& op) {
   // arg: [0]=x [1]=mod [2]=env [3]=params ([3][B]) [4]=state ([2][B]) or -1 [5]=y [6]=cells or -1
   //      [7]=target or -1 [8]=loss partials ([C][B]) or -1 [9]=B [10]=T [11]=L [12]=sanitize
+  //      [13]=coefficient tape ([T][B]) or -1
   // As DGEN_HIP_K_STREAM_SVF: state required, no cells or loss, and a run
   // processes the first frame_count frames.
   const int64_t x = op.arg[0], prm = op.arg[3], st = op.arg[4], y = op.arg[5], cl = op.arg[6], tgt = op.arg[7],
@@ -502,7 +543,9 @@ int launch_svf_seq(const Launch& L, const dgen_hip_op& op) {
   SvfShape s;
   if (int rc = svf_shape(op.arg[9], op.arg[10], op.arg[11], s, "svf_seq")) return rc;
   const int64_t T = stream ? std::min<int64_t>(s.T, L.frames) : s.T;
-  DGEN_REQUIRE(!stream || (st >= 0 && cl < 0 && tgt < 0), "stream_svf: needs a state cell, stores no cells or loss");
+  const int64_t tape = op.arg[13];
+  DGEN_REQUIRE(!stream || (st >= 0 && cl < 0 && tgt < 0 && tape < 0),
+               "stream_svf: needs a state cell, stores no cells, loss or coefficient tape");
   Ctl ctl{};
   if (int rc = svf_ctl(L, op.arg[1], op.arg[2], s.T, "svf_seq.mod/env", ctl)) return rc;
   float sr;
@@ -517,17 +560,28 @@ int launch_svf_seq(const Launch& L, const dgen_hip_op& op) {
     DGEN_CHECK_CELL(L, tgt, s.B * s.T, "svf_seq.target");
     DGEN_CHECK_CELL(L, lossp, s.C * s.B, "svf_seq.loss_partials");
   }
+  if (tape >= 0) DGEN_CHECK_CELL(L, tape, s.B * s.T, "svf_seq.coefficient_tape");
   if (L.dry) return 0;
   const dim3 grid((unsigned)((s.B + kSeqThreads - 1) / kSeqThreads));
   float* sp = st >= 0 ? cell(L, st) : nullptr;
   float* cp = cl >= 0 ? cell(L, cl) : nullptr;
   const int reset = stream && L.reset ? 1 : 0, san = op.arg[12] ? 1 : 0;
+  float* tp = tape >= 0 ? cell(L, tape) : nullptr;
+  if (tp) {
+    hipLaunchKernelGGL(k_svf_coef, svf_grid(s), dim3(kThreads), 0, L.stream, ctl, cell(L, prm), tp, (int)s.B,
+                       (int)s.T, (int)s.L, sr);
+    DGEN_LAUNCH_CHECK("k_svf_coef");
+  }
+  float* tg = tgt >= 0 ? cell(L, tgt) : nullptr;
+  float* lp = lossp >= 0 ? cell(L, lossp) : nullptr;
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, dim3(kSeqThreads), 0, L.stream, cell(L, x), ctl, cell(L, prm), tp, sp, reset,
+                       cell(L, y), cp, tg, lp, (int)s.B, (int)T, (int)s.L, sr, san);
+  };
   if (tgt >= 0)
-    hipLaunchKernelGGL(k_svf_seq<true>, grid, dim3(kSeqThreads), 0, L.stream, cell(L, x), ctl, cell(L, prm), sp,
-                       reset, cell(L, y), cp, cell(L, tgt), cell(L, lossp), (int)s.B, (int)T, (int)s.L, sr, san);
+    tp ? go(k_svf_seq<true, true>) : go(k_svf_seq<true, false>);
   else
-    hipLaunchKernelGGL(k_svf_seq<false>, grid, dim3(kSeqThreads), 0, L.stream, cell(L, x), ctl, cell(L, prm), sp,
-                       reset, cell(L, y), cp, nullptr, nullptr, (int)s.B, (int)T, (int)s.L, sr, san);
+    tp ? go(k_svf_seq<false, true>) : go(k_svf_seq<false, false>);
   DGEN_LAUNCH_CHECK("k_svf_seq");
   return 0;
 }

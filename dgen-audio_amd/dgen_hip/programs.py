@@ -520,9 +520,10 @@ def svf_program(cfg: SvfConfig, train: bool = True, optimizer: bool = True, satu
     lossp = p.alloc("loss_partials", C * B) if train else -1
     # per lane-frame: coefficients (clip, div, tan, 1/Q, 4 mul/add) ~ 30 flops, one SVF frame 12
     if sat:
-        p.add(R.K_SVF_SEQ, [x, mod, env, prm, -1, y, cells, tgt, lossp, B, T, L, 0], sr, label="svf_seq",
-              dispatch=f"fixedWithFrameLoop({B})", bytes=n * f4 * (5 if train else 2) + ctl_b,
-              flops=n * (30 + 18), bound="valu")
+        tape = p.alloc("coef_tape", T * B)
+        p.add(R.K_SVF_SEQ, [x, mod, env, prm, -1, y, cells, tgt, lossp, B, T, L, 0, tape], sr, label="svf_seq",
+              dispatch=f"coefficient tape + fixedWithFrameLoop({B})",
+              bytes=n * f4 * ((5 if train else 2) + 2) + ctl_b, flops=n * (30 + 18), bound="valu")
     else:
         summ = p.alloc("summary", 12 * C * B)  # fp64
         init = p.alloc("init", 2 * C * B)
@@ -582,7 +583,7 @@ def stream_svf_program(cfg: SvfConfig, max_frames: int | None = None) -> Program
     prm = p.alloc("params", 3 * B)
     st = p.alloc("state", 2 * B)
     y = p.alloc("y", T * B)
-    p.add(R.K_STREAM_SVF, [x, mod, env, prm, st, y, -1, -1, -1, B, T, SVF_CHUNK, 1], [cfg.sr], label="stream_svf",
+    p.add(R.K_STREAM_SVF, [x, mod, env, prm, st, y, -1, -1, -1, B, T, SVF_CHUNK, 1, -1], [cfg.sr], label="stream_svf",
           dispatch=f"fixedWithFrameLoop({B})", bytes=8.0 * T * B, flops=float(T * B) * (30 + 18), bound="valu")
     p.output_cell = "y"
     ins = [("x", k, B) for k in range(B)] + [("mod", 0, 1), ("env", 0, 1)]

@@ -331,7 +331,9 @@ enum dgen_hip_kernel {
    * reference's per-lane frame loop); loss partials per L-frame chunk.
    * arg: [0]=x [1]=mod [2]=env [3]=params [4]=state ([2][B]) or -1 [5]=y
    *      [6]=cells or -1 [7]=target or -1 [8]=loss partials or -1 [9]=B
-   *      [10]=T [11]=L [12]=sanitize (non-finite out stores -> 0) */
+   *      [10]=T [11]=L [12]=sanitize (non-finite out stores -> 0)
+   *      [13]=coefficient tape ([T][B]: g, filled by the call before the
+   *      sequential loop reads it) or -1 (evaluated in the loop) */
   DGEN_HIP_K_SVF_SEQ = 35,
 
   /* BPTT part 1: per (lane, chunk), reverse, the cells' adjoint from a zero
