@@ -60,11 +60,19 @@ __device__ __forceinline__ float hw_rcp(float v) { return __builtin_amdgcn_rcpf(
 
 // LDS of one size's launch, sized for that size (smaller sizes fit more
 // workgroups per CU).
+// The tile accumulator is stored with 2 pad floats after every 64 samples:
+// a group's windows start N samples apart, so without the pad every window
+// of a wave (1024/N of them for N <= 512) would hit the same LDS banks in the
+// overlap-add; with it window s is shifted by 2s (N/64) banks.  Pairs (even
+// sample index) never straddle a pad and stay 8-byte aligned.
+__device__ __forceinline__ int accp(int i) { return i + 2 * (i >> 6); }
+__host__ __device__ constexpr int acc_floats(int n) { return n + 2 * (n >> 6) + 2; }
+
 template <int LOGN>
 struct MssLds {
   static constexpr int N = 1 << LOGN, M = N / 2;
   static constexpr int kAccN = kTile + N;  // dx of samples [a - (N-1), a + kTile), + 1 pad (even length)
-  float acc[kAccN];
+  float acc[acc_floats(kAccN)];
   c2 buf[lds_pad(2048)];           // FFT slots: (4096/N windows) x (N/2), padded
   c2 aux[lds_pad(2048)];           // second signal's spectrum / gradient spectrum
   float red[kThreads / 64][2];
@@ -290,7 +298,7 @@ __device__ __forceinline__ void mss_size(const MssArgs& a, MssLds<LOGN>& L, int 
         const int t = s0 + 2 * op[e];
         a0w[e] = live && t >= 0 && t < a.T;
         a1w[e] = live && t + 1 >= 0 && t + 1 < a.T;
-        ai[e] = min(max(t - (a0 - (N - 1)), 0), kAccN - 2);
+        ai[e] = accp(min(max(t - (a0 - (N - 1)), 0), kAccN - 2));
         ac[e] = *reinterpret_cast<const float2*>(&L.acc[ai[e]]);
       }
 #pragma unroll
@@ -332,11 +340,11 @@ __global__ __launch_bounds__(kThreads) void k_mss(MssArgs a, int si, int first) 
     }
 #pragma unroll
     for (int q = 0; q < AP; ++q)
-      if ((int)threadIdx.x + q * kThreads < kSpan) L.acc[threadIdx.x + q * kThreads] = av[q];
+      if ((int)threadIdx.x + q * kThreads < kSpan) L.acc[accp(threadIdx.x + q * kThreads)] = av[q];
   }
   lds_barrier();
   mss_size<LOGN>(a, L, si, b, tile);
-  for (int i = threadIdx.x; i < kSpan; i += kThreads) part[kOff + i] = L.acc[i];
+  for (int i = threadIdx.x; i < kSpan; i += kThreads) part[kOff + i] = L.acc[accp(i)];
   // the first size also clears the row's part left of its own halo
   if (first)
     for (int i = threadIdx.x; i < kOff; i += kThreads) part[i] = 0.f;

@@ -207,14 +207,13 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     garg = [dy, -1, B, T, len(sizes)] + (sizes + [0] * 8)[:8] + [mss_part] + [0] * 7 + (wloss_cells + [0] * 8)[:8]
     p.add(R.K_SPECTRAL_GATHER, garg, [wl, wg, maxf], label="spectral_combine", dispatch=f"perFrameScaled({B})",
           bytes=(B * ntiles * (MSS_TILE + 2047) + B * T) * f4, flops=float(B * T))
-    # the per-frame loss signal in a launch of its own (one row of blocks):
-    # folded into the combine, its blocks were the combine's tail (measured
-    # 25 -> 9 us + a separate 9 us); on the side stream the step measured
-    # 75 us slower
+    # the per-frame loss signal (only reported, nothing in the backward reads
+    # it) is a launch of its own at the end of stream 0, which finishes
+    # before the side stream: folded into the combine, its blocks were the
+    # combine's tail (25 -> 9 us + a separate 9 us); between the combine and
+    # the synth backward it cost the step ~9 us; on the side stream 75 us
     larg2 = [-1, lossf] + garg[2:]
     nwin_all = sum((T + N // 4 - 1) // (N // 4) for N in sizes)
-    p.add(R.K_SPECTRAL_GATHER, larg2, [wl, wg, maxf], label="loss_frames",
-          dispatch="perFrame", bytes=(nwin_all * B * 2 + T) * f4, flops=float(nwin_all * B * 2))
 
     part = p.alloc("synth_partials", B * nseg * SLOTS * LDC)
     dctrl = p.alloc("dctrl", M * LDC)
@@ -286,6 +285,8 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     p.add(R.K_COLSUM, [dcol[0], gw1, mt, (din + 1) * Hd, (din + 1) * Hd, ws_col], label="dWb_l1",
           dispatch="chunkPartialsReduceToCell", bytes=(mt + 1) * (din + 1) * Hd * f4,
           flops=float(mt * (din + 1) * Hd))
+    p.add(R.K_SPECTRAL_GATHER, larg2, [wl, wg, maxf], label="loss_frames",
+          dispatch="perFrame", bytes=(nwin_all * B * 2 + T) * f4, flops=float(nwin_all * B * 2))
     if optimizer:
         m = p.alloc("adam_m", npar)
         v = p.alloc("adam_v", npar)
