@@ -152,13 +152,17 @@ __device__ __forceinline__ float wave_sum(float v) {
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
   return v;
 }
+// e^x and ln x on the hardware exp2 / log2 (v_exp_f32, v_log_f32, ~1 ulp);
+// the argument scaling adds ~|x| 6e-8 relative to e^x.
+__device__ __forceinline__ float hw_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+__device__ __forceinline__ float hw_ln(float x) { return __builtin_amdgcn_logf(x) * 0.69314718055994531f; }
 // softplus(x) = max(x,0) + log(1 + exp(-|x|))  (Model.swift:153-157)
-__device__ __forceinline__ float softplus(float x) { return fmaxf(x, 0.f) + logf(1.f + expf(-fabsf(x))); }
+__device__ __forceinline__ float softplus(float x) { return fmaxf(x, 0.f) + hw_ln(1.f + hw_exp(-fabsf(x))); }
 // d softplus through the reference AD rules: [x>=0] - sign(x) e^{-|x|}/(1+e^{-|x|})
 __device__ __forceinline__ float softplus_grad(float x) {
-  float e = expf(-fabsf(x));
-  float sg = x > 0.f ? 1.f : (x < 0.f ? -1.f : 0.f);
-  return (x >= 0.f ? 1.f : 0.f) - sg * (e / (1.f + e));
+  const float e = hw_exp(-fabsf(x));
+  const float sg = x > 0.f ? 1.f : (x < 0.f ? -1.f : 0.f);
+  return (x >= 0.f ? 1.f : 0.f) - sg * (e * __builtin_amdgcn_rcpf(1.f + e));
 }
 
 }  // namespace dgen

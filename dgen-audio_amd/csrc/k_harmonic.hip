@@ -28,6 +28,7 @@
 
 #include <type_traits>
 
+#include "dev_math.h"
 #include "internal.h"
 
 namespace dgen {
@@ -838,7 +839,7 @@ __global__ void k_synth_bwd_reduce(const float* __restrict__ part, const float* 
     const bool amp = c < K, gain = c == K || c == K + 1, noise = c >= K + 2 && c < K + 2 + NF;
     const float z = (amp || gain || noise) ? Z[row * ldc + c] : 0.f;
     const float sp = amp ? softplus(z) : 0.f;
-    const float th = noise ? tanhf(z) : 0.f;
+    const float th = noise ? fast_tanh(z) : 0.f;
     float r0 = wave_sum(sp), r1 = wave_sum(fabsf(th));
     if (lane == 0) {
       red[wave][0] = r0;
@@ -852,8 +853,9 @@ __global__ void k_synth_bwd_reduce(const float* __restrict__ part, const float* 
     }
     den += 1e-6f;
     nrm += 1e-4f;
-    r0 = wave_sum(amp ? s * (sp / den) : 0.f);
-    r1 = wave_sum(noise ? s * (th / nrm) : 0.f);
+    const float rden = rcp_rn(den), rnrm = rcp_rn(nrm);
+    r0 = wave_sum(amp ? s * (sp * rden) : 0.f);
+    r1 = wave_sum(noise ? s * (th * rnrm) : 0.f);
     if (lane == 0) {
       red[wave][2] = r0;
       red[wave][3] = r1;
@@ -866,12 +868,12 @@ __global__ void k_synth_bwd_reduce(const float* __restrict__ part, const float* 
     }
     float out = 0.f;  // padding columns stay exactly zero
     if (amp) {
-      out = (s - dot) / den * softplus_grad(z);
+      out = (s - dot) * rden * softplus_grad(z);
     } else if (gain) {
       out = s * softplus_grad(z);
     } else if (noise) {
       const float sg = th > 0.f ? 1.f : (th < 0.f ? -1.f : 0.f);
-      out = (s - sg * dot2) / nrm * (1.f - th * th);
+      out = (s - sg * dot2) * rnrm * (1.f - th * th);
     }
     if (c < ldc) dZ[row * ldc + c] = out;
   }

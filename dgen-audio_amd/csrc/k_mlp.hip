@@ -8,6 +8,7 @@
 //
 // Reductions are deterministic: fixed-order per-thread loops and fixed-shape
 // two-stage sums, no atomics.
+#include "dev_math.h"
 #include "internal.h"
 
 namespace dgen {
@@ -239,10 +240,11 @@ __global__ void k_heads_fwd(const float* __restrict__ Z, int ldz, float* __restr
     if (k < K) den += sp[q];
   }
   den = wave_sum(den) + 1e-6f;
+  const float rden = rcp_rn(den);
 #pragma unroll
   for (int q = 0; q < kHeadPer; ++q) {
     const int k = lane + q * kWave;
-    if (k < K) c[k] = sp[q] / den;
+    if (k < K) c[k] = sp[q] * rden;
   }
   if (lane == 0) {
     c[K] = softplus(z[K]);
@@ -252,14 +254,15 @@ __global__ void k_heads_fwd(const float* __restrict__ Z, int ldz, float* __restr
 #pragma unroll
   for (int q = 0; q < kHeadPer; ++q) {
     const int i = lane + q * kWave;
-    th[q] = i < NF ? tanhf(z[K + 2 + i]) : 0.f;
+    th[q] = i < NF ? fast_tanh(z[K + 2 + i]) : 0.f;
     if (i < NF) nrm += fabsf(th[q]);
   }
   nrm = wave_sum(nrm) + 1e-4f;
+  const float rnrm = rcp_rn(nrm);
 #pragma unroll
   for (int q = 0; q < kHeadPer; ++q) {
     const int i = lane + q * kWave;
-    if (i < NF) c[K + 2 + i] = th[q] / nrm;
+    if (i < NF) c[K + 2 + i] = th[q] * rnrm;
   }
 }
 
