@@ -147,6 +147,11 @@ int launch_svf_seq(const Launch&, const dgen_hip_op&);
 int launch_svf_adj_chunk(const Launch&, const dgen_hip_op&);
 int launch_svf_bwd(const Launch&, const dgen_hip_op&);
 
+// (segment, slot) entries listed per control row by the static row schedule
+// (a row is read by at most this many synth segments: 3 at a control hop of
+// 64 frames, ~9 at 256).
+constexpr int kRowEntries = 16;
+
 // Sum over the 64 lanes of a wave (butterfly; every lane gets the total).
 __device__ __forceinline__ float wave_sum(float v) {
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);

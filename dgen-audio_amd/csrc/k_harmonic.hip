@@ -810,15 +810,15 @@ __global__ void k_synth_bwd_reduce(const float* __restrict__ part, const float* 
   if (!HEADS && c >= ldc) return;
   float s = 0.f;
   if (c < NC) {
-    // the row's entries (a prefix of the 8, then -1), then every listed
-    // partial in flight at once; the adds keep the list order
-    const float* lst = row_list + (size_t)f * 8;
-    float e[8], v[8];
+    // the row's entries (a prefix of the kRowEntries, then -1), then every
+    // listed partial in flight at once; the adds keep the list order
+    const float* lst = row_list + (size_t)f * kRowEntries;
+    float e[kRowEntries], v[kRowEntries];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) e[q] = lst[q];
+    for (int q = 0; q < kRowEntries; ++q) e[q] = lst[q];
     bool live = true;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
+    for (int q = 0; q < kRowEntries; ++q) {
       live = live && e[q] >= 0.f;
       const int ent = live ? (int)e[q] : 0;
       const int seg = ent / kSlots, slot = ent % kSlots;
@@ -826,7 +826,7 @@ __global__ void k_synth_bwd_reduce(const float* __restrict__ part, const float* 
     }
     live = true;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
+    for (int q = 0; q < kRowEntries; ++q) {
       live = live && e[q] >= 0.f;
       if (live) s += v[q];
     }
@@ -966,7 +966,7 @@ int launch_synth_bwd_reduce(const Launch& L, const dgen_hip_op& op) {
                (long long)F, (long long)T, (long long)seg, (long long)ldc);
   const int64_t nseg = (T + seg - 1) / seg;
   DGEN_CHECK_CELL(L, part, B * nseg * kSlots * ldc, "synth_bwd_reduce.partials");
-  DGEN_CHECK_CELL(L, rl, F * 8, "synth_bwd_reduce.row_list");
+  DGEN_CHECK_CELL(L, rl, F * kRowEntries, "synth_bwd_reduce.row_list");
   DGEN_CHECK_CELL(L, dc, B * F * ldc, "synth_bwd_reduce.dctrl");
   if (heads) {
     DGEN_REQUIRE(K > 0 && NF > 0 && K + 2 + NF == NC, "synth_bwd_reduce: heads K %lld NF %lld NC %lld", (long long)K,

@@ -72,12 +72,11 @@ int launch_noise_table(const Launch& L, const dgen_hip_op& op) {
 // wrap to 0, frac, 1-frac).  Produces
 //   lerp[t][8]   = lo, hi, frac, 1-frac, slot(lo), slot(hi), 0, 0
 //   seg_rows[s][4] = distinct rows touched by frame segment s (-1 unused)
-//   row_list[f][8] = (segment*4 + slot) entries that touch row f (-1 unused)
+//   row_list[f][kRowEntries] = (segment*4 + slot) entries that touch row f (-1 unused)
 //   flag[0]      = 0 ok, 1 a segment touches > 4 rows, 2 a row has > 8 entries,
 //                  3 a non-finite playhead
 // The gradient of a row read is then reduced per row in a fixed order.
 constexpr int kSlots = 4;
-constexpr int kRowEntries = 8;
 
 __global__ void k_row_schedule(const float* play, float* lerp, float* seg_rows, float* row_list, float* flag,
                                int rows, int frames, int seg) {

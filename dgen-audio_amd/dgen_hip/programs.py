@@ -16,7 +16,7 @@ from .workloads import (BiquadConfig, HarmonicConfig, MembraneConfig, OscBankCon
 
 SEG = 64          # frames per synth segment (checkpoint spacing)
 SLOTS = 4         # control rows a segment may touch
-ROW_ENTRIES = 8   # (segment, slot) entries per control row
+ROW_ENTRIES = 16  # (segment, slot) entries per control row (kRowEntries)
 LDC = 128         # padded control-row stride (K + 2 + NF <= 128)
 SPLITK_ROWS = 1024  # rows per split of the weight-gradient GEMMs
 GEMM_TILE_M = 128  # output rows per GEMM workgroup tile (k_gemm.hip BM)
@@ -311,9 +311,9 @@ class HarmonicSession:
     forward+backward(+Adam) pass with all data resident in HBM."""
 
     def __init__(self, cfg: HarmonicConfig, device: int = 0, optimizer: bool = True, target=None,
-                 side_stream: bool = True):
+                 side_stream: bool = True, data=None):
         self.cfg = cfg
-        f0, uv, X = cfg.data()
+        f0, uv, X = cfg.data() if data is None else data
         self.f0, self.uv, self.X = f0, uv, X
         self.params0 = cfg.weights()
         if target is None:
@@ -338,6 +338,19 @@ class HarmonicSession:
             rt.write("params", params)
             rt.runNoCopy()
             return rt.read("y").reshape(self.cfg.B, self.cfg.T)
+
+    def set_batch(self, f0, uv, X, target) -> None:
+        """Stage the next batch (f0, uv [F][B], features X [B*F][din], target
+        [B][T]; e.g. ``dataset.harmonic_batch`` of cached chunks) for the
+        following steps, as the reference trainer updates its data tensors."""
+        cfg = self.cfg
+        for name, a, n in (("f0", f0, cfg.F * cfg.B), ("uv", uv, cfg.F * cfg.B), ("X", X, cfg.M * cfg.din),
+                           ("target", target, cfg.B * cfg.T)):
+            if np.asarray(a).size != n:
+                raise ValueError(f"{name}: {np.asarray(a).size} values, the session takes {n}")
+            self.rt.write(name, np.ascontiguousarray(a, np.float32))
+        self.f0, self.uv, self.X = f0, uv, X
+        self.target = np.ascontiguousarray(target, np.float32).reshape(cfg.B, cfg.T)
 
     def step(self) -> None:
         self.rt.runNoCopy()

@@ -1,0 +1,92 @@
+"""HarmonicE2E training from the dataset cache on the GPU: WAV files are
+preprocessed into a cache (dataset.preprocess), a batch of cached chunks is
+assembled as the reference trainer does (dataset.harmonic_batch: 3
+conditioning features, frame-rate f0 / uv, target audio) and one training
+step runs through the config-3 schedule; loss and gradient are checked
+against the oracle's step on the same batch, and the trained parameters
+round-trip through a checkpoint file bit for bit.  Needs a GPU."""
+import os
+import wave
+
+import numpy as np
+import pytest
+
+import oracle as O
+from dgen_hip import HarmonicConfig
+from dgen_hip import audiofile as A
+from dgen_hip import checkpoint as C
+from dgen_hip import dataset as D
+from dgen_hip.programs import HarmonicSession
+
+pytestmark = pytest.mark.gpu
+
+
+def rel(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
+
+
+def make_cache(tmp_path):
+    root, cache = str(tmp_path / "wavs"), str(tmp_path / "cache")
+    os.makedirs(root)
+    n = np.arange(40000)
+    tone = 0.4 * np.sin(2 * np.pi * 330 * n / 16000) + 0.1 * np.sin(2 * np.pi * 660 * n / 16000)
+    pcm = np.round(np.stack([tone, tone], 1) * 32767).astype(np.int16)
+    with wave.open(os.path.join(root, "a.wav"), "wb") as w:
+        w.setnchannels(2)
+        w.setsampwidth(2)
+        w.setframerate(16000)
+        w.writeframes(pcm.tobytes())
+    sweep = 0.3 * np.sin(2 * np.pi * np.cumsum(np.linspace(200, 500, 50000)) / 24000)
+    A.save(os.path.join(root, "b.wav"), sweep.astype(np.float32), 24000.0)
+    D.preprocess(root, cache, {"chunkSize": 16384, "chunkHop": 8192})
+    return D.CachedDataset.load(cache)
+
+
+def test_training_step_on_cached_chunks(gpu, tmp_path):
+    ds = make_cache(tmp_path)
+    chunks = [ds.load_chunk(e) for e in ds.entries("train")[:2]]
+    dcfg = D.make_config()
+    cfg = HarmonicConfig(B=2, T=16384, sr=24000.0, control_hop=256, din=3, K=32, NF=63, hidden=64, layers=2,
+                         fft_sizes=(512, 256, 128))
+    f0, uv, X, tgt = D.harmonic_batch(chunks, dcfg, cfg.F, cfg.T)
+    print(f"batch: {len(chunks)} chunks, F={cfg.F}, voiced frames {int(uv.sum())}", flush=True)
+    s = HarmonicSession(cfg, optimizer=False, target=tgt, data=(f0, uv, X))
+    try:
+        s.step()
+        loss, g = s.loss(), s.rt.read("grads").astype(np.float64)
+        P0 = s.params0
+    finally:
+        s.close()
+    l64, g64, _ = O.harmonic_step(cfg, X, P0, f0, uv, tgt, grad=True, prec="f64")
+    l32, g32, _ = O.harmonic_step(cfg, X, P0, f0, uv, tgt, grad=True, prec="f32")
+    print(f"loss HIP {loss:.7e} fp64 oracle {l64:.7e} fp32 oracle {l32:.7e}; grad rel L2 vs fp64 HIP "
+          f"{rel(g, g64):.3e}, fp32 oracle {rel(g32, g64):.3e}")
+    assert abs(loss - l64) <= 2.0 * abs(l32 - l64) + 1e-5 * abs(l64)
+    assert rel(g, g64) <= 2.0 * rel(g32, g64) + 1e-4
+
+
+def test_trained_parameters_round_trip_through_a_checkpoint(gpu, tmp_path):
+    ds = make_cache(tmp_path)
+    chunks = [ds.load_chunk(e) for e in ds.entries()[:2]]
+    cfg = HarmonicConfig(B=2, T=16384, sr=24000.0, control_hop=256, din=3, K=32, NF=63, hidden=64, layers=2,
+                         fft_sizes=(512, 256, 128), lr=1e-3)
+    f0, uv, X, tgt = D.harmonic_batch(chunks, D.make_config(), cfg.F, cfg.T)
+    s = HarmonicSession(cfg, optimizer=True, target=tgt, data=(f0, uv, X))
+    try:
+        s.step()
+        first = s.loss()
+        for _ in range(19):
+            s.step()
+        last = s.loss()
+        P = s.rt.read("params")
+        # the next batch (the same chunks in the other order) stages without a rebuild
+        s.set_batch(f0[:, ::-1], uv[:, ::-1], X.reshape(2, -1, 3)[::-1].reshape(-1, 3), tgt[::-1])
+        s.step()
+    finally:
+        s.close()
+    print(f"loss after 1 step {first:.6e}, after 20 {last:.6e}")
+    assert np.isfinite(last) and last < first
+    path = C.write_model_state(str(tmp_path), 20, C.harmonic_snapshots(cfg, P))
+    q = C.load_harmonic_snapshots(cfg, C.read_model_state(path).params, cfg.weights())
+    np.testing.assert_array_equal(q, P)
