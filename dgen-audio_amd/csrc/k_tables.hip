@@ -13,19 +13,30 @@
 namespace dgen {
 
 // u_accum (Sources/DGen/Definitions.swift:215-246) with constant increment,
-// reset 0; output = clip(pre-increment value, lo, hi).
+// reset 0; output = clip(pre-increment value, lo, hi).  The chain is
+// sequential in fp32.  Where next lies in [mn, mn + span * 0.99) the wrap
+// quotient (next - mn) / span rounds below 1, so k = 0 and w = next exactly:
+// those frames skip the division (the chain's slow part); the others take
+// the full expression.
 __global__ void k_accum_table(float* out, int frames, float step, float mn, float mx, float lo, float hi) {
   if (blockIdx.x != 0 || threadIdx.x != 0) return;
   float acc = 0.f;
   const float span = mx - mn;
+  const float safe = span * 0.99f;
   for (int t = 0; t < frames; ++t) {
-    float prev = acc;
-    float next = acc + step;
-    float k = floorf((next - mn) / span);
-    float w = next - k * span;
-    if (w >= mx) w = w - span;
+    const float prev = acc;
+    const float next = acc + step;
+    const float d = next - mn;
+    float w;
+    if (d >= 0.f && d < safe) {
+      w = next;
+    } else {
+      const float k = floorf(d / span);
+      w = next - k * span;
+      if (w >= mx) w = w - span;
+    }
     acc = w;
-    float p = prev < lo ? lo : prev;
+    const float p = prev < lo ? lo : prev;
     out[t] = p > hi ? hi : p;
   }
 }
@@ -44,16 +55,60 @@ int launch_accum_table(const Launch& L, const dgen_hip_op& op) {
 
 // Signal.noise(): xorshift32 on a zeroed float cell (state 0 -> 1), output
 // s / 2^32 (Sources/DGen/Renderer/CRenderer.swift:685-693).  Every run starts
-// from the zeroed cell, so the per-run stream is this fixed sequence.
-__global__ void k_noise_table(float* out, int frames) {
-  if (blockIdx.x != 0 || threadIdx.x != 0) return;
-  uint32_t s = 0u;
-  for (int t = 0; t < frames; ++t) {
-    if (s == 0u) s = 1u;
-    s ^= s << 13;
-    s ^= s >> 17;
-    s ^= s << 5;
+// from the zeroed cell, so the per-run stream is this fixed sequence:
+// s_1 = xs(1), s_{n+1} = xs(s_n), out[n] = s_{n+1} / 2^32.
+//
+// xs is linear over GF(2) (shifts and xors), so s_n = M^(n-1) s_1 with M the
+// 32x32 bit matrix whose column b is xs(1 << b).  Each of kNoiseThreads
+// threads jumps to the start of its run of frames with M^chunk raised to its
+// index (binary powering of bit matrices) and steps the run sequentially.
+constexpr int kNoiseThreads = 256;
+
+__device__ __forceinline__ uint32_t xs32(uint32_t s) {
+  s ^= s << 13;
+  s ^= s >> 17;
+  s ^= s << 5;
+  return s;
+}
+struct BitMat {
+  uint32_t c[32];  // column b = image of bit b
+};
+__device__ __forceinline__ uint32_t bm_apply(const BitMat& m, uint32_t x) {
+  uint32_t y = 0u;
+#pragma unroll
+  for (int b = 0; b < 32; ++b) y ^= ((x >> b) & 1u) ? m.c[b] : 0u;
+  return y;
+}
+__device__ __forceinline__ BitMat bm_mul(const BitMat& a, const BitMat& b) {  // a after b
+  BitMat r;
+#pragma unroll
+  for (int k = 0; k < 32; ++k) r.c[k] = bm_apply(a, b.c[k]);
+  return r;
+}
+__device__ __forceinline__ BitMat bm_pow(BitMat base, uint32_t e) {
+  BitMat r;
+#pragma unroll
+  for (int k = 0; k < 32; ++k) r.c[k] = 1u << k;
+  while (e) {
+    if (e & 1u) r = bm_mul(base, r);
+    base = bm_mul(base, base);
+    e >>= 1;
+  }
+  return r;
+}
+
+__global__ __launch_bounds__(kNoiseThreads) void k_noise_table(float* out, int frames) {
+  const int i = threadIdx.x;
+  const int chunk = (frames + kNoiseThreads - 1) / kNoiseThreads;
+  const int t0 = i * chunk, t1 = min(frames, t0 + chunk);
+  if (t0 >= t1) return;
+  BitMat m;
+#pragma unroll
+  for (int b = 0; b < 32; ++b) m.c[b] = xs32(1u << b);
+  uint32_t s = bm_apply(bm_pow(bm_pow(m, (uint32_t)chunk), (uint32_t)i), xs32(1u));  // s_{t0 + 1}
+  for (int t = t0; t < t1; ++t) {
     out[t] = (float)s / 4294967296.0f;
+    s = xs32(s);
   }
 }
 
@@ -62,7 +117,7 @@ int launch_noise_table(const Launch& L, const dgen_hip_op& op) {
   DGEN_REQUIRE(frames > 0 && frames <= (1 << 26), "noise_table: frames %lld", (long long)frames);
   DGEN_CHECK_CELL(L, out, frames, "noise_table.out");
   if (L.dry) return 0;
-  hipLaunchKernelGGL(k_noise_table, dim3(1), dim3(64), 0, L.stream, cell(L, out), (int)frames);
+  hipLaunchKernelGGL(k_noise_table, dim3(1), dim3(kNoiseThreads), 0, L.stream, cell(L, out), (int)frames);
   DGEN_LAUNCH_CHECK("k_noise_table");
   return 0;
 }
@@ -71,75 +126,108 @@ int launch_noise_table(const Launch& L, const dgen_hip_op& op) {
 // (Sources/DGen/Emit+RowSelection.swift:164-197: fmod wrap, floor/ceil with
 // wrap to 0, frac, 1-frac).  Produces
 //   lerp[t][8]   = lo, hi, frac, 1-frac, slot(lo), slot(hi), 0, 0
-//   seg_rows[s][4] = distinct rows touched by frame segment s (-1 unused)
-//   row_list[f][kRowEntries] = (segment*4 + slot) entries that touch row f (-1 unused)
-//   flag[0]      = 0 ok, 1 a segment touches > 4 rows, 2 a row has > 8 entries,
-//                  3 a non-finite playhead
+//   seg_rows[s][4] = distinct rows touched by frame segment s, in the order
+//                  its frames first touch them (-1 unused)
+//   row_list[f][kRowEntries] = (segment*4 + slot) entries that touch row f,
+//                  in segment order (-1 unused)
+//   flag[0]      = 0 ok; else the largest of 1 (a segment touches > 4 rows),
+//                  2 (a row has > kRowEntries entries), 3 (a non-finite playhead)
 // The gradient of a row read is then reduced per row in a fixed order.
+// Two passes: a thread per segment (its frames in order), then a thread per
+// row (every segment's rows, in segment order).
 constexpr int kSlots = 4;
+constexpr int kSchedThreads = 256;
 
-__global__ void k_row_schedule(const float* play, float* lerp, float* seg_rows, float* row_list, float* flag,
-                               int rows, int frames, int seg) {
-  if (blockIdx.x != 0 || threadIdx.x != 0) return;
+__global__ __launch_bounds__(kSchedThreads) void k_row_segments(const float* play, float* lerp, float* seg_rows,
+                                                                 float* seg_status, int rows, int frames, int seg) {
+  const int s = blockIdx.x * kSchedThreads + threadIdx.x;
   const int nseg = (frames + seg - 1) / seg;
-  for (int i = 0; i < nseg * kSlots; ++i) seg_rows[i] = -1.f;
-  for (int i = 0; i < rows * kRowEntries; ++i) row_list[i] = -1.f;
-  float status = 0.f;
+  if (s >= nseg) return;
   const float nr = (float)rows;
-  for (int s = 0; s < nseg; ++s) {
-    int srow[kSlots] = {-1, -1, -1, -1};
-    int nslot = 0;
-    for (int t = s * seg; t < frames && t < (s + 1) * seg; ++t) {
-      float w = fmodf(play[t], nr);
-      if (w < 0.f) w = w + nr;
-      float fl = floorf(w);
-      if (!(fl >= 0.f && fl < nr)) {  // non-finite playhead: keep every index in range
-        fl = 0.f;
-        w = 0.f;
-        status = 3.f;
-      }
-      float ce = fl + 1.0f;
-      if (ce >= nr) ce = 0.f;
-      float frac = w - fl;
-      int ids[2] = {(int)fl, (int)ce};
-      int slots[2] = {0, 0};
-      for (int q = 0; q < 2; ++q) {
-        int found = -1;
-        for (int j = 0; j < nslot; ++j)
-          if (srow[j] == ids[q]) found = j;
-        if (found < 0) {
-          if (nslot < kSlots) {
-            srow[nslot] = ids[q];
-            found = nslot++;
-          } else {
-            status = 1.f;
-            found = 0;
-          }
-        }
-        slots[q] = found;
-      }
-      float* e = lerp + (size_t)t * 8;
-      e[0] = fl;
-      e[1] = ce;
-      e[2] = frac;
-      e[3] = 1.0f - frac;
-      e[4] = (float)slots[0];
-      e[5] = (float)slots[1];
-      e[6] = 0.f;
-      e[7] = 0.f;
+  int srow[kSlots] = {-1, -1, -1, -1};
+  int nslot = 0;
+  float status = 0.f;
+  for (int t = s * seg; t < frames && t < (s + 1) * seg; ++t) {
+    float w = fmodf(play[t], nr);
+    if (w < 0.f) w = w + nr;
+    float fl = floorf(w);
+    if (!(fl >= 0.f && fl < nr)) {  // non-finite playhead: keep every index in range
+      fl = 0.f;
+      w = 0.f;
+      status = fmaxf(status, 3.f);
     }
-    for (int j = 0; j < nslot; ++j) {
-      seg_rows[s * kSlots + j] = (float)srow[j];
-      float* lst = row_list + (size_t)srow[j] * kRowEntries;
-      int q = 0;
-      while (q < kRowEntries && lst[q] >= 0.f) ++q;
+    float ce = fl + 1.0f;
+    if (ce >= nr) ce = 0.f;
+    const float frac = w - fl;
+    const int ids[2] = {(int)fl, (int)ce};
+    int slots[2] = {0, 0};
+    for (int q = 0; q < 2; ++q) {
+      int found = -1;
+      for (int j = 0; j < nslot; ++j)
+        if (srow[j] == ids[q]) found = j;
+      if (found < 0) {
+        if (nslot < kSlots) {
+          srow[nslot] = ids[q];
+          found = nslot++;
+        } else {
+          status = fmaxf(status, 1.f);
+          found = 0;
+        }
+      }
+      slots[q] = found;
+    }
+    float* e = lerp + (size_t)t * 8;
+    e[0] = fl;
+    e[1] = ce;
+    e[2] = frac;
+    e[3] = 1.0f - frac;
+    e[4] = (float)slots[0];
+    e[5] = (float)slots[1];
+    e[6] = 0.f;
+    e[7] = 0.f;
+  }
+  for (int j = 0; j < kSlots; ++j) seg_rows[s * kSlots + j] = (float)srow[j];
+  seg_status[s] = status;
+}
+
+__global__ __launch_bounds__(kSchedThreads) void k_row_lists(const float* seg_rows, const float* seg_status,
+                                                              float* row_list, float* row_status, int rows,
+                                                              int nseg) {
+  const int f = blockIdx.x * kSchedThreads + threadIdx.x;
+  if (f >= rows) return;
+  float* lst = row_list + (size_t)f * kRowEntries;
+  int q = 0;
+  float status = 0.f;
+  for (int s = 0; s < nseg; ++s) {
+    const float4 r = *reinterpret_cast<const float4*>(seg_rows + (size_t)s * kSlots);
+    const float rv[kSlots] = {r.x, r.y, r.z, r.w};
+    for (int j = 0; j < kSlots; ++j) {
+      if ((int)rv[j] != f || rv[j] < 0.f) continue;
       if (q < kRowEntries)
-        lst[q] = (float)(s * kSlots + j);
+        lst[q++] = (float)(s * kSlots + j);
       else
         status = 2.f;
     }
   }
-  flag[0] = status;
+  for (int k = q; k < kRowEntries; ++k) lst[k] = -1.f;
+  // the row's status, and (row 0) the segments' largest
+  if (f == 0)
+    for (int s = 0; s < nseg; ++s) status = fmaxf(status, seg_status[s]);
+  row_status[f] = status;
+}
+
+// flag = the largest status (one workgroup, fixed order).
+__global__ __launch_bounds__(kSchedThreads) void k_row_flag(const float* row_status, float* flag, int rows) {
+  __shared__ float red[kSchedThreads];
+  float m = 0.f;
+  for (int f = threadIdx.x; f < rows; f += kSchedThreads) m = fmaxf(m, row_status[f]);
+  red[threadIdx.x] = m;
+  __syncthreads();
+  for (int w = kSchedThreads / 2; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + w]);
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) flag[0] = red[0];
 }
 
 int launch_row_schedule(const Launch& L, const dgen_hip_op& op) {
@@ -153,10 +241,21 @@ int launch_row_schedule(const Launch& L, const dgen_hip_op& op) {
   DGEN_CHECK_CELL(L, segr, nseg * kSlots, "row_schedule.seg_rows");
   DGEN_CHECK_CELL(L, rowl, rows * kRowEntries, "row_schedule.row_list");
   DGEN_CHECK_CELL(L, flag, 1, "row_schedule.flag");
+  const int64_t ws = op.arg[8];
+  DGEN_CHECK_CELL(L, ws, nseg + rows, "row_schedule.workspace");
+  DGEN_REQUIRE(segr % 4 == 0, "row_schedule: segment rows cell must be 16-byte aligned");
   if (L.dry) return 0;
-  hipLaunchKernelGGL(k_row_schedule, dim3(1), dim3(64), 0, L.stream, cell(L, play), cell(L, lerp), cell(L, segr),
-                     cell(L, rowl), cell(L, flag), (int)rows, (int)frames, (int)seg);
-  DGEN_LAUNCH_CHECK("k_row_schedule");
+  float* seg_status = cell(L, ws);
+  float* row_status = seg_status + nseg;
+  hipLaunchKernelGGL(k_row_segments, dim3((unsigned)((nseg + kSchedThreads - 1) / kSchedThreads)),
+                     dim3(kSchedThreads), 0, L.stream, cell(L, play), cell(L, lerp), cell(L, segr), seg_status,
+                     (int)rows, (int)frames, (int)seg);
+  DGEN_LAUNCH_CHECK("k_row_segments");
+  hipLaunchKernelGGL(k_row_lists, dim3((unsigned)((rows + kSchedThreads - 1) / kSchedThreads)), dim3(kSchedThreads),
+                     0, L.stream, cell(L, segr), seg_status, cell(L, rowl), row_status, (int)rows, (int)nseg);
+  DGEN_LAUNCH_CHECK("k_row_lists");
+  hipLaunchKernelGGL(k_row_flag, dim3(1), dim3(kSchedThreads), 0, L.stream, row_status, cell(L, flag), (int)rows);
+  DGEN_LAUNCH_CHECK("k_row_flag");
   return 0;
 }
 

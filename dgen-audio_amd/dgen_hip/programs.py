@@ -121,7 +121,8 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     p.add(R.K_ACCUM_TABLE, [play, T], [step, 0.0, fmaxi if F > 1 else 1.0, 0.0, hi], flags=R.OP_STATIC,
           label="playhead", dispatch="static singleThreaded")
     p.add(R.K_NOISE_TABLE, [noise, T], flags=R.OP_STATIC, label="noise", dispatch="static singleThreaded")
-    p.add(R.K_ROW_SCHEDULE, [play, lerp, segrows, rowlist, flag, F, T, SEG], flags=R.OP_STATIC,
+    rs_ws = p.alloc("row_schedule_ws", nseg + F)
+    p.add(R.K_ROW_SCHEDULE, [play, lerp, segrows, rowlist, flag, F, T, SEG, rs_ws], flags=R.OP_STATIC,
           label="row_schedule", dispatch="static singleThreaded")
 
     # ---- activations

@@ -167,9 +167,11 @@ enum dgen_hip_kernel {
   /* Row schedule of a sampleRow read (Emit+RowSelection.swift:164-197) from a
    * playhead table, a static table set.  arg: [0]=playhead [1]=lerp ([T][8]:
    * lo, hi, frac, 1-frac, slot(lo), slot(hi), 0, 0) [2]=segment rows
-   * ([nseg][4]) [3]=row entries ([F][16]) [4]=status flag cell [5]=F [6]=T
-   * [7]=segment length.  The flag is 0 when every segment touches <= 4 rows
-   * and every row has <= 16 (segment, slot) entries. */
+   * ([nseg][4], 16-byte aligned) [3]=row entries ([F][16]) [4]=status flag
+   * cell [5]=F [6]=T [7]=segment length [8]=workspace (nseg + F floats).
+   * The flag is 0 when every segment touches <= 4 rows, every row has <= 16
+   * (segment, slot) entries and the playhead is finite; else the largest of
+   * 1, 2, 3 for those three conditions. */
   DGEN_HIP_K_ROW_SCHEDULE = 17,
 
   /* Radix-2 spectral-loss tables for one FFT size (HigherOps.swift:71-99):
