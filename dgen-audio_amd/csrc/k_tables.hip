@@ -16,28 +16,50 @@ namespace dgen {
 // reset 0; output = clip(pre-increment value, lo, hi).  The chain is
 // sequential in fp32.  Where next lies in [mn, mn + span * 0.99) the wrap
 // quotient (next - mn) / span rounds below 1, so k = 0 and w = next exactly:
-// those frames skip the division (the chain's slow part); the others take
-// the full expression.
-__global__ void k_accum_table(float* out, int frames, float step, float mn, float mx, float lo, float hi) {
-  if (blockIdx.x != 0 || threadIdx.x != 0) return;
+// those frames skip the division; the others take the full expression.  One
+// wave runs the (uniform) chain in every lane; lane t % 64 keeps frame t, and
+// each 64 frames leave in one coalesced store (a lone lane storing every
+// frame is bound by its outstanding-store limit).
+__global__ __launch_bounds__(64) void k_accum_table(float* out, int frames, float step, float mn, float mx, float lo,
+                                                    float hi) {
+  const int lane = threadIdx.x;
   float acc = 0.f;
   const float span = mx - mn;
   const float safe = span * 0.99f;
-  for (int t = 0; t < frames; ++t) {
-    const float prev = acc;
-    const float next = acc + step;
-    const float d = next - mn;
-    float w;
-    if (d >= 0.f && d < safe) {
-      w = next;
-    } else {
-      const float k = floorf(d / span);
-      w = next - k * span;
-      if (w >= mx) w = w - span;
+  // a block of 64 adds moves acc by at most 64 step plus 64 roundings of
+  // half an ulp of |acc| <= |mn| + |mx| (+ a margin)
+  const float drift = 65.f * step + 65.f * (fabsf(mx) + fabsf(mn) + fabsf(step)) * 1.2e-7f;
+  for (int t0 = 0; t0 < frames; t0 += 64) {
+    float mine = 0.f;
+    const int n = min(64, frames - t0);
+    if (n == 64 && step >= 0.f && acc - mn >= 0.f && (acc - mn) + drift < safe * 0.999f) {
+      // every frame of the block takes the k = 0 path: branch-free
+#pragma unroll
+      for (int j = 0; j < 64; ++j) {
+        mine = lane == j ? acc : mine;
+        acc = acc + step;
+      }
+      const float p = mine < lo ? lo : mine;
+      out[t0 + lane] = p > hi ? hi : p;
+      continue;
     }
-    acc = w;
-    const float p = prev < lo ? lo : prev;
-    out[t] = p > hi ? hi : p;
+    for (int j = 0; j < n; ++j) {
+      const float prev = acc;
+      const float next = acc + step;
+      const float d = next - mn;
+      float w;
+      if (d >= 0.f && d < safe) {
+        w = next;
+      } else {
+        const float k = floorf(d / span);
+        w = next - k * span;
+        if (w >= mx) w = w - span;
+      }
+      acc = w;
+      const float p = prev < lo ? lo : prev;
+      if (lane == j) mine = p > hi ? hi : p;
+    }
+    if (lane < n) out[t0 + lane] = mine;
   }
 }
 
@@ -190,26 +212,48 @@ __global__ __launch_bounds__(kSchedThreads) void k_row_segments(const float* pla
   seg_status[s] = status;
 }
 
+// The segments' rows pass through LDS in tiles of kSegTile segments, read
+// once per workgroup instead of once per row.
+constexpr int kSegTile = 4096;
+
 __global__ __launch_bounds__(kSchedThreads) void k_row_lists(const float* seg_rows, const float* seg_status,
                                                               float* row_list, float* row_status, int rows,
                                                               int nseg) {
+  __shared__ float4 tile[kSegTile];
   const int f = blockIdx.x * kSchedThreads + threadIdx.x;
-  if (f >= rows) return;
-  float* lst = row_list + (size_t)f * kRowEntries;
   int q = 0;
   float status = 0.f;
-  for (int s = 0; s < nseg; ++s) {
-    const float4 r = *reinterpret_cast<const float4*>(seg_rows + (size_t)s * kSlots);
-    const float rv[kSlots] = {r.x, r.y, r.z, r.w};
-    for (int j = 0; j < kSlots; ++j) {
-      if ((int)rv[j] != f || rv[j] < 0.f) continue;
-      if (q < kRowEntries)
-        lst[q++] = (float)(s * kSlots + j);
-      else
-        status = 2.f;
+  float ent[kRowEntries];
+#pragma unroll
+  for (int k = 0; k < kRowEntries; ++k) ent[k] = -1.f;
+  for (int s0 = 0; s0 < nseg; s0 += kSegTile) {
+    const int n = min(kSegTile, nseg - s0);
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += kSchedThreads)
+      tile[i] = *reinterpret_cast<const float4*>(seg_rows + (size_t)(s0 + i) * kSlots);
+    __syncthreads();
+    if (f >= rows) continue;
+    for (int i = 0; i < n; ++i) {
+      const float4 r = tile[i];
+      const float rv[kSlots] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+      for (int j = 0; j < kSlots; ++j) {
+        if ((int)rv[j] != f || rv[j] < 0.f) continue;
+        if (q < kRowEntries) {
+#pragma unroll
+          for (int k = 0; k < kRowEntries; ++k)
+            if (k == q) ent[k] = (float)((s0 + i) * kSlots + j);
+          ++q;
+        } else {
+          status = 2.f;
+        }
+      }
     }
   }
-  for (int k = q; k < kRowEntries; ++k) lst[k] = -1.f;
+  if (f >= rows) return;
+  float* lst = row_list + (size_t)f * kRowEntries;
+#pragma unroll
+  for (int k = 0; k < kRowEntries; ++k) lst[k] = ent[k];
   // the row's status, and (row 0) the segments' largest
   if (f == 0)
     for (int s = 0; s < nseg; ++s) status = fmaxf(status, seg_status[s]);
