@@ -58,59 +58,68 @@ __device__ __forceinline__ float hw_sqrt(float v) { return __builtin_amdgcn_sqrt
 __device__ __forceinline__ float hw_log(float v) { return __builtin_amdgcn_logf(v) * 0.69314718055994531f; }
 __device__ __forceinline__ float hw_rcp(float v) { return __builtin_amdgcn_rcpf(v); }
 
-// LDS of one size's launch, sized for that size (smaller sizes fit more
-// workgroups per CU).
-// The tile accumulator is stored with 2 pad floats after every 64 samples:
-// a group's windows start N samples apart, so without the pad every window
-// of a wave (1024/N of them for N <= 512) would hit the same LDS banks in the
-// overlap-add; with it window s is shifted by 2s (N/64) banks.  Pairs (even
-// sample index) never straddle a pad and stay 8-byte aligned.
-__device__ __forceinline__ int accp(int i) { return i + 2 * (i >> 6); }
-__host__ __device__ constexpr int acc_floats(int n) { return n + 2 * (n >> 6) + 2; }
+// LDS of the launch (every size runs in it, one after the other).
+// The tile accumulator holds dx of samples [a - kHalo, a + kTile) (whole
+// 64-sample blocks), stored swizzled: sample i lives at
+// i ^ (((i >> 6) & 7) << 3), its 8-float group within its 64-sample block
+// flipped by the block index.  A group's windows start N samples apart, and
+// in the overlap-add each lane of a window adds a pair of samples, a window's
+// lanes covering one aligned run of 2*min(N/16, 32) floats; unswizzled, the
+// windows that share a 16- or 32-lane LDS cycle (N <= 256) would all hit the
+// same banks, swizzled each falls on its own (32 or 64 banks).  Pairs (even
+// sample index) stay together and 8-byte aligned, and the layout needs no
+// padding.
+__device__ __forceinline__ int accp(int i) { return i ^ (((i >> 6) & 7) << 3); }
 
-template <int LOGN>
 struct MssLds {
-  static constexpr int N = 1 << LOGN, M = N / 2;
-  static constexpr int kAccN = kTile + N;  // dx of samples [a - (N-1), a + kTile), + 1 pad (even length)
-  float acc[acc_floats(kAccN)];
-  c2 buf[lds_pad(2048)];           // FFT slots: (4096/N windows) x (N/2), padded
-  c2 aux[lds_pad(2048)];           // second signal's spectrum / gradient spectrum
+  static constexpr int kAccN = kAcc + 1;  // 64-sample blocks
+  float acc[kAccN];
+  c2 buf[2048];                    // FFT slots: (4096/N windows) x (N/2), swizzled
+  c2 aux[2048];                    // second signal's spectrum / gradient spectrum
   float red[kThreads / 64][2];
-  float hann[N];                   // this size's window
-  c2 tw[M];                        // exp(-2 pi i k / N), k < N/2, correctly rounded
+  c2 tw[1024];                     // this size's exp(-2 pi i k / N), k < N/2, correctly rounded
 };
+static_assert(MssLds::kAccN % 64 == 0, "the accumulator swizzle works on whole 64-sample blocks");
 
 // One FFT size: 4 groups of 4096/N windows, windows in a group 4 hops apart.
+// tid: the thread's index, opaque to the optimiser in each call (else every
+// size's values that depend only on it would be hoisted out of the size loop
+// and held in registers together)
 template <int LOGN>
-__device__ __forceinline__ void mss_size(const MssArgs& a, MssLds<LOGN>& L, int si, int b, int tile) {
+__device__ __forceinline__ void mss_size(const MssArgs& a, MssLds& L, int si, int b, int tile, int tid) {
   constexpr int N = 1 << LOGN, M = N / 2, LOGM = LOGN - 1, H = N / 4, P = M / 8, W = kThreads / P;
   static_assert(W * M == 2048, "window slots must fill the FFT buffer");
-  const TableTwiddle tw{L.tw, M};
+  // accumulator index of sample t: t - (a0 - kHalo); for an output pair of a
+  // window with hop frame f: f - a0 + kOff + 2 op[e]
+  constexpr int kOff = kHalo - (N - 1);
   // a window's P threads (and its FFT slots) lie in one wave when P <= 64:
   // its transforms and bins then need only wave-level ordering; the
   // workgroup barrier is kept for the shared accumulator (windows of
   // consecutive groups overlap) and for the cross-wave loss sums (P > 64)
   constexpr bool WL = P <= 64;
-  const int tid = threadIdx.x;
   const int slot = tid / P, j = tid % P;
-  const PadBuf buf{L.buf + slot * lds_pad(M)};
-  const PadBuf spec{L.aux + slot * lds_pad(M)};
+  const SwzBuf buf(L.buf, slot * M);
+  const SwzBuf spec(L.aux, slot * M);
+  const int sj = buf.part(j);  // spec.part(j) too
   const int a0 = tile * kTile;
   const int nwin = (a.T + H - 1) / H;
   const float* xs = a.x + (size_t)b * a.T;
   const float* ts = a.tgt + (size_t)b * a.T;
+  // The size's table cell holds hann[N] | cos[N-1] | sin[N-1] in the
+  // reference's radix-2 layout (stage with half-size h at h-1): the last
+  // stage's row is cos, sin(2 pi k / N), k < N/2.  The window values this
+  // thread multiplies (samples 2n, 2n+1 of the first pass's inputs n and of
+  // the last pass's outputs n) are kept in registers for every group.
+  const float* tab = a.hann[si];
+  float2 hin[8], hout[8];
   {
+    int opl[8];
+    pass_positions<M, pass_radix(LOGM, pass_count(LOGM) - 1), pass_span(LOGM, pass_count(LOGM) - 1)>(j, opl);
     // all of the thread's loads in flight before any LDS write (a loop that
     // stored each load as it arrived waited out one memory latency per
-    // iteration).  The size's table cell holds hann[N] | cos[N-1] | sin[N-1]
-    // in the reference's radix-2 layout (stage with half-size h at h-1): the
-    // last stage's row is cos, sin(2 pi k / N), k < N/2.
-    constexpr int HP = (N + kThreads - 1) / kThreads;
+    // iteration)
     constexpr int TP = (M + kThreads - 1) / kThreads;
-    const float* tab = a.hann[si];
-    float hv[HP], cv[TP], sv[TP];
-#pragma unroll
-    for (int q = 0; q < HP; ++q) hv[q] = tab[min(tid + q * kThreads, N - 1)];
+    float cv[TP], sv[TP];
 #pragma unroll
     for (int q = 0; q < TP; ++q) {
       const int k = min(tid + q * kThreads, M - 1);
@@ -118,29 +127,49 @@ __device__ __forceinline__ void mss_size(const MssArgs& a, MssLds<LOGN>& L, int 
       sv[q] = tab[2 * N - 1 + (M - 1) + k];
     }
 #pragma unroll
-    for (int q = 0; q < HP; ++q)
-      if (tid + q * kThreads < N) L.hann[tid + q * kThreads] = hv[q];
+    for (int e = 0; e < 8; ++e) {
+      const int n = in_pos<M, pass_radix(LOGM, 0)>(j, e);
+      hin[e] = float2{tab[2 * n], tab[2 * n + 1]};
+      hout[e] = float2{tab[2 * opl[e]], tab[2 * opl[e] + 1]};
+    }
 #pragma unroll
     for (int q = 0; q < TP; ++q)
       if (tid + q * kThreads < M) L.tw[tid + q * kThreads] = c2{cv[q], -sv[q]};
   }
   lds_barrier();
+  const RegTwiddle<LOGM> tw(TableTwiddle{L.tw, M}, j);
   // window samples of group g for this thread: element e of the first pass
   // needs samples s0 + 2n and s0 + 2n + 1, n = in_pos(j, e)
   float pt[16], px[16];
+  // (a window inside [0, T) needs no per-sample checks: its loads are one
+  // base address plus constant offsets)
   auto fetch = [&](int g) {
     const int w = a0 / H + g + 4 * slot;
     const bool live = w < nwin && w * H < a0 + kTile;
     const int s0 = w * H - N + 1;
+    if (live && s0 >= 0 && s0 + N <= a.T) {
+      const float* tb = ts + s0 + 2 * j;
+      const float* xb = xs + s0 + 2 * j;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int n = in_pos<M, pass_radix(LOGM, 0)>(j, e);
-      const int t0 = s0 + 2 * n, t1 = t0 + 1;
-      const bool i0 = live && t0 >= 0 && t0 < a.T, i1 = live && t1 >= 0 && t1 < a.T;
-      pt[2 * e] = i0 ? ts[t0] : 0.0f;
-      pt[2 * e + 1] = i1 ? ts[t1] : 0.0f;
-      px[2 * e] = i0 ? xs[t0] : 0.0f;
-      px[2 * e + 1] = i1 ? xs[t1] : 0.0f;
+      for (int e = 0; e < 8; ++e) {
+        constexpr int R0 = pass_radix(LOGM, 0);
+        const int o = 2 * in_off<M, R0>(e);
+        pt[2 * e] = tb[o];
+        pt[2 * e + 1] = tb[o + 1];
+        px[2 * e] = xb[o];
+        px[2 * e + 1] = xb[o + 1];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int n = in_pos<M, pass_radix(LOGM, 0)>(j, e);
+        const int t0 = s0 + 2 * n, t1 = t0 + 1;
+        const bool i0 = live && t0 >= 0 && t0 < a.T, i1 = live && t1 >= 0 && t1 < a.T;
+        pt[2 * e] = i0 ? ts[t0] : 0.0f;
+        pt[2 * e + 1] = i1 ? ts[t1] : 0.0f;
+        px[2 * e] = i0 ? xs[t0] : 0.0f;
+        px[2 * e + 1] = i1 ? xs[t1] : 0.0f;
+      }
     }
   };
   fetch(0);
@@ -158,17 +187,13 @@ __device__ __forceinline__ void mss_size(const MssArgs& a, MssLds<LOGN>& L, int 
       c2 vt[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int n = in_pos<M, pass_radix(LOGM, 0)>(j, e);
-        const float2 h = *reinterpret_cast<const float2*>(&L.hann[2 * n]);
+        const float2 h = hin[e];
         vt[e] = c2{pt[2 * e] * h.x, pt[2 * e + 1] * h.y};
         v[e] = c2{px[2 * e] * h.x, px[2 * e + 1] * h.y};
       }
       fft2<LOGM, false, WL>(spec, buf, j, vt, v, op, tw);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        spec[op[e]] = vt[e];
-        buf[op[e]] = v[e];
-      }
+      fft_store<LOGM>(spec, j, vt);
+      fft_store<LOGM>(buf, j, v);
       lds_sync<WL>();
     }
     if (g + 1 < 4) fetch(g + 1);  // overlaps the bins and the inverse transform
@@ -231,10 +256,11 @@ __device__ __forceinline__ void mss_size(const MssArgs& a, MssLds<LOGN>& L, int 
       c2 zxa[NB], zxb[NB], zta[NB], ztb[NB];
 #pragma unroll
       for (int i = 0; i < NB; ++i) {
-        const int k = min(j + i * P, M / 2), km = (M - k) & (M - 1);  // clamped: pairs past M/2 are skipped below
-        zxa[i] = buf[k];
+        // k = j + i*P < M for every i (pairs past M/2 are read and skipped)
+        const int km = (M - j - i * P) & (M - 1);
+        zxa[i] = buf.at(sj, i * P);
         zxb[i] = buf[km];
-        zta[i] = spec[k];
+        zta[i] = spec.at(sj, i * P);
         ztb[i] = spec[km];
       }
 #pragma unroll
@@ -278,8 +304,7 @@ __device__ __forceinline__ void mss_size(const MssArgs& a, MssLds<LOGN>& L, int 
       wl[1] = sg;
     }
     // ---- real-output inverse transform and windowed overlap-add
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = spec[in_pos<M, pass_radix(LOGM, 0)>(j, e)];
+    fft_load<LOGM>(spec, j, v);
     fft<LOGM, true, WL>(buf, j, v, op, tw);
     // each accumulator element of a group belongs to one thread (the group's
     // windows are disjoint), so all of the thread's reads are issued before
@@ -288,8 +313,22 @@ __device__ __forceinline__ void mss_size(const MssArgs& a, MssLds<LOGN>& L, int 
     // pair is one 8-byte LDS access.  Pairs outside the tile's range read a
     // clamped element and are not written; a pair with one sample outside
     // [0, T) writes only the other.
-    {
-      constexpr int kAccN = MssLds<LOGN>::kAccN;
+    if (live && s0 >= 0 && s0 + N <= a.T) {
+      // the whole window inside [0, T): every pair is written
+      float2 ac[8];
+      int ai[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        ai[e] = accp(f - a0 + kOff + 2 * op[e]);
+        ac[e] = *reinterpret_cast<const float2*>(&L.acc[ai[e]]);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float2 h = hout[e];
+        *reinterpret_cast<float2*>(&L.acc[ai[e]]) = float2{ac[e].x + v[e].x * h.x, ac[e].y + v[e].y * h.y};
+      }
+    } else {
+      constexpr int kAccN = MssLds::kAccN;
       float2 ac[8];
       int ai[8];
       bool a0w[8], a1w[8];
@@ -298,12 +337,12 @@ __device__ __forceinline__ void mss_size(const MssArgs& a, MssLds<LOGN>& L, int 
         const int t = s0 + 2 * op[e];
         a0w[e] = live && t >= 0 && t < a.T;
         a1w[e] = live && t + 1 >= 0 && t + 1 < a.T;
-        ai[e] = accp(min(max(t - (a0 - (N - 1)), 0), kAccN - 2));
+        ai[e] = accp(min(max(t - (a0 - kHalo), 0), kAccN - 2));
         ac[e] = *reinterpret_cast<const float2*>(&L.acc[ai[e]]);
       }
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float2 h = *reinterpret_cast<const float2*>(&L.hann[2 * op[e]]);
+        const float2 h = hout[e];
         const float2 r = {ac[e].x + v[e].x * h.x, ac[e].y + v[e].y * h.y};
         if (a0w[e] && a1w[e]) *reinterpret_cast<float2*>(&L.acc[ai[e]]) = r;
         else if (a0w[e]) L.acc[ai[e]] = r.x;
@@ -315,39 +354,29 @@ __device__ __forceinline__ void mss_size(const MssArgs& a, MssLds<LOGN>& L, int 
   }
 }
 
-// One launch per FFT size (each size gets its own register allocation); the
-// tile accumulator starts at zero for the first size and is carried in the
-// tile partials between launches, which run in the op's size order.
-template <int LOGN>
-__global__ __launch_bounds__(kThreads) void k_mss(MssArgs a, int si, int first) {
+// All sizes in one launch, in the op's size order: the tile accumulator
+// stays in LDS from the first size to the last and is written to the tile
+// partials once.
+__global__ __launch_bounds__(kThreads) void k_mss(MssArgs a) {
   extern __shared__ float4 smem4[];
-  MssLds<LOGN>& L = *reinterpret_cast<MssLds<LOGN>*>(smem4);
-  constexpr int N = 1 << LOGN;
-  constexpr int kSpan = kTile + N - 1;  // samples [a - (N-1), a + kTile) of the tile row
-  constexpr int kOff = kHalo - (N - 1);  // their place in the row of kAcc
+  MssLds& L = *reinterpret_cast<MssLds*>(smem4);
   const int tile = blockIdx.x, b = blockIdx.y;
-  float* part = a.part + ((size_t)b * a.ntiles + tile) * kAcc;
-  {
-    // the tile partials: every load in flight before the LDS writes
-    constexpr int AP = (kSpan + kThreads - 1) / kThreads;
-    float av[AP];
-    if (first) {
-#pragma unroll
-      for (int q = 0; q < AP; ++q) av[q] = 0.f;
-    } else {
-#pragma unroll
-      for (int q = 0; q < AP; ++q) av[q] = part[kOff + min((int)threadIdx.x + q * kThreads, kSpan - 1)];
-    }
-#pragma unroll
-    for (int q = 0; q < AP; ++q)
-      if ((int)threadIdx.x + q * kThreads < kSpan) L.acc[accp(threadIdx.x + q * kThreads)] = av[q];
-  }
+  for (int i = threadIdx.x; i < MssLds::kAccN; i += kThreads) L.acc[i] = 0.f;
   lds_barrier();
-  mss_size<LOGN>(a, L, si, b, tile);
-  for (int i = threadIdx.x; i < kSpan; i += kThreads) part[kOff + i] = L.acc[accp(i)];
-  // the first size also clears the row's part left of its own halo
-  if (first)
-    for (int i = threadIdx.x; i < kOff; i += kThreads) part[i] = 0.f;
+  for (int s = 0; s < a.nsizes; ++s) {
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    switch (a.logn[s]) {
+      case 6: mss_size<6>(a, L, s, b, tile, tid); break;
+      case 7: mss_size<7>(a, L, s, b, tile, tid); break;
+      case 8: mss_size<8>(a, L, s, b, tile, tid); break;
+      case 9: mss_size<9>(a, L, s, b, tile, tid); break;
+      case 10: mss_size<10>(a, L, s, b, tile, tid); break;
+      default: mss_size<11>(a, L, s, b, tile, tid); break;
+    }
+  }
+  float* part = a.part + ((size_t)b * a.ntiles + tile) * kAcc;
+  for (int i = threadIdx.x; i < kAcc; i += kThreads) part[i] = L.acc[accp(i)];
 }
 
 int launch_spectral_loss(const Launch& L, const dgen_hip_op& op) {
@@ -388,18 +417,8 @@ int launch_spectral_loss(const Launch& L, const dgen_hip_op& op) {
   a.gl = op.farg[0];
   a.gg = op.farg[1];
   const dim3 grid((unsigned)ntiles, (unsigned)B);
-  for (int s = 0; s < ns; ++s) {
-    const int first = s == 0;
-    switch (a.logn[s]) {
-      case 6: hipLaunchKernelGGL(k_mss<6>, grid, dim3(kThreads), sizeof(MssLds<6>), L.stream, a, s, first); break;
-      case 7: hipLaunchKernelGGL(k_mss<7>, grid, dim3(kThreads), sizeof(MssLds<7>), L.stream, a, s, first); break;
-      case 8: hipLaunchKernelGGL(k_mss<8>, grid, dim3(kThreads), sizeof(MssLds<8>), L.stream, a, s, first); break;
-      case 9: hipLaunchKernelGGL(k_mss<9>, grid, dim3(kThreads), sizeof(MssLds<9>), L.stream, a, s, first); break;
-      case 10: hipLaunchKernelGGL(k_mss<10>, grid, dim3(kThreads), sizeof(MssLds<10>), L.stream, a, s, first); break;
-      default: hipLaunchKernelGGL(k_mss<11>, grid, dim3(kThreads), sizeof(MssLds<11>), L.stream, a, s, first); break;
-    }
-    DGEN_LAUNCH_CHECK("k_mss");
-  }
+  hipLaunchKernelGGL(k_mss, grid, dim3(kThreads), sizeof(MssLds), L.stream, a);
+  DGEN_LAUNCH_CHECK("k_mss");
   return 0;
 }
 

@@ -51,7 +51,7 @@ struct StftArgs {
 
 // Real N-point spectrum bins k and M-k (k = 0: bins 0 and M) from the
 // N/2-point complex transform Z of the even/odd-packed signal.
-__device__ __forceinline__ void split_bins(PadBuf Z, int k, int M, float invN, c2& Xk, c2& Xm) {
+__device__ __forceinline__ void split_bins(const SwzBuf& Z, int k, int M, float invN, c2& Xk, c2& Xm) {
   const int km = (M - k) & (M - 1);
   const c2 zk = Z[k], zm = Z[km];
   const c2 e = {0.5f * (zk.x + zm.x), 0.5f * (zk.y - zm.y)};
@@ -100,8 +100,7 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 
 struct FwdLds {
   float acc[kTile];
-  c2 buf[lds_pad(2048)];
-  float win[2048];
+  c2 buf[2048];
   float gain[1025];
   float red[kThreads / 64];
 };
@@ -119,19 +118,27 @@ __global__ __launch_bounds__(kThreads) void k_stft_fwd(StftArgs a) {
   const int s = blockIdx.y, tile = blockIdx.x, H = a.H;
   const int a0 = tile * kTile, a1 = min(a.T, a0 + kTile);
   const float* xs = a.x + (size_t)s * a.T;
-  stage<N>(L.win, a.win, tid);
   stage<M + 1>(L.gain, a.gains, tid);
   for (int i = tid; i < kTile; i += kThreads) L.acc[i] = 0.0f;
   // windows h = w*H with outputs [h, h+N) meeting [a0, a1)
   const int w_lo = a0 - N < 0 ? 0 : (a0 - N) / H + 1;
   const int w_hi = (a1 - 1) / H;
   const int nw = w_hi - w_lo + 1;
-  const PadBuf buf{L.buf + slot * lds_pad(M)};
-  // after the inverse transform a slot's region holds its N real outputs,
-  // unpadded: slot q's at zs + q * 2 * lds_pad(M)
+  const SwzBuf buf(L.buf, slot * M);
+  const int sj = buf.part(j);
+  // after the inverse transform a slot's region holds its N real outputs in
+  // order: slot q's at zs + q * 2 * M
   const float* zs = reinterpret_cast<const float*>(L.buf);
-  constexpr int kZStride = 2 * lds_pad(M);
+  constexpr int kZStride = 2 * M;
   constexpr float invN = 1.0f / (float)N;
+  // the window values this thread multiplies (samples 2n, 2n+1 of its first
+  // pass inputs n), in registers for every round
+  float2 hw[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int n = in_pos<M, pass_radix(LOGM, 0)>(j, e);
+    hw[e] = float2{a.win[2 * n], a.win[2 * n + 1]};
+  }
   // this thread's window samples of round r (element e of the first pass
   // needs samples 2n and 2n+1 of the window, n = in_pos(j, e)); the next
   // round's are loaded while this one is transformed and gathered
@@ -154,14 +161,10 @@ __global__ __launch_bounds__(kThreads) void k_stft_fwd(StftArgs a) {
     c2 v[8];
     int op[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int n = in_pos<M, pass_radix(LOGM, 0)>(j, e);
-      v[e] = c2{px[2 * e] * L.win[2 * n], px[2 * e + 1] * L.win[2 * n + 1]};
-    }
+    for (int e = 0; e < 8; ++e) v[e] = c2{px[2 * e] * hw[e].x, px[2 * e + 1] * hw[e].y};
     fft<LOGM, false, WL>(buf, j, v, op);
     if (r0 + W < nw) fetch(r0 + W);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) buf[op[e]] = v[e];
+    fft_store<LOGM>(buf, j, v);
     lds_sync<WL>();
     // gains on the one-sided spectrum, then the Hermitian inverse
     // pre-processing: z'_k = (G_k + conj G_{M-k}) + i (G_k - conj G_{M-k}) W_N^{-k}
@@ -170,9 +173,9 @@ __global__ __launch_bounds__(kThreads) void k_stft_fwd(StftArgs a) {
     c2 zk[U], zm[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int k = min(j + u * P, M / 2);  // clamped: pairs past M/2 are skipped below
-      zk[u] = buf[k];
-      zm[u] = buf[(M - k) & (M - 1)];
+      // k = j + u*P < M for every u (pairs past M/2 are read and skipped)
+      zk[u] = buf.at(sj, u * P);
+      zm[u] = buf[(M - j - u * P) & (M - 1)];
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -196,17 +199,13 @@ __global__ __launch_bounds__(kThreads) void k_stft_fwd(StftArgs a) {
       }
     }
     lds_sync<WL>();
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = buf[in_pos<M, pass_radix(LOGM, 0)>(j, e)];
+    fft_load<LOGM>(buf, j, v);
     lds_sync<WL>();
     fft<LOGM, true, WL>(buf, j, v, op);
     // complex output q holds samples 2q, 2q+1 (unnormalised): scale by 1/N
-    float* zb = reinterpret_cast<float*>(buf.p);
+    float* zb = buf.raw();
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      zb[2 * op[e]] = v[e].x * invN;
-      zb[2 * op[e] + 1] = v[e].y * invN;
-    }
+    for (int e = 0; e < 8; ++e) *reinterpret_cast<float2*>(zb + 2 * op[e]) = float2{v[e].x * invN, v[e].y * invN};
     lds_barrier();
     // gather this round's windows into the tile, position by position
     const int wb = w_lo + r0, hb = wb * H;
@@ -283,9 +282,8 @@ __global__ __launch_bounds__(kThreads) void k_stft_fwd(StftArgs a) {
 }
 
 struct BwdLds {
-  c2 buf[lds_pad(2048)];
-  c2 aux[lds_pad(2048)];
-  float win[2048];
+  c2 buf[2048];
+  c2 aux[2048];
 };
 
 template <int LOGN>
@@ -301,9 +299,15 @@ __global__ __launch_bounds__(kThreads) void k_stft_bwd(StftArgs a) {
   const int wb = blk * kRounds * W, we = min(nwin, wb + kRounds * W);
   const float* xs = a.x + (size_t)s * a.T;
   const float* gs = a.dyin + (size_t)s * a.T;
-  stage<N>(L.win, a.win, tid);
-  const PadBuf buf{L.buf + slot * lds_pad(M)};
-  const PadBuf spec{L.aux + slot * lds_pad(M)};
+  const SwzBuf buf(L.buf, slot * M);
+  const SwzBuf spec(L.aux, slot * M);
+  // the window values this thread multiplies, in registers for every round
+  float2 hw[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int n = in_pos<M, pass_radix(LOGM, 0)>(j, e);
+    hw[e] = float2{a.win[2 * n], a.win[2 * n + 1]};
+  }
   constexpr float invN = 1.0f / (float)N;
   float acc_k[U], acc_m[U];
 #pragma unroll
@@ -324,16 +328,13 @@ __global__ __launch_bounds__(kThreads) void k_stft_bwd(StftArgs a) {
         const int t0 = h - N + 1 + 2 * n;
         const float x0 = live && t0 >= 0 ? xs[t0] : 0.0f;
         const float x1 = live && t0 + 1 >= 0 ? xs[t0 + 1] : 0.0f;
-        vx[e] = c2{x0 * L.win[2 * n], x1 * L.win[2 * n + 1]};
+        vx[e] = c2{x0 * hw[e].x, x1 * hw[e].y};
         const int g0 = h + 2 * n;
         vg[e] = c2{live && g0 < a.T ? gs[g0] : 0.0f, live && g0 + 1 < a.T ? gs[g0 + 1] : 0.0f};
       }
       fft2<LOGM, false, WL>(spec, buf, j, vx, vg, op);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        spec[op[e]] = vx[e];
-        buf[op[e]] = vg[e];
-      }
+      fft_store<LOGM>(spec, j, vx);
+      fft_store<LOGM>(buf, j, vg);
       lds_sync<WL>();
     }
 #pragma unroll
