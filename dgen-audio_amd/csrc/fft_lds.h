@@ -31,7 +31,10 @@
 
 namespace dgen {
 
-struct c2 {
+// 8-byte aligned so that every access is one ds_read_b64 / ds_write_b64 (at
+// 4-byte alignment each splits into two 4-byte halves, each half strided 8
+// bytes across the lanes: two LDS passes, each 2-way bank conflicted)
+struct alignas(8) c2 {
   float x, y;
 };
 
