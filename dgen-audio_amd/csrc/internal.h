@@ -113,6 +113,7 @@ int launch_accum_table(const Launch&, const dgen_hip_op&);
 int launch_dense_small(const Launch&, const dgen_hip_op&);
 int launch_dense_small_wgrad(const Launch&, const dgen_hip_op&);
 int launch_gemm(const Launch&, const dgen_hip_op&);
+int launch_split_bf16(const Launch&, const dgen_hip_op&);
 int launch_colsum(const Launch&, const dgen_hip_op&);
 int launch_heads_fwd(const Launch&, const dgen_hip_op&);
 int launch_heads_bwd(const Launch&, const dgen_hip_op&);

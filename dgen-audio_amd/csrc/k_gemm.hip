@@ -64,6 +64,134 @@ __device__ __forceinline__ float apply_epi(int epi, float acc, int row, int col,
   }
 }
 
+// The epilogue of a 128x128 tile: the MFMA accumulators (four 32x32 blocks
+// per wave) to C (bias, tanh, tanh gradient, column partials) or to the
+// split-K workspace.  scr0 / scr1: two LDS areas of at least 1280 and 512
+// floats that no wave reads any more (the operand tiles after the k-loop's
+// last barrier).
+__device__ __forceinline__ void gemm_epilogue(floatx16 (&acc)[2][2], float* scr0, float* scr1, int m0, int n0, int by,
+                                              int bz, int M, int N, float* __restrict__ C, int ldc, int epi,
+                                              const float* __restrict__ bias, const float* __restrict__ aux, int ldaux,
+                                              float* __restrict__ ws, float* __restrict__ cs,
+                                              const float* __restrict__ cw, int ncw) {
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int h = lane >> 5, r = lane & 31;
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+  // Accumulator layout of a 32x32 MFMA block: register v of lane l holds
+  // row 8*(v/4) + 4*(l/32) + v%4, column l%32.
+  if (!ws && epi == EPI_TANH_GRAD) {
+    // per 32x32 block: issue its 16 loads of the tanh outputs, then use them
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+      for (int tj = 0; tj < 2; ++tj) {
+        const int col = n0 + wn + tj * 32 + r;
+        float hv[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int row = m0 + wm + ti * 32 + (v >> 2) * 8 + h * 4 + (v & 3);
+          hv[v] = (row < M && col < N) ? aux[(size_t)row * ldaux + col] : 0.f;
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int row = m0 + wm + ti * 32 + (v >> 2) * 8 + h * 4 + (v & 3);
+          acc[ti][tj][v] *= 1.f - hv[v] * hv[v];
+          if (row < M && col < N) C[(size_t)row * ldc + col] = acc[ti][tj][v];
+        }
+      }
+    if (cs) {
+      // column sums of the 128-row tile just stored, weighted by the ncw
+      // columns of cw ([M][ncw]) and plain: each lane sums its 32 rows of
+      // column wn + tj*32 + r, lanes r and r+32 (the other four rows of
+      // every group of eight) are added, then the two waves sharing the
+      // columns, top half first; the tile writes rows q < ncw (weighted by
+      // cw[.][q]) and ncw (plain) of its partials.  The k-loop's last
+      // barrier has retired every read of the operand tiles, so the
+      // weights are staged in one of them and the sums meet in the other.
+      float* red = scr0;
+      if (ncw) {
+        // [q][BM] weights of the tile's rows, zero past M (where the
+        // accumulators are zero too: those A rows were loaded as zeros)
+        float* wt = scr1;
+        for (int i = tid; i < ncw * BM; i += 256) {
+          const int rr = i / ncw, q = i - rr * ncw;
+          wt[q * BM + rr] = m0 + rr < M ? cw[(size_t)m0 * ncw + i] : 0.f;
+        }
+        __syncthreads();
+#pragma unroll 1
+        for (int q = 0; q < ncw; ++q) {
+          const float* wq = wt + q * BM + wm + h * 4;
+          float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+          for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              // rows 8g + e (e < 4) of this lane's 32-row block
+              const float4 w = *reinterpret_cast<const float4*>(wq + ti * 32 + g * 8);
+              s0 = fmaf(w.x, acc[ti][0][g * 4 + 0], s0);
+              s1 = fmaf(w.x, acc[ti][1][g * 4 + 0], s1);
+              s0 = fmaf(w.y, acc[ti][0][g * 4 + 1], s0);
+              s1 = fmaf(w.y, acc[ti][1][g * 4 + 1], s1);
+              s0 = fmaf(w.z, acc[ti][0][g * 4 + 2], s0);
+              s1 = fmaf(w.z, acc[ti][1][g * 4 + 2], s1);
+              s0 = fmaf(w.w, acc[ti][0][g * 4 + 3], s0);
+              s1 = fmaf(w.w, acc[ti][1][g * 4 + 3], s1);
+            }
+          s0 += __shfl_xor(s0, 32, 64);
+          s1 += __shfl_xor(s1, 32, 64);
+          red[(q * 4 + wave) * 64 + lane] = lane < 32 ? s0 : s1;
+        }
+      }
+      float s[2];
+#pragma unroll
+      for (int tj = 0; tj < 2; ++tj) {
+        s[tj] = 0.f;
+#pragma unroll
+        for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int row = m0 + wm + ti * 32 + (v >> 2) * 8 + h * 4 + (v & 3);
+            s[tj] += row < M ? acc[ti][tj][v] : 0.f;
+          }
+        s[tj] += __shfl_xor(s[tj], 32, 64);
+      }
+      red[(ncw * 4 + wave) * 64 + lane] = lane < 32 ? s[0] : s[1];
+      __syncthreads();
+      if (wave < 2) {
+        const int col = n0 + wn + lane;
+        if (col < N)
+          for (int q = 0; q <= ncw; ++q)
+            cs[((size_t)by * (ncw + 1) + q) * N + col] = red[(q * 4 + wave) * 64 + lane] + red[(q * 4 + wave + 2) * 64 + lane];
+      }
+    }
+    return;
+  }
+  // one uniform branch per epilogue kind, then a straight store loop
+  auto store_all = [&](auto f) {
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+      for (int tj = 0; tj < 2; ++tj) {
+        const int col = n0 + wn + tj * 32 + r;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int row = m0 + wm + ti * 32 + (v >> 2) * 8 + h * 4 + (v & 3);
+          if (row < M && col < N) f(row, col, acc[ti][tj][v]);
+        }
+      }
+  };
+  if (ws) {
+    store_all([&](int row, int col, float a) { ws[((size_t)bz * M + row) * N + col] = a; });
+  } else if (epi == EPI_BIAS_TANH) {
+    store_all([&](int row, int col, float a) { C[(size_t)row * ldc + col] = fast_tanh(a + bias[col]); });
+  } else if (epi == EPI_BIAS) {
+    store_all([&](int row, int col, float a) { C[(size_t)row * ldc + col] = a + bias[col]; });
+  } else {
+    store_all([&](int row, int col, float a) { C[(size_t)row * ldc + col] = a; });
+  }
+}
+
 // A_KMAJ: A stored [K][M] (else [M][K]); B_NK: B stored [N][K] (else [K][N]).
 // VA / VB: the operand's rows are 16-byte aligned, so its tiles load as
 // float4 (the heads' 127-column weights are not, their activations are).
@@ -252,118 +380,238 @@ __global__ __launch_bounds__(256, BK == 16 ? 4 : 2) void k_gemm(const float* __r
     buf ^= 1;
   }
 
-  // Accumulator layout of a 32x32 MFMA block: register v of lane l holds
-  // row 8*(v/4) + 4*(l/32) + v%4, column l%32.
-  if (!ws && epi == EPI_TANH_GRAD) {
-    // per 32x32 block: issue its 16 loads of the tanh outputs, then use them
+  gemm_epilogue(acc, As_[0], As_[1], m0, n0, by, bz, M, N, C, ldc, epi, bias, aux, ldaux, ws, cs, cw, ncw);
+}
+
+// ---------------------------------------------------------------------------
+// Split-bf16 GEMM (the same tiles, epilogues and operand layouts as k_gemm).
+//
+// Each fp32 operand value x is split exactly into three bfloat16 parts,
+// x = h + m + l (h = bf16(x), m = bf16(x - h), l = bf16(x - h - m); each
+// part carries the next 8 significant bits, so the three hold all 24), and
+// a product is the sum of the six partial products whose significance
+// reaches 2^-16 of h*h: l*h + h*l + m*m + m*h + h*m + h*h (smallest first),
+// each exact in the fp32 accumulator of v_mfma_f32_32x32x16_bf16 (Henry,
+// Tang and Heinecke, "Leveraging the bfloat16 Artificial Intelligence
+// Datatype For Higher-Precision Computations", ARITH 2019: the "bf16x6"
+// scheme).  The dropped terms (m*l, l*m, l*l) are below 2^-23 of |h*h|, so
+// the result is as accurate as an fp32 product accumulated in fp32: against
+// fp64, measured on this hardware, relative L2 errors 3.6e-8 / 3.4e-7 /
+// 3.2e-6 at K = 16 / 512 / 32000 where the fp32 MFMA (32x32x2) gives
+// 7.3e-8 / 3.9e-7 / 3.2e-6.  Six bf16 MFMAs of 32x32x16 take 192 cycles
+// where the eight fp32 32x32x2 MFMAs of the same 32x32x16 product take 512.
+// (Values beyond the largest bfloat16, |x| > 3.39e38, would split to
+// infinities; inputs are never near.)
+//
+// LDS holds per k-step (BK = 16) and operand the three planes as
+// [plane][k-half][128 rows][8 k-values] (16 bytes per row and half): a
+// thread stages 8 k-values of one row (one 16-byte write per plane) and a
+// wave's MFMA operand read (32 rows x 2 halves of 16 bytes) is contiguous.
+// Double buffered: 48 KB per workgroup, three workgroups per CU.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ void split8(const float (&x)[8], uint4& ph, uint4& pm, uint4& pl) {
+  bf16x8 h, m, l;
 #pragma unroll
-    for (int ti = 0; ti < 2; ++ti)
+  for (int i = 0; i < 8; ++i) {
+    const __bf16 a = (__bf16)x[i];
+    const float r = x[i] - (float)a;
+    const __bf16 b = (__bf16)r;
+    h[i] = a;
+    m[i] = b;
+    l[i] = (__bf16)(r - (float)b);
+  }
+  ph = __builtin_bit_cast(uint4, h);
+  pm = __builtin_bit_cast(uint4, m);
+  pl = __builtin_bit_cast(uint4, l);
+}
+
+// BPL: B arrives already split (DGEN_HIP_K_SPLIT_BF16 planes in bpl, K8
+// groups of 8 k-values per column): its tile loads are one 16-byte load per
+// plane and nothing is split in the tile (B_NK and VB are then unused).
+template <bool A_KMAJ, bool B_NK, bool VA, bool VB, bool FULL, bool BPL>
+__global__ __launch_bounds__(256, 3) void k_gemm_x6(const float* __restrict__ A, const float* __restrict__ B,
+                                                    float* __restrict__ C, int M, int N, int K, int lda, int ldb,
+                                                    int ldc, int epi, const float* __restrict__ bias,
+                                                    const float* __restrict__ aux, int ldaux, int kchunk,
+                                                    float* __restrict__ ws, float* __restrict__ cs,
+                                                    const float* __restrict__ cw, int ncw,
+                                                    const uint4* __restrict__ bpl, int K8) {
+  constexpr int BK = 16;
+  // [buffer][operand][plane][k-half][row]: 8 bf16 per entry
+  __shared__ uint4 Xs[2][2][3][2][BM];
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int h = lane >> 5, r = lane & 31;
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+  int bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
+  {
+    // XCD-contiguous tile order, as in k_gemm
+    const int tiles = gridDim.x * gridDim.y, total = tiles * gridDim.z;
+    if (total % 8 == 0) {
+      const int hw = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+      const int lg = (hw % 8) * (total / 8) + hw / 8;
+      bz = lg / tiles;
+      bx = (lg % tiles) % gridDim.x;
+      by = (lg % tiles) / gridDim.x;
+    }
+  }
+  const int m0 = by * BM, n0 = bx * BN;
+  const int kbeg = bz * kchunk;
+  const int kend = min(K, kbeg + kchunk);
+
+  floatx16 acc[2][2];
 #pragma unroll
-      for (int tj = 0; tj < 2; ++tj) {
-        const int col = n0 + wn + tj * 32 + r;
-        float hv[16];
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int row = m0 + wm + ti * 32 + (v >> 2) * 8 + h * 4 + (v & 3);
-          hv[v] = (row < M && col < N) ? aux[(size_t)row * ldaux + col] : 0.f;
-        }
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int row = m0 + wm + ti * 32 + (v >> 2) * 8 + h * 4 + (v & 3);
-          acc[ti][tj][v] *= 1.f - hv[v] * hv[v];
-          if (row < M && col < N) C[(size_t)row * ldc + col] = acc[ti][tj][v];
-        }
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  // staging: thread (si, sh) holds k-values 8*sh .. 8*sh+7 of row si of
+  // each operand tile (A row m0+si, B column n0+si)
+  const int si = tid & (BM - 1), sh = tid >> 7;
+  float xa[8], xb[BPL ? 1 : 8];
+  uint4 pb[BPL ? 3 : 1];
+  auto load_tile = [&](int k0) {
+    const int kk = k0 + 8 * sh;
+    if (!A_KMAJ) {  // [M][K]: 8 consecutive values of one row
+      const int row = m0 + si;
+      const float* p = A + (size_t)row * lda + kk;
+      if (FULL || (VA && row < M && kk + 8 <= kend)) {
+        const float4 u = *reinterpret_cast<const float4*>(p), w = *reinterpret_cast<const float4*>(p + 4);
+        xa[0] = u.x; xa[1] = u.y; xa[2] = u.z; xa[3] = u.w;
+        xa[4] = w.x; xa[5] = w.y; xa[6] = w.z; xa[7] = w.w;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xa[j] = (row < M && kk + j < kend) ? p[j] : 0.f;
       }
-    if (cs) {
-      // column sums of the 128-row tile just stored, weighted by the ncw
-      // columns of cw ([M][ncw]) and plain: each lane sums its 32 rows of
-      // column wn + tj*32 + r, lanes r and r+32 (the other four rows of
-      // every group of eight) are added, then the two waves sharing the
-      // columns, top half first; the tile writes rows q < ncw (weighted by
-      // cw[.][q]) and ncw (plain) of its partials.  The k-loop's last
-      // barrier has retired every read of the operand tiles, so the
-      // weights are staged in one of them and the sums meet in the other.
-      float* red = As_[0];
-      if (ncw) {
-        // [q][BM] weights of the tile's rows, zero past M (where the
-        // accumulators are zero too: those A rows were loaded as zeros)
-        float* wt = As_[1];
-        for (int i = tid; i < ncw * BM; i += 256) {
-          const int rr = i / ncw, q = i - rr * ncw;
-          wt[q * BM + rr] = m0 + rr < M ? cw[(size_t)m0 * ncw + i] : 0.f;
-        }
-        __syncthreads();
-#pragma unroll 1
-        for (int q = 0; q < ncw; ++q) {
-          const float* wq = wt + q * BM + wm + h * 4;
-          float s0 = 0.f, s1 = 0.f;
+    } else {  // [K][M]: one value in each of 8 rows (coalesced across the wave)
+      const int col = m0 + si;
 #pragma unroll
-          for (int ti = 0; ti < 2; ++ti)
+      for (int j = 0; j < 8; ++j)
+        xa[j] = (FULL || (col < M && kk + j < kend)) ? A[(size_t)(kk + j) * lda + col] : 0.f;
+    }
+    if constexpr (BPL) {  // planes: 16 bytes per plane (zero past K8 and N)
+      const int kg = (k0 >> 3) + sh, col = n0 + si;
+      const bool ok = FULL || (col < N && kg < K8);
+      const size_t plane = (size_t)K8 * N, at = (size_t)kg * N + col;
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-              // rows 8g + e (e < 4) of this lane's 32-row block
-              const float4 w = *reinterpret_cast<const float4*>(wq + ti * 32 + g * 8);
-              s0 = fmaf(w.x, acc[ti][0][g * 4 + 0], s0);
-              s1 = fmaf(w.x, acc[ti][1][g * 4 + 0], s1);
-              s0 = fmaf(w.y, acc[ti][0][g * 4 + 1], s0);
-              s1 = fmaf(w.y, acc[ti][1][g * 4 + 1], s1);
-              s0 = fmaf(w.z, acc[ti][0][g * 4 + 2], s0);
-              s1 = fmaf(w.z, acc[ti][1][g * 4 + 2], s1);
-              s0 = fmaf(w.w, acc[ti][0][g * 4 + 3], s0);
-              s1 = fmaf(w.w, acc[ti][1][g * 4 + 3], s1);
-            }
-          s0 += __shfl_xor(s0, 32, 64);
-          s1 += __shfl_xor(s1, 32, 64);
-          red[(q * 4 + wave) * 64 + lane] = lane < 32 ? s0 : s1;
-        }
-      }
-      float s[2];
+      for (int q = 0; q < 3; ++q) pb[q] = ok ? bpl[q * plane + at] : make_uint4(0u, 0u, 0u, 0u);
+    } else if (!B_NK) {  // [K][N]
+      const int col = n0 + si;
 #pragma unroll
-      for (int tj = 0; tj < 2; ++tj) {
-        s[tj] = 0.f;
+      for (int j = 0; j < 8; ++j)
+        xb[j] = (FULL || (col < N && kk + j < kend)) ? B[(size_t)(kk + j) * ldb + col] : 0.f;
+    } else {  // [N][K]
+      const int row = n0 + si;
+      const float* p = B + (size_t)row * ldb + kk;
+      if (FULL || (VB && row < N && kk + 8 <= kend)) {
+        const float4 u = *reinterpret_cast<const float4*>(p), w = *reinterpret_cast<const float4*>(p + 4);
+        xb[0] = u.x; xb[1] = u.y; xb[2] = u.z; xb[3] = u.w;
+        xb[4] = w.x; xb[5] = w.y; xb[6] = w.z; xb[7] = w.w;
+      } else {
 #pragma unroll
-        for (int ti = 0; ti < 2; ++ti)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int row = m0 + wm + ti * 32 + (v >> 2) * 8 + h * 4 + (v & 3);
-            s[tj] += row < M ? acc[ti][tj][v] : 0.f;
-          }
-        s[tj] += __shfl_xor(s[tj], 32, 64);
-      }
-      red[(ncw * 4 + wave) * 64 + lane] = lane < 32 ? s[0] : s[1];
-      __syncthreads();
-      if (wave < 2) {
-        const int col = n0 + wn + lane;
-        if (col < N)
-          for (int q = 0; q <= ncw; ++q)
-            cs[((size_t)by * (ncw + 1) + q) * N + col] = red[(q * 4 + wave) * 64 + lane] + red[(q * 4 + wave + 2) * 64 + lane];
+        for (int j = 0; j < 8; ++j) xb[j] = (row < N && kk + j < kend) ? p[j] : 0.f;
       }
     }
-    return;
-  }
-  // one uniform branch per epilogue kind, then a straight store loop
-  auto store_all = [&](auto f) {
-#pragma unroll
-    for (int ti = 0; ti < 2; ++ti)
-#pragma unroll
-      for (int tj = 0; tj < 2; ++tj) {
-        const int col = n0 + wn + tj * 32 + r;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int row = m0 + wm + ti * 32 + (v >> 2) * 8 + h * 4 + (v & 3);
-          if (row < M && col < N) f(row, col, acc[ti][tj][v]);
-        }
-      }
   };
-  if (ws) {
-    store_all([&](int row, int col, float a) { ws[((size_t)bz * M + row) * N + col] = a; });
-  } else if (epi == EPI_BIAS_TANH) {
-    store_all([&](int row, int col, float a) { C[(size_t)row * ldc + col] = fast_tanh(a + bias[col]); });
-  } else if (epi == EPI_BIAS) {
-    store_all([&](int row, int col, float a) { C[(size_t)row * ldc + col] = a + bias[col]; });
-  } else {
-    store_all([&](int row, int col, float a) { C[(size_t)row * ldc + col] = a; });
+  auto store_tile = [&](int buf) {
+    uint4 p0, p1, p2;
+    split8(xa, p0, p1, p2);
+    Xs[buf][0][0][sh][si] = p0;
+    Xs[buf][0][1][sh][si] = p1;
+    Xs[buf][0][2][sh][si] = p2;
+    if constexpr (BPL) {
+      p0 = pb[0];
+      p1 = pb[1];
+      p2 = pb[2];
+    } else {
+      split8(xb, p0, p1, p2);
+    }
+    Xs[buf][1][0][sh][si] = p0;
+    Xs[buf][1][1][sh][si] = p1;
+    Xs[buf][1][2][sh][si] = p2;
+  };
+
+  int buf = 0;
+  if (kbeg < kend) {
+    load_tile(kbeg);
+    store_tile(0);
   }
+  __syncthreads();
+  for (int k0 = kbeg; k0 < kend; k0 += BK) {
+    const bool more = k0 + BK < kend;
+    if (more) load_tile(k0 + BK);
+    // this wave's operand parts: rows wm + 32 ti + r of A, columns
+    // wn + 32 tj + r of B, k-half h (8 values each)
+    bf16x8 fa[2][3], fb[2][3];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int q = 0; q < 3; ++q) {
+        fa[t][q] = __builtin_bit_cast(bf16x8, Xs[buf][0][q][h][wm + 32 * t + r]);
+        fb[t][q] = __builtin_bit_cast(bf16x8, Xs[buf][1][q][h][wn + 32 * t + r]);
+      }
+    // the six partial products, smallest first, each over the four blocks
+    // (four independent accumulators between dependent MFMAs)
+    constexpr int pa[6] = {2, 0, 1, 1, 0, 0}, pb[6] = {0, 2, 1, 0, 1, 0};
+#pragma unroll
+    for (int q = 0; q < 6; ++q)
+#pragma unroll
+      for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+        for (int tj = 0; tj < 2; ++tj)
+          acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ti][pa[q]], fb[tj][pb[q]], acc[ti][tj], 0, 0, 0);
+    if (more) store_tile(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+  }
+  gemm_epilogue(acc, reinterpret_cast<float*>(&Xs[0][0][0][0][0]), reinterpret_cast<float*>(&Xs[1][0][0][0][0]), m0,
+                n0, by, bz, M, N, C, ldc, epi, bias, aux, ldaux, ws, cs, cw, ncw);
+}
+
+// Three bfloat16 planes of an fp32 matrix, for an operand that many tiles
+// of the split-bf16 GEMM share (the weights): value (k, n) at
+// src[k*ldk + n*ldn] (0 <= k < K, 0 <= n < N) goes to plane p at
+// dst[(p*K8 + k/8)*N + n] element k%8 (uint4 = 8 bf16; K8 = ceil(K/8); zero
+// for k >= K): the 8 k-values of column n that a GEMM thread stages are one
+// 16-byte load per plane.
+__global__ void k_split_bf16(const float* __restrict__ src, uint4* __restrict__ dst, int K, int N, int ldk, int ldn,
+                             int K8) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= K8 * N) return;
+  const int kg = i / N, n = i - kg * N;
+  float x[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int k = kg * 8 + j;
+    x[j] = k < K ? src[(size_t)k * ldk + (size_t)n * ldn] : 0.f;
+  }
+  uint4 h, m, l;
+  split8(x, h, m, l);
+  const size_t plane = (size_t)K8 * N;
+  dst[i] = h;
+  dst[plane + i] = m;
+  dst[2 * plane + i] = l;
+}
+
+int launch_split_bf16(const Launch& L, const dgen_hip_op& op) {
+  // arg: [0]=src [1]=planes [2]=K [3]=N [4]=ld_k [5]=ld_n
+  const int64_t src = op.arg[0], dst = op.arg[1], K = op.arg[2], N = op.arg[3], ldk = op.arg[4], ldn = op.arg[5];
+  DGEN_REQUIRE(K > 0 && N > 0 && K < (1 << 24) && N < (1 << 24) && ldk >= 0 && ldn >= 0,
+               "split_bf16: K %lld N %lld ld %lld %lld", (long long)K, (long long)N, (long long)ldk, (long long)ldn);
+  const int64_t K8 = (K + 7) / 8;
+  DGEN_REQUIRE(K8 * N < (1ll << 31), "split_bf16: %lld x %lld too large", (long long)K, (long long)N);
+  DGEN_REQUIRE(dst % 4 == 0, "split_bf16: planes cell %lld not 16-byte aligned", (long long)dst);
+  DGEN_CHECK_CELL(L, src, (K - 1) * ldk + (N - 1) * ldn + 1, "split_bf16.src");
+  DGEN_CHECK_CELL(L, dst, 3 * K8 * N * 4, "split_bf16.planes");
+  if (L.dry) return 0;
+  const int64_t n = K8 * N;
+  hipLaunchKernelGGL(k_split_bf16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, L.stream, cell(L, src),
+                     reinterpret_cast<uint4*>(cell(L, dst)), (int)K, (int)N, (int)ldk, (int)ldn, (int)K8);
+  DGEN_LAUNCH_CHECK("k_split_bf16");
+  return 0;
 }
 
 // C = sum over the k-splits of the partial products, in split order, then
@@ -436,6 +684,26 @@ static void launch_variant(bool va, bool vb, dim3 g, hipStream_t s, const float*
     launch_vb<BK, AK, BT, false>(vb, g, s, A, B, C, M, N, K, lda, ldb, ldc, epi, bias, aux, ldaux, kchunk, ws, cs, cw, ncw, full);
 }
 
+template <bool AK, bool BT>
+static void launch_x6(bool va, bool vb, bool full, dim3 g, hipStream_t s, const float* A, const float* B, float* C,
+                      int M, int N, int K, int lda, int ldb, int ldc, int epi, const float* bias, const float* aux,
+                      int ldaux, int kchunk, float* ws, float* cs, const float* cw, int ncw, const uint4* bpl,
+                      int K8) {
+#define DGEN_X6(VA_, VB_, F_, P_)                                                                                   \
+  hipLaunchKernelGGL((k_gemm_x6<AK, P_ ? false : BT, VA_, P_ || VB_, F_, P_>), g, dim3(256), 0, s, A, B, C, M, N, \
+                     K, lda, ldb, ldc, epi, bias, aux, ldaux, kchunk, ws, cs, cw, ncw, bpl, K8)
+  if (bpl) {
+    if (full) DGEN_X6(true, true, true, true);
+    else if (va) DGEN_X6(true, true, false, true);
+    else DGEN_X6(false, true, false, true);
+  } else if (full) DGEN_X6(true, true, true, false);
+  else if (va && vb) DGEN_X6(true, true, false, false);
+  else if (va) DGEN_X6(true, false, false, false);
+  else if (vb) DGEN_X6(false, true, false, false);
+  else DGEN_X6(false, false, false, false);
+#undef DGEN_X6
+}
+
 template <int BK>
 static void launch_layout(int64_t alay, int64_t blay, bool va, bool vb, dim3 g, hipStream_t s, const float* A,
                           const float* B, float* C, int M, int N, int K, int lda, int ldb, int ldc, int epi,
@@ -460,12 +728,21 @@ int launch_gemm(const Launch& L, const dgen_hip_op& op) {
   const int64_t lda = op.arg[6], ldb = op.arg[7], ldc = op.arg[8], alay = op.arg[9], blay = op.arg[10];
   const int64_t epi = op.arg[11], bias = op.arg[12], aux = op.arg[13], ldaux = op.arg[14];
   const int64_t split = op.arg[15], ws = op.arg[16], colsum = op.arg[17], cwc = op.arg[18], ncw64 = op.arg[19];
+  const int64_t mode = op.arg[20], planes = op.arg[21];
   DGEN_REQUIRE(M > 0 && N > 0 && K > 0 && M < (1ll << 31) && N < (1ll << 31) && K < (1ll << 31),
                "gemm: M %lld N %lld K %lld", (long long)M, (long long)N, (long long)K);
   DGEN_REQUIRE(alay == 0 || alay == 1, "gemm: a_layout %lld", (long long)alay);
   DGEN_REQUIRE(blay == 0 || blay == 1, "gemm: b_layout %lld", (long long)blay);
   DGEN_REQUIRE(epi >= 0 && epi <= 3, "gemm: epilogue %lld", (long long)epi);
   DGEN_REQUIRE(split >= 1 && split <= 1024, "gemm: split_k %lld", (long long)split);
+  DGEN_REQUIRE(mode == 0 || mode == 1, "gemm: product mode %lld (0 fp32, 1 split bf16)", (long long)mode);
+  // B's split-bf16 planes (DGEN_HIP_K_SPLIT_BF16 of op(B) as [K][N]), or -1
+  const int64_t K8 = (K + 7) / 8;
+  if (planes >= 0) {
+    DGEN_REQUIRE(mode == 1, "gemm: B planes need the split-bf16 product mode");
+    DGEN_REQUIRE(planes % 4 == 0, "gemm: B planes cell %lld not 16-byte aligned", (long long)planes);
+    DGEN_CHECK_CELL(L, planes, 3 * K8 * N * 4, "gemm.B_planes");
+  }
   DGEN_REQUIRE(ldc >= N, "gemm: ldc %lld < N %lld", (long long)ldc, (long long)N);
   DGEN_REQUIRE(alay == 0 ? lda >= K : lda >= M, "gemm: lda %lld too small", (long long)lda);
   DGEN_REQUIRE(blay == 0 ? ldb >= N : ldb >= K, "gemm: ldb %lld too small", (long long)ldb);
@@ -507,9 +784,23 @@ int launch_gemm(const Launch& L, const dgen_hip_op& op) {
   float* pcs = colsum >= 0 ? cell(L, colsum) : nullptr;
   const float* pcw = ncw ? cell(L, cwc) : nullptr;
   const int e = split > 1 ? EPI_NONE : (int)epi;
-  launch_layout<BK>(alay, blay, va, vb, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk,
-                    pws, pcs, pcw, ncw, full);
-  DGEN_LAUNCH_CHECK("k_gemm");
+  if (mode == 1) {
+    const uint4* pbpl = planes >= 0 ? reinterpret_cast<const uint4*>(cell(L, planes)) : nullptr;
+    const bool full6 = va && (vb || pbpl) && M % BM == 0 && N % BN == 0 && K % BK == 0;
+#define DGEN_X6L(AK_, BT_)                                                                                          \
+  launch_x6<AK_, BT_>(va, vb, full6, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk, \
+                      pws, pcs, pcw, ncw, pbpl, (int)K8)
+    if (alay == 0 && blay == 0) DGEN_X6L(false, false);
+    else if (alay == 0) DGEN_X6L(false, true);
+    else if (blay == 0) DGEN_X6L(true, false);
+    else DGEN_X6L(true, true);
+#undef DGEN_X6L
+    DGEN_LAUNCH_CHECK("k_gemm_x6");
+  } else {
+    launch_layout<BK>(alay, blay, va, vb, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux,
+                      kchunk, pws, pcs, pcw, ncw, full);
+    DGEN_LAUNCH_CHECK("k_gemm");
+  }
   if (split > 1) {
     const size_t total = (size_t)M * N;
     if (N % 4 == 0 && ws % 4 == 0)

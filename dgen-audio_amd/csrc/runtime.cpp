@@ -84,6 +84,7 @@ static Launcher launcher_for(uint32_t k) {
     case DGEN_HIP_K_STREAM_SVF: return launch_svf_seq;
     case DGEN_HIP_K_SVF_ADJ_CHUNK: return launch_svf_adj_chunk;
     case DGEN_HIP_K_SVF_BWD: return launch_svf_bwd;
+    case DGEN_HIP_K_SPLIT_BF16: return launch_split_bf16;
     default: return nullptr;
   }
 }

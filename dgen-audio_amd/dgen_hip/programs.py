@@ -30,6 +30,30 @@ MEM_TILE = 32       # membrane cells per workgroup tile side
 MEM_WAVES = 16      # membrane waves per workgroup (4-row strips of a 64-row region)
 
 
+GEMM_PRODUCTS = {"fp32": 0, "split-bf16": 1}  # DGEN_HIP_K_GEMM arg[20]
+
+
+def _gemm_args(mode: int, args: list, b_planes: int = -1) -> list:
+    """DGEN_HIP_K_GEMM arguments with the product mode at [20] and B's
+    split-bf16 planes at [21] (column weights [18..19] default to none)."""
+    a = list(args)
+    if len(a) == 18:
+        a += [-1, 0]
+    if len(a) != 20:
+        raise ValueError(f"gemm op with {len(a)} arguments")
+    return a + [mode, b_planes if mode == 1 else -1]
+
+
+def _split_planes(p: Program, name: str, src: int, K: int, N: int, ldk: int, ldn: int) -> int:
+    """A DGEN_HIP_K_SPLIT_BF16 op of the [K][N] view (k, n) -> src[k*ldk + n*ldn]
+    into a new planes cell; returns the cell."""
+    k8 = (K + 7) // 8
+    cell = p.alloc(name, 3 * k8 * N * 4)
+    p.add(R.K_SPLIT_BF16, [src, cell, K, N, ldk, ldn], label=name, dispatch="perElement",
+          bytes=K * N * 4.0 + 3 * k8 * N * 16.0, flops=6.0 * K * N)
+    return cell
+
+
 def _f32(x) -> float:
     return float(np.float32(x))
 
@@ -85,6 +109,9 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     FORK = R.OP_FORK if side_stream else 0
     B, T, F, K, NF, NC, M = cfg.B, cfg.T, cfg.F, cfg.K, cfg.NF, cfg.NC, cfg.M
     Hd, din, Lyr = cfg.hidden, cfg.din, cfg.layers
+    if cfg.gemm_products not in GEMM_PRODUCTS:
+        raise ValueError(f"gemm_products {cfg.gemm_products!r}: one of {sorted(GEMM_PRODUCTS)}")
+    gm = GEMM_PRODUCTS[cfg.gemm_products]
     if NC > LDC:
         raise ValueError(f"K + 2 + NF = {NC} exceeds {LDC}")
     if K > 64:
@@ -151,11 +178,27 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     p.add(R.K_DENSE_SMALL, [X, W1, b1, Hs[0], M, din, Hd], label="mlp_in", dispatch="gemmSmall",
           bytes=(M * din + din * Hd + Hd + M * Hd) * f4, flops=2.0 * M * din * Hd)
     gemm_hh = dict(flops=2.0 * M * Hd * Hd, bound="mfma")
+    # split-bf16 products: the weights are split into bfloat16 planes once
+    # per step (W for the forward layers, W^T for the data gradients), so no
+    # GEMM tile splits them again
+    fwd_pl, bwd_pl = [-1] * Lyr, [-1] * Lyr
+    fwd_plh = bwd_plh = -1
+    if gm == 1:
+        for l in range(1, Lyr):
+            W, _b = woff[l]
+            fwd_pl[l] = _split_planes(p, f"W{l + 1}_planes", W, Hd, Hd, Hd, 1)
+            if train:
+                bwd_pl[l] = _split_planes(p, f"W{l + 1}T_planes", W, Hd, Hd, 1, Hd)
+        fwd_plh = _split_planes(p, "Wh_planes", Wh, Hd, NC, NC, 1)
+        if train:
+            bwd_plh = _split_planes(p, "WhT_planes", Wh, NC, Hd, 1, NC)
     for l in range(1, Lyr):
         W, b = woff[l]
-        p.add(R.K_GEMM, [Hs[l - 1], W, Hs[l], M, Hd, Hd, Hd, Hd, Hd, 0, 0, R.EPI_BIAS_TANH, b, -1, 0, 1, 0, -1],
+        p.add(R.K_GEMM, _gemm_args(gm, [Hs[l - 1], W, Hs[l], M, Hd, Hd, Hd, Hd, Hd, 0, 0, R.EPI_BIAS_TANH, b, -1, 0, 1,
+                                        0, -1], fwd_pl[l]),
               label=f"mlp_l{l + 1}", dispatch="gemm", bytes=(2 * M * Hd + Hd * Hd + Hd) * f4, **gemm_hh)
-    p.add(R.K_GEMM, [Hs[-1], Wh, Z, M, NC, Hd, Hd, NC, LDC, 0, 0, R.EPI_BIAS, bh, -1, 0, 1, 0, -1],
+    p.add(R.K_GEMM, _gemm_args(gm, [Hs[-1], Wh, Z, M, NC, Hd, Hd, NC, LDC, 0, 0, R.EPI_BIAS, bh, -1, 0, 1, 0, -1],
+                               fwd_plh),
           label="mlp_heads",
           dispatch="gemm", bytes=(M * Hd + Hd * NC + NC + M * NC) * f4, flops=2.0 * M * Hd * NC, bound="mfma")
     p.add(R.K_HEADS_FWD, [Z, ctrl, M, K, NF, LDC], label="heads", dispatch=f"perFrameScaled({M})",
@@ -246,7 +289,7 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     gW = [(G + (w - P), G + (b - P)) for (w, b) in woff]
     gWh, gbh = G + (Wh - P), G + (bh - P)
     # heads: dWh = H_L^T dZ ; dbh = colsum(dZ) ; dH_L = (dZ Wh^T) * (1 - H_L^2)
-    p.add(R.K_GEMM, [Hs[-1], dZ, gWh, Hd, NC, M, Hd, LDC, NC, 1, 0, R.EPI_NONE, -1, -1, 0, split_h, ws_gemm, -1],
+    p.add(R.K_GEMM, _gemm_args(gm, [Hs[-1], dZ, gWh, Hd, NC, M, Hd, LDC, NC, 1, 0, R.EPI_NONE, -1, -1, 0, split_h, ws_gemm, -1]),
           flags=SIDE | FORK, label="dW_heads", dispatch="gemmChunkPartials", bytes=(M * Hd + M * NC + Hd * NC) * f4,
           flops=2.0 * M * Hd * NC, bound="mfma")
     p.add(R.K_COLSUM, [dZ, gbh, M, NC, LDC, ws_col_side], flags=SIDE, label="db_heads",
@@ -262,8 +305,8 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
         raise ValueError(f"first-layer fan-in {din} > 4")
     dcol = [p.alloc(f"dZ{l + 1}_tile_colsums", mt * (din + 1 if l == 0 else 1) * Hd) for l in range(Lyr)]
     wcol = [[X, din] if l == 0 else [-1, 0] for l in range(Lyr)]
-    p.add(R.K_GEMM, [dZ, Wh, dH[-1], M, Hd, NC, LDC, NC, Hd, 0, 1, R.EPI_TANH_GRAD, -1, Hs[-1], Hd, 1, 0, dcol[-1]]
-          + wcol[-1],
+    p.add(R.K_GEMM, _gemm_args(gm, [dZ, Wh, dH[-1], M, Hd, NC, LDC, NC, Hd, 0, 1, R.EPI_TANH_GRAD, -1, Hs[-1], Hd, 1, 0,
+                                    dcol[-1]] + wcol[-1], bwd_plh),
           label=f"dX_heads", dispatch="gemm", bytes=(M * NC + Hd * NC + 2 * M * Hd) * f4, flops=2.0 * M * Hd * NC,
           bound="mfma")
     for l in range(Lyr - 1, 0, -1):
@@ -274,11 +317,12 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
         # after the final weight GEMM
         p.add(R.K_COLSUM, [dcol[l], gb, mt, Hd, Hd, ws_col_side], flags=SIDE | FORK, label=f"db_l{l + 1}",
               dispatch="chunkPartialsReduceToCell", bytes=(mt * Hd + Hd) * f4, flops=float(mt * Hd))
-        p.add(R.K_GEMM, [Hs[l - 1], dH[l], gw, Hd, Hd, M, Hd, Hd, Hd, 1, 0, R.EPI_NONE, -1, -1, 0, split, ws_gemm, -1],
+        p.add(R.K_GEMM, _gemm_args(gm, [Hs[l - 1], dH[l], gw, Hd, Hd, M, Hd, Hd, Hd, 1, 0, R.EPI_NONE, -1, -1, 0, split, ws_gemm,
+                                         -1]),
               flags=SIDE, label=f"dW_l{l + 1}", dispatch="gemmChunkPartials",
               bytes=(2 * M * Hd + Hd * Hd) * f4, **gemm_hh)
-        p.add(R.K_GEMM, [dH[l], W, dH[l - 1], M, Hd, Hd, Hd, Hd, Hd, 0, 1, R.EPI_TANH_GRAD, -1, Hs[l - 1], Hd, 1, 0,
-                         dcol[l - 1]] + wcol[l - 1],
+        p.add(R.K_GEMM, _gemm_args(gm, [dH[l], W, dH[l - 1], M, Hd, Hd, Hd, Hd, Hd, 0, 1, R.EPI_TANH_GRAD, -1, Hs[l - 1], Hd, 1,
+                                         0, dcol[l - 1]] + wcol[l - 1], bwd_pl[l]),
               label=f"dX_l{l + 1}", dispatch="gemm", bytes=(3 * M * Hd + Hd * Hd) * f4, **gemm_hh)
     gw1, gb1 = gW[0]
     if gb1 != gw1 + din * Hd:

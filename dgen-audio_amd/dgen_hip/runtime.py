@@ -61,6 +61,7 @@ K_SVF_SEQ = 35
 K_SVF_ADJ_CHUNK = 36
 K_SVF_BWD = 37
 K_STREAM_SVF = 38
+K_SPLIT_BF16 = 39
 
 KERNEL_NAMES = {v: k[2:].lower() for k, v in globals().items() if k.startswith("K_")}
 

@@ -103,6 +103,11 @@ class HarmonicConfig:
     weight_seed: int = 5
     target_seed: int = 4
     lr: float = 1e-3
+    # products of the MLP GEMMs: "split-bf16" (each fp32 operand split into
+    # three bfloat16 parts, six partial products accumulated in fp32: as
+    # accurate as fp32 products, on the bf16 matrix cores) or "fp32" (the
+    # fp32 matrix cores)
+    gemm_products: str = "split-bf16"
 
     @property
     def F(self) -> int:

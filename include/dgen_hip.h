@@ -58,7 +58,7 @@ enum dgen_hip_kernel {
    * arg: [0]=X [1]=W [2]=b [3]=H (cells) [4]=rows [5]=fan_in [6]=width */
   DGEN_HIP_K_DENSE_SMALL = 2,
 
-  /* fp32 MFMA GEMM  C[M][N] = op(A) op(B) with fused epilogue.
+  /* MFMA GEMM  C[M][N] = op(A) op(B) with fused epilogue, fp32 results.
    * arg: [0]=A [1]=B [2]=C [3]=M [4]=N [5]=K [6]=lda [7]=ldb [8]=ldc
    *      [9]=a_layout (0: A stored [M][K], 1: A stored [K][M])
    *      [10]=b_layout (0: B stored [K][N], 1: B stored [N][K])
@@ -72,7 +72,14 @@ enum dgen_hip_kernel {
    *           plain column sums, so the weight and bias gradients of a
    *           layer fed by X are a reduction over ceil(M/128) rows instead
    *           of M (DGEN_HIP_K_COLSUM on the cell)
-   *      [18]=X cell ([M][nw], read when nw > 0) [19]=nw (0..4) */
+   *      [18]=X cell ([M][nw], read when nw > 0) [19]=nw (0..4)
+   *      [20]=products: 0 fp32 matrix cores (v_mfma_f32_32x32x2_f32),
+   *           1 split bf16: each operand value split into three bfloat16
+   *           parts and the six partial products of significance down to
+   *           2^-16 accumulated in fp32 (v_mfma_f32_32x32x16_bf16), as
+   *           accurate as fp32 products
+   *      [21]=B planes cell or -1: with products 1, op(B) already split
+   *           ([K][N] view, DGEN_HIP_K_SPLIT_BF16) */
   DGEN_HIP_K_GEMM = 3,
 
   /* Head activations of HarmonicDecoderModel (Model.swift:100-114):
@@ -358,6 +365,16 @@ enum dgen_hip_kernel {
    * no cells and no loss; a run processes frames [0, frame_count) and
    * carries ic1, ic2 to the next (zero after a reset). */
   DGEN_HIP_K_STREAM_SVF = 38,
+
+  /* Split of an fp32 matrix into three bfloat16 planes for the split-bf16
+   * GEMM (DGEN_HIP_K_GEMM arg[21]): value (k, n) at src[k*ld_k + n*ld_n]
+   * goes to plane p (p = 0..2: x = h + m + l, h = bf16(x), m = bf16(x - h),
+   * l = bf16(x - h - m)) as bf16 element k%8 of 16-byte entry
+   * (p*K8 + k/8)*N + n, K8 = ceil(K/8), zero for k >= K.  Done once for an
+   * operand that many GEMM tiles share (the weights, per step).
+   * arg: [0]=src [1]=planes cell (3*K8*N*4 floats, 16-byte aligned) [2]=K
+   *      [3]=N [4]=ld_k [5]=ld_n */
+  DGEN_HIP_K_SPLIT_BF16 = 39,
 };
 
 /* GEMM epilogues */
