@@ -30,7 +30,8 @@ class Op:
     dispatch: str = ""
     bytes: float = 0.0   # algorithmic HBM bytes per launch (interface read once + written once)
     flops: float = 0.0   # algorithmic flops per launch
-    bound: str = "hbm"   # roof that bounds the op: "hbm", "mfma" (fp32 matrix) or "valu" (fp32 vector)
+    bound: str = "hbm"   # roof that bounds the op: "hbm", "mfma" (fp32 matrix), "mfma_x6" (split-bf16
+                         # products on the bf16 matrix cores) or "valu" (fp32 vector)
 
 
 @dataclass
@@ -62,7 +63,7 @@ class Program:
         farg = [float(a) for a in farg]
         if len(arg) > 32 or len(farg) > 8:
             raise ValueError("too many op arguments")
-        if bound not in ("hbm", "mfma", "valu"):
+        if bound not in ("hbm", "mfma", "mfma_x6", "valu"):
             raise ValueError(f"unknown bound {bound}")
         self.ops.append(Op(kernel, arg + [0] * (32 - len(arg)), farg + [0.0] * (8 - len(farg)), flags, label,
                            dispatch, float(bytes), float(flops), bound))

@@ -177,7 +177,8 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     W1, b1 = woff[0]
     p.add(R.K_DENSE_SMALL, [X, W1, b1, Hs[0], M, din, Hd], label="mlp_in", dispatch="gemmSmall",
           bytes=(M * din + din * Hd + Hd + M * Hd) * f4, flops=2.0 * M * din * Hd)
-    gemm_hh = dict(flops=2.0 * M * Hd * Hd, bound="mfma")
+    mfma = "mfma_x6" if gm == 1 else "mfma"
+    gemm_hh = dict(flops=2.0 * M * Hd * Hd, bound=mfma)
     # split-bf16 products: the weights are split into bfloat16 planes once
     # per step (W for the forward layers, W^T for the data gradients), so no
     # GEMM tile splits them again
@@ -200,7 +201,7 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     p.add(R.K_GEMM, _gemm_args(gm, [Hs[-1], Wh, Z, M, NC, Hd, Hd, NC, LDC, 0, 0, R.EPI_BIAS, bh, -1, 0, 1, 0, -1],
                                fwd_plh),
           label="mlp_heads",
-          dispatch="gemm", bytes=(M * Hd + Hd * NC + NC + M * NC) * f4, flops=2.0 * M * Hd * NC, bound="mfma")
+          dispatch="gemm", bytes=(M * Hd + Hd * NC + NC + M * NC) * f4, flops=2.0 * M * Hd * NC, bound=mfma)
     p.add(R.K_HEADS_FWD, [Z, ctrl, M, K, NF, LDC], label="heads", dispatch=f"perFrameScaled({M})",
           bytes=2 * M * NC * f4, flops=M * (K * 12.0 + NF * 8.0))
     aux = p.alloc("synth_tape", 3 * B * T) if train else -1
@@ -291,7 +292,7 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     # heads: dWh = H_L^T dZ ; dbh = colsum(dZ) ; dH_L = (dZ Wh^T) * (1 - H_L^2)
     p.add(R.K_GEMM, _gemm_args(gm, [Hs[-1], dZ, gWh, Hd, NC, M, Hd, LDC, NC, 1, 0, R.EPI_NONE, -1, -1, 0, split_h, ws_gemm, -1]),
           flags=SIDE | FORK, label="dW_heads", dispatch="gemmChunkPartials", bytes=(M * Hd + M * NC + Hd * NC) * f4,
-          flops=2.0 * M * Hd * NC, bound="mfma")
+          flops=2.0 * M * Hd * NC, bound=mfma)
     p.add(R.K_COLSUM, [dZ, gbh, M, NC, LDC, ws_col_side], flags=SIDE, label="db_heads",
           dispatch="chunkPartialsReduceToCell", bytes=(M * NC + NC) * f4, flops=float(M * NC))
     dH = [p.alloc(f"dZ{l + 1}", M * Hd) for l in range(Lyr)]
@@ -308,7 +309,7 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     p.add(R.K_GEMM, _gemm_args(gm, [dZ, Wh, dH[-1], M, Hd, NC, LDC, NC, Hd, 0, 1, R.EPI_TANH_GRAD, -1, Hs[-1], Hd, 1, 0,
                                     dcol[-1]] + wcol[-1], bwd_plh),
           label=f"dX_heads", dispatch="gemm", bytes=(M * NC + Hd * NC + 2 * M * Hd) * f4, flops=2.0 * M * Hd * NC,
-          bound="mfma")
+          bound=mfma)
     for l in range(Lyr - 1, 0, -1):
         W, _b = woff[l]
         gw, gb = gW[l]

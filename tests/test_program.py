@@ -36,14 +36,20 @@ def test_train_schedule_order():
     assert labels[-1] == "adam"
 
 
-def test_roofline_model_config3():
-    p = harmonic_program(HarmonicConfig())
-    gemm = [op for op in p.ops if op.bound == "mfma"]
+@pytest.mark.parametrize("products,bound,roof", [("fp32", "mfma", (0.5, 2.0)), ("split-bf16", "mfma_x6", (0.2, 1.0))])
+def test_roofline_model_config3(products, bound, roof):
+    p = harmonic_program(HarmonicConfig(gemm_products=products))
+    gemm = [op for op in p.ops if op.bound in ("mfma", "mfma_x6")]
+    assert all(op.bound == bound for op in gemm)
     flops = sum(op.flops for op in gemm)
     # 3 x 512 MLP over 32000 rows: forward + two backward GEMMs per layer
     assert abs(flops - 2 * 32000 * (2 * 512 * 512 * 3 + 512 * 127 * 3)) < 1e6
-    assert 0.5 < step_roof_ms(p) < 2.0
+    assert roof[0] < step_roof_ms(p) < roof[1]
     assert all(roof_seconds(op) >= 0 for op in p.ops)
+    # the split-bf16 GEMM roof: six bf16 partial products per fp32 product
+    if bound == "mfma_x6":
+        op = next(op for op in gemm if op.label == "mlp_l2")
+        assert roof_seconds(op) == pytest.approx(op.flops * 6 / 2.5e15)
 
 
 def test_invalid_configs_raise():
