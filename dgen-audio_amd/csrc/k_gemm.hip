@@ -69,6 +69,8 @@ __device__ __forceinline__ float apply_epi(int epi, float acc, int row, int col,
 // split-K workspace.  scr0 / scr1: two LDS areas of at least 1280 and 512
 // floats that no wave reads any more (the operand tiles after the k-loop's
 // last barrier).
+// FULLT: the tile lies inside C (no bounds tests on the stores).
+template <bool FULLT = false>
 __device__ __forceinline__ void gemm_epilogue(floatx16 (&acc)[2][2], float* scr0, float* scr1, int m0, int n0, int by,
                                               int bz, int M, int N, float* __restrict__ C, int ldc, int epi,
                                               const float* __restrict__ bias, const float* __restrict__ aux, int ldaux,
@@ -177,7 +179,7 @@ __device__ __forceinline__ void gemm_epilogue(floatx16 (&acc)[2][2], float* scr0
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int row = m0 + wm + ti * 32 + (v >> 2) * 8 + h * 4 + (v & 3);
-          if (row < M && col < N) f(row, col, acc[ti][tj][v]);
+          if (FULLT || (row < M && col < N)) f(row, col, acc[ti][tj][v]);
         }
       }
   };
@@ -571,6 +573,119 @@ __global__ __launch_bounds__(256, 3) void k_gemm_x6(const float* __restrict__ A,
                 n0, by, bz, M, N, C, ldc, epi, bias, aux, ldaux, ws, cs, cw, ncw);
 }
 
+// Split-bf16 GEMM for full tiles of a row-major A and a pre-split B (the
+// MLP's forward and data-gradient layers): both operand tiles of a k-step
+// are copied global -> LDS by the load-to-LDS instructions (no staging
+// registers), in two stages: each k-step waits for its own copies (at the
+// barrier), starts the next k-step's copies into the other stage, then reads
+// its fragments, splits A and runs the MFMAs while those copies land.  A
+// stage holds the fp32 A tile (128 rows x 4 16-byte quarters, quarter q of
+// row R in slot 4R + (q ^ f(R)), f(R) = ((R >> 1) ^ (R >> 3)) & 3, so the
+// fragment reads are free of bank conflicts) and B's three planes
+// ([plane][k-half][128 columns], 16 bytes each): 20 KB.  Three workgroups
+// per CU (157 registers; at four the allocator spills, and the spill
+// reloads wait behind the copies in flight).
+__device__ __forceinline__ int aswz(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void k_gemm_x6d(
+    const float* __restrict__ A, float* __restrict__ C, int M, int N, int K, int lda, int ldc, int epi,
+    const float* __restrict__ bias, const float* __restrict__ aux, int ldaux, float* __restrict__ cs,
+    const float* __restrict__ cw, int ncw, const uint4* __restrict__ bpl, int K8) {
+  constexpr int BK = 16, ASLOTS = BM * 4, SLOTS = ASLOTS + 3 * 2 * BN;
+  // the two stages are separate LDS objects: a read of one is then not held
+  // back by the copies in flight to the other
+  __shared__ uint4 L0[SLOTS];
+  __shared__ uint4 L1[SLOTS];
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int h = lane >> 5, r = lane & 31;
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+  int bx = blockIdx.x, by = blockIdx.y;
+  {
+    const int total = gridDim.x * gridDim.y;
+    if (total % 8 == 0) {
+      const int hw = blockIdx.y * gridDim.x + blockIdx.x;
+      const int lg = (hw % 8) * (total / 8) + hw / 8;
+      bx = lg % gridDim.x;
+      by = lg / gridDim.x;
+    }
+  }
+  const int m0 = by * BM, n0 = bx * BN;
+  // this lane's copies (element offsets): A slots (2w + i)*64 + lane, B
+  // slots (3w + j)*64 + lane
+  unsigned aoff[2], boff[3];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int s = (wave * 2 + i) * 64 + lane, row = s >> 2, q = (s & 3) ^ aswz(row);
+    aoff[i] = (unsigned)((m0 + row) * lda + 4 * q);
+  }
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    const int u = (wave * 3 + j) * 64 + lane, p = u / (2 * BN), hh = (u / BN) & 1, col = u % BN;
+    boff[j] = (unsigned)((p * K8 + hh) * N + n0 + col);
+  }
+  auto issue = [&](uint4* Ld, int k0) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(A + aoff[i] + k0),
+                                       (__attribute__((address_space(3))) void*)&Ld[(wave * 2 + i) * 64], 16, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+      __builtin_amdgcn_global_load_lds((const void*)(bpl + boff[j] + (unsigned)((k0 >> 3) * N)),
+                                       (__attribute__((address_space(3))) void*)&Ld[ASLOTS + (wave * 3 + j) * 64], 16,
+                                       0, 0);
+  };
+
+  floatx16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  // one k-step on the stage in Lc, the next one's copies into Ln
+  auto step = [&](const uint4* Lc, uint4* Ln, int knext) {
+    // this stage's copies landed (the barrier waits for them) and every
+    // wave is done reading Ln
+    __syncthreads();
+    if (knext < K) issue(Ln, knext);
+    bf16x8 fb[2][3];
+#pragma unroll
+    for (int tj = 0; tj < 2; ++tj)
+#pragma unroll
+      for (int q = 0; q < 3; ++q) fb[tj][q] = __builtin_bit_cast(bf16x8, Lc[ASLOTS + (q * 2 + h) * BN + wn + 32 * tj + r]);
+    constexpr int pa[6] = {2, 0, 1, 1, 0, 0}, pb[6] = {0, 2, 1, 0, 1, 0};
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti) {
+      const int R = wm + 32 * ti + r, f = aswz(R);
+      const float4 x0 = __builtin_bit_cast(float4, Lc[4 * R + ((2 * h) ^ f)]);
+      const float4 x1 = __builtin_bit_cast(float4, Lc[4 * R + ((2 * h + 1) ^ f)]);
+      const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+      uint4 u0, u1, u2;
+      split8(x, u0, u1, u2);
+      const bf16x8 fa[3] = {__builtin_bit_cast(bf16x8, u0), __builtin_bit_cast(bf16x8, u1),
+                            __builtin_bit_cast(bf16x8, u2)};
+#pragma unroll
+      for (int q = 0; q < 6; ++q)
+#pragma unroll
+        for (int tj = 0; tj < 2; ++tj)
+          acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[pa[q]], fb[tj][pb[q]], acc[ti][tj], 0, 0, 0);
+    }
+  };
+
+  issue(L0, 0);
+  // K is a multiple of 2 * BK here: the stages alternate L0, L1
+  for (int k0 = 0; k0 < K; k0 += 2 * BK) {
+    step(L0, L1, k0 + BK);
+    step(L1, L0, k0 + 2 * BK);
+  }
+  // every wave's reads of the last stage done before the epilogue's LDS use
+  __syncthreads();
+  gemm_epilogue<true>(acc, reinterpret_cast<float*>(&L0[0]), reinterpret_cast<float*>(&L1[0]), m0, n0, by, 0, M, N,
+                      C, ldc, epi, bias, aux, ldaux, nullptr, cs, cw, ncw);
+}
+
 // Three bfloat16 planes of an fp32 matrix, for an operand that many tiles
 // of the split-bf16 GEMM share (the weights): value (k, n) at
 // src[k*ldk + n*ldn] (0 <= k < K, 0 <= n < N) goes to plane p at
@@ -728,7 +843,10 @@ int launch_gemm(const Launch& L, const dgen_hip_op& op) {
   const int64_t lda = op.arg[6], ldb = op.arg[7], ldc = op.arg[8], alay = op.arg[9], blay = op.arg[10];
   const int64_t epi = op.arg[11], bias = op.arg[12], aux = op.arg[13], ldaux = op.arg[14];
   const int64_t split = op.arg[15], ws = op.arg[16], colsum = op.arg[17], cwc = op.arg[18], ncw64 = op.arg[19];
-  const int64_t mode = op.arg[20], planes = op.arg[21];
+  const int64_t mode = op.arg[20];
+  // arg[21] is read with the split-bf16 products only (ops written before it
+  // existed leave it 0)
+  const int64_t planes = mode == 1 ? op.arg[21] : -1;
   DGEN_REQUIRE(M > 0 && N > 0 && K > 0 && M < (1ll << 31) && N < (1ll << 31) && K < (1ll << 31),
                "gemm: M %lld N %lld K %lld", (long long)M, (long long)N, (long long)K);
   DGEN_REQUIRE(alay == 0 || alay == 1, "gemm: a_layout %lld", (long long)alay);
@@ -739,7 +857,6 @@ int launch_gemm(const Launch& L, const dgen_hip_op& op) {
   // B's split-bf16 planes (DGEN_HIP_K_SPLIT_BF16 of op(B) as [K][N]), or -1
   const int64_t K8 = (K + 7) / 8;
   if (planes >= 0) {
-    DGEN_REQUIRE(mode == 1, "gemm: B planes need the split-bf16 product mode");
     DGEN_REQUIRE(planes % 4 == 0, "gemm: B planes cell %lld not 16-byte aligned", (long long)planes);
     DGEN_CHECK_CELL(L, planes, 3 * K8 * N * 4, "gemm.B_planes");
   }
@@ -790,7 +907,11 @@ int launch_gemm(const Launch& L, const dgen_hip_op& op) {
 #define DGEN_X6L(AK_, BT_)                                                                                          \
   launch_x6<AK_, BT_>(va, vb, full6, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk, \
                       pws, pcs, pcw, ncw, pbpl, (int)K8)
-    if (alay == 0 && blay == 0) DGEN_X6L(false, false);
+    if (pbpl && full6 && alay == 0 && splits == 1 && K % 32 == 0 && (int64_t)M * lda < (1ll << 32) &&
+        3 * K8 * N < (1ll << 32)) {
+      hipLaunchKernelGGL(k_gemm_x6d, g, dim3(256), 0, L.stream, pa, pc, (int)M, (int)N, (int)K, (int)lda, (int)ldc, e,
+                         pbias, paux, (int)ldaux, pcs, pcw, ncw, pbpl, (int)K8);
+    } else if (alay == 0 && blay == 0) DGEN_X6L(false, false);
     else if (alay == 0) DGEN_X6L(false, true);
     else if (blay == 0) DGEN_X6L(true, false);
     else DGEN_X6L(true, true);

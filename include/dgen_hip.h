@@ -78,8 +78,9 @@ enum dgen_hip_kernel {
    *           parts and the six partial products of significance down to
    *           2^-16 accumulated in fp32 (v_mfma_f32_32x32x16_bf16), as
    *           accurate as fp32 products
-   *      [21]=B planes cell or -1: with products 1, op(B) already split
-   *           ([K][N] view, DGEN_HIP_K_SPLIT_BF16) */
+   *      [21]=with products 1 only: B planes cell or -1 (op(B) already
+   *           split, [K][N] view, DGEN_HIP_K_SPLIT_BF16); not read with
+   *           products 0 */
   DGEN_HIP_K_GEMM = 3,
 
   /* Head activations of HarmonicDecoderModel (Model.swift:100-114):

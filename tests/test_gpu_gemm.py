@@ -165,6 +165,25 @@ def test_split_planes_sum_to_the_fp32_values_exactly(gpu):
     np.testing.assert_array_equal(h, rne.astype(np.uint32).view(np.float32).astype(np.float64))
 
 
+def test_fp32_ops_written_without_the_planes_argument_still_run(gpu):
+    """An fp32-product op built before arg[21] existed (left 0, as the op
+    builder pads) configures and computes as before."""
+    rng = np.random.default_rng(3)
+    A = rng.standard_normal((128, 64)).astype(np.float32)
+    B = rng.standard_normal((64, 128)).astype(np.float32)
+    p = Program(max_frames=1)
+    ca, cb, cc = p.alloc("A", A.size), p.alloc("B", B.size), p.alloc("C", 128 * 128)
+    p.add(R.K_GEMM, [ca, cb, cc, 128, 128, 64, 64, 128, 128, 0, 0, R.EPI_NONE, -1, -1, 128, 1, 0, -1, -1, 0, 0],
+          label="gemm")
+    assert p.ops[0].arg[21] == 0
+    with R.HIPLazyRuntime(p, 0) as rt:
+        rt.write("A", A)
+        rt.write("B", B)
+        rt.runNoCopy()
+        C = rt.read("C").reshape(128, 128)
+    assert rel(C, A.astype(np.float64) @ B) < 1e-5
+
+
 def test_product_mode_is_validated(gpu):
     p = Program(max_frames=1)
     a = p.alloc("A", 16 * 16)
