@@ -1,16 +1,29 @@
-// fp32 GEMM on the gfx950 matrix cores (v_mfma_f32_32x32x2_f32) for the
-// control network: forward layers with fused bias+tanh, backward data GEMMs
-// with the fused tanh derivative, and weight-gradient GEMMs reduced over the
-// 32k-row batch with a deterministic split-K.
+// GEMM on the gfx950 matrix cores for the control network: forward layers
+// with fused bias+tanh, backward data GEMMs with the fused tanh derivative,
+// and weight-gradient GEMMs reduced over the 32k-row batch with a
+// deterministic split-K.  Two product modes share the tiling and the fused
+// epilogue:
+//
+// - fp32 products (k_gemm, v_mfma_f32_32x32x2_f32);
+// - split-bf16 products (k_gemm_x6, k_gemm_x6d, v_mfma_f32_32x32x16_bf16):
+//   each fp32 operand value is split exactly into three bfloat16 parts and
+//   the six partial products above 2^-16 of the leading one are accumulated
+//   in fp32 (Henry, Tang and Heinecke, "Leveraging the bfloat16 artificial
+//   intelligence datatype for higher-precision computations", ARITH 2019),
+//   as accurate as the fp32 products against fp64 at 192 matrix-core cycles
+//   per 32x32x16 step instead of 512.  A weight operand shared by many row
+//   tiles is split once per step into bfloat16 planes (k_split_bf16);
+//   k_gemm_x6d copies full tiles of row-major A and those planes global ->
+//   LDS with the load-to-LDS instructions and splits A at the fragment read.
 //
 // The reference lowers these matmuls to 8x8 simdgroup fp32 tiles
 // (Sources/DGen/Emit+GEMM.swift:10-80, GEMMPass.swift:60-109); here each
 // 256-thread workgroup owns a 128x128 output tile, each wave a 64x64 quadrant
 // of four 32x32 MFMA accumulators (64 fp32 registers per lane).
 //
-// LDS holds both operand tiles k-major ([BK][BM] and [BK][BN]) so every
-// layout (A as [M][K] or [K][M], B as [K][N] or [N][K]) feeds the MFMA with
-// conflict-free single-float reads; tiles are double buffered with one
+// In k_gemm, LDS holds both operand tiles k-major ([BK][BM] and [BK][BN]) so
+// every layout (A as [M][K] or [K][M], B as [K][N] or [N][K]) feeds the MFMA
+// with conflict-free single-float reads; tiles are double buffered with one
 // barrier per k-step.  The k-step depth is a template parameter (16 or 32);
 // every launch uses BK = 16: 33 KB of LDS and at most 128 registers per lane,
 // so four workgroups share a CU (four waves per SIMD): a 1000-tile grid runs
@@ -490,9 +503,21 @@ __global__ __launch_bounds__(256, 3) void k_gemm_x6(const float* __restrict__ A,
       }
     } else {  // [K][M]: one value in each of 8 rows (coalesced across the wave)
       const int col = m0 + si;
+      if constexpr (FULL) {
+        // raw buffer loads: the lane's column in a VGPR, each row's offset in
+        // an SGPR (sh is uniform in a wave), no address arithmetic per load
+        const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(A), 0, (int)(4u * (unsigned)(K * lda)),
+                                                          0x00020000);
+        const int ku = k0 + 8 * __builtin_amdgcn_readfirstlane(sh);
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        xa[j] = (FULL || (col < M && kk + j < kend)) ? A[(size_t)(kk + j) * lda + col] : 0.f;
+        for (int j = 0; j < 8; ++j)
+          xa[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, 4u * (unsigned)col,
+                                                                                  (int)(4u * (unsigned)((ku + j) * lda)), 0));
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          xa[j] = (col < M && kk + j < kend) ? A[(size_t)(kk + j) * lda + col] : 0.f;
+      }
     }
     if constexpr (BPL) {  // planes: 16 bytes per plane (zero past K8 and N)
       const int kg = (k0 >> 3) + sh, col = n0 + si;
@@ -502,9 +527,19 @@ __global__ __launch_bounds__(256, 3) void k_gemm_x6(const float* __restrict__ A,
       for (int q = 0; q < 3; ++q) pb[q] = ok ? bpl[q * plane + at] : make_uint4(0u, 0u, 0u, 0u);
     } else if (!B_NK) {  // [K][N]
       const int col = n0 + si;
+      if constexpr (FULL) {
+        const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(B), 0, (int)(4u * (unsigned)(K * ldb)),
+                                                          0x00020000);
+        const int ku = k0 + 8 * __builtin_amdgcn_readfirstlane(sh);
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        xb[j] = (FULL || (col < N && kk + j < kend)) ? B[(size_t)(kk + j) * ldb + col] : 0.f;
+        for (int j = 0; j < 8; ++j)
+          xb[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, 4u * (unsigned)col,
+                                                                                  (int)(4u * (unsigned)((ku + j) * ldb)), 0));
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          xb[j] = (col < N && kk + j < kend) ? B[(size_t)(kk + j) * ldb + col] : 0.f;
+      }
     } else {  // [N][K]
       const int row = n0 + si;
       const float* p = B + (size_t)row * ldb + kk;
@@ -903,7 +938,9 @@ int launch_gemm(const Launch& L, const dgen_hip_op& op) {
   const int e = split > 1 ? EPI_NONE : (int)epi;
   if (mode == 1) {
     const uint4* pbpl = planes >= 0 ? reinterpret_cast<const uint4*>(cell(L, planes)) : nullptr;
-    const bool full6 = va && (vb || pbpl) && M % BM == 0 && N % BN == 0 && K % BK == 0;
+    // (full tiles: raw buffer loads over the operands, so their byte extents stay below 2^31)
+    const bool full6 = va && (vb || pbpl) && M % BM == 0 && N % BN == 0 && K % BK == 0 && ext_a < (1ll << 31) &&
+                       ext_b < (1ll << 31);
 #define DGEN_X6L(AK_, BT_)                                                                                          \
   launch_x6<AK_, BT_>(va, vb, full6, g, L.stream, pa, pb, pc, M, N, K, lda, ldb, ldc, e, pbias, paux, ldaux, kchunk, \
                       pws, pcs, pcw, ncw, pbpl, (int)K8)

@@ -20,7 +20,7 @@ ROW_ENTRIES = 16  # (segment, slot) entries per control row (kRowEntries)
 LDC = 128         # padded control-row stride (K + 2 + NF <= 128)
 SPLITK_ROWS = 1024  # rows per split of the weight-gradient GEMMs
 GEMM_TILE_M = 128  # output rows per GEMM workgroup tile (k_gemm.hip BM)
-SPLITK_ROWS_HEADS = 512  # the heads' weight gradient has one 128-wide column tile: split finer to fill the chip
+SPLITK_ROWS_HEADS = 256  # the heads' weight gradient has one 128-wide column tile: split finer to fill the chip
 MSS_TILE = 4096     # output samples per spectral-loss workgroup
 BQ_CHUNK = 256      # frames per biquad scan chunk
 SVF_CHUNK = 256     # frames per SVF scan chunk
