@@ -418,6 +418,9 @@ struct FrameRec {
 // Per-wave LDS of the synth kernels.
 struct SegLds {
   FrameRec fr[kSeg];
+  // per-frame weights of the four row slots: a frame's control value is
+  // sum_j wt[i][j] * row[j][c] = (1-frac) row[lo][c] + frac row[hi][c]
+  float4 wt[kSeg];
   float row[kSlots][kMaxNC];      // control rows touched by the segment
   float pre[kSlots][kMaxK + 1];   // prefix sums of the harmonic columns of each row
   float noise[kMaxNoise];         // noise[t0 - (NF-1) ... t0 + 63]
@@ -428,11 +431,12 @@ struct SegLds {
   float dfl[kSeg];
 };
 
-// Stage the segment's frame records, rows, their harmonic prefix sums (if
-// want_pre) and the noise window.  Returns 1 if every frame's f0 admits the
-// fast chain step.
+// Stage the segment's frame records and slot weights, rows, their harmonic
+// prefix sums (if want_pre) and the noise window; nslot_out = the number of
+// row slots in use, pairs_out = every frame reads two distinct rows.
+// Returns 1 if every frame's f0 admits the fast chain step.
 __device__ __forceinline__ int stage_segment(const SynthArgs& a, SegLds& L, int s, int b, int lane, int nt,
-                                             bool want_pre) {
+                                             bool want_pre, int& nslot_out, bool& pairs_out) {
   const int t0 = s * kSeg;
   const int NC = a.K + 2 + a.NF;
   int ok = 1;
@@ -449,6 +453,12 @@ __device__ __forceinline__ int stage_segment(const SynthArgs& a, SegLds& L, int 
       ok = fast_f0(r.f0) ? 1 : 0;
     }
     L.fr[lane] = r;
+    const int slo = r.slots & 255, shi = r.slots >> 8;
+    float w[kSlots];
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) w[j] = (slo == j ? r.omf : 0.0f) + (shi == j ? r.frac : 0.0f);
+    L.wt[lane] = make_float4(w[0], w[1], w[2], w[3]);
+    pairs_out = __all(lane >= nt || slo != shi);
   }
   int nslot = 0;
   for (int j = 0; j < kSlots; ++j) {
@@ -458,6 +468,7 @@ __device__ __forceinline__ int stage_segment(const SynthArgs& a, SegLds& L, int 
     for (int c = lane; c < NC; c += 64) L.row[j][c] = src[c];
     ++nslot;
   }
+  nslot_out = nslot;
   for (int i = lane; i < a.NF - 1 + kSeg; i += 64) {
     const int tt = t0 - (a.NF - 1) + i;
     L.noise[i] = (tt >= 0 && tt < a.T) ? a.noise[tt] : 0.0f;
@@ -513,27 +524,75 @@ __device__ __forceinline__ float frame_fir(const SynthArgs& a, const SegLds& L, 
 // the backward reuses.
 constexpr int kWavesFwd = 2;
 
+// Row-slot arithmetic of a frame.  NS = 2 or 4: the slot-weight form over
+// the slots that can be nonzero (a weight-0 slot contributes 0 * value, so
+// the operands must be finite: the kernels vote for it per segment).
+// NS = 0: the exact per-frame form of the reference's sampleRow lerp and its
+// gradient, which touches only the frame's rows lo and hi (non-finite
+// values stay in the frames and rows that read them).
+// A lane's control value of a frame (slot weights w) from its row-slot
+// values rv (0 past the slots in use); the exact form reads rows lo and hi.
+// Products and sums are rounded one by one (no fma): with finite rows and
+// lo != hi the two nonzero terms are (1-frac) row[lo] and frac row[hi] and
+// the others add a signed zero, so the value is the exact form's bit for bit.
+template <int NS>
+__device__ __forceinline__ float slot_lerp(const float4& w, const float (&rv)[kSlots]) {
+  static_assert(NS == 2 || NS == kSlots, "slot-weight form");
+  float v = w.x * rv[0] + w.y * rv[1];
+  if constexpr (NS > 2) v = v + w.z * rv[2];
+  if constexpr (NS > 3) v = v + w.w * rv[3];
+  return v;
+}
+
+// Adds a frame's gradient x of one control column into the row slots.
+template <int NS>
+__device__ __forceinline__ void slot_acc(float (&acc)[kSlots], const FrameRec& r, const float4& w, float x) {
+  if constexpr (NS == 0) {
+    const int slo = r.slots & 255, shi = r.slots >> 8;
+    const float vl = r.omf * x, vh = r.frac * x;
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+      acc[j] += slo == j ? vl : 0.0f;
+      acc[j] += shi == j ? vh : 0.0f;
+    }
+  } else {
+    acc[0] = fmaf(w.x, x, acc[0]);
+    acc[1] = fmaf(w.y, x, acc[1]);
+    if constexpr (NS > 2) acc[2] = fmaf(w.z, x, acc[2]);
+    if constexpr (NS > 3) acc[3] = fmaf(w.w, x, acc[3]);
+  }
+}
+
 // Chain pass of the forward held in registers: v[i] = sin(2 pi phase_k(i)) *
 // masked amplitude for frame i of this lane's harmonic k (0 for lanes >= K
 // and frames >= nt).  The phase steps are those of the reference's stateful
 // phasor (pre-increment output, wrap), the backward's pass repeats them bit
-// for bit.
-template <bool FAST>
+// for bit.  rv = this lane's amplitude column in each row slot.
+template <bool FAST, int NS>
 __device__ __forceinline__ void chain_regs(const SynthArgs& a, const SegLds& L, float (&v)[kSeg], int lane, int nt,
-                                           float ph) {
+                                           float ph, const float (&rv)[kSlots]) {
   const float kf = (float)(lane + 1);
   const float nyq = a.nyq;
   const bool harm = lane < a.K;
   const int kk = harm ? lane : 0;
 #pragma unroll
   for (int i0 = 0; i0 < kSeg; i0 += kBlk) {
+    // the block's reads are issued at its start, not hoisted over the
+    // whole segment (which would hold every frame's values in registers)
+    asm volatile("" ::: "memory");
     FrameRec r[kBlk];
-    float al[kBlk], ah[kBlk];
+    float4 w[kBlk];
+    float al[kBlk], ah[kBlk];  // exact form: the lane's values in rows lo and hi
 #pragma unroll
     for (int j = 0; j < kBlk; ++j) {
-      r[j] = L.fr[i0 + j];
-      al[j] = L.row[r[j].slots & 255][kk];
-      ah[j] = L.row[r[j].slots >> 8][kk];
+      if constexpr (NS == 0) {
+        r[j] = L.fr[i0 + j];
+        al[j] = L.row[r[j].slots & 255][kk];
+        ah[j] = L.row[r[j].slots >> 8][kk];
+      } else {
+        r[j].f0 = L.fr[i0 + j].f0;
+        w[j] = L.wt[i0 + j];
+      }
     }
 #pragma unroll
     for (int j = 0; j < kBlk; ++j) {
@@ -552,7 +611,11 @@ __device__ __forceinline__ void chain_regs(const SynthArgs& a, const SegLds& L, 
       }
       const float p = ph;
       ph = FAST ? __builtin_amdgcn_fractf(ph + inc) : phasor_wrap(ph + inc);
-      const float amp = r[j].omf * al[j] + r[j].frac * ah[j];
+      float amp;
+      if constexpr (NS == 0)
+        amp = r[j].omf * al[j] + r[j].frac * ah[j];
+      else
+        amp = slot_lerp<NS>(w[j], rv);
       v[i] = (harm && freq < nyq) ? sin2pi(p) * amp : 0.0f;
     }
   }
@@ -593,14 +656,31 @@ __global__ __launch_bounds__(64 * kWavesFwd) void k_synth_fwd(SynthArgs a, float
   if (s >= nseg) return;
   SegLds& L = lds[wave];
   const int t0 = s * kSeg, nt = min(kSeg, a.T - t0);
-  const int fast = stage_segment(a, L, s, b, lane, nt, true);
+  int nslot;
+  bool pairs;
+  const int fast = stage_segment(a, L, s, b, lane, nt, true, nslot, pairs);
   float v[kSeg];
   {
-    const float ph = a.ckpt[((size_t)s * a.B + b) * a.K + (lane < a.K ? lane : 0)];
-    if (fast)
-      chain_regs<true>(a, L, v, lane, nt, ph);
+    const int kk = lane < a.K ? lane : 0;
+    const float ph = a.ckpt[((size_t)s * a.B + b) * a.K + kk];
+    float rv[kSlots];
+    bool fin = true;
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+      rv[j] = j < nslot ? L.row[j][kk] : 0.0f;
+      fin = fin && isfinite(rv[j]);
+    }
+    // slot weights need finite rows and two distinct rows per frame; else
+    // the exact per-frame form
+    const int ns = !(__all(fin) && pairs) ? 0 : (nslot <= 2 ? 2 : kSlots);
+    if (fast && ns == 2)
+      chain_regs<true, 2>(a, L, v, lane, nt, ph, rv);
+    else if (fast && ns == kSlots)
+      chain_regs<true, kSlots>(a, L, v, lane, nt, ph, rv);
+    else if (fast)
+      chain_regs<true, 0>(a, L, v, lane, nt, ph, rv);
     else
-      chain_regs<false>(a, L, v, lane, nt, ph);
+      chain_regs<false, 0>(a, L, v, lane, nt, ph, rv);
   }
   const float num = reduce_scatter64(v, lane);  // frame = lane
   if (lane < nt) {
@@ -638,62 +718,33 @@ __global__ __launch_bounds__(64 * kWavesFwd) void k_synth_fwd(SynthArgs a, float
 // handled by lane c & 63 in pass c >> 6.
 constexpr int kWavesBwd = 2;
 
-// Four row-slot accumulators of one control column.  Frames come in runs
-// with a constant slot pair; a run is summed in two registers and added to
-// the slots when the pair changes.
-struct SlotAcc {
-  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-  float sl = 0.f, sh = 0.f;
-  int cur = -1;
-  __device__ __forceinline__ void put(int slot, float v) {
-    a0 += slot == 0 ? v : 0.f;
-    a1 += slot == 1 ? v : 0.f;
-    a2 += slot == 2 ? v : 0.f;
-    a3 += slot == 3 ? v : 0.f;
-  }
-  __device__ __forceinline__ void flush() {
-    if (cur >= 0) {
-      put(cur & 255, sl);
-      put(cur >> 8, sh);
-    }
-    sl = sh = 0.f;
-  }
-  __device__ __forceinline__ void add(int slots, float wl, float wh) {
-    if (slots != cur) {
-      flush();
-      cur = slots;
-    }
-    sl += wl;
-    sh += wh;
-  }
-  __device__ __forceinline__ void store(float* out, int ldc, int c) {
-    flush();
-    out[0 * ldc + c] = a0;
-    out[1 * ldc + c] = a1;
-    out[2 * ldc + c] = a2;
-    out[3 * ldc + c] = a3;
-  }
-};
-
-// Column passes of the backward.  Pass 1 runs the phase chain (lane =
-// harmonic k, the forward's chain bit for bit) and accumulates harmonic
-// column k in the same loop, so no per-frame sine table is staged; lanes
-// k >= K take the non-harmonic columns lane + 64.  Pass 2 takes columns
-// K + lane.  Together they cover every column c < K + 128 >= NC.
-template <bool FAST>
-__device__ __forceinline__ void bwd_harmonic_pass(const SynthArgs& a, const SegLds& L, SlotAcc& acc, int lane,
+// Column passes of the backward, each accumulating its column's gradient
+// into the four row slots with the frames' slot weights.  Pass 1 runs the
+// phase chain (lane = harmonic k, the forward's chain bit for bit) and
+// accumulates harmonic column k in the same loop, so no per-frame sine table
+// is staged; lanes k >= K take the non-harmonic columns lane + 64.  Pass 2
+// takes columns K + lane.  Together they cover every column c < K + 128 >= NC.
+template <bool FAST, int NS>
+__device__ __forceinline__ void bwd_harmonic_pass(const SynthArgs& a, const SegLds& L, float (&acc)[kSlots], int lane,
                                                   int nt, float ph, int nidx_spare) {
   const float kf = (float)(lane + 1);
   const float nyq = a.nyq;
   const bool harm = lane < a.K;
   const int n = FAST ? kSeg : nt;
+  // (rolled: the blocks' reads and sums stay within a few registers)
+#pragma unroll 1
   for (int i0 = 0; i0 < n; i0 += kBlk) {
     FrameRec r[kBlk];
     float hs[kBlk], cf[kBlk], ex[kBlk];
+    float4 w[kBlk];
 #pragma unroll
     for (int j = 0; j < kBlk; ++j) {
       const int i = i0 + j;
-      r[j] = L.fr[i];
+      if constexpr (NS == 0)
+        r[j] = L.fr[i];
+      else
+        r[j].f0 = L.fr[i].f0;
+      w[j] = L.wt[i];
       hs[j] = L.hs[i];
       cf[j] = L.coef[i];
       ex[j] = L.dfl[i] * L.noise[i + nidx_spare];
@@ -712,11 +763,44 @@ __device__ __forceinline__ void bwd_harmonic_pass(const SynthArgs& a, const SegL
       }
       const float p = ph;
       ph = FAST ? __builtin_amdgcn_fractf(ph + inc) : phasor_wrap(ph + inc);
-      const float sv = sin2pi(p);
-      const float dm = harm ? (freq < nyq ? (sv - hs[j]) * cf[j] : 0.0f) : ex[j];
-      acc.add(r[j].slots, r[j].omf * dm, r[j].frac * dm);
+      // every lane evaluates the sine (opaque to the compiler), so the
+      // selects below stay branch-free instead of nested exec-mask regions
+      float sv = sin2pi(p);
+      asm volatile("" : "+v"(sv));
+      const float hm = (sv - hs[j]) * cf[j];
+      const float dm = harm ? (freq < nyq ? hm : 0.0f) : ex[j];
+      slot_acc<NS>(acc, r[j], w[j], dm);
     }
   }
+}
+
+// Pass 2: column K + q, q = lane (0: gain, 1: noise gain, q >= 2: tap q-2).
+template <int NS>
+__device__ __forceinline__ void bwd_gain_pass(const SegLds& L, float (&acc)[kSlots], int q, int nt) {
+  const int nidx = max(q - 2, 0);
+#pragma unroll 1
+  for (int i0 = 0; i0 < nt; i0 += kBlk) {
+    FrameRec r[kBlk];
+    float ex[kBlk];
+    float4 w[kBlk];
+#pragma unroll
+    for (int j = 0; j < kBlk; ++j) {
+      const int i = i0 + j;
+      if constexpr (NS == 0) r[j] = L.fr[i];
+      w[j] = L.wt[i];
+      ex[j] = q == 0 ? L.dg[i] : (q == 1 ? L.dng[i] : L.dfl[i] * L.noise[i + nidx]);
+    }
+#pragma unroll
+    for (int j = 0; j < kBlk; ++j) {
+      if (i0 + j >= nt) break;
+      slot_acc<NS>(acc, r[j], w[j], ex[j]);
+    }
+  }
+}
+
+__device__ __forceinline__ void store_slots(const float (&acc)[kSlots], float* out, int ldc, int c) {
+#pragma unroll
+  for (int j = 0; j < kSlots; ++j) out[j * ldc + c] = acc[j];
 }
 
 __global__ __launch_bounds__(64 * kWavesBwd) void k_synth_bwd(SynthArgs a, const float* __restrict__ dy,
@@ -729,7 +813,13 @@ __global__ __launch_bounds__(64 * kWavesBwd) void k_synth_bwd(SynthArgs a, const
   if (s >= nseg) return;
   SegLds& L = lds[wave];
   const int t0 = s * kSeg, nt = min(kSeg, a.T - t0);
-  const int fast = stage_segment(a, L, s, b, lane, nt, false);
+  int nslot;
+  bool pairs;  // (the backward's slot-weight sums need no distinct rows)
+  const int fast = stage_segment(a, L, s, b, lane, nt, false, nslot, pairs);
+  // the slot-weight form needs every per-frame factor of the column
+  // gradients (and the noise window) below 2^50 in magnitude, so that no
+  // weight-0 term is 0 * inf or 0 * NaN and no sum overflows
+  bool bnd;
   {
     float hs = 0.f, coef = 0.f, dg = 0.f, dng = 0.f, dfl = 0.f;
     if (lane < nt) {
@@ -753,8 +843,12 @@ __global__ __launch_bounds__(64 * kWavesBwd) void k_synth_bwd(SynthArgs a, const
     L.dg[lane] = dg;
     L.dng[lane] = dng;
     L.dfl[lane] = dfl;
+    constexpr float kBig = 0x1p50f;
+    bnd = fabsf(hs) < kBig && fabsf(coef) < kBig && fabsf(dg) < kBig && fabsf(dng) < kBig && fabsf(dfl) < kBig;
+    for (int i = lane; i < a.NF - 1 + kSeg; i += 64) bnd = bnd && fabsf(L.noise[i]) < kBig;
   }
   wave_sync();
+  const int ns = !__all(bnd) ? 0 : (nslot <= 2 ? 2 : kSlots);
 
   const int NC = a.K + 2 + a.NF;
   float* out = part + ((size_t)b * nseg + s) * kSlots * a.ldc;
@@ -763,35 +857,28 @@ __global__ __launch_bounds__(64 * kWavesBwd) void k_synth_bwd(SynthArgs a, const
     const int c = lane < a.K ? lane : lane + 64;
     const int nidx = lane < a.K ? 0 : c - a.K - 2;
     const float ph = a.ckpt[((size_t)s * a.B + b) * a.K + (lane < a.K ? lane : 0)];
-    SlotAcc acc;
-    if (fast)
-      bwd_harmonic_pass<true>(a, L, acc, lane, nt, ph, nidx);
+    float acc[kSlots] = {0.f, 0.f, 0.f, 0.f};
+    if (fast && ns == 2)
+      bwd_harmonic_pass<true, 2>(a, L, acc, lane, nt, ph, nidx);
+    else if (fast && ns == kSlots)
+      bwd_harmonic_pass<true, kSlots>(a, L, acc, lane, nt, ph, nidx);
+    else if (fast)
+      bwd_harmonic_pass<true, 0>(a, L, acc, lane, nt, ph, nidx);
     else
-      bwd_harmonic_pass<false>(a, L, acc, lane, nt, ph, nidx);
-    if (c < NC) acc.store(out, a.ldc, c);
+      bwd_harmonic_pass<false, 0>(a, L, acc, lane, nt, ph, nidx);
+    if (c < NC) store_slots(acc, out, a.ldc, c);
   }
   {
     // pass 2: column K + lane (gain, noise gain, taps 0..61)
     const int c = a.K + lane;
-    const int q = lane;  // 0: gain, 1: noise gain, q >= 2: tap q-2
-    const int nidx = max(q - 2, 0);
-    SlotAcc acc;
-    for (int i0 = 0; i0 < nt; i0 += kBlk) {
-      FrameRec r[kBlk];
-      float ex[kBlk];
-#pragma unroll
-      for (int j = 0; j < kBlk; ++j) {
-        const int i = i0 + j;
-        r[j] = L.fr[i];
-        ex[j] = q == 0 ? L.dg[i] : (q == 1 ? L.dng[i] : L.dfl[i] * L.noise[i + nidx]);
-      }
-#pragma unroll
-      for (int j = 0; j < kBlk; ++j) {
-        if (i0 + j >= nt) break;
-        acc.add(r[j].slots, r[j].omf * ex[j], r[j].frac * ex[j]);
-      }
-    }
-    if (c < NC) acc.store(out, a.ldc, c);
+    float acc[kSlots] = {0.f, 0.f, 0.f, 0.f};
+    if (ns == 2)
+      bwd_gain_pass<2>(L, acc, lane, nt);
+    else if (ns == kSlots)
+      bwd_gain_pass<kSlots>(L, acc, lane, nt);
+    else
+      bwd_gain_pass<0>(L, acc, lane, nt);
+    if (c < NC) store_slots(acc, out, a.ldc, c);
   }
 }
 
