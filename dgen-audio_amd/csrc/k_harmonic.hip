@@ -421,7 +421,10 @@ struct SegLds {
   // per-frame weights of the four row slots: a frame's control value is
   // sum_j wt[i][j] * row[j][c] = (1-frac) row[lo][c] + frac row[hi][c]
   float4 wt[kSeg];
-  float row[kSlots][kMaxNC];      // control rows touched by the segment
+  // control rows touched by the segment; the stride (4 mod 64 words) puts
+  // one column of the four slots in different banks, as the FIR's lanes
+  // (frames) read rows lo and hi of their own frames
+  float row[kSlots][kMaxNC + 4];
   float pre[kSlots][kMaxK + 1];   // prefix sums of the harmonic columns of each row
   float noise[kMaxNoise];         // noise[t0 - (NF-1) ... t0 + 63]
   float hs[kSeg];                 // per-frame scalars of the backward
@@ -623,27 +626,55 @@ __device__ __forceinline__ void chain_regs(const SynthArgs& a, const SegLds& L, 
 
 // Butterfly reduce-scatter across the wave: on entry v[i] is this lane's
 // term of frame i; on return v[0] is the sum over all 64 lanes of frame
-// `lane`'s terms.  Stage D keeps the half of the frames selected by bit D
-// of the lane and adds the partner lane's (lane ^ D) copy of that half.
+// `lane`'s terms.  Stage D keeps the half of the frames selected by bit D of
+// the lane and adds a partner's copy of that half, the partner being a lane
+// with the other bit D that holds the same frames: lane ^ 32 and lane ^ 16
+// by v_permlane32_swap / v_permlane16_swap (x's upper lanes trade places
+// with y's lower lanes, so x + y is each lane's kept half plus its
+// partner's, no selects), then the row mirror (lane ^ 15 in a row of 16),
+// the half-row mirror (^ 7) and two quad permutations (^ 2, ^ 1) by DPP.
+// The swaps need two wait states after a VALU write of their operands.
+#define DGEN_SWAP4(OP, D, j)                                                                                        \
+  asm("s_nop 1\n\t" OP " %0, %1\n\t" OP " %2, %3\n\t" OP " %4, %5\n\t" OP " %6, %7"                             \
+      : "+v"(v[j]), "+v"(v[j + D]), "+v"(v[j + 1]), "+v"(v[j + 1 + D]), "+v"(v[j + 2]), "+v"(v[j + 2 + D]),         \
+        "+v"(v[j + 3]), "+v"(v[j + 3 + D]))
+
 template <int D>
-__device__ __forceinline__ void rs_stage(float (&v)[kSeg], int lane) {
+__device__ __forceinline__ void rs_swap_stage(float (&v)[kSeg]) {
+  static_assert(D == 32 || D == 16, "lane-swap stages");
+#pragma unroll
+  for (int j = 0; j < D; j += 4) {
+    if constexpr (D == 32)
+      DGEN_SWAP4("v_permlane32_swap_b32", 32, j);
+    else
+      DGEN_SWAP4("v_permlane16_swap_b32", 16, j);
+  }
+#pragma unroll
+  for (int j = 0; j < D; ++j) v[j] = v[j] + v[j + D];
+}
+#undef DGEN_SWAP4
+
+template <int D, int CTRL>
+__device__ __forceinline__ void rs_dpp_stage(float (&v)[kSeg], int lane) {
   const bool up = (lane & D) != 0;
 #pragma unroll
   for (int j = 0; j < D; ++j) {
     const float send = up ? v[j] : v[j + D];
     const float keep = up ? v[j + D] : v[j];
-    v[j] = keep + __shfl_xor(send, D, 64);
+    const float got = __builtin_bit_cast(
+        float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, send), CTRL, 0xf, 0xf, false));
+    v[j] = keep + got;
   }
 }
 
 __device__ __forceinline__ float reduce_scatter64(float (&v)[kSeg], int lane) {
   static_assert(kSeg == 64, "one frame per lane");
-  rs_stage<32>(v, lane);
-  rs_stage<16>(v, lane);
-  rs_stage<8>(v, lane);
-  rs_stage<4>(v, lane);
-  rs_stage<2>(v, lane);
-  rs_stage<1>(v, lane);
+  rs_swap_stage<32>(v);
+  rs_swap_stage<16>(v);
+  rs_dpp_stage<8, 0x140>(v, lane);  // row_mirror
+  rs_dpp_stage<4, 0x141>(v, lane);  // row_half_mirror
+  rs_dpp_stage<2, 0x4e>(v, lane);   // quad_perm [2,3,0,1]
+  rs_dpp_stage<1, 0xb1>(v, lane);   // quad_perm [1,0,3,2]
   return v[0];
 }
 
