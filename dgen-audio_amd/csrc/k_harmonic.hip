@@ -427,11 +427,11 @@ struct SegLds {
   float row[kSlots][kMaxNC + 4];
   float pre[kSlots][kMaxK + 1];   // prefix sums of the harmonic columns of each row
   float noise[kMaxNoise];         // noise[t0 - (NF-1) ... t0 + 63]
-  float hs[kSeg];                 // per-frame scalars of the backward
-  float coef[kSeg];
+  // per-frame scalars of the backward: (f0, hs, coef, dfl) as one 16-byte
+  // record (the harmonic pass reads all four per frame), and dg, dng
+  float4 pk[kSeg];
   float dg[kSeg];
   float dng[kSeg];
-  float dfl[kSeg];
 };
 
 // Stage the segment's frame records and slot weights, rows, their harmonic
@@ -755,9 +755,13 @@ constexpr int kWavesBwd = 2;
 // accumulates harmonic column k in the same loop, so no per-frame sine table
 // is staged; lanes k >= K take the non-harmonic columns lane + 64.  Pass 2
 // takes columns K + lane.  Together they cover every column c < K + 128 >= NC.
-template <bool FAST, int NS>
+// MASKC: no harmonic crosses the Nyquist limit inside the segment, so each
+// lane's mask is one value for all its frames (the caller zeroes the sums
+// of lanes that are masked throughout) and no frame tests it.
+template <bool FAST, int NS, bool MASKC = false>
 __device__ __forceinline__ void bwd_harmonic_pass(const SynthArgs& a, const SegLds& L, float (&acc)[kSlots], int lane,
                                                   int nt, float ph, int nidx_spare) {
+  static_assert(!MASKC || (FAST && NS != 0), "the constant mask is a fast slot-weight form");
   const float kf = (float)(lane + 1);
   const float nyq = a.nyq;
   const bool harm = lane < a.K;
@@ -771,14 +775,19 @@ __device__ __forceinline__ void bwd_harmonic_pass(const SynthArgs& a, const SegL
 #pragma unroll
     for (int j = 0; j < kBlk; ++j) {
       const int i = i0 + j;
-      if constexpr (NS == 0)
+      if constexpr (NS == 0) {
         r[j] = L.fr[i];
-      else
-        r[j].f0 = L.fr[i].f0;
+        hs[j] = L.pk[i].y;
+        cf[j] = L.pk[i].z;
+        ex[j] = L.pk[i].w * L.noise[i + nidx_spare];
+      } else {
+        const float4 q = L.pk[i];
+        r[j].f0 = q.x;
+        hs[j] = q.y;
+        cf[j] = q.z;
+        ex[j] = q.w * L.noise[i + nidx_spare];
+      }
       w[j] = L.wt[i];
-      hs[j] = L.hs[i];
-      cf[j] = L.coef[i];
-      ex[j] = L.dfl[i] * L.noise[i + nidx_spare];
     }
 #pragma unroll
     for (int j = 0; j < kBlk; ++j) {
@@ -799,7 +808,7 @@ __device__ __forceinline__ void bwd_harmonic_pass(const SynthArgs& a, const SegL
       float sv = sin2pi(p);
       asm volatile("" : "+v"(sv));
       const float hm = (sv - hs[j]) * cf[j];
-      const float dm = harm ? (freq < nyq ? hm : 0.0f) : ex[j];
+      const float dm = harm ? (MASKC || freq < nyq ? hm : 0.0f) : ex[j];
       slot_acc<NS>(acc, r[j], w[j], dm);
     }
   }
@@ -819,7 +828,7 @@ __device__ __forceinline__ void bwd_gain_pass(const SegLds& L, float (&acc)[kSlo
       const int i = i0 + j;
       if constexpr (NS == 0) r[j] = L.fr[i];
       w[j] = L.wt[i];
-      ex[j] = q == 0 ? L.dg[i] : (q == 1 ? L.dng[i] : L.dfl[i] * L.noise[i + nidx]);
+      ex[j] = q == 0 ? L.dg[i] : (q == 1 ? L.dng[i] : L.pk[i].w * L.noise[i + nidx]);
     }
 #pragma unroll
     for (int j = 0; j < kBlk; ++j) {
@@ -869,11 +878,9 @@ __global__ __launch_bounds__(64 * kWavesBwd) void k_synth_bwd(SynthArgs a, const
       dng = ((g * filt) * 0.12f) * a.nscale;
       dfl = ((g * ngain) * 0.12f) * a.nscale;
     }
-    L.hs[lane] = hs;
-    L.coef[lane] = coef;
+    L.pk[lane] = make_float4(L.fr[lane].f0, hs, coef, dfl);
     L.dg[lane] = dg;
     L.dng[lane] = dng;
-    L.dfl[lane] = dfl;
     constexpr float kBig = 0x1p50f;
     bnd = fabsf(hs) < kBig && fabsf(coef) < kBig && fabsf(dg) < kBig && fabsf(dng) < kBig && fabsf(dfl) < kBig;
     for (int i = lane; i < a.NF - 1 + kSeg; i += 64) bnd = bnd && fabsf(L.noise[i]) < kBig;
@@ -889,7 +896,29 @@ __global__ __launch_bounds__(64 * kWavesBwd) void k_synth_bwd(SynthArgs a, const
     const int nidx = lane < a.K ? 0 : c - a.K - 2;
     const float ph = a.ckpt[((size_t)s * a.B + b) * a.K + (lane < a.K ? lane : 0)];
     float acc[kSlots] = {0.f, 0.f, 0.f, 0.f};
-    if (fast && ns == 2)
+    // Nyquist mask of harmonic lane k over the segment: freq = RN((k+1) f0)
+    // is monotone in f0, so the frames' extreme f0 decide whether every
+    // frame is below (on) or none is (off); a lane between the two needs
+    // the per-frame test
+    bool mixed = false, off = false;
+    if (fast) {
+      float lo = L.fr[lane].f0, hi = lo;
+#pragma unroll
+      for (int d = 32; d > 0; d >>= 1) {
+        lo = fminf(lo, __shfl_xor(lo, d, 64));
+        hi = fmaxf(hi, __shfl_xor(hi, d, 64));
+      }
+      const float kf = (float)(lane + 1);
+      const bool on = kf * hi < a.nyq;
+      off = !(kf * lo < a.nyq);
+      mixed = lane < a.K && !on && !off;
+    }
+    const bool maskc = !__any(mixed);
+    if (fast && ns == 2 && maskc)
+      bwd_harmonic_pass<true, 2, true>(a, L, acc, lane, nt, ph, nidx);
+    else if (fast && ns == kSlots && maskc)
+      bwd_harmonic_pass<true, kSlots, true>(a, L, acc, lane, nt, ph, nidx);
+    else if (fast && ns == 2)
       bwd_harmonic_pass<true, 2>(a, L, acc, lane, nt, ph, nidx);
     else if (fast && ns == kSlots)
       bwd_harmonic_pass<true, kSlots>(a, L, acc, lane, nt, ph, nidx);
@@ -897,6 +926,11 @@ __global__ __launch_bounds__(64 * kWavesBwd) void k_synth_bwd(SynthArgs a, const
       bwd_harmonic_pass<true, 0>(a, L, acc, lane, nt, ph, nidx);
     else
       bwd_harmonic_pass<false, 0>(a, L, acc, lane, nt, ph, nidx);
+    if (fast && ns != 0 && maskc && lane < a.K && off) {
+      // masked in every frame: the per-frame form adds only zeros
+#pragma unroll
+      for (int j = 0; j < kSlots; ++j) acc[j] = 0.0f;
+    }
     if (c < NC) store_slots(acc, out, a.ldc, c);
   }
   {
