@@ -571,9 +571,13 @@ __device__ __forceinline__ void slot_acc(float (&acc)[kSlots], const FrameRec& r
 // and frames >= nt).  The phase steps are those of the reference's stateful
 // phasor (pre-increment output, wrap), the backward's pass repeats them bit
 // for bit.  rv = this lane's amplitude column in each row slot.
-template <bool FAST, int NS>
+// MASKC: no harmonic crosses the Nyquist limit inside the segment and the
+// caller has zeroed rv of the lanes masked throughout (and of lanes >= K),
+// so no frame tests the mask: those lanes add sin * 0.
+template <bool FAST, int NS, bool MASKC = false>
 __device__ __forceinline__ void chain_regs(const SynthArgs& a, const SegLds& L, float (&v)[kSeg], int lane, int nt,
                                            float ph, const float (&rv)[kSlots]) {
+  static_assert(!MASKC || (FAST && NS != 0), "the constant mask is a fast slot-weight form");
   const float kf = (float)(lane + 1);
   const float nyq = a.nyq;
   const bool harm = lane < a.K;
@@ -619,7 +623,7 @@ __device__ __forceinline__ void chain_regs(const SynthArgs& a, const SegLds& L, 
         amp = r[j].omf * al[j] + r[j].frac * ah[j];
       else
         amp = slot_lerp<NS>(w[j], rv);
-      v[i] = (harm && freq < nyq) ? sin2pi(p) * amp : 0.0f;
+      v[i] = MASKC ? sin2pi(p) * amp : ((harm && freq < nyq) ? sin2pi(p) * amp : 0.0f);
     }
   }
 }
@@ -704,7 +708,33 @@ __global__ __launch_bounds__(64 * kWavesFwd) void k_synth_fwd(SynthArgs a, float
     // slot weights need finite rows and two distinct rows per frame; else
     // the exact per-frame form
     const int ns = !(__all(fin) && pairs) ? 0 : (nslot <= 2 ? 2 : kSlots);
-    if (fast && ns == 2)
+    // Nyquist mask of lane k over the segment, from the frames' extreme f0
+    // (RN((k+1) f0) is monotone in f0): on in every frame, off in every
+    // frame, or mixed (the per-frame test)
+    bool mixed = false, zero = lane >= a.K;
+    if (fast && ns != 0) {
+      float lo = L.fr[lane].f0, hi = lo;
+#pragma unroll
+      for (int d = 32; d > 0; d >>= 1) {
+        lo = fminf(lo, __shfl_xor(lo, d, 64));
+        hi = fmaxf(hi, __shfl_xor(hi, d, 64));
+      }
+      const float kf = (float)(lane + 1);
+      const bool on = kf * hi < a.nyq, off = !(kf * lo < a.nyq);
+      mixed = lane < a.K && !on && !off;
+      zero = zero || off;
+    }
+    if (fast && ns != 0 && !__any(mixed)) {
+      // finite rows (ns != 0): a zeroed lane adds sin * 0 = +-0, which leaves
+      // every frame's sum as the per-frame form's
+      float rz[kSlots];
+#pragma unroll
+      for (int j = 0; j < kSlots; ++j) rz[j] = zero ? 0.0f : rv[j];
+      if (ns == 2)
+        chain_regs<true, 2, true>(a, L, v, lane, nt, ph, rz);
+      else
+        chain_regs<true, kSlots, true>(a, L, v, lane, nt, ph, rz);
+    } else if (fast && ns == 2)
       chain_regs<true, 2>(a, L, v, lane, nt, ph, rv);
     else if (fast && ns == kSlots)
       chain_regs<true, kSlots>(a, L, v, lane, nt, ph, rv);
