@@ -38,6 +38,8 @@
 // envelope are per-frame signals shared by all lanes ([T], optional).
 #pragma clang fp contract(off)
 
+#include <type_traits>
+
 #include "dev_math.h"
 #include "internal.h"
 
@@ -314,6 +316,106 @@ __global__ __launch_bounds__(kSeqThreads) void k_svf_seq(const float* __restrict
   }
 }
 
+// The saturating forward of a training step, staged through LDS.  Each
+// wave's 64 lanes step 32-frame tiles: a tile's x, target and coefficient
+// rows arrive by 16-byte load-to-LDS copies issued one tile ahead (each
+// instruction brings four frames of the wave's 64 lanes), the frame loop
+// reads and writes only LDS, and the tile's cells and y leave as 16-byte
+// stores.  Per frame the wave issues a fraction of one global memory
+// instruction instead of six, so the loop is bound by its own dependent
+// chain instead of by outstanding memory operations.  The arithmetic is
+// k_svf_seq's (tape coefficients, the saturating step, loss partials per
+// L frames), so the results are the same bit for bit.  Needs B a multiple
+// of 64 and T and L multiples of 32.
+constexpr int kTileF = 32;
+__global__ __launch_bounds__(64) void k_svf_seq_tiled(const float* __restrict__ x, const float* __restrict__ prm,
+                                                      const float* __restrict__ tape, float* __restrict__ state,
+                                                      float* __restrict__ y, float* __restrict__ cells,
+                                                      const float* __restrict__ tgt, float* __restrict__ lossp, int B,
+                                                      int T, int L, int sanitize) {
+  // inputs, double buffered: [array: x, target, g][frame][lane]; outputs
+  // [array: c1, c2, y][frame][lane].  (Reading a1 and a2 from two more tape
+  // planes instead of computing them from g measured no faster: the loop is
+  // bound by the latency of its ~23 dependent operations per frame.)
+  constexpr int NI = 3;
+  __shared__ __align__(16) float in0[NI][kTileF][64];
+  __shared__ __align__(16) float in1[NI][kTileF][64];
+  __shared__ __align__(16) float out[3][kTileF][64];
+  const int lane = threadIdx.x, k0 = blockIdx.x * 64, k = k0 + lane;
+  const float kd = 1.0f / prm[B + k], ks = prm[2 * B + k];
+  float c1 = 0.0f, c2 = 0.0f;
+  if (state) {
+    c1 = state[k];
+    c2 = state[B + k];
+  }
+  const size_t plane = (size_t)T * B;
+  // lane l copies/stores frame 4i + l/16 of an instruction's four, lanes
+  // k0 + 4(l%16) .. +3 of it
+  const int fq = lane >> 4, kq = k0 + 4 * (lane & 15);
+  const float* const srcs[NI] = {x, tgt, tape};
+  // (the buffers are named, not passed by reference: a generic pointer to
+  // them here made the compiler emit an illegal aperture compare)
+  auto issue = [&](auto bi, int n0) {
+#pragma unroll
+    for (int a = 0; a < NI; ++a)
+#pragma unroll
+      for (int i = 0; i < kTileF / 4; ++i) {
+        const void* src = srcs[a] + (size_t)(n0 + 4 * i + fq) * B + kq;
+        if constexpr (decltype(bi)::value == 0)
+          __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)&in0[a][4 * i][0], 16, 0, 0);
+        else
+          __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)&in1[a][4 * i][0], 16, 0, 0);
+      }
+  };
+  float ls = 0.0f;
+  auto tile = [&](const float (&buf)[NI][kTileF][64], int n0) {
+#pragma unroll 4
+    for (int f = 0; f < kTileF; ++f) {
+      SvfK K;
+      K.g = buf[2][f][lane];
+      K.Q = 1.0f + K.g * (K.g + kd);
+      K.a1 = rcp_rn(K.Q);
+      K.a2 = K.g * K.a1;
+      out[0][f][lane] = c1;
+      out[1][f][lane] = c2;
+      const float o = svf_step<true>(K, ks, buf[0][f][lane], c1, c2);
+      out[2][f][lane] = sanitize && !isfinite(o) ? 0.0f : o;
+      const float d = o - buf[1][f][lane];
+      ls += d * d;
+    }
+    // the wave's own LDS writes land before its reads below (in order)
+    wave_sync();
+    float* const dsts[3] = {cells, cells + plane, y};
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
+#pragma unroll
+      for (int i = 0; i < kTileF / 4; ++i) {
+        const float4 v = *reinterpret_cast<const float4*>(&out[a][4 * i + fq][4 * (lane & 15)]);
+        *reinterpret_cast<float4*>(dsts[a] + (size_t)(n0 + 4 * i + fq) * B + kq) = v;
+      }
+    if ((n0 + kTileF) % L == 0) {
+      lossp[(size_t)((n0 + kTileF) / L - 1) * B + k] = ls;
+      ls = 0.0f;
+    }
+  };
+  const int ntile = T / kTileF;
+  const std::integral_constant<int, 0> b0;
+  const std::integral_constant<int, 1> b1;
+  issue(b0, 0);
+  for (int t = 0; t < ntile; t += 2) {
+    // tile t from in0 (its copies landed), tile t+1's copies into in1
+    if (t + 1 < ntile) issue(b1, (t + 1) * kTileF);
+    tile(in0, t * kTileF);
+    if (t + 1 >= ntile) break;
+    if (t + 2 < ntile) issue(b0, (t + 2) * kTileF);
+    tile(in1, (t + 1) * kTileF);
+  }
+  if (state) {
+    state[k] = c1;
+    state[B + k] = c2;
+  }
+}
+
 // ------------------------------------------------------------ adjoint scan
 // d s / d c for s = c / (1 + |ks c|): 1/D - (c/D^2) sgn(ks c) ks (1 when linear).
 __device__ __forceinline__ float sgn(float v) { return v > 0.0f ? 1.0f : (v < 0.0f ? -1.0f : 0.0f); }
@@ -574,6 +676,13 @@ int launch_svf_seq(const Launch& L, const dgen_hip_op& op) {
   }
   float* tg = tgt >= 0 ? cell(L, tgt) : nullptr;
   float* lp = lossp >= 0 ? cell(L, lossp) : nullptr;
+  if (tgt >= 0 && tp && cp && !stream && s.B % 64 == 0 && T % kTileF == 0 && s.L % kTileF == 0) {
+    // the training forward through LDS tiles (the same arithmetic)
+    hipLaunchKernelGGL(k_svf_seq_tiled, dim3((unsigned)(s.B / 64)), dim3(64), 0, L.stream, cell(L, x), cell(L, prm),
+                       tp, sp, cell(L, y), cp, tg, lp, (int)s.B, (int)T, (int)s.L, san);
+    DGEN_LAUNCH_CHECK("k_svf_seq_tiled");
+    return 0;
+  }
   auto go = [&](auto kern) {
     hipLaunchKernelGGL(kern, grid, dim3(kSeqThreads), 0, L.stream, cell(L, x), ctl, cell(L, prm), tp, sp, reset,
                        cell(L, y), cp, tg, lp, (int)s.B, (int)T, (int)s.L, sr, san);

@@ -343,7 +343,9 @@ enum dgen_hip_kernel {
    *      [6]=cells or -1 [7]=target or -1 [8]=loss partials or -1 [9]=B
    *      [10]=T [11]=L [12]=sanitize (non-finite out stores -> 0)
    *      [13]=coefficient tape ([T][B]: g, filled by the call before the
-   *      sequential loop reads it) or -1 (evaluated in the loop) */
+   *      sequential loop reads it) or -1 (evaluated in the loop)
+   * With a target, cells and a tape, B a multiple of 64 and T and L of 32,
+   * the loop runs on 32-frame LDS tiles (the same results). */
   DGEN_HIP_K_SVF_SEQ = 35,
 
   /* BPTT part 1: per (lane, chunk), reverse, the cells' adjoint from a zero

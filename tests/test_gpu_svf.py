@@ -117,3 +117,29 @@ def test_streaming_calls_carry_the_cells():
     print(f"stream: max|y - fp32 oracle| {np.abs(one - ref).max():.3e}, HIP vs fp64 {np.abs(one - ref64).max():.3e}, "
           f"fp32 oracle vs fp64 {np.abs(ref - ref64).max():.3e}")
     assert np.abs(one - ref64).max() <= 2.0 * np.abs(ref - ref64).max() + 1e-6
+
+
+def test_training_forward_through_lds_tiles_equals_the_per_frame_kernel():
+    """The saturating training forward (the LDS-tiled lane loop: 32-frame
+    tiles by 16-byte copies) and the streaming kernel (per-frame loads and
+    stores, coefficients evaluated in the loop) give the same y bit for bit
+    on the same input and parameters."""
+    cfg = SvfConfig(B=128, T=1 << 14, saturating=True)
+    s = SvfSession(cfg, optimizer=False)
+    try:
+        s.step()
+        y = s.rt.read("y").reshape(cfg.T, cfg.B)
+        labels = [op.label for op in s.program.ops]
+    finally:
+        s.close()
+    prog = stream_svf_program(cfg)
+    x, m, env = cfg.inputs(), cfg.modulation(), cfg.envelope()
+    rt = HIPLazyRuntime(prog, 0)
+    try:
+        rt.write("params", cfg.params())
+        rt.setProcessPorts(*prog.meta["ports"])
+        one = rt.process([x[:, k] for k in range(cfg.B)] + [m, env], cfg.T, reset=True).T
+    finally:
+        rt.close()
+    assert "svf_seq" in labels
+    np.testing.assert_array_equal(y, one)
