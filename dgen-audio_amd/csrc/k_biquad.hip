@@ -24,8 +24,9 @@
 // The adjoint lambda[n] = g[n] - a1[n+1] lambda[n+1] - a2[n+2] lambda[n+2],
 // g = 2 (y - tgt), is the same kind of recurrence run backwards, with the
 // carries (v1, v2) = what is owed to lambda[n-1] and lambda[n-2]:
-//   k_bq_adj_chunk, k_bq_carry (reverse), k_bq_bwd -> per-chunk gradient
-//   partials [C][2][B], summed per lane by the deterministic column sum.
+//   chunk summaries (k_bq_adj_chunk, or formed by k_bq_fwd's replay),
+//   k_bq_carry (reverse), k_bq_bwd -> per-chunk gradient partials [C][2][B],
+//   summed per lane by the deterministic column sum.
 //
 // Layout: x, y, tgt are [T][B] (frame-major, lane-minor: a wave reads 256
 // contiguous bytes per frame); parameters are [2][B] = base | Q; the cutoff
@@ -292,11 +293,23 @@ __global__ __launch_bounds__(kCarryLanes* kCarryGroups) void k_bq_carry(const do
   }
 }
 
-template <bool MOD, bool LOSS>
+// ADJ (with LOSS): the chunk's adjoint summary as well, the map that
+// k_bq_adj_chunk forms by running the chunk backwards, accumulated forwards
+// here from the values the replay has in hand.  Per frame the adjoint state
+// (v1, v2) goes to A_n (v1, v2) + b_n g_n with A_n = [[-a1, 1], [-a2, 0]],
+// b_n = (-a1, -a2) and g_n = 2 (y_n - tgt_n), so over the chunk (frames
+// n0..n1-1, taken from n1-1 down) the state leaving is M (v1, v2) + z with
+// M = A_n0 A_n0+1 ... A_n1-1 and z = sum_n P_n b_n g_n, P_n = A_n0 ... A_n-1:
+// both are prefix products, and P_n b_n is the first column of P_n+1.  The
+// summary [6][B] per chunk is (z, M e1, M e2) in fp64, as k_bq_adj_chunk's
+// (v, u, w), so the separate backward pass over y and the target is not run.
+template <bool MOD, bool LOSS, bool ADJ = false>
 __global__ __launch_bounds__(kThreads) void k_bq_fwd(const float* __restrict__ x, const float* __restrict__ mod,
                                                      const float* __restrict__ prm, const float* __restrict__ init,
                                                      float* __restrict__ y, const float* __restrict__ tgt,
-                                                     float* __restrict__ lossp, int B, int T, int L) {
+                                                     float* __restrict__ lossp, int B, int T, int L,
+                                                     double* __restrict__ asumm) {
+  static_assert(!ADJ || LOSS, "the adjoint summary needs the target");
   LaneChunk lc;
   if (!lane_chunk(prm, B, T, L, lc)) return;
   const int k = lc.k;
@@ -304,6 +317,8 @@ __global__ __launch_bounds__(kThreads) void k_bq_fwd(const float* __restrict__ x
   float x1 = lc.n0 >= 1 ? x[(size_t)(lc.n0 - 1) * B + k] : 0.0f;
   float x2 = lc.n0 >= 2 ? x[(size_t)(lc.n0 - 2) * B + k] : 0.0f;
   float ls = 0.0f;
+  // adjoint prefix product P = [[p11, p12], [p21, p22]] and sum z
+  double p11 = 1.0, p12 = 0.0, p21 = 0.0, p22 = 1.0, z1 = 0.0, z2 = 0.0;
   auto step = [&](int n, const float* v, float m) {
     const Coef K = coef(lc.base * m, lc.q, lc.rq);
     const float x0 = v[0];
@@ -312,6 +327,17 @@ __global__ __launch_bounds__(kThreads) void k_bq_fwd(const float* __restrict__ x
     if constexpr (LOSS) {
       const float d = out - v[1];
       ls += d * d;
+    }
+    if constexpr (ADJ) {
+      const double a1 = K.a1, a2 = K.a2;
+      const double g = 2.0 * ((double)out - (double)v[1]);
+      const double q1 = -a1 * p11 - a2 * p12, q2 = -a1 * p21 - a2 * p22;
+      p12 = p11;
+      p22 = p21;
+      p11 = q1;
+      p21 = q2;
+      z1 += g * q1;
+      z2 += g * q2;
     }
     y2 = y1;
     y1 = out;
@@ -322,6 +348,15 @@ __global__ __launch_bounds__(kThreads) void k_bq_fwd(const float* __restrict__ x
     const float* const src[2] = {x, tgt};
     walk_fwd<2, MOD>(src, mod, B, k, lc.n0, lc.n1, step);
     lossp[(size_t)lc.c * B + k] = ls;
+    if constexpr (ADJ) {
+      double* o = asumm + (size_t)lc.c * 6 * B + k;
+      o[0] = z1;
+      o[(size_t)B] = z2;
+      o[(size_t)2 * B] = p11;
+      o[(size_t)3 * B] = p21;
+      o[(size_t)4 * B] = p12;
+      o[(size_t)5 * B] = p22;
+    }
   } else {
     const float* const src[1] = {x};
     walk_fwd<1, MOD>(src, mod, B, k, lc.n0, lc.n1, step);
@@ -449,12 +484,14 @@ void bq_enqueue_carry(hipStream_t st, const double* summ, float* init, int64_t B
                      dim3(kCarryLanes * kCarryGroups), 0, st, summ, init, (int)B, (int)C, rev);
 }
 void bq_enqueue_fwd(hipStream_t st, const float* x, const float* m, const float* prm, const float* init, float* y,
-                    const float* t, float* lp, const BqShape& s) {
+                    const float* t, float* lp, const BqShape& s, double* asumm = nullptr) {
   auto go = [&](auto kern) {
     hipLaunchKernelGGL(kern, bq_grid(s), dim3(kThreads), 0, st, x, m, prm, init, y, t, lp, (int)s.B, (int)s.T,
-                       (int)s.L);
+                       (int)s.L, asumm);
   };
-  if (m && t) go(k_bq_fwd<true, true>);
+  if (m && t && asumm) go(k_bq_fwd<true, true, true>);
+  else if (t && asumm) go(k_bq_fwd<false, true, true>);
+  else if (m && t) go(k_bq_fwd<true, true>);
   else if (m) go(k_bq_fwd<true, false>);
   else if (t) go(k_bq_fwd<false, true>);
   else go(k_bq_fwd<false, false>);
@@ -505,9 +542,20 @@ int launch_biquad_fwd(const Launch& L, const dgen_hip_op& op) {
     DGEN_CHECK_CELL(L, tgt, s.B * s.T, "biquad_fwd.target");
     DGEN_CHECK_CELL(L, lossp, s.C * s.B, "biquad_fwd.loss_partials");
   }
+  // arg[11] = 1: the adjoint chunk summaries too, into arg[10]
+  const bool adj = op.arg[11] == 1;
+  const int64_t asumm = op.arg[10];
+  DGEN_REQUIRE(op.arg[11] == 0 || adj, "biquad_fwd: arg[11] %lld (0, or 1 with adjoint summaries)",
+               (long long)op.arg[11]);
+  if (adj) {
+    DGEN_REQUIRE(tgt >= 0, "biquad_fwd: adjoint summaries need the target");
+    DGEN_REQUIRE(asumm % 2 == 0, "biquad_fwd: summary cell must be 8-byte aligned");
+    DGEN_CHECK_CELL(L, asumm, 12 * s.C * s.B, "biquad_fwd.adjoint_summary");
+  }
   if (L.dry) return 0;
   bq_enqueue_fwd(L.stream, cell(L, x), mod >= 0 ? cell(L, mod) : nullptr, cell(L, prm), cell(L, init), cell(L, y),
-                 tgt >= 0 ? cell(L, tgt) : nullptr, lossp >= 0 ? cell(L, lossp) : nullptr, s);
+                 tgt >= 0 ? cell(L, tgt) : nullptr, lossp >= 0 ? cell(L, lossp) : nullptr, s,
+                 adj ? dcell(L, asumm) : nullptr);
   DGEN_LAUNCH_CHECK("k_bq_fwd");
   return 0;
 }

@@ -414,14 +414,17 @@ def _colsum_ws(rows: int, cols: int) -> int:
 
 
 def biquad_program(cfg: BiquadConfig, train: bool = True, optimizer: bool = True, modulated: bool = True,
-                   chunk: int = BQ_CHUNK) -> Program:
+                   chunk: int = BQ_CHUNK, fuse_adjoint: bool = True) -> Program:
     """Tensor biquad bank: x -> RBJ low-pass with cutoff base[k]*mod[n] and Q[k].
 
     ``train=False`` builds the forward render only (used for the fixed target
     bank, ``modulated=False``).  With ``train=True``: forward, loss
     sum (y - target)^2, BPTT to (base, Q), and (``optimizer``) one Adam step.
     Each recurrence runs as a chunked scan (chunk summaries, per-lane carry
-    composition, replay) forward and, for the adjoint, backward."""
+    composition, replay) forward and, for the adjoint, backward.  With
+    ``fuse_adjoint`` the forward replay also forms the adjoint's chunk
+    summaries; without it a separate reverse pass over y and the target
+    does."""
     B, T, L = cfg.B, cfg.T, int(chunk)
     if L <= 0:
         raise ValueError("chunk length must be positive")
@@ -458,16 +461,20 @@ def biquad_program(cfg: BiquadConfig, train: bool = True, optimizer: bool = True
     gpart = p.alloc("grad_partials", 2 * C * B)
     G = p.alloc("grads", 2 * B)
     ws = p.alloc("colsum_ws", max(_colsum_ws(C, 2 * B), _colsum_ws(C, B), _colsum_ws(B, 1)))
-    p.add(R.K_BIQUAD_FWD, [x, mod, P, init, y, B, T, L, tgt, lossp], label="bq_fwd",
-          dispatch="chunk replay + loss partials", bytes=3 * n * f4 + mod_b + 3.0 * C * B * f4,
-          flops=n * (16 + 9 + 3))
+    # fused: the replay also forms the adjoint chunk summaries (forward
+    # prefix products), so no separate backward pass over y and the target
+    p.add(R.K_BIQUAD_FWD, [x, mod, P, init, y, B, T, L, tgt, lossp] + ([asumm, 1] if fuse_adjoint else []),
+          label="bq_fwd", dispatch="chunk replay + loss partials" + (" + adjoint summaries" if fuse_adjoint else ""),
+          bytes=3 * n * f4 + mod_b + 3.0 * C * B * f4 + (12.0 * C * B * f4 if fuse_adjoint else 0.0),
+          flops=n * (16 + 9 + 3 + (12 if fuse_adjoint else 0)))
     p.add(R.K_COLSUM, [lossp, lane_loss, C, B, B, ws], label="loss_lanes", dispatch="chunkPartialsReduceToCell",
           bytes=(C * B + B) * f4, flops=float(C * B))
     p.add(R.K_COLSUM, [lane_loss, loss, B, 1, 1, ws], label="loss_sum", dispatch="chunkPartialsReduceToCell",
           bytes=(B + 1) * f4, flops=float(B))
-    p.add(R.K_BIQUAD_ADJ_CHUNK, [mod, P, y, tgt, asumm, B, T, L], label="bq_adj_chunk",
-          dispatch=f"reverse chunk summaries {C}x{B}", bytes=2 * n * f4 + mod_b + 12.0 * C * B * f4,
-          flops=n * (16 + 3 * 6))
+    if not fuse_adjoint:
+        p.add(R.K_BIQUAD_ADJ_CHUNK, [mod, P, y, tgt, asumm, B, T, L], label="bq_adj_chunk",
+              dispatch=f"reverse chunk summaries {C}x{B}", bytes=2 * n * f4 + mod_b + 12.0 * C * B * f4,
+              flops=n * (16 + 3 * 6))
     p.add(R.K_BIQUAD_CARRY, [asumm, ainit, B, C, 1], label="bq_adj_carry", dispatch=f"reverse scan of {C} maps",
           bytes=(12.0 + 2.0) * C * B * f4, flops=24.0 * C * B)
     p.add(R.K_BIQUAD_BWD, [x, mod, P, y, tgt, ainit, gpart, B, T, L], label="bq_bwd",
@@ -511,7 +518,7 @@ class BiquadSession:
     every ``step()`` is forward + loss + BPTT (+ Adam) with all data in HBM."""
 
     def __init__(self, cfg: BiquadConfig, device: int = 0, optimizer: bool = True, chunk: int = BQ_CHUNK,
-                 target=None):
+                 target=None, fuse_adjoint: bool = True):
         self.cfg = cfg
         self.x = cfg.inputs()
         self.mod = cfg.modulation()
@@ -519,7 +526,7 @@ class BiquadSession:
         if target is None:
             target = self.render(cfg.target_params(), device, modulated=False, chunk=chunk)
         self.target = np.ascontiguousarray(target, np.float32).reshape(cfg.T, cfg.B)
-        self.program = biquad_program(cfg, train=True, optimizer=optimizer, chunk=chunk)
+        self.program = biquad_program(cfg, train=True, optimizer=optimizer, chunk=chunk, fuse_adjoint=fuse_adjoint)
         self.rt = R.HIPLazyRuntime(self.program, device)
         self.rt.write("x", self.x)
         self.rt.write("mod", self.mod)

@@ -213,7 +213,10 @@ enum dgen_hip_kernel {
   /* Forward part 2: each chunk re-run from its initial state; writes y and,
    * when a target is given, per-chunk partial sums of (y - target)^2.
    * arg: [0]=x [1]=mod [2]=params [3]=init [4]=y [5]=B [6]=T [7]=L
-   *      [8]=target or -1 [9]=loss partials [C][B] (with a target) or -1 */
+   *      [8]=target or -1 [9]=loss partials [C][B] (with a target) or -1
+   *      [10]=adjoint summary cell when [11]=1 (with a target): the chunk
+   *      summaries DGEN_HIP_K_BIQUAD_ADJ_CHUNK would write, accumulated
+   *      forwards during the replay (that op is then not needed) */
   DGEN_HIP_K_BIQUAD_FWD = 22,
 
   /* BPTT part 1 (BPTTEmission.swift:133-160): per (lane, chunk), the reverse

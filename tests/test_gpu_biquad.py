@@ -86,6 +86,30 @@ def test_loss_and_gradient_match_oracle(gpu):
     np.testing.assert_array_equal(g, g2)
 
 
+@pytest.mark.parametrize("B,T,chunk", [(6, 3000, 128), (70, 2000, 7), (64, 4097, 64)])
+def test_fused_adjoint_summaries_equal_the_reverse_pass(gpu, B, T, chunk):
+    """The forward replay's prefix-product adjoint summaries and the
+    separate reverse pass compose the same affine chunk maps: equal to fp64
+    rounding, and the gradients equal to fp32 rounding."""
+    cfg = BiquadConfig(B=B, T=T)
+    print(f"case B={B} T={T} chunk={chunk}", flush=True)
+    target = O.biquad_fwd(cfg.inputs(), None, cfg.target_params()[:B], cfg.target_params()[B:], prec="f32")
+    out = {}
+    for fused in (True, False):
+        s = BiquadSession(cfg, optimizer=False, chunk=chunk, target=target, fuse_adjoint=fused)
+        try:
+            s.step()
+            out[fused] = (s.rt.read("adj_summary").view(np.float64), s.rt.read("grads"), s.loss())
+        finally:
+            s.close()
+    (a1, g1, l1), (a0, g0, l0) = out[True], out[False]
+    assert abs(l1 - l0) <= 1e-6 * abs(l0)
+    scale = np.abs(a0).max()
+    print(f"summary max diff {np.abs(a1 - a0).max():.3e} (scale {scale:.3e})")
+    np.testing.assert_allclose(a1, a0, rtol=0, atol=1e-12 * scale)
+    np.testing.assert_allclose(g1, g0, rtol=1e-5, atol=1e-6 * np.abs(g0).max())
+
+
 def test_gradient_matches_finite_differences(gpu):
     """within 1e-2 relative of central differences of the
     fp64 oracle forward, per parameter and along the gradient."""
