@@ -25,7 +25,8 @@
 // of the cells IS affine in both cases (its Jacobians read the stored
 // cells), so the backward is always chunked:
 //   k_svf_adj_chunk  per (lane, chunk), reverse: zero-carry adjoint and unit
-//                    responses (fp64), then the carry kernel in reverse
+//                    responses (fp64; for the linear bank k_svf_fwd can form
+//                    them instead), then the carry kernel in reverse
 //   k_svf_bwd        each chunk's adjoint replayed in fp32 from its carry,
 //                    chained through the coefficient nodes to per-chunk
 //                    gradient partials [C][P][B] (base, res[, kSat]) and
@@ -202,17 +203,27 @@ __global__ __launch_bounds__(kThreads) void k_svf_chunk(const float* __restrict_
   o[(size_t)5 * B] = w2;
 }
 
-template <bool LOSS>
+// ADJ (with LOSS): the chunk's adjoint summary as well, the map that
+// k_svf_adj_chunk<false> forms running backwards, accumulated forwards here.
+// With kSat = 0 one frame takes the cells' adjoint (l1, l2) to A_n (l1, l2)
+// + b_n e_n, e_n = 2 (y_n - tgt_n), where (from the reverse of svf_step)
+// A_n = [[2 a1 - 1, 2 a1 g], [-2 a2, 1 - 2 a2 g]] and b_n = (a1 g, 1 - a2 g).
+// Over frames n0..n1-1 (taken from n1-1 down) the state leaving is M l + z
+// with M = A_n0 ... A_n1-1 and z = sum_n P_n b_n e_n, P_n = A_n0 ... A_n-1:
+// prefix products, carried in fp64.  Summary [6][B] = (z, M e1, M e2).
+template <bool LOSS, bool ADJ = false>
 __global__ __launch_bounds__(kThreads) void k_svf_fwd(const float* __restrict__ x, Ctl ctl,
                                                       const float* __restrict__ prm, const float* __restrict__ init,
                                                       float* __restrict__ y, float* __restrict__ cells,
                                                       const float* __restrict__ tgt, float* __restrict__ lossp, int B,
-                                                      int T, int L, float sr) {
+                                                      int T, int L, float sr, double* __restrict__ asumm) {
+  static_assert(!ADJ || LOSS, "the adjoint summary needs the target");
   Lane l;
   if (!lane_chunk(prm, B, T, L, sr, false, l)) return;
   const int k = l.k;
   float c1 = init[(size_t)l.c * 2 * B + k], c2 = init[((size_t)l.c * 2 + 1) * B + k];
   float ls = 0.0f;
+  double p11 = 1.0, p12 = 0.0, p21 = 0.0, p22 = 1.0, z1 = 0.0, z2 = 0.0;
   const size_t plane = (size_t)T * B;
   auto step = [&](int n, const float* v, float m, float e) {
     const SvfK K = svf_coef(raw_cutoff(l.base, m, e, ctl), l.kd, sr, l.rsr);
@@ -227,11 +238,34 @@ __global__ __launch_bounds__(kThreads) void k_svf_fwd(const float* __restrict__ 
       const float d = out - v[1];
       ls += d * d;
     }
+    if constexpr (ADJ) {
+      const double a1 = K.a1, a2 = K.a2, g = K.g;
+      const double ee = 2.0 * ((double)out - (double)v[1]);
+      const double b1 = a1 * g, b2 = 1.0 - a2 * g;
+      z1 += ee * (p11 * b1 + p12 * b2);
+      z2 += ee * (p21 * b1 + p22 * b2);
+      const double A11 = 2.0 * a1 - 1.0, A12 = 2.0 * a1 * g, A21 = -2.0 * a2, A22 = 1.0 - 2.0 * a2 * g;
+      const double n11 = p11 * A11 + p12 * A21, n12 = p11 * A12 + p12 * A22;
+      const double n21 = p21 * A11 + p22 * A21, n22 = p21 * A12 + p22 * A22;
+      p11 = n11;
+      p12 = n12;
+      p21 = n21;
+      p22 = n22;
+    }
   };
   if constexpr (LOSS) {
     const float* const src[2] = {x, tgt};
     walk<2, false>(src, ctl, B, k, l.n0, l.n1, step);
     lossp[(size_t)l.c * B + k] = ls;
+    if constexpr (ADJ) {
+      double* o = asumm + (size_t)l.c * 6 * B + k;
+      o[0] = z1;
+      o[(size_t)B] = z2;
+      o[(size_t)2 * B] = p11;
+      o[(size_t)3 * B] = p21;
+      o[(size_t)4 * B] = p12;
+      o[(size_t)5 * B] = p22;
+    }
   } else {
     const float* const src[1] = {x};
     walk<1, false>(src, ctl, B, k, l.n0, l.n1, step);
@@ -603,6 +637,7 @@ int launch_svf_chunk(const Launch& L, const dgen_hip_op& op) {
 int launch_svf_fwd(const Launch& L, const dgen_hip_op& op) {
   // arg: [0]=x [1]=mod [2]=env [3]=params ([2][B]) [4]=init ([C][2][B]) [5]=y [6]=cells ([2][T][B]) or -1
   //      [7]=target or -1 [8]=loss partials ([C][B]) or -1 [9]=B [10]=T [11]=L
+  //      [12]=adjoint summary ([C][6][B] fp64) when [13]=1
   const int64_t x = op.arg[0], prm = op.arg[3], init = op.arg[4], y = op.arg[5], cl = op.arg[6], tgt = op.arg[7],
                 lossp = op.arg[8];
   SvfShape s;
@@ -621,14 +656,26 @@ int launch_svf_fwd(const Launch& L, const dgen_hip_op& op) {
     DGEN_CHECK_CELL(L, tgt, s.B * s.T, "svf_fwd.target");
     DGEN_CHECK_CELL(L, lossp, s.C * s.B, "svf_fwd.loss_partials");
   }
+  const bool adj = op.arg[13] == 1;
+  const int64_t asumm = op.arg[12];
+  if (adj) {
+    DGEN_REQUIRE(tgt >= 0, "svf_fwd: the adjoint summary needs the target");
+    DGEN_REQUIRE(asumm % 2 == 0, "svf_fwd: summary cell must be 8-byte aligned");
+    DGEN_CHECK_CELL(L, asumm, 12 * s.C * s.B, "svf_fwd.adjoint_summary");
+  }
   if (L.dry) return 0;
   float* cp = cl >= 0 ? cell(L, cl) : nullptr;
-  if (tgt >= 0)
+  if (adj)
+    hipLaunchKernelGGL((k_svf_fwd<true, true>), svf_grid(s), dim3(kThreads), 0, L.stream, cell(L, x), ctl,
+                       cell(L, prm), cell(L, init), cell(L, y), cp, cell(L, tgt), cell(L, lossp), (int)s.B, (int)s.T,
+                       (int)s.L, sr, dcell(L, asumm));
+  else if (tgt >= 0)
     hipLaunchKernelGGL(k_svf_fwd<true>, svf_grid(s), dim3(kThreads), 0, L.stream, cell(L, x), ctl, cell(L, prm),
-                       cell(L, init), cell(L, y), cp, cell(L, tgt), cell(L, lossp), (int)s.B, (int)s.T, (int)s.L, sr);
+                       cell(L, init), cell(L, y), cp, cell(L, tgt), cell(L, lossp), (int)s.B, (int)s.T, (int)s.L, sr,
+                       nullptr);
   else
     hipLaunchKernelGGL(k_svf_fwd<false>, svf_grid(s), dim3(kThreads), 0, L.stream, cell(L, x), ctl, cell(L, prm),
-                       cell(L, init), cell(L, y), cp, nullptr, nullptr, (int)s.B, (int)s.T, (int)s.L, sr);
+                       cell(L, init), cell(L, y), cp, nullptr, nullptr, (int)s.B, (int)s.T, (int)s.L, sr, nullptr);
   DGEN_LAUNCH_CHECK("k_svf_fwd");
   return 0;
 }

@@ -555,7 +555,7 @@ class BiquadSession:
 
 # ------------------------------------------------------ ZDF SVF bank (BPTT)
 def svf_program(cfg: SvfConfig, train: bool = True, optimizer: bool = True, saturating: bool | None = None,
-                chunk: int = SVF_CHUNK, xbar: bool = False) -> Program:
+                chunk: int = SVF_CHUNK, xbar: bool = False, fuse_adjoint: bool = True) -> Program:
     """ZDF SVF low-pass bank: x -> y with cutoff clip(base[k]*mod[n] + env[n])
     and res[k] (and, saturating, kSat[k]).
 
@@ -564,7 +564,10 @@ def svf_program(cfg: SvfConfig, train: bool = True, optimizer: bool = True, satu
     thread over all frames.  ``train=False`` renders y only.  With
     ``train=True``: forward storing the cells entering every frame, loss
     sum (y - target)^2, BPTT to the parameters as a chunked reverse scan
-    (``xbar``: also d loss / d x), and (``optimizer``) one Adam step."""
+    (``xbar``: also d loss / d x), and (``optimizer``) one Adam step.  With
+    ``fuse_adjoint`` (linear bank) the forward replay also forms the
+    adjoint's chunk summaries, else a separate reverse pass over y and the
+    target does."""
     sat = cfg.saturating if saturating is None else bool(saturating)
     B, T, L = cfg.B, cfg.T, int(chunk)
     if L <= 0:
@@ -585,6 +588,9 @@ def svf_program(cfg: SvfConfig, train: bool = True, optimizer: bool = True, satu
     cells = p.alloc("cells", 2 * T * B) if train else -1
     tgt = p.alloc("target", T * B) if train else -1
     lossp = p.alloc("loss_partials", C * B) if train else -1
+    asumm = p.alloc("adj_summary", 12 * C * B) if train else -1  # fp64
+    # linear: the forward replay forms the adjoint chunk summaries too
+    fused = train and fuse_adjoint and not sat
     # per lane-frame: coefficients (clip, div, tan, 1/Q, 4 mul/add) ~ 30 flops, one SVF frame 12
     if sat:
         tape = p.alloc("coef_tape", T * B)
@@ -599,15 +605,17 @@ def svf_program(cfg: SvfConfig, train: bool = True, optimizer: bool = True, satu
               flops=n * (30 + 3 * 10))
         p.add(R.K_BIQUAD_CARRY, [summ, init, B, C, 0], label="svf_carry", dispatch=f"per-lane scan of {C} chunk maps",
               bytes=(12.0 + 2.0) * C * B * f4, flops=24.0 * C * B)
-        p.add(R.K_SVF_FWD, [x, mod, env, prm, init, y, cells, tgt, lossp, B, T, L], sr, label="svf_fwd",
-              dispatch="chunk replay" + (" + cells + loss partials" if train else ""),
-              bytes=n * f4 * (5 if train else 2) + ctl_b + 2.0 * C * B * f4, flops=n * (30 + 12))
+        p.add(R.K_SVF_FWD, [x, mod, env, prm, init, y, cells, tgt, lossp, B, T, L] + ([asumm, 1] if fused else []),
+              sr, label="svf_fwd",
+              dispatch="chunk replay" + (" + cells + loss partials" if train else "")
+              + (" + adjoint summaries" if fused else ""),
+              bytes=n * f4 * (5 if train else 2) + ctl_b + 2.0 * C * B * f4 + (12.0 * C * B * f4 if fused else 0.0),
+              flops=n * (30 + 12 + (22 if fused else 0)))
     if not train:
         p.output_cell = "y"
         return p
     lane_loss = p.alloc("lane_loss", B)
     loss = p.alloc("loss", 1)
-    asumm = p.alloc("adj_summary", 12 * C * B)  # fp64
     ainit = p.alloc("adj_init", 2 * C * B)
     gpart = p.alloc("grad_partials", P * C * B)
     G = p.alloc("grads", P * B)
@@ -617,9 +625,10 @@ def svf_program(cfg: SvfConfig, train: bool = True, optimizer: bool = True, satu
           bytes=(C * B + B) * f4, flops=float(C * B))
     p.add(R.K_COLSUM, [lane_loss, loss, B, 1, 1, ws], label="loss_sum", dispatch="chunkPartialsReduceToCell",
           bytes=(B + 1) * f4, flops=float(B))
-    p.add(R.K_SVF_ADJ_CHUNK, [mod, env, prm, y, tgt, cells if sat else -1, asumm, B, T, L, int(sat)], sr,
-          label="svf_adj_chunk", dispatch=f"reverse chunk summaries {C}x{B}",
-          bytes=n * f4 * (4 if sat else 2) + ctl_b + 12.0 * C * B * f4, flops=n * (30 + 3 * 12))
+    if not fused:
+        p.add(R.K_SVF_ADJ_CHUNK, [mod, env, prm, y, tgt, cells if sat else -1, asumm, B, T, L, int(sat)], sr,
+              label="svf_adj_chunk", dispatch=f"reverse chunk summaries {C}x{B}",
+              bytes=n * f4 * (4 if sat else 2) + ctl_b + 12.0 * C * B * f4, flops=n * (30 + 3 * 12))
     p.add(R.K_BIQUAD_CARRY, [asumm, ainit, B, C, 1], label="svf_adj_carry", dispatch=f"reverse scan of {C} maps",
           bytes=(12.0 + 2.0) * C * B * f4, flops=24.0 * C * B)
     p.add(R.K_SVF_BWD, [x, mod, env, prm, y, tgt, cells, ainit, gpart, xb, B, T, L, int(sat)], sr, label="svf_bwd",
@@ -664,7 +673,7 @@ class SvfSession:
     forward + loss + BPTT (+ Adam) with all data in HBM."""
 
     def __init__(self, cfg: SvfConfig, device: int = 0, optimizer: bool = True, chunk: int = SVF_CHUNK,
-                 target=None, xbar: bool = False):
+                 target=None, xbar: bool = False, fuse_adjoint: bool = True):
         self.cfg = cfg
         self.x = cfg.inputs()
         self.mod = cfg.modulation()
@@ -673,7 +682,8 @@ class SvfSession:
         if target is None:
             target = self.render(cfg.target_params(), device, saturating=False, chunk=chunk)
         self.target = np.ascontiguousarray(target, np.float32).reshape(cfg.T, cfg.B)
-        self.program = svf_program(cfg, train=True, optimizer=optimizer, chunk=chunk, xbar=xbar)
+        self.program = svf_program(cfg, train=True, optimizer=optimizer, chunk=chunk, xbar=xbar,
+                                   fuse_adjoint=fuse_adjoint)
         self.rt = R.HIPLazyRuntime(self.program, device)
         for name, a in (("x", self.x), ("mod", self.mod), ("env", self.env), ("params", self.params0),
                         ("target", self.target)):

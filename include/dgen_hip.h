@@ -337,7 +337,10 @@ enum dgen_hip_kernel {
    * (or -1), per-chunk loss partials sum (y - target)^2 (with a target).
    * arg: [0]=x [1]=mod [2]=env [3]=params (P = 2) [4]=init ([C][2][B])
    *      [5]=y [6]=cells or -1 [7]=target or -1 [8]=loss partials ([C][B])
-   *      or -1 [9]=B [10]=T [11]=L */
+   *      or -1 [9]=B [10]=T [11]=L
+   *      [12]=adjoint summary cell when [13]=1 (with a target): the chunk
+   *      summaries DGEN_HIP_K_SVF_ADJ_CHUNK would write for the linear bank,
+   *      accumulated forwards during the replay (that op is then not needed) */
   DGEN_HIP_K_SVF_FWD = 34,
 
   /* Saturating forward (P = 3), one lane per thread over all frames (the

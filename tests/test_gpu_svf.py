@@ -69,6 +69,31 @@ def test_forward_loss_and_gradient_match_the_oracle(svf_run):
         assert eh <= 2.0 * eo + 1e-5
 
 
+@pytest.mark.parametrize("B,T,chunk", [(64, 4096, 256), (70, 3001, 7), (256, 1 << 18, 256)])
+def test_fused_adjoint_summaries_equal_the_reverse_pass(B, T, chunk):
+    """Linear bank: the forward replay's prefix-product adjoint summaries and
+    the separate reverse pass compose the same affine chunk maps: equal to
+    fp64 rounding, the gradients to fp32 rounding."""
+    cfg = SvfConfig(B=B, T=T, saturating=False)
+    print(f"case B={B} T={T} chunk={chunk}", flush=True)
+    target = None
+    out = {}
+    for fused in (True, False):
+        s = SvfSession(cfg, optimizer=False, chunk=chunk, target=target, fuse_adjoint=fused)
+        target = s.target
+        try:
+            s.step()
+            out[fused] = (s.rt.read("adj_summary").view(np.float64), s.rt.read("grads"), s.loss())
+        finally:
+            s.close()
+    (a1, g1, l1), (a0, g0, l0) = out[True], out[False]
+    assert abs(l1 - l0) <= 1e-6 * abs(l0)
+    scale = np.abs(a0).max()
+    print(f"summary max diff {np.abs(a1 - a0).max():.3e} (scale {scale:.3e})")
+    np.testing.assert_allclose(a1, a0, rtol=0, atol=1e-12 * scale)
+    np.testing.assert_allclose(g1, g0, rtol=1e-5, atol=1e-6 * np.abs(g0).max())
+
+
 def test_input_gradient_matches_the_oracle():
     for sat in (False, True):
         cfg = SvfConfig(B=64, T=1 << 14, saturating=sat)
