@@ -234,10 +234,11 @@ def biquad_cpu_baseline(cfg, repeats: int) -> dict:
 
 def run_biquad(args) -> dict:
     from dgen_hip import BiquadConfig
-    from dgen_hip.programs import BiquadSession
+    from dgen_hip.programs import BQ_CHUNK, BiquadSession
     cfg = BiquadConfig()
-    log(f"bench: biquad session B={cfg.B} T={cfg.T} chunk={args.chunk}")
-    sess = BiquadSession(cfg, device=0, optimizer=True, chunk=args.chunk)
+    chunk = args.chunk or BQ_CHUNK
+    log(f"bench: biquad session B={cfg.B} T={cfg.T} chunk={chunk}")
+    sess = BiquadSession(cfg, device=0, optimizer=True, chunk=chunk)
     if args.traffic_runs:
         try:
             traffic_run(sess, "biquad", args.traffic_runs)
@@ -261,7 +262,7 @@ def run_biquad(args) -> dict:
         "data": "synthetic (U[-1,1] SplitMix64 input per lane, 2 Hz geometric cutoff sweep)",
         "config": {"workload": "config 4: tensor biquad bank, RBJ low-pass with per-sample coefficients, MSE vs "
                                "fixed bank, BPTT to base cutoff and Q, Adam", "B": cfg.B, "T": cfg.T, "sr": cfg.sr,
-                   "chunk": args.chunk, "parallelism": "single GPU"},
+                   "chunk": chunk, "parallelism": "single GPU"},
     }
     out.update(roofline_fields(rows, dom, roof_ms, ms_per_step, "biquad"))
     out["loss"] = loss
@@ -304,11 +305,12 @@ def svf_cpu_baseline(cfg, lanes: int, repeats: int) -> dict:
 
 def run_svf(args, saturating: bool) -> dict:
     from dgen_hip import SvfConfig
-    from dgen_hip.programs import SvfSession
+    from dgen_hip.programs import SVF_CHUNK, SvfSession
     cfg = SvfConfig(saturating=saturating)
     name = "svf-sat" if saturating else "svf"
-    log(f"bench: SVF session B={cfg.B} T={cfg.T} saturating={saturating} chunk={args.chunk}")
-    sess = SvfSession(cfg, device=0, optimizer=True, chunk=args.chunk)
+    chunk = args.chunk or SVF_CHUNK
+    log(f"bench: SVF session B={cfg.B} T={cfg.T} saturating={saturating} chunk={chunk}")
+    sess = SvfSession(cfg, device=0, optimizer=True, chunk=chunk)
     if args.traffic_runs:
         try:
             traffic_run(sess, name, args.traffic_runs)
@@ -332,7 +334,7 @@ def run_svf(args, saturating: bool) -> dict:
         "data": "synthetic (U[-1,1] SplitMix64 input per lane, 2 Hz geometric cutoff sweep + 900 Hz envelope)",
         "config": {"workload": "ZDF SVF bank (SVFBPTTScratchTests.swift:21-34 per lane), MSE vs a fixed linear bank, "
                                "BPTT to base cutoff, res" + (" and kSat" if saturating else "") + ", Adam",
-                   "B": cfg.B, "T": cfg.T, "sr": cfg.sr, "saturating": saturating, "chunk": args.chunk,
+                   "B": cfg.B, "T": cfg.T, "sr": cfg.sr, "saturating": saturating, "chunk": chunk,
                    "parallelism": "single GPU"},
     }
     out.update(roofline_fields(rows, dom, roof_ms, ms_per_step, name))
@@ -543,7 +545,8 @@ def main() -> int:
     ap.add_argument("--workload", choices=("harmonic", "biquad", "stft", "membrane", "oscbank", "svf", "svf-sat"),
                     default="harmonic")
     ap.add_argument("--mem-steps", type=int, default=16, help="membrane frames per time-blocked launch")
-    ap.add_argument("--chunk", type=int, default=256, help="biquad / SVF scan chunk length (frames)")
+    ap.add_argument("--chunk", type=int, default=None,
+                    help="biquad / SVF scan chunk length (frames; default: the program's, 512 biquad, 256 SVF)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this backend runs on one GPU; the multi-GPU "

@@ -22,7 +22,7 @@ SPLITK_ROWS = 1024  # rows per split of the weight-gradient GEMMs
 GEMM_TILE_M = 128  # output rows per GEMM workgroup tile (k_gemm.hip BM)
 SPLITK_ROWS_HEADS = 256  # the heads' weight gradient has one 128-wide column tile: split finer to fill the chip
 MSS_TILE = 4096     # output samples per spectral-loss workgroup
-BQ_CHUNK = 256      # frames per biquad scan chunk
+BQ_CHUNK = 512      # frames per biquad scan chunk (512 measured fastest of 128..1024)
 SVF_CHUNK = 256     # frames per SVF scan chunk
 STFT_TILE = 8192    # output samples per STFT forward workgroup
 MEM_STEPS = 16      # membrane frames per time-blocked launch

@@ -73,7 +73,7 @@ def noalloc_forward(x, mod, params, B, T, chunk):
 
 
 def test_noalloc_forward_matches_the_schedule_forward_on_two_calls(gpu):
-    cases = [(BiquadConfig(B=256, T=1 << 16), True, 256),   # modulated, the config-4 chunk
+    cases = [(BiquadConfig(B=256, T=1 << 16), True, 512),   # modulated, the config-4 chunk
              (BiquadConfig(B=37, T=3001), False, 64)]         # smaller, ragged, unmodulated
     for cfg, modulated, chunk in cases:
         print(f"no-alloc biquad forward B={cfg.B} T={cfg.T} chunk={chunk} modulated={modulated}", flush=True)
