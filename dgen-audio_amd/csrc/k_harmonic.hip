@@ -55,11 +55,17 @@ __device__ __forceinline__ float div_sr(float x, float sr, float rsr) {
   return x / sr;
 }
 
-// sin(2*pi*p) for p in [0, 1): the gfx950 transcendental unit takes its
-// argument in revolutions (v_sin_f32).  Measured max abs error over a 2^24
-// point grid of [0,1): 1.3e-7, against 4.2e-7 for sinf(fl(p * 2pi_f32)), the
-// expression the reference evaluates (CRenderer.swift:825-827).
-__device__ __forceinline__ float sin2pi(float p) { return __builtin_amdgcn_sinf(p); }
+// sin(p * 2pi_f32), the expression the reference evaluates
+// (CRenderer.swift:825-827), for p in [0, 1): the synth forward evaluates
+// it by polynomial (sin_2pif, ~1 ulp), because the prediction's rounding
+// reaches the gradient through the log-magnitude loss's ill-conditioned
+// bins (measured at B=4, T=64000 against finite differences of the fp64
+// forward: the whole gradient 4.2% from fp64 with the hardware sin(2 pi p),
+// 1.3% with this); the backward's amplitude factors take the hardware form
+// of the same function (sin_2pif_hw), whose rounding enters the gradient
+// only linearly.
+__device__ __forceinline__ float sin2pi(float p) { return sin_2pif(p); }
+__device__ __forceinline__ float sin2pi_bwd(float p) { return sin_2pif_hw(p); }
 
 // ------------------------------------------------------------ frame-rate data
 // out[b][t] = (1-frac_t) * src[lo_t][b] + frac_t * src[hi_t][b]: the sampleRow
@@ -835,7 +841,7 @@ __device__ __forceinline__ void bwd_harmonic_pass(const SynthArgs& a, const SegL
       ph = FAST ? __builtin_amdgcn_fractf(ph + inc) : phasor_wrap(ph + inc);
       // every lane evaluates the sine (opaque to the compiler), so the
       // selects below stay branch-free instead of nested exec-mask regions
-      float sv = sin2pi(p);
+      float sv = sin2pi_bwd(p);
       asm volatile("" : "+v"(sv));
       const float hm = (sv - hs[j]) * cf[j];
       const float dm = harm ? (MASKC || freq < nyq ? hm : 0.0f) : ex[j];

@@ -70,7 +70,7 @@ __global__ __launch_bounds__(kTile) void k_osc_tiles(const float* __restrict__ f
       const float r = s_inc[k] * fn;
       const float phase = r - floorf(r);
       // sin(phase * 2pi): the transcendental unit takes revolutions
-      acc = acc + __builtin_amdgcn_sinf(phase) * s_amp[k];
+      acc = acc + sin_2pif_hw(phase) * s_amp[k];
     }
   }
   const bool live = n < frames;
@@ -180,7 +180,7 @@ __global__ __launch_bounds__(64) void k_stream_osc(const float* __restrict__ fre
     wave_sync();
     if (lane < nb) {
       float x = 0.f;
-      for (int k = 0; k < nosc; ++k) x = x + __builtin_amdgcn_sinf(s_ph[lane][k]) * s_amp[k];
+      for (int k = 0; k < nosc; ++k) x = x + sin_2pif_hw(s_ph[lane][k]) * s_amp[k];
       s_x[lane] = x;
     }
     wave_sync();

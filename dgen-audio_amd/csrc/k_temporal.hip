@@ -106,11 +106,11 @@ __global__ __launch_bounds__(kThreads) void k_swept_phasor(const float* __restri
     if (w >= 1.0f) w = w - 1.0f;
     ph = rs ? 0.0f : w;
     // sin / cos of 2 pi acc: the transcendental unit takes revolutions
-    const float v = smooth ? __builtin_amdgcn_sinf(acc) : acc;
+    const float v = smooth ? sin_2pif_hw(acc) : acc;
     const float d = v - target;
     ls = ls + (double)(d * d);
     if (phase) phase[(size_t)n * E + e] = acc;
-    gout[(size_t)n * E + e] = smooth ? 2.0f * d * (__builtin_amdgcn_cosf(acc) * kTwoPi) : 2.0f * d;
+    gout[(size_t)n * E + e] = smooth ? 2.0f * d * (cos_2pif_hw(acc) * kTwoPi) : 2.0f * d;
   }
   lossp[e] = (float)ls;
 }

@@ -8,6 +8,7 @@ call with B=1 gives that lane's share times B), the lanes spread over host
 threads (the oracle is plain C behind ctypes, which releases the GIL).
 Needs a GPU."""
 import dataclasses
+import json
 import os
 from concurrent.futures import ThreadPoolExecutor
 
@@ -113,32 +114,88 @@ def test_full_size_loss(full):
     assert e_hip < 1e-5
 
 
+# The fp32 floor of this gradient (tests/golden/fp32_floor.py): the CPU
+# oracle's fp32 evaluation of the reference semantics against central
+# finite differences of its fp64 build, at the default parameters and at
+# last-ulp moves of them.  The log-magnitude term weights each bin by
+# 1/(|X|+1e-8) and the L1 terms take their signs from |X| - |T|, so the
+# gradient moves by percents when the prediction moves by its fp32
+# rounding: the fp64 backward evaluated at an fp32 prediction is itself
+# ~2.5-4% (relative L2) from the fp64 gradient.  The bars below are the
+# north star's 1e-2 where the floor allows it, and otherwise 1.5 times the
+# largest value the fp32 oracle reaches over its draws.
+FLOOR = json.load(open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "fp32_floor.json")))
+DRAW_SEED = FLOOR["config"]["seed"]
+
+
+def param_draw(P0, rng):
+    """Every parameter moved one ulp up or down at random (as fp32_floor.py)."""
+    up = rng.random(P0.shape) < 0.5
+    return np.where(up, np.nextafter(P0, np.float32(np.inf)), np.nextafter(P0, np.float32(-np.inf))).astype(np.float32)
+
+
 @pytest.fixture(scope="module")
 def lane4(gpu):
     cfg = HarmonicConfig(B=4)
     f0, uv, X = cfg.data()
     print(f"gradient at the per-lane shape: B={cfg.B} T={cfg.T} hidden={cfg.hidden} fft={cfg.fft_sizes}", flush=True)
+    P0 = cfg.weights()
+    rng = np.random.default_rng(DRAW_SEED)
     s = HarmonicSession(cfg, optimizer=False)
+    draws = []
     try:
-        s.step()
-        g = s.rt.read("grads").astype(np.float64)
+        for d in range(3):
+            P = P0 if d == 0 else param_draw(P0, rng)
+            s.rt.write("params", P)
+            s.step()
+            draws.append((P, s.rt.read("grads").astype(np.float64)))
+            if d == 0:
+                stages = {k: s.rt.read(k) for k in ("y", "dy", "ctrl", "dctrl")}
         tgt = s.target
-        stages = {k: s.rt.read(k) for k in ("y", "dy", "ctrl", "dctrl")}
     finally:
         s.close()
     lanes = Lanes(cfg, X, f0, uv)
-    P64 = cfg.weights().astype(np.float64)
+    P64 = P0.astype(np.float64)
     _, g64, _ = lanes.step(P64, tgt, True, "f64")
-    _, g32, _ = lanes.step(cfg.weights(), tgt, True, "f32")
-    yield cfg, lanes, P64, tgt, g, g64, g32, stages, (X, f0, uv)
+    _, g32, _ = lanes.step(P0, tgt, True, "f32")
+    yield cfg, lanes, P64, tgt, draws[0][1], g64, g32, stages, (X, f0, uv), draws
     lanes.close()
+
+
+def test_full_shape_backward_at_its_own_prediction(lane4):
+    """The whole HIP backward (spectral gradient, synth adjoint, MLP
+    backward) against the exact backward evaluated at the HIP step's own
+    prediction y and controls: what the HIP backward's arithmetic adds,
+    separated from how far the fp32 forward's rounding moves the exact
+    gradient.  The fp32 oracle's backward at the same point is printed
+    beside it (both measured 0.5-0.7%)."""
+    cfg, lanes, P64, tgt, g, g64, g32, st, (X, f0, uv), _ = lane4
+    B, T = cfg.B, cfg.T
+    y = st["y"].reshape(B, T)
+    ctrl = st["ctrl"].reshape(cfg.M, 128)[:, :cfg.NC]
+
+    def bwd(prec):
+        dy = np.concatenate(list(lanes.pool.map(
+            lambda b: O.mss_bwd(y[b:b + 1], tgt[b:b + 1], 1, T, cfg.fft_sizes, cfg.hop_div, cfg.w_lin, cfg.w_log, T,
+                                prec=prec) / B, range(B))))
+        dc = O.synth_bwd(ctrl, f0, uv, dy, B, cfg.F, T, cfg.K, cfg.NF, cfg.sr, prec=prec)
+        return O.mlp_bwd(X, cfg.weights(), dc, cfg.M, cfg.din, cfg.hidden, cfg.layers, cfg.K, cfg.NF,
+                         prec=prec).astype(np.float64)
+
+    gx = bwd("f64")
+    e_hip, e_o32 = rel(g, gx), rel(bwd("f32"), gx)
+    print(f"backward at the HIP prediction, rel L2 vs the fp64 backward there: HIP {e_hip:.3e}, fp32 oracle {e_o32:.3e}")
+    assert e_hip < 1e-2
+    assert e_hip <= 2.0 * e_o32 + 1e-3
 
 
 def test_full_shape_gradient_stages(lane4):
     """Each backward stage of the HIP step against the fp64 oracle fed the
-    HIP path's own upstream values, at T=64000 (names the stage that carries
-    the gradient's distance to fp64)."""
-    cfg, lanes, P64, tgt, g, g64, g32, st, (X, f0, uv) = lane4
+    HIP path's own upstream values, at T=64000: the synth adjoint and the
+    MLP backward to 1e-4; the spectral dL/dy, whose fp32 evaluation sits
+    percents from fp64 at any prediction (fp32_floor.json: the oracle's
+    median 4.8%, max 6.8%), to 1.5 times the oracle's largest draw."""
+    cfg, lanes, P64, tgt, g, g64, g32, st, (X, f0, uv), _ = lane4
     B, T = cfg.B, cfg.T
     y = st["y"].reshape(B, T)
     dy64 = np.concatenate(list(lanes.pool.map(
@@ -154,45 +211,17 @@ def test_full_shape_gradient_stages(lane4):
     gm64 = O.mlp_bwd(X, cfg.weights(), dctrl, cfg.M, cfg.din, cfg.hidden, cfg.layers, cfg.K, cfg.NF, prec="f64")
     e_dy, e_dy32 = rel(dy, dy64), rel(dy32, dy64)
     e_dc, e_g = rel(dctrl, dc64), rel(g, gm64)
-    # The spectral gradient's distance to fp64 comes from a few near-silent
-    # bins (the log term scales by 1/|X|): for any fp32 evaluation it moves by
-    # several times when y moves by one ulp.  Its fp32 scale here is the
-    # largest of the fp32 oracle's distances at y and at two last-ulp
-    # perturbations of y (each against fp64 at the same point).
-    rng = np.random.default_rng(11)
-    scale32 = [e_dy32]
-    for _ in range(2):
-        yp = (y * (1.0 + rng.choice([-1.0, 1.0], size=y.shape) * 2.0 ** -24)).astype(np.float32)
-        d64 = np.concatenate(list(lanes.pool.map(
-            lambda b: O.mss_bwd(yp[b:b + 1], tgt[b:b + 1], 1, T, cfg.fft_sizes, cfg.hop_div, cfg.w_lin, cfg.w_log, T,
-                                prec="f64") / B, range(B))))
-        d32 = np.concatenate(list(lanes.pool.map(
-            lambda b: O.mss_bwd(yp[b:b + 1], tgt[b:b + 1], 1, T, cfg.fft_sizes, cfg.hop_div, cfg.w_lin, cfg.w_log, T,
-                                prec="f32") / B, range(B))))
-        scale32.append(rel(d32, d64))
-    print(f"stages vs fp64 oracle at HIP inputs: spectral dL/dy HIP {e_dy:.3e} (fp32 oracle at y and two last-ulp "
-          f"perturbations {', '.join(f'{e:.3e}' for e in scale32)}); synth backward {e_dc:.3e}; "
+    print(f"stages vs fp64 oracle at HIP inputs: spectral dL/dy HIP {e_dy:.3e} (fp32 oracle {e_dy32:.3e}; its floor "
+          f"median {FLOOR['dy_stage']['median']:.3e} max {FLOOR['dy_stage']['max']:.3e}); synth backward {e_dc:.3e}; "
           f"MLP backward {e_g:.3e}")
     assert e_dc < 1e-4 and e_g < 1e-4
-    assert e_dy <= 1.5 * max(scale32) + 2e-3
+    assert e_dy <= 1.5 * FLOOR["dy_stage"]["max"]
 
 
 def _fd(lanes, P64, tgt, v, eps):
     lp = lanes.step(P64 + eps * v, tgt, False, "f64")[0]
     lm = lanes.step(P64 - eps * v, tgt, False, "f64")[0]
     return (lp - lm) / (2 * eps)
-
-
-# The fp32 floor of this loss at the full shape.  The log-magnitude term
-# scales the gradient by 1/(|X|+1e-8) in quiet passages (lane 0 frames
-# ~12000-12500 and ~61000-63000 at N = 64 and 2048 carry 97% of the
-# distance), and the L1 terms flip sign where |X| ~ |T|: there an fp32
-# evaluation of the reference semantics is percent-level off the exact one.
-# At the same y the HIP spectral gradient is as far from fp64 as the fp32
-# oracle's (test_full_shape_gradient_stages); the noise-filter head
-# parameters, whose gradient correlates dL/dy with white noise, carry it.
-ALONG_BAR = 2e-2        # fp32 oracle itself: 0.8%
-TAP_BAR = 1e-1          # noise-filter head columns; fp32 oracle itself: up to 2.9%
 
 
 def _is_noise_filter_param(cfg, i):
@@ -204,13 +233,26 @@ def _is_noise_filter_param(cfg, i):
 
 
 def test_full_shape_gradient_along_gradient_and_random_directions(lane4):
-    cfg, lanes, P64, tgt, g, g64, g32 = lane4[:7]
-    print(f"grad rel L2 vs fp64 oracle: HIP {rel(g, g64):.3e}, fp32 oracle {rel(g32, g64):.3e}")
-    u = g64 / np.linalg.norm(g64)
-    d = _fd(lanes, P64, tgt, u, 1e-6)
-    print(f"along grad: HIP {g @ u:.6e}, fp32 oracle {g32 @ u:.6e}, FD {d:.6e}; rel err HIP "
-          f"{abs(g @ u - d) / abs(d):.2e}, fp32 oracle {abs(g32 @ u - d) / abs(d):.2e}")
-    assert abs(g @ u - d) / abs(d) < ALONG_BAR
+    """Along the fp64 gradient, against central finite differences of the
+    fp64 forward, at the default parameters and two last-ulp moves of
+    them: the north star's 1e-2 on the median (the fp32 oracle's own median
+    is 0.94%, max 1.28%) and 1.5 times the oracle's largest draw on each."""
+    cfg, lanes, P64, tgt, g, g64, g32, st, _, draws = lane4
+    print(f"grad rel L2 vs fp64 oracle: HIP {rel(g, g64):.3e}, fp32 oracle {rel(g32, g64):.3e} (its floor median "
+          f"{FLOOR['whole']['median']:.3e} max {FLOOR['whole']['max']:.3e})")
+    assert rel(g, g64) <= 1.5 * FLOOR["whole"]["max"]
+    errs = []
+    for d, (P, gd) in enumerate(draws):
+        Pd = P.astype(np.float64)
+        gd64 = g64 if d == 0 else lanes.step(Pd, tgt, True, "f64")[1]
+        u = gd64 / np.linalg.norm(gd64)
+        fd = _fd(lanes, Pd, tgt, u, 1e-6)
+        errs.append(abs(gd @ u - fd) / abs(fd))
+        print(f"draw {d}: along grad HIP {gd @ u:.6e}, FD {fd:.6e}, rel err {errs[-1]:.2e}")
+    print(f"along-gradient errors {', '.join(f'{e:.2e}' for e in errs)} (fp32 oracle floor median "
+          f"{FLOOR['along']['median']:.2e} max {FLOOR['along']['max']:.2e})")
+    assert np.median(errs) <= 1e-2
+    assert max(errs) <= 1.5 * FLOOR["along"]["max"]
     rng = np.random.default_rng(22)
     gn = np.linalg.norm(g)
     for _ in range(3):
@@ -222,7 +264,13 @@ def test_full_shape_gradient_along_gradient_and_random_directions(lane4):
 
 
 def test_full_shape_gradient_largest_components(lane4):
+    """The 8 largest components against central finite differences: 1e-2
+    for the harmonic-gain bias; the noise-filter head parameters (their
+    gradient correlates dL/dy with white noise, so it carries the
+    ill-conditioned bins' error in full) to 1.5 times the fp32 oracle's
+    largest component error over its draws."""
     cfg, lanes, P64, tgt, g, g64, g32 = lane4[:7]
+    tap_bar = 1.5 * FLOOR["components"]["max"]
     for i in np.argsort(-np.abs(g64))[:8]:
         e = np.zeros_like(P64)
         e[i] = 1.0
@@ -231,4 +279,4 @@ def test_full_shape_gradient_largest_components(lane4):
         tap = _is_noise_filter_param(cfg, i)
         print(f"param {i}{' (noise filter)' if tap else ''}: HIP {g[i]:.6e}, fp32 oracle {g32[i]:.6e}, FD {d:.6e}; "
               f"rel err HIP {eh:.2e}, fp32 oracle {eo:.2e}")
-        assert eh < (TAP_BAR if tap else 1e-2)
+        assert eh < (tap_bar if tap else 1e-2)
