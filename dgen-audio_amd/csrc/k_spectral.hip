@@ -39,6 +39,9 @@ constexpr int kThreads = 256;
 constexpr int kMaxSizes = 8;
 constexpr float kLogEps = 1e-8f;   // DGenSpectralConfig.logMagnitudeEpsilon (GradientConfig.swift:38)
 constexpr float kMagEps = 1e-8f;   // safeMag = max(mag, 1e-8) (Emit+SpectralLoss.swift:1005-1006)
+// loss-mode bits (DGEN_HIP_MSS_*): each term's lossMode .l2 (else .l1) and
+// useSmoothLogMagnitude for the log term (HigherOps.swift:49-65)
+constexpr int kL2Lin = 1, kL2Log = 2, kSmoothLog = 4;
 
 struct MssArgs {
   const float* x;
@@ -49,6 +52,7 @@ struct MssArgs {
   int logn[kMaxSizes];
   int nsizes, B, T, ntiles;
   float gl, gg;                    // upstream gradient of each window's lin / log sum
+  int mode;                        // kL2Lin | kL2Log | kSmoothLog (the generic kernel only)
 };
 
 __device__ __forceinline__ float sgn(float v) { return v > 0.f ? 1.f : (v < 0.f ? -1.f : 0.f); }
@@ -85,7 +89,9 @@ static_assert(MssLds::kAccN % 64 == 0, "the accumulator swizzle works on whole 6
 // tid: the thread's index, opaque to the optimiser in each call (else every
 // size's values that depend only on it would be hoisted out of the size loop
 // and held in registers together)
-template <int LOGN>
+// GEN: the generic bin arithmetic (a.mode's L1/L2 terms and smooth log
+// magnitude); otherwise the trainer's L1 magnitude and log(mag + eps) terms
+template <int LOGN, bool GEN>
 __device__ __forceinline__ void mss_size(const MssArgs& a, MssLds& L, int si, int b, int tile, int tid) {
   constexpr int N = 1 << LOGN, M = N / 2, LOGM = LOGN - 1, H = N / 4, P = M / 8, W = kThreads / P;
   static_assert(W * M == 2048, "window slots must fill the FFT buffer");
@@ -220,14 +226,35 @@ __device__ __forceinline__ void mss_size(const MssArgs& a, MssLds& L, int si, in
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
           if (q >= nb) break;
-          const float m1 = hw_sqrt(X[q].x * X[q].x + X[q].y * X[q].y);
-          const float m2 = hw_sqrt(Tt[q].x * Tt[q].x + Tt[q].y * Tt[q].y);
-          const float dlog = hw_log(m1 + kLogEps) - hw_log(m2 + kLogEps);
-          lin += fabsf(m1 - m2);
-          lg += fabsf(dlog);
-          const float dmag = a.gl * sgn(m1 - m2) + a.gg * sgn(dlog) * hw_rcp(m1 + kLogEps);
-          const float sc = dmag * hw_rcp(fmaxf(m1, kMagEps));
-          G[q] = {sc * X[q].x, sc * X[q].y};
+          if constexpr (!GEN) {
+            const float m1 = hw_sqrt(X[q].x * X[q].x + X[q].y * X[q].y);
+            const float m2 = hw_sqrt(Tt[q].x * Tt[q].x + Tt[q].y * Tt[q].y);
+            const float dlog = hw_log(m1 + kLogEps) - hw_log(m2 + kLogEps);
+            lin += fabsf(m1 - m2);
+            lg += fabsf(dlog);
+            const float dmag = a.gl * sgn(m1 - m2) + a.gg * sgn(dlog) * hw_rcp(m1 + kLogEps);
+            const float sc = dmag * hw_rcp(fmaxf(m1, kMagEps));
+            G[q] = {sc * X[q].x, sc * X[q].y};
+          } else {
+            // Emit+SpectralLoss.swift:150-188 (forward) and :232-291 (GradSpec):
+            // the log term's magnitude is sqrt(p + eps^2) when smooth (its
+            // difference log m1 - log m2, its gradient over that magnitude
+            // twice), else m + eps in the log and max(m, 1e-8) below X
+            const bool l2lin = (a.mode & kL2Lin) != 0, l2log = (a.mode & kL2Log) != 0;
+            const bool smooth = (a.mode & kSmoothLog) != 0;
+            const float p1 = X[q].x * X[q].x + X[q].y * X[q].y;
+            const float p2 = Tt[q].x * Tt[q].x + Tt[q].y * Tt[q].y;
+            const float m1 = hw_sqrt(p1), m2 = hw_sqrt(p2);
+            const float s1 = smooth ? hw_sqrt(p1 + kLogEps * kLogEps) : m1 + kLogEps;
+            const float s2 = smooth ? hw_sqrt(p2 + kLogEps * kLogEps) : m2 + kLogEps;
+            const float dl = m1 - m2, dg = hw_log(s1) - hw_log(s2);
+            lin += l2lin ? dl * dl : fabsf(dl);
+            lg += l2log ? dg * dg : fabsf(dg);
+            const float sl = l2lin ? 2.f * dl : sgn(dl), sg = l2log ? 2.f * dg : sgn(dg);
+            const float rm = hw_rcp(fmaxf(m1, kMagEps)), rs = hw_rcp(s1);
+            const float sc = smooth ? a.gl * sl * rm + a.gg * sg * rs * rs : (a.gl * sl + a.gg * sg * rs) * rm;
+            G[q] = {sc * X[q].x, sc * X[q].y};
+          }
         }
         // inverse pre-processing (Hermitian extension of the one-sided G):
         //   E'_k = (G_k + conj G_{M-k})/2, O'_k = (G_k - conj G_{M-k})/2 * W_N^{-k},
@@ -357,6 +384,7 @@ __device__ __forceinline__ void mss_size(const MssArgs& a, MssLds& L, int si, in
 // All sizes in one launch, in the op's size order: the tile accumulator
 // stays in LDS from the first size to the last and is written to the tile
 // partials once.
+template <bool GEN>
 __global__ __launch_bounds__(kThreads) void k_mss(MssArgs a) {
   extern __shared__ float4 smem4[];
   MssLds& L = *reinterpret_cast<MssLds*>(smem4);
@@ -367,12 +395,12 @@ __global__ __launch_bounds__(kThreads) void k_mss(MssArgs a) {
     int tid = threadIdx.x;
     asm volatile("" : "+v"(tid));
     switch (a.logn[s]) {
-      case 6: mss_size<6>(a, L, s, b, tile, tid); break;
-      case 7: mss_size<7>(a, L, s, b, tile, tid); break;
-      case 8: mss_size<8>(a, L, s, b, tile, tid); break;
-      case 9: mss_size<9>(a, L, s, b, tile, tid); break;
-      case 10: mss_size<10>(a, L, s, b, tile, tid); break;
-      default: mss_size<11>(a, L, s, b, tile, tid); break;
+      case 6: mss_size<6, GEN>(a, L, s, b, tile, tid); break;
+      case 7: mss_size<7, GEN>(a, L, s, b, tile, tid); break;
+      case 8: mss_size<8, GEN>(a, L, s, b, tile, tid); break;
+      case 9: mss_size<9, GEN>(a, L, s, b, tile, tid); break;
+      case 10: mss_size<10, GEN>(a, L, s, b, tile, tid); break;
+      default: mss_size<11, GEN>(a, L, s, b, tile, tid); break;
     }
   }
   float* part = a.part + ((size_t)b * a.ntiles + tile) * kAcc;
@@ -382,8 +410,11 @@ __global__ __launch_bounds__(kThreads) void k_mss(MssArgs a) {
 int launch_spectral_loss(const Launch& L, const dgen_hip_op& op) {
   // arg: [0]=x ([B][T]) [1]=target ([B][T]) [2]=tile partials ([B][ntiles][6143]) [3]=B [4]=T [5]=n_sizes
   //      [6..13]=N_s [14..21]=per-window loss cells ([nwin_s][B][2]) [22..29]=FFT tables ([3 N_s - 2])
+  //      [30]=loss mode (kL2Lin | kL2Log | kSmoothLog; 0: L1 terms, log(mag + eps))
   // farg: [0]=lin upstream grad per window [1]=log upstream grad per window
   const int64_t x = op.arg[0], tgt = op.arg[1], part = op.arg[2], B = op.arg[3], T = op.arg[4], ns = op.arg[5];
+  const int64_t mode = op.arg[30];
+  DGEN_REQUIRE(mode >= 0 && mode <= (kL2Lin | kL2Log | kSmoothLog), "spectral_loss: loss mode %lld", (long long)mode);
   DGEN_REQUIRE(B > 0 && B <= 65535 && T > 0 && T <= (1 << 26) && ns >= 1 && ns <= kMaxSizes,
                "spectral_loss: B %lld T %lld sizes %lld", (long long)B, (long long)T, (long long)ns);
   const int64_t ntiles = (T + kTile - 1) / kTile;
@@ -416,8 +447,12 @@ int launch_spectral_loss(const Launch& L, const dgen_hip_op& op) {
   a.ntiles = (int)ntiles;
   a.gl = op.farg[0];
   a.gg = op.farg[1];
+  a.mode = (int)mode;
   const dim3 grid((unsigned)ntiles, (unsigned)B);
-  hipLaunchKernelGGL(k_mss, grid, dim3(kThreads), sizeof(MssLds), L.stream, a);
+  if (mode)
+    hipLaunchKernelGGL(k_mss<true>, grid, dim3(kThreads), sizeof(MssLds), L.stream, a);
+  else
+    hipLaunchKernelGGL(k_mss<false>, grid, dim3(kThreads), sizeof(MssLds), L.stream, a);
   DGEN_LAUNCH_CHECK("k_mss");
   return 0;
 }
@@ -431,22 +466,39 @@ struct CombineArgs {
   const float* wloss[kMaxSizes];
 };
 
+// With w_mse != 0 the trainer's time-domain term joins in
+// (Trainer.swift:547-551): w * sum_b (x - tgt)^2 / B per frame, first in the
+// frame's loss, and its gradient 2 w (x - tgt) / B added to dx.
 __global__ void k_mss_combine(CombineArgs g, const float* __restrict__ part, float* __restrict__ dx,
                               float* __restrict__ lossf, int B, int T, int ntiles, float wl, float wg,
-                              float max_frames) {
+                              float max_frames, const float* __restrict__ xs, const float* __restrict__ ts,
+                              float w_mse) {
   const int t = blockIdx.x * blockDim.x + threadIdx.x;
   const int b = blockIdx.y;
   if (t >= T) return;
+  const float inv_b = 1.0f / (float)B;
   if (dx) {
     const int tile = t / kTile, a0 = tile * kTile;
     const float* p = part + ((size_t)b * ntiles + tile) * kAcc;
     float v = p[t - a0 + kHalo];
     const int a1 = a0 + kTile;
     if (tile + 1 < ntiles && t >= a1 - kHalo) v += p[kAcc + (t - a1 + kHalo)];
+    if (w_mse != 0.f) {
+      const size_t i = (size_t)b * T + t;
+      v += w_mse * (2.f * (xs[i] - ts[i])) * inv_b;
+    }
     dx[(size_t)b * T + t] = v;
   }
   if (b == 0 && lossf) {
     float lf = 0.f;
+    if (w_mse != 0.f) {
+      float s = 0.f;
+      for (int bb = 0; bb < B; ++bb) {
+        const float d = xs[(size_t)bb * T + t] - ts[(size_t)bb * T + t];
+        s = s + d * d;
+      }
+      lf = s * inv_b * w_mse;
+    }
     for (int s = 0; s < g.nsizes; ++s) {
       const int hop = g.hop[s];
       if (t % hop) continue;
@@ -469,9 +521,16 @@ __global__ void k_mss_combine(CombineArgs g, const float* __restrict__ part, flo
 int launch_spectral_gather(const Launch& L, const dgen_hip_op& op) {
   // arg: [0]=dx ([B][T]) or -1 [1]=loss frames ([T]) or -1 [2]=B [3]=T [4]=n_sizes [5..12]=N_s
   //      [13]=tile partials [21..28]=per-window loss cells
+  //      with farg[3] != 0: [29]=x ([B][T]) [30]=target ([B][T])
   // farg: [0]=lin weight per size [1]=log weight per size [2]=maxFrameCount
+  //       [3]=weight of the time-domain MSE term (0: none)
   const int64_t dx = op.arg[0], lossf = op.arg[1], B = op.arg[2], T = op.arg[3], ns = op.arg[4];
   DGEN_REQUIRE(dx >= 0 || lossf >= 0, "spectral_gather: neither dx nor loss frames requested");
+  const float w_mse = op.farg[3];
+  if (w_mse != 0.f) {
+    DGEN_CHECK_CELL(L, op.arg[29], B * T, "spectral_gather.x");
+    DGEN_CHECK_CELL(L, op.arg[30], B * T, "spectral_gather.target");
+  }
   const int64_t part = op.arg[13];
   DGEN_REQUIRE(B > 0 && B <= 65535 && T > 0 && T <= (1 << 26) && ns >= 1 && ns <= kMaxSizes,
                "spectral_gather: B %lld T %lld sizes %lld", (long long)B, (long long)T, (long long)ns);
@@ -496,7 +555,8 @@ int launch_spectral_gather(const Launch& L, const dgen_hip_op& op) {
   // without dx only the lane-0 row of blocks (the loss signal) is launched
   hipLaunchKernelGGL(k_mss_combine, dim3((unsigned)((T + 255) / 256), (unsigned)(dx >= 0 ? B : 1)), dim3(256), 0,
                      L.stream, g, cell(L, part), dx >= 0 ? cell(L, dx) : nullptr, lossf >= 0 ? cell(L, lossf) : nullptr,
-                     (int)B, (int)T, (int)ntiles, op.farg[0], op.farg[1], op.farg[2]);
+                     (int)B, (int)T, (int)ntiles, op.farg[0], op.farg[1], op.farg[2],
+                     w_mse != 0.f ? cell(L, op.arg[29]) : nullptr, w_mse != 0.f ? cell(L, op.arg[30]) : nullptr, w_mse);
   DGEN_LAUNCH_CHECK("k_mss_combine");
   return 0;
 }

@@ -427,8 +427,10 @@ __global__ __launch_bounds__(64) void k_svf_seq_tiled(const float* __restrict__ 
         const float4 v = *reinterpret_cast<const float4*>(&out[a][4 * i + fq][4 * (lane & 15)]);
         *reinterpret_cast<float4*>(dsts[a] + (size_t)(n0 + 4 * i + fq) * B + kq) = v;
       }
-    if ((n0 + kTileF) % L == 0) {
-      lossp[(size_t)((n0 + kTileF) / L - 1) * B + k] = ls;
+    // a chunk's partial is complete at its last tile; the last chunk ends
+    // at T, which need not be a multiple of L
+    if ((n0 + kTileF) % L == 0 || n0 + kTileF == T) {
+      lossp[(size_t)((n0 + kTileF - 1) / L) * B + k] = ls;
       ls = 0.0f;
     }
   };

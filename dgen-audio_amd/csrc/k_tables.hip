@@ -307,10 +307,11 @@ int launch_row_schedule(const Launch& L, const dgen_hip_op& op) {
 // symmetric Hann 0.5*(1-cos(2*pi*i/(N-1))) and twiddles cos/sin(2*pi*k/(2h))
 // at offset h-1, all evaluated in double and rounded to float.
 // out = hann[N] | twre[N-1] | twim[N-1].
-__global__ void k_fft_tables(float* out, int n) {
+// rect: useHannWindow false, the all-1.0 window (HigherOps.swift:69-76).
+__global__ void k_fft_tables(float* out, int n, int rect) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   const double two_pi = 6.283185307179586476925286766559;
-  if (i < n) out[i] = (float)(0.5 * (1.0 - cos(two_pi * (double)i / (double)(n - 1))));
+  if (i < n) out[i] = rect ? 1.0f : (float)(0.5 * (1.0 - cos(two_pi * (double)i / (double)(n - 1))));
   if (i < n - 1) {
     int h = 1;
     while (2 * h - 1 <= i) h <<= 1;  // i in [h-1, 2h-1)
@@ -322,11 +323,13 @@ __global__ void k_fft_tables(float* out, int n) {
 }
 
 int launch_fft_tables(const Launch& L, const dgen_hip_op& op) {
-  const int64_t out = op.arg[0], n = op.arg[1];
+  const int64_t out = op.arg[0], n = op.arg[1], rect = op.arg[2];
   DGEN_REQUIRE(n >= 2 && n <= 65536 && (n & (n - 1)) == 0, "fft_tables: N=%lld must be a power of two", (long long)n);
+  DGEN_REQUIRE(rect == 0 || rect == 1, "fft_tables: window kind %lld", (long long)rect);
   DGEN_CHECK_CELL(L, out, 3 * n - 2, "fft_tables.out");
   if (L.dry) return 0;
-  hipLaunchKernelGGL(k_fft_tables, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, L.stream, cell(L, out), (int)n);
+  hipLaunchKernelGGL(k_fft_tables, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, L.stream, cell(L, out), (int)n,
+                     (int)rect);
   DGEN_LAUNCH_CHECK("k_fft_tables");
   return 0;
 }

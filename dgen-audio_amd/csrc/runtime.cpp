@@ -19,10 +19,12 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
 
+#include "dgen_process_v1.h"
 #include "internal.h"
 
 namespace dgen {
@@ -118,6 +120,8 @@ struct dgen_hip_ctx {
   std::vector<uint32_t> in_stride, out_stride;
   // the next enqueue starts the streaming classes from zero state
   bool reset_next = false;
+  // a dgen_hip_run_async whose declared outputs the next dgen_hip_sync downloads
+  bool outputs_pending = false;
 };
 
 static int set_device(dgen_hip_ctx* c) {
@@ -273,8 +277,11 @@ int dgen_hip_create(int device, dgen_hip_ctx** out) {
   return 0;
 }
 
+static void process_unbind_if(dgen_hip_ctx* c);
+
 int dgen_hip_destroy(dgen_hip_ctx* c) {
   if (!c) return 0;
+  process_unbind_if(c);
   (void)hipSetDevice(c->device);
   if (c->s0) (void)hipStreamSynchronize(c->s0);
   if (c->s1) (void)hipStreamSynchronize(c->s1);
@@ -448,7 +455,9 @@ static int run_static(dgen_hip_ctx* c) {
 int dgen_hip_run_async(dgen_hip_ctx* c, uint32_t frame_count) {
   int rc = run_checks(c, frame_count);
   if (rc) return rc;
-  return launch_run(c, frame_count);
+  rc = launch_run(c, frame_count);
+  c->outputs_pending = rc == 0 && c->out_n != 0;
+  return rc;
 }
 
 int dgen_hip_set_graphs(dgen_hip_ctx* c, int enable) {
@@ -462,8 +471,8 @@ int dgen_hip_set_graphs(dgen_hip_ctx* c, int enable) {
   return 0;
 }
 
-int dgen_hip_sync(dgen_hip_ctx* c) {
-  if (!c) return fail(DGEN_HIP_E_INVALID, "sync: null context");
+// Wait for both streams (no output download).
+static int sync_streams(dgen_hip_ctx* c) {
   int rc = set_device(c);
   if (rc) return rc;
   DGEN_HIP_TRY(hipStreamSynchronize(c->s0));
@@ -471,16 +480,27 @@ int dgen_hip_sync(dgen_hip_ctx* c) {
   return 0;
 }
 
+int dgen_hip_sync(dgen_hip_ctx* c) {
+  if (!c) return fail(DGEN_HIP_E_INVALID, "sync: null context");
+  int rc = sync_streams(c);
+  if (rc) return rc;
+  // the declared outputs of a dgen_hip_run_async become host-visible here, as
+  // the reference's shared-storage outputs buffer is after run()
+  // (MetalRuntime.swift:232, 334-337)
+  if (c->outputs_pending) {
+    c->outputs_pending = false;
+    if (c->out_n) return dgen_hip_download(c, c->out_off, c->out_n);
+  }
+  return 0;
+}
+
 int dgen_hip_run(dgen_hip_ctx* c, uint32_t frame_count) {
   int rc = dgen_hip_run_async(c, frame_count);
   if (rc) {
-    if (c) (void)dgen_hip_sync(c);
+    if (c) (void)sync_streams(c);
     return rc;
   }
-  if ((rc = dgen_hip_sync(c))) return rc;
-  // outputs are host-visible on return, as the reference's shared-storage
-  // outputs buffer is after run() (MetalRuntime.swift:232, 334-337)
-  return c->out_n ? dgen_hip_download(c, c->out_off, c->out_n) : 0;
+  return dgen_hip_sync(c);
 }
 
 int dgen_hip_set_outputs(dgen_hip_ctx* c, uint64_t off, uint64_t n) {
@@ -517,6 +537,24 @@ int dgen_hip_set_process_ports(dgen_hip_ctx* c, uint32_t n_in, const uint64_t* i
   int rc = check(in_cells, in_strides, n_in, "input");
   if (!rc) rc = check(out_cells, out_strides, n_out, "output");
   if (rc) return rc;
+  // input channels must not share a cell: a call writes each input cell from
+  // exactly one channel (and process_v1 relies on it to tell whether the
+  // ports fill their span)
+  if (n_in > 1) {
+    uint64_t lo = UINT64_MAX, hi = 0;
+    for (uint32_t i = 0; i < n_in; ++i) {
+      lo = std::min(lo, in_cells[i]);
+      hi = std::max(hi, in_cells[i] + (uint64_t)(c->max_frames - 1) * in_strides[i] + 1);
+    }
+    std::vector<uint8_t> used(hi - lo, 0);
+    for (uint32_t i = 0; i < n_in; ++i)
+      for (uint32_t f = 0; f < c->max_frames; ++f) {
+        uint8_t& u = used[in_cells[i] + (uint64_t)f * in_strides[i] - lo];
+        if (u) return fail(DGEN_HIP_E_INVALID, "set_process_ports: input channel %u frame %u shares cell %llu with "
+                           "another input channel", i, f, (unsigned long long)(in_cells[i] + (uint64_t)f * in_strides[i]));
+        u = 1;
+      }
+  }
   c->in_cell.assign(in_cells, in_cells + n_in);
   c->in_stride.assign(in_strides, in_strides + n_in);
   c->out_cell.assign(out_cells, out_cells + n_out);
@@ -558,15 +596,19 @@ int dgen_hip_process_v1(dgen_hip_ctx* c, const float* const* inputs, float* cons
     if (!inputs[i]) return fail(DGEN_HIP_E_INVALID, "process_v1: input channel %zu is null", i);
   for (size_t i = 0; i < c->out_cell.size(); ++i)
     if (!outputs[i]) return fail(DGEN_HIP_E_INVALID, "process_v1: output channel %zu is null", i);
-  // inputs -> host mirror -> device (one copy over the ports' span)
+  // inputs -> host mirror -> device, one copy over the ports' span.  When the
+  // ports do not fill their span (the span holds cells of other data, e.g.
+  // state the device carries between calls), the span is refreshed from the
+  // device first, so the copy writes those cells back unchanged.
   if (!c->in_cell.empty()) {
+    uint64_t lo, hi;
+    port_span(c->in_cell, c->in_stride, frame_count, &lo, &hi);
+    if ((uint64_t)c->in_cell.size() * frame_count != hi - lo && (rc = dgen_hip_download(c, lo, hi - lo))) return rc;
     for (size_t i = 0; i < c->in_cell.size(); ++i) {
       float* dst = c->h_arena + c->in_cell[i];
       const uint32_t st = c->in_stride[i];
       for (uint32_t f = 0; f < frame_count; ++f) dst[(size_t)f * st] = inputs[i][f];
     }
-    uint64_t lo, hi;
-    port_span(c->in_cell, c->in_stride, frame_count, &lo, &hi);
     if ((rc = dgen_hip_upload(c, lo, hi - lo))) return rc;
   }
   // the run, eagerly enqueued, at the call's host rate and reset flag
@@ -682,6 +724,96 @@ int dgen_hip_time_op(dgen_hip_ctx* c, uint32_t frame_count, uint32_t op_index, i
   for (auto& e : evs) (void)hipEventDestroy(e);
   *ms_out = total / iters;
   return rc;
+}
+
+
+// ---- the reference-named process-function exports (dgen_process_v1.h) ----
+// One bound schedule per process, as the reference loads one compiled graph
+// per process-function library.  The graph's memory range of the arena is
+// copied from the caller's state block before each block and back after it,
+// so every instance's carried state lives in its own block.
+namespace {
+std::mutex g_proc_mu;
+dgen_hip_ctx* g_proc_ctx = nullptr;
+uint64_t g_proc_off = 0, g_proc_n = 0;
+}  // namespace
+
+static void process_unbind_if(dgen_hip_ctx* c) {
+  std::lock_guard<std::mutex> lk(g_proc_mu);
+  if (g_proc_ctx == c) {
+    g_proc_ctx = nullptr;
+    g_proc_off = g_proc_n = 0;
+  }
+}
+
+int dgen_hip_process_bind(dgen_hip_ctx* c, uint64_t off, uint64_t n) {
+  std::lock_guard<std::mutex> lk(g_proc_mu);
+  if (!c) {
+    g_proc_ctx = nullptr;
+    g_proc_off = g_proc_n = 0;
+    return 0;
+  }
+  if (!c->configured) return fail(DGEN_HIP_E_STATE, "process_bind: context not configured");
+  if (c->in_cell.empty() && c->out_cell.empty())
+    return fail(DGEN_HIP_E_STATE, "process_bind: the context has no process ports (dgen_hip_set_process_ports)");
+  if (n == 0 || off > c->floats || n > c->floats - off)
+    return fail(DGEN_HIP_E_RANGE, "process_bind: memory [%llu, +%llu) outside the arena of %llu floats",
+                (unsigned long long)off, (unsigned long long)n, (unsigned long long)c->floats);
+  g_proc_ctx = c;
+  g_proc_off = off;
+  g_proc_n = n;
+  return 0;
+}
+
+uint64_t dgen_hip_process_memory_size(void) {
+  std::lock_guard<std::mutex> lk(g_proc_mu);
+  return g_proc_ctx ? std::max<uint64_t>(g_proc_n, 1024) : 0;
+}
+
+void dgen_process_v1(const float* const* inputs, float* const* outputs, uint32_t frame_count, void* state,
+                     const DGenProcessContextV1* context, const DGenHostServicesV1* host) {
+  (void)host;
+  std::lock_guard<std::mutex> lk(g_proc_mu);
+  dgen_hip_ctx* c = g_proc_ctx;
+  // silence on failure: every output channel the bound ports name, for the
+  // frames the call asked for
+  auto silence = [&]() {
+    if (!c || !outputs) return;
+    for (size_t i = 0; i < c->out_cell.size(); ++i)
+      if (outputs[i]) std::memset(outputs[i], 0, (size_t)frame_count * sizeof(float));
+  };
+  if (!c) {
+    fail(DGEN_HIP_E_STATE, "dgen_process_v1: no schedule bound (dgen_hip_process_bind)");
+    return;
+  }
+  if (!state) {
+    fail(DGEN_HIP_E_INVALID, "dgen_process_v1: null state block");
+    silence();
+    return;
+  }
+  // the reference's reading of the context (CRenderer.swift:357-359): its
+  // rate counts only for a v1 struct of full size; otherwise the graph's own
+  dgen_hip_process_context_v1 pc{DGEN_HIP_ABI_VERSION, sizeof(dgen_hip_process_context_v1), 0.f, 0u};
+  if (context && context->abi_version == DGEN_ABI_VERSION_V1 && context->struct_size >= sizeof(DGenProcessContextV1))
+    pc.sample_rate = context->sample_rate;
+  float* blk = static_cast<float*>(state);
+  int rc = run_checks(c, frame_count);
+  if (!rc) {
+    std::memcpy(c->h_arena + g_proc_off, blk, g_proc_n * sizeof(float));
+    rc = dgen_hip_upload(c, g_proc_off, g_proc_n);
+  }
+  if (!rc) rc = dgen_hip_process_v1(c, inputs, outputs, frame_count, &pc);
+  if (!rc) rc = dgen_hip_download(c, g_proc_off, g_proc_n);
+  if (rc) {
+    silence();
+    return;
+  }
+  std::memcpy(blk, c->h_arena + g_proc_off, g_proc_n * sizeof(float));
+}
+
+void dgen_set_param_value_v1(int32_t cell_id, float value) {
+  (void)cell_id;
+  (void)value;
 }
 
 }  // extern "C"

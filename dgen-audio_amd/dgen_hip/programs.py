@@ -81,15 +81,18 @@ def stream_oscbank_program(cfg: OscBankConfig, stateful: bool = True, max_frames
     oscillator phases (stateful) and the one-pole's y[n-1] carry over."""
     T = int(max_frames or cfg.frames)
     p = Program(max_frames=T)
+    # the graph's memory first (what the reference keeps in the host's state
+    # block), then the output channel's staging cell
     freqs = p.alloc("freqs", cfg.n_osc)
     amps = p.alloc("amps", cfg.n_osc)
-    out = p.alloc("out", T)
     st = p.alloc("state", cfg.n_osc + 1)
+    memory = p.size
+    out = p.alloc("out", T)
     p.add(R.K_STREAM_OSC_BANK, [freqs, amps, out, cfg.n_osc, T, st, 1 if stateful else 0], [cfg.sr, cfg.pole],
           label="stream_osc_bank", dispatch="singleThreaded frame loop (one wave)", bytes=4.0 * T,
           flops=float(T) * (26.0 * cfg.n_osc + 2.0), bound="valu")
     p.output_cell = "out"
-    p.meta.update(cfg=cfg, stateful=stateful, ports=([], [("out", 0, 1)]))
+    p.meta.update(cfg=cfg, stateful=stateful, ports=([], [("out", 0, 1)]), memory=(0, memory))
     return p
 
 
@@ -239,19 +242,23 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
         nwin = (T + hop - 1) // hop
         wloss_cells.append(p.alloc(f"win_loss_{N}", nwin * B * 2))
         tab = p.alloc(f"fft_tables_{N}", 3 * N - 2)
-        p.add(R.K_FFT_TABLES, [tab, N], flags=R.OP_STATIC, label=f"fft_tables_{N}", dispatch="static")
+        p.add(R.K_FFT_TABLES, [tab, N, 0 if cfg.hann else 1], flags=R.OP_STATIC, label=f"fft_tables_{N}",
+              dispatch="static")
         hann_cells.append(tab)
         # two real forward transforms + one real-output inverse (2.5 N log2 N each) + bin math
         mss_flops += nwin * B * (7.5 * N * np.log2(N) + 30.0 * N)
     larg = [y, target, mss_part, B, T, len(sizes)] + (sizes + [0] * 8)[:8] + (wloss_cells + [0] * 8)[:8] \
-        + (hann_cells + [0] * 8)[:8]
+        + (hann_cells + [0] * 8)[:8] + [cfg.mss_mode & 7]
     p.add(R.K_SPECTRAL_LOSS, larg, [gl, gg], label="spectral_mss",
           dispatch=f"perFrameScaledThreadgroup1({B}) x {len(sizes)} sizes",
           bytes=(2 * B * T + B * ntiles * (MSS_TILE + 2047) + sum((T + N // 4 - 1) // (N // 4) for N in sizes) * B * 2)
           * f4, flops=mss_flops, bound="valu")
-    garg = [dy, -1, B, T, len(sizes)] + (sizes + [0] * 8)[:8] + [mss_part] + [0] * 7 + (wloss_cells + [0] * 8)[:8]
-    p.add(R.K_SPECTRAL_GATHER, garg, [wl, wg, maxf], label="spectral_combine", dispatch=f"perFrameScaled({B})",
-          bytes=(B * ntiles * (MSS_TILE + 2047) + B * T) * f4, flops=float(B * T))
+    garg = [dy, -1, B, T, len(sizes)] + (sizes + [0] * 8)[:8] + [mss_part] + [0] * 7 + (wloss_cells + [0] * 8)[:8] \
+        + [y, target]
+    w_mse = np.float32(cfg.w_mse)
+    mse_b = 2 * B * T * f4 if w_mse else 0
+    p.add(R.K_SPECTRAL_GATHER, garg, [wl, wg, maxf, w_mse], label="spectral_combine", dispatch=f"perFrameScaled({B})",
+          bytes=(B * ntiles * (MSS_TILE + 2047) + B * T) * f4 + mse_b, flops=float(B * T))
     # the per-frame loss signal (only reported, nothing in the backward reads
     # it) is a launch of its own at the end of stream 0, which finishes
     # before the side stream: folded into the combine, its blocks were the
@@ -331,8 +338,8 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     p.add(R.K_COLSUM, [dcol[0], gw1, mt, (din + 1) * Hd, (din + 1) * Hd, ws_col], label="dWb_l1",
           dispatch="chunkPartialsReduceToCell", bytes=(mt + 1) * (din + 1) * Hd * f4,
           flops=float(mt * (din + 1) * Hd))
-    p.add(R.K_SPECTRAL_GATHER, larg2, [wl, wg, maxf], label="loss_frames",
-          dispatch="perFrame", bytes=(nwin_all * B * 2 + T) * f4, flops=float(nwin_all * B * 2))
+    p.add(R.K_SPECTRAL_GATHER, larg2, [wl, wg, maxf, w_mse], label="loss_frames",
+          dispatch="perFrame", bytes=(nwin_all * B * 2 + T) * f4 + mse_b, flops=float(nwin_all * B * 2))
     if optimizer:
         m = p.alloc("adam_m", npar)
         v = p.alloc("adam_v", npar)
@@ -499,16 +506,19 @@ def stream_biquad_program(cfg: BiquadConfig, max_frames: int | None = None, modu
     frame loop)."""
     B, T = cfg.B, int(max_frames or cfg.T)
     p = Program(max_frames=T)
-    x = p.alloc("x", T * B)
-    mod = p.alloc("mod", T) if modulated else -1
+    # the graph's memory first (parameters, the lanes' history cells), then
+    # the channels' staging cells
     P = p.alloc("params", 2 * B)
     st = p.alloc("state", 4 * B)
+    memory = p.size
+    x = p.alloc("x", T * B)
+    mod = p.alloc("mod", T) if modulated else -1
     y = p.alloc("y", T * B)
     p.add(R.K_STREAM_BIQUAD, [x, mod, P, st, y, B, T], label="stream_biquad",
           dispatch=f"fixedWithFrameLoop({B})", bytes=8.0 * T * B, flops=float(T * B) * (16 + 9), bound="valu")
     p.output_cell = "y"
     ins = [("x", k, B) for k in range(B)] + ([("mod", 0, 1)] if modulated else [])
-    p.meta.update(cfg=cfg, ports=(ins, [("y", k, B) for k in range(B)]))
+    p.meta.update(cfg=cfg, ports=(ins, [("y", k, B) for k in range(B)]), memory=(0, memory))
     return p
 
 
@@ -653,17 +663,20 @@ def stream_svf_program(cfg: SvfConfig, max_frames: int | None = None) -> Program
     filter).  Out stores map non-finite values to 0."""
     B, T = cfg.B, int(max_frames or cfg.T)
     p = Program(max_frames=T)
+    # the graph's memory first (parameters, the lanes' two cells), then the
+    # channels' staging cells
+    prm = p.alloc("params", 3 * B)
+    st = p.alloc("state", 2 * B)
+    memory = p.size
     x = p.alloc("x", T * B)
     mod = p.alloc("mod", T)
     env = p.alloc("env", T)
-    prm = p.alloc("params", 3 * B)
-    st = p.alloc("state", 2 * B)
     y = p.alloc("y", T * B)
     p.add(R.K_STREAM_SVF, [x, mod, env, prm, st, y, -1, -1, -1, B, T, SVF_CHUNK, 1, -1], [cfg.sr], label="stream_svf",
           dispatch=f"fixedWithFrameLoop({B})", bytes=8.0 * T * B, flops=float(T * B) * (30 + 18), bound="valu")
     p.output_cell = "y"
     ins = [("x", k, B) for k in range(B)] + [("mod", 0, 1), ("env", 0, 1)]
-    p.meta.update(cfg=cfg, ports=(ins, [("y", k, B) for k in range(B)]))
+    p.meta.update(cfg=cfg, ports=(ins, [("y", k, B) for k in range(B)]), memory=(0, memory))
     return p
 
 

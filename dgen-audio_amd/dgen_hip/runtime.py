@@ -74,8 +74,11 @@ EXPORTED_SYMBOLS = (
     "dgen_hip_download", "dgen_hip_zero", "dgen_hip_run", "dgen_hip_run_async", "dgen_hip_sync", "dgen_hip_set_graphs",
     "dgen_hip_profile", "dgen_hip_time_runs", "dgen_hip_time_op", "dgen_hip_run_op", "dgen_hip_set_outputs",
     "dgen_hip_host_outputs", "dgen_hip_set_sample_rate", "dgen_hip_biquad_forward_noalloc",
-    "dgen_hip_set_process_ports", "dgen_hip_process_v1",
+    "dgen_hip_set_process_ports", "dgen_hip_process_v1", "dgen_hip_process_bind", "dgen_hip_process_memory_size",
 )
+# the reference-named process-function exports (include/dgen_process_v1.h)
+PROCESS_V1_SYMBOLS = ("dgen_process_v1", "dgen_set_param_value_v1")
+DGEN_ABI_VERSION_V1 = 1
 PROCESS_RESET = 1
 
 
@@ -91,6 +94,12 @@ class COp(ctypes.Structure):
 class CProcessContext(ctypes.Structure):
     _fields_ = [("abi_version", ctypes.c_uint32), ("struct_size", ctypes.c_uint32), ("sample_rate", ctypes.c_float),
                 ("flags", ctypes.c_uint32)]
+
+
+class DGenProcessContextV1(ctypes.Structure):
+    """The reference's process context (dgen_runtime.h:252-257)."""
+    _fields_ = [("abi_version", ctypes.c_uint32), ("struct_size", ctypes.c_uint32), ("sample_rate", ctypes.c_float),
+                ("reserved", ctypes.c_uint32)]
 
 
 class CKernelTime(ctypes.Structure):
@@ -139,6 +148,12 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "dgen_hip_process_v1": ([vp, ctypes.POINTER(ctypes.POINTER(ctypes.c_float)),
                                  ctypes.POINTER(ctypes.POINTER(ctypes.c_float)), u32, ctypes.POINTER(CProcessContext)],
                                 i32),
+        "dgen_hip_process_bind": ([vp, u64, u64], i32),
+        "dgen_hip_process_memory_size": ([], u64),
+        "dgen_process_v1": ([ctypes.POINTER(ctypes.POINTER(ctypes.c_float)),
+                             ctypes.POINTER(ctypes.POINTER(ctypes.c_float)), u32, vp,
+                             ctypes.POINTER(DGenProcessContextV1), vp], None),
+        "dgen_set_param_value_v1": ([ctypes.c_int32, ctypes.c_float], None),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -291,6 +306,16 @@ class HIPLazyRuntime:
         _check(self.L.dgen_hip_process_v1(self._ctx, ip, op, int(frames), ctypes.byref(ctxv)), "dgen_hip_process_v1")
         return outs
 
+    def bindProcess(self) -> int:
+        """Bind this runtime's schedule to the reference-named exports
+        dgen_process_v1 / dgen_set_param_value_v1 (dgen_hip_process_bind), with
+        the program's graph memory (``meta["memory"]``: the cells the reference
+        keeps in the host's state block).  The process ports must be set.
+        Returns the state block size in floats (dgen_hip_process_memory_size)."""
+        off, end = self.program.meta["memory"]
+        _check(self.L.dgen_hip_process_bind(self._ctx, off, end - off), "dgen_hip_process_bind")
+        return int(self.L.dgen_hip_process_memory_size())
+
     def set_graphs(self, enable: bool = True) -> None:
         """Replay runs as a captured HIP graph (dgen_hip_set_graphs)."""
         _check(self.L.dgen_hip_set_graphs(self._ctx, 1 if enable else 0), "dgen_hip_set_graphs")
@@ -319,6 +344,7 @@ class HIPLazyRuntime:
 
     def close(self) -> None:
         if getattr(self, "_ctx", None):
+            # (destroying the bound context unbinds the process exports)
             self.L.dgen_hip_destroy(self._ctx)
             self._ctx = None
 
@@ -333,3 +359,28 @@ class HIPLazyRuntime:
 
     def __exit__(self, *exc):
         self.close()
+
+
+def process_v1(inputs, n_out: int, frames: int, state: np.ndarray, sample_rate: float | None = None,
+               context: bool = True) -> np.ndarray:
+    """Drive the reference-named export dgen_process_v1 as a host does
+    (CCompiledKernel.runWithMemory, Runtime.swift:746-787): channel pointer
+    arrays, the caller's state block (a float32 array of
+    dgen_hip_process_memory_size() values, zeroed by the host for a fresh
+    instance) and a DGenProcessContextV1 carrying the host rate.  Returns the
+    output channels [n_out][frames].  Failures leave the outputs at 0 (the
+    export returns nothing); the message is in dgen_hip_last_error()."""
+    L = load_library()
+    fp = ctypes.POINTER(ctypes.c_float)
+    ins = [np.ascontiguousarray(a, np.float32) for a in inputs]
+    outs = np.full((n_out, frames), np.nan, np.float32)
+    ip = (fp * max(1, len(ins)))(*[a.ctypes.data_as(fp) for a in ins])
+    op = (fp * max(1, n_out))(*[outs[i].ctypes.data_as(fp) for i in range(n_out)])
+    if state.dtype != np.float32 or not state.flags["C_CONTIGUOUS"]:
+        raise ValueError("state block: a contiguous float32 array")
+    c = DGenProcessContextV1(DGEN_ABI_VERSION_V1, ctypes.sizeof(DGenProcessContextV1),
+                             0.0 if sample_rate is None else float(sample_rate), 0)
+    L.dgen_process_v1(ip, op, int(frames), state.ctypes.data_as(ctypes.c_void_p),
+                      ctypes.byref(c) if context else None, None)
+    return outs
+

@@ -95,6 +95,15 @@ class HarmonicConfig:
     hop_div: int = 4
     w_lin: float = 1.0
     w_log: float = 0.5
+    # spectralLossFFT options of the two terms (HigherOps.swift:49-65,
+    # Functions.swift:870-910): lossMode "l1" (the trainer's) or "l2" (the
+    # API default) per term, useSmoothLogMagnitude for the log term,
+    # useHannWindow; and the trainer's mseLossWeight (Trainer.swift:547-551)
+    loss_lin: str = "l1"
+    loss_log: str = "l1"
+    smooth_log: bool = False
+    hann: bool = True
+    w_mse: float = 0.0
     min_f0: float = 50.0
     max_f0: float = 1000.0
     hscale: float = 1.0
@@ -116,6 +125,16 @@ class HarmonicConfig:
     @property
     def NC(self) -> int:
         return self.K + 2 + self.NF
+
+    @property
+    def mss_mode(self) -> int:
+        """Loss-mode bits of the multi-scale loss: 1 magnitude term L2, 2 log
+        term L2, 4 smooth log magnitude, 8 rectangular window."""
+        for name, v in (("loss_lin", self.loss_lin), ("loss_log", self.loss_log)):
+            if v not in ("l1", "l2"):
+                raise ValueError(f"{name} {v!r}: 'l1' or 'l2'")
+        return ((1 if self.loss_lin == "l2" else 0) | (2 if self.loss_log == "l2" else 0)
+                | (4 if self.smooth_log else 0) | (0 if self.hann else 8))
 
     @property
     def M(self) -> int:

@@ -44,6 +44,15 @@ extern "C" {
 
 typedef struct dgen_hip_ctx dgen_hip_ctx;
 
+/* Loss-mode bits of DGEN_HIP_K_SPECTRAL_LOSS (spectralLossFFT's options,
+ * HigherOps.swift:49-65): the magnitude term's and the log-magnitude term's
+ * lossMode .l2 (else .l1), and useSmoothLogMagnitude for the log term
+ * (0.5 log(|X|^2 + eps^2)).  useHannWindow: false is the window of the FFT
+ * tables (DGEN_HIP_K_FFT_TABLES arg[2]). */
+#define DGEN_HIP_MSS_L2_LIN 1
+#define DGEN_HIP_MSS_L2_LOG 2
+#define DGEN_HIP_MSS_SMOOTH_LOG 4
+
 /* ---- kernel classes ----------------------------------------------------
  * Argument meaning per class is documented at each class below.
  * "cell" = arena offset in floats; "n" = element count.                   */
@@ -117,6 +126,8 @@ enum dgen_hip_kernel {
    *      [14..21]=window-loss cells ([ceil(T/hop)][B][2])
    *      [22..29]=FFT tables (DGEN_HIP_K_FFT_TABLES output, 3N-2 floats: the
    *      window and the transforms' twiddles)
+   *      [30]=loss mode: DGEN_HIP_MSS_* bits (0: the trainer's L1 terms on
+   *      magnitude and log(magnitude + 1e-8))
    * farg: [0]=lin upstream grad per window (w_lin/nsizes/maxFrames/B)
    *       [1]=log upstream grad per window */
   DGEN_HIP_K_SPECTRAL_LOSS = 7,
@@ -126,7 +137,11 @@ enum dgen_hip_kernel {
    * arg: [0]=dx ([B][T]) or -1 [1]=loss frames ([T]) or -1 (not both -1)
    *      [2]=B [3]=T
    *      [4]=n_sizes [5..12]=N_s [13]=tile partials [21..28]=window-loss cells
-   * farg: [0]=lin weight per size [1]=log weight per size [2]=maxFrameCount */
+   *      [29]=x [30]=target ([B][T]; read only when farg[3] != 0)
+   * farg: [0]=lin weight per size [1]=log weight per size [2]=maxFrameCount
+   *       [3]=weight of the time-domain term w sum_b (x - target)^2 / B per
+   *       frame (the trainer's mseLossWeight, Trainer.swift:547-551; its
+   *       gradient 2 w (x - target) / B joins dx) or 0 */
   DGEN_HIP_K_SPECTRAL_GATHER = 8,
 
   /* Synth backward: d ctrl row partials per segment.
@@ -182,8 +197,9 @@ enum dgen_hip_kernel {
    * 1, 2, 3 for those three conditions. */
   DGEN_HIP_K_ROW_SCHEDULE = 17,
 
-  /* Radix-2 spectral-loss tables for one FFT size (HigherOps.swift:71-99):
-   * symmetric hann[N] | twre[N-1] | twim[N-1].  arg: [0]=out cell [1]=N */
+  /* Radix-2 spectral-loss tables for one FFT size (HigherOps.swift:69-99):
+   * window[N] | twre[N-1] | twim[N-1].  arg: [0]=out cell [1]=N [2]=window:
+   * 0 the symmetric Hann, 1 all ones (useHannWindow: false) */
   DGEN_HIP_K_FFT_TABLES = 18,
 
   /* Frame-rate sampleRow read of a [F][B] data table through a lerp table
@@ -467,12 +483,15 @@ int dgen_hip_zero(dgen_hip_ctx* ctx, uint64_t off, uint64_t n);
  * are laid out for that count).  Any other frame_count fails with
  * DGEN_HIP_E_RANGE before anything is enqueued. */
 int dgen_hip_run(dgen_hip_ctx* ctx, uint32_t frame_count);
-/* As dgen_hip_run but returns without waiting; dgen_hip_sync waits. */
+/* As dgen_hip_run but returns without waiting: dgen_hip_sync waits for the
+ * run and then copies the declared output cells to the host mirror, so
+ * dgen_hip_host_outputs is current after the sync (not before it). */
 int dgen_hip_run_async(dgen_hip_ctx* ctx, uint32_t frame_count);
 int dgen_hip_sync(dgen_hip_ctx* ctx);
 
 /* Declare the output cells [off, off+n) of the schedule: every dgen_hip_run
- * copies them to the host mirror after the run, and dgen_hip_host_outputs
+ * (and the dgen_hip_sync after a dgen_hip_run_async) copies them to the host
+ * mirror after the run, and dgen_hip_host_outputs
  * returns where they are (LazyRuntime.outputsPointer, Realize.swift:17;
  * MetalCompiledKernel's host-visible outputs buffer, MetalRuntime.swift:
  * 232-254).  n = 0 declares none.  Reset by dgen_hip_configure. */
@@ -504,7 +523,10 @@ typedef struct dgen_hip_process_context_v1 {
  * written to cell in_cells[c] + i * in_strides[c], output channel c's frame i
  * read from out_cells[c] + i * out_strides[c] (a [frames][lanes] cell is one
  * channel per lane with stride lanes).  Every channel must fit max_frames
- * frames in the arena.  Reset by dgen_hip_configure. */
+ * frames in the arena, and no two input channels may share a cell
+ * (DGEN_HIP_E_INVALID).  Cells between the input ports that are not ports
+ * (e.g. state a streaming class carries) keep their device values across a
+ * process call.  Reset by dgen_hip_configure. */
 int dgen_hip_set_process_ports(dgen_hip_ctx* ctx, uint32_t n_in, const uint64_t* in_cells, const uint32_t* in_strides,
                                uint32_t n_out, const uint64_t* out_cells, const uint32_t* out_strides);
 
@@ -517,6 +539,22 @@ int dgen_hip_set_process_ports(dgen_hip_ctx* ctx, uint32_t n_in, const uint64_t*
  * sample rate, no reset).  Ops are enqueued one by one (no graph replay). */
 int dgen_hip_process_v1(dgen_hip_ctx* ctx, const float* const* inputs, float* const* outputs, uint32_t frame_count,
                         const dgen_hip_process_context_v1* context);
+
+/* Bind the schedule the reference-named exports dgen_process_v1 /
+ * dgen_set_param_value_v1 (dgen_process_v1.h) run: a configured context with
+ * its process ports set, and the arena range [memory_off, memory_off +
+ * memory_floats) that is the graph's memory -- the cells the reference keeps
+ * in the host's state block (Runtime.swift:728-740): parameters, tensors and
+ * every state cell a streaming class carries between calls.  The reference
+ * loads one compiled graph per process-function library; here one context
+ * is bound per process at a time.  ctx NULL unbinds.  The context must
+ * outlive its binding (dgen_hip_destroy of the bound context unbinds it).
+ * No counterpart in the reference beyond the library load it replaces. */
+int dgen_hip_process_bind(dgen_hip_ctx* ctx, uint64_t memory_off, uint64_t memory_floats);
+/* Floats of the state block dgen_process_v1 reads and writes:
+ * max(memory_floats, 1024) of the bound schedule (the reference's
+ * getMemorySize(), Runtime.swift:228-237, 728-730), 0 when nothing is bound. */
+uint64_t dgen_hip_process_memory_size(void);
 
 /* Graph replay of runs (enable != 0): the per-run schedule for a frame count
  * is captured once from both streams into a HIP graph and every later

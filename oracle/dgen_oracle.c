@@ -632,7 +632,7 @@ typedef struct {
   int* bitrev;
 } FftTables;
 
-static void fft_tables_init(FftTables* t, int n) {
+static void fft_tables_init(FftTables* t, int n, int rect) {
   t->n = n;
   t->stages = 0;
   while ((1 << t->stages) < n) t->stages++;
@@ -640,7 +640,9 @@ static void fft_tables_init(FftTables* t, int n) {
   t->twre = (float*)malloc(sizeof(float) * (n > 1 ? n - 1 : 1));
   t->twim = (float*)malloc(sizeof(float) * (n > 1 ? n - 1 : 1));
   t->bitrev = (int*)malloc(sizeof(int) * n);
-  for (int i = 0; i < n; ++i) t->hann[i] = (float)(0.5 * (1.0 - cos(2.0 * M_PI * (double)i / (double)(n - 1))));
+  /* useHannWindow: false keeps the all-1.0 window (HigherOps.swift:69-76) */
+  for (int i = 0; i < n; ++i)
+    t->hann[i] = rect ? 1.0f : (float)(0.5 * (1.0 - cos(2.0 * M_PI * (double)i / (double)(n - 1))));
   for (int s = 0; s < t->stages; ++s) {
     int half = 1 << s;
     for (int k = 0; k < half; ++k) {
@@ -714,25 +716,57 @@ static void window_fft(const FftTables* tb, const REAL* x, int T, int f, REAL* r
 }
 
 #define LOG_EPS ((REAL)1e-8f) /* DGenSpectralConfig.logMagnitudeEpsilon, GradientConfig.swift:38 */
+/* Loss-mode bits of the multi-scale loss (one spectralLossFFT call per term
+ * and size in the reference, HigherOps.swift:49-65, Functions.swift:870-910):
+ * the magnitude term's and the log-magnitude term's lossMode (.l1 default of
+ * the trainer, .l2 the API default), useSmoothLogMagnitude for the log term,
+ * and useHannWindow: false for both. */
+#define MSS_L2_LIN 1
+#define MSS_L2_LOG 2
+#define MSS_SMOOTH_LOG 4
+#define MSS_RECT_WINDOW 8
 
 /* Multi-scale spectral loss, HarmonicE2E Trainer.fullBatchedLoss
  * (Examples/HarmonicE2E/Trainer.swift:538-583) over spectralLossFFTBatched +
  * BatchedReduce (Emit+SpectralLoss.swift:719-938) with normalize
- * (Sources/DGenLazy/Functions.swift:945-955: / maxFrameCount).
- * x, tgt: [B][T].  lf[T]: the per-frame loss signal.
+ * (Sources/DGenLazy/Functions.swift:945-955: / maxFrameCount), and the
+ * trainer's time-domain term mseLossWeight * sum_b (y - tgt)^2 / B per frame
+ * (Trainer.swift:547-551).
+ * x, tgt: [B][T].  lf[T]: the per-frame loss signal.  mode: MSS_* bits.
+ * Per bin the forward follows Emit+SpectralLoss.swift:150-188: m = sqrt(re^2 +
+ * im^2) (with MSS_SMOOTH_LOG the log term's magnitude is sqrt(re^2 + im^2 +
+ * eps^2) and its difference log(m1) - log(m2), else log(m1+eps) -
+ * log(m2+eps)); L1 accumulates |diff|, L2 diff^2.
  * With dx != NULL also writes d sum_frames(loss) / d x: GradSpec
- * (Emit+SpectralLoss.swift:940-1030: sign(diff), /(mag+eps) for log,
- * * X/max(|X|,1e-8), bins above N/2 zeroed), unnormalised positive-twiddle
+ * (Emit+SpectralLoss.swift:196-291: scale sign(diff) (L1) or 2 diff (L2),
+ * / (m+eps) or / m_smooth for the log term, times X / max(m, 1e-8) or
+ * X / m_smooth, bins above N/2 zeroed), the unnormalised positive-twiddle
  * IFFT (:1032-1160), window multiply, and the per-sample gather over the hop
- * windows containing it (:1163-1235). */
+ * windows containing it (:1163-1235); plus the MSE term's 2 w (y - tgt) / B. */
 static double mss_core(const REAL* x, const REAL* tgt, int B, int T, const int* sizes, int n_sizes, int hop_div,
-                       float w_lin, float w_log, float max_frames, REAL* lf, REAL* dx) {
+                       float w_lin, float w_log, float max_frames, int mode, float w_mse, REAL* lf, REAL* dx) {
   memset(lf, 0, sizeof(REAL) * T);
   if (dx) memset(dx, 0, sizeof(REAL) * (size_t)B * T);
+  const int l2lin = (mode & MSS_L2_LIN) != 0, l2log = (mode & MSS_L2_LOG) != 0;
+  const int smooth = (mode & MSS_SMOOTH_LOG) != 0;
+  if (w_mse != 0.0f) {
+    /* batchMSE = (diff*diff).sum() * (1/B), times mseLossWeight, first in
+     * the frame's total */
+    const REAL inv_b = (REAL)(1.0f / (float)B);
+    for (int t = 0; t < T; ++t) {
+      REAL s = 0;
+      for (int b = 0; b < B; ++b) {
+        const REAL d = x[(size_t)b * T + t] - tgt[(size_t)b * T + t];
+        s = s + d * d;
+        if (dx) dx[(size_t)b * T + t] = (REAL)w_mse * ((REAL)2 * d) * inv_b;
+      }
+      lf[t] = s * inv_b * (REAL)w_mse;
+    }
+  }
   for (int si = 0; si < n_sizes; ++si) {
     int N = sizes[si], H = N / hop_div > 0 ? N / hop_div : 1;
     FftTables tb;
-    fft_tables_init(&tb, N);
+    fft_tables_init(&tb, N, (mode & MSS_RECT_WINDOW) != 0);
     REAL *r1 = (REAL*)malloc(sizeof(REAL) * N), *i1 = (REAL*)malloc(sizeof(REAL) * N);
     REAL *r2 = (REAL*)malloc(sizeof(REAL) * N), *i2 = (REAL*)malloc(sizeof(REAL) * N);
     REAL *gr = (REAL*)malloc(sizeof(REAL) * N), *gi = (REAL*)malloc(sizeof(REAL) * N);
@@ -748,16 +782,32 @@ static double mss_core(const REAL* x, const REAL* tgt, int B, int T, const int* 
         REAL bl = 0, bg = 0;
         for (int k = 0; k < N; ++k) gr[k] = gi[k] = 0;
         for (int k = 0; k <= N / 2; ++k) {
-          REAL m1 = R_SQRT(r1[k] * r1[k] + i1[k] * i1[k]);
-          REAL m2 = R_SQRT(r2[k] * r2[k] + i2[k] * i2[k]);
-          REAL dlog = R_LOG(m1 + LOG_EPS) - R_LOG(m2 + LOG_EPS);
-          bl = bl + R_ABS(m1 - m2);
-          bg = bg + R_ABS(dlog);
+          REAL p1 = r1[k] * r1[k] + i1[k] * i1[k];
+          REAL p2 = r2[k] * r2[k] + i2[k] * i2[k];
+          REAL m1 = R_SQRT(p1);
+          REAL m2 = R_SQRT(p2);
+          /* the log term's denominators: m + eps, or the smooth magnitude */
+          REAL s1 = smooth ? R_SQRT(p1 + LOG_EPS * LOG_EPS) : m1 + LOG_EPS;
+          REAL s2 = smooth ? R_SQRT(p2 + LOG_EPS * LOG_EPS) : m2 + LOG_EPS;
+          REAL dlin = m1 - m2;
+          REAL dlog = R_LOG(s1) - R_LOG(s2);
+          bl = bl + (l2lin ? dlin * dlin : R_ABS(dlin));
+          bg = bg + (l2log ? dlog * dlog : R_ABS(dlog));
           if (dx) {
-            REAL dmag = gl * r_sign(m1 - m2) + gg * r_sign(dlog) / (m1 + LOG_EPS);
+            REAL sl = l2lin ? (REAL)2 * dlin : r_sign(dlin);
+            REAL sg = l2log ? (REAL)2 * dlog : r_sign(dlog);
             REAL sm = r_max(m1, (REAL)1e-8f);
-            gr[k] = dmag * r1[k] / sm;
-            gi[k] = dmag * i1[k] / sm;
+            if (!smooth) {
+              REAL dmag = gl * sl + gg * sg / (m1 + LOG_EPS);
+              gr[k] = dmag * r1[k] / sm;
+              gi[k] = dmag * i1[k] / sm;
+            } else {
+              /* the two calls' spectra: lin over max(m, 1e-8), log over the
+               * smooth magnitude twice (1/m_s from the log, X/m_s) */
+              REAL cl = gl * sl / sm, cg = gg * sg / s1 / s1;
+              gr[k] = cl * r1[k] + cg * r1[k];
+              gi[k] = cl * i1[k] + cg * i1[k];
+            }
           }
         }
         lin = lin + bl;
@@ -788,11 +838,12 @@ static double mss_core(const REAL* x, const REAL* tgt, int B, int T, const int* 
 }
 
 double FN(dgen_oracle_mss_fwd)(const float* x, const float* tgt, int B, int T, const int* sizes, int n_sizes,
-                               int hop_div, float w_lin, float w_log, float max_frames, float* loss_frames) {
+                               int hop_div, float w_lin, float w_log, float max_frames, int mode, float w_mse,
+                               float* loss_frames) {
   REAL* xr = to_real(x, (size_t)B * T);
   REAL* tr = to_real(tgt, (size_t)B * T);
   REAL* lf = (REAL*)malloc(sizeof(REAL) * T);
-  double tot = mss_core(xr, tr, B, T, sizes, n_sizes, hop_div, w_lin, w_log, max_frames, lf, NULL);
+  double tot = mss_core(xr, tr, B, T, sizes, n_sizes, hop_div, w_lin, w_log, max_frames, mode, w_mse, lf, NULL);
   if (loss_frames) to_float(lf, T, loss_frames);
   free(xr);
   free(tr);
@@ -803,22 +854,23 @@ double FN(dgen_oracle_mss_fwd)(const float* x, const float* tgt, int B, int T, c
 /* As dgen_oracle_mss_fwd with the prediction in this build's precision, so
  * finite differences can perturb it below fp32 resolution. */
 double FN(dgen_oracle_mss_fwd_real)(const REAL* x, const float* tgt, int B, int T, const int* sizes, int n_sizes,
-                                    int hop_div, float w_lin, float w_log, float max_frames) {
+                                    int hop_div, float w_lin, float w_log, float max_frames, int mode, float w_mse) {
   REAL* tr = to_real(tgt, (size_t)B * T);
   REAL* lf = (REAL*)malloc(sizeof(REAL) * T);
-  double tot = mss_core(x, tr, B, T, sizes, n_sizes, hop_div, w_lin, w_log, max_frames, lf, NULL);
+  double tot = mss_core(x, tr, B, T, sizes, n_sizes, hop_div, w_lin, w_log, max_frames, mode, w_mse, lf, NULL);
   free(tr);
   free(lf);
   return tot;
 }
 
 void FN(dgen_oracle_mss_bwd)(const float* x, const float* tgt, int B, int T, const int* sizes, int n_sizes,
-                             int hop_div, float w_lin, float w_log, float max_frames, float* dx_out) {
+                             int hop_div, float w_lin, float w_log, float max_frames, int mode, float w_mse,
+                             float* dx_out) {
   REAL* xr = to_real(x, (size_t)B * T);
   REAL* tr = to_real(tgt, (size_t)B * T);
   REAL* lf = (REAL*)malloc(sizeof(REAL) * T);
   REAL* dx = (REAL*)malloc(sizeof(REAL) * (size_t)B * T);
-  mss_core(xr, tr, B, T, sizes, n_sizes, hop_div, w_lin, w_log, max_frames, lf, dx);
+  mss_core(xr, tr, B, T, sizes, n_sizes, hop_div, w_lin, w_log, max_frames, mode, w_mse, lf, dx);
   to_float(dx, (size_t)B * T, dx_out);
   free(xr);
   free(tr);
@@ -835,7 +887,7 @@ double FN(dgen_oracle_harmonic_step)(const float* X, const REAL* P, const float*
                                      const float* tgt, int B, int F, int T, int K, int NF, int din, int hid,
                                      int layers, float sr, float hscale, float nscale, const int* sizes,
                                      int n_sizes, int hop_div, float w_lin, float w_log, float max_frames,
-                                     REAL* dP, float* y_out) {
+                                     int mode, float w_mse, REAL* dP, float* y_out) {
   const int NC = K + 2 + NF;
   const int M = B * F;
   REAL* ctrl = (REAL*)malloc(sizeof(REAL) * (size_t)M * NC);
@@ -849,13 +901,13 @@ double FN(dgen_oracle_harmonic_step)(const float* X, const REAL* P, const float*
   if (dP) {
     REAL* dy = (REAL*)malloc(sizeof(REAL) * (size_t)B * T);
     REAL* dc = (REAL*)malloc(sizeof(REAL) * (size_t)M * NC);
-    tot = mss_core(y, tr, B, T, sizes, n_sizes, hop_div, w_lin, w_log, max_frames, lf, dy);
+    tot = mss_core(y, tr, B, T, sizes, n_sizes, hop_div, w_lin, w_log, max_frames, mode, w_mse, lf, dy);
     synth_core(ctrl, f0, uv, B, F, T, K, NF, sr, sr, hscale, nscale, NULL, dy, dc);
     mlp_backward(X, P, dc, M, din, hid, layers, K, NF, dP);
     free(dy);
     free(dc);
   } else {
-    tot = mss_core(y, tr, B, T, sizes, n_sizes, hop_div, w_lin, w_log, max_frames, lf, NULL);
+    tot = mss_core(y, tr, B, T, sizes, n_sizes, hop_div, w_lin, w_log, max_frames, mode, w_mse, lf, NULL);
   }
   free(ctrl);
   free(y);

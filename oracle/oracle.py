@@ -54,14 +54,15 @@ def lib(name: str = "liboracle.so") -> ctypes.CDLL:
             _sig(L, "dgen_oracle_mlp_param_count" + sfx, [_c_int] * 4, _c_size)
             _sig(L, "dgen_oracle_mlp_fwd" + sfx, [_f32p, _f32p] + [_c_int] * 6 + [_f32p])
             _sig(L, "dgen_oracle_mlp_bwd" + sfx, [_f32p, _f32p, _f32p] + [_c_int] * 6 + [_f32p])
-            mss = [_f32p, _f32p, _c_int, _c_int, _i32p, _c_int, _c_int, _c_float, _c_float, _c_float]
+            mss = [_f32p, _f32p, _c_int, _c_int, _i32p, _c_int, _c_int, _c_float, _c_float, _c_float, _c_int,
+                   _c_float]
             _sig(L, "dgen_oracle_mss_fwd" + sfx, mss + [ctypes.c_void_p], ctypes.c_double)
             _sig(L, "dgen_oracle_mss_bwd" + sfx, mss + [_f32p])
             _sig(L, "dgen_oracle_mss_fwd_real" + sfx, [rp_(sfx), _f32p] + mss[2:], ctypes.c_double)
             rp = _f32p if sfx == "_f32" else np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
             _sig(L, "dgen_oracle_harmonic_step" + sfx,
                  [_f32p, rp, _f32p, _f32p, _f32p] + [_c_int] * 8 + [_c_float] * 3 + [_i32p, _c_int, _c_int]
-                 + [_c_float] * 3 + [ctypes.c_void_p, ctypes.c_void_p], ctypes.c_double)
+                 + [_c_float] * 3 + [_c_int, _c_float, ctypes.c_void_p, ctypes.c_void_p], ctypes.c_double)
             _sig(L, "dgen_oracle_adam" + sfx, [_f32p, _f32p, _f32p, _f32p, _c_size] + [_c_float] * 4 + [_c_int])
             vp = ctypes.c_void_p
             _sig(L, "dgen_oracle_biquad_fwd" + sfx, [_f32p, vp, rp, rp, _c_int, _c_int, _f32p])
@@ -221,28 +222,34 @@ def mlp_bwd(X, P, dctrl, M, din, hid, layers, K, NF, prec="f32"):
     return dP
 
 
+# loss-mode bits of the multi-scale loss (dgen_oracle.c MSS_*): the
+# magnitude and log-magnitude terms' lossMode .l2 (else .l1),
+# useSmoothLogMagnitude, useHannWindow: false
+MSS_L2_LIN, MSS_L2_LOG, MSS_SMOOTH_LOG, MSS_RECT_WINDOW = 1, 2, 4, 8
+
+
 def mss_fwd(x, tgt, B, T, sizes, hop_div, w_lin, w_log, max_frames, prec="f32", frames=False,
-            libname="liboracle.so"):
+            libname="liboracle.so", mode=0, w_mse=0.0):
     sizes = np.ascontiguousarray(sizes, np.int32)
     lf = np.zeros(T, np.float32) if frames else None
     ptr = lf.ctypes.data_as(ctypes.c_void_p) if frames else None
     tot = _fn("dgen_oracle_mss_fwd", prec, libname)(_f(x), _f(tgt), B, T, sizes, len(sizes), hop_div, w_lin,
-                                                    w_log, max_frames, ptr)
+                                                    w_log, max_frames, int(mode), float(w_mse), ptr)
     return (tot, lf) if frames else tot
 
 
-def mss_fwd_x64(x, tgt, B, T, sizes, hop_div, w_lin, w_log, max_frames):
+def mss_fwd_x64(x, tgt, B, T, sizes, hop_div, w_lin, w_log, max_frames, mode=0, w_mse=0.0):
     """fp64 spectral loss with a float64 prediction (finite differences)."""
     sizes = np.ascontiguousarray(sizes, np.int32)
     return lib().dgen_oracle_mss_fwd_real_f64(np.ascontiguousarray(x, np.float64), _f(tgt), B, T, sizes, len(sizes),
-                                              hop_div, w_lin, w_log, max_frames)
+                                              hop_div, w_lin, w_log, max_frames, int(mode), float(w_mse))
 
 
-def mss_bwd(x, tgt, B, T, sizes, hop_div, w_lin, w_log, max_frames, prec="f32"):
+def mss_bwd(x, tgt, B, T, sizes, hop_div, w_lin, w_log, max_frames, prec="f32", mode=0, w_mse=0.0):
     sizes = np.ascontiguousarray(sizes, np.int32)
     dx = np.zeros((B, T), np.float32)
     _fn("dgen_oracle_mss_bwd", prec)(_f(x), _f(tgt), B, T, sizes, len(sizes), hop_div, w_lin, w_log,
-                                     max_frames, dx)
+                                     max_frames, int(mode), float(w_mse), dx)
     return dx
 
 
@@ -265,7 +272,8 @@ def harmonic_step(cfg, X, P, f0, uv, tgt, grad=True, want_y=False, prec="f64", l
     fn = _fn("dgen_oracle_harmonic_step", prec, libname)
     loss = fn(_f(X), P, _f(f0), _f(uv), _f(tgt), cfg.B, cfg.F, cfg.T, cfg.K, cfg.NF, cfg.din, cfg.hidden,
               cfg.layers, cfg.sr, cfg.hscale, cfg.nscale, sizes, len(sizes), cfg.hop_div, cfg.w_lin, cfg.w_log,
-              float(cfg.T), dP.ctypes.data_as(ctypes.c_void_p) if grad else None,
+              float(cfg.T), int(getattr(cfg, "mss_mode", 0)), float(getattr(cfg, "w_mse", 0.0)),
+              dP.ctypes.data_as(ctypes.c_void_p) if grad else None,
               y.ctypes.data_as(ctypes.c_void_p) if want_y else None)
     return loss, dP, y
 

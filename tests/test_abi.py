@@ -4,17 +4,21 @@ through status codes and dgen_hip_last_error() instead of aborting."""
 import ctypes
 import os
 import re
+import subprocess
+
+import numpy as np
 
 import dgen_hip
 from dgen_hip import runtime as R
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "dgen_hip.h")
+PROCESS_HEADER = os.path.join(ROOT, "include", "dgen_process_v1.h")
 
 
-def declared():
-    text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(dgen_hip_\w+)\s*\(", text, re.M)))
+def declared(header=HEADER, prefix="dgen_hip_"):
+    text = open(header).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(" + prefix + r"\w+)\s*\(", text, re.M)))
 
 
 def test_header_declares_the_runtime_interface():
@@ -27,8 +31,35 @@ def test_header_declares_the_runtime_interface():
 
 def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(R.LIB_PATH)
-    missing = [n for n in declared() if not hasattr(lib, n)]
+    missing = [n for n in declared() + declared(PROCESS_HEADER, "dgen_") if not hasattr(lib, n)]
     assert not missing, missing
+
+
+def test_process_header_declares_the_reference_exports():
+    # dgen_runtime.h:283-291: exactly these two symbols
+    assert declared(PROCESS_HEADER, "dgen_") == sorted(R.PROCESS_V1_SYMBOLS)
+
+
+def test_process_exports_unbound_return_silence_and_a_message():
+    L = dgen_hip.load_library()
+    assert L.dgen_hip_process_memory_size() == 0
+    out = np.ones((1, 32), np.float32)
+    state = np.zeros(1024, np.float32)
+    # nothing bound: the call returns (void), leaves the state block alone
+    got = R.process_v1([], 1, 32, state)
+    assert b"no schedule bound" in L.dgen_hip_last_error()
+    assert not np.any(state) and got.shape == out.shape
+    L.dgen_set_param_value_v1(3, 1.0)  # the reference C backend's no-op
+    assert L.dgen_hip_process_bind(None, 0, 16) == 0  # unbinding is always allowed
+
+
+def test_a_c_host_resolves_the_process_exports_by_name(tmp_path):
+    exe = tmp_path / "process_host"
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"),
+                    os.path.join(ROOT, "tests", "process_host.c"), "-o", str(exe), "-ldl"], check=True)
+    r = subprocess.run([str(exe), R.LIB_PATH], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, (r.returncode, r.stdout, r.stderr)
+    assert "no schedule bound" in r.stdout
 
 
 def test_kernel_class_ids_match_header():

@@ -168,3 +168,27 @@ def test_training_forward_through_lds_tiles_equals_the_per_frame_kernel():
         rt.close()
     assert "svf_seq" in labels
     np.testing.assert_array_equal(y, one)
+
+
+@pytest.mark.parametrize("B,T,chunk", [(64, 4096 + 32, 256), (128, 48000, 256)])
+def test_saturating_training_loss_covers_a_ragged_last_chunk(B, T, chunk):
+    """The saturating training forward on LDS tiles with T not a multiple of
+    the chunk length: the last chunk's loss partial (T mod L frames) is
+    written, so the loss is the whole signal's (against the oracle) and the
+    gradient is unchanged."""
+    cfg = SvfConfig(B=B, T=T, saturating=True)
+    print(f"case B={B} T={T} chunk={chunk}", flush=True)
+    s = SvfSession(cfg, optimizer=False, chunk=chunk)
+    try:
+        s.step()
+        loss, labels = s.loss(), [op.label for op in s.program.ops]
+        g = s.rt.read("grads").astype(np.float64)
+    finally:
+        s.close()
+    assert "svf_seq" in labels
+    a = oracle_args(cfg, s.params0)
+    l64, g64, _, _ = O.svf_step(s.x, tgt=s.target, **a)
+    l32, _, _, _ = O.svf_step(s.x, tgt=s.target, prec="f32", **a)
+    print(f"loss HIP {loss:.8e}, fp64 oracle {l64:.8e}, fp32 oracle {l32:.8e}")
+    assert abs(loss - l64) <= 2.0 * abs(l32 - l64) + 1e-5 * abs(l64)
+    assert np.linalg.norm(g - g64) <= 1e-4 * np.linalg.norm(g64)

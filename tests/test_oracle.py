@@ -110,17 +110,20 @@ def test_phase_checkpoints_follow_the_phasor():
 
 
 # ---------------------------------------------------------------- spectral loss
-def np_mss(x, tgt, sizes, w_lin, w_log, max_frames):
+def np_mss(x, tgt, sizes, w_lin, w_log, max_frames, mode=0, w_mse=0.0):
     """Multi-scale spectral loss per frame with numpy.fft: windows end at the
-    hop frame (zero before 0), symmetric Hann, bins 0..N/2, L1 on magnitude
-    and on log(magnitude + 1e-8), batch mean, / maxFrames."""
+    hop frame (zero before 0), symmetric Hann (all ones with
+    MSS_RECT_WINDOW), bins 0..N/2; the magnitude term and the term on
+    log(magnitude + 1e-8) (with MSS_SMOOTH_LOG on 0.5 log(|X|^2 + 1e-16)),
+    each L1 or (MSS_L2_*) L2; batch mean, / maxFrames; plus the time-domain
+    term w_mse * sum_b (x - tgt)^2 / B per frame."""
     x = np.asarray(x, np.float64)
     tgt = np.asarray(tgt, np.float64)
     B, T = x.shape
-    lf = np.zeros(T)
+    lf = w_mse * ((x - tgt) ** 2).sum(0) / B
     for N in sizes:
         H = N // 4
-        hann = 0.5 * (1 - np.cos(2 * np.pi * np.arange(N) / (N - 1)))
+        hann = np.ones(N) if mode & O.MSS_RECT_WINDOW else 0.5 * (1 - np.cos(2 * np.pi * np.arange(N) / (N - 1)))
         frames = np.arange(0, T, H)
         idx = frames[:, None] - (N - 1) + np.arange(N)[None, :]
         valid = idx >= 0
@@ -128,12 +131,21 @@ def np_mss(x, tgt, sizes, w_lin, w_log, max_frames):
         lin = np.zeros(len(frames))
         lg = np.zeros(len(frames))
         for b in range(B):
-            X = np.abs(np.fft.rfft(np.where(valid, x[b][idc], 0.0) * hann, axis=1))
-            Y = np.abs(np.fft.rfft(np.where(valid, tgt[b][idc], 0.0) * hann, axis=1))
-            lin += np.abs(X - Y).sum(1)
-            lg += np.abs(np.log(X + 1e-8) - np.log(Y + 1e-8)).sum(1)
+            X = np.fft.rfft(np.where(valid, x[b][idc], 0.0) * hann, axis=1)
+            Y = np.fft.rfft(np.where(valid, tgt[b][idc], 0.0) * hann, axis=1)
+            dlin = np.abs(X) - np.abs(Y)
+            if mode & O.MSS_SMOOTH_LOG:
+                dlog = 0.5 * (np.log(np.abs(X) ** 2 + 1e-16) - np.log(np.abs(Y) ** 2 + 1e-16))
+            else:
+                dlog = np.log(np.abs(X) + 1e-8) - np.log(np.abs(Y) + 1e-8)
+            lin += (dlin ** 2 if mode & O.MSS_L2_LIN else np.abs(dlin)).sum(1)
+            lg += (dlog ** 2 if mode & O.MSS_L2_LOG else np.abs(dlog)).sum(1)
         lf[frames] += (lin / B / max_frames) * (w_lin / len(sizes)) + (lg / B / max_frames) * (w_log / len(sizes))
     return lf
+
+
+MODES = [0, O.MSS_L2_LIN | O.MSS_L2_LOG, O.MSS_SMOOTH_LOG, O.MSS_L2_LOG | O.MSS_SMOOTH_LOG | O.MSS_RECT_WINDOW,
+         O.MSS_RECT_WINDOW]
 
 
 @pytest.fixture(scope="module")
@@ -145,27 +157,49 @@ def signals():
     return B, T, x, t
 
 
-def test_spectral_loss_matches_numpy_fft(signals):
+@pytest.mark.parametrize("mode", MODES)
+def test_spectral_loss_matches_numpy_fft(signals, mode):
     B, T, x, t = signals
     sizes = (512, 256, 128, 64)
-    tot, lf = O.mss_fwd(x, t, B, T, sizes, 4, 1.0, 0.5, T, prec="f64", frames=True)
-    ref = np_mss(x, t, sizes, 1.0, 0.5, T)
+    w_mse = 0.25 if mode else 0.0
+    tot, lf = O.mss_fwd(x, t, B, T, sizes, 4, 1.0, 0.5, T, prec="f64", frames=True, mode=mode, w_mse=w_mse)
+    ref = np_mss(x, t, sizes, 1.0, 0.5, T, mode=mode, w_mse=w_mse)
     assert abs(tot - ref.sum()) / ref.sum() < 1e-6
     np.testing.assert_allclose(lf, ref, rtol=1e-5, atol=1e-12)
 
 
-def test_spectral_loss_of_identical_signals_is_zero(signals):
+@pytest.mark.parametrize("mode", [O.MSS_SMOOTH_LOG, O.MSS_SMOOTH_LOG | O.MSS_L2_LOG, 0])
+def test_spectral_log_terms_near_the_epsilon(mode):
+    """Signals of amplitude ~1e-9 put |X| near the 1e-8 epsilon, where the
+    smooth log magnitude 0.5 log(|X|^2 + eps^2) and log(|X| + eps) differ by
+    up to log(sqrt 2): the oracle follows the mode's formula there."""
+    rng = np.random.default_rng(17)
+    B, T = 2, 1024
+    x = (1e-9 * rng.standard_normal((B, T))).astype(np.float32)
+    t = (3e-9 * rng.standard_normal((B, T))).astype(np.float32)
+    sizes = (256, 64)
+    tot, lf = O.mss_fwd(x, t, B, T, sizes, 4, 0.0, 1.0, T, prec="f64", frames=True, mode=mode)
+    ref = np_mss(x, t, sizes, 0.0, 1.0, T, mode=mode)
+    other = np_mss(x, t, sizes, 0.0, 1.0, T, mode=mode ^ O.MSS_SMOOTH_LOG)
+    assert abs(tot - ref.sum()) / ref.sum() < 1e-6
+    assert abs(other.sum() - ref.sum()) / ref.sum() > 1e-3  # the two forms differ here (1000x the bar)
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_spectral_loss_of_identical_signals_is_zero(signals, mode):
     # TensorFFTTests.swift:1057-1098: same signal -> zero loss per bin
     B, T, x, _ = signals
     sizes = (256, 64)
-    assert O.mss_fwd(x, x, B, T, sizes, 4, 1.0, 0.5, T) == 0.0
-    assert np.all(O.mss_bwd(x, x, B, T, sizes, 4, 1.0, 0.5, T) == 0.0)
+    assert O.mss_fwd(x, x, B, T, sizes, 4, 1.0, 0.5, T, mode=mode, w_mse=0.5) == 0.0
+    assert np.all(O.mss_bwd(x, x, B, T, sizes, 4, 1.0, 0.5, T, mode=mode, w_mse=0.5) == 0.0)
 
 
-def test_spectral_gradient_matches_finite_differences(signals):
+@pytest.mark.parametrize("mode", MODES)
+def test_spectral_gradient_matches_finite_differences(signals, mode):
     B, T, x, t = signals
     sizes = (256, 128, 64)
-    g = O.mss_bwd(x, t, B, T, sizes, 4, 1.0, 0.5, T, prec="f64").astype(np.float64)
+    w_mse = 0.25 if mode else 0.0
+    g = O.mss_bwd(x, t, B, T, sizes, 4, 1.0, 0.5, T, prec="f64", mode=mode, w_mse=w_mse).astype(np.float64)
     rng = np.random.default_rng(3)
     x64 = x.astype(np.float64)
     # directional derivatives with a step far below the distance to the
@@ -173,11 +207,22 @@ def test_spectral_gradient_matches_finite_differences(signals):
     for _ in range(3):
         v = rng.standard_normal((B, T))
         eps = 1e-7
-        lp = O.mss_fwd_x64(x64 + eps * v, t, B, T, sizes, 4, 1.0, 0.5, T)
-        lm = O.mss_fwd_x64(x64 - eps * v, t, B, T, sizes, 4, 1.0, 0.5, T)
+        lp = O.mss_fwd_x64(x64 + eps * v, t, B, T, sizes, 4, 1.0, 0.5, T, mode=mode, w_mse=w_mse)
+        lm = O.mss_fwd_x64(x64 - eps * v, t, B, T, sizes, 4, 1.0, 0.5, T, mode=mode, w_mse=w_mse)
         fd = (lp - lm) / (2 * eps)
         an = float((g * v).sum())
         assert abs(fd - an) / abs(an) < 1e-5, (fd, an)
+
+
+def test_mse_term_closed_form(signals):
+    """Trainer.swift:547-551: w * sum_b (x - t)^2 / B per frame; gradient
+    2 w (x - t) / B."""
+    B, T, x, t = signals
+    tot, lf = O.mss_fwd(x, t, B, T, (64,), 4, 0.0, 0.0, T, prec="f64", frames=True, w_mse=0.75)
+    d = x.astype(np.float64) - t
+    np.testing.assert_allclose(lf, 0.75 * (d * d).sum(0) / B, rtol=1e-6)
+    g = O.mss_bwd(x, t, B, T, (64,), 4, 0.0, 0.0, T, prec="f64", w_mse=0.75)
+    np.testing.assert_allclose(g, 0.75 * 2 * d / B, rtol=1e-6)
 
 
 # ---------------------------------------------------------------- control network + whole step
