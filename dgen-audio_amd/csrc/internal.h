@@ -13,6 +13,14 @@
 
 namespace dgen {
 
+// A generic UOp block as loaded for a context (uop_render.cpp renders it,
+// the runtime compiles and loads it): the kernel and what its launch needs.
+struct BlockInfo {
+  hipFunction_t fn = nullptr;
+  int dispatch = 0, n = 0, frame_order = 0;
+  int64_t max_cell = -1;  // largest cell addressed directly
+};
+
 struct Launch {
   hipStream_t stream = nullptr;
   float* arena = nullptr;       // device arena base
@@ -23,6 +31,8 @@ struct Launch {
   bool dry = false;             // validate only
   float host_sr = 0.f;          // host sample rate of this run; 0: each op's own
   bool reset = false;           // streaming classes start from zero state (else the state cells)
+  const BlockInfo* blocks = nullptr;  // the context's generic UOp blocks
+  size_t n_blocks = 0;
 };
 
 // Sample rate a phase increment divides by: the run's host sample rate when
@@ -147,6 +157,15 @@ int launch_svf_fwd(const Launch&, const dgen_hip_op&);
 int launch_svf_seq(const Launch&, const dgen_hip_op&);
 int launch_svf_adj_chunk(const Launch&, const dgen_hip_op&);
 int launch_svf_bwd(const Launch&, const dgen_hip_op&);
+
+// Generic UOp blocks (uop_render.cpp): the HIP C++ source of a block list,
+// and the largest cell a block addresses directly (-1: none).
+}  // namespace dgen
+#include <string>
+namespace dgen {
+int render_blocks(const dgen_hip_block* blocks, uint32_t n, std::string& source);
+int64_t block_max_cell(const dgen_hip_block& b);
+int launch_uop_block(const Launch&, const dgen_hip_op&);
 
 // (segment, slot) entries listed per control row by the static row schedule
 // (a row is read by at most this many synth segments: 3 at a control hop of

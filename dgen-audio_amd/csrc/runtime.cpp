@@ -14,6 +14,7 @@
 // - run() is synchronous like MetalCompiledKernel.run (commit+wait,
 //   MetalRuntime.swift:334-337).
 #include <hip/hip_runtime.h>
+#include <hip/hiprtc.h>
 
 #include <algorithm>
 #include <cstdarg>
@@ -87,6 +88,7 @@ static Launcher launcher_for(uint32_t k) {
     case DGEN_HIP_K_SVF_ADJ_CHUNK: return launch_svf_adj_chunk;
     case DGEN_HIP_K_SVF_BWD: return launch_svf_bwd;
     case DGEN_HIP_K_SPLIT_BF16: return launch_split_bf16;
+    case DGEN_HIP_K_UOP_BLOCK: return launch_uop_block;
     default: return nullptr;
   }
 }
@@ -122,6 +124,9 @@ struct dgen_hip_ctx {
   bool reset_next = false;
   // a dgen_hip_run_async whose declared outputs the next dgen_hip_sync downloads
   bool outputs_pending = false;
+  // generic UOp blocks (dgen_hip_set_blocks): their loaded module and kernels
+  hipModule_t blk_module = nullptr;
+  std::vector<BlockInfo> blocks;
 };
 
 static int set_device(dgen_hip_ctx* c) {
@@ -137,6 +142,8 @@ static Launch make_launch(dgen_hip_ctx* c, hipStream_t s, uint32_t frames, bool 
   L.frames = frames;
   L.device = c->device;
   L.cu_count = c->cu_count;
+  L.blocks = c->blocks.empty() ? nullptr : c->blocks.data();
+  L.n_blocks = c->blocks.size();
   L.dry = dry;
   L.host_sr = c->host_sr;
   L.reset = c->reset_next;
@@ -286,6 +293,7 @@ int dgen_hip_destroy(dgen_hip_ctx* c) {
   if (c->s0) (void)hipStreamSynchronize(c->s0);
   if (c->s1) (void)hipStreamSynchronize(c->s1);
   release_arena(c);
+  if (c->blk_module) (void)hipModuleUnload(c->blk_module);
   if (c->ev_start) (void)hipEventDestroy(c->ev_start);
   if (c->ev_side) (void)hipEventDestroy(c->ev_side);
   if (c->ev_fork) (void)hipEventDestroy(c->ev_fork);
@@ -417,6 +425,7 @@ static FrameArg frame_arg(uint32_t k) {
     case DGEN_HIP_K_STREAM_SVF: return {10, true};
     case DGEN_HIP_K_SVF_ADJ_CHUNK: return {8, false};
     case DGEN_HIP_K_SVF_BWD: return {11, false};
+    case DGEN_HIP_K_UOP_BLOCK: return {7, true};
     default: return {-1, false};
   }
 }
@@ -726,6 +735,97 @@ int dgen_hip_time_op(dgen_hip_ctx* c, uint32_t frame_count, uint32_t op_index, i
   return rc;
 }
 
+
+// ---- generic UOp blocks: hiprtc compile with a per-process cache ---------
+namespace {
+std::mutex g_rtc_mu;
+std::vector<std::pair<std::string, std::vector<char>>> g_rtc_cache;  // source -> code object
+}  // namespace
+
+// Compile HIP C++ for gfx950: packed fp32 off, as every kernel here, and no
+// contraction of a*b+c into fma, so each UOp rounds as the reference's fp32
+// node does (a contracted (f/sr)*n - floor(...) moves a phase by half an ulp
+// of the product: up to 2.4e-4 revolutions at n = 65536).
+static int rtc_compile(const std::string& src, std::vector<char>& code) {
+  {
+    std::lock_guard<std::mutex> lk(g_rtc_mu);
+    for (const auto& e : g_rtc_cache)
+      if (e.first == src) {
+        code = e.second;
+        return 0;
+      }
+  }
+  hiprtcProgram prog;
+  if (hiprtcCreateProgram(&prog, src.c_str(), "dgen_blocks.hip", 0, nullptr, nullptr) != HIPRTC_SUCCESS)
+    return fail(DGEN_HIP_E_INVALID, "blocks: hiprtcCreateProgram failed");
+  const char* opts[] = {"--offload-arch=gfx950", "-O3",           "-ffp-contract=off", "-Xclang",
+                        "-target-feature",       "-Xclang",       "-packed-fp32-ops"};
+  const hiprtcResult r = hiprtcCompileProgram(prog, 7, opts);
+  if (r != HIPRTC_SUCCESS) {
+    size_t n = 0;
+    hiprtcGetProgramLogSize(prog, &n);
+    std::string log(n + 1, '\0');
+    if (n) hiprtcGetProgramLog(prog, &log[0]);
+    hiprtcDestroyProgram(&prog);
+    return fail(DGEN_HIP_E_INVALID, "blocks: compile failed: %s", log.c_str());
+  }
+  size_t n = 0;
+  hiprtcGetCodeSize(prog, &n);
+  code.assign(n, 0);
+  hiprtcGetCode(prog, code.data());
+  hiprtcDestroyProgram(&prog);
+  std::lock_guard<std::mutex> lk(g_rtc_mu);
+  g_rtc_cache.emplace_back(src, code);
+  return 0;
+}
+
+int dgen_hip_render_blocks(const dgen_hip_block* blocks, uint32_t n, int compile, char* buf, size_t cap, size_t* len) {
+  std::string src;
+  int rc = render_blocks(blocks, n, src);
+  if (rc) return rc;
+  if (len) *len = src.size();
+  if (buf && cap) {
+    const size_t k = std::min(cap - 1, src.size());
+    std::memcpy(buf, src.data(), k);
+    buf[k] = '\0';
+  }
+  if (compile) {
+    std::vector<char> code;
+    if ((rc = rtc_compile(src, code))) return rc;
+  }
+  return 0;
+}
+
+int dgen_hip_set_blocks(dgen_hip_ctx* c, const dgen_hip_block* blocks, uint32_t n) {
+  if (!c) return fail(DGEN_HIP_E_INVALID, "set_blocks: null context");
+  std::string src;
+  int rc = render_blocks(blocks, n, src);
+  if (rc) return rc;
+  std::vector<char> code;
+  if (n && (rc = rtc_compile(src, code))) return rc;
+  if ((rc = set_device(c))) return rc;
+  DGEN_HIP_TRY(hipStreamSynchronize(c->s0));
+  DGEN_HIP_TRY(hipStreamSynchronize(c->s1));
+  drop_graph(c);
+  if (c->blk_module) {
+    (void)hipModuleUnload(c->blk_module);
+    c->blk_module = nullptr;
+  }
+  c->blocks.clear();
+  if (!n) return 0;
+  DGEN_HIP_TRY(hipModuleLoadData(&c->blk_module, code.data()));
+  c->blocks.resize(n);
+  for (uint32_t i = 0; i < n; ++i) {
+    BlockInfo& b = c->blocks[i];
+    const std::string name = "dgen_block_" + std::to_string(i);
+    DGEN_HIP_TRY(hipModuleGetFunction(&b.fn, c->blk_module, name.c_str()));
+    b.dispatch = blocks[i].dispatch;
+    b.n = blocks[i].dispatch_n;
+    b.frame_order = blocks[i].frame_order;
+    b.max_cell = block_max_cell(blocks[i]);
+  }
+  return 0;
+}
 
 // ---- the reference-named process-function exports (dgen_process_v1.h) ----
 // One bound schedule per process, as the reference loads one compiled graph

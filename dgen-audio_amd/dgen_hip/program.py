@@ -42,6 +42,8 @@ class Program:
     max_frames: int = 0
     output_cell: str = ""
     meta: dict = field(default_factory=dict)
+    # generic UOp blocks (dgen_hip.uop.Block) the DGEN_HIP_K_UOP_BLOCK ops index
+    blocks: list = field(default_factory=list)
 
     def alloc(self, name: str, n: int) -> int:
         if name in self.cells:

@@ -62,6 +62,7 @@ K_SVF_ADJ_CHUNK = 36
 K_SVF_BWD = 37
 K_STREAM_SVF = 38
 K_SPLIT_BF16 = 39
+K_UOP_BLOCK = 40
 
 KERNEL_NAMES = {v: k[2:].lower() for k, v in globals().items() if k.startswith("K_")}
 
@@ -75,6 +76,7 @@ EXPORTED_SYMBOLS = (
     "dgen_hip_profile", "dgen_hip_time_runs", "dgen_hip_time_op", "dgen_hip_run_op", "dgen_hip_set_outputs",
     "dgen_hip_host_outputs", "dgen_hip_set_sample_rate", "dgen_hip_biquad_forward_noalloc",
     "dgen_hip_set_process_ports", "dgen_hip_process_v1", "dgen_hip_process_bind", "dgen_hip_process_memory_size",
+    "dgen_hip_set_blocks", "dgen_hip_render_blocks",
 )
 # the reference-named process-function exports (include/dgen_process_v1.h)
 PROCESS_V1_SYMBOLS = ("dgen_process_v1", "dgen_set_param_value_v1")
@@ -154,6 +156,9 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
                              ctypes.POINTER(ctypes.POINTER(ctypes.c_float)), u32, vp,
                              ctypes.POINTER(DGenProcessContextV1), vp], None),
         "dgen_set_param_value_v1": ([ctypes.c_int32, ctypes.c_float], None),
+        "dgen_hip_set_blocks": ([vp, vp, u32], i32),
+        "dgen_hip_render_blocks": ([vp, u32, i32, ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)],
+                                   i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -203,6 +208,12 @@ class HIPLazyRuntime:
             for j, a in enumerate(op.farg):
                 ops[i].farg[j] = float(a)
         self._ops = ops
+        if program.blocks:
+            # generic UOp blocks: rendered, compiled and loaded before the
+            # schedule that launches them is configured
+            from .uop import SerializedBlocks
+            self._blocks = SerializedBlocks(program.blocks)
+            _check(self.L.dgen_hip_set_blocks(ctx, self._blocks.array, self._blocks.n), "dgen_hip_set_blocks")
         # Static ops run inside configure and may read data cells, so data
         # staged before configure would be lost; the program's static ops only
         # read constants, and inputs are written afterwards via write().

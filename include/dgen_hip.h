@@ -400,6 +400,18 @@ enum dgen_hip_kernel {
    * arg: [0]=src [1]=planes cell (3*K8*N*4 floats, 16-byte aligned) [2]=K
    *      [3]=N [4]=ld_k [5]=ld_n */
   DGEN_HIP_K_SPLIT_BF16 = 39,
+
+  /* One generic UOp block (dgen_hip_set_blocks): the kernel the renderer
+   * generated for it, launched with its dispatch mode's grid
+   * (DispatchMode.threadCount, Renderer.swift:71-86) for the run's frame
+   * count.  Runs any frame_count up to arg[7].
+   * arg: [0]=block index [1]=tape cell ([slots][frames], `t`) or -1
+   *      [2]=tape slots [3]=outputs cell ([channels][frames]) or -1
+   *      [4]=output channels [5]=inputs cell ([channels][frames]) or -1
+   *      [6]=input channels [7]=frames the tape/outputs/inputs cells hold
+   * farg: [0]=the graph's sample rate (the hostSampleRate UOp; a run's host
+   *       rate replaces it) */
+  DGEN_HIP_K_UOP_BLOCK = 40,
 };
 
 /* GEMM epilogues */
@@ -429,6 +441,126 @@ typedef struct dgen_hip_op {
   float farg[DGEN_HIP_OP_NFARG];
 } dgen_hip_op;
 
+/* ---- generic UOp blocks ------------------------------------------------
+ * The compiler's fused blocks as it hands them to a renderer: BlockUOps
+ * (Renderer.swift:3-24) = UOps (UOps.swift:17-138) + frame order + temporality
+ * + dispatch mode.  dgen_hip_set_blocks renders them to HIP C++ the way the
+ * Metal renderer renders MSL (prepareSchedule's range guard, frame loop and
+ * hop check, MetalRenderer.swift:787-938; per-UOp emission :1316-1720),
+ * compiles them with hiprtc for the context's device and loads them; each
+ * DGEN_HIP_K_UOP_BLOCK op of the schedule launches one.  This is the path for
+ * blocks no kernel class pattern-matches. */
+
+/* An operand (the reference's Lazy, UOps.swift:1-7). */
+enum dgen_hip_lazy_kind {
+  DGEN_HIP_LAZY_EMPTY = 0,
+  DGEN_HIP_LAZY_CONST = 1,      /* .constant: value */
+  DGEN_HIP_LAZY_VAR = 2,        /* .variable: a kernel-local value, id = VarID */
+  DGEN_HIP_LAZY_GLOBAL = 3,     /* .global / a variable in ctx.globals: id = its tape slot (getGlobalId) */
+  DGEN_HIP_LAZY_FRAME_COUNT = 4 /* the variable -1: the run's frame count */
+};
+typedef struct dgen_hip_lazy {
+  int32_t kind; /* enum dgen_hip_lazy_kind */
+  int32_t id;
+  float value;
+  int32_t reserved;
+} dgen_hip_lazy;
+
+/* UOp operations, in the reference's order (Op, UOps.swift:17-138).  Cells,
+ * channels, counts and steps go in imm[0] (threadgroupArrayDecl: imm[0] the
+ * scratch id, imm[1] its size). */
+enum dgen_hip_uop_op {
+  DGEN_HIP_UOP_NOP = 0,          /* view ops and markers: no code */
+  DGEN_HIP_UOP_LOAD = 1,         /* value = memory[imm0] */
+  DGEN_HIP_UOP_STORE,            /* memory[imm0] = a */
+  DGEN_HIP_UOP_DELAY1,           /* value = memory[imm0]; memory[imm0] = a */
+  DGEN_HIP_UOP_MUTATE,           /* a = b */
+  DGEN_HIP_UOP_ADD, DGEN_HIP_UOP_SUB, DGEN_HIP_UOP_MUL, DGEN_HIP_UOP_DIV,
+  DGEN_HIP_UOP_ABS, DGEN_HIP_UOP_SIGN, DGEN_HIP_UOP_SIN, DGEN_HIP_UOP_COS,
+  DGEN_HIP_UOP_AND, DGEN_HIP_UOP_OR, DGEN_HIP_UOP_XOR,
+  DGEN_HIP_UOP_TAN, DGEN_HIP_UOP_ATAN, DGEN_HIP_UOP_TANH, DGEN_HIP_UOP_EXP, DGEN_HIP_UOP_LOG,
+  DGEN_HIP_UOP_LOG10, DGEN_HIP_UOP_SQRT, DGEN_HIP_UOP_POW, DGEN_HIP_UOP_ATAN2, DGEN_HIP_UOP_MOD,
+  DGEN_HIP_UOP_GT, DGEN_HIP_UOP_GTE, DGEN_HIP_UOP_LTE, DGEN_HIP_UOP_LT, DGEN_HIP_UOP_EQ,
+  DGEN_HIP_UOP_MIN, DGEN_HIP_UOP_MAX, DGEN_HIP_UOP_FLOOR, DGEN_HIP_UOP_CEIL, DGEN_HIP_UOP_ROUND,
+  DGEN_HIP_UOP_NOISE,            /* xorshift32 on memory[imm0]'s bits, value in [0, 1) */
+  DGEN_HIP_UOP_MEMORY_READ,      /* value = memory[imm0 + a] */
+  DGEN_HIP_UOP_MEMORY_WRITE,     /* memory[imm0 + a] = b */
+  DGEN_HIP_UOP_MEMORY_ACCUMULATE,/* atomic memory[imm0 + a] += b */
+  DGEN_HIP_UOP_SIMD_BROADCAST_LOAD, /* as MEMORY_READ */
+  DGEN_HIP_UOP_BROADCAST_SCALAR, /* value = a */
+  DGEN_HIP_UOP_BEGIN_IF,         /* if (a) { */
+  DGEN_HIP_UOP_GSWITCH,          /* value = a > 0 ? b : c */
+  DGEN_HIP_UOP_SELECTOR,         /* value = options[ceil(a) - 1] (list), 0 outside */
+  DGEN_HIP_UOP_END_IF,
+  DGEN_HIP_UOP_DEFINE_GLOBAL,    /* a = the global (GLOBAL operand) this block defines */
+  DGEN_HIP_UOP_LOAD_GLOBAL,      /* no code: globals are read through their operands */
+  DGEN_HIP_UOP_BEGIN_LOOP,       /* for (i = 0; i < a; i += imm0 (1 if 0)), negative step reverses */
+  DGEN_HIP_UOP_BEGIN_FOR_LOOP,   /* for (a = 0; a < b; a++), a a VAR operand */
+  DGEN_HIP_UOP_BEGIN_REVERSE_LOOP, /* for (i = a - 1; i >= 0; i--) */
+  DGEN_HIP_UOP_END_LOOP,
+  DGEN_HIP_UOP_BEGIN_RANGE,      /* if (id >= a && id < b) { */
+  DGEN_HIP_UOP_END_RANGE,
+  DGEN_HIP_UOP_BEGIN_PARALLEL_RANGE, /* for (value = 0; value < imm0; value++) */
+  DGEN_HIP_UOP_END_PARALLEL_RANGE,
+  DGEN_HIP_UOP_SET_THREAD_COUNT_SCALE, /* no code (the dispatch mode carries it) */
+  DGEN_HIP_UOP_SET_FRAME_INDEX,  /* the frame index of later outputs and tape accesses = a */
+  DGEN_HIP_UOP_OUTPUT,           /* outputs[imm0][frame] = a (non-finite -> 0) */
+  DGEN_HIP_UOP_INPUT,            /* value = inputs[imm0][frame] */
+  DGEN_HIP_UOP_FRAME_COUNT,      /* value = frameCount (no code with an EMPTY value) */
+  DGEN_HIP_UOP_HOST_SAMPLE_RATE, /* value = the run's host sample rate */
+  DGEN_HIP_UOP_FRAME_INDEX,      /* value = the frame (thread in parallel blocks, loop index in sequential) */
+  DGEN_HIP_UOP_THREAD_INDEX,     /* value = the thread index */
+  DGEN_HIP_UOP_LOAD_TAPE,        /* value = tape a at frame b, 0 outside [0, frameCount) */
+  DGEN_HIP_UOP_CAST,             /* value = (imm0 ? int : float) a */
+  DGEN_HIP_UOP_IDENTITY,         /* value = a */
+  DGEN_HIP_UOP_DECLARE_VAR,      /* value = a */
+  DGEN_HIP_UOP_BEGIN_HOP_CHECK,  /* if (a == 0) { */
+  DGEN_HIP_UOP_END_HOP_CHECK,
+  DGEN_HIP_UOP_THREADGROUP_ARRAY_DECL, /* __shared__ float scratch_imm0[imm1] */
+  DGEN_HIP_UOP_THREADGROUP_READ, /* value = scratch_imm0[a] */
+  DGEN_HIP_UOP_THREADGROUP_WRITE,/* scratch_imm0[a] = b */
+  DGEN_HIP_UOP_THREADGROUP_BARRIER
+};
+
+typedef struct dgen_hip_uop {
+  int32_t op;        /* enum dgen_hip_uop_op */
+  int32_t int_typed; /* UOp.scalarType == .int: the value is declared int */
+  dgen_hip_lazy value;
+  dgen_hip_lazy a, b, c;
+  int64_t imm[2];
+  const dgen_hip_lazy* list; /* SELECTOR options */
+  uint32_t n_list;
+  uint32_t reserved;
+} dgen_hip_uop;
+
+/* DispatchMode (Renderer.swift:26-67), without the GEMM modes. */
+enum dgen_hip_dispatch {
+  DGEN_HIP_DISPATCH_SINGLE_THREADED = 0,     /* 1 thread, frame loop */
+  DGEN_HIP_DISPATCH_PER_FRAME = 1,           /* frameCount threads */
+  DGEN_HIP_DISPATCH_PER_FRAME_SCALED = 2,    /* frameCount * n threads */
+  DGEN_HIP_DISPATCH_FIXED_WITH_FRAME_LOOP = 3, /* n threads, each loops over the frames */
+  DGEN_HIP_DISPATCH_STATIC_THREADS = 4,      /* n threads, no frame loop */
+  DGEN_HIP_DISPATCH_SELF_MANAGED = 5,        /* 1 thread, the block's own loops */
+  DGEN_HIP_DISPATCH_SELF_MANAGED_THREADS = 6,/* n threads, the block's own loops */
+  DGEN_HIP_DISPATCH_PER_FRAME_TG1 = 7,       /* frameCount threads, groups of 1 */
+  DGEN_HIP_DISPATCH_PER_FRAME_SCALED_TG1 = 8 /* frameCount * n threads, groups of 1 */
+};
+enum { DGEN_HIP_FRAME_SEQUENTIAL = 0, DGEN_HIP_FRAME_PARALLEL = 1 };
+enum { DGEN_HIP_TEMPORAL_FRAME = 0, DGEN_HIP_TEMPORAL_HOP = 1, DGEN_HIP_TEMPORAL_STATIC = 2 };
+
+typedef struct dgen_hip_block {
+  int32_t dispatch;    /* enum dgen_hip_dispatch */
+  int32_t dispatch_n;  /* n of the scaled / fixed / static / self-managed-threads modes */
+  int32_t frame_order; /* DGEN_HIP_FRAME_* */
+  int32_t temporality; /* DGEN_HIP_TEMPORAL_* */
+  int32_t hop_size;
+  int32_t reserved;
+  dgen_hip_lazy hop_counter; /* hop-based: the counter value (runs where it is 0) */
+  const dgen_hip_uop* ops;
+  uint32_t n_ops;
+  uint32_t reserved2;
+} dgen_hip_block;
+
 typedef struct dgen_hip_kernel_time {
   uint32_t index;  /* position in the schedule */
   uint32_t kernel; /* enum dgen_hip_kernel */
@@ -457,6 +589,20 @@ const char* dgen_hip_last_error(void);
  * max_frames bounds dgen_hip_run's frame_count (maxFrameCount). */
 int dgen_hip_configure(dgen_hip_ctx* ctx, const dgen_hip_op* ops, uint32_t n_ops, uint64_t memory_floats,
                        uint32_t max_frames);
+
+/* Render, compile (hiprtc, gfx950) and load the context's generic UOp
+ * blocks; DGEN_HIP_K_UOP_BLOCK op arg[0] indexes them.  Replaces the blocks
+ * set before.  Call before dgen_hip_configure (configure checks the ops that
+ * name a block).  A block that does not render or compile fails with
+ * DGEN_HIP_E_INVALID and the compiler's log in dgen_hip_last_error().
+ * Compiled code objects are cached per process by source text. */
+int dgen_hip_set_blocks(dgen_hip_ctx* ctx, const dgen_hip_block* blocks, uint32_t n_blocks);
+/* The HIP C++ source dgen_hip_set_blocks would compile for these blocks,
+ * without a context or a device: writes up to cap bytes (NUL-terminated) to
+ * buf and the full length to *len.  With compile != 0 it also compiles the
+ * source with hiprtc (no device needed) and fails with the log on errors. */
+int dgen_hip_render_blocks(const dgen_hip_block* blocks, uint32_t n_blocks, int compile, char* buf, size_t cap,
+                           size_t* len);
 
 /* Host mirror of the arena (LazyRuntime.memoryPointer, Realize.swift:16).
  * Valid until the next configure/destroy. */
