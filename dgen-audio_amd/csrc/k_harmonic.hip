@@ -34,10 +34,15 @@
 namespace dgen {
 
 constexpr int kSeg = 64;      // frames per segment = checkpoint spacing
-constexpr int kMaxK = 64;     // harmonics (one lane per harmonic)
-constexpr int kMaxNC = 128;   // control columns
 constexpr int kSlots = 4;     // distinct control rows a segment may touch
-constexpr int kMaxNoise = kSeg + kMaxNC;  // noise window of one segment
+// Harmonics run one per lane, in groups of 64 (a wave's lanes).  The
+// narrow layout (one group, <= 128 control columns) is the common case;
+// the wide one takes up to four groups and 512 columns, at about twice the
+// LDS per wave.
+constexpr int kMaxK = 64;        // narrow: harmonics
+constexpr int kMaxNC = 128;      // narrow: control columns
+constexpr int kMaxKWide = 256;   // wide: harmonics (four groups)
+constexpr int kMaxNCWide = 512;  // wide: control columns
 
 __device__ __forceinline__ float phasor_wrap(float next) {
   float w = next - floorf(next);
@@ -126,20 +131,26 @@ constexpr int kCarryBufs = 2 * kIv;     // increment ring
 constexpr int kRing = 16;               // segments per f0 block
 constexpr int kIncLd = kSeg + 4;        // k-major row stride (floats)
 
-__device__ __forceinline__ bool fast_f0(float f0) {
-  // every increment (k+1)*f0/sr, k < 64, is then computed by the exact
-  // reciprocal-product form and is finite and >= 0
-  return f0 == 0.0f || (f0 >= 0x1p-20f && f0 < 0x1p18f);
+// f0lim = 2^24 / (64 G) for G harmonic groups (2^18 for one): every
+// increment (k+1)*f0/sr, k < 64 G, is then computed by the exact
+// reciprocal-product form and is finite and >= 0
+__device__ __forceinline__ bool fast_f0(float f0, float f0lim) {
+  return f0 == 0.0f || (f0 >= 0x1p-20f && f0 < f0lim);
 }
 
+__host__ __device__ constexpr int harmonic_groups(int K) { return (K + 63) / 64; }
+inline float fast_f0_limit(int K) { return 0x1p24f / (float)(64 * harmonic_groups(K)); }
+
+// Grid (B, harmonic groups): workgroup (b, g) runs harmonics 64 g .. 64 g + 63.
 __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* __restrict__ f0f,
                                                                    float* __restrict__ ckpt, int B, int K, int T,
-                                                                   float sr, float rsr) {
+                                                                   float sr, float rsr, float f0lim) {
   __shared__ __align__(16) float s_inc[kCarryBufs][64 * kIncLd];  // [k][frame]
   __shared__ __align__(16) float s_f0[2][kRing * kSeg];
   __shared__ int s_flag[kCarryBufs * kProducers];  // [buf][producer]: segment needs the literal wrap form
   __shared__ int s_blkbad[2][kProducers];           // f0 block holds a value outside the fast range
   const int b = blockIdx.x, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int k0 = 64 * (int)blockIdx.y;  // first harmonic of the group
   const int nseg = (T + kSeg - 1) / kSeg;
   const float* f0b = f0f + (size_t)b * T;
   const int ptid = threadIdx.x - 64;  // producer thread index
@@ -166,7 +177,7 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
       const int i = ptid + j * 64 * kProducers;
       if (i < kRing * kSeg) {
         const float v = t0 + i < T ? blk_v[j] : 0.0f;
-        bad |= !fast_f0(v);
+        bad |= !fast_f0(v, f0lim);
         dst[i] = v;
       }
     }
@@ -191,7 +202,7 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
       f[4 * q + 2] = v.z;
       f[4 * q + 3] = v.w;
     }
-    const float kf = (float)(lane + 1);
+    const float kf = (float)(k0 + lane + 1);
     const int* bb = s_blkbad[(s / kRing) & 1];
     int blkbad = 0;
 #pragma unroll
@@ -232,9 +243,10 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
   // checkpoint stores through a buffer resource bounded to this batch
   // lane's rows: lanes >= K get an offset past the bound and the hardware
   // drops their store, so the store needs no branch around it
-  const auto ck_rsrc = __builtin_amdgcn_make_buffer_rsrc(ckpt + (size_t)b * K, 0,
-                                                         (int)(4u * (unsigned)((nseg - 1) * B * K + K)), 0x00020000);
-  const unsigned ck_voff = lane < K ? 4u * (unsigned)lane : 0x80000000u;
+  const auto ck_rsrc = __builtin_amdgcn_make_buffer_rsrc(ckpt + (size_t)b * K + k0, 0,
+                                                         (int)(4u * (unsigned)((nseg - 1) * B * K + K - k0)),
+                                                         0x00020000);
+  const unsigned ck_voff = k0 + lane < K ? 4u * (unsigned)lane : 0x80000000u;
   auto store_ckpt = [&](int s) {
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, ph), ck_rsrc, ck_voff,
                                           (int)(4u * (unsigned)(s * B * K)), 0);
@@ -386,7 +398,7 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
 int launch_phasor_carry(const Launch& L, const dgen_hip_op& op) {
   // arg: [0]=f0f ([B][T]) [1]=checkpoints ([nseg][B][K]) [2]=B [3]=K [4]=T   farg: [0]=sr
   const int64_t f0f = op.arg[0], ck = op.arg[1], B = op.arg[2], K = op.arg[3], T = op.arg[4];
-  DGEN_REQUIRE(B > 0 && B <= 65535 && K > 0 && K <= kMaxK && T > 0 && T <= (1 << 26),
+  DGEN_REQUIRE(B > 0 && B <= 65535 && K > 0 && K <= kMaxKWide && T > 0 && T <= (1 << 26),
                "phasor_carry: B %lld K %lld T %lld", (long long)B, (long long)K, (long long)T);
   DGEN_REQUIRE(op.farg[0] > 0.f && op.farg[0] < 1e30f, "phasor_carry: sample rate %g", (double)op.farg[0]);
   const int64_t nseg = (T + kSeg - 1) / kSeg;
@@ -395,8 +407,9 @@ int launch_phasor_carry(const Launch& L, const dgen_hip_op& op) {
   DGEN_REQUIRE(nseg * B * K < (1ll << 29), "phasor_carry: %lld checkpoints (< 2^29)", (long long)(nseg * B * K));
   if (L.dry) return 0;
   const float sr = host_rate(L, op.farg[0]), rsr = 1.0f / sr;
-  hipLaunchKernelGGL(k_phasor_carry, dim3((unsigned)B), dim3(64 * kCarryWaves), 0, L.stream, cell(L, f0f),
-                     cell(L, ck), (int)B, (int)K, (int)T, sr, rsr);
+  hipLaunchKernelGGL(k_phasor_carry, dim3((unsigned)B, (unsigned)harmonic_groups((int)K)), dim3(64 * kCarryWaves), 0,
+                     L.stream, cell(L, f0f), cell(L, ck), (int)B, (int)K, (int)T, sr, rsr,
+                     fast_f0_limit((int)K));
   DGEN_LAUNCH_CHECK("k_phasor_carry");
   return 0;
 }
@@ -413,6 +426,7 @@ struct SynthArgs {
   int ldc, B, K, NF, F, T;
   float sr, rsr, hscale, nscale;
   float nyq;  // half the graph's sample rate: the Nyquist mask (Synth.swift:158-167)
+  float f0lim;  // fast-step bound of f0 (fast_f0)
 };
 
 // Per-frame values of a segment, staged in LDS and read as broadcasts.
@@ -421,8 +435,11 @@ struct FrameRec {
   int slots;  // slot(lo) | slot(hi) << 8
 };
 
-// Per-wave LDS of the synth kernels.
-struct SegLds {
+// Per-wave LDS of the synth kernels, for up to MAXK harmonics and MAXNC
+// control columns (the narrow layout SegLds, or the wide one).
+template <int MAXK, int MAXNC>
+struct SegLdsT {
+  static constexpr int kMaxK = MAXK, kMaxNC = MAXNC, kGroups = MAXK / 64;
   FrameRec fr[kSeg];
   // per-frame weights of the four row slots: a frame's control value is
   // sum_j wt[i][j] * row[j][c] = (1-frac) row[lo][c] + frac row[hi][c]
@@ -430,21 +447,24 @@ struct SegLds {
   // control rows touched by the segment; the stride (4 mod 64 words) puts
   // one column of the four slots in different banks, as the FIR's lanes
   // (frames) read rows lo and hi of their own frames
-  float row[kSlots][kMaxNC + 4];
-  float pre[kSlots][kMaxK + 1];   // prefix sums of the harmonic columns of each row
-  float noise[kMaxNoise];         // noise[t0 - (NF-1) ... t0 + 63]
+  float row[kSlots][MAXNC + 4];
+  float pre[kSlots][MAXK + 1];    // prefix sums of the harmonic columns of each row
+  float noise[kSeg + MAXNC];      // noise[t0 - (NF-1) ... t0 + 63]
   // per-frame scalars of the backward: (f0, hs, coef, dfl) as one 16-byte
   // record (the harmonic pass reads all four per frame), and dg, dng
   float4 pk[kSeg];
   float dg[kSeg];
   float dng[kSeg];
 };
+using SegLds = SegLdsT<kMaxK, kMaxNC>;
+using SegLdsWide = SegLdsT<kMaxKWide, kMaxNCWide>;
 
 // Stage the segment's frame records and slot weights, rows, their harmonic
 // prefix sums (if want_pre) and the noise window; nslot_out = the number of
 // row slots in use, pairs_out = every frame reads two distinct rows.
 // Returns 1 if every frame's f0 admits the fast chain step.
-__device__ __forceinline__ int stage_segment(const SynthArgs& a, SegLds& L, int s, int b, int lane, int nt,
+template <class SL>
+__device__ __forceinline__ int stage_segment(const SynthArgs& a, SL& L, int s, int b, int lane, int nt,
                                              bool want_pre, int& nslot_out, bool& pairs_out) {
   const int t0 = s * kSeg;
   const int NC = a.K + 2 + a.NF;
@@ -459,7 +479,7 @@ __device__ __forceinline__ int stage_segment(const SynthArgs& a, SegLds& L, int 
       r.frac = e0.z;
       r.omf = e0.w;
       r.slots = (int)e1.x | ((int)e1.y << 8);
-      ok = fast_f0(r.f0) ? 1 : 0;
+      ok = fast_f0(r.f0, a.f0lim) ? 1 : 0;
     }
     L.fr[lane] = r;
     const int slo = r.slots & 255, shi = r.slots >> 8;
@@ -484,15 +504,24 @@ __device__ __forceinline__ int stage_segment(const SynthArgs& a, SegLds& L, int 
   }
   wave_sync();
   if (want_pre) {
-    // inclusive wave scan of each row's first K columns -> pre[j][k+1]
+    // inclusive wave scan of each row's first K columns -> pre[j][k+1], a
+    // group of 64 harmonics at a time, each group's scan added to the sum
+    // of the groups before it
     for (int j = 0; j < nslot; ++j) {
-      float v = lane < a.K ? L.row[j][lane] : 0.0f;
+      float carry = 0.0f;
+      for (int g = 0; g < SL::kGroups; ++g) {
+        const int k = 64 * g + lane;
+        if (64 * g >= a.K) break;
+        float v = k < a.K ? L.row[j][k] : 0.0f;
 #pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const float u = __shfl_up(v, d, 64);
-        if (lane >= d) v += u;
+        for (int d = 1; d < 64; d <<= 1) {
+          const float u = __shfl_up(v, d, 64);
+          if (lane >= d) v += u;
+        }
+        if (g > 0) v = carry + v;
+        if (k < a.K) L.pre[j][k + 1] = v;
+        carry = __shfl(v, 63, 64);
       }
-      if (lane < a.K) L.pre[j][lane + 1] = v;
       if (lane == 0) L.pre[j][0] = 0.0f;
     }
     wave_sync();
@@ -516,7 +545,8 @@ __device__ __forceinline__ int below_nyquist(float f0, float nyq, int K) {
 constexpr int kBlk = 8;
 
 // FIR noise branch for frame i: sum_j noise[t-(NF-1)+j] * tap_j(t).
-__device__ __forceinline__ float frame_fir(const SynthArgs& a, const SegLds& L, int i, const FrameRec& r) {
+template <class SL>
+__device__ __forceinline__ float frame_fir(const SynthArgs& a, const SL& L, int i, const FrameRec& r) {
   const float* rl = &L.row[r.slots & 255][a.K + 2];
   const float* rh = &L.row[r.slots >> 8][a.K + 2];
   const float* w = &L.noise[i];
@@ -576,18 +606,20 @@ __device__ __forceinline__ void slot_acc(float (&acc)[kSlots], const FrameRec& r
 // masked amplitude for frame i of this lane's harmonic k (0 for lanes >= K
 // and frames >= nt).  The phase steps are those of the reference's stateful
 // phasor (pre-increment output, wrap), the backward's pass repeats them bit
-// for bit.  rv = this lane's amplitude column in each row slot.
+// for bit.  rv = this lane's amplitude column in each row slot; kh = the
+// lane's harmonic (lane + 64 g in group g).
 // MASKC: no harmonic crosses the Nyquist limit inside the segment and the
 // caller has zeroed rv of the lanes masked throughout (and of lanes >= K),
 // so no frame tests the mask: those lanes add sin * 0.
-template <bool FAST, int NS, bool MASKC = false>
-__device__ __forceinline__ void chain_regs(const SynthArgs& a, const SegLds& L, float (&v)[kSeg], int lane, int nt,
+// ADD: v[i] += the term (harmonic groups after the first), else v[i] = it.
+template <bool FAST, int NS, bool MASKC = false, bool ADD = false, class SL>
+__device__ __forceinline__ void chain_regs(const SynthArgs& a, const SL& L, float (&v)[kSeg], int kh, int nt,
                                            float ph, const float (&rv)[kSlots]) {
   static_assert(!MASKC || (FAST && NS != 0), "the constant mask is a fast slot-weight form");
-  const float kf = (float)(lane + 1);
+  const float kf = (float)(kh + 1);
   const float nyq = a.nyq;
-  const bool harm = lane < a.K;
-  const int kk = harm ? lane : 0;
+  const bool harm = kh < a.K;
+  const int kk = harm ? kh : 0;
 #pragma unroll
   for (int i0 = 0; i0 < kSeg; i0 += kBlk) {
     // the block's reads are issued at its start, not hoisted over the
@@ -611,7 +643,7 @@ __device__ __forceinline__ void chain_regs(const SynthArgs& a, const SegLds& L, 
     for (int j = 0; j < kBlk; ++j) {
       const int i = i0 + j;
       if (!FAST && i >= nt) {
-        v[i] = 0.0f;
+        if constexpr (!ADD) v[i] = 0.0f;
         continue;
       }
       const float freq = kf * r[j].f0;
@@ -629,7 +661,11 @@ __device__ __forceinline__ void chain_regs(const SynthArgs& a, const SegLds& L, 
         amp = r[j].omf * al[j] + r[j].frac * ah[j];
       else
         amp = slot_lerp<NS>(w[j], rv);
-      v[i] = MASKC ? sin2pi(p) * amp : ((harm && freq < nyq) ? sin2pi(p) * amp : 0.0f);
+      const float term = MASKC ? sin2pi(p) * amp : ((harm && freq < nyq) ? sin2pi(p) * amp : 0.0f);
+      if constexpr (ADD)
+        v[i] = v[i] + term;
+      else
+        v[i] = term;
     }
   }
 }
@@ -688,66 +724,85 @@ __device__ __forceinline__ float reduce_scatter64(float (&v)[kSeg], int lane) {
   return v[0];
 }
 
+// The chain pass of harmonic kh = lane + 64 g of one group into v (ADD: v +=).
+// ns: the row-slot form; [flo, fhi]: the segment's f0 range (fast slot forms).
+template <bool ADD, class SL>
+__device__ __forceinline__ void fwd_group(const SynthArgs& a, const SL& L, float (&v)[kSeg], int kh, int s, int b,
+                                          int nt, int fast, int ns, int nslot, float flo, float fhi) {
+  const int kk = kh < a.K ? kh : 0;
+  const float ph = a.ckpt[((size_t)s * a.B + b) * a.K + kk];
+  float rv[kSlots];
+#pragma unroll
+  for (int j = 0; j < kSlots; ++j) rv[j] = j < nslot ? L.row[j][kk] : 0.0f;
+  // Nyquist mask of harmonic k over the segment, from the frames' extreme
+  // f0 (RN((k+1) f0) is monotone in f0): on in every frame, off in every
+  // frame, or mixed (the per-frame test)
+  bool mixed = false, zero = kh >= a.K;
+  if (fast && ns != 0) {
+    const float kf = (float)(kh + 1);
+    const bool on = kf * fhi < a.nyq, off = !(kf * flo < a.nyq);
+    mixed = kh < a.K && !on && !off;
+    zero = zero || off;
+  }
+  if (fast && ns != 0 && !__any(mixed)) {
+    // finite rows (ns != 0): a zeroed lane adds sin * 0 = +-0, which leaves
+    // every frame's sum as the per-frame form's
+    float rz[kSlots];
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) rz[j] = zero ? 0.0f : rv[j];
+    if (ns == 2)
+      chain_regs<true, 2, true, ADD>(a, L, v, kh, nt, ph, rz);
+    else
+      chain_regs<true, kSlots, true, ADD>(a, L, v, kh, nt, ph, rz);
+  } else if (fast && ns == 2)
+    chain_regs<true, 2, false, ADD>(a, L, v, kh, nt, ph, rv);
+  else if (fast && ns == kSlots)
+    chain_regs<true, kSlots, false, ADD>(a, L, v, kh, nt, ph, rv);
+  else if (fast)
+    chain_regs<true, 0, false, ADD>(a, L, v, kh, nt, ph, rv);
+  else
+    chain_regs<false, 0, false, ADD>(a, L, v, kh, nt, ph, rv);
+}
+
+template <class SL>
 __global__ __launch_bounds__(64 * kWavesFwd) void k_synth_fwd(SynthArgs a, float* __restrict__ y,
                                                               float* __restrict__ aux) {
-  __shared__ SegLds lds[kWavesFwd];
+  __shared__ SL lds[kWavesFwd];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int nseg = (a.T + kSeg - 1) / kSeg;
   const int s = blockIdx.x * kWavesFwd + wave, b = blockIdx.y;
   if (s >= nseg) return;
-  SegLds& L = lds[wave];
+  SL& L = lds[wave];
   const int t0 = s * kSeg, nt = min(kSeg, a.T - t0);
   int nslot;
   bool pairs;
   const int fast = stage_segment(a, L, s, b, lane, nt, true, nslot, pairs);
   float v[kSeg];
   {
-    const int kk = lane < a.K ? lane : 0;
-    const float ph = a.ckpt[((size_t)s * a.B + b) * a.K + kk];
-    float rv[kSlots];
     bool fin = true;
+    for (int g = 0; g < SL::kGroups; ++g) {
+      if (64 * g >= a.K) break;
+      const int kh = 64 * g + lane, kk = kh < a.K ? kh : 0;
 #pragma unroll
-    for (int j = 0; j < kSlots; ++j) {
-      rv[j] = j < nslot ? L.row[j][kk] : 0.0f;
-      fin = fin && isfinite(rv[j]);
+      for (int j = 0; j < kSlots; ++j) fin = fin && isfinite(j < nslot ? L.row[j][kk] : 0.0f);
     }
     // slot weights need finite rows and two distinct rows per frame; else
     // the exact per-frame form
     const int ns = !(__all(fin) && pairs) ? 0 : (nslot <= 2 ? 2 : kSlots);
-    // Nyquist mask of lane k over the segment, from the frames' extreme f0
-    // (RN((k+1) f0) is monotone in f0): on in every frame, off in every
-    // frame, or mixed (the per-frame test)
-    bool mixed = false, zero = lane >= a.K;
+    float flo = 0.0f, fhi = 0.0f;
     if (fast && ns != 0) {
-      float lo = L.fr[lane].f0, hi = lo;
+      flo = fhi = L.fr[lane].f0;
 #pragma unroll
       for (int d = 32; d > 0; d >>= 1) {
-        lo = fminf(lo, __shfl_xor(lo, d, 64));
-        hi = fmaxf(hi, __shfl_xor(hi, d, 64));
+        flo = fminf(flo, __shfl_xor(flo, d, 64));
+        fhi = fmaxf(fhi, __shfl_xor(fhi, d, 64));
       }
-      const float kf = (float)(lane + 1);
-      const bool on = kf * hi < a.nyq, off = !(kf * lo < a.nyq);
-      mixed = lane < a.K && !on && !off;
-      zero = zero || off;
     }
-    if (fast && ns != 0 && !__any(mixed)) {
-      // finite rows (ns != 0): a zeroed lane adds sin * 0 = +-0, which leaves
-      // every frame's sum as the per-frame form's
-      float rz[kSlots];
-#pragma unroll
-      for (int j = 0; j < kSlots; ++j) rz[j] = zero ? 0.0f : rv[j];
-      if (ns == 2)
-        chain_regs<true, 2, true>(a, L, v, lane, nt, ph, rz);
-      else
-        chain_regs<true, kSlots, true>(a, L, v, lane, nt, ph, rz);
-    } else if (fast && ns == 2)
-      chain_regs<true, 2>(a, L, v, lane, nt, ph, rv);
-    else if (fast && ns == kSlots)
-      chain_regs<true, kSlots>(a, L, v, lane, nt, ph, rv);
-    else if (fast)
-      chain_regs<true, 0>(a, L, v, lane, nt, ph, rv);
-    else
-      chain_regs<false, 0>(a, L, v, lane, nt, ph, rv);
+    fwd_group<false>(a, L, v, lane, s, b, nt, fast, ns, nslot, flo, fhi);
+    for (int g = 1; g < SL::kGroups; ++g) {
+      if (64 * g >= a.K) break;
+      fwd_group<true>(a, L, v, 64 * g + lane, s, b, nt, fast, ns, nslot, flo, fhi);
+    }
   }
   const float num = reduce_scatter64(v, lane);  // frame = lane
   if (lane < nt) {
@@ -781,26 +836,28 @@ __global__ __launch_bounds__(64 * kWavesFwd) void k_synth_fwd(SynthArgs a, float
 //   d gain  = g * hsum * uv * hscale,  d ngain = g * filt * 0.12 * nscale
 //   d tap_j = g * ngain * 0.12 * nscale * noise[t-(NF-1)+j]
 // each scattered to rows lo/hi with weights 1-frac / frac
-// (sampleInline gradient, Emit+RowSelection.swift:100-141).  Column c is
-// handled by lane c & 63 in pass c >> 6.
+// (sampleInline gradient, Emit+RowSelection.swift:100-141).
 constexpr int kWavesBwd = 2;
 
 // Column passes of the backward, each accumulating its column's gradient
-// into the four row slots with the frames' slot weights.  Pass 1 runs the
-// phase chain (lane = harmonic k, the forward's chain bit for bit) and
-// accumulates harmonic column k in the same loop, so no per-frame sine table
-// is staged; lanes k >= K take the non-harmonic columns lane + 64.  Pass 2
-// takes columns K + lane.  Together they cover every column c < K + 128 >= NC.
+// into the four row slots with the frames' slot weights.  The harmonic
+// passes (one per group of 64 harmonics) run the phase chain (harmonic
+// kh = lane + 64 g, the forward's chain bit for bit) and accumulate harmonic
+// column kh in the same loop, so no per-frame sine table is staged; in the
+// last group the lanes past K take the last non-harmonic columns
+// (K + 64 P + kh - K).  The P gain passes take columns K + 64 p + lane
+// (gain, noise gain, taps), P the fewest that cover the rest; with one
+// group and NC <= 128, P = 1 and the spare lanes' columns are lane + 64.
 // MASKC: no harmonic crosses the Nyquist limit inside the segment, so each
 // lane's mask is one value for all its frames (the caller zeroes the sums
 // of lanes that are masked throughout) and no frame tests it.
-template <bool FAST, int NS, bool MASKC = false>
-__device__ __forceinline__ void bwd_harmonic_pass(const SynthArgs& a, const SegLds& L, float (&acc)[kSlots], int lane,
+template <bool FAST, int NS, bool MASKC = false, class SL>
+__device__ __forceinline__ void bwd_harmonic_pass(const SynthArgs& a, const SL& L, float (&acc)[kSlots], int kh,
                                                   int nt, float ph, int nidx_spare) {
   static_assert(!MASKC || (FAST && NS != 0), "the constant mask is a fast slot-weight form");
-  const float kf = (float)(lane + 1);
+  const float kf = (float)(kh + 1);
   const float nyq = a.nyq;
-  const bool harm = lane < a.K;
+  const bool harm = kh < a.K;
   const int n = FAST ? kSeg : nt;
   // (rolled: the blocks' reads and sums stay within a few registers)
 #pragma unroll 1
@@ -850,10 +907,11 @@ __device__ __forceinline__ void bwd_harmonic_pass(const SynthArgs& a, const SegL
   }
 }
 
-// Pass 2: column K + q, q = lane (0: gain, 1: noise gain, q >= 2: tap q-2).
-template <int NS>
-__device__ __forceinline__ void bwd_gain_pass(const SegLds& L, float (&acc)[kSlots], int q, int nt) {
-  const int nidx = max(q - 2, 0);
+// A gain pass: column K + q (q = 0: gain, 1: noise gain, q >= 2: tap q-2;
+// columns past NC read the window's last tap and are not stored).
+template <int NS, class SL>
+__device__ __forceinline__ void bwd_gain_pass(const SL& L, float (&acc)[kSlots], int q, int nt, int NF) {
+  const int nidx = min(max(q - 2, 0), NF - 1);
 #pragma unroll 1
   for (int i0 = 0; i0 < nt; i0 += kBlk) {
     FrameRec r[kBlk];
@@ -879,15 +937,16 @@ __device__ __forceinline__ void store_slots(const float (&acc)[kSlots], float* o
   for (int j = 0; j < kSlots; ++j) out[j * ldc + c] = acc[j];
 }
 
+template <class SL>
 __global__ __launch_bounds__(64 * kWavesBwd) void k_synth_bwd(SynthArgs a, const float* __restrict__ dy,
                                                               const float* __restrict__ aux,
                                                               float* __restrict__ part) {
-  __shared__ SegLds lds[kWavesBwd];
+  __shared__ SL lds[kWavesBwd];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int nseg = (a.T + kSeg - 1) / kSeg;
   const int s = blockIdx.x * kWavesBwd + wave, b = blockIdx.y;
   if (s >= nseg) return;
-  SegLds& L = lds[wave];
+  SL& L = lds[wave];
   const int t0 = s * kSeg, nt = min(kSeg, a.T - t0);
   int nslot;
   bool pairs;  // (the backward's slot-weight sums need no distinct rows)
@@ -926,59 +985,68 @@ __global__ __launch_bounds__(64 * kWavesBwd) void k_synth_bwd(SynthArgs a, const
 
   const int NC = a.K + 2 + a.NF;
   float* out = part + ((size_t)b * nseg + s) * kSlots * a.ldc;
-  {
-    // pass 1: harmonic k = lane, or (lane >= K) the tap column lane + 64
-    const int c = lane < a.K ? lane : lane + 64;
-    const int nidx = lane < a.K ? 0 : c - a.K - 2;
-    const float ph = a.ckpt[((size_t)s * a.B + b) * a.K + (lane < a.K ? lane : 0)];
+  const int spare = 64 * harmonic_groups(a.K) - a.K;          // lanes past K in the last group
+  const int npass = max(1, (NC - a.K - spare + 63) / 64);      // gain passes
+  // the segment's f0 range, for the harmonics' Nyquist masks
+  float flo = 0.0f, fhi = 0.0f;
+  if (fast) {
+    flo = fhi = L.fr[lane].f0;
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) {
+      flo = fminf(flo, __shfl_xor(flo, d, 64));
+      fhi = fmaxf(fhi, __shfl_xor(fhi, d, 64));
+    }
+  }
+  for (int g = 0; g < SL::kGroups; ++g) {
+    if (64 * g >= a.K) break;
+    // harmonic kh, or (kh >= K) the tap column K + 64 npass + kh - K
+    const int kh = 64 * g + lane;
+    const bool harm = kh < a.K;
+    const int c = harm ? kh : a.K + 64 * npass + (kh - a.K);
+    const int nidx = harm ? 0 : min(c - a.K - 2, a.NF - 1);
+    const float ph = a.ckpt[((size_t)s * a.B + b) * a.K + (harm ? kh : 0)];
     float acc[kSlots] = {0.f, 0.f, 0.f, 0.f};
-    // Nyquist mask of harmonic lane k over the segment: freq = RN((k+1) f0)
+    // Nyquist mask of harmonic kh over the segment: freq = RN((k+1) f0)
     // is monotone in f0, so the frames' extreme f0 decide whether every
     // frame is below (on) or none is (off); a lane between the two needs
     // the per-frame test
     bool mixed = false, off = false;
     if (fast) {
-      float lo = L.fr[lane].f0, hi = lo;
-#pragma unroll
-      for (int d = 32; d > 0; d >>= 1) {
-        lo = fminf(lo, __shfl_xor(lo, d, 64));
-        hi = fmaxf(hi, __shfl_xor(hi, d, 64));
-      }
-      const float kf = (float)(lane + 1);
-      const bool on = kf * hi < a.nyq;
-      off = !(kf * lo < a.nyq);
-      mixed = lane < a.K && !on && !off;
+      const float kf = (float)(kh + 1);
+      const bool on = kf * fhi < a.nyq;
+      off = !(kf * flo < a.nyq);
+      mixed = harm && !on && !off;
     }
     const bool maskc = !__any(mixed);
     if (fast && ns == 2 && maskc)
-      bwd_harmonic_pass<true, 2, true>(a, L, acc, lane, nt, ph, nidx);
+      bwd_harmonic_pass<true, 2, true>(a, L, acc, kh, nt, ph, nidx);
     else if (fast && ns == kSlots && maskc)
-      bwd_harmonic_pass<true, kSlots, true>(a, L, acc, lane, nt, ph, nidx);
+      bwd_harmonic_pass<true, kSlots, true>(a, L, acc, kh, nt, ph, nidx);
     else if (fast && ns == 2)
-      bwd_harmonic_pass<true, 2>(a, L, acc, lane, nt, ph, nidx);
+      bwd_harmonic_pass<true, 2>(a, L, acc, kh, nt, ph, nidx);
     else if (fast && ns == kSlots)
-      bwd_harmonic_pass<true, kSlots>(a, L, acc, lane, nt, ph, nidx);
+      bwd_harmonic_pass<true, kSlots>(a, L, acc, kh, nt, ph, nidx);
     else if (fast)
-      bwd_harmonic_pass<true, 0>(a, L, acc, lane, nt, ph, nidx);
+      bwd_harmonic_pass<true, 0>(a, L, acc, kh, nt, ph, nidx);
     else
-      bwd_harmonic_pass<false, 0>(a, L, acc, lane, nt, ph, nidx);
-    if (fast && ns != 0 && maskc && lane < a.K && off) {
+      bwd_harmonic_pass<false, 0>(a, L, acc, kh, nt, ph, nidx);
+    if (fast && ns != 0 && maskc && harm && off) {
       // masked in every frame: the per-frame form adds only zeros
 #pragma unroll
       for (int j = 0; j < kSlots; ++j) acc[j] = 0.0f;
     }
     if (c < NC) store_slots(acc, out, a.ldc, c);
   }
-  {
-    // pass 2: column K + lane (gain, noise gain, taps 0..61)
-    const int c = a.K + lane;
+  for (int pp = 0; pp < npass; ++pp) {
+    // gain pass pp: column K + 64 pp + lane
+    const int q = 64 * pp + lane, c = a.K + q;
     float acc[kSlots] = {0.f, 0.f, 0.f, 0.f};
     if (ns == 2)
-      bwd_gain_pass<2>(L, acc, lane, nt);
+      bwd_gain_pass<2>(L, acc, q, nt, a.NF);
     else if (ns == kSlots)
-      bwd_gain_pass<kSlots>(L, acc, lane, nt);
+      bwd_gain_pass<kSlots>(L, acc, q, nt, a.NF);
     else
-      bwd_gain_pass<0>(L, acc, lane, nt);
+      bwd_gain_pass<0>(L, acc, q, nt, a.NF);
     if (c < NC) store_slots(acc, out, a.ldc, c);
   }
 }
@@ -1072,8 +1140,8 @@ static int synth_args(const Launch& L, const dgen_hip_op& op, SynthArgs& a, cons
   //      [11]=seg (64) [12]=partials (bwd) [13]=noise [14]=ldc [15]=seg_rows
   const int64_t B = op.arg[6], K = op.arg[7], NF = op.arg[8], F = op.arg[9], T = op.arg[10], seg = op.arg[11];
   const int64_t ldc = op.arg[14];
-  DGEN_REQUIRE(B > 0 && B <= 65535 && K > 0 && K <= kMaxK && NF > 0 && F > 0 && T > 0 && T <= (1 << 26) &&
-                   seg == kSeg && K + 2 + NF <= kMaxNC && ldc >= K + 2 + NF,
+  DGEN_REQUIRE(B > 0 && B <= 65535 && K > 0 && K <= kMaxKWide && NF > 0 && F > 0 && T > 0 && T <= (1 << 26) &&
+                   seg == kSeg && K + 2 + NF <= kMaxNCWide && ldc >= K + 2 + NF,
                "%s: B %lld K %lld NF %lld F %lld T %lld seg %lld ldc %lld", who, (long long)B, (long long)K,
                (long long)NF, (long long)F, (long long)T, (long long)seg, (long long)ldc);
   DGEN_REQUIRE(op.farg[0] > 0.f && op.farg[0] < 1e30f, "%s: sample rate %g", who, (double)op.farg[0]);
@@ -1109,8 +1177,12 @@ static int synth_args(const Launch& L, const dgen_hip_op& op, SynthArgs& a, cons
   a.nyq = op.farg[0] * 0.5f;
   a.hscale = op.farg[1];
   a.nscale = op.farg[2];
+  a.f0lim = fast_f0_limit((int)K);
   return 0;
 }
+
+// The narrow LDS layout when the harmonics fit one group and the columns 128.
+static bool synth_narrow(const SynthArgs& a) { return a.K <= kMaxK && a.K + 2 + a.NF <= kMaxNC; }
 
 int launch_synth_fwd(const Launch& L, const dgen_hip_op& op) {
   SynthArgs a{};
@@ -1119,9 +1191,12 @@ int launch_synth_fwd(const Launch& L, const dgen_hip_op& op) {
   if (op.arg[12] >= 0) DGEN_CHECK_CELL(L, op.arg[12], 3 * op.arg[6] * op.arg[10], "synth_fwd.aux");
   if (L.dry) return 0;
   const int nseg = (a.T + kSeg - 1) / kSeg;
-  hipLaunchKernelGGL(k_synth_fwd, dim3((unsigned)((nseg + kWavesFwd - 1) / kWavesFwd), (unsigned)a.B),
-                     dim3(64 * kWavesFwd), 0, L.stream, a, cell(L, op.arg[5]),
-                     op.arg[12] >= 0 ? cell(L, op.arg[12]) : nullptr);
+  const dim3 grid((unsigned)((nseg + kWavesFwd - 1) / kWavesFwd), (unsigned)a.B), block(64 * kWavesFwd);
+  float* aux = op.arg[12] >= 0 ? cell(L, op.arg[12]) : nullptr;
+  if (synth_narrow(a))
+    hipLaunchKernelGGL(k_synth_fwd<SegLds>, grid, block, 0, L.stream, a, cell(L, op.arg[5]), aux);
+  else
+    hipLaunchKernelGGL(k_synth_fwd<SegLdsWide>, grid, block, 0, L.stream, a, cell(L, op.arg[5]), aux);
   DGEN_LAUNCH_CHECK("k_synth_fwd");
   return 0;
 }
@@ -1135,9 +1210,13 @@ int launch_synth_bwd(const Launch& L, const dgen_hip_op& op) {
   DGEN_CHECK_CELL(L, op.arg[12], B * nseg * kSlots * ldc, "synth_bwd.partials");
   DGEN_CHECK_CELL(L, op.arg[16], 3 * B * T, "synth_bwd.aux");
   if (L.dry) return 0;
-  hipLaunchKernelGGL(k_synth_bwd, dim3((unsigned)((nseg + kWavesBwd - 1) / kWavesBwd), (unsigned)a.B),
-                     dim3(64 * kWavesBwd), 0, L.stream, a, cell(L, op.arg[5]), cell(L, op.arg[16]),
-                     cell(L, op.arg[12]));
+  const dim3 grid((unsigned)((nseg + kWavesBwd - 1) / kWavesBwd), (unsigned)a.B), block(64 * kWavesBwd);
+  if (synth_narrow(a))
+    hipLaunchKernelGGL(k_synth_bwd<SegLds>, grid, block, 0, L.stream, a, cell(L, op.arg[5]), cell(L, op.arg[16]),
+                       cell(L, op.arg[12]));
+  else
+    hipLaunchKernelGGL(k_synth_bwd<SegLdsWide>, grid, block, 0, L.stream, a, cell(L, op.arg[5]),
+                       cell(L, op.arg[16]), cell(L, op.arg[12]));
   DGEN_LAUNCH_CHECK("k_synth_bwd");
   return 0;
 }

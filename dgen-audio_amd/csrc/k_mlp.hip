@@ -219,11 +219,11 @@ int launch_dense_small_wgrad(const Launch& L, const dgen_hip_op& op) {
 // ---------------------------------------------------------------- heads
 
 // One wave per row; Z and ctrl rows have stride ldz / ldc.  Lane l owns
-// elements l and l + 64 of each head group (K, NF <= 128), and every
-// softplus / tanh of a row is evaluated once, in registers (the sums add
-// the same terms in the same order as a per-group loop).
-constexpr int kHeadPer = 2;
-
+// elements l, l + 64, ..., l + 64 (HP - 1) of each head group (K, NF <=
+// 64 HP: HP = 2 up to 128, 4 up to 256), and every softplus / tanh of a row
+// is evaluated once, in registers (the sums add the same terms in the same
+// order as a per-group loop).
+template <int kHeadPer>
 __global__ void k_heads_fwd(const float* __restrict__ Z, int ldz, float* __restrict__ C, int ldc, int rows, int K,
                             int NF) {
   const int m = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
@@ -266,6 +266,7 @@ __global__ void k_heads_fwd(const float* __restrict__ Z, int ldz, float* __restr
   }
 }
 
+template <int kHeadPer>
 __global__ void k_heads_bwd(const float* __restrict__ Z, int ldz, const float* __restrict__ dC, int ldc,
                             float* __restrict__ dZ, int lddz, int rows, int K, int NF) {
   const int m = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
@@ -330,14 +331,19 @@ __global__ void k_heads_bwd(const float* __restrict__ Z, int ldz, const float* _
 int launch_heads_fwd(const Launch& L, const dgen_hip_op& op) {
   const int64_t Z = op.arg[0], C = op.arg[1], rows = op.arg[2], K = op.arg[3], NF = op.arg[4];
   const int64_t ld = op.arg[5];
-  DGEN_REQUIRE(rows > 0 && K > 0 && NF > 0 && K <= kHeadPer * kWave && NF <= kHeadPer * kWave && ld >= K + 2 + NF,
+  DGEN_REQUIRE(rows > 0 && K > 0 && NF > 0 && K <= 4 * kWave && NF <= 4 * kWave && ld >= K + 2 + NF,
                "heads_fwd: rows %lld K %lld NF %lld ld %lld",
                (long long)rows, (long long)K, (long long)NF, (long long)ld);
   DGEN_CHECK_CELL(L, Z, rows * ld, "heads_fwd.Z");
   DGEN_CHECK_CELL(L, C, rows * ld, "heads_fwd.ctrl");
   if (L.dry) return 0;
-  hipLaunchKernelGGL(k_heads_fwd, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, L.stream, cell(L, Z), (int)ld,
-                     cell(L, C), (int)ld, (int)rows, (int)K, (int)NF);
+  const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+  if (K <= 2 * kWave && NF <= 2 * kWave)
+    hipLaunchKernelGGL(k_heads_fwd<2>, grid, block, 0, L.stream, cell(L, Z), (int)ld, cell(L, C), (int)ld,
+                       (int)rows, (int)K, (int)NF);
+  else
+    hipLaunchKernelGGL(k_heads_fwd<4>, grid, block, 0, L.stream, cell(L, Z), (int)ld, cell(L, C), (int)ld,
+                       (int)rows, (int)K, (int)NF);
   DGEN_LAUNCH_CHECK("k_heads_fwd");
   return 0;
 }
@@ -345,15 +351,20 @@ int launch_heads_fwd(const Launch& L, const dgen_hip_op& op) {
 int launch_heads_bwd(const Launch& L, const dgen_hip_op& op) {
   const int64_t Z = op.arg[0], dC = op.arg[1], dZ = op.arg[2], rows = op.arg[3], K = op.arg[4], NF = op.arg[5];
   const int64_t ld = op.arg[6];
-  DGEN_REQUIRE(rows > 0 && K > 0 && NF > 0 && K <= kHeadPer * kWave && NF <= kHeadPer * kWave && ld >= K + 2 + NF,
+  DGEN_REQUIRE(rows > 0 && K > 0 && NF > 0 && K <= 4 * kWave && NF <= 4 * kWave && ld >= K + 2 + NF,
                "heads_bwd: rows %lld K %lld NF %lld ld %lld",
                (long long)rows, (long long)K, (long long)NF, (long long)ld);
   DGEN_CHECK_CELL(L, Z, rows * ld, "heads_bwd.Z");
   DGEN_CHECK_CELL(L, dC, rows * ld, "heads_bwd.dctrl");
   DGEN_CHECK_CELL(L, dZ, rows * ld, "heads_bwd.dZ");
   if (L.dry) return 0;
-  hipLaunchKernelGGL(k_heads_bwd, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, L.stream, cell(L, Z), (int)ld,
-                     cell(L, dC), (int)ld, cell(L, dZ), (int)ld, (int)rows, (int)K, (int)NF);
+  const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+  if (K <= 2 * kWave && NF <= 2 * kWave)
+    hipLaunchKernelGGL(k_heads_bwd<2>, grid, block, 0, L.stream, cell(L, Z), (int)ld, cell(L, dC), (int)ld,
+                       cell(L, dZ), (int)ld, (int)rows, (int)K, (int)NF);
+  else
+    hipLaunchKernelGGL(k_heads_bwd<4>, grid, block, 0, L.stream, cell(L, Z), (int)ld, cell(L, dC), (int)ld,
+                       cell(L, dZ), (int)ld, (int)rows, (int)K, (int)NF);
   DGEN_LAUNCH_CHECK("k_heads_bwd");
   return 0;
 }

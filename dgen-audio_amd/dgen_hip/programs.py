@@ -17,7 +17,8 @@ from .workloads import (BiquadConfig, HarmonicConfig, MembraneConfig, OscBankCon
 SEG = 64          # frames per synth segment (checkpoint spacing)
 SLOTS = 4         # control rows a segment may touch
 ROW_ENTRIES = 16  # (segment, slot) entries per control row (kRowEntries)
-LDC = 128         # padded control-row stride (K + 2 + NF <= 128)
+MAX_HARMONICS = 256  # the synth kernels' harmonic groups (four of 64)
+MAX_CONTROLS = 512   # control columns K + 2 + NF
 SPLITK_ROWS = 1024  # rows per split of the weight-gradient GEMMs
 GEMM_TILE_M = 128  # output rows per GEMM workgroup tile (k_gemm.hip BM)
 SPLITK_ROWS_HEADS = 256  # the heads' weight gradient has one 128-wide column tile: split finer to fill the chip
@@ -115,10 +116,11 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     if cfg.gemm_products not in GEMM_PRODUCTS:
         raise ValueError(f"gemm_products {cfg.gemm_products!r}: one of {sorted(GEMM_PRODUCTS)}")
     gm = GEMM_PRODUCTS[cfg.gemm_products]
-    if NC > LDC:
-        raise ValueError(f"K + 2 + NF = {NC} exceeds {LDC}")
-    if K > 64:
-        raise ValueError("K > 64 harmonics is not supported by the synth kernels")
+    if K > MAX_HARMONICS:
+        raise ValueError(f"K = {K} harmonics exceeds {MAX_HARMONICS}")
+    if NC > MAX_CONTROLS:
+        raise ValueError(f"K + 2 + NF = {NC} exceeds {MAX_CONTROLS}")
+    LDC = cfg.ldc
     nseg = (T + SEG - 1) // SEG
     p = Program(max_frames=T)
     p.meta.update(cfg=cfg, nseg=nseg, train=train)

@@ -140,6 +140,12 @@ class HarmonicConfig:
     def M(self) -> int:
         return self.B * self.F
 
+    @property
+    def ldc(self) -> int:
+        """Padded stride of the control rows (Z, ctrl, dctrl, dZ): 128 for
+        up to 128 columns, else NC rounded up to 64."""
+        return 128 if self.NC <= 128 else (self.NC + 63) // 64 * 64
+
     def param_count(self) -> int:
         n, fan = 0, self.din
         for _ in range(self.layers):

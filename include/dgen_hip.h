@@ -94,7 +94,7 @@ enum dgen_hip_kernel {
 
   /* Head activations of HarmonicDecoderModel (Model.swift:100-114):
    * amps = softplus/sum, gain/noise gain = softplus, taps = tanh/sum|.|.
-   * arg: [0]=Z [1]=ctrl [2]=rows [3]=K (<= 128) [4]=NF (<= 128)
+   * arg: [0]=Z [1]=ctrl [2]=rows [3]=K (<= 256) [4]=NF (<= 256)
    *      [5]=row stride of Z and ctrl (>= K + 2 + NF) */
   DGEN_HIP_K_HEADS_FWD = 4,
 
@@ -102,17 +102,18 @@ enum dgen_hip_kernel {
    * lanes (b,k), freq = (k+1) * f0 frames[b][t]; stores the phase at the
    * start of every 64-frame segment.
    * arg: [0]=f0 frames cell ([B][T], from DGEN_HIP_K_LERP_FRAMES)
-   *      [1]=checkpoints cell ([nseg][B][K]) [2]=B [3]=K [4]=T
+   *      [1]=checkpoints cell ([nseg][B][K]) [2]=B [3]=K (<= 256) [4]=T
    * farg: [0]=sample rate */
   DGEN_HIP_K_PHASOR_CARRY = 5,
 
   /* Batched harmonic + FIR-noise synth forward
    * (Examples/HarmonicE2E/Synth.swift:47-102).
    * arg: [0]=ctrl ([B*F][ldc]) [1]=f0 frames ([B][T]) [2]=uv frames ([B][T])
-   *      [3]=lerp table ([T][8]) [4]=checkpoints [5]=y ([B][T]) [6]=B [7]=K
-   *      [8]=NF [9]=F [10]=T [11]=segment length (64) [12]=per-frame tape
-   *      ([3][B][T]: harmonic sum, normaliser, FIR output) or -1
-   *      [13]=noise ([T]) [14]=ldc [15]=segment rows ([nseg][4])
+   *      [3]=lerp table ([T][8]) [4]=checkpoints [5]=y ([B][T]) [6]=B
+   *      [7]=K (<= 256) [8]=NF (K + 2 + NF <= 512) [9]=F [10]=T
+   *      [11]=segment length (64) [12]=per-frame tape ([3][B][T]: harmonic
+   *      sum, normaliser, FIR output) or -1 [13]=noise ([T]) [14]=ldc
+   *      [15]=segment rows ([nseg][4])
    * farg: [0]=sample rate [1]=harmonic scale [2]=noise scale */
   DGEN_HIP_K_SYNTH_FWD = 6,
 
@@ -157,7 +158,7 @@ enum dgen_hip_kernel {
   DGEN_HIP_K_SYNTH_BWD_REDUCE = 10,
 
   /* Head backward: dZ from d ctrl and Z.  arg: [0]=Z [1]=dctrl [2]=dZ
-   * [3]=rows [4]=K (<= 128) [5]=NF (<= 128) [6]=row stride (>= K + 2 + NF;
+   * [3]=rows [4]=K (<= 256) [5]=NF (<= 256) [6]=row stride (>= K + 2 + NF;
    * dZ's padding columns are written as zero) */
   DGEN_HIP_K_HEADS_BWD = 11,
 

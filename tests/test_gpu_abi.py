@@ -105,7 +105,7 @@ def test_host_sample_rate_drives_the_harmonic_phases_not_the_nyquist_mask(gpu):
         f0f = out["f0_frames"].reshape(cfg.B, cfg.T)
         ck = O.phase_checkpoints(f0f, cfg.B, cfg.K, cfg.T, 22050.0)
         np.testing.assert_array_equal(out["checkpoints"].reshape(ck.shape), ck)
-        ctrl = out["ctrl"].reshape(cfg.M, 128)[:, :cfg.NC]
+        ctrl = out["ctrl"].reshape(cfg.M, cfg.ldc)[:, :cfg.NC]
         ref = O.synth_fwd_rates(ctrl, f0, uv, cfg.B, cfg.F, cfg.T, cfg.K, cfg.NF, 22050.0, cfg.sr)
         err = np.abs(out["y"].reshape(cfg.B, cfg.T) - ref).max()
         print(f"harmonic render at a 22.05 kHz host rate (graphs {graphs}): max|y - oracle| = {err:.3e}")

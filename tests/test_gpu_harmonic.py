@@ -39,14 +39,14 @@ def test_static_tables(small):
 
 def test_controls_match_oracle_mlp(small):
     cfg, X, f0, uv, tgt, out = small
-    ctrl = out["ctrl"].reshape(cfg.M, 128)[:, :cfg.NC]
+    ctrl = out["ctrl"].reshape(cfg.M, cfg.ldc)[:, :cfg.NC]
     ref = O.mlp_fwd(X, cfg.weights(), cfg.M, cfg.din, cfg.hidden, cfg.layers, cfg.K, cfg.NF)
     assert np.abs(ctrl - ref).max() < 1e-5
 
 
 def test_synth_forward_matches_oracle(small):
     cfg, X, f0, uv, tgt, out = small
-    ctrl = out["ctrl"].reshape(cfg.M, 128)[:, :cfg.NC]
+    ctrl = out["ctrl"].reshape(cfg.M, cfg.ldc)[:, :cfg.NC]
     y = out["y"].reshape(cfg.B, cfg.T)
     ref = O.synth_fwd(ctrl, f0, uv, cfg.B, cfg.F, cfg.T, cfg.K, cfg.NF, cfg.sr)
     # the kernel evaluates sin(2 pi p) to ~2e-7 abs where the oracle takes
@@ -102,16 +102,16 @@ def test_spectral_gradient_matches_oracle(small):
 
 def test_synth_backward_matches_oracle(small):
     cfg, X, f0, uv, tgt, out = small
-    ctrl = out["ctrl"].reshape(cfg.M, 128)[:, :cfg.NC]
+    ctrl = out["ctrl"].reshape(cfg.M, cfg.ldc)[:, :cfg.NC]
     dy = out["dy"].reshape(cfg.B, cfg.T)
     ref = O.synth_bwd(ctrl, f0, uv, dy, cfg.B, cfg.F, cfg.T, cfg.K, cfg.NF, cfg.sr)
-    got = out["dctrl"].reshape(cfg.M, 128)[:, :cfg.NC]
+    got = out["dctrl"].reshape(cfg.M, cfg.ldc)[:, :cfg.NC]
     assert rel(got, ref) < 1e-4
 
 
 def test_mlp_backward_matches_oracle(small):
     cfg, X, f0, uv, tgt, out = small
-    dctrl = out["dctrl"].reshape(cfg.M, 128)[:, :cfg.NC]
+    dctrl = out["dctrl"].reshape(cfg.M, cfg.ldc)[:, :cfg.NC]
     ref = O.mlp_bwd(X, cfg.weights(), dctrl, cfg.M, cfg.din, cfg.hidden, cfg.layers, cfg.K, cfg.NF)
     assert rel(out["grads"], ref) < 1e-4
     # first layer on its own (W1 then b1: reduced from the weighted tile

@@ -172,7 +172,7 @@ def test_full_shape_backward_at_its_own_prediction(lane4):
     cfg, lanes, P64, tgt, g, g64, g32, st, (X, f0, uv), _ = lane4
     B, T = cfg.B, cfg.T
     y = st["y"].reshape(B, T)
-    ctrl = st["ctrl"].reshape(cfg.M, 128)[:, :cfg.NC]
+    ctrl = st["ctrl"].reshape(cfg.M, cfg.ldc)[:, :cfg.NC]
 
     def bwd(prec):
         dy = np.concatenate(list(lanes.pool.map(
@@ -205,8 +205,8 @@ def test_full_shape_gradient_stages(lane4):
         lambda b: O.mss_bwd(y[b:b + 1], tgt[b:b + 1], 1, T, cfg.fft_sizes, cfg.hop_div, cfg.w_lin, cfg.w_log, T,
                             prec="f32") / B, range(B))))
     dy = st["dy"].reshape(B, T)
-    ctrl = st["ctrl"].reshape(cfg.M, 128)[:, :cfg.NC]
-    dctrl = st["dctrl"].reshape(cfg.M, 128)[:, :cfg.NC]
+    ctrl = st["ctrl"].reshape(cfg.M, cfg.ldc)[:, :cfg.NC]
+    dctrl = st["dctrl"].reshape(cfg.M, cfg.ldc)[:, :cfg.NC]
     dc64 = O.synth_bwd(ctrl, f0, uv, dy, B, cfg.F, T, cfg.K, cfg.NF, cfg.sr, prec="f64")
     gm64 = O.mlp_bwd(X, cfg.weights(), dctrl, cfg.M, cfg.din, cfg.hidden, cfg.layers, cfg.K, cfg.NF, prec="f64")
     e_dy, e_dy32 = rel(dy, dy64), rel(dy32, dy64)

@@ -53,14 +53,24 @@ def test_roofline_model_config3(products, bound, roof):
 
 
 def test_invalid_configs_raise():
-    with pytest.raises(ValueError):
-        harmonic_program(HarmonicConfig(K=65))
-    with pytest.raises(ValueError):
-        harmonic_program(HarmonicConfig(NF=70))
+    with pytest.raises(ValueError, match="harmonics"):
+        harmonic_program(HarmonicConfig(K=257))
+    with pytest.raises(ValueError, match="exceeds 512"):
+        harmonic_program(HarmonicConfig(K=256, NF=255))
     with pytest.raises(ValueError):
         harmonic_program(HarmonicConfig(fft_sizes=(4096,)))
     with pytest.raises(ValueError):
         Program().alloc("x", 0)
+
+
+def test_wide_harmonic_programs_use_a_wider_row_stride():
+    # one group and <= 128 columns keep the 128 stride; beyond, NC rounded up to 64
+    for (K, NF, ldc) in [(60, 65, 128), (64, 62, 128), (65, 63, 192), (100, 100, 256), (256, 254, 512)]:
+        cfg = HarmonicConfig(B=2, T=6400, K=K, NF=NF, hidden=64)
+        assert cfg.ldc == ldc
+        p = harmonic_program(cfg)
+        assert p.cells["ctrl"].n == cfg.M * ldc and p.cells["dZ"].n == cfg.M * ldc
+        assert p.cells["checkpoints"].n == ((cfg.T + 63) // 64) * cfg.B * K
 
 
 def test_splitmix_matches_reference_sequence():
