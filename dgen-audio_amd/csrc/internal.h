@@ -137,6 +137,7 @@ int launch_adam(const Launch&, const dgen_hip_op&);
 int launch_osc_bank(const Launch&, const dgen_hip_op&);
 int launch_noise_table(const Launch&, const dgen_hip_op&);
 int launch_row_schedule(const Launch&, const dgen_hip_op&);
+int launch_run_table(const Launch&, const dgen_hip_op&);
 int launch_fft_tables(const Launch&, const dgen_hip_op&);
 int launch_lerp_frames(const Launch&, const dgen_hip_op&);
 int launch_biquad_chunk(const Launch&, const dgen_hip_op&);

@@ -437,7 +437,7 @@ struct FrameRec {
 
 // Per-wave LDS of the synth kernels, for up to MAXK harmonics and MAXNC
 // control columns (the narrow layout SegLds, or the wide one).
-template <int MAXK, int MAXNC>
+template <int MAXK, int MAXNC, bool PRE = true>
 struct SegLdsT {
   static constexpr int kMaxK = MAXK, kMaxNC = MAXNC, kGroups = MAXK / 64;
   FrameRec fr[kSeg];
@@ -448,7 +448,7 @@ struct SegLdsT {
   // one column of the four slots in different banks, as the FIR's lanes
   // (frames) read rows lo and hi of their own frames
   float row[kSlots][MAXNC + 4];
-  float pre[kSlots][MAXK + 1];    // prefix sums of the harmonic columns of each row
+  float pre[kSlots][PRE ? MAXK + 1 : 1];  // prefix sums of the harmonic columns of each row (forward)
   float noise[kSeg + MAXNC];      // noise[t0 - (NF-1) ... t0 + 63]
   // per-frame scalars of the backward: (f0, hs, coef, dfl) as one 16-byte
   // record (the harmonic pass reads all four per frame), and dg, dng
@@ -458,6 +458,9 @@ struct SegLdsT {
 };
 using SegLds = SegLdsT<kMaxK, kMaxNC>;
 using SegLdsWide = SegLdsT<kMaxKWide, kMaxNCWide>;
+// the backward's layouts (no prefix sums)
+using SegLdsBwd = SegLdsT<kMaxK, kMaxNC, false>;
+using SegLdsBwdWide = SegLdsT<kMaxKWide, kMaxNCWide, false>;
 
 // Stage the segment's frame records and slot weights, rows, their harmonic
 // prefix sums (if want_pre) and the noise window; nslot_out = the number of
@@ -837,7 +840,24 @@ __global__ __launch_bounds__(64 * kWavesFwd) void k_synth_fwd(SynthArgs a, float
 //   d tap_j = g * ngain * 0.12 * nscale * noise[t-(NF-1)+j]
 // each scattered to rows lo/hi with weights 1-frac / frac
 // (sampleInline gradient, Emit+RowSelection.swift:100-141).
-constexpr int kWavesBwd = 2;
+//
+// A workgroup owns a run of kRunSegs consecutive segments of one lane (a
+// wave each).  Each wave leaves its four row-slot sums per column in its own
+// LDS (over the staged rows, which the passes no longer read); then the
+// workgroup sums, for every control row its segments touch, the run's
+// entries of that row in the row list's (segment) order.  A row whose
+// entries all lie in the run is final and goes to d ctrl; a row shared
+// with other runs (at most two per run boundary, and row 0 when the
+// playhead wraps in the last frame) goes to its boundary partial
+// [B][F][kRunParts][ldc] at the index of the run among the row's runs, and
+// DGEN_HIP_K_SYNTH_BWD_REDUCE adds those partials in run order.  A row's
+// at most 16 entries come from consecutive segments plus the wrap, so it
+// meets at most 6 runs of 4.  Four segments a run: five workgroups (20
+// waves, the registers' limit) per CU, one wave per SIMD each; larger
+// runs left some SIMDs a wave short (8: 16 waves per CU, 193 against
+// 155 us; 10: 273 us).
+constexpr int kRunSegs = 4;
+constexpr int kRunParts = 6;
 
 // Column passes of the backward, each accumulating its column's gradient
 // into the four row slots with the frames' slot weights.  The harmonic
@@ -932,21 +952,16 @@ __device__ __forceinline__ void bwd_gain_pass(const SL& L, float (&acc)[kSlots],
   }
 }
 
-__device__ __forceinline__ void store_slots(const float (&acc)[kSlots], float* out, int ldc, int c) {
+// A column's four slot sums into the wave's LDS (the staged rows' space).
+template <class SL>
+__device__ __forceinline__ void store_slots(const float (&acc)[kSlots], SL& L, int c) {
 #pragma unroll
-  for (int j = 0; j < kSlots; ++j) out[j * ldc + c] = acc[j];
+  for (int j = 0; j < kSlots; ++j) L.row[j][c] = acc[j];
 }
 
 template <class SL>
-__global__ __launch_bounds__(64 * kWavesBwd) void k_synth_bwd(SynthArgs a, const float* __restrict__ dy,
-                                                              const float* __restrict__ aux,
-                                                              float* __restrict__ part) {
-  __shared__ SL lds[kWavesBwd];
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int nseg = (a.T + kSeg - 1) / kSeg;
-  const int s = blockIdx.x * kWavesBwd + wave, b = blockIdx.y;
-  if (s >= nseg) return;
-  SL& L = lds[wave];
+__device__ __forceinline__ void bwd_segment(const SynthArgs& a, SL& L, const float* __restrict__ dy,
+                                            const float* __restrict__ aux, int s, int b, int lane) {
   const int t0 = s * kSeg, nt = min(kSeg, a.T - t0);
   int nslot;
   bool pairs;  // (the backward's slot-weight sums need no distinct rows)
@@ -984,7 +999,6 @@ __global__ __launch_bounds__(64 * kWavesBwd) void k_synth_bwd(SynthArgs a, const
   const int ns = !__all(bnd) ? 0 : (nslot <= 2 ? 2 : kSlots);
 
   const int NC = a.K + 2 + a.NF;
-  float* out = part + ((size_t)b * nseg + s) * kSlots * a.ldc;
   const int spare = 64 * harmonic_groups(a.K) - a.K;          // lanes past K in the last group
   const int npass = max(1, (NC - a.K - spare + 63) / 64);      // gain passes
   // the segment's f0 range, for the harmonics' Nyquist masks
@@ -1035,7 +1049,7 @@ __global__ __launch_bounds__(64 * kWavesBwd) void k_synth_bwd(SynthArgs a, const
 #pragma unroll
       for (int j = 0; j < kSlots; ++j) acc[j] = 0.0f;
     }
-    if (c < NC) store_slots(acc, out, a.ldc, c);
+    if (c < NC) store_slots(acc, L, c);
   }
   for (int pp = 0; pp < npass; ++pp) {
     // gain pass pp: column K + 64 pp + lane
@@ -1047,91 +1061,236 @@ __global__ __launch_bounds__(64 * kWavesBwd) void k_synth_bwd(SynthArgs a, const
       bwd_gain_pass<kSlots>(L, acc, q, nt, a.NF);
     else
       bwd_gain_pass<0>(L, acc, q, nt, a.NF);
-    if (c < NC) store_slots(acc, out, a.ldc, c);
+    if (c < NC) store_slots(acc, L, c);
   }
 }
 
-// d ctrl[b*F+f][c] = sum over the (segment, slot) entries listed for row f.
-// With HEADS the workgroup also runs the head backward of its row (the
-// same rules as k_heads_bwd, Model.swift:100-114): thread c owns column c,
-// and the row sums (softplus over the K amplitudes, |tanh| over the NF
-// noise taps, then the two dot products) combine the waves' sums through
-// LDS in wave order.
-template <bool HEADS>
-__global__ void k_synth_bwd_reduce(const float* __restrict__ part, const float* __restrict__ row_list,
-                                   float* __restrict__ dctrl, int B, int NC, int ldc, int F, int nseg,
-                                   const float* __restrict__ Z, float* __restrict__ dZ, int K, int NF) {
-  const int c = threadIdx.x;
-  const int f = blockIdx.x, b = blockIdx.y;
-  if (!HEADS && c >= ldc) return;
-  float s = 0.f;
-  if (c < NC) {
-    // the row's entries (a prefix of the kRowEntries, then -1), then every
-    // listed partial in flight at once; the adds keep the list order
-    const float* lst = row_list + (size_t)f * kRowEntries;
-    float e[kRowEntries], v[kRowEntries];
+// Head backward of one control row (the rules of k_heads_bwd,
+// Model.swift:100-114) on one wave: lane l holds d ctrl of columns
+// l + 64 q (q < QN) in s[q] and gets dZ of those columns in out[q].  The
+// row sums (softplus over the K amplitudes, |tanh| over the NF noise taps,
+// then the two dot products) add each 64-column block's wave sum in block
+// order.  Columns past K + 2 + NF get 0.
+template <int QN>
+__device__ __forceinline__ void head_row_bwd(const float (&s)[QN], const float* __restrict__ zrow,
+                                             float (&out)[QN], int lane, int K, int NF) {
+  float z[QN], sp[QN], th[QN];
+  float den = 0.f, nrm = 0.f;
 #pragma unroll
-    for (int q = 0; q < kRowEntries; ++q) e[q] = lst[q];
-    bool live = true;
+  for (int q = 0; q < QN; ++q) {
+    const int c = lane + 64 * q;
+    const bool amp = c < K, noise = c >= K + 2 && c < K + 2 + NF;
+    z[q] = c < K + 2 + NF ? zrow[c] : 0.f;
+    sp[q] = amp ? softplus(z[q]) : 0.f;
+    th[q] = noise ? fast_tanh(z[q]) : 0.f;
+  }
 #pragma unroll
-    for (int q = 0; q < kRowEntries; ++q) {
-      live = live && e[q] >= 0.f;
-      const int ent = live ? (int)e[q] : 0;
-      const int seg = ent / kSlots, slot = ent % kSlots;
-      v[q] = live ? part[(((size_t)b * nseg + seg) * kSlots + slot) * ldc + c] : 0.f;
+  for (int q = 0; q < QN; ++q) {
+    den += wave_sum(sp[q]);
+    nrm += wave_sum(fabsf(th[q]));
+  }
+  den += 1e-6f;
+  nrm += 1e-4f;
+  const float rden = rcp_rn(den), rnrm = rcp_rn(nrm);
+  float dot = 0.f, dot2 = 0.f;
+#pragma unroll
+  for (int q = 0; q < QN; ++q) {
+    const int c = lane + 64 * q;
+    const bool amp = c < K, noise = c >= K + 2 && c < K + 2 + NF;
+    dot += wave_sum(amp ? s[q] * (sp[q] * rden) : 0.f);
+    dot2 += wave_sum(noise ? s[q] * (th[q] * rnrm) : 0.f);
+  }
+#pragma unroll
+  for (int q = 0; q < QN; ++q) {
+    const int c = lane + 64 * q;
+    const bool amp = c < K, gain = c == K || c == K + 1, noise = c >= K + 2 && c < K + 2 + NF;
+    float o = 0.f;  // padding columns stay exactly zero
+    if (amp) {
+      o = (s[q] - dot) * rden * softplus_grad(z[q]);
+    } else if (gain) {
+      o = s[q] * softplus_grad(z[q]);
+    } else if (noise) {
+      const float sg = th[q] > 0.f ? 1.f : (th[q] < 0.f ? -1.f : 0.f);
+      o = (s[q] - sg * dot2) * rnrm * (1.f - th[q] * th[q]);
     }
-    live = true;
+    out[q] = o;
+  }
+}
+
+// The row table of the backward runs (a static table, from the segment
+// rows and the row list): per run, entry 0 = {rows, 0, 0, 0}, then one
+// entry per control row its segments touch, in order of the row's first
+// in-run (segment, slot) entry: {row, before | outside << 8 | n << 16,
+// entries lo, hi}: where the run's sum goes (d ctrl when no entry of the row
+// lies outside the run, else the boundary partial at index `before`, the
+// number of runs listed before this one) and the run's n entries of the row
+// in list order, 4 bits each: (segment - s0) * 4 + slot.
+constexpr int kRunRows = kRunSegs * kSlots;
+static_assert(kRunRows <= 16 && kRowEntries <= 16, "run entries pack into 64 bits");
+
+__global__ void k_run_table(const float* __restrict__ seg_rows, const float* __restrict__ row_list,
+                            uint4* __restrict__ tab, int nseg) {
+  // one wave per run, one lane per (segment, slot) of the run: the lane
+  // holding its row's first in-run entry lists the row
+  const int run = blockIdx.x, lane = threadIdx.x;
+  const int s0 = run * kRunSegs, s1 = min(s0 + kRunSegs, nseg);
+  const int nq = (s1 - s0) * kSlots;
+  int r = -1;
+  if (lane < nq) {
+    const float rf = seg_rows[(size_t)s0 * kSlots + lane];
+    r = rf >= 0.0f ? (int)rf : -1;
+  }
+  float e[kRowEntries];
 #pragma unroll
-    for (int q = 0; q < kRowEntries; ++q) {
-      live = live && e[q] >= 0.f;
-      if (live) s += v[q];
+  for (int i = 0; i < kRowEntries; ++i) e[i] = r >= 0 ? row_list[(size_t)r * kRowEntries + i] : -1.0f;
+  int first = -1, before = 0, prev = -1, n = 0;
+  bool outside = false, live = true;
+  unsigned long long ent = 0;
+#pragma unroll
+  for (int i = 0; i < kRowEntries; ++i) {
+    live = live && e[i] >= 0.0f;
+    if (live) {
+      const int en = (int)e[i], rr = en / kSlots / kRunSegs;
+      if (rr == run) {
+        if (first < 0) first = en;
+        ent |= (unsigned long long)(en - s0 * kSlots) << (4 * n);
+        ++n;
+      } else {
+        outside = true;
+        if (first < 0 && rr != prev) ++before;
+      }
+      prev = rr;
     }
   }
+  const bool own = r >= 0 && first == s0 * kSlots + lane;
+  const unsigned long long m = __ballot(own);
+  uint4* t = tab + (size_t)run * (kRunRows + 1);
+  if (own) {
+    const int idx = __popcll(m & ((1ull << lane) - 1ull));
+    t[1 + idx] = make_uint4((unsigned)r, (unsigned)(before | (outside ? 1 : 0) << 8 | n << 16), (unsigned)ent,
+                            (unsigned)(ent >> 32));
+  }
+  if (lane == 0) t[0] = make_uint4((unsigned)__popcll(m), 0u, 0u, 0u);
+}
+
+int launch_run_table(const Launch& L, const dgen_hip_op& op) {
+  // arg: [0]=segment rows ([nseg][4]) [1]=row list ([F][16]) [2]=run table ([nruns][17] x 16 bytes) [3]=nseg [4]=F
+  const int64_t segr = op.arg[0], rowl = op.arg[1], tab = op.arg[2], nseg = op.arg[3], F = op.arg[4];
+  DGEN_REQUIRE(nseg > 0 && nseg <= (1 << 22) && F > 0 && F <= (1 << 22), "run_table: nseg %lld F %lld",
+               (long long)nseg, (long long)F);
+  const int64_t nruns = (nseg + kRunSegs - 1) / kRunSegs;
+  DGEN_CHECK_CELL(L, segr, nseg * kSlots, "run_table.seg_rows");
+  DGEN_CHECK_CELL(L, rowl, F * kRowEntries, "run_table.row_list");
+  DGEN_CHECK_CELL(L, tab, nruns * (kRunRows + 1) * 4, "run_table.table");
+  DGEN_REQUIRE(tab % 4 == 0, "run_table: table cell must be 16-byte aligned");
+  if (L.dry) return 0;
+  hipLaunchKernelGGL(k_run_table, dim3((unsigned)nruns), dim3(64), 0, L.stream, cell(L, segr), cell(L, rowl),
+                     reinterpret_cast<uint4*>(cell(L, tab)), (int)nseg);
+  DGEN_LAUNCH_CHECK("k_run_table");
+  return 0;
+}
+
+template <class SL>
+__global__ __launch_bounds__(64 * kRunSegs) void k_synth_bwd(SynthArgs a, const float* __restrict__ dy,
+                                                             const float* __restrict__ aux,
+                                                             const uint4* __restrict__ runtab,
+                                                             float* __restrict__ dctrl, float* __restrict__ bpart) {
+  __shared__ SL lds[kRunSegs];
+  __shared__ uint4 s_tab[kRunRows + 1];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int nseg = (a.T + kSeg - 1) / kSeg;
+  const int run = blockIdx.x, b = blockIdx.y;
+  const int s0 = run * kRunSegs;
+  // the run's row table, loaded at the start and staged after wave 0's segment
+  uint4 tv = make_uint4(0u, 0u, 0u, 0u);
+  if (wave == 0 && lane <= kRunRows) tv = runtab[(size_t)run * (kRunRows + 1) + lane];
+  if (s0 + wave < nseg) bwd_segment(a, lds[wave], dy, aux, s0 + wave, b, lane);
+  if (wave == 0 && lane <= kRunRows) s_tab[lane] = tv;
+  __syncthreads();
+  // each row's sum over the run's entries in list order, a wave per row
+  // (lane l: columns l + 64 q)
+  constexpr int QN = SL::kMaxNC / 64;
+  const int NC = a.K + 2 + a.NF;
+  const int ntab = (int)s_tab[0].x;
+  for (int t = wave; t < ntab; t += kRunSegs) {
+    const uint4 rr = s_tab[1 + t];
+    const int before = rr.y & 255, n_in = rr.y >> 16;
+    const bool outside = ((rr.y >> 8) & 255) != 0;
+    const unsigned long long ent = (unsigned long long)rr.z | (unsigned long long)rr.w << 32;
+    const size_t row = (size_t)b * a.F + rr.x;
+    float* dst = outside ? bpart + (row * kRunParts + min(before, kRunParts - 1)) * a.ldc : dctrl + row * a.ldc;
+#pragma unroll
+    for (int q = 0; q < QN; ++q) {
+      const int c = lane + 64 * q;
+      float sum = 0.0f;
+      if (c < NC)
+        for (int i = 0; i < n_in; ++i) {
+          const int le = (int)((ent >> (4 * i)) & 15ull);
+          sum += lds[le / kSlots].row[le % kSlots][c];
+        }
+      // a row in more runs than the partials hold (not produced by a
+      // playhead that wraps once) is marked NaN
+      if (c < a.ldc) dst[c] = before < kRunParts ? sum : __builtin_nanf("");
+    }
+  }
+}
+
+// d ctrl rows the synth backward left as boundary partials, a wave per row
+// (lane l: columns l + 64 q): row f's runs (the distinct runs of its listed
+// entries, in list order) each left one partial; they are added in that
+// order.  A row no segment touches is zero.  A row within one run was
+// completed by the synth backward (with Z it is read here for the head
+// backward; else skipped).  With Z, the head backward of every row.
+template <bool HEADS, int QN>
+__global__ __launch_bounds__(256) void k_synth_bwd_reduce(const float* __restrict__ bpart,
+                                                          const float* __restrict__ row_list, float* __restrict__ dctrl,
+                                                          int B, int NC, int ldc, int F, const float* __restrict__ Z,
+                                                          float* __restrict__ dZ, int K, int NF) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int f = blockIdx.x * 4 + wave, b = blockIdx.y;
+  if (f >= F) return;
   const size_t row = (size_t)b * F + f;
-  if (c < ldc) dctrl[row * ldc + c] = s;
+  // the row's runs (uniform across the wave)
+  const float* lst = row_list + (size_t)f * kRowEntries;
+  int nruns = 0, prev = -1;
+  for (int e = 0; e < kRowEntries; ++e) {
+    const float ef = lst[e];
+    if (ef < 0.0f) break;
+    const int rr = (int)ef / kSlots / kRunSegs;
+    if (rr != prev) ++nruns;
+    prev = rr;
+  }
+  const bool done = nruns == 1;  // completed by the synth backward
+  if (done && !HEADS) return;
+  float s[QN];
+#pragma unroll
+  for (int q = 0; q < QN; ++q) {
+    const int c = lane + 64 * q;
+    float v = 0.f;
+    if (done) {
+      if (c < NC) v = dctrl[row * ldc + c];
+      s[q] = v;
+      continue;
+    }
+    if (c < NC) {
+      const float* bp = bpart + row * kRunParts * ldc + c;
+      float u[kRunParts];
+#pragma unroll
+      for (int p = 0; p < kRunParts; ++p) u[p] = p < nruns ? bp[(size_t)p * ldc] : 0.f;
+#pragma unroll
+      for (int p = 0; p < kRunParts; ++p)
+        if (p < nruns) v += u[p];
+      if (nruns > kRunParts) v = __builtin_nanf("");
+    }
+    s[q] = v;
+    if (c < ldc) dctrl[row * ldc + c] = v;
+  }
   if constexpr (HEADS) {
-    __shared__ float red[16][4];  // per wave: sum sp, sum |th|, then the two dots
-    const int wave = c >> 6, lane = c & 63, nw = blockDim.x >> 6;
-    const bool amp = c < K, gain = c == K || c == K + 1, noise = c >= K + 2 && c < K + 2 + NF;
-    const float z = (amp || gain || noise) ? Z[row * ldc + c] : 0.f;
-    const float sp = amp ? softplus(z) : 0.f;
-    const float th = noise ? fast_tanh(z) : 0.f;
-    float r0 = wave_sum(sp), r1 = wave_sum(fabsf(th));
-    if (lane == 0) {
-      red[wave][0] = r0;
-      red[wave][1] = r1;
-    }
-    __syncthreads();
-    float den = 0.f, nrm = 0.f;
-    for (int w = 0; w < nw; ++w) {
-      den += red[w][0];
-      nrm += red[w][1];
-    }
-    den += 1e-6f;
-    nrm += 1e-4f;
-    const float rden = rcp_rn(den), rnrm = rcp_rn(nrm);
-    r0 = wave_sum(amp ? s * (sp * rden) : 0.f);
-    r1 = wave_sum(noise ? s * (th * rnrm) : 0.f);
-    if (lane == 0) {
-      red[wave][2] = r0;
-      red[wave][3] = r1;
-    }
-    __syncthreads();
-    float dot = 0.f, dot2 = 0.f;
-    for (int w = 0; w < nw; ++w) {
-      dot += red[w][2];
-      dot2 += red[w][3];
-    }
-    float out = 0.f;  // padding columns stay exactly zero
-    if (amp) {
-      out = (s - dot) * rden * softplus_grad(z);
-    } else if (gain) {
-      out = s * softplus_grad(z);
-    } else if (noise) {
-      const float sg = th > 0.f ? 1.f : (th < 0.f ? -1.f : 0.f);
-      out = (s - sg * dot2) * rnrm * (1.f - th * th);
-    }
-    if (c < ldc) dZ[row * ldc + c] = out;
+    float dz[QN];
+    head_row_bwd<QN>(s, Z + row * ldc, dz, lane, K, NF);
+#pragma unroll
+    for (int q = 0; q < QN; ++q)
+      if (lane + 64 * q < ldc) dZ[row * ldc + lane + 64 * q] = dz[q];
   }
 }
 
@@ -1181,8 +1340,9 @@ static int synth_args(const Launch& L, const dgen_hip_op& op, SynthArgs& a, cons
   return 0;
 }
 
-// The narrow LDS layout when the harmonics fit one group and the columns 128.
-static bool synth_narrow(const SynthArgs& a) { return a.K <= kMaxK && a.K + 2 + a.NF <= kMaxNC; }
+// The narrow LDS layout when the harmonics fit one group and the columns
+// (and the row stride) 128.
+static bool synth_narrow(const SynthArgs& a) { return a.K <= kMaxK && a.K + 2 + a.NF <= kMaxNC && a.ldc <= kMaxNC; }
 
 int launch_synth_fwd(const Launch& L, const dgen_hip_op& op) {
   SynthArgs a{};
@@ -1205,34 +1365,39 @@ int launch_synth_bwd(const Launch& L, const dgen_hip_op& op) {
   SynthArgs a{};
   int rc = synth_args(L, op, a, "synth_bwd");
   if (rc) return rc;
-  const int64_t T = op.arg[10], B = op.arg[6], ldc = op.arg[14];
+  // [12]=boundary partials ([B][F][6][ldc]) [16]=tape [17]=run table (DGEN_HIP_K_RUN_TABLE) [18]=dctrl
+  const int64_t T = op.arg[10], B = op.arg[6], F = op.arg[9], ldc = op.arg[14];
   const int64_t nseg = (T + kSeg - 1) / kSeg;
-  DGEN_CHECK_CELL(L, op.arg[12], B * nseg * kSlots * ldc, "synth_bwd.partials");
+  DGEN_CHECK_CELL(L, op.arg[12], B * F * kRunParts * ldc, "synth_bwd.boundary_partials");
   DGEN_CHECK_CELL(L, op.arg[16], 3 * B * T, "synth_bwd.aux");
+  DGEN_CHECK_CELL(L, op.arg[17], (nseg + kRunSegs - 1) / kRunSegs * (kRunRows + 1) * 4, "synth_bwd.run_table");
+  DGEN_REQUIRE(op.arg[17] % 4 == 0, "synth_bwd: run table cell must be 16-byte aligned");
+  DGEN_REQUIRE(ldc <= kMaxNCWide, "synth_bwd: row stride %lld > %d", (long long)ldc, kMaxNCWide);
+  DGEN_CHECK_CELL(L, op.arg[18], B * F * ldc, "synth_bwd.dctrl");
   if (L.dry) return 0;
-  const dim3 grid((unsigned)((nseg + kWavesBwd - 1) / kWavesBwd), (unsigned)a.B), block(64 * kWavesBwd);
+  const dim3 grid((unsigned)((nseg + kRunSegs - 1) / kRunSegs), (unsigned)a.B), block(64 * kRunSegs);
   if (synth_narrow(a))
-    hipLaunchKernelGGL(k_synth_bwd<SegLds>, grid, block, 0, L.stream, a, cell(L, op.arg[5]), cell(L, op.arg[16]),
-                       cell(L, op.arg[12]));
+    hipLaunchKernelGGL(k_synth_bwd<SegLdsBwd>, grid, block, 0, L.stream, a, cell(L, op.arg[5]), cell(L, op.arg[16]),
+                       reinterpret_cast<const uint4*>(cell(L, op.arg[17])), cell(L, op.arg[18]), cell(L, op.arg[12]));
   else
-    hipLaunchKernelGGL(k_synth_bwd<SegLdsWide>, grid, block, 0, L.stream, a, cell(L, op.arg[5]),
-                       cell(L, op.arg[16]), cell(L, op.arg[12]));
+    hipLaunchKernelGGL(k_synth_bwd<SegLdsBwdWide>, grid, block, 0, L.stream, a, cell(L, op.arg[5]),
+                       cell(L, op.arg[16]), reinterpret_cast<const uint4*>(cell(L, op.arg[17])),
+                       cell(L, op.arg[18]), cell(L, op.arg[12]));
   DGEN_LAUNCH_CHECK("k_synth_bwd");
   return 0;
 }
 
 int launch_synth_bwd_reduce(const Launch& L, const dgen_hip_op& op) {
-  // arg: [0]=partials [1]=row_list [2]=dctrl [3]=B [4]=NC [5]=F [6]=T [7]=seg [8]=ldc
+  // arg: [0]=boundary partials [1]=row_list [2]=dctrl [3]=B [4]=NC [5]=F [6]=T [7]=seg [8]=ldc
   //      [9]=Z or -1 [10]=dZ [11]=K [12]=NF (with Z: the head backward too)
   const int64_t part = op.arg[0], rl = op.arg[1], dc = op.arg[2], B = op.arg[3], NC = op.arg[4], F = op.arg[5],
                 T = op.arg[6], seg = op.arg[7], ldc = op.arg[8];
   const int64_t Zc = op.arg[9], dZc = op.arg[10], K = op.arg[11], NF = op.arg[12];
   const bool heads = Zc >= 0;
-  DGEN_REQUIRE(B > 0 && B <= 65535 && NC > 0 && ldc >= NC && ldc <= 1024 && F > 0 && T > 0 && seg == kSeg,
+  DGEN_REQUIRE(B > 0 && B <= 65535 && NC > 0 && ldc >= NC && ldc <= kMaxNCWide && F > 0 && T > 0 && seg == kSeg,
                "synth_bwd_reduce: B %lld NC %lld F %lld T %lld seg %lld ldc %lld", (long long)B, (long long)NC,
                (long long)F, (long long)T, (long long)seg, (long long)ldc);
-  const int64_t nseg = (T + seg - 1) / seg;
-  DGEN_CHECK_CELL(L, part, B * nseg * kSlots * ldc, "synth_bwd_reduce.partials");
+  DGEN_CHECK_CELL(L, part, B * F * kRunParts * ldc, "synth_bwd_reduce.boundary_partials");
   DGEN_CHECK_CELL(L, rl, F * kRowEntries, "synth_bwd_reduce.row_list");
   DGEN_CHECK_CELL(L, dc, B * F * ldc, "synth_bwd_reduce.dctrl");
   if (heads) {
@@ -1242,13 +1407,17 @@ int launch_synth_bwd_reduce(const Launch& L, const dgen_hip_op& op) {
     DGEN_CHECK_CELL(L, dZc, B * F * ldc, "synth_bwd_reduce.dZ");
   }
   if (L.dry) return 0;
-  const dim3 grid((unsigned)F, (unsigned)B), block((unsigned)((ldc + 63) / 64 * 64));
-  if (heads)
-    hipLaunchKernelGGL(k_synth_bwd_reduce<true>, grid, block, 0, L.stream, cell(L, part), cell(L, rl), cell(L, dc),
-                       (int)B, (int)NC, (int)ldc, (int)F, (int)nseg, cell(L, Zc), cell(L, dZc), (int)K, (int)NF);
+  const dim3 grid((unsigned)((F + 3) / 4), (unsigned)B), block(256);
+  float* zp = heads ? cell(L, Zc) : nullptr;
+  float* dzp = heads ? cell(L, dZc) : nullptr;
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, block, 0, L.stream, cell(L, part), cell(L, rl), cell(L, dc), (int)B, (int)NC,
+                       (int)ldc, (int)F, zp, dzp, (int)K, (int)NF);
+  };
+  if (ldc <= 128)
+    heads ? go(k_synth_bwd_reduce<true, 2>) : go(k_synth_bwd_reduce<false, 2>);
   else
-    hipLaunchKernelGGL(k_synth_bwd_reduce<false>, grid, block, 0, L.stream, cell(L, part), cell(L, rl), cell(L, dc),
-                       (int)B, (int)NC, (int)ldc, (int)F, (int)nseg, nullptr, nullptr, 0, 0);
+    heads ? go(k_synth_bwd_reduce<true, 8>) : go(k_synth_bwd_reduce<false, 8>);
   DGEN_LAUNCH_CHECK("k_synth_bwd_reduce");
   return 0;
 }

@@ -89,6 +89,7 @@ static Launcher launcher_for(uint32_t k) {
     case DGEN_HIP_K_SVF_BWD: return launch_svf_bwd;
     case DGEN_HIP_K_SPLIT_BF16: return launch_split_bf16;
     case DGEN_HIP_K_UOP_BLOCK: return launch_uop_block;
+    case DGEN_HIP_K_RUN_TABLE: return launch_run_table;
     default: return nullptr;
   }
 }

@@ -17,6 +17,8 @@ from .workloads import (BiquadConfig, HarmonicConfig, MembraneConfig, OscBankCon
 SEG = 64          # frames per synth segment (checkpoint spacing)
 SLOTS = 4         # control rows a segment may touch
 ROW_ENTRIES = 16  # (segment, slot) entries per control row (kRowEntries)
+RUN_SEGS = 4      # segments per synth-backward workgroup (kRunSegs)
+RUN_PARTS = 6     # boundary partials a control row holds (kRunParts)
 MAX_HARMONICS = 256  # the synth kernels' harmonic groups (four of 64)
 MAX_CONTROLS = 512   # control columns K + 2 + NF
 SPLITK_ROWS = 1024  # rows per split of the weight-gradient GEMMs
@@ -156,6 +158,11 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     rs_ws = p.alloc("row_schedule_ws", nseg + F)
     p.add(R.K_ROW_SCHEDULE, [play, lerp, segrows, rowlist, flag, F, T, SEG, rs_ws], flags=R.OP_STATIC,
           label="row_schedule", dispatch="static singleThreaded")
+    # the synth backward's runs of RUN_SEGS segments: each run's control rows
+    nruns = (nseg + RUN_SEGS - 1) // RUN_SEGS
+    runtab = p.alloc("run_table", nruns * (RUN_SEGS * SLOTS + 1) * 4)
+    p.add(R.K_RUN_TABLE, [segrows, rowlist, runtab, nseg, F], flags=R.OP_STATIC, label="run_table",
+          dispatch="static perRun")
 
     # ---- activations
     Hs = [p.alloc(f"H{l + 1}", M * Hd) for l in range(Lyr)]
@@ -269,21 +276,26 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     larg2 = [-1, lossf] + garg[2:]
     nwin_all = sum((T + N // 4 - 1) // (N // 4) for N in sizes)
 
-    part = p.alloc("synth_partials", B * nseg * SLOTS * LDC)
+    # the backward's workgroups own runs of RUN_SEGS segments and write the
+    # rows within their run to d ctrl; a row shared between runs leaves one
+    # partial per run ([B][F][RUN_PARTS][LDC]), added by the row reduce
+    bpart = p.alloc("synth_boundary_partials", B * F * RUN_PARTS * LDC)
     dctrl = p.alloc("dctrl", M * LDC)
     bargs = list(synth_args)
     bargs[5] = dy
-    bargs[12] = part
-    bargs.append(aux)
-    part_b = B * nseg * SLOTS * NC * f4
+    bargs[12] = bpart
+    bargs += [aux, runtab, dctrl]
+    # rows per lane: shared by two runs at each run boundary
+    shared = min(F, 2 * max(0, nruns - 1))
+    bpart_b = B * 2 * shared * NC * f4
     p.add(R.K_SYNTH_BWD, bargs, [cfg.sr, hs, ns], label="synth_bwd", dispatch=f"selfManagedThreads({B})",
-          bytes=ctrl_b + lerp_b + ck_b + data_b + 4 * B * T * f4 + part_b,
+          bytes=ctrl_b + lerp_b + ck_b + data_b + 4 * B * T * f4 + (M - B * shared) * NC * f4 + bpart_b,
           flops=synth_flops + float(B) * T * (6.0 * K + 4.0 * NC), bound="valu")
-    # the row reduce also runs the head backward of its row (dZ from d ctrl and Z)
+    # the row reduce also runs the head backward of every row (dZ from d ctrl and Z)
     dZ = p.alloc("dZ", M * LDC)
-    p.add(R.K_SYNTH_BWD_REDUCE, [part, rowlist, dctrl, B, NC, F, T, SEG, LDC, Z, dZ, K, NF], label="synth_bwd_reduce",
-          dispatch=f"perFrameScaled({M})", bytes=part_b + F * ROW_ENTRIES * f4 + 3 * M * NC * f4,
-          flops=part_b / f4 + M * (K * 20.0 + NF * 14.0))
+    p.add(R.K_SYNTH_BWD_REDUCE, [bpart, rowlist, dctrl, B, NC, F, T, SEG, LDC, Z, dZ, K, NF], label="synth_bwd_reduce",
+          dispatch=f"perFrameScaled({M})", bytes=bpart_b + F * ROW_ENTRIES * f4 + 3 * M * NC * f4,
+          flops=bpart_b / f4 + M * (K * 20.0 + NF * 14.0))
 
     G = p.alloc("grads", npar)
     split = max(1, (M + SPLITK_ROWS - 1) // SPLITK_ROWS)

@@ -63,6 +63,7 @@ K_SVF_BWD = 37
 K_STREAM_SVF = 38
 K_SPLIT_BF16 = 39
 K_UOP_BLOCK = 40
+K_RUN_TABLE = 41
 
 KERNEL_NAMES = {v: k[2:].lower() for k, v in globals().items() if k.startswith("K_")}
 

@@ -145,16 +145,23 @@ enum dgen_hip_kernel {
    *       gradient 2 w (x - target) / B joins dx) or 0 */
   DGEN_HIP_K_SPECTRAL_GATHER = 8,
 
-  /* Synth backward: d ctrl row partials per segment.
-   * arg: as DGEN_HIP_K_SYNTH_FWD with [5]=dy ([B][T]) [12]=partials cell
-   *      ([B][nseg][4][ldc]) [16]=the forward's per-frame tape */
+  /* Synth backward.  A workgroup owns a run of 4 consecutive segments of a
+   * lane and sums its segments' row-slot gradients per control row in LDS:
+   * rows whose listed (segment, slot) entries all lie in the run are
+   * written to d ctrl; a row shared with other runs leaves one partial per
+   * run, at the run's index among the row's runs.
+   * arg: as DGEN_HIP_K_SYNTH_FWD with [5]=dy ([B][T]) [12]=boundary partials
+   *      cell ([B][F][6][ldc]) [16]=the forward's per-frame tape [17]=run
+   *      table (DGEN_HIP_K_RUN_TABLE) [18]=dctrl ([B*F][ldc]) */
   DGEN_HIP_K_SYNTH_BWD = 9,
 
-  /* Deterministic reduction of synth-backward segment partials into d ctrl.
-   * arg: [0]=partials [1]=playhead [2]=dctrl [3]=B [4]=NC [5]=F [6]=T [7]=seg
-   *      [8]=row stride [9]=Z cell or -1: with Z, the head backward of each
-   *      row too (as DGEN_HIP_K_HEADS_BWD), into [10]=dZ, [11]=K [12]=NF
-   *      (K + 2 + NF = NC) */
+  /* d ctrl of the rows shared between synth-backward runs: their partials
+   * added in run order (deterministic); a row no segment touches is zero.
+   * Rows within one run are left as the synth backward wrote them.
+   * arg: [0]=boundary partials [1]=row list [2]=dctrl [3]=B [4]=NC [5]=F
+   *      [6]=T [7]=seg [8]=row stride [9]=Z cell or -1: with Z, the head
+   *      backward of every row too (as DGEN_HIP_K_HEADS_BWD), into [10]=dZ,
+   *      [11]=K [12]=NF (K + 2 + NF = NC) */
   DGEN_HIP_K_SYNTH_BWD_REDUCE = 10,
 
   /* Head backward: dZ from d ctrl and Z.  arg: [0]=Z [1]=dctrl [2]=dZ
@@ -413,6 +420,16 @@ enum dgen_hip_kernel {
    * farg: [0]=the graph's sample rate (the hostSampleRate UOp; a run's host
    *       rate replaces it) */
   DGEN_HIP_K_UOP_BLOCK = 40,
+
+  /* Row table of the synth backward's runs of 4 segments, a static table:
+   * per run, {rows, 0, 0, 0} then per control row its segments touch
+   * {row, before | outside << 8 | n << 16, entries lo, hi} (where the run's
+   * sum of the row goes, and the run's n (segment, slot) entries of the row
+   * in list order, 4 bits each).
+   * arg: [0]=segment rows ([nseg][4]) [1]=row list ([F][16], both from
+   *      DGEN_HIP_K_ROW_SCHEDULE) [2]=table (ceil(nseg/4) x 17 x 4 floats,
+   *      16-byte aligned) [3]=nseg [4]=F */
+  DGEN_HIP_K_RUN_TABLE = 41,
 };
 
 /* GEMM epilogues */

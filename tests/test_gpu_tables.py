@@ -3,7 +3,8 @@
 a sequential restatement of Emit+RowSelection.swift:164-197, bit for bit,
 for config 3's playhead, a control hop of 256, a wrapping playhead, and
 playheads that overflow a segment's slots, a row's entries or are not
-finite; the xorshift32 noise table (built by bit-matrix jump-ahead) and the
+finite; the synth backward's run table (DGEN_HIP_K_RUN_TABLE) against a
+restatement from the same segment rows and row lists; the xorshift32 noise table (built by bit-matrix jump-ahead) and the
 playhead accumulator against the oracle's sequential streams.  Needs a GPU."""
 import math
 
@@ -17,6 +18,7 @@ from dgen_hip.program import Program
 pytestmark = pytest.mark.gpu
 
 SEG, SLOTS, ENTRIES = 64, 4, 16
+RUN_SEGS, RUN_PARTS = 4, 6
 
 
 def schedule_ref(play, rows, frames):
@@ -61,8 +63,47 @@ def schedule_ref(play, rows, frames):
     return lerp, seg_rows, row_list, status
 
 
+def run_table_ref(seg_rows, row_list, nseg):
+    """Per run of RUN_SEGS segments: [0] = (rows, 0, 0, 0), then per control
+    row its segments touch, in order of the row's first in-run entry,
+    (row, before | outside << 8 | n << 16, entries lo, hi) with the run's n
+    entries of the row packed 4 bits each as (segment - s0) * 4 + slot."""
+    nruns = (nseg + RUN_SEGS - 1) // RUN_SEGS
+    tab = np.zeros((nruns, RUN_SEGS * SLOTS + 1, 4), np.uint32)
+    for run in range(nruns):
+        s0, s1 = run * RUN_SEGS, min(run * RUN_SEGS + RUN_SEGS, nseg)
+        out = []
+        for q in range((s1 - s0) * SLOTS):
+            sq, j = s0 + q // SLOTS, q % SLOTS
+            if seg_rows[sq, j] < 0:
+                continue
+            r = int(seg_rows[sq, j])
+            first, before, prev, outside, ents = -1, 0, -1, False, []
+            for e in row_list[r]:
+                if e < 0:
+                    break
+                en = int(e)
+                rr = en // SLOTS // RUN_SEGS
+                if rr == run:
+                    first = en if first < 0 else first
+                    ents.append(en - s0 * SLOTS)
+                else:
+                    outside = True
+                    if first < 0 and rr != prev:
+                        before += 1
+                prev = rr
+            if first == sq * SLOTS + j:
+                packed = sum(v << (4 * i) for i, v in enumerate(ents))
+                out.append((r, before | int(outside) << 8 | len(ents) << 16, packed & 0xFFFFFFFF, packed >> 32))
+        tab[run, 0, 0] = len(out)
+        for i, e in enumerate(out):
+            tab[run, 1 + i] = e
+    return tab
+
+
 def run_schedule(play, rows, frames):
     nseg = (frames + SEG - 1) // SEG
+    nruns = (nseg + RUN_SEGS - 1) // RUN_SEGS
     p = Program(max_frames=frames)
     pc = p.alloc("play", frames)
     lerp = p.alloc("lerp", frames * 8)
@@ -70,12 +111,15 @@ def run_schedule(play, rows, frames):
     rowl = p.alloc("row_list", rows * ENTRIES)
     flag = p.alloc("flag", 1)
     ws = p.alloc("ws", nseg + rows)
+    tab = p.alloc("run_table", nruns * (RUN_SEGS * SLOTS + 1) * 4)
     p.add(R.K_ROW_SCHEDULE, [pc, lerp, segr, rowl, flag, rows, frames, SEG, ws], label="row_schedule")
+    p.add(R.K_RUN_TABLE, [segr, rowl, tab, nseg, rows], label="run_table")
     with R.HIPLazyRuntime(p, 0) as rt:
         rt.write("play", np.asarray(play, np.float32))
         rt.runNoCopy()
         return (rt.read("lerp").reshape(frames, 8), rt.read("seg_rows").reshape(nseg, SLOTS),
-                rt.read("row_list").reshape(rows, ENTRIES), float(rt.read("flag")[0]))
+                rt.read("row_list").reshape(rows, ENTRIES), float(rt.read("flag")[0]),
+                rt.read("run_table").view(np.uint32).reshape(nruns, RUN_SEGS * SLOTS + 1, 4))
 
 
 CASES = {
@@ -104,6 +148,16 @@ def test_row_schedule_matches_the_sequential_schedule(gpu, name):
     assert got[3] == ref[3], (got[3], ref[3])
     expect = {"slot overflow": 1.0, "entry overflow": 2.0, "non-finite": 3.0}.get(name, 0.0)
     assert got[3] == expect
+    # the run table from the GPU's segment rows and row lists (rows past a
+    # run's count are not read)
+    tab, tref = got[4], run_table_ref(got[1], got[2], got[1].shape[0])
+    for run in range(tab.shape[0]):
+        n = int(tref[run, 0, 0])
+        np.testing.assert_array_equal(tab[run, :1 + n], tref[run, :1 + n], err_msg=f"run {run}")
+    if expect == 0.0:
+        # a valid schedule's rows meet at most RUN_PARTS runs
+        before = tref[:, 1:, 1] & 255
+        assert before.max() < RUN_PARTS
 
 
 @pytest.mark.parametrize("frames", [1, 255, 256, 257, 64000, 100003])
