@@ -185,40 +185,14 @@ __device__ __forceinline__ float wave_sum(float v) {
 // evaluate sin(2 pi p), a function whose phase runs 2.78e-8 slow: a
 // systematic, phase-proportional error (up to 1.75e-7 rad) that puts
 // coherent error lines into the spectrum, where a random rounding error of
-// the same size would not.  Both forms below evaluate the reference's
+// the same size would not.  The forms below evaluate the reference's
 // function itself.
 //
 // kTwoPiF32Excess = 2pi_f32 - 2pi (rounded to fp32).
 constexpr float kTwoPiF32Excess = 0x1.777a5cp-23f;
-// kTwoPiF32Rel = (2pi_f32 - 2pi) / 2pi (rounded to fp32).
-constexpr float kTwoPiF32Rel = 0x1.de12ccp-26f;
-
-// sin(p * 2pi_f32) for p in [0, 1), to ~1.3 ulp (max abs error 8e-8
-// against the exact value over a 2^15-point grid): p = q/4 + r exactly
-// (|r| <= 1/8), r corrected by the constant's excess, then the Taylor
-// polynomials of sin(2 pi r) (through r^9) and cos(2 pi r) (through r^10)
-// and the quadrant's sign and swap.  ~18 VALU operations.
-__device__ __forceinline__ float sin_2pif(float p) {
-  const float q = rintf(4.0f * p);
-  const float r = fmaf(kTwoPiF32Rel, p, fmaf(-q, 0.25f, p));
-  const float r2 = r * r;
-  float ps = fmaf(r2, 0x1.507834p+5f, -0x1.32d2ccp+6f);
-  ps = fmaf(r2, ps, 0x1.466bc6p+6f);
-  ps = fmaf(r2, ps, -0x1.4abbcep+5f);
-  ps = fmaf(r2, ps, 0x1.921fb6p+2f);
-  const float sv = ps * r;
-  float pc = fmaf(r2, -0x1.a6d1f2p+4f, 0x1.e1f506p+5f);
-  pc = fmaf(r2, pc, -0x1.55d3c8p+6f);
-  pc = fmaf(r2, pc, 0x1.03c1f0p+6f);
-  pc = fmaf(r2, pc, -0x1.3bd3ccp+4f);
-  const float cv = fmaf(r2, pc, 1.0f);
-  const int qi = (int)q;
-  const float v = (qi & 1) ? cv : sv;
-  return (qi & 2) ? -v : v;
-}
-
-// The same function on the hardware units, to their accuracy (~1.3e-7
-// absolute): sin(2 pi p + e p) ~ sin(2 pi p) + e p cos(2 pi p), e the
+// sin(p * 2pi_f32) for p in [0, 1) on the hardware units, to their
+// accuracy (max abs error 1.4e-7 against the exact value over a 2^24-point
+// grid): sin(2 pi p + e p) ~ sin(2 pi p) + e p cos(2 pi p), e the
 // constant's excess.  Two transcendental operations and one FMA.
 __device__ __forceinline__ float sin_2pif_hw(float p) {
   return fmaf(p * kTwoPiF32Excess, __builtin_amdgcn_cosf(p), __builtin_amdgcn_sinf(p));

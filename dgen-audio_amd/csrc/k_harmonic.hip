@@ -61,16 +61,17 @@ __device__ __forceinline__ float div_sr(float x, float sr, float rsr) {
 }
 
 // sin(p * 2pi_f32), the expression the reference evaluates
-// (CRenderer.swift:825-827), for p in [0, 1): the synth forward evaluates
-// it by polynomial (sin_2pif, ~1 ulp), because the prediction's rounding
-// reaches the gradient through the log-magnitude loss's ill-conditioned
-// bins (measured at B=4, T=64000 against finite differences of the fp64
-// forward: the whole gradient 4.2% from fp64 with the hardware sin(2 pi p),
-// 1.3% with this); the backward's amplitude factors take the hardware form
-// of the same function (sin_2pif_hw), whose rounding enters the gradient
-// only linearly.
-__device__ __forceinline__ float sin2pi(float p) { return sin_2pif(p); }
-__device__ __forceinline__ float sin2pi_bwd(float p) { return sin_2pif_hw(p); }
+// (CRenderer.swift:825-827), for p in [0, 1): the hardware sine of 2 pi p
+// with the first-order correction for the fp32 constant's excess
+// (sin_2pif_hw).  Against the reference's own fp32 evaluation,
+// sinf(RN(p * 2pi_f32)), it is within 3.0e-7 (rms 7.5e-8; the argument's
+// rounding dominates), against the exact sin(p * 2pi_f32) within 1.4e-7.
+// The uncorrected sin(2 pi p) put a phase-proportional error into the
+// prediction that doubled the gradient's distance from finite differences
+// through the log-magnitude loss (B=4, T=64000: the whole gradient 4.2%
+// from fp64, against 2.3% with the correction and 2.6% for the fp32
+// oracle).
+__device__ __forceinline__ float sin2pi(float p) { return sin_2pif_hw(p); }
 
 // ------------------------------------------------------------ frame-rate data
 // out[b][t] = (1-frac_t) * src[lo_t][b] + frac_t * src[hi_t][b]: the sampleRow
@@ -918,7 +919,7 @@ __device__ __forceinline__ void bwd_harmonic_pass(const SynthArgs& a, const SL& 
       ph = FAST ? __builtin_amdgcn_fractf(ph + inc) : phasor_wrap(ph + inc);
       // every lane evaluates the sine (opaque to the compiler), so the
       // selects below stay branch-free instead of nested exec-mask regions
-      float sv = sin2pi_bwd(p);
+      float sv = sin2pi(p);
       asm volatile("" : "+v"(sv));
       const float hm = (sv - hs[j]) * cf[j];
       const float dm = harm ? (MASKC || freq < nyq ? hm : 0.0f) : ex[j];
