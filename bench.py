@@ -144,7 +144,7 @@ def time_session(rt, program, args):
     dom.meas_ms = rt.time_op(dom.index, args.op_iters)
     top = sorted(rows, key=lambda r: -r.in_step_ms)[:14]
     for r in top:
-        r.meas_ms = dom.meas_ms if r is dom else rt.time_op(r.index, args.op_iters)
+        r.meas_ms = rt.time_op_alone(r.index, args.op_iters)
     for r in sorted(top, key=lambda r: -r.meas_ms):
         log(f"  {r.label:18s} {r.bound:5s} {'side' if r.side else 'main'} alone {r.meas_ms * 1e3:8.1f} us  "
             f"in step {r.in_step_ms * 1e3:8.1f} us  roof {r.roof_ms * 1e3:8.1f} us  frac {r.frac:6.3f}")
@@ -165,12 +165,13 @@ def measured_traffic(workload: str, label: str):
         return None
 
 
-def traffic_run(sess, workload: str, runs: int) -> int:
-    """Driver for the traffic passes: one full run (so every cell holds
-    its values), then for each op with the largest roofline time a plain
-    1 GiB device-to-device copy (the HIP runtime's copy kernel: the counter
-    calibration, and a separator) and the op alone `runs` times.  Prints the
-    op labels as one JSON line."""
+def traffic_run(sess, workload: str, runs: int, labels: str | None = None) -> int:
+    """Driver for the counter passes: one full run (so every cell holds
+    its values), then for each op with the largest roofline time (or each
+    op in the comma-separated `labels`) a plain 1 GiB device-to-device copy
+    (the HIP runtime's copy kernel: the counter calibration, and a
+    separator) and the op alone `runs` times.  Prints the op labels as one
+    JSON line."""
     import ctypes
 
     from dgen_hip.roofline import roof_seconds
@@ -179,6 +180,8 @@ def traffic_run(sess, workload: str, runs: int) -> int:
     per_run = [(i, roof_seconds(op)) for i, op in enumerate(prog.ops) if not op.flags & OP_STATIC]
     top = max(r for _, r in per_run)
     idx = [i for i, r in per_run if r >= top * (1.0 - 1e-9)]
+    if labels:
+        idx = [prog.find(lab) for lab in labels.split(",")]
     sess.rt.runNoCopy()
     hip = ctypes.CDLL("libamdhip64.so")  # the runtime libdgen_hip.so is linked against, already loaded
     hip.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
@@ -553,6 +556,8 @@ def main() -> int:
     ap.add_argument("--op-iters", type=int, default=10, help="runs averaged for the dominant kernel's time")
     ap.add_argument("--traffic-runs", type=int, default=0,
                     help="instead of timing: run the dominant op alone this many times (for rocprofv3 --pmc)")
+    ap.add_argument("--traffic-ops", default=None,
+                    help="with --traffic-runs: the comma-separated op labels to run instead of the dominant op")
     ap.add_argument("--no-graphs", dest="graphs", action="store_false",
                     help="enqueue every kernel from the host instead of replaying each step as a HIP graph")
     ap.add_argument("--workload", choices=("harmonic", "biquad", "stft", "membrane", "oscbank", "svf", "svf-sat"),
@@ -583,7 +588,7 @@ def run_harmonic(args) -> dict:
     sess = HarmonicSession(cfg, device=0, optimizer=True)
     if args.traffic_runs:
         try:
-            traffic_run(sess, "harmonic", args.traffic_runs)
+            traffic_run(sess, "harmonic", args.traffic_runs, args.traffic_ops)
         finally:
             sess.close()
         return None

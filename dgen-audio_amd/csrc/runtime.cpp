@@ -736,6 +736,36 @@ int dgen_hip_time_op(dgen_hip_ctx* c, uint32_t frame_count, uint32_t op_index, i
   return rc;
 }
 
+int dgen_hip_time_op_alone(dgen_hip_ctx* c, uint32_t frame_count, uint32_t op_index, int iters, double* ms_out) {
+  if (!ms_out || iters <= 0) return fail(DGEN_HIP_E_INVALID, "time_op_alone: bad arguments");
+  int rc = run_checks(c, frame_count);
+  if (rc) return rc;
+  if (op_index >= c->ops.size() || (c->ops[op_index].flags & DGEN_HIP_OP_STATIC))
+    return fail(DGEN_HIP_E_INVALID, "time_op_alone: op %u is not a per-run op", op_index);
+  rc = dgen_hip_sync(c);
+  if (rc) return rc;
+  const dgen_hip_op& op = c->ops[op_index];
+  const Launch L = make_launch(c, c->s0, frame_count, false);
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  DGEN_HIP_TRY(hipEventCreate(&e0));
+  if (hipEventCreate(&e1) != hipSuccess) {
+    (void)hipEventDestroy(e0);
+    return fail(DGEN_HIP_E_DEVICE, "time_op_alone: hipEventCreate failed");
+  }
+  rc = launcher_for(op.kernel)(L, op);
+  if (!rc && hipEventRecord(e0, c->s0) != hipSuccess) rc = fail(DGEN_HIP_E_DEVICE, "time_op_alone: event record");
+  for (int it = 0; it < iters && !rc; ++it) rc = launcher_for(op.kernel)(L, op);
+  if (!rc && hipEventRecord(e1, c->s0) != hipSuccess) rc = fail(DGEN_HIP_E_DEVICE, "time_op_alone: event record");
+  const int rc2 = dgen_hip_sync(c);
+  if (!rc) rc = rc2;
+  float ms = 0.f;
+  if (!rc && hipEventElapsedTime(&ms, e0, e1) != hipSuccess)
+    rc = fail(DGEN_HIP_E_DEVICE, "time_op_alone: hipEventElapsedTime failed");
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  *ms_out = rc ? 0.0 : (double)ms / iters;
+  return rc;
+}
 
 // ---- generic UOp blocks: hiprtc compile with a per-process cache ---------
 namespace {

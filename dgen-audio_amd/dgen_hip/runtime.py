@@ -74,7 +74,8 @@ EXPORTED_SYMBOLS = (
     "dgen_hip_abi_version", "dgen_hip_device_count", "dgen_hip_create", "dgen_hip_destroy",
     "dgen_hip_last_error", "dgen_hip_configure", "dgen_hip_host_memory", "dgen_hip_upload",
     "dgen_hip_download", "dgen_hip_zero", "dgen_hip_run", "dgen_hip_run_async", "dgen_hip_sync", "dgen_hip_set_graphs",
-    "dgen_hip_profile", "dgen_hip_time_runs", "dgen_hip_time_op", "dgen_hip_run_op", "dgen_hip_set_outputs",
+    "dgen_hip_profile", "dgen_hip_time_runs", "dgen_hip_time_op", "dgen_hip_time_op_alone", "dgen_hip_run_op",
+    "dgen_hip_set_outputs",
     "dgen_hip_host_outputs", "dgen_hip_set_sample_rate", "dgen_hip_biquad_forward_noalloc",
     "dgen_hip_set_process_ports", "dgen_hip_process_v1", "dgen_hip_process_bind", "dgen_hip_process_memory_size",
     "dgen_hip_set_blocks", "dgen_hip_render_blocks",
@@ -141,6 +142,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
                               ctypes.POINTER(ctypes.c_size_t)], i32),
         "dgen_hip_time_runs": ([vp, u32, i32, i32, ctypes.POINTER(ctypes.c_double)], i32),
         "dgen_hip_time_op": ([vp, u32, u32, i32, ctypes.POINTER(ctypes.c_double)], i32),
+        "dgen_hip_time_op_alone": ([vp, u32, u32, i32, ctypes.POINTER(ctypes.c_double)], i32),
         "dgen_hip_run_op": ([vp, u32, u32], i32),
         "dgen_hip_set_outputs": ([vp, u64, u64], i32),
         "dgen_hip_host_outputs": ([vp, ctypes.POINTER(u64)], ctypes.POINTER(ctypes.c_float)),
@@ -348,6 +350,13 @@ class HIPLazyRuntime:
         ms = ctypes.c_double(0.0)
         _check(self.L.dgen_hip_time_op(self._ctx, self._frames(frameCount), index, iters,
                                        ctypes.byref(ms)), "dgen_hip_time_op")
+        return ms.value
+
+    def time_op_alone(self, index: int, iters: int, frameCount: int | None = None) -> float:
+        """Average ms of op `index` run alone, back to back on stream 0."""
+        ms = ctypes.c_double(0.0)
+        _check(self.L.dgen_hip_time_op_alone(self._ctx, self._frames(frameCount), index, iters,
+                                             ctypes.byref(ms)), "dgen_hip_time_op_alone")
         return ms.value
 
     def run_op(self, index: int, frameCount: int | None = None) -> None:

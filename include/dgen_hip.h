@@ -751,6 +751,13 @@ int dgen_hip_run_op(dgen_hip_ctx* ctx, uint32_t frame_count, uint32_t op_index);
  * runs, timed with hipEvents recorded on the stream that op launches on. */
 int dgen_hip_time_op(dgen_hip_ctx* ctx, uint32_t frame_count, uint32_t op_index, int iters, double* ms_out);
 
+/* Average duration of schedule op `op_index` run alone: one untimed run,
+ * then `iters` runs back to back on stream 0 between one hipEvent pair, on
+ * the arena's current contents, nothing else in flight.  (dgen_hip_time_op
+ * times the op inside whole runs, where a side-stream op shares the chip
+ * with the stream-0 work it overlaps.)  No counterpart in the reference. */
+int dgen_hip_time_op_alone(dgen_hip_ctx* ctx, uint32_t frame_count, uint32_t op_index, int iters, double* ms_out);
+
 /* ---- bank forward without allocation --------------------------------------
  * No counterpart in the reference.  For callers that cannot allocate device
  * memory (code under HIP graph capture, real-time render loops, hosts that
