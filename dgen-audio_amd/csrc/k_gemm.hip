@@ -747,11 +747,12 @@ __global__ void k_split_bf16(const float* __restrict__ src, uint4* __restrict__ 
 }
 
 int launch_split_bf16(const Launch& L, const dgen_hip_op& op) {
-  // arg: [0]=src [1]=planes [2]=K [3]=N [4]=ld_k [5]=ld_n
+  // arg: [0]=src [1]=planes [2]=K [3]=N [4]=ld_k [5]=ld_n [6]=groups of 8 k-values (0: ceil(K/8))
   const int64_t src = op.arg[0], dst = op.arg[1], K = op.arg[2], N = op.arg[3], ldk = op.arg[4], ldn = op.arg[5];
   DGEN_REQUIRE(K > 0 && N > 0 && K < (1 << 24) && N < (1 << 24) && ldk >= 0 && ldn >= 0,
                "split_bf16: K %lld N %lld ld %lld %lld", (long long)K, (long long)N, (long long)ldk, (long long)ldn);
-  const int64_t K8 = (K + 7) / 8;
+  const int64_t K8 = op.arg[6] > 0 ? op.arg[6] : (K + 7) / 8;
+  DGEN_REQUIRE(K8 >= (K + 7) / 8 && K8 < (1 << 21), "split_bf16: %lld groups for K %lld", (long long)K8, (long long)K);
   DGEN_REQUIRE(K8 * N < (1ll << 31), "split_bf16: %lld x %lld too large", (long long)K, (long long)N);
   DGEN_REQUIRE(dst % 4 == 0, "split_bf16: planes cell %lld not 16-byte aligned", (long long)dst);
   DGEN_CHECK_CELL(L, src, (K - 1) * ldk + (N - 1) * ldn + 1, "split_bf16.src");
@@ -897,9 +898,11 @@ int launch_gemm(const Launch& L, const dgen_hip_op& op) {
   }
   DGEN_REQUIRE(ldc >= N, "gemm: ldc %lld < N %lld", (long long)ldc, (long long)N);
   DGEN_REQUIRE(alay == 0 ? lda >= K : lda >= M, "gemm: lda %lld too small", (long long)lda);
-  DGEN_REQUIRE(blay == 0 ? ldb >= N : ldb >= K, "gemm: ldb %lld too small", (long long)ldb);
   DGEN_CHECK_CELL(L, A, alay == 0 ? (M - 1) * lda + K : (K - 1) * lda + M, "gemm.A");
-  DGEN_CHECK_CELL(L, Bc, blay == 0 ? (K - 1) * ldb + N : (N - 1) * ldb + K, "gemm.B");
+  if (planes < 0) {  // with planes the kernels read B only through them
+    DGEN_REQUIRE(blay == 0 ? ldb >= N : ldb >= K, "gemm: ldb %lld too small", (long long)ldb);
+    DGEN_CHECK_CELL(L, Bc, blay == 0 ? (K - 1) * ldb + N : (N - 1) * ldb + K, "gemm.B");
+  }
   DGEN_CHECK_CELL(L, Cc, (M - 1) * ldc + N, "gemm.C");
   if (epi == EPI_BIAS || epi == EPI_BIAS_TANH) DGEN_CHECK_CELL(L, bias, N, "gemm.bias");
   if (epi == EPI_TANH_GRAD) {

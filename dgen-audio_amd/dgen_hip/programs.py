@@ -47,12 +47,12 @@ def _gemm_args(mode: int, args: list, b_planes: int = -1) -> list:
     return a + [mode, b_planes if mode == 1 else -1]
 
 
-def _split_planes(p: Program, name: str, src: int, K: int, N: int, ldk: int, ldn: int) -> int:
+def _split_planes(p: Program, name: str, src: int, K: int, N: int, ldk: int, ldn: int, k_pad: int = 0) -> int:
     """A DGEN_HIP_K_SPLIT_BF16 op of the [K][N] view (k, n) -> src[k*ldk + n*ldn]
-    into a new planes cell; returns the cell."""
-    k8 = (K + 7) // 8
+    into a new planes cell (zero for K <= k < k_pad); returns the cell."""
+    k8 = (max(K, k_pad) + 7) // 8
     cell = p.alloc(name, 3 * k8 * N * 4)
-    p.add(R.K_SPLIT_BF16, [src, cell, K, N, ldk, ldn], label=name, dispatch="perElement",
+    p.add(R.K_SPLIT_BF16, [src, cell, K, N, ldk, ldn, k8], label=name, dispatch="perElement",
           bytes=K * N * 4.0 + 3 * k8 * N * 16.0, flops=6.0 * K * N)
     return cell
 
@@ -196,6 +196,10 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     # GEMM tile splits them again
     fwd_pl, bwd_pl = [-1] * Lyr, [-1] * Lyr
     fwd_plh = bwd_plh = -1
+    # the heads' data gradient runs over NC rounded up to 32 (dZ's padding
+    # columns are zero, and so are the planes' rows past NC), so its tiles
+    # take the pipelined full-tile kernel (whole k-steps of 32)
+    kh = NC if gm == 0 else min(LDC, (NC + 31) // 32 * 32)
     if gm == 1:
         for l in range(1, Lyr):
             W, _b = woff[l]
@@ -204,7 +208,7 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
                 bwd_pl[l] = _split_planes(p, f"W{l + 1}T_planes", W, Hd, Hd, 1, Hd)
         fwd_plh = _split_planes(p, "Wh_planes", Wh, Hd, NC, NC, 1)
         if train:
-            bwd_plh = _split_planes(p, "WhT_planes", Wh, NC, Hd, 1, NC)
+            bwd_plh = _split_planes(p, "WhT_planes", Wh, NC, Hd, 1, NC, k_pad=kh)
     for l in range(1, Lyr):
         W, b = woff[l]
         p.add(R.K_GEMM, _gemm_args(gm, [Hs[l - 1], W, Hs[l], M, Hd, Hd, Hd, Hd, Hd, 0, 0, R.EPI_BIAS_TANH, b, -1, 0, 1,
@@ -327,7 +331,7 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
         raise ValueError(f"first-layer fan-in {din} > 4")
     dcol = [p.alloc(f"dZ{l + 1}_tile_colsums", mt * (din + 1 if l == 0 else 1) * Hd) for l in range(Lyr)]
     wcol = [[X, din] if l == 0 else [-1, 0] for l in range(Lyr)]
-    p.add(R.K_GEMM, _gemm_args(gm, [dZ, Wh, dH[-1], M, Hd, NC, LDC, NC, Hd, 0, 1, R.EPI_TANH_GRAD, -1, Hs[-1], Hd, 1, 0,
+    p.add(R.K_GEMM, _gemm_args(gm, [dZ, Wh, dH[-1], M, Hd, kh, LDC, NC, Hd, 0, 1, R.EPI_TANH_GRAD, -1, Hs[-1], Hd, 1, 0,
                                     dcol[-1]] + wcol[-1], bwd_plh),
           label=f"dX_heads", dispatch="gemm", bytes=(M * NC + Hd * NC + 2 * M * Hd) * f4, flops=2.0 * M * Hd * NC,
           bound=mfma)

@@ -88,8 +88,8 @@ enum dgen_hip_kernel {
    *           2^-16 accumulated in fp32 (v_mfma_f32_32x32x16_bf16), as
    *           accurate as fp32 products
    *      [21]=with products 1 only: B planes cell or -1 (op(B) already
-   *           split, [K][N] view, DGEN_HIP_K_SPLIT_BF16); not read with
-   *           products 0 */
+   *           split, [K][N] view, DGEN_HIP_K_SPLIT_BF16; B itself and its
+   *           stride are then not read); not read with products 0 */
   DGEN_HIP_K_GEMM = 3,
 
   /* Head activations of HarmonicDecoderModel (Model.swift:100-114):
@@ -406,7 +406,8 @@ enum dgen_hip_kernel {
    * (p*K8 + k/8)*N + n, K8 = ceil(K/8), zero for k >= K.  Done once for an
    * operand that many GEMM tiles share (the weights, per step).
    * arg: [0]=src [1]=planes cell (3*K8*N*4 floats, 16-byte aligned) [2]=K
-   *      [3]=N [4]=ld_k [5]=ld_n */
+   *      [3]=N [4]=ld_k [5]=ld_n [6]=K8 or 0 (ceil(K/8)): more groups pad
+   *      the planes with zeros, for a GEMM whose K runs past the source's */
   DGEN_HIP_K_SPLIT_BF16 = 39,
 
   /* One generic UOp block (dgen_hip_set_blocks): the kernel the renderer
