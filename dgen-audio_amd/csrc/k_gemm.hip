@@ -425,20 +425,36 @@ __global__ __launch_bounds__(256, BK == 16 ? 4 : 2) void k_gemm(const float* __r
 // Double buffered: 48 KB per workgroup, three workgroups per CU.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two values rounded to bfloat16 as one packed word (v_cvt_pk_bf16_f32),
+// and the rounded values back as fp32: the low half shifted up, the high
+// half masked (one operation each, where converting each rounded value
+// back on its own costs a second conversion and a shift).
+__device__ __forceinline__ unsigned bf16_pair(float a, float b, float& ra, float& rb) {
+  const bf16x2 p = {(__bf16)a, (__bf16)b};
+  unsigned u = __builtin_bit_cast(unsigned, p);
+  // (opaque: else the compiler converts a again on its own for the low half)
+  asm("" : "+v"(u));
+  ra = __builtin_bit_cast(float, u << 16);
+  rb = __builtin_bit_cast(float, u & 0xffff0000u);
+  return u;
+}
+
 __device__ __forceinline__ void split8(const float (&x)[8], uint4& ph, uint4& pm, uint4& pl) {
-  bf16x8 h, m, l;
+  unsigned h[4], m[4], l[4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const __bf16 a = (__bf16)x[i];
-    const float r = x[i] - (float)a;
-    const __bf16 b = (__bf16)r;
-    h[i] = a;
-    m[i] = b;
-    l[i] = (__bf16)(r - (float)b);
+  for (int i = 0; i < 4; ++i) {
+    float a0, a1, b0, b1;
+    h[i] = bf16_pair(x[2 * i], x[2 * i + 1], a0, a1);
+    const float r0 = x[2 * i] - a0, r1 = x[2 * i + 1] - a1;
+    m[i] = bf16_pair(r0, r1, b0, b1);
+    const bf16x2 q = {(__bf16)(r0 - b0), (__bf16)(r1 - b1)};
+    l[i] = __builtin_bit_cast(unsigned, q);
   }
-  ph = __builtin_bit_cast(uint4, h);
-  pm = __builtin_bit_cast(uint4, m);
-  pl = __builtin_bit_cast(uint4, l);
+  ph = make_uint4(h[0], h[1], h[2], h[3]);
+  pm = make_uint4(m[0], m[1], m[2], m[3]);
+  pl = make_uint4(l[0], l[1], l[2], l[3]);
 }
 
 // BPL: B arrives already split (DGEN_HIP_K_SPLIT_BF16 planes in bpl, K8
