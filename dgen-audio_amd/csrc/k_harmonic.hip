@@ -142,10 +142,19 @@ __device__ __forceinline__ bool fast_f0(float f0, float f0lim) {
 __host__ __device__ constexpr int harmonic_groups(int K) { return (K + 63) / 64; }
 inline float fast_f0_limit(int K) { return 0x1p24f / (float)(64 * harmonic_groups(K)); }
 
+// In-kernel timer record of one workgroup (TIMED): shader-clock cycles
+// (s_memtime) the chain wave and the first producer wave spent from their
+// arrival at each interval barrier to its release, summed; the chain's
+// first and last cycle and the matching 100 MHz real-time stamps; and the
+// interval count.
+enum CarryTimer { kTmChainWait, kTmProdWait, kTmCycle0, kTmCycle1, kTmReal0, kTmReal1, kTmIntervals, kTmWords = 8 };
+
 // Grid (B, harmonic groups): workgroup (b, g) runs harmonics 64 g .. 64 g + 63.
+template <bool TIMED>
 __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* __restrict__ f0f,
                                                                    float* __restrict__ ckpt, int B, int K, int T,
-                                                                   float sr, float rsr, float f0lim) {
+                                                                   float sr, float rsr, float f0lim,
+                                                                   unsigned long long* __restrict__ timer) {
   __shared__ __align__(16) float s_inc[kCarryBufs][64 * kIncLd];  // [k][frame]
   __shared__ __align__(16) float s_f0[2][kRing * kSeg];
   __shared__ int s_flag[kCarryBufs * kProducers];  // [buf][producer]: segment needs the literal wrap form
@@ -286,6 +295,13 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
     for (int s = 0; s < kIv && s < nseg; ++s) produce(s);
   lds_barrier();
   if (wave == 0) __builtin_amdgcn_s_setprio(3);
+  // (TIMED: each barrier's stamps are summed at the next barrier, where
+  // its wait has returned them, so the chain never waits for a stamp)
+  unsigned long long tm_wait = 0, tm_b = 0, tm_a = 0, tm_c0 = 0, tm_r0 = 0;
+  if constexpr (TIMED) {
+    tm_c0 = __builtin_amdgcn_s_memtime();
+    tm_r0 = __builtin_amdgcn_s_memrealtime();
+  }
   for (int iv = 0; iv < nint; ++iv) {
     const int s0 = iv * kIv;
     if (wave == 0) {
@@ -392,13 +408,38 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
       }
       if (pending >= 0) commit_block(pending);
     }
-    lds_barrier();
+    if constexpr (TIMED) {
+      const unsigned long long t = __builtin_amdgcn_s_memtime();
+      lds_barrier();
+      tm_wait += tm_a - tm_b;
+      tm_b = t;
+      tm_a = __builtin_amdgcn_s_memtime();
+    } else {
+      lds_barrier();
+    }
+  }
+  if constexpr (TIMED) {
+    tm_wait += tm_a - tm_b;
+    const unsigned long long c1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+    unsigned long long* rec = timer + ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * kTmWords;
+    if (wave == 0 && lane == 0) {
+      rec[kTmChainWait] = tm_wait;
+      rec[kTmCycle0] = tm_c0;
+      rec[kTmCycle1] = c1;
+      rec[kTmReal0] = tm_r0;
+      rec[kTmReal1] = r1;
+      rec[kTmIntervals] = (unsigned long long)nint;
+      rec[kTmIntervals + 1] = 0;
+    }
+    if (wave == 1 && lane == 0) rec[kTmProdWait] = tm_wait;
   }
 }
 
 int launch_phasor_carry(const Launch& L, const dgen_hip_op& op) {
-  // arg: [0]=f0f ([B][T]) [1]=checkpoints ([nseg][B][K]) [2]=B [3]=K [4]=T   farg: [0]=sr
+  // arg: [0]=f0f ([B][T]) [1]=checkpoints ([nseg][B][K]) [2]=B [3]=K [4]=T
+  //      [5]=timer cell ([G][B][8] uint64, read only if [6] == 1) [6]=timed   farg: [0]=sr
   const int64_t f0f = op.arg[0], ck = op.arg[1], B = op.arg[2], K = op.arg[3], T = op.arg[4];
+  const bool timed = op.arg[6] == 1;
   DGEN_REQUIRE(B > 0 && B <= 65535 && K > 0 && K <= kMaxKWide && T > 0 && T <= (1 << 26),
                "phasor_carry: B %lld K %lld T %lld", (long long)B, (long long)K, (long long)T);
   DGEN_REQUIRE(op.farg[0] > 0.f && op.farg[0] < 1e30f, "phasor_carry: sample rate %g", (double)op.farg[0]);
@@ -406,11 +447,19 @@ int launch_phasor_carry(const Launch& L, const dgen_hip_op& op) {
   DGEN_CHECK_CELL(L, f0f, B * T, "phasor_carry.f0_frames");
   DGEN_CHECK_CELL(L, ck, nseg * B * K, "phasor_carry.checkpoints");
   DGEN_REQUIRE(nseg * B * K < (1ll << 29), "phasor_carry: %lld checkpoints (< 2^29)", (long long)(nseg * B * K));
+  DGEN_REQUIRE(op.arg[6] == 0 || op.arg[6] == 1, "phasor_carry: timed flag %lld", (long long)op.arg[6]);
+  const int64_t G = harmonic_groups((int)K);
+  if (timed) DGEN_CHECK_CELL(L, op.arg[5], 2 * kTmWords * G * B, "phasor_carry.timer");
   if (L.dry) return 0;
   const float sr = host_rate(L, op.farg[0]), rsr = 1.0f / sr;
-  hipLaunchKernelGGL(k_phasor_carry, dim3((unsigned)B, (unsigned)harmonic_groups((int)K)), dim3(64 * kCarryWaves), 0,
-                     L.stream, cell(L, f0f), cell(L, ck), (int)B, (int)K, (int)T, sr, rsr,
-                     fast_f0_limit((int)K));
+  const dim3 grid((unsigned)B, (unsigned)G);
+  if (timed)
+    hipLaunchKernelGGL(k_phasor_carry<true>, grid, dim3(64 * kCarryWaves), 0, L.stream, cell(L, f0f), cell(L, ck),
+                       (int)B, (int)K, (int)T, sr, rsr, fast_f0_limit((int)K),
+                       reinterpret_cast<unsigned long long*>(cell(L, op.arg[5])));
+  else
+    hipLaunchKernelGGL(k_phasor_carry<false>, grid, dim3(64 * kCarryWaves), 0, L.stream, cell(L, f0f), cell(L, ck),
+                       (int)B, (int)K, (int)T, sr, rsr, fast_f0_limit((int)K), nullptr);
   DGEN_LAUNCH_CHECK("k_phasor_carry");
   return 0;
 }

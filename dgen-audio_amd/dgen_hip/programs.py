@@ -101,7 +101,7 @@ def stream_oscbank_program(cfg: OscBankConfig, stateful: bool = True, max_frames
 
 # ------------------------------------------------------------------ config 3
 def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = True,
-                     side_stream: bool = True) -> Program:
+                     side_stream: bool = True, chain_timer: bool = False) -> Program:
     """Batched harmonic + noise synth with MLP decoder and MSS loss.
 
     ``train=False`` builds the forward render only (controls -> audio), used
@@ -109,7 +109,9 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     backward to every parameter and (``optimizer``) one Adam step.  With
     ``side_stream`` the phase-carry chain (which depends only on f0) runs on a
     second stream, overlapping the control-network forward, and the weight
-    and bias gradients of the backward overlap its data-gradient chain."""
+    and bias gradients of the backward overlap its data-gradient chain.
+    ``chain_timer`` runs the phase chain's timed build, which fills the cell
+    ``chain_timer`` ([G][B][8] uint64 records; see ``chain_timer.py``)."""
     SIDE = R.OP_SIDE if side_stream else 0
     JOIN = R.OP_JOIN if side_stream else 0
     FORK = R.OP_FORK if side_stream else 0
@@ -182,7 +184,8 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     frames_b = lerp_b + F * B * f4 + B * T * f4
     p.add(R.K_LERP_FRAMES, [f0, lerp, f0f, B, F, T], flags=SIDE, label="f0_frames",
           dispatch=f"perFrameScaled({B})", bytes=frames_b, flops=3.0 * B * T)
-    p.add(R.K_PHASOR_CARRY, [f0f, ck, B, K, T], [cfg.sr], flags=SIDE, label="phasor_carry",
+    tm = p.alloc("chain_timer", 16 * B * ((K + 63) // 64)) if chain_timer else 0
+    p.add(R.K_PHASOR_CARRY, [f0f, ck, B, K, T, tm, int(chain_timer)], [cfg.sr], flags=SIDE, label="phasor_carry",
           dispatch=f"fixedWithFrameLoop({B * K})", bytes=B * T * f4 + ck_b, flops=6.0 * B * K * T, bound="valu")
     p.add(R.K_LERP_FRAMES, [uv, lerp, uvf, B, F, T], label="uv_frames", dispatch=f"perFrameScaled({B})",
           bytes=frames_b, flops=3.0 * B * T)
@@ -382,7 +385,7 @@ class HarmonicSession:
     forward+backward(+Adam) pass with all data resident in HBM."""
 
     def __init__(self, cfg: HarmonicConfig, device: int = 0, optimizer: bool = True, target=None,
-                 side_stream: bool = True, data=None):
+                 side_stream: bool = True, data=None, chain_timer: bool = False):
         self.cfg = cfg
         f0, uv, X = cfg.data() if data is None else data
         self.f0, self.uv, self.X = f0, uv, X
@@ -390,7 +393,8 @@ class HarmonicSession:
         if target is None:
             target = self.render(cfg.weights(seed=cfg.target_seed), device)
         self.target = np.ascontiguousarray(target, np.float32).reshape(cfg.B, cfg.T)
-        self.program = harmonic_program(cfg, train=True, optimizer=optimizer, side_stream=side_stream)
+        self.program = harmonic_program(cfg, train=True, optimizer=optimizer, side_stream=side_stream,
+                                        chain_timer=chain_timer)
         self.rt = R.HIPLazyRuntime(self.program, device)
         check_row_schedule(self.rt)
         self.rt.write("X", X)

@@ -103,6 +103,13 @@ enum dgen_hip_kernel {
    * start of every 64-frame segment.
    * arg: [0]=f0 frames cell ([B][T], from DGEN_HIP_K_LERP_FRAMES)
    *      [1]=checkpoints cell ([nseg][B][K]) [2]=B [3]=K (<= 256) [4]=T
+   *      [5]=timer cell, read only if [6] == 1 [6]=1: the timed build,
+   *      which writes per workgroup (g, b) at [(g*B + b)*8] eight uint64:
+   *      the chain wave's and the first producer wave's summed barrier
+   *      waits (shader-clock cycles), the chain's first and last cycle
+   *      stamps, the matching 100 MHz real-time stamps, the interval count
+   *      and 0 (0 leaves it out: the timer has no counterpart in the
+   *      reference; it measures the chain)
    * farg: [0]=sample rate */
   DGEN_HIP_K_PHASOR_CARRY = 5,
 
