@@ -157,8 +157,7 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
                                                                    unsigned long long* __restrict__ timer) {
   __shared__ __align__(16) float s_inc[kCarryBufs][64 * kIncLd];  // [k][frame]
   __shared__ __align__(16) float s_f0[2][kRing * kSeg];
-  __shared__ int s_flag[kCarryBufs * kProducers];  // [buf][producer]: segment needs the literal wrap form
-  __shared__ int s_blkbad[2][kProducers];           // f0 block holds a value outside the fast range
+  __shared__ __align__(16) int s_blkbad[2][kProducers];  // f0 block holds a value outside the fast range
   const int b = blockIdx.x, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int k0 = 64 * (int)blockIdx.y;  // first harmonic of the group
   const int nseg = (T + kSeg - 1) / kSeg;
@@ -233,7 +232,6 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
     float4* dst = reinterpret_cast<float4*>(&s_inc[buf][lane * kIncLd + i0]);
 #pragma unroll
     for (int q = 0; q < kGroups; ++q) dst[q] = make_float4(inc[4 * q], inc[4 * q + 1], inc[4 * q + 2], inc[4 * q + 3]);
-    s_flag[buf * kProducers + wave - 1] = fast ? 0 : 1;  // every lane stores the same value: no branch
   };
   // chain: v[32h .. 32h+31] <- half h of segment s's increments
   auto fetch_half = [&](int s, float* v, int h) {
@@ -294,7 +292,6 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
   if (wave > 0)
     for (int s = 0; s < kIv && s < nseg; ++s) produce(s);
   lds_barrier();
-  if (wave == 0) __builtin_amdgcn_s_setprio(3);
   // (TIMED: each barrier's stamps are summed at the next barrier, where
   // its wait has returned them, so the chain never waits for a stamp)
   unsigned long long tm_wait = 0, tm_b = 0, tm_a = 0, tm_c0 = 0, tm_r0 = 0;
@@ -302,31 +299,43 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
     tm_c0 = __builtin_amdgcn_s_memtime();
     tm_r0 = __builtin_amdgcn_s_memrealtime();
   }
-  for (int iv = 0; iv < nint; ++iv) {
-    const int s0 = iv * kIv;
-    if (wave == 0) {
-      float va[kSeg], vb[kSeg];
-      // the interval's flags and its first segment's increments, one LDS
-      // round trip: the interval's buffers are consecutive in the ring, so
-      // lane q * kProducers + p reads producer p's flag for segment s0 + q
-      // and one ballot gathers them; a segment past the end or shorter than
-      // kSeg also takes the wrap form
-      static_assert(kCarryBufs % kIv == 0 && kIv * kProducers <= 64, "interval flags in one read");
-      const int fv = lane < kIv * kProducers ? s_flag[(s0 % kCarryBufs) * kProducers + lane] : 0;
-      fetch_half(s0, va, 0);
-      fetch_half(s0, va, 1);
-      const unsigned long long fm = __ballot(fv != 0);
-      int fl[kIv];
-#pragma unroll
-      for (int q = 0; q < kIv; ++q)
-        fl[q] = ((fm >> (q * kProducers)) & ((1ull << kProducers) - 1)) != 0 || (T - (s0 + q) * kSeg) < kSeg;
-      bool straight = true;
-#pragma unroll
-      for (int q = 0; q < kIv; ++q) straight = straight && !fl[q];
-      if (straight) {
-        // every segment full-length and in the fast form: one run of
-        // kIv * kSeg steps without a branch (a taken branch stalls the lone
-        // chain wave for its instruction refetch)
+  auto interval_barrier = [&]() {
+    if constexpr (TIMED) {
+      const unsigned long long t = __builtin_amdgcn_s_memtime();
+      lds_barrier();
+      tm_wait += tm_a - tm_b;
+      tm_b = t;
+      tm_a = __builtin_amdgcn_s_memtime();
+    } else {
+      lds_barrier();
+    }
+  };
+  // The chain and the producers run loops of their own with the same
+  // barriers (in one loop the compiler reconciles the two roles' registers
+  // with copies on the chain's path at every interval).
+  if (wave == 0) {
+    __builtin_amdgcn_s_setprio(3);
+    // The fast-step vote of the f0 block an interval lies in (an interval
+    // never spans two blocks): committed by the producers at least four
+    // intervals before the chain reads it, and overwritten (by block + 2)
+    // only after the chain has passed that block's last interval.
+    static_assert(kRing % kIv == 0, "an interval lies in one f0 block");
+    static_assert(kProducers == 4, "one 16-byte read of the block's votes");
+    auto block_votes = [&](int s0) { return *reinterpret_cast<const int4*>(s_blkbad[(s0 / kRing) & 1]); };
+    auto any_vote = [](int4 v) { return v.x | v.y | v.z | v.w; };
+    int nbad = any_vote(block_votes(0));  // the next interval's vote, read an interval ahead
+    int iv = 0;
+    while (iv < nint) {
+      // Intervals whose segments are all full-length in the fast form, in
+      // a loop of their own: the steps, the next interval's vote and the
+      // barrier, without a branch over the general form or a per-lane flag
+      // vote (each cost the chain hundreds of cycles an interval).
+      for (;;) {
+        const int s0 = iv * kIv;
+        if (__builtin_amdgcn_readfirstlane(nbad) != 0 || (s0 + kIv) * kSeg > T) break;
+        float va[kSeg], vb[kSeg];
+        fetch_half(s0, va, 0);
+        fetch_half(s0, va, 1);
         // Three rotating half-segment buffers X, Y, Z: each half steps
         // while the half two ahead loads into the buffer the previous half
         // freed (the empty asm statements keep every load at its place).
@@ -356,40 +365,61 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
         store_ckpt(s0);
         ld(s0 + 1, 0, Z); st(X); ld(s0 + 1, 1, X); st(Y);
         store_ckpt(s0 + 1);
+        // (read here, combined after the run: its wait then costs nothing)
+        const int4 votes = block_votes(s0 + kIv);
         ld(s0 + 2, 0, Y); st(Z); ld(s0 + 2, 1, Z); st(X);
         store_ckpt(s0 + 2);
         ld(s0 + 3, 0, X); st(Y); ld(s0 + 3, 1, Y); st(Z);
         store_ckpt(s0 + 3);
         st(X); st(Y);
-      } else {
-      // (loaded again: the run's registers stay its own)
-      fetch_half(s0, va, 0);
-      fetch_half(s0, va, 1);
-      int fa = fl[0], fb = 0;
+        nbad = any_vote(votes);
+        interval_barrier();
+        if (++iv >= nint) break;
+      }
+      if (iv >= nint) break;
+      {
+        // one interval in the general form: a segment of a block with an
+        // f0 outside the fast range, past the end or shorter than kSeg
+        // takes the literal wrap form
+        const int s0 = iv * kIv;
+        const int bad = __builtin_amdgcn_readfirstlane(nbad);
+        int fl[kIv];
 #pragma unroll
-      for (int q = 0; q < kIv; ++q) {
-        const int s = s0 + q;
-        if (s >= nseg) break;
-        // the next segment's increments are loaded while this one steps
-        const bool more = q + 1 < kIv && s + 1 < nseg;
-        if (q % 2 == 0) {
-          if (more) {
-            fb = fl[q + 1];
-            step_seg(s, va, fa, vb, std::true_type{});
+        for (int q = 0; q < kIv; ++q) fl[q] = bad != 0 || (T - (s0 + q) * kSeg) < kSeg;
+        float va[kSeg], vb[kSeg];
+        fetch_half(s0, va, 0);
+        fetch_half(s0, va, 1);
+        int fa = fl[0], fb = 0;
+#pragma unroll
+        for (int q = 0; q < kIv; ++q) {
+          const int s = s0 + q;
+          if (s >= nseg) break;
+          // the next segment's increments are loaded while this one steps
+          const bool more = q + 1 < kIv && s + 1 < nseg;
+          if (q % 2 == 0) {
+            if (more) {
+              fb = fl[q + 1];
+              step_seg(s, va, fa, vb, std::true_type{});
+            } else {
+              step_seg(s, va, fa, vb, std::false_type{});
+            }
           } else {
-            step_seg(s, va, fa, vb, std::false_type{});
-          }
-        } else {
-          if (more) {
-            fa = fl[q + 1];
-            step_seg(s, vb, fb, va, std::true_type{});
-          } else {
-            step_seg(s, vb, fb, va, std::false_type{});
+            if (more) {
+              fa = fl[q + 1];
+              step_seg(s, vb, fb, va, std::true_type{});
+            } else {
+              step_seg(s, vb, fb, va, std::false_type{});
+            }
           }
         }
+        nbad = any_vote(block_votes(s0 + kIv));
+        interval_barrier();
+        ++iv;
       }
-      }
-    } else {
+    }
+  } else {
+    for (int iv = 0; iv < nint; ++iv) {
+      const int s0 = iv * kIv;
       // f0 block s/16 + 1 (s the interval's segment at a block boundary)
       // goes into the half whose segments are all produced; its loads are
       // issued before the interval's produce work and committed after it
@@ -407,15 +437,7 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
         for (int s = next; s < nseg; ++s) produce(s);
       }
       if (pending >= 0) commit_block(pending);
-    }
-    if constexpr (TIMED) {
-      const unsigned long long t = __builtin_amdgcn_s_memtime();
-      lds_barrier();
-      tm_wait += tm_a - tm_b;
-      tm_b = t;
-      tm_a = __builtin_amdgcn_s_memtime();
-    } else {
-      lds_barrier();
+      interval_barrier();
     }
   }
   if constexpr (TIMED) {
