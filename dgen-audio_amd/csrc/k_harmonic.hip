@@ -107,29 +107,36 @@ int launch_lerp_frames(const Launch& L, const dgen_hip_op& op) {
 // (lane = k); at 2 dependent VALU ops per step its 64-step segment costs
 // ~128 issue slots, so everything else is kept off its path:
 // - waves 1..kProducers compute increments into a ring of kCarryBufs
-//   segment buffers, kIv segments per barrier interval, one interval ahead
-//   of the chain; producer p owns frames 16p .. 16p+15 of a segment, lane = k
-//   (four producers: with three, one per SIMD, each producer's division
-//   work and LDS writes took longer than the chain's segment and the chain
-//   waited at every barrier; a fourth shares the chain's SIMD at lower
-//   priority);
+//   segment buffers, kIv segments per barrier interval, kIv + 1 segments
+//   ahead of the chain, so the chain reads the next interval's first
+//   segment before the barrier that ends its interval and steps on from
+//   registers after it; producer p owns float4 frame groups
+//   kSplit[p] .. kSplit[p+1]-1 of every segment, lane = k;
+// - a producer's time goes to the latency of its LDS reads and increment
+//   chains, not to issue: measured against the chain, four producers of
+//   four groups each had ~12% slack, five groups left none and six made
+//   the producer the bound; seven producers (two or three groups, two
+//   waves on most SIMDs, overlapping each other's latency) give the chain
+//   the most room (331 against 339 us alone for four);
 // - increments are stored k-major ([k][frame], stride 68 floats), so the
 //   chain reads a lane's 64 increments with 16 ds_read_b128 and producers
 //   write them with ds_write_b128, both bank-conflict free;
-// - f0 is staged from global memory 16 segments at a time into a
-//   double-buffered LDS ring, so load latency is paid once per 16 segments;
+// - f0 is staged from global memory kRing segments at a time into a
+//   double-buffered LDS ring, a block's loads issued an interval before
+//   they are committed, so load latency is paid once per block and hidden;
 //   the fast-step test (every f0 of the block in the exact range) is voted
-//   once per block while loading it;
+//   once per block while committing it;
 // - the chain wave reads segment s+1's increments into registers while it
 //   steps segment s, and has issue priority on its SIMD.
-constexpr int kProducers = 4;
+constexpr int kProducers = 7;
 constexpr int kCarryWaves = 1 + kProducers;
-constexpr int kGroups = kSeg / 4 / kProducers;  // float4 frame groups per producer
-static_assert(kGroups * kProducers * 4 == kSeg, "producers split a segment evenly");
-constexpr int kFrames = 4 * kGroups;
+// A segment's 16 float4 frame groups over the producers
+constexpr int kSplit[kProducers + 1] = {0, 2, 4, 6, 8, 10, 13, 16};
+static_assert(kSplit[kProducers] * 4 == kSeg, "the producers cover a segment");
 constexpr int kIv = 4;                  // segments per barrier interval
-constexpr int kCarryBufs = 2 * kIv;     // increment ring
-constexpr int kRing = 16;               // segments per f0 block
+constexpr int kAhead = kIv + 1;         // producers write segments s0 + kAhead .. s0 + kAhead + kIv - 1
+constexpr int kCarryBufs = kIv + kAhead;  // increment ring: the chain's interval and its next segment, the producers'
+constexpr int kRing = 3 * kIv;          // segments per f0 block
 constexpr int kIncLd = kSeg + 4;        // k-major row stride (floats)
 
 // f0lim = 2^24 / (64 G) for G harmonic groups (2^18 for one): every
@@ -149,6 +156,20 @@ inline float fast_f0_limit(int K) { return 0x1p24f / (float)(64 * harmonic_group
 // interval count.
 enum CarryTimer { kTmChainWait, kTmProdWait, kTmCycle0, kTmCycle1, kTmReal0, kTmReal1, kTmIntervals, kTmWords = 8 };
 
+__device__ __forceinline__ int4 votes8(const int* p) {
+  const int4 a = reinterpret_cast<const int4*>(p)[0], b = reinterpret_cast<const int4*>(p)[1];
+  return make_int4(a.x | b.x, a.y | b.y, a.z | b.z, a.w | b.w);
+}
+template <int P, class F>
+__device__ __forceinline__ void dispatch_producer(int wave, F& body) {
+  if constexpr (P < kProducers) {
+    if (wave == P + 1)
+      body(std::integral_constant<int, kSplit[P]>{}, std::integral_constant<int, kSplit[P + 1] - kSplit[P]>{});
+    else
+      dispatch_producer<P + 1>(wave, body);
+  }
+}
+
 // Grid (B, harmonic groups): workgroup (b, g) runs harmonics 64 g .. 64 g + 63.
 template <bool TIMED>
 __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* __restrict__ f0f,
@@ -157,10 +178,11 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
                                                                    unsigned long long* __restrict__ timer) {
   __shared__ __align__(16) float s_inc[kCarryBufs][64 * kIncLd];  // [k][frame]
   __shared__ __align__(16) float s_f0[2][kRing * kSeg];
-  __shared__ __align__(16) int s_blkbad[2][kProducers];  // f0 block holds a value outside the fast range
+  __shared__ __align__(16) int s_blkbad[2][8];  // f0 block holds a value outside the fast range
   const int b = blockIdx.x, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int k0 = 64 * (int)blockIdx.y;  // first harmonic of the group
   const int nseg = (T + kSeg - 1) / kSeg;
+  const int nblk = (nseg + kRing - 1) / kRing;
   const float* f0b = f0f + (size_t)b * T;
   const int ptid = threadIdx.x - 64;  // producer thread index
   // An f0 block is loaded in two parts: issue (every load of the thread in
@@ -197,41 +219,62 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
     issue_block(blk);
     commit_block(blk);
   };
-  auto produce = [&](int s) {
-    const int buf = s % kCarryBufs;
-    // producer p owns frames [4 kGroups p, 4 kGroups (p + 1)) of the segment
-    const int i0 = (wave - 1) * kFrames;
-    const float4* f4 = reinterpret_cast<const float4*>(&s_f0[(s / kRing) & 1][(s % kRing) * kSeg + i0]);
-    float f[kFrames];
-#pragma unroll
-    for (int q = 0; q < kGroups; ++q) {
-      const float4 v = f4[q];
-      f[4 * q] = v.x;
-      f[4 * q + 1] = v.y;
-      f[4 * q + 2] = v.z;
-      f[4 * q + 3] = v.w;
-    }
+  auto inc_fast = [&](float x) {
+    const float q0 = x * rsr;
+    return fmaf(fmaf(-q0, sr, x), rsr, q0);
+  };
+  // one producer's float4 frame groups [G0, G0 + NG) of segment s
+  auto produce = [&](int s, auto g0c, auto ngc) __attribute__((always_inline)) {
+    constexpr int G0 = decltype(g0c)::value, NG = decltype(ngc)::value;
+    const int par = (s / kRing) & 1;
+    const float4* f4 = reinterpret_cast<const float4*>(&s_f0[par][(s % kRing) * kSeg]) + G0;
+    const int4 v = votes8(s_blkbad[par]);
+    const bool fast = (v.x | v.y | v.z | v.w) == 0;
     const float kf = (float)(k0 + lane + 1);
-    const int* bb = s_blkbad[(s / kRing) & 1];
-    int blkbad = 0;
+    float4* dst = reinterpret_cast<float4*>(&s_inc[s % kCarryBufs][lane * kIncLd]) + G0;
+    if (fast) {
 #pragma unroll
-    for (int w = 0; w < kProducers; ++w) blkbad |= bb[w];
-    const bool fast = !blkbad;
-    float inc[kFrames];
-    if (__builtin_expect(fast, 1)) {
-#pragma unroll
-      for (int j = 0; j < kFrames; ++j) {
-        const float x = kf * f[j];
-        const float q0 = x * rsr;
-        inc[j] = fmaf(fmaf(-q0, sr, x), rsr, q0);
+      for (int g = 0; g < NG; ++g) {
+        const float4 f = f4[g];
+        dst[g] = make_float4(inc_fast(kf * f.x), inc_fast(kf * f.y), inc_fast(kf * f.z), inc_fast(kf * f.w));
       }
     } else {
-#pragma unroll
-      for (int j = 0; j < kFrames; ++j) inc[j] = div_sr(kf * f[j], sr, rsr);
+      for (int g = 0; g < NG; ++g) {
+        const float4 f = f4[g];
+        dst[g] = make_float4(div_sr(kf * f.x, sr, rsr), div_sr(kf * f.y, sr, rsr), div_sr(kf * f.z, sr, rsr),
+                             div_sr(kf * f.w, sr, rsr));
+      }
     }
-    float4* dst = reinterpret_cast<float4*>(&s_inc[buf][lane * kIncLd + i0]);
+  };
+  // the kIv segments next .. next + kIv - 1 (all before the end): every
+  // LDS read first (the interval's f0 values and block votes), then the
+  // increments, so the producer pays one LDS round trip per interval
+  auto produce_interval = [&](int next, auto g0c, auto ngc) __attribute__((always_inline)) {
+    constexpr int G0 = decltype(g0c)::value, NG = decltype(ngc)::value;
+    float4 f[kIv][NG > 0 ? NG : 1];
+    int anybad = 0;
 #pragma unroll
-    for (int q = 0; q < kGroups; ++q) dst[q] = make_float4(inc[4 * q], inc[4 * q + 1], inc[4 * q + 2], inc[4 * q + 3]);
+    for (int q = 0; q < kIv; ++q) {
+      const int sq = next + q, par = (sq / kRing) & 1;
+      const float4* f4 = reinterpret_cast<const float4*>(&s_f0[par][(sq % kRing) * kSeg]) + G0;
+#pragma unroll
+      for (int g = 0; g < NG; ++g) f[q][g] = f4[g];
+      const int4 v = votes8(s_blkbad[par]);
+      anybad |= v.x | v.y | v.z | v.w;
+    }
+    const float kf = (float)(k0 + lane + 1);
+    if (__builtin_expect(!anybad, 1)) {
+#pragma unroll
+      for (int q = 0; q < kIv; ++q) {
+        float4* dst = reinterpret_cast<float4*>(&s_inc[(next + q) % kCarryBufs][lane * kIncLd]) + G0;
+#pragma unroll
+        for (int g = 0; g < NG; ++g)
+          dst[g] = make_float4(inc_fast(kf * f[q][g].x), inc_fast(kf * f[q][g].y), inc_fast(kf * f[q][g].z),
+                               inc_fast(kf * f[q][g].w));
+      }
+    } else {
+      for (int q = 0; q < kIv; ++q) produce(next + q, g0c, ngc);
+    }
   };
   // chain: v[32h .. 32h+31] <- half h of segment s's increments
   auto fetch_half = [&](int s, float* v, int h) {
@@ -284,13 +327,20 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
   };
 
   const int nint = (nseg + kIv - 1) / kIv;
+  if (threadIdx.x < 16) s_blkbad[0][threadIdx.x] = 0;
+  lds_barrier();
   if (wave > 0) {
     load_block(0);
     load_block(1);
   }
   lds_barrier();
+  // producer p's frame groups, as constants of its code
+  auto as_producer = [&](auto body) __attribute__((always_inline)) { dispatch_producer<0>(wave, body); };
+
   if (wave > 0)
-    for (int s = 0; s < kIv && s < nseg; ++s) produce(s);
+    as_producer([&](auto g0c, auto ngc) __attribute__((always_inline)) {
+      for (int s = 0; s < kAhead && s < nseg; ++s) produce(s, g0c, ngc);
+    });
   lds_barrier();
   // (TIMED: each barrier's stamps are summed at the next barrier, where
   // its wait has returned them, so the chain never waits for a stamp)
@@ -320,10 +370,14 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
     // intervals before the chain reads it, and overwritten (by block + 2)
     // only after the chain has passed that block's last interval.
     static_assert(kRing % kIv == 0, "an interval lies in one f0 block");
-    static_assert(kProducers == 4, "one 16-byte read of the block's votes");
-    auto block_votes = [&](int s0) { return *reinterpret_cast<const int4*>(s_blkbad[(s0 / kRing) & 1]); };
+    auto block_votes = [&](int s0) { return votes8(s_blkbad[(s0 / kRing) & 1]); };
     auto any_vote = [](int4 v) { return v.x | v.y | v.z | v.w; };
     int nbad = any_vote(block_votes(0));  // the next interval's vote, read an interval ahead
+    // va holds the interval's first segment on entry (read before the
+    // barrier that ends the previous interval)
+    float va[kSeg], vb[kSeg];
+    fetch_half(0, va, 0);
+    fetch_half(0, va, 1);
     int iv = 0;
     while (iv < nint) {
       // Intervals whose segments are all full-length in the fast form, in
@@ -333,16 +387,16 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
       for (;;) {
         const int s0 = iv * kIv;
         if (__builtin_amdgcn_readfirstlane(nbad) != 0 || (s0 + kIv) * kSeg > T) break;
-        float va[kSeg], vb[kSeg];
-        fetch_half(s0, va, 0);
-        fetch_half(s0, va, 1);
-        // Three rotating half-segment buffers X, Y, Z: each half steps
-        // while the half two ahead loads into the buffer the previous half
-        // freed (the empty asm statements keep every load at its place).
+        // Four rotating half-segment buffers A, B, C, D: each half steps
+        // while the half two ahead loads into the buffer the half before
+        // freed, ending with the next interval's first segment in A, B
+        // (the empty asm statements keep every load at its place).  Past
+        // the last interval that read lands in the ring, in bounds, unused.
         static_assert(kIv == 4, "the run below covers four segments");
-        float* X = va;
-        float* Y = va + kSeg / 2;
-        float* Z = vb;
+        float* A = va;
+        float* B = va + kSeg / 2;
+        float* C = vb;
+        float* D = vb + kSeg / 2;
         auto ld = [&](int s, int h, float* d) {
           asm volatile("" ::: "memory");
           const float4* src = reinterpret_cast<const float4*>(&s_inc[s % kCarryBufs][lane * kIncLd]) + 8 * h;
@@ -363,15 +417,15 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
           __builtin_amdgcn_sched_barrier(0);
         };
         store_ckpt(s0);
-        ld(s0 + 1, 0, Z); st(X); ld(s0 + 1, 1, X); st(Y);
+        ld(s0 + 1, 0, C); st(A); ld(s0 + 1, 1, D); st(B);
         store_ckpt(s0 + 1);
         // (read here, combined after the run: its wait then costs nothing)
         const int4 votes = block_votes(s0 + kIv);
-        ld(s0 + 2, 0, Y); st(Z); ld(s0 + 2, 1, Z); st(X);
+        ld(s0 + 2, 0, A); st(C); ld(s0 + 2, 1, B); st(D);
         store_ckpt(s0 + 2);
-        ld(s0 + 3, 0, X); st(Y); ld(s0 + 3, 1, Y); st(Z);
+        ld(s0 + 3, 0, C); st(A); ld(s0 + 3, 1, D); st(B);
         store_ckpt(s0 + 3);
-        st(X); st(Y);
+        ld(s0 + kIv, 0, A); st(C); ld(s0 + kIv, 1, B); st(D);
         nbad = any_vote(votes);
         interval_barrier();
         if (++iv >= nint) break;
@@ -386,9 +440,6 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
         int fl[kIv];
 #pragma unroll
         for (int q = 0; q < kIv; ++q) fl[q] = bad != 0 || (T - (s0 + q) * kSeg) < kSeg;
-        float va[kSeg], vb[kSeg];
-        fetch_half(s0, va, 0);
-        fetch_half(s0, va, 1);
         int fa = fl[0], fb = 0;
 #pragma unroll
         for (int q = 0; q < kIv; ++q) {
@@ -413,32 +464,34 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
           }
         }
         nbad = any_vote(block_votes(s0 + kIv));
+        fetch_half(s0 + kIv, va, 0);
+        fetch_half(s0 + kIv, va, 1);
         interval_barrier();
         ++iv;
       }
     }
   } else {
-    for (int iv = 0; iv < nint; ++iv) {
-      const int s0 = iv * kIv;
-      // f0 block s/16 + 1 (s the interval's segment at a block boundary)
-      // goes into the half whose segments are all produced; its loads are
-      // issued before the interval's produce work and committed after it
-      // (it is first read 16 segments later)
-      const int next = s0 + kIv;
-      // at most one block boundary falls in an interval (kIv <= kRing)
-      static_assert(kIv <= kRing, "one f0 block boundary per interval");
-      const int sb = (next + kRing - 1) / kRing * kRing;
-      const int pending = sb < next + kIv && sb < nseg ? sb / kRing + 1 : -1;
-      if (pending >= 0) issue_block(pending);
-      if (__builtin_expect(next + kIv <= nseg, 1)) {
-#pragma unroll
-        for (int q = 0; q < kIv; ++q) produce(next + q);
-      } else {
-        for (int s = next; s < nseg; ++s) produce(s);
+    // Interval iv produces segments 4 iv + 5 .. 4 iv + 8, so f0 block j
+    // (segments 12 j .. 12 j + 11) is read in intervals 3 j - 2 .. 3 j + 1.
+    // Block m replaces block m - 2 in its buffer: its loads are issued in
+    // interval 3 m - 5 and committed in 3 m - 4, after block m - 2's last
+    // reader and three intervals before block m's first (blocks 0 and 1
+    // are loaded before the loop); the chain reads a block's vote from
+    // interval 3 m - 1 to 3 m + 1.
+    static_assert(kAhead == 5 && kRing == 12 && kIv == 4, "the block schedule below");
+    as_producer([&](auto g0c, auto ngc) __attribute__((always_inline)) {
+      for (int iv = 0; iv < nint; ++iv) {
+        const int next = iv * kIv + kAhead;
+        if ((iv + 5) % 3 == 0 && (iv + 5) / 3 < nblk) issue_block((iv + 5) / 3);
+        if (__builtin_expect(next + kIv <= nseg, 1)) {
+          produce_interval(next, g0c, ngc);
+        } else {
+          for (int s = next; s < nseg; ++s) produce(s, g0c, ngc);
+        }
+        if ((iv + 4) % 3 == 0 && (iv + 4) / 3 < nblk) commit_block((iv + 4) / 3);
+        interval_barrier();
       }
-      if (pending >= 0) commit_block(pending);
-      interval_barrier();
-    }
+    });
   }
   if constexpr (TIMED) {
     tm_wait += tm_a - tm_b;

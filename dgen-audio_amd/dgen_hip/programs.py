@@ -207,11 +207,7 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
         for l in range(1, Lyr):
             W, _b = woff[l]
             fwd_pl[l] = _split_planes(p, f"W{l + 1}_planes", W, Hd, Hd, Hd, 1)
-            if train:
-                bwd_pl[l] = _split_planes(p, f"W{l + 1}T_planes", W, Hd, Hd, 1, Hd)
         fwd_plh = _split_planes(p, "Wh_planes", Wh, Hd, NC, NC, 1)
-        if train:
-            bwd_plh = _split_planes(p, "WhT_planes", Wh, NC, Hd, 1, NC, k_pad=kh)
     for l in range(1, Lyr):
         W, b = woff[l]
         p.add(R.K_GEMM, _gemm_args(gm, [Hs[l - 1], W, Hs[l], M, Hd, Hd, Hd, Hd, Hd, 0, 0, R.EPI_BIAS_TANH, b, -1, 0, 1,
@@ -223,6 +219,13 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
           dispatch="gemm", bytes=(M * Hd + Hd * NC + NC + M * NC) * f4, flops=2.0 * M * Hd * NC, bound=mfma)
     p.add(R.K_HEADS_FWD, [Z, ctrl, M, K, NF, LDC], label="heads", dispatch=f"perFrameScaled({M})",
           bytes=2 * M * NC * f4, flops=M * (K * 12.0 + NF * 8.0))
+    if gm == 1 and train:
+        # the data gradients' W^T planes: after the control network, where
+        # stream 0 waits for the phase chain, not before the forward GEMMs
+        for l in range(1, Lyr):
+            W, _b = woff[l]
+            bwd_pl[l] = _split_planes(p, f"W{l + 1}T_planes", W, Hd, Hd, 1, Hd)
+        bwd_plh = _split_planes(p, "WhT_planes", Wh, NC, Hd, 1, NC, k_pad=kh)
     aux = p.alloc("synth_tape", 3 * B * T) if train else -1
     synth_args = [ctrl, f0f, uvf, lerp, ck, y, B, K, NF, F, T, SEG, aux, noise, LDC, segrows]
     hs, ns = cfg.hscale, cfg.nscale
