@@ -298,9 +298,9 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
                                                          (int)(4u * (unsigned)((nseg - 1) * B * K + K - k0)),
                                                          0x00020000);
   const unsigned ck_voff = k0 + lane < K ? 4u * (unsigned)lane : 0x80000000u;
+  const int ck_stride = 4 * B * K;  // bytes per segment of checkpoints
   auto store_ckpt = [&](int s) {
-    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, ph), ck_rsrc, ck_voff,
-                                          (int)(4u * (unsigned)(s * B * K)), 0);
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, ph), ck_rsrc, ck_voff, s * ck_stride, 0);
   };
   auto step_seg = [&](int s, const float* v, int slow, float* nv, auto has_next) {
     constexpr bool kNext = decltype(has_next)::value;
@@ -397,9 +397,15 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
         float* B = va + kSeg / 2;
         float* C = vb;
         float* D = vb + kSeg / 2;
-        auto ld = [&](int s, int h, float* d) {
+        // (ring slots and checkpoint offsets from the interval's base, so the
+        // chain wave issues a few scalar adds per segment instead of a
+        // modulo and a product)
+        const int b0 = s0 % kCarryBufs;
+        const int ck0 = s0 * ck_stride;
+        auto ld = [&](int k, int h, float* d) {
           asm volatile("" ::: "memory");
-          const float4* src = reinterpret_cast<const float4*>(&s_inc[s % kCarryBufs][lane * kIncLd]) + 8 * h;
+          const int bk = b0 + k >= kCarryBufs ? b0 + k - kCarryBufs : b0 + k;
+          const float4* src = reinterpret_cast<const float4*>(&s_inc[bk][lane * kIncLd]) + 8 * h;
 #pragma unroll
           for (int q = 0; q < 8; ++q) {
             const float4 u = src[q];
@@ -416,16 +422,19 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
           for (int i = 0; i < kSeg / 2; ++i) ph = __builtin_amdgcn_fractf(ph + v[i]);
           __builtin_amdgcn_sched_barrier(0);
         };
-        store_ckpt(s0);
-        ld(s0 + 1, 0, C); st(A); ld(s0 + 1, 1, D); st(B);
-        store_ckpt(s0 + 1);
+        auto ck = [&](int k) {
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, ph), ck_rsrc, ck_voff, ck0 + k * ck_stride, 0);
+        };
+        ck(0);
+        ld(1, 0, C); st(A); ld(1, 1, D); st(B);
+        ck(1);
         // (read here, combined after the run: its wait then costs nothing)
         const int4 votes = block_votes(s0 + kIv);
-        ld(s0 + 2, 0, A); st(C); ld(s0 + 2, 1, B); st(D);
-        store_ckpt(s0 + 2);
-        ld(s0 + 3, 0, C); st(A); ld(s0 + 3, 1, D); st(B);
-        store_ckpt(s0 + 3);
-        ld(s0 + kIv, 0, A); st(C); ld(s0 + kIv, 1, B); st(D);
+        ld(2, 0, A); st(C); ld(2, 1, B); st(D);
+        ck(2);
+        ld(3, 0, C); st(A); ld(3, 1, D); st(B);
+        ck(3);
+        ld(kIv, 0, A); st(C); ld(kIv, 1, B); st(D);
         nbad = any_vote(votes);
         interval_barrier();
         if (++iv >= nint) break;
