@@ -291,20 +291,33 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
   float ph = 0.0f;  // the phasor state cell is zero at the start of every run
   // steps segment s from v; if nv, loads segment s+1 into nv half by half in
   // between so at most ~8 LDS reads are in flight
-  // checkpoint stores through a buffer resource bounded to this batch
-  // lane's rows: lanes >= K get an offset past the bound and the hardware
-  // drops their store, so the store needs no branch around it
+  // Checkpoints: the chain writes the phase entering segment s into the
+  // padding word of its lane's row of the segment's ring slot (word kSeg,
+  // which no producer writes and no increment read covers; an LDS write
+  // costs the chain less than a store to memory), and producer wave 1
+  // copies an interval's checkpoints to memory during the next interval
+  // (the slot's padding is next written by the chain for segment s + 9,
+  // two intervals later).  The copies go through a buffer resource bounded
+  // to this batch lane's rows: lanes >= K get an offset past the bound and
+  // the hardware drops their store, so the store needs no branch around it.
+  static_assert(kIncLd > kSeg && kCarryBufs > 2 * kIv, "a free word per row, not rewritten for two intervals");
   const auto ck_rsrc = __builtin_amdgcn_make_buffer_rsrc(ckpt + (size_t)b * K + k0, 0,
                                                          (int)(4u * (unsigned)((nseg - 1) * B * K + K - k0)),
                                                          0x00020000);
   const unsigned ck_voff = k0 + lane < K ? 4u * (unsigned)lane : 0x80000000u;
   const int ck_stride = 4 * B * K;  // bytes per segment of checkpoints
-  auto store_ckpt = [&](int s) {
-    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, ph), ck_rsrc, ck_voff, s * ck_stride, 0);
+  auto keep_ckpt = [&](int slot) { s_inc[slot][lane * kIncLd + kSeg] = ph; };
+  auto copy_ckpts = [&](int iv) {  // producer wave 1: interval iv's checkpoints to memory
+    for (int q = 0; q < kIv; ++q) {
+      const int s = iv * kIv + q;
+      if (s < nseg)
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, s_inc[s % kCarryBufs][lane * kIncLd + kSeg]),
+                                              ck_rsrc, ck_voff, s * ck_stride, 0);
+    }
   };
   auto step_seg = [&](int s, const float* v, int slow, float* nv, auto has_next) {
     constexpr bool kNext = decltype(has_next)::value;
-    store_ckpt(s);
+    keep_ckpt(s % kCarryBufs);
     if (!slow) {
       if constexpr (kNext) fetch_half(s + 1, nv, 0);
       __builtin_amdgcn_sched_barrier(0);
@@ -397,11 +410,9 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
         float* B = va + kSeg / 2;
         float* C = vb;
         float* D = vb + kSeg / 2;
-        // (ring slots and checkpoint offsets from the interval's base, so the
-        // chain wave issues a few scalar adds per segment instead of a
-        // modulo and a product)
+        // (ring slots from the interval's base, so the chain wave issues a
+        // few scalar adds per segment instead of a modulo)
         const int b0 = s0 % kCarryBufs;
-        const int ck0 = s0 * ck_stride;
         auto ld = [&](int k, int h, float* d) {
           asm volatile("" ::: "memory");
           const int bk = b0 + k >= kCarryBufs ? b0 + k - kCarryBufs : b0 + k;
@@ -422,9 +433,7 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
           for (int i = 0; i < kSeg / 2; ++i) ph = __builtin_amdgcn_fractf(ph + v[i]);
           __builtin_amdgcn_sched_barrier(0);
         };
-        auto ck = [&](int k) {
-          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, ph), ck_rsrc, ck_voff, ck0 + k * ck_stride, 0);
-        };
+        auto ck = [&](int k) { keep_ckpt(b0 + k >= kCarryBufs ? b0 + k - kCarryBufs : b0 + k); };
         ck(0);
         ld(1, 0, C); st(A); ld(1, 1, D); st(B);
         ck(1);
@@ -498,8 +507,10 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
           for (int s = next; s < nseg; ++s) produce(s, g0c, ngc);
         }
         if ((iv + 4) % 3 == 0 && (iv + 4) / 3 < nblk) commit_block((iv + 4) / 3);
+        if (wave == 1 && iv > 0) copy_ckpts(iv - 1);
         interval_barrier();
       }
+      if (wave == 1) copy_ckpts(nint - 1);
     });
   }
   if constexpr (TIMED) {
