@@ -156,10 +156,6 @@ inline float fast_f0_limit(int K) { return 0x1p24f / (float)(64 * harmonic_group
 // interval count.
 enum CarryTimer { kTmChainWait, kTmProdWait, kTmCycle0, kTmCycle1, kTmReal0, kTmReal1, kTmIntervals, kTmWords = 8 };
 
-__device__ __forceinline__ int4 votes8(const int* p) {
-  const int4 a = reinterpret_cast<const int4*>(p)[0], b = reinterpret_cast<const int4*>(p)[1];
-  return make_int4(a.x | b.x, a.y | b.y, a.z | b.z, a.w | b.w);
-}
 template <int P, class F>
 __device__ __forceinline__ void dispatch_producer(int wave, F& body) {
   if constexpr (P < kProducers) {
@@ -178,7 +174,8 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
                                                                    unsigned long long* __restrict__ timer) {
   __shared__ __align__(16) float s_inc[kCarryBufs][64 * kIncLd];  // [k][frame]
   __shared__ __align__(16) float s_f0[2][kRing * kSeg];
-  __shared__ __align__(16) int s_blkbad[2][8];  // f0 block holds a value outside the fast range
+  __shared__ __align__(16) int s_blkbad[2][8];  // producer p's part of an f0 block holds a value outside the fast range
+  __shared__ int s_vote[2];                      // the block's parts combined (producer wave 1, an interval after the commit)
   const int b = blockIdx.x, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int k0 = 64 * (int)blockIdx.y;  // first harmonic of the group
   const int nseg = (T + kSeg - 1) / kSeg;
@@ -228,8 +225,7 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
     constexpr int G0 = decltype(g0c)::value, NG = decltype(ngc)::value;
     const int par = (s / kRing) & 1;
     const float4* f4 = reinterpret_cast<const float4*>(&s_f0[par][(s % kRing) * kSeg]) + G0;
-    const int4 v = votes8(s_blkbad[par]);
-    const bool fast = (v.x | v.y | v.z | v.w) == 0;
+    const bool fast = s_vote[par] == 0;
     const float kf = (float)(k0 + lane + 1);
     float4* dst = reinterpret_cast<float4*>(&s_inc[s % kCarryBufs][lane * kIncLd]) + G0;
     if (fast) {
@@ -259,8 +255,7 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
       const float4* f4 = reinterpret_cast<const float4*>(&s_f0[par][(sq % kRing) * kSeg]) + G0;
 #pragma unroll
       for (int g = 0; g < NG; ++g) f[q][g] = f4[g];
-      const int4 v = votes8(s_blkbad[par]);
-      anybad |= v.x | v.y | v.z | v.w;
+      anybad |= s_vote[par];
     }
     const float kf = (float)(k0 + lane + 1);
     if (__builtin_expect(!anybad, 1)) {
@@ -347,6 +342,18 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
     load_block(1);
   }
   lds_barrier();
+  // block m's vote: the OR of its producers' parts
+  auto combine_votes = [&](int m) {
+    int v = 0;
+#pragma unroll
+    for (int w = 0; w < kProducers; ++w) v |= s_blkbad[m & 1][w];
+    s_vote[m & 1] = v;
+  };
+  if (wave == 1 && lane == 0) {
+    combine_votes(0);
+    combine_votes(1);
+  }
+  lds_barrier();
   // producer p's frame groups, as constants of its code
   auto as_producer = [&](auto body) __attribute__((always_inline)) { dispatch_producer<0>(wave, body); };
 
@@ -383,9 +390,8 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
     // intervals before the chain reads it, and overwritten (by block + 2)
     // only after the chain has passed that block's last interval.
     static_assert(kRing % kIv == 0, "an interval lies in one f0 block");
-    auto block_votes = [&](int s0) { return votes8(s_blkbad[(s0 / kRing) & 1]); };
-    auto any_vote = [](int4 v) { return v.x | v.y | v.z | v.w; };
-    int nbad = any_vote(block_votes(0));  // the next interval's vote, read an interval ahead
+    auto block_vote = [&](int s0) { return s_vote[(s0 / kRing) & 1]; };
+    int nbad = block_vote(0);  // the next interval's vote, read an interval ahead
     // va holds the interval's first segment on entry (read before the
     // barrier that ends the previous interval)
     float va[kSeg], vb[kSeg];
@@ -438,13 +444,13 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
         ld(1, 0, C); st(A); ld(1, 1, D); st(B);
         ck(1);
         // (read here, combined after the run: its wait then costs nothing)
-        const int4 votes = block_votes(s0 + kIv);
+        const int vote = block_vote(s0 + kIv);
         ld(2, 0, A); st(C); ld(2, 1, B); st(D);
         ck(2);
         ld(3, 0, C); st(A); ld(3, 1, D); st(B);
         ck(3);
         ld(kIv, 0, A); st(C); ld(kIv, 1, B); st(D);
-        nbad = any_vote(votes);
+        nbad = vote;
         interval_barrier();
         if (++iv >= nint) break;
       }
@@ -481,7 +487,7 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
             }
           }
         }
-        nbad = any_vote(block_votes(s0 + kIv));
+        nbad = block_vote(s0 + kIv);
         fetch_half(s0 + kIv, va, 0);
         fetch_half(s0 + kIv, va, 1);
         interval_barrier();
@@ -494,8 +500,10 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
     // Block m replaces block m - 2 in its buffer: its loads are issued in
     // interval 3 m - 5 and committed in 3 m - 4, after block m - 2's last
     // reader and three intervals before block m's first (blocks 0 and 1
-    // are loaded before the loop); the chain reads a block's vote from
-    // interval 3 m - 1 to 3 m + 1.
+    // are loaded before the loop).  Producer wave 1 combines block m's
+    // votes in interval 3 m - 3; the producers read the vote from 3 m - 2
+    // and the chain from 3 m - 1, both until 3 m + 1, before block m + 2's
+    // combine (3 m + 3) overwrites it.
     static_assert(kAhead == 5 && kRing == 12 && kIv == 4, "the block schedule below");
     as_producer([&](auto g0c, auto ngc) __attribute__((always_inline)) {
       for (int iv = 0; iv < nint; ++iv) {
@@ -507,6 +515,7 @@ __global__ __launch_bounds__(64 * kCarryWaves) void k_phasor_carry(const float* 
           for (int s = next; s < nseg; ++s) produce(s, g0c, ngc);
         }
         if ((iv + 4) % 3 == 0 && (iv + 4) / 3 < nblk) commit_block((iv + 4) / 3);
+        if (wave == 1 && lane == 0 && iv % 3 == 0 && iv / 3 + 1 < nblk && iv > 0) combine_votes(iv / 3 + 1);
         if (wave == 1 && iv > 0) copy_ckpts(iv - 1);
         interval_barrier();
       }

@@ -40,8 +40,9 @@ def with_slow_blocks(cfg, f0):
 
 
 # (T, K): whole intervals; a partial last interval of whole segments; a
-# partial last segment; two harmonic groups with a partial segment
-CASES = [(6400, 60), (6400 + 3 * 64, 60), (6400 + 100, 60), (4096 + 17, 100)]
+# partial last segment; two harmonic groups with a partial segment; fewer
+# segments than the producers' lead; one f0 block and a partial second
+CASES = [(6400, 60), (6400 + 3 * 64, 60), (6400 + 100, 60), (4096 + 17, 100), (100, 60), (64 * 13 + 5, 60)]
 
 
 @pytest.mark.parametrize("T,K", CASES, ids=[f"T{t}-K{k}" for t, k in CASES])
