@@ -17,6 +17,8 @@ Prints ONE JSON line (rank 0):
                 which for a side-stream op also covers waiting for CU slots
                 beside the stream-0 work it overlaps
   step_roofline sum of per-op roofline times / measured step time
+  phase_chain   the phase chain alone and in the step against its latency
+                floor (T dependent add+fract steps at their measured cycles)
   cpu_baseline  the CPU oracle forward (fp32, -O3 -ffast-math) on a bounded
                 sample of the same workload, timed on this host
 
@@ -203,6 +205,11 @@ def traffic_run(sess, workload: str, runs: int, labels: str | None = None) -> in
     print(json.dumps({"traffic_ops": [prog.ops[i].label for i in idx], "runs": runs, "workload": workload}),
           flush=True)
     return 0
+
+
+# cycles of one dependent add+fract step of a lone wave, measured on gfx950
+# (dgen-audio_amd/csrc/probe_chain.cpp, mode 0)
+CHAIN_STEP_CYCLES = 9.2
 
 
 def roofline_fields(rows, dom, roof_ms, ms_per_step, workload: str = "harmonic"):
@@ -621,6 +628,15 @@ def run_harmonic(args) -> dict:
                    + [cfg.NC], "parallelism": "single GPU"},
     }
     out.update(roofline_fields(rows, dom, roof_ms, ms_per_step, "harmonic"))
+    # the phase chain is a latency bound, not a VALU-throughput one: its
+    # floor is T dependent add+fract steps at the cycles one takes
+    # (dgen-audio_amd/csrc/probe_chain.cpp) at the part's 2.4 GHz
+    chain = [r for r in rows if r.label == "phasor_carry"]
+    if chain:
+        floor_ms = cfg.T * CHAIN_STEP_CYCLES / 2.4e9 * 1e3
+        out["phase_chain"] = {"ms": chain[0].meas_ms, "in_step_ms": getattr(chain[0], "in_step_ms", chain[0].meas_ms),
+                              "latency_floor_ms": floor_ms, "frac_of_floor": floor_ms / chain[0].meas_ms,
+                              "step_cycles_measured_floor": CHAIN_STEP_CYCLES}
     out["loss"] = loss
     out["cpu_baseline"] = cpu
     return out
