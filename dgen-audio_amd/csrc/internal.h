@@ -81,6 +81,14 @@ using Launcher = int (*)(const Launch&, const dgen_hip_op&);
 // __syncthreads() also waits for those, which exposes prefetch latency).
 // Kernels use it only where no global-memory ordering between threads of
 // the workgroup is needed.
+// Spectral-loss tiles: a workgroup owns kMssTile output samples and keeps the
+// gradient of [a - kMssHalo, a + kMssTile) (kMssHalo = largest N - 1); the
+// tile partials are [B][ntiles][kMssAcc].  The synth backward adds them up
+// per sample when it reads the prediction's gradient.
+constexpr int kMssTile = 4096;
+constexpr int kMssHalo = 2047;
+constexpr int kMssAcc = kMssTile + kMssHalo;
+
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // Orders one wave's LDS accesses around this point for every lane of the

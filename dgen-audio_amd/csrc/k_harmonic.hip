@@ -1113,8 +1113,19 @@ __device__ __forceinline__ void store_slots(const float (&acc)[kSlots], SL& L, i
   for (int j = 0; j < kSlots; ++j) L.row[j][c] = acc[j];
 }
 
+// MssGrad: with part, the prediction's gradient is gathered here from the
+// spectral loss's tile partials (plus the time-domain MSE term) and also
+// stored to dy, instead of in a launch of its own between the two kernels.
+struct MssGrad {
+  const float* part;  // [B][ntiles][kMssAcc] or null: read dy
+  const float* x;     // the prediction and the target ([B][T]) for the MSE term
+  const float* tgt;
+  int ntiles;
+  float w_mse;
+};
+
 template <class SL>
-__device__ __forceinline__ void bwd_segment(const SynthArgs& a, SL& L, const float* __restrict__ dy,
+__device__ __forceinline__ void bwd_segment(const SynthArgs& a, SL& L, float* __restrict__ dy, const MssGrad& mg,
                                             const float* __restrict__ aux, int s, int b, int lane) {
   const int t0 = s * kSeg, nt = min(kSeg, a.T - t0);
   int nslot;
@@ -1135,7 +1146,19 @@ __device__ __forceinline__ void bwd_segment(const SynthArgs& a, SL& L, const flo
       const float gain = r.omf * L.row[slo][a.K] + r.frac * L.row[shi][a.K];
       const float ngain = r.omf * L.row[slo][a.K + 1] + r.frac * L.row[shi][a.K + 1];
       const float uv = a.uvf[bt];
-      const float g = dy[bt];
+      float g;
+      if (mg.part) {
+        // the two tiles whose accumulators hold sample t, in the order the
+        // separate gather added them, then the MSE term's 2 w (x - tgt) / B
+        const int tile = t / kMssTile, ta = tile * kMssTile;
+        const float* pp = mg.part + ((size_t)b * mg.ntiles + tile) * kMssAcc;
+        g = pp[t - ta + kMssHalo];
+        if (tile + 1 < mg.ntiles && t >= ta + kMssTile - kMssHalo) g += pp[kMssAcc + (t - ta - kMssTile + kMssHalo)];
+        if (mg.w_mse != 0.f) g += mg.w_mse * (2.f * (mg.x[bt] - mg.tgt[bt])) * (1.0f / (float)a.B);
+        dy[bt] = g;
+      } else {
+        g = dy[bt];
+      }
       hs = hsum;
       coef = (((g * gain) * uv) * a.hscale) / den;
       dg = ((g * hsum) * uv) * a.hscale;
@@ -1345,10 +1368,11 @@ int launch_run_table(const Launch& L, const dgen_hip_op& op) {
 }
 
 template <class SL>
-__global__ __launch_bounds__(64 * kRunSegs) void k_synth_bwd(SynthArgs a, const float* __restrict__ dy,
+__global__ __launch_bounds__(64 * kRunSegs) void k_synth_bwd(SynthArgs a, float* __restrict__ dy,
                                                              const float* __restrict__ aux,
                                                              const uint4* __restrict__ runtab,
-                                                             float* __restrict__ dctrl, float* __restrict__ bpart) {
+                                                             float* __restrict__ dctrl, float* __restrict__ bpart,
+                                                             MssGrad mg) {
   __shared__ SL lds[kRunSegs];
   __shared__ uint4 s_tab[kRunRows + 1];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -1358,7 +1382,7 @@ __global__ __launch_bounds__(64 * kRunSegs) void k_synth_bwd(SynthArgs a, const 
   // the run's row table, loaded at the start and staged after wave 0's segment
   uint4 tv = make_uint4(0u, 0u, 0u, 0u);
   if (wave == 0 && lane <= kRunRows) tv = runtab[(size_t)run * (kRunRows + 1) + lane];
-  if (s0 + wave < nseg) bwd_segment(a, lds[wave], dy, aux, s0 + wave, b, lane);
+  if (s0 + wave < nseg) bwd_segment(a, lds[wave], dy, mg, aux, s0 + wave, b, lane);
   if (wave == 0 && lane <= kRunRows) s_tab[lane] = tv;
   __syncthreads();
   // each row's sum over the run's entries in list order, a wave per row
@@ -1520,7 +1544,20 @@ int launch_synth_bwd(const Launch& L, const dgen_hip_op& op) {
   int rc = synth_args(L, op, a, "synth_bwd");
   if (rc) return rc;
   // [12]=boundary partials ([B][F][6][ldc]) [16]=tape [17]=run table (DGEN_HIP_K_RUN_TABLE) [18]=dctrl
+  // [19]=1: [5] (dy) is gathered here from the spectral loss's tile
+  // partials [20] ([B][ntiles][kMssAcc]) plus farg[3] times the MSE term of
+  // the prediction [21] and target [22] ([B][T]), and stored to [5]
   const int64_t T = op.arg[10], B = op.arg[6], F = op.arg[9], ldc = op.arg[14];
+  DGEN_REQUIRE(op.arg[19] == 0 || op.arg[19] == 1, "synth_bwd: gather flag %lld", (long long)op.arg[19]);
+  MssGrad mg{};
+  const int64_t ntiles = (T + kMssTile - 1) / kMssTile;
+  if (op.arg[19] == 1) {
+    DGEN_CHECK_CELL(L, op.arg[20], B * ntiles * kMssAcc, "synth_bwd.mss_tiles");
+    if (op.farg[3] != 0.f) {
+      DGEN_CHECK_CELL(L, op.arg[21], B * T, "synth_bwd.prediction");
+      DGEN_CHECK_CELL(L, op.arg[22], B * T, "synth_bwd.target");
+    }
+  }
   const int64_t nseg = (T + kSeg - 1) / kSeg;
   DGEN_CHECK_CELL(L, op.arg[12], B * F * kRunParts * ldc, "synth_bwd.boundary_partials");
   DGEN_CHECK_CELL(L, op.arg[16], 3 * B * T, "synth_bwd.aux");
@@ -1529,14 +1566,24 @@ int launch_synth_bwd(const Launch& L, const dgen_hip_op& op) {
   DGEN_REQUIRE(ldc <= kMaxNCWide, "synth_bwd: row stride %lld > %d", (long long)ldc, kMaxNCWide);
   DGEN_CHECK_CELL(L, op.arg[18], B * F * ldc, "synth_bwd.dctrl");
   if (L.dry) return 0;
+  if (op.arg[19] == 1) {
+    mg.part = cell(L, op.arg[20]);
+    mg.ntiles = (int)ntiles;
+    mg.w_mse = op.farg[3];
+    if (mg.w_mse != 0.f) {
+      mg.x = cell(L, op.arg[21]);
+      mg.tgt = cell(L, op.arg[22]);
+    }
+  }
   const dim3 grid((unsigned)((nseg + kRunSegs - 1) / kRunSegs), (unsigned)a.B), block(64 * kRunSegs);
   if (synth_narrow(a))
     hipLaunchKernelGGL(k_synth_bwd<SegLdsBwd>, grid, block, 0, L.stream, a, cell(L, op.arg[5]), cell(L, op.arg[16]),
-                       reinterpret_cast<const uint4*>(cell(L, op.arg[17])), cell(L, op.arg[18]), cell(L, op.arg[12]));
+                       reinterpret_cast<const uint4*>(cell(L, op.arg[17])), cell(L, op.arg[18]), cell(L, op.arg[12]),
+                       mg);
   else
     hipLaunchKernelGGL(k_synth_bwd<SegLdsBwdWide>, grid, block, 0, L.stream, a, cell(L, op.arg[5]),
                        cell(L, op.arg[16]), reinterpret_cast<const uint4*>(cell(L, op.arg[17])),
-                       cell(L, op.arg[18]), cell(L, op.arg[12]));
+                       cell(L, op.arg[18]), cell(L, op.arg[12]), mg);
   DGEN_LAUNCH_CHECK("k_synth_bwd");
   return 0;
 }

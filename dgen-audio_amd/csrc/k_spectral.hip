@@ -32,9 +32,9 @@
 
 namespace dgen {
 
-constexpr int kTile = 4096;        // output samples owned by a workgroup
-constexpr int kHalo = 2047;        // largest N - 1
-constexpr int kAcc = kTile + kHalo;
+constexpr int kTile = kMssTile;    // output samples owned by a workgroup
+constexpr int kHalo = kMssHalo;    // largest N - 1
+constexpr int kAcc = kMssAcc;
 constexpr int kThreads = 256;
 constexpr int kMaxSizes = 8;
 constexpr float kLogEps = 1e-8f;   // DGenSpectralConfig.logMagnitudeEpsilon (GradientConfig.swift:38)

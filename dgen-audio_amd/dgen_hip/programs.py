@@ -276,8 +276,8 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
         + [y, target]
     w_mse = np.float32(cfg.w_mse)
     mse_b = 2 * B * T * f4 if w_mse else 0
-    p.add(R.K_SPECTRAL_GATHER, garg, [wl, wg, maxf, w_mse], label="spectral_combine", dispatch=f"perFrameScaled({B})",
-          bytes=(B * ntiles * (MSS_TILE + 2047) + B * T) * f4 + mse_b, flops=float(B * T))
+    # d loss / d y (the tile partials gathered per sample, plus the MSE
+    # term) is formed by the synth backward as it reads it, and stored to dy
     # the per-frame loss signal (only reported, nothing in the backward reads
     # it) is a launch of its own at the end of stream 0, which finishes
     # before the side stream: folded into the combine, its blocks were the
@@ -294,12 +294,13 @@ def harmonic_program(cfg: HarmonicConfig, train: bool = True, optimizer: bool = 
     bargs = list(synth_args)
     bargs[5] = dy
     bargs[12] = bpart
-    bargs += [aux, runtab, dctrl]
+    bargs += [aux, runtab, dctrl, 1, mss_part, y, target]
     # rows per lane: shared by two runs at each run boundary
     shared = min(F, 2 * max(0, nruns - 1))
     bpart_b = B * 2 * shared * NC * f4
-    p.add(R.K_SYNTH_BWD, bargs, [cfg.sr, hs, ns], label="synth_bwd", dispatch=f"selfManagedThreads({B})",
-          bytes=ctrl_b + lerp_b + ck_b + data_b + 4 * B * T * f4 + (M - B * shared) * NC * f4 + bpart_b,
+    p.add(R.K_SYNTH_BWD, bargs, [cfg.sr, hs, ns, w_mse], label="synth_bwd", dispatch=f"selfManagedThreads({B})",
+          bytes=ctrl_b + lerp_b + ck_b + data_b + 4 * B * T * f4 + (M - B * shared) * NC * f4 + bpart_b
+          + B * ntiles * (MSS_TILE + 2047) * f4 + mse_b,
           flops=synth_flops + float(B) * T * (6.0 * K + 4.0 * NC), bound="valu")
     # the row reduce also runs the head backward of every row (dZ from d ctrl and Z)
     dZ = p.alloc("dZ", M * LDC)

@@ -32,7 +32,7 @@ def test_op_operands_lie_in_cells():
 def test_train_schedule_order():
     labels = [op.label for op in harmonic_program(HarmonicConfig()).ops if not op.flags & R.OP_STATIC]
     assert labels.index("phasor_carry") < labels.index("synth_fwd") < labels.index("spectral_mss")
-    assert labels.index("spectral_combine") < labels.index("synth_bwd") < labels.index("synth_bwd_reduce")
+    assert labels.index("spectral_mss") < labels.index("synth_bwd") < labels.index("synth_bwd_reduce")
     assert labels[-1] == "adam"
 
 
