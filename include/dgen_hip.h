@@ -159,7 +159,16 @@ enum dgen_hip_kernel {
    * run, at the run's index among the row's runs.
    * arg: as DGEN_HIP_K_SYNTH_FWD with [5]=dy ([B][T]) [12]=boundary partials
    *      cell ([B][F][6][ldc]) [16]=the forward's per-frame tape [17]=run
-   *      table (DGEN_HIP_K_RUN_TABLE) [18]=dctrl ([B*F][ldc]) */
+   *      table (DGEN_HIP_K_RUN_TABLE) [18]=dctrl ([B*F][ldc])
+   *      [19]=1 to form dy here, else 0 (dy read as given)
+   *      [20]=spectral-loss tile partials ([B][ntiles][tile + halo] as
+   *      DGEN_HIP_K_SPECTRAL_LOSS leaves them) [21]=prediction x ([B][T])
+   *      [22]=target ([B][T]; read only when farg[3] != 0)
+   * farg: as DGEN_HIP_K_SYNTH_FWD with [3]=weight of the time-domain term
+   *       (its gradient 2 w (x - target) / B joins dy) or 0.
+   * With [19]=1 each sample's d loss / d y (owning tile + next tile's halo,
+   * plus the time-domain term) is summed as the segment reads it and also
+   * stored to dy, so no DGEN_HIP_K_SPECTRAL_GATHER launch is needed. */
   DGEN_HIP_K_SYNTH_BWD = 9,
 
   /* d ctrl of the rows shared between synth-backward runs: their partials
