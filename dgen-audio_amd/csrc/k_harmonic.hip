@@ -1244,20 +1244,21 @@ __device__ __forceinline__ void bwd_segment(const SynthArgs& a, SL& L, float* __
 
 // Head backward of one control row (the rules of k_heads_bwd,
 // Model.swift:100-114) on one wave: lane l holds d ctrl of columns
-// l + 64 q (q < QN) in s[q] and gets dZ of those columns in out[q].  The
+// l + 64 q (q < QN) in s[q] and Z of those columns in zin[q] (read for
+// columns below K + 2 + NF) and gets dZ of those columns in out[q].  The
 // row sums (softplus over the K amplitudes, |tanh| over the NF noise taps,
 // then the two dot products) add each 64-column block's wave sum in block
 // order.  Columns past K + 2 + NF get 0.
 template <int QN>
-__device__ __forceinline__ void head_row_bwd(const float (&s)[QN], const float* __restrict__ zrow,
-                                             float (&out)[QN], int lane, int K, int NF) {
+__device__ __forceinline__ void head_row_bwd(const float (&s)[QN], const float (&zin)[QN], float (&out)[QN],
+                                             int lane, int K, int NF) {
   float z[QN], sp[QN], th[QN];
   float den = 0.f, nrm = 0.f;
 #pragma unroll
   for (int q = 0; q < QN; ++q) {
     const int c = lane + 64 * q;
     const bool amp = c < K, noise = c >= K + 2 && c < K + 2 + NF;
-    z[q] = c < K + 2 + NF ? zrow[c] : 0.f;
+    z[q] = c < K + 2 + NF ? zin[q] : 0.f;
     sp[q] = amp ? softplus(z[q]) : 0.f;
     th[q] = noise ? fast_tanh(z[q]) : 0.f;
   }
@@ -1428,16 +1429,25 @@ __global__ __launch_bounds__(256) void k_synth_bwd_reduce(const float* __restric
   const int f = blockIdx.x * 4 + wave, b = blockIdx.y;
   if (f >= F) return;
   const size_t row = (size_t)b * F + f;
-  // the row's runs (uniform across the wave)
+  // Every load that does not depend on the row's run count is issued
+  // first: the row list (entry e on lane e), d ctrl as the synth backward
+  // left it (used when the row is complete) and, with the heads, Z.  The
+  // partials are the only dependent stage, for shared rows.
   const float* lst = row_list + (size_t)f * kRowEntries;
-  int nruns = 0, prev = -1;
-  for (int e = 0; e < kRowEntries; ++e) {
-    const float ef = lst[e];
-    if (ef < 0.0f) break;
-    const int rr = (int)ef / kSlots / kRunSegs;
-    if (rr != prev) ++nruns;
-    prev = rr;
+  const float ef = lane < kRowEntries ? lst[lane] : -1.0f;
+  float dc[QN], zr[QN];
+#pragma unroll
+  for (int q = 0; q < QN; ++q) {
+    const int c = lane + 64 * q;
+    dc[q] = c < NC ? dctrl[row * ldc + c] : 0.f;
+    zr[q] = HEADS && c < NC ? Z[row * ldc + c] : 0.f;
   }
+  // the row's runs: the entries before the first negative one, a new run
+  // wherever an entry's run differs from the previous entry's (uniform)
+  const int nvalid = (int)__builtin_ctzll(__ballot(lane >= kRowEntries || ef < 0.0f));
+  const int rr = lane < nvalid ? (int)ef / kSlots / kRunSegs : -1;
+  const int rprev = __shfl_up(rr, 1, 64);
+  const int nruns = (int)__popcll(__ballot(lane < nvalid && (lane == 0 || rr != rprev)));
   const bool done = nruns == 1;  // completed by the synth backward
   if (done && !HEADS) return;
   float s[QN];
@@ -1446,8 +1456,7 @@ __global__ __launch_bounds__(256) void k_synth_bwd_reduce(const float* __restric
     const int c = lane + 64 * q;
     float v = 0.f;
     if (done) {
-      if (c < NC) v = dctrl[row * ldc + c];
-      s[q] = v;
+      s[q] = dc[q];
       continue;
     }
     if (c < NC) {
@@ -1465,7 +1474,7 @@ __global__ __launch_bounds__(256) void k_synth_bwd_reduce(const float* __restric
   }
   if constexpr (HEADS) {
     float dz[QN];
-    head_row_bwd<QN>(s, Z + row * ldc, dz, lane, K, NF);
+    head_row_bwd<QN>(s, zr, dz, lane, K, NF);
 #pragma unroll
     for (int q = 0; q < QN; ++q)
       if (lane + 64 * q < ldc) dZ[row * ldc + lane + 64 * q] = dz[q];
