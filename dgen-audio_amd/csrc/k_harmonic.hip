@@ -720,7 +720,7 @@ __device__ __forceinline__ float frame_fir(const SynthArgs& a, const SL& L, int 
 // the backward reuses.
 constexpr int kWavesFwd = 2;
 
-// Row-slot arithmetic of a frame.  NS = 2 or 4: the slot-weight form over
+// Row-slot arithmetic of a frame.  NS = 2, 3 or 4: the slot-weight form over
 // the slots that can be nonzero (a weight-0 slot contributes 0 * value, so
 // the operands must be finite: the kernels vote for it per segment).
 // NS = 0: the exact per-frame form of the reference's sampleRow lerp and its
@@ -733,7 +733,7 @@ constexpr int kWavesFwd = 2;
 // the others add a signed zero, so the value is the exact form's bit for bit.
 template <int NS>
 __device__ __forceinline__ float slot_lerp(const float4& w, const float (&rv)[kSlots]) {
-  static_assert(NS == 2 || NS == kSlots, "slot-weight form");
+  static_assert(NS == 2 || NS == 3 || NS == kSlots, "slot-weight form");
   float v = w.x * rv[0] + w.y * rv[1];
   if constexpr (NS > 2) v = v + w.z * rv[2];
   if constexpr (NS > 3) v = v + w.w * rv[3];
@@ -791,6 +791,10 @@ __device__ __forceinline__ void chain_regs(const SynthArgs& a, const SL& L, floa
         r[j] = L.fr[i0 + j];
         al[j] = L.row[r[j].slots & 255][kk];
         ah[j] = L.row[r[j].slots >> 8][kk];
+      } else if constexpr (NS == 3) {
+        // three slots: the record's fourth word holds the frame's f0
+        w[j] = L.wt[i0 + j];
+        r[j].f0 = w[j].w;
       } else {
         r[j].f0 = L.fr[i0 + j].f0;
         w[j] = L.wt[i0 + j];
@@ -909,10 +913,14 @@ __device__ __forceinline__ void fwd_group(const SynthArgs& a, const SL& L, float
     for (int j = 0; j < kSlots; ++j) rz[j] = zero ? 0.0f : rv[j];
     if (ns == 2)
       chain_regs<true, 2, true, ADD>(a, L, v, kh, nt, ph, rz);
+    else if (ns == 3)
+      chain_regs<true, 3, true, ADD>(a, L, v, kh, nt, ph, rz);
     else
       chain_regs<true, kSlots, true, ADD>(a, L, v, kh, nt, ph, rz);
   } else if (fast && ns == 2)
     chain_regs<true, 2, false, ADD>(a, L, v, kh, nt, ph, rv);
+  else if (fast && ns == 3)
+    chain_regs<true, 3, false, ADD>(a, L, v, kh, nt, ph, rv);
   else if (fast && ns == kSlots)
     chain_regs<true, kSlots, false, ADD>(a, L, v, kh, nt, ph, rv);
   else if (fast)
@@ -944,8 +952,15 @@ __global__ __launch_bounds__(64 * kWavesFwd) void k_synth_fwd(SynthArgs a, float
       for (int j = 0; j < kSlots; ++j) fin = fin && isfinite(j < nslot ? L.row[j][kk] : 0.0f);
     }
     // slot weights need finite rows and two distinct rows per frame; else
-    // the exact per-frame form
-    const int ns = !(__all(fin) && pairs) ? 0 : (nslot <= 2 ? 2 : kSlots);
+    // the exact per-frame form.  With three slots (nearly every segment when
+    // control rows are about a segment apart) the weight record's unused
+    // fourth word takes the frame's f0, so a frame's chain step reads one
+    // 16-byte record and forms its amplitude from three slots.
+    const int ns = !(__all(fin) && pairs) ? 0 : (nslot <= 2 ? 2 : (nslot == 3 ? 3 : kSlots));
+    if (ns == 3) {
+      L.wt[lane].w = L.fr[lane].f0;
+      wave_sync();
+    }
     float flo = 0.0f, fhi = 0.0f;
     if (fast && ns != 0) {
       flo = fhi = L.fr[lane].f0;
