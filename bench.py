@@ -123,6 +123,10 @@ def time_session(rt, program, args):
     from dgen_hip.roofline import step_roof_ms, table
     if args.graphs:
         rt.set_graphs(True)
+    # The timed region is the device work of the steps: with the program's
+    # output cells declared, the sync that ends it would also copy them (the
+    # rendered audio, 8 MB to 268 MB) to the host, which no step needs.
+    rt.setOutputs(None)
     log(f"bench: warmup {args.warmup} (runs replayed as a HIP graph: {args.graphs})")
     for _ in range(args.warmup):
         rt.run_async()

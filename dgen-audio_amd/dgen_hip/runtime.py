@@ -245,6 +245,16 @@ class HIPLazyRuntime:
     def memoryPointer(self) -> np.ndarray:
         return self._host
 
+    def setOutputs(self, cell: str | None) -> None:
+        """Declare the program's cell `cell` as the output cells that every
+        dgen_hip_run (and the sync after a run_async) copies to the host, or
+        none (None).  The program's output_cell is declared at configure."""
+        if cell is None:
+            _check(self.L.dgen_hip_set_outputs(self._ctx, 0, 0), "dgen_hip_set_outputs")
+        else:
+            c = self.program.cells[cell]
+            _check(self.L.dgen_hip_set_outputs(self._ctx, c.off, c.n), "dgen_hip_set_outputs")
+
     def outputsPointer(self) -> np.ndarray:
         """The output cells in the host mirror, as the last run left them
         (dgen_hip_run copies them back; dgen_hip_host_outputs)."""
