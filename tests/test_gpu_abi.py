@@ -61,6 +61,27 @@ def test_outputs_are_host_visible_after_a_run(osc):
     np.testing.assert_array_equal(rt.outputsPointer(), ref)
 
 
+def test_outputs_can_be_undeclared_and_declared_again(osc):
+    # (the bench's timed region declares none, so its closing sync copies
+    # nothing; the sync after a run_async copies the declared cells)
+    cfg, freqs, amps, rt = osc
+    rt.runNoCopy()
+    ref = rt.read("out")
+    try:
+        rt.setOutputs(None)
+        with pytest.raises(HIPError, match="no output cells"):
+            rt.outputsPointer()
+        rt.run_async()
+        rt.sync()
+    finally:
+        rt.setOutputs("out")
+    view = rt.outputsPointer()
+    view[:] = -7.0
+    rt.run_async()
+    rt.sync()
+    np.testing.assert_array_equal(rt.outputsPointer(), ref)
+
+
 def test_host_sample_rate_drives_the_oscillator_phases(osc):
     cfg, freqs, amps, rt = osc
     rt.runNoCopy()
