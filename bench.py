@@ -1,7 +1,7 @@
 """Benchmark of the HIP backend on its headline workload.
 
 One step = one training pass of the batch-32 harmonic + FIR-noise synth with
-multi-scale spectral loss: control MLP forward (MFMA
+multi-scale spectral loss (benchmark config 3): control MLP forward (MFMA
 GEMMs), synth forward, 6-scale spectral loss, backward to all 0.59M MLP
 parameters, and the Adam update, with every input resident in HBM.
 
@@ -22,7 +22,7 @@ Prints ONE JSON line (rank 0):
   cpu_baseline  the CPU oracle forward (fp32, -O3 -ffast-math) on a bounded
                 sample of the same workload, timed on this host
 
-With ``--workload biquad`` the same line is printed for BASELINE config 4
+With ``--workload biquad`` the same line is printed for benchmark config 4
 (256-lane x 2^18 tensor biquad bank, forward + loss + BPTT + Adam) and with
 ``--workload stft`` for config 2 (8 x 2^20 STFT round trip with per-bin
 gains, forward + loss + gain gradient + Adam) and with ``--workload

@@ -2,7 +2,7 @@
 
 The compute lives in libdgen_hip.so (HIP kernels + C ABI, include/dgen_hip.h);
 this package is the host-side mirror of the reference's runtime interface
-(LazyRuntime) plus the schedule builders for the BASELINE workloads.
+(LazyRuntime) plus the schedule builders for the benchmark workloads.
 """
 from .program import Program  # noqa: F401
 from .runtime import HIPError, HIPLazyRuntime, device_count, load_library  # noqa: F401

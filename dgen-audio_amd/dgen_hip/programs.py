@@ -1,4 +1,4 @@
-"""Schedules for the BASELINE workloads, as the HIP renderer lowers them.
+"""Schedules for the benchmark workloads, as the HIP renderer lowers them.
 
 Each builder returns a :class:`Program` whose ops follow the block order the
 reference compiler produces for the same DGenLazy graph (forward blocks, then

@@ -1,4 +1,4 @@
-"""Synthetic, seeded inputs for the five BASELINE workloads.
+"""Synthetic, seeded inputs for the five benchmark workloads.
 
 All randomness comes from SplitMix64, the generator the reference's
 HarmonicE2E example uses (Examples/HarmonicE2E/Config.swift:245-259), so every

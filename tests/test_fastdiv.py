@@ -1,7 +1,7 @@
 """The phase kernels divide by the sample rate with a reciprocal product and
 two fma corrections (k_harmonic.hip div_sr); it must equal the IEEE quotient
 bit for bit on the range they use it on.  Exhaustive for the sample rates of
-the BASELINE workloads, every 7th float for other common rates."""
+the benchmark workloads, every 7th float for other common rates."""
 import os
 import subprocess
 

@@ -1,5 +1,5 @@
 """Config 1: deterministic phasor bank -> sin -> sum -> history one-pole on
-the GPU against the oracle, at the BASELINE size (65536 frames) and at
+the GPU against the oracle, at the benchmark size (65536 frames) and at
 ragged lengths."""
 import numpy as np
 import pytest

@@ -49,7 +49,7 @@ def test_onepole_is_convolution_with_geometric_kernel():
 
 
 def test_oscbank_config1_inputs():
-    # 16 phasors at k * 220 Hz, amps normalised to sum 1
+    # benchmark config 1: 16 phasors at k * 220 Hz, amps normalised to sum 1
     freqs = (np.arange(1, 17) * 220.0).astype(np.float32)
     rng = np.random.default_rng(1)
     amps = rng.uniform(0, 1, 16).astype(np.float32)
