@@ -1,5 +1,5 @@
 """HIP tensor biquad bank (config 4: chunked forward scan + BPTT adjoint)
-against the CPU oracle: forward within the north-star 1e-4 max-abs of the
+against the CPU oracle: forward within the 1e-4 max-abs parity bar of the
 fp32 oracle and no further from the fp64 oracle than twice the fp32 oracle's
 own rounding, gradients against the fp64 oracle and central finite
 differences, at small ragged shapes and at the full 256 x 2^18
@@ -43,7 +43,7 @@ def test_forward_matches_oracle(gpu, B, T, chunk):
     y64 = O.biquad_fwd(x, m, base, Q, prec="f64")
     err, e_hip, e_o32 = (np.abs(y - y32).max(), np.abs(y - y64).max(), np.abs(y32 - y64).max())
     print(f"max|y - y_oracle32| = {err:.3e}; vs fp64: HIP {e_hip:.3e}, fp32 oracle {e_o32:.3e}")
-    assert err < 1e-4
+    assert err < 1e-4                      # parity bar
     assert e_hip <= 2.0 * e_o32 + 1e-6     # no worse than the reference's own fp32 rounding
 
 
@@ -111,7 +111,7 @@ def test_fused_adjoint_summaries_equal_the_reverse_pass(gpu, B, T, chunk):
 
 
 def test_gradient_matches_finite_differences(gpu):
-    """within 1e-2 relative of central differences of the
+    """Parity bar: within 1e-2 relative of central differences of the
     fp64 oracle forward, per parameter and along the gradient."""
     cfg, s = small_session(B=4, T=2500, chunk=100)
     try:

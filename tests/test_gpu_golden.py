@@ -64,7 +64,7 @@ def test_golden_gradient_close_to_fp64(golden):
 
 
 def test_gradient_matches_finite_differences(golden):
-    """the HIP gradient of sum(loss) within 1e-2 relative of
+    """Parity bar: the HIP gradient of sum(loss) within 1e-2 relative of
     central finite differences of the fp64 oracle forward, measured
     (a) along the gradient direction, (b) on the 8 largest components one by
     one, (c) along random unit directions relative to |grad| (a random

@@ -2,7 +2,7 @@
 
 Each stage is compared with the oracle fed the HIP path's own upstream
 values (so a mismatch names its stage), then end to end.  Tolerances:
-forward audio 1e-4 max-abs (north star), losses 1e-5 relative, gradients of
+forward audio 1e-4 max-abs (the parity bar), losses 1e-5 relative, gradients of
 the well-conditioned stages 1e-3 relative (L2)."""
 import numpy as np
 import pytest

@@ -1,5 +1,5 @@
 """Config 3 at the size the bench times: B=32 lanes x T=64000 frames, hidden
-512, all six FFT sizes, against the CPU oracle; and the north-star gradient
+512, all six FFT sizes, against the CPU oracle; and the 1e-2 gradient
 bar (central finite differences of the fp64 oracle forward within 1e-2) at
 the full per-lane shape (B=4, T=64000, hidden 512, six sizes).
 
@@ -122,7 +122,7 @@ def test_full_size_loss(full):
 # gradient moves by percents when the prediction moves by its fp32
 # rounding: the fp64 backward evaluated at an fp32 prediction is itself
 # ~2.5-4% (relative L2) from the fp64 gradient.  The bars below are the
-# north star's 1e-2 where the floor allows it, and otherwise 1.5 times the
+# the 1e-2 parity bar where the floor allows it, and otherwise 1.5 times the
 # largest value the fp32 oracle reaches over its draws.
 FLOOR = json.load(open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "fp32_floor.json")))
 DRAW_SEED = FLOOR["config"]["seed"]
@@ -235,7 +235,7 @@ def _is_noise_filter_param(cfg, i):
 def test_full_shape_gradient_along_gradient_and_random_directions(lane4):
     """Along the fp64 gradient, against central finite differences of the
     fp64 forward, at the default parameters and two last-ulp moves of
-    them: the north star's 1e-2 on the median (the fp32 oracle's own median
+    them: the 1e-2 parity bar on the median (the fp32 oracle's own median
     is 0.94%, max 1.28%) and 1.5 times the oracle's largest draw on each."""
     cfg, lanes, P64, tgt, g, g64, g32, st, _, draws = lane4
     print(f"grad rel L2 vs fp64 oracle: HIP {rel(g, g64):.3e}, fp32 oracle {rel(g32, g64):.3e} (its floor median "

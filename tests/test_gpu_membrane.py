@@ -1,5 +1,5 @@
 """HIP 2D membrane (config 5: time-blocked stencil forward and discrete
-adjoint) against the CPU oracle: the pickup series within the north-star
+adjoint) against the CPU oracle: the pickup series within the
 1e-4 max-abs of the fp32 oracle (held here to 1e-3 of the series' peak),
 gradients against the fp64 oracle and central finite differences, at small
 ragged grids and launch splits and at the full 512^2 x 4800 configuration.
@@ -88,7 +88,7 @@ def test_loss_and_gradient_match_oracle(gpu, steps):
 
 
 def test_gradient_matches_finite_differences(gpu):
-    """within 1e-2 of central differences of the fp64
+    """Parity bar: within 1e-2 of central differences of the fp64
     oracle forward."""
     cfg, s = small_session(R=40, C=36, T=150)
     try:
@@ -124,7 +124,7 @@ def test_adam_step_matches_oracle(gpu):
 def test_full_configuration_matches_oracle(gpu):
     """512 x 512 grid, 4800 frames (benchmark config 5): target and pickup
     series within 1e-4 of the fp32 oracle, loss and both gradients against
-    the fp64 oracle within the north-star 1e-2.  dL/dc2 (-2.51) is a small
+    the fp64 oracle within the 1e-2 parity bar.  dL/dc2 (-2.51) is a small
     residue of much larger oscillating terms; the sequential fp32 oracle's
     own gradient is 3.1% (c2) and 0.9% (d) from fp64 here, this kernel's
     about 0.6% and 0.004%."""

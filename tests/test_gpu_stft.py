@@ -1,6 +1,6 @@
 """HIP STFT round trip (config 2: window -> FFT -> gains -> IFFT ->
 overlap-add, and the gain gradient) against the CPU oracle: forward within
-the north-star 1e-4 max-abs of the fp32 oracle and within a small multiple
+the 1e-4 max-abs parity bar against the fp32 oracle and within a small multiple
 of the fp32 oracle's own distance from the fp64 oracle, gradients against the
 fp64 oracle and central finite differences, at small ragged shapes and at
 the full 8 x 2^20 configuration.  Needs a GPU."""
@@ -83,7 +83,7 @@ def test_loss_and_gradient_match_oracle(gpu):
 
 
 def test_gradient_matches_finite_differences(gpu):
-    """within 1e-2 of central differences of the fp64 oracle
+    """Parity bar: within 1e-2 of central differences of the fp64 oracle
     forward, per bin and along the gradient."""
     cfg, s = small_session(S=1, T=3000, N=128, H=32)
     try:

@@ -99,7 +99,7 @@ def test_lanes_are_independent():
         np.testing.assert_array_equal(y[:, k], yk[:, 0])
 
 
-def test_fp32_build_within_north_star_bar_of_fp64():
+def test_fp32_build_within_parity_bar_of_fp64():
     cfg = BiquadConfig(B=8, T=1 << 15)
     x, m, p = cfg.inputs(), cfg.modulation(), cfg.params()
     y32 = O.biquad_fwd(x, m, p[:8], p[8:], prec="f32")
