@@ -215,13 +215,17 @@ static void playhead_real(int F, int T, REAL* out) {
   float denom = (float)(T > 2 ? T - 1 : 1);
   float step = fmaxi / denom;
   float hi = fmaxi - 1e-4f > 0.f ? fmaxi - 1e-4f : 0.f;
+  /* the accumulator's wrap span: fmaxi, or 1 for a single control row (a
+   * zero span would divide 0 by 0; with step 0 the playhead stays at row
+   * 0 either way), as the schedule's accumulator table is set up */
+  float span = F > 1 ? fmaxi : 1.0f;
   float st = 0;
   for (int t = 0; t < T; ++t) {
     float acc = st;
     float next = acc + step;
-    float k = floorf(next / fmaxi);
-    float w = next - k * fmaxi;
-    if (w >= fmaxi) w = w - fmaxi;
+    float k = floorf(next / span);
+    float w = next - k * span;
+    if (w >= span) w = w - span;
     st = w;
     float p = acc < 0.f ? 0.f : acc;
     out[t] = (REAL)(p > hi ? hi : p);

@@ -3,7 +3,9 @@ bit against the oracle's stateful phasor (Emit+State.swift:322-369): f0
 blocks holding values outside the fast-step range (tiny, huge) beside
 zero and ordinary ones, and lengths that end in a partial interval and a
 partial segment; one and two harmonic groups; and the timed build, which
-must step the same phases.  Needs a GPU."""
+must step the same phases.  The f0 frames the chain reads (the sampleRow
+lerp of the f0 rows, Emit+RowSelection.swift:164-197) are checked bit for
+bit too, down to a single control row.  Needs a GPU."""
 import numpy as np
 import pytest
 
@@ -53,6 +55,7 @@ def test_checkpoints_bit_exact_with_slow_blocks_and_ragged_ends(gpu, T, K):
     for name, f in (("ordinary f0", f0), ("slow blocks", with_slow_blocks(cfg, f0))):
         out = render_checkpoints(cfg, f, uv, X)
         f0f = out["f0_frames"].reshape(cfg.B, cfg.T)
+        np.testing.assert_array_equal(f0f, O.lerp_frames(f, cfg.B, cfg.F, cfg.T))
         slow = ~((f0f == 0) | ((f0f >= 2.0 ** -20) & (f0f < 2.0 ** 24 / (64 * ((K + 63) // 64)))))
         ck = O.phase_checkpoints(f0f, cfg.B, cfg.K, cfg.T, cfg.sr)
         print(f"  {name}: {int(slow.sum())} frames outside the fast range", flush=True)

@@ -98,6 +98,16 @@ def test_lerp_frames_of_a_ramp_is_the_playhead():
         assert np.abs(out[b] - ref).max() < 1e-3
 
 
+def test_one_control_row_is_read_by_every_frame():
+    # F = 1: the playhead stays at row 0 (step 0, and the accumulator's wrap
+    # span is 1, as the schedule's accumulator table is set up), so every
+    # frame reads the single row exactly
+    B, T = 3, 100
+    src = np.array([[430.25, -1.5, 0.0]], np.float32)
+    assert not O.playhead(1, T).any()
+    np.testing.assert_array_equal(O.lerp_frames(src, B, 1, T), np.repeat(src[0][:, None], T, 1))
+
+
 def test_phase_checkpoints_follow_the_phasor():
     B, K, T, sr = 2, 5, 700, 16000.0
     rng = np.random.default_rng(2)
